@@ -1,0 +1,320 @@
+"""State-op decode benchmark on one MI355X: tiered v4 vs fresh at the
+Nemotron-Nano-9B-v2 mixer shape (27 Mamba2 layers, H=128, P=80, N=128, G=8).
+
+A step is one decode token through the state op of all layers (one kernel
+launch per layer), inputs resident in HBM, synthetic seeded data. Prints one
+JSON line (the driver contract); progress goes to stderr.
+
+    python bench.py [--steps 64] [--warmup 8] [--B 256] [--c 4] [--k 32] [--cold fp32]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+L_DEF, H, P, N, G = 27, 128, 80, 128, 8
+PEAK_HBM_GBS = 8000.0
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# algorithmic byte model (per request per layer-token); see DESIGN.md
+def bytes_io():
+    # x bf16 + B, C bf16 + dt bf16 in, y fp32 out
+    return H * P * 2 + 2 * G * N * 2 + H * 2 + H * P * 4
+
+
+def bytes_fresh_token():
+    return 2 * H * P * N * 4 + bytes_io()
+
+
+def bytes_v4_token(k, c, cold):
+    nc = N - k
+    esz = {"fp32": 4, "bf16": 2, "fp8": 1}[cold]
+    hot = 2 * H * P * k * 4
+    read = H * P * nc * esz + (H * P * 4 if cold == "fp8" else 0)
+    if cold == "fp32":
+        flush = H * P * nc * 4  # rewrite of the single copy
+    else:  # master read + master write + read-copy write (+ scale)
+        flush = H * P * nc * (4 + 4 + esz) + (H * P * 4 if cold == "fp8" else 0)
+    ring_entry = H * P * 2 + H * 4 + G * nc * 4  # x bf16, dt, B' cold
+    ring = (c - 1) / c * 2 * ring_entry  # written by c-1 of c tokens, read once at the flush
+    return hot + read + flush / c + ring + bytes_io()
+
+
+def bytes_rotation():
+    return G * N * N * 4
+
+
+# ---------------------------------------------------------------------------
+def make_layers(L, dev, seed):
+    """Per layer: dt_bias = log(expm1(U(1e-3, 1e-1))), A = -exp(U(0, ln 16)), D ~ N(0,1) per head;
+    R = Q of QR(N(0,1)) with the sign fix, per group."""
+    from nested_ssm_amd import LayerParams
+
+    gen = torch.Generator().manual_seed(seed)
+    out = []
+    f = dict(device=dev, dtype=torch.float32)
+    for _ in range(L):
+        u = 1e-3 + (1e-1 - 1e-3) * torch.rand(H, generator=gen, dtype=torch.float64)
+        dt_bias = torch.log(torch.expm1(u))
+        A = -torch.exp(torch.rand(H, generator=gen, dtype=torch.float64) * 2.772588722239781)
+        D = torch.randn(H, generator=gen, dtype=torch.float64)
+        Q, Rr = torch.linalg.qr(torch.randn(G, N, N, generator=gen, dtype=torch.float64))
+        R = Q * torch.sign(torch.diagonal(Rr, dim1=-2, dim2=-1))[..., None, :]
+        out.append(LayerParams(H, P, N, G, dt_bias.to(**f), A.to(**f), D.to(**f), R.to(**f).contiguous()))
+    return out
+
+
+def make_inputs(L, B, dev, seed, pool=2):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    sets = []
+    for _ in range(pool):
+        per = []
+        for _ in range(L):
+            x = torch.randn(B, H, P, device=dev, generator=g).to(torch.bfloat16)
+            Bm = (torch.randn(B, G, N, device=dev, generator=g) / N ** 0.5).to(torch.bfloat16)
+            Cm = (torch.randn(B, G, N, device=dev, generator=g) / N ** 0.5).to(torch.bfloat16)
+            dt = torch.randn(B, H, device=dev, generator=g).to(torch.bfloat16)
+            per.append((x, Bm, Cm, dt))
+        sets.append(per)
+    return sets
+
+
+def rand_state(B, dev, g):
+    return torch.randn(B, H, P, N, device=dev, generator=g).mul_(0.1)
+
+
+def timed(step_fn, steps, warmup, launches_per_step):
+    """Warmup, then time exactly `steps` steps with events on the launch stream."""
+    for i in range(warmup):
+        step_fn(i)
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for i in range(steps):
+        step_fn(warmup + i)
+    e1.record(st)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    return ms / steps, ms / (steps * launches_per_step)
+
+
+def per_launch_ms(launch_fn, n):
+    """Average duration of n launches, each bracketed by its own event pair."""
+    st = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for i, (a, b) in enumerate(evs):
+        a.record(st)
+        launch_fn(i)
+        b.record(st)
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in evs) / n
+
+
+def bench_fresh(args, layers, inputs, dev):
+    from nested_ssm_amd import fresh_step
+
+    g = torch.Generator(device=dev).manual_seed(args.seed + 1)
+    states = [rand_state(args.B, dev, g) for _ in range(args.layers)]
+    ys = [torch.empty(args.B, H, P, device=dev) for _ in range(args.layers)]
+
+    def step(i):
+        inp = inputs[i % len(inputs)]
+        for l in range(args.layers):
+            fresh_step(layers[l], states[l], *inp[l], y=ys[l])
+
+    ms_step, ms_launch = timed(step, args.steps, args.warmup, args.layers)
+
+    def one(i):
+        l = i % args.layers
+        fresh_step(layers[l], states[l], *inputs[0][l], y=ys[l])
+
+    ms_ev = per_launch_ms(one, min(4 * args.layers, 108))
+    del states
+    torch.cuda.empty_cache()
+    return ms_step, ms_launch, ms_ev
+
+
+def bench_v4(args, layers, inputs, dev):
+    from nested_ssm_amd import V4Tier
+
+    g = torch.Generator(device=dev).manual_seed(args.seed + 1)
+    tiers, ys = [], []
+    for l in range(args.layers):
+        t = V4Tier(args.B, H, P, G, k_hot=args.k, c=args.c, cold=args.cold, device=dev)
+        S0 = rand_state(args.B, dev, g)
+        t.join(layers[l], S0)
+        del S0
+        tiers.append(t)
+        ys.append(torch.empty(args.B, H, P, device=dev))
+    torch.cuda.synchronize()
+
+    def step(i):
+        inp = inputs[i % len(inputs)]
+        for l in range(args.layers):
+            tiers[l].step(layers[l], *inp[l], y=ys[l])
+
+    # warmup is rounded to whole flush windows so the timed steps start phase-aligned
+    warm = ((args.warmup + args.c - 1) // args.c) * args.c
+    ms_step, ms_launch = timed(step, args.steps, warm, args.layers)
+
+    # per-launch events over whole flush windows (c tokens of layer 0 .. L-1)
+    seq = []
+    for tok in range(args.c):
+        for l in range(args.layers):
+            seq.append((tok, l))
+
+    def one(i):
+        tok, l = seq[i % len(seq)]
+        tiers[l].step(layers[l], *inputs[tok % len(inputs)][l], y=ys[l])
+
+    ms_ev = per_launch_ms(one, len(seq) * max(1, 108 // len(seq)))
+    tier_gb = sum(t.nbytes() for t in tiers) / 1e9
+    del tiers
+    torch.cuda.empty_cache()
+    return ms_step, ms_launch, ms_ev, tier_gb
+
+
+def cpu_baseline(args, budget_s):
+    """The oracle's reference step (full fp32 state updated every token, stale
+    cold readout, scale/v4_native_decode.py semantics) on the host, one layer at
+    B requests; tokens/s for the whole L-layer model = B / (L * t_layer)."""
+    import oracle
+
+    threads = torch.get_num_threads()
+    gen = torch.Generator().manual_seed(args.seed)
+    prm = oracle.make_layer_params(H, P, N, G, gen)
+    B = args.B
+    ref = oracle.NativeV4(B, H, P, N, args.k, args.c, cold=args.cold)
+    ref.join(torch.arange(B), oracle.make_state(B, H, P, N, gen))
+    x, Bm, Cm, dt = oracle.make_step_inputs(B, H, P, N, G, gen)
+    ref.step(x, Bm, Cm, dt, prm)  # warm
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        ref.step(x, Bm, Cm, dt, prm)
+        n += 1
+        if time.perf_counter() - t0 > budget_s or n >= 16:
+            break
+    t_layer = (time.perf_counter() - t0) / n
+    return {
+        "value": round(B / (args.layers * t_layer), 2),
+        "unit": "state-op tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"oracle NativeV4 step ({args.cold} cold, k={args.k}, c={args.c}), 1 layer x B={B} x {n} tokens "
+                  f"on the host, {t_layer * 1e3:.0f} ms/layer-token, scaled to {args.layers} layers",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--B", type=int, default=256)
+    ap.add_argument("--layers", type=int, default=L_DEF)
+    ap.add_argument("--k", type=int, default=32)
+    ap.add_argument("--c", type=int, default=4)
+    ap.add_argument("--cold", default="fp32", choices=["fp32", "bf16", "fp8"])
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the host baseline")
+    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of host work for the baseline")
+    ap.add_argument("--only", choices=["v4", "fresh"], default=None, help="profile one path only")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): the tiered state op has no "
+              f"cross-GPU exchange; see DESIGN.md for how it would shard", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    if args.steps % args.c:
+        args.steps += args.c - args.steps % args.c
+        log(f"steps rounded up to {args.steps} (a multiple of c, so flushes are counted evenly)")
+
+    dev = "cuda"
+    log(f"device {torch.cuda.get_device_name(0)}; B={args.B} L={args.layers} k={args.k} c={args.c} cold={args.cold}")
+    layers = make_layers(args.layers, dev, args.seed)
+    inputs = make_inputs(args.layers, args.B, dev, args.seed + 7)
+    torch.cuda.synchronize()
+
+    res = {}
+    if args.only != "v4":
+        log("fresh ...")
+        f_step, f_launch, f_ev = bench_fresh(args, layers, inputs, dev)
+        res["fresh"] = (f_step, f_launch, f_ev)
+        fb = args.B * bytes_fresh_token() + bytes_rotation()
+        log(f"fresh: {f_step:.3f} ms/step, {args.B / f_step * 1e3:,.0f} tok/s, launch {f_ev * 1e3:.1f} us "
+            f"-> {fb / (f_ev * 1e-3) / 1e9:,.0f} GB/s")
+    if args.only != "fresh":
+        log("v4 ...")
+        v_step, v_launch, v_ev, tier_gb = bench_v4(args, layers, inputs, dev)
+        res["v4"] = (v_step, v_launch, v_ev)
+        vb = args.B * bytes_v4_token(args.k, args.c, args.cold) + bytes_rotation()
+        log(f"v4: {v_step:.3f} ms/step, {args.B / v_step * 1e3:,.0f} tok/s, launch {v_ev * 1e3:.1f} us "
+            f"-> {vb / (v_ev * 1e-3) / 1e9:,.0f} GB/s (tiers {tier_gb:.1f} GB)")
+
+    head = "v4" if "v4" in res else "fresh"
+    ms_step, ms_launch, ms_ev = res[head]
+    per_launch_bytes = args.B * (bytes_v4_token(args.k, args.c, args.cold) if head == "v4"
+                                 else bytes_fresh_token()) + bytes_rotation()
+    achieved = per_launch_bytes / (ms_ev * 1e-3) / 1e9
+    out = {
+        "metric": "state-op tokens/s at 9B shape B=256 (v4-c4 vs fresh); achieved HBM GB/s vs peak",
+        "value": round(args.B / ms_step * 1e3, 1),
+        "unit": "state-op tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded; bf16 x/B/C/dt, fp32 state ~N(0,0.1^2), random orthogonal R per layer-group)",
+        "config": {
+            "workload": (f"{head} state op, Nemotron-Nano-9B-v2 mixer shape, {args.layers} layers, B={args.B}"
+                         + (f", k_hot={args.k}, c={args.c}, {args.cold} cold, phase-aligned" if head == "v4" else "")),
+            "layers": args.layers, "B": args.B, "H": H, "P": P, "N": N, "G": G,
+            "k_hot": args.k, "c": args.c, "cold": args.cold,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": None,
+            "kernel": f"step_kernel<{args.k if head == 'v4' else N}, {args.cold if head == 'v4' else 'none'}>",
+            "algorithmic_bytes_per_launch": int(per_launch_bytes),
+            "avg_launch_us_events": round(ms_ev * 1e3, 2),
+            "avg_launch_us_region": round(ms_launch * 1e3, 2),
+        },
+    }
+    if "fresh" in res and "v4" in res:
+        out["fresh_tok_s"] = round(args.B / res["fresh"][0] * 1e3, 1)
+        out["fresh_ms_per_step"] = round(res["fresh"][0], 4)
+        fb = args.B * bytes_fresh_token() + bytes_rotation()
+        out["fresh_achieved_gbs"] = round(fb / (res["fresh"][2] * 1e-3) / 1e9, 1)
+        out["speedup_v4_vs_fresh"] = round(res["fresh"][0] / res["v4"][0], 3)
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        out["cpu_baseline"] = cpu_baseline(args, args.cpu_budget)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

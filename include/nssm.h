@@ -1,0 +1,164 @@
+/*
+ * nssm.h — C ABI of the MI355X (gfx950) Mamba2 decode-step state update with
+ * nested hot/cold tiering ("v4").
+ *
+ * Everything here is plain C: device pointers, sizes and a hipStream_t passed
+ * as void*. No torch types. Every entry point enqueues work on `stream`,
+ * never synchronises the host, never allocates device memory, and returns 0
+ * or a negative NSSM_E* code (nssm_strerror() names it).
+ *
+ * Notation: b = requests in a call, H heads, P headdim, N d_state (128),
+ * G groups (HG = H/G heads per group), K = k_hot (hot columns, a multiple of
+ * 32 below N), NC = N-K cold columns, c = flush period in tokens.
+ *
+ * Reference interfaces these entry points replace (files of the reference
+ * repository omin-Kwon/nested_ssm):
+ *   nssm_fresh_step      scale/bench_v4_decode.py:250-253 (fresh SSU arm) and
+ *                        scale/v4_native_decode.py:58-78 (pb >= N branch)
+ *   nssm_v4_step         scale/v4_fused_decode.py:28-95 (_v4_fused_decode),
+ *                        scale/v4_native_decode.py:58-167 (_v4_decode state
+ *                        part), scale/vllm_v4_patch.py:140-179 (decode_readout)
+ *   nssm_v4_join         scale/vllm_v4_patch.py:123-137 (prefill_snapshot),
+ *                        scale/v4_native_decode.py:234-243,
+ *                        scale/v4_fused_decode.py:121-159 (prefill capture)
+ *   nssm_v4_materialize  no single reference function: the exact current
+ *                        state that scale/v4_native_decode.py:65-67 keeps in
+ *                        the cache, rebuilt from the tiers
+ *   nssm_fp8_readout     scale/bench_v4_decode.py:33-60 (_fp8_matvec /
+ *                        fp8_cold_readout)
+ *   nssm_rotate          scale/nemotron_retrofit.py:24-27 (ActRotMask._rot),
+ *                        scale/vllm_v4_patch.py:41-45 (rot_flat)
+ */
+#ifndef NSSM_H_
+#define NSSM_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NSSM_ABI_VERSION 1
+
+/* error codes */
+#define NSSM_OK 0
+#define NSSM_E_NULL (-1)        /* a required pointer is NULL            */
+#define NSSM_E_DIMS (-2)        /* sizes out of the supported range      */
+#define NSSM_E_ALIGN (-3)       /* a pointer is not 16-byte aligned      */
+#define NSSM_E_KIND (-4)        /* unknown cold storage kind             */
+#define NSSM_E_LAUNCH (-5)      /* the HIP launch reported an error      */
+#define NSSM_E_TUNING (-6)      /* launch override does not fit the dims */
+
+/* cold tier storage kinds */
+#define NSSM_COLD_FP32 0 /* one exact fp32 copy, read every token, rewritten at flush */
+#define NSSM_COLD_BF16 1 /* bf16 read copy (RNE of the master) + exact fp32 master */
+#define NSSM_COLD_FP8 2  /* e4m3fn read copy, fp32 scale per (slot,head,p) row
+                            (amax/448 + 1e-12), + exact fp32 master */
+
+/* Per-layer constants. Mirrors the mixer attributes the reference reads:
+ * dt_bias, A = -exp(A_log), D, time_step_min, and the ActRotMask R. */
+typedef struct nssm_layer_params {
+  int32_t H, P, N, G;
+  const float* dt_bias; /* [H] */
+  const float* A;       /* [H], already -exp(A_log) */
+  const float* D;       /* [H] */
+  const float* R;       /* [G][N][N], R[g][m][n]; B'[m] = sum_n R[g][m][n] B[n]; NULL = identity */
+  float dt_min;         /* dt = max(dt, dt_min) when dt_min > 0 (v4_native_decode.py:55) */
+} nssm_layer_params;
+
+/* One decode token for b requests (all bf16, as the model emits them). */
+typedef struct nssm_step_inputs {
+  int32_t b;
+  const uint16_t* x;        /* [b][H][P] bf16 conv/SiLU output, head view */
+  const uint16_t* B;        /* [b][G][N] bf16, before rotation */
+  const uint16_t* C;        /* [b][G][N] bf16, before rotation */
+  const uint16_t* dt;       /* [b][H] bf16, before dt_bias and softplus */
+  const int32_t* slot_ids;  /* [b] state slot of each request, unique; NULL = 0..b-1 */
+} nssm_step_inputs;
+
+/* Tiered state of one layer for `slots` sequence slots (all buffers are
+ * owned by the caller). Layouts, all row-major:
+ *   hot      fp32 [slots][H][P][K]
+ *   cold     [slots][H][P][NC]   fp32 | bf16 | e4m3fn bytes, by cold_kind
+ *   scale    fp32 [slots][H][P]         (NSSM_COLD_FP8 only, else NULL)
+ *   master   fp32 [slots][H][P][NC]     (BF16/FP8 only, else NULL)
+ *   ring_x   bf16 [slots][H][c][P]      x of buffered tokens
+ *   ring_dt  fp32 [slots][H][c]         softplus'd dt of buffered tokens
+ *   ring_b   fp32 [slots][G][c][NC]     rotated B cold columns of buffered tokens
+ *   t        int32 [slots][H]           decode steps (phase = t % c)
+ *   nv       int32 [slots][H]           buffered tokens since the last snapshot
+ *   glog     fp32 [slots][H]            log-decay since the snapshot, one token lagged
+ * All heads of a slot carry equal t and nv. */
+typedef struct nssm_tier {
+  int32_t slots, k_hot, c, cold_kind;
+  float* hot;
+  void* cold;
+  float* scale;
+  float* master;
+  uint16_t* ring_x;
+  float* ring_dt;
+  float* ring_b;
+  int32_t* t;
+  int32_t* nv;
+  float* glog;
+} nssm_tier;
+
+/* Byte size of each tier buffer, in the struct's order (hot, cold, scale,
+ * master, ring_x, ring_dt, ring_b, t, nv, glog): sizes_out[10]. */
+int nssm_tier_sizes(int32_t slots, int32_t H, int32_t P, int32_t N, int32_t G,
+                    int32_t k_hot, int32_t c, int32_t cold_kind, int64_t* sizes_out);
+
+/* Untiered decode step over the full fp32 state [slots][H][P][N]:
+ *   B',C' = R_g B, R_g C;  dt = softplus(dt + dt_bias);  a = dt*A
+ *   S <- exp(a) S + (dt x) (x) B';   y = S C' + D x          (y fp32 [b][H][P]) */
+int nssm_fresh_step(const nssm_layer_params* prm, float* state, int32_t slots,
+                    const nssm_step_inputs* in, float* y, void* stream);
+
+/* Tiered decode step (hot fresh, cold stale + decay-corrected, ring append,
+ * in-launch flush for requests whose phase wraps):
+ *   hot  <- exp(a) hot + (dt x) (x) B'[:K]
+ *   y    =  hot C'[:K] + exp(glog) * (cold_read C'[K:]) + D x
+ *   t += 1; if t % c == 0: cold <- exact cold state at t (chunked decayed
+ *   replay of the ring plus this token), glog <- 0; else glog += a and this
+ *   token is appended to the ring. */
+int nssm_v4_step(const nssm_layer_params* prm, const nssm_tier* tier,
+                 const nssm_step_inputs* in, float* y, void* stream);
+
+/* Capture a tier from full fp32 states [b][H][P][N] into slot_ids[b] (NULL =
+ * 0..b-1): hot = S[..,:K], cold = S[..,K:] (quantized for BF16/FP8),
+ * t = phase[i] (NULL = 0), nv = 0, glog = 0. */
+int nssm_v4_join(const nssm_layer_params* prm, const nssm_tier* tier, const float* state,
+                 int32_t b, const int32_t* slot_ids, const int32_t* phase, void* stream);
+
+/* Rebuild the exact current full fp32 state [b][H][P][N] of slot_ids[b]:
+ * hot as stored; cold = exp(sum a) master + decayed replay of the nv buffered
+ * tokens. The tier is not modified. */
+int nssm_v4_materialize(const nssm_layer_params* prm, const nssm_tier* tier, float* state_out,
+                        int32_t b, const int32_t* slot_ids, void* stream);
+
+/* y[r][p] = sum_n q[r][n] * scale[r][n] * e4m3fn(s8[r][n][p]); rows x nc x pd. */
+int nssm_fp8_readout(const float* q, const uint8_t* s8, const float* scale, float* y,
+                     int32_t rows, int32_t nc, int32_t pd, void* stream);
+
+/* out[t][g][m] = sum_n R[g][m][n] * in[t][g][n]; in bf16, out fp32. */
+int nssm_rotate(const uint16_t* in, const float* R, float* out, int32_t T, int32_t G, int32_t N,
+                void* stream);
+
+/* Launch-shape override for the step kernels (0, 0 = automatic): heads per
+ * workgroup and waves per workgroup. Process-wide; for tuning sweeps. */
+int nssm_set_launch(int32_t heads_per_wg, int32_t waves_per_wg);
+
+/* Host-side (CPU) conversions used by the kernels, exported so the CPU test
+ * suite can compare them bit for bit with torch's casts. */
+void nssm_host_f32_to_e4m3fn(const float* in, uint8_t* out, int64_t n);
+void nssm_host_e4m3fn_to_f32(const uint8_t* in, float* out, int64_t n);
+void nssm_host_f32_to_bf16(const float* in, uint16_t* out, int64_t n);
+
+const char* nssm_strerror(int code);
+int nssm_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NSSM_H_ */

@@ -1,0 +1,12 @@
+"""nested_ssm_amd — MI355X (gfx950) Mamba2 decode-step state update with nested
+hot/cold tiering ("v4"), behind the decode-step call signatures of
+omin-Kwon/nested_ssm (scale/v4_native_decode.py, scale/v4_fused_decode.py,
+scale/bench_v4_decode.py).
+
+The kernels live in libnssm_hip.so (C ABI: include/nssm.h), built in-tree by
+`python -m nested_ssm_amd.build`. There is no CPU fallback.
+"""
+from ._lib import COLD_KINDS, NssmError, lib  # noqa: F401
+from .ops import LayerParams, V4Tier, fp8_cold_readout, fresh_step, rotate, set_launch  # noqa: F401
+
+__version__ = "0.1.0"

@@ -1,0 +1,894 @@
+// gfx950 kernels for the Mamba2 decode-step recurrent-state update with
+// nested hot/cold tiering, and the C ABI declared in include/nssm.h.
+//
+// Work decomposition (one launch per layer per decode token):
+//   workgroup = (request i, group g, head block hb) with `hpw` heads of group g.
+//   The workgroup rotates B and C of (i, g) once (B' = R_g B, C' = R_g C, fp32)
+//   into LDS, then its waves stream the heads' state rows.
+//   A "unit" is 8 consecutive headdim rows p of one head. In a unit, lane l owns
+//   row p0 + (l >> 3) and, in every 32-column segment s of the row, the four
+//   columns 32 s + 4 (l & 7) .. +3. One dwordx4 per lane per segment moves
+//   8 rows x 128 B = 1 KB per wave instruction; the C.h readout of a row is a
+//   sum over its 8 lanes (three DPP steps).
+//   Hot columns [0, K) are read and written every token. Cold columns [K, N)
+//   are only read, except at the flush token of the request, when the
+//   workgroup replays the buffered tokens into them.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "../../include/nssm.h"
+#include "nssm_formats.h"
+
+namespace {
+
+constexpr int kN = 128;  // d_state handled by these kernels
+constexpr int kMaxC = 64;
+constexpr int kMaxWaves = 8;
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+
+struct StepArgs {
+  // tier state (fresh: hot is the full state, the rest NULL)
+  float* hot;
+  void* cold;
+  float* scale;
+  float* master;
+  uint16_t* ring_x;
+  float* ring_dt;
+  float* ring_b;
+  int32_t* t;
+  int32_t* nv;
+  float* glog;
+  // inputs
+  const uint16_t* x;
+  const uint16_t* Bm;
+  const uint16_t* Cm;
+  const uint16_t* dt_raw;
+  const int32_t* slot_ids;
+  const float* dt_bias;
+  const float* A;
+  const float* D;
+  const float* R;
+  float* y;
+  int32_t b, slots, H, P, G, HG, c, hpw, nhb;
+  float dt_min;
+};
+
+__device__ __forceinline__ float bf2f(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+// DPP controls: quad_perm [1,0,3,2] = 0xB1, quad_perm [2,3,0,1] = 0x4E,
+// row_half_mirror (lane i <-> 7-i within 8) = 0x141, row_mirror (within 16) = 0x140.
+__device__ __forceinline__ float sum8(float v) {
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0x141>(v);
+  return v;
+}
+__device__ __forceinline__ float max8(float v) {
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  return v;
+}
+__device__ __forceinline__ float sum32(float v) {
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0x141>(v);
+  v += dpp<0x140>(v);
+  v += __shfl_xor(v, 16);
+  return v;
+}
+
+__device__ __forceinline__ float softplus_f(float v) { return v > 20.f ? v : log1pf(expf(v)); }
+
+// ---------------------------------------------------------------------------
+// per-head scalars kept in LDS
+// (stride padded to a multiple of 4 floats so the LDS arrays after it stay 16-byte aligned)
+enum { HD_DT = 0, HD_A, HD_DECAY, HD_EG, HD_D, HD_FLUSH, HD_DTOT, HD_T, HD_NV, HD_STRIDE = 12 };
+
+// Cold-tier row access for one lane: NC/32 segments of 4 columns.
+template <int COLD, int CS>
+struct ColdRead {
+  // read-copy values (what the readout sees)
+  static __device__ __forceinline__ void load(const StepArgs& a, size_t row, int q, float (&v)[CS][4]) {
+    constexpr int NC = CS * 32;
+    if constexpr (COLD == NSSM_COLD_FP32) {
+      const f4* p = reinterpret_cast<const f4*>(static_cast<const float*>(a.cold) + row * NC) + q;
+#pragma unroll
+      for (int s = 0; s < CS; ++s) {
+        f4 t = __builtin_nontemporal_load(p + 8 * s);
+        v[s][0] = t.x; v[s][1] = t.y; v[s][2] = t.z; v[s][3] = t.w;
+      }
+    } else if constexpr (COLD == NSSM_COLD_BF16) {
+      const u2v* p = reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.cold) + row * NC) + q;
+#pragma unroll
+      for (int s = 0; s < CS; ++s) {
+        u2v t = __builtin_nontemporal_load(p + 8 * s);
+        v[s][0] = __uint_as_float(t.x << 16);
+        v[s][1] = __uint_as_float(t.x & 0xffff0000u);
+        v[s][2] = __uint_as_float(t.y << 16);
+        v[s][3] = __uint_as_float(t.y & 0xffff0000u);
+      }
+    } else {  // FP8: per-row scale
+      const uint32_t* p = reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(a.cold) + row * NC) + q;
+      const float sc = a.scale[row];
+#pragma unroll
+      for (int s = 0; s < CS; ++s) {
+        uint32_t t = __builtin_nontemporal_load(p + 8 * s);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[s][e] = nssm_e4m3fn_to_f32((uint8_t)(t >> (8 * e))) * sc;
+      }
+    }
+  }
+};
+
+// Write the new exact cold values of one row: fp32 copy, or master + read copy.
+template <int COLD, int CS>
+__device__ __forceinline__ void cold_store(const StepArgs& a, size_t row, int q, const float (&v)[CS][4]) {
+  constexpr int NC = CS * 32;
+  if constexpr (COLD == NSSM_COLD_FP32) {
+    f4* p = reinterpret_cast<f4*>(static_cast<float*>(a.cold) + row * NC) + q;
+#pragma unroll
+    for (int s = 0; s < CS; ++s) __builtin_nontemporal_store(f4{v[s][0], v[s][1], v[s][2], v[s][3]}, p + 8 * s);
+  } else {
+    f4* pm = reinterpret_cast<f4*>(a.master + row * NC) + q;
+#pragma unroll
+    for (int s = 0; s < CS; ++s) __builtin_nontemporal_store(f4{v[s][0], v[s][1], v[s][2], v[s][3]}, pm + 8 * s);
+    if constexpr (COLD == NSSM_COLD_BF16) {
+      u2v* p = reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.cold) + row * NC) + q;
+#pragma unroll
+      for (int s = 0; s < CS; ++s) {
+        u2v t;
+        t.x = (uint32_t)nssm_f32_to_bf16(v[s][0]) | ((uint32_t)nssm_f32_to_bf16(v[s][1]) << 16);
+        t.y = (uint32_t)nssm_f32_to_bf16(v[s][2]) | ((uint32_t)nssm_f32_to_bf16(v[s][3]) << 16);
+        __builtin_nontemporal_store(t, p + 8 * s);
+      }
+    } else {  // FP8 with per-row amax scale, as scale/vllm_v4_patch.py:106-111
+      float am = 0.f;
+#pragma unroll
+      for (int s = 0; s < CS; ++s)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) am = fmaxf(am, fabsf(v[s][e]));
+      am = max8(am);
+      const float sc = am / 448.0f + 1e-12f;
+      uint32_t* p = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.cold) + row * NC) + q;
+#pragma unroll
+      for (int s = 0; s < CS; ++s) {
+        uint32_t t = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t |= (uint32_t)nssm_f32_to_e4m3fn(v[s][e] / sc) << (8 * e);
+        __builtin_nontemporal_store(t, p + 8 * s);
+      }
+      if (q == 0) a.scale[row] = sc;
+    }
+  }
+}
+
+template <int CS>
+__device__ __forceinline__ void master_load(const StepArgs& a, size_t row, int q, float (&v)[CS][4]) {
+  constexpr int NC = CS * 32;
+  const f4* p = reinterpret_cast<const f4*>(a.master + row * NC) + q;
+#pragma unroll
+  for (int s = 0; s < CS; ++s) {
+    f4 t = __builtin_nontemporal_load(p + 8 * s);
+    v[s][0] = t.x; v[s][1] = t.y; v[s][2] = t.z; v[s][3] = t.w;
+  }
+}
+
+// One unit (8 rows of head j) of the step. FLUSH selects the replay of the
+// buffered window into the cold columns (sU/sBc staged by the caller).
+template <int K, int COLD, bool FLUSH>
+__device__ __forceinline__ void do_unit(const StepArgs& a, int slot, int bi, int h, int j, int p, int q,
+                                        const float (&Bh)[K / 32][4], const float (&Ch)[K / 32][4],
+                                        const float (&Cc)[(kN - K) / 32 > 0 ? (kN - K) / 32 : 1][4],
+                                        const float* sX, const float* sHd, const float* sU, const float* sBc,
+                                        int m) {
+  constexpr int HS = K / 32;
+  constexpr int NC = kN - K;
+  constexpr int CS = NC / 32;
+  const int P = a.P;
+  const size_t row = ((size_t)slot * a.H + h) * P + p;
+
+  f4* hp = reinterpret_cast<f4*>(a.hot + row * K) + q;
+  f4 hv[HS];
+#pragma unroll
+  for (int s = 0; s < HS; ++s) hv[s] = __builtin_nontemporal_load(hp + 8 * s);
+
+  float cv[CS > 0 ? CS : 1][4];
+  float mv[CS > 0 ? CS : 1][4];
+  if constexpr (CS > 0) {
+    ColdRead<COLD, CS>::load(a, row, q, cv);
+    if constexpr (FLUSH && COLD != NSSM_COLD_FP32) master_load<CS>(a, row, q, mv);
+  }
+
+  const float* hd = sHd + j * HD_STRIDE;
+  const float xp = sX[j * P + p];
+  const float uu = hd[HD_DT] * xp;
+  const float dec = hd[HD_DECAY];
+  float ph = 0.f;
+#pragma unroll
+  for (int s = 0; s < HS; ++s) {
+    f4 v = hv[s];
+    v.x = fmaf(v.x, dec, uu * Bh[s][0]);
+    v.y = fmaf(v.y, dec, uu * Bh[s][1]);
+    v.z = fmaf(v.z, dec, uu * Bh[s][2]);
+    v.w = fmaf(v.w, dec, uu * Bh[s][3]);
+    ph = fmaf(v.x, Ch[s][0], ph);
+    ph = fmaf(v.y, Ch[s][1], ph);
+    ph = fmaf(v.z, Ch[s][2], ph);
+    ph = fmaf(v.w, Ch[s][3], ph);
+    hv[s] = v;
+  }
+#pragma unroll
+  for (int s = 0; s < HS; ++s) __builtin_nontemporal_store(hv[s], hp + 8 * s);
+
+  float part = ph;
+  if constexpr (CS > 0) {
+    float pc = 0.f;
+#pragma unroll
+    for (int s = 0; s < CS; ++s)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pc = fmaf(cv[s][e], Cc[s][e], pc);
+    part = fmaf(hd[HD_EG], pc, ph);
+
+    if constexpr (FLUSH) {
+      if (hd[HD_FLUSH] != 0.f) {
+        // exact cold state at this token: decayed snapshot + decayed replay of
+        // the window (buffered tokens and this one), scale/v4_fused_decode.py:76-85
+        const float dtot = hd[HD_DTOT];
+        float nvv[CS][4];
+#pragma unroll
+        for (int s = 0; s < CS; ++s)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) nvv[s][e] = dtot * (COLD == NSSM_COLD_FP32 ? cv[s][e] : mv[s][e]);
+        for (int i = 0; i < m; ++i) {
+          const float coef = sU[i * P + p];
+          const float* bc = sBc + i * NC + 4 * q;
+#pragma unroll
+          for (int s = 0; s < CS; ++s) {
+            const f4 bb = *reinterpret_cast<const f4*>(bc + 32 * s);
+            nvv[s][0] = fmaf(coef, bb.x, nvv[s][0]);
+            nvv[s][1] = fmaf(coef, bb.y, nvv[s][1]);
+            nvv[s][2] = fmaf(coef, bb.z, nvv[s][2]);
+            nvv[s][3] = fmaf(coef, bb.w, nvv[s][3]);
+          }
+        }
+        cold_store<COLD, CS>(a, row, q, nvv);
+      }
+    }
+  }
+  part = sum8(part);
+  if (q == 0) a.y[((size_t)bi * a.H + h) * P + p] = fmaf(hd[HD_D], xp, part);
+}
+
+template <int K, int COLD>
+__global__ void __launch_bounds__(kMaxWaves * 64) step_kernel(StepArgs a) {
+  constexpr int HS = K / 32;
+  constexpr int NC = kN - K;
+  constexpr int CS = NC / 32;
+  constexpr bool TIERED = NC > 0;
+  extern __shared__ float lds[];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+  const int hb = blockIdx.x % a.nhb;
+  const int bg = blockIdx.x / a.nhb;
+  const int g = bg % a.G;
+  const int bi = bg / a.G;
+  const int P = a.P, H = a.H, hpw = a.hpw;
+  const int h0 = g * a.HG + hb * hpw;
+
+  float* sBraw = lds;
+  float* sCraw = sBraw + kN;
+  float* sB = sCraw + kN;
+  float* sC = sB + kN;
+  float* sX = sC + kN;
+  float* sHd = sX + hpw * P;
+  float* sBc = sHd + hpw * HD_STRIDE;       // [c][NC] rotated B cold columns of the window
+  float* sU = sBc + (TIERED ? a.c * NC : 0);  // [c][P] w_i dt_i x_i
+  float* sLa = sU + (TIERED ? a.c * P : 0);   // [c] log decays a_i
+  float* sDt = sLa + (TIERED ? a.c : 0);      // [c] dt_i
+  float* sW = sDt + (TIERED ? a.c : 0);       // [c] w_i dt_i
+
+  const int slot = a.slot_ids ? a.slot_ids[bi] : bi;
+  if (slot < 0 || slot >= a.slots) {  // uniform over the workgroup
+    for (int i = tid; i < hpw * P; i += blockDim.x) a.y[((size_t)bi * H + h0) * P + i] = __builtin_nanf("");
+    return;
+  }
+
+  // 1. stage B, C (fp32), x, per-head scalars
+  {
+    const size_t bgo = ((size_t)bi * a.G + g) * kN;
+    for (int i = tid; i < kN; i += blockDim.x) {
+      sBraw[i] = bf2f(a.Bm[bgo + i]);
+      sCraw[i] = bf2f(a.Cm[bgo + i]);
+    }
+    const size_t xo = ((size_t)bi * H + h0) * P;
+    for (int i = tid; i < hpw * P; i += blockDim.x) sX[i] = bf2f(a.x[xo + i]);
+    if (tid < hpw) {
+      const int h = h0 + tid;
+      float dt = softplus_f(bf2f(a.dt_raw[(size_t)bi * H + h]) + a.dt_bias[h]);
+      if (a.dt_min > 0.f) dt = fmaxf(dt, a.dt_min);
+      const float av = dt * a.A[h];
+      float* hd = sHd + tid * HD_STRIDE;
+      hd[HD_DT] = dt;
+      hd[HD_A] = av;
+      hd[HD_DECAY] = expf(av);
+      hd[HD_D] = a.D[h];
+      if constexpr (TIERED) {
+        // t >= 0 and 0 <= nv < c hold for every tier written by these kernels; the
+        // clamps keep ring indexing inside the buffers even for a corrupted phase
+        const int tt = max(a.t[(size_t)slot * H + h], 0);
+        const int nvv = min(max(a.nv[(size_t)slot * H + h], 0), a.c - 1);
+        hd[HD_EG] = expf(a.glog[(size_t)slot * H + h]);
+        hd[HD_FLUSH] = ((tt + 1) % a.c == 0) ? 1.f : 0.f;
+        hd[HD_T] = __int_as_float(tt);
+        hd[HD_NV] = __int_as_float(nvv);
+      } else {
+        hd[HD_EG] = 0.f;
+        hd[HD_FLUSH] = 0.f;
+      }
+    }
+  }
+  __syncthreads();
+
+  // 2. rotation B' = R_g B, C' = R_g C: half-wave per output row of R
+  if (a.R) {
+    const int hw = lane >> 5, hl = lane & 31;
+    const f4 bv = *reinterpret_cast<const f4*>(sBraw + 4 * hl);
+    const f4 cv = *reinterpret_cast<const f4*>(sCraw + 4 * hl);
+    const float* Rg = a.R + (size_t)g * kN * kN;
+    for (int mrow = 2 * wave + hw; mrow < kN; mrow += 2 * nw) {
+      const f4 r = *reinterpret_cast<const f4*>(Rg + (size_t)mrow * kN + 4 * hl);
+      float db = r.x * bv.x;
+      db = fmaf(r.y, bv.y, db);
+      db = fmaf(r.z, bv.z, db);
+      db = fmaf(r.w, bv.w, db);
+      float dc = r.x * cv.x;
+      dc = fmaf(r.y, cv.y, dc);
+      dc = fmaf(r.z, cv.z, dc);
+      dc = fmaf(r.w, cv.w, dc);
+      db = sum32(db);
+      dc = sum32(dc);
+      if (hl == 0) {
+        sB[mrow] = db;
+        sC[mrow] = dc;
+      }
+    }
+  } else {
+    for (int i = tid; i < kN; i += blockDim.x) {
+      sB[i] = sBraw[i];
+      sC[i] = sCraw[i];
+    }
+  }
+  __syncthreads();
+
+  // 3. per-lane coefficients
+  const int q = lane & 7, rr = lane >> 3;
+  float Bh[HS][4], Ch[HS][4];
+  constexpr int CSR = CS > 0 ? CS : 1;
+  float Cc[CSR][4];
+#pragma unroll
+  for (int s = 0; s < HS; ++s)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      Bh[s][e] = sB[32 * s + 4 * q + e];
+      Ch[s][e] = sC[32 * s + 4 * q + e];
+    }
+#pragma unroll
+  for (int s = 0; s < CSR; ++s)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Cc[s][e] = CS > 0 ? sC[K + 32 * s + 4 * q + e] : 0.f;
+
+  const int RG = P >> 3;
+  bool any_flush = false;
+  if constexpr (TIERED) {
+    for (int j = 0; j < hpw; ++j) any_flush |= sHd[j * HD_STRIDE + HD_FLUSH] != 0.f;
+  }
+
+  if (!any_flush) {
+    const int units = hpw * RG;
+    for (int u = wave; u < units; u += nw) {
+      const int j = u / RG;
+      const int p = (u - j * RG) * 8 + rr;
+      do_unit<K, COLD, false>(a, slot, bi, h0 + j, j, p, q, Bh, Ch, Cc, sX, sHd, sU, sBc, 0);
+    }
+  } else if constexpr (TIERED) {
+    // window: nv buffered tokens at ring positions [c-1-nv, c-1) plus this one
+    const int c = a.c;
+    const int nv0 = __float_as_int(sHd[HD_NV]);
+    const int m = nv0 + 1;
+    {
+      const size_t rb = ((size_t)slot * a.G + g) * c;
+      for (int i = tid; i < (m - 1) * NC; i += blockDim.x) {
+        const int e = i / NC, n = i - e * NC;
+        sBc[i] = a.ring_b[(rb + (c - 1 - nv0 + e)) * NC + n];
+      }
+      for (int n = tid; n < NC; n += blockDim.x) sBc[(m - 1) * NC + n] = sB[K + n];
+    }
+    for (int j = 0; j < hpw; ++j) {
+      const int h = h0 + j;
+      float* hd = sHd + j * HD_STRIDE;
+      const bool fl = hd[HD_FLUSH] != 0.f;
+      __syncthreads();  // sU / sAw of the previous head consumed
+      if (fl) {
+        const size_t rh = ((size_t)slot * H + h) * c;
+        // log decays a_i and dt_i of the window (token i = 0..m-1, the last is this token)
+        if (tid < m) {
+          const float dti = tid < m - 1 ? a.ring_dt[rh + (c - 1 - nv0 + tid)] : hd[HD_DT];
+          sDt[tid] = dti;
+          sLa[tid] = dti * a.A[h];
+        }
+        __syncthreads();
+        // w_i = exp(sum_{l>i} a_l) * dt_i;  total decay exp(sum_l a_l)
+        if (tid < m) {
+          float suf = 0.f;
+          for (int l = m - 1; l > tid; --l) suf += sLa[l];
+          sW[tid] = expf(suf) * sDt[tid];
+          if (tid == 0) hd[HD_DTOT] = expf(suf + sLa[0]);
+        }
+        __syncthreads();
+        for (int i = tid; i < m * P; i += blockDim.x) {
+          const int e = i / P, p = i - e * P;
+          const float xv = e < m - 1 ? bf2f(a.ring_x[(rh + (c - 1 - nv0 + e)) * P + p]) : sX[j * P + p];
+          sU[i] = sW[e] * xv;
+        }
+        __syncthreads();
+        for (int r = wave; r < RG; r += nw)
+          do_unit<K, COLD, true>(a, slot, bi, h, j, r * 8 + rr, q, Bh, Ch, Cc, sX, sHd, sU, sBc, m);
+      } else {
+        for (int r = wave; r < RG; r += nw)
+          do_unit<K, COLD, false>(a, slot, bi, h, j, r * 8 + rr, q, Bh, Ch, Cc, sX, sHd, sU, sBc, 0);
+      }
+    }
+  }
+
+  // 4. ring append (non-flush tokens) and bookkeeping
+  if constexpr (TIERED) {
+    const int c = a.c;
+    for (int j = 0; j < hpw; ++j) {
+      const float* hd = sHd + j * HD_STRIDE;
+      if (hd[HD_FLUSH] != 0.f) continue;
+      const int pos = __float_as_int(hd[HD_T]) % c;
+      const size_t rh = ((size_t)slot * H + h0 + j) * c + pos;
+      const size_t xo = ((size_t)bi * H + h0 + j) * P;
+      for (int p = tid; p < P; p += blockDim.x) a.ring_x[rh * P + p] = a.x[xo + p];
+      if (tid == 0) a.ring_dt[rh] = hd[HD_DT];
+    }
+    if (hb == 0 && sHd[HD_FLUSH] == 0.f) {
+      const int pos = __float_as_int(sHd[HD_T]) % c;
+      const size_t rb = (((size_t)slot * a.G + g) * c + pos) * NC;
+      for (int n = tid; n < NC; n += blockDim.x) a.ring_b[rb + n] = sB[K + n];
+    }
+    if (tid < hpw) {
+      const float* hd = sHd + tid * HD_STRIDE;
+      const size_t o = (size_t)slot * H + h0 + tid;
+      const int tt = __float_as_int(hd[HD_T]);
+      a.t[o] = tt + 1;
+      if (hd[HD_FLUSH] != 0.f) {
+        a.nv[o] = 0;
+        a.glog[o] = 0.f;
+      } else {
+        a.nv[o] = __float_as_int(hd[HD_NV]) + 1;
+        a.glog[o] = a.glog[o] + hd[HD_A];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// join: full state -> tiers; one workgroup per (request, head)
+__global__ void join_kernel(StepArgs a, const float* __restrict__ S, const int32_t* __restrict__ phase, int K,
+                            int kind) {
+  const int bi = blockIdx.x / a.H, h = blockIdx.x % a.H;
+  const int slot = a.slot_ids ? a.slot_ids[bi] : bi;
+  if (slot < 0 || slot >= a.slots) return;
+  const int NC = kN - K;
+  const float* src = S + ((size_t)bi * a.H + h) * a.P * kN;
+  const size_t row0 = ((size_t)slot * a.H + h) * a.P;
+  // element pass (coalesced): hot columns, and the fp32 cold copy or master
+  for (int i = threadIdx.x; i < a.P * kN; i += blockDim.x) {
+    const int p = i / kN, n = i - p * kN;
+    const float v = src[i];
+    if (n < K) {
+      a.hot[(row0 + p) * K + n] = v;
+    } else {
+      float* dst = kind == NSSM_COLD_FP32 ? static_cast<float*>(a.cold) : a.master;
+      dst[(row0 + p) * NC + (n - K)] = v;
+      if (kind == NSSM_COLD_BF16) static_cast<uint16_t*>(a.cold)[(row0 + p) * NC + (n - K)] = nssm_f32_to_bf16(v);
+    }
+  }
+  if (kind == NSSM_COLD_FP8) {  // row pass: per-row amax scale, scale/vllm_v4_patch.py:106-111
+    for (int p = threadIdx.x; p < a.P; p += blockDim.x) {
+      const float* r = src + (size_t)p * kN + K;
+      float am = 0.f;
+      for (int n = 0; n < NC; ++n) am = fmaxf(am, fabsf(r[n]));
+      const float sc = am / 448.0f + 1e-12f;
+      uint8_t* d8 = static_cast<uint8_t*>(a.cold) + (row0 + p) * NC;
+      for (int n = 0; n < NC; ++n) d8[n] = nssm_f32_to_e4m3fn(r[n] / sc);
+      a.scale[row0 + p] = sc;
+    }
+  }
+  if (threadIdx.x == 0) {
+    const size_t o = (size_t)slot * a.H + h;
+    a.t[o] = phase ? phase[bi] : 0;
+    a.nv[o] = 0;
+    a.glog[o] = 0.f;
+  }
+}
+
+// materialize: tiers -> exact full state; one workgroup per (request, head)
+__global__ void materialize_kernel(StepArgs a, float* __restrict__ S, int K, int kind) {
+  __shared__ float w[kMaxC + 1];
+  __shared__ float lg[kMaxC];
+  const int bi = blockIdx.x / a.H, h = blockIdx.x % a.H, g = h / a.HG;
+  const int slot = a.slot_ids ? a.slot_ids[bi] : bi;
+  const int NC = kN - K, c = a.c;
+  if (slot < 0 || slot >= a.slots) {
+    for (int i = threadIdx.x; i < a.P * kN; i += blockDim.x)
+      S[((size_t)bi * a.H + h) * a.P * kN + i] = __builtin_nanf("");
+    return;
+  }
+  const size_t o = (size_t)slot * a.H + h;
+  const int nv = min(max(a.nv[o], 0), c - 1);
+  const int t0 = max(a.t[o] - nv, 0);  // step count at the snapshot; pending token i sits at ring (t0 + i) % c
+  const size_t rh = o * c;
+  if ((int)threadIdx.x < nv) lg[threadIdx.x] = a.ring_dt[rh + (t0 + threadIdx.x) % c] * a.A[h];
+  __syncthreads();
+  if ((int)threadIdx.x < nv) {
+    float suf = 0.f;
+    for (int l = nv - 1; l > (int)threadIdx.x; --l) suf += lg[l];
+    w[threadIdx.x] = expf(suf) * a.ring_dt[rh + (t0 + threadIdx.x) % c];
+    if (threadIdx.x == 0) w[kMaxC] = expf(suf + lg[0]);
+  }
+  if (threadIdx.x == 0 && nv == 0) w[kMaxC] = 1.f;
+  __syncthreads();
+  const float dtot = w[kMaxC];
+  const size_t rbg = ((size_t)slot * a.G + g) * c;
+  for (int p = threadIdx.x; p < a.P; p += blockDim.x) {
+    const size_t row = o * a.P + p;
+    float* dst = S + (((size_t)bi * a.H + h) * a.P + p) * kN;
+    for (int n = 0; n < K; ++n) dst[n] = a.hot[row * K + n];
+    const float* cm = kind == NSSM_COLD_FP32 ? static_cast<const float*>(a.cold) + row * NC : a.master + row * NC;
+    for (int n = 0; n < NC; ++n) {
+      float v = dtot * cm[n];
+      for (int i = 0; i < nv; ++i) {
+        const int pos = (t0 + i) % c;
+        const float u = w[i] * bf2f(a.ring_x[(rh + pos) * a.P + p]);
+        v = fmaf(u, a.ring_b[(rbg + pos) * NC + n], v);
+      }
+      dst[K + n] = v;
+    }
+  }
+}
+
+// fp8 dequant-matvec with per-(row, column) scale; one thread per (row, p)
+__global__ void fp8_readout_kernel(const float* __restrict__ q, const uint8_t* __restrict__ s8,
+                                   const float* __restrict__ scale, float* __restrict__ y, int rows, int nc,
+                                   int pd) {
+  const int r = blockIdx.y;
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows || p >= pd) return;
+  float acc = 0.f;
+  const uint8_t* src = s8 + (size_t)r * nc * pd + p;
+  for (int n = 0; n < nc; ++n) {
+    const float qs = q[(size_t)r * nc + n] * scale[(size_t)r * nc + n];
+    acc = fmaf(qs, nssm_e4m3fn_to_f32(src[(size_t)n * pd]), acc);
+  }
+  y[(size_t)r * pd + p] = acc;
+}
+
+// rotation of flat [T][G][N] bf16 vectors; one workgroup per (t, g), one thread per output m
+__global__ void rotate_kernel(const uint16_t* __restrict__ in, const float* __restrict__ R, float* __restrict__ out,
+                              int G, int N) {
+  extern __shared__ float sv[];
+  const int tg = blockIdx.x, g = tg % G;
+  for (int n = threadIdx.x; n < N; n += blockDim.x) sv[n] = bf2f(in[(size_t)tg * N + n]);
+  __syncthreads();
+  for (int m = threadIdx.x; m < N; m += blockDim.x) {
+    const float* Rr = R + ((size_t)g * N + m) * N;
+    float acc = 0.f;
+    for (int n = 0; n < N; ++n) acc = fmaf(Rr[n], sv[n], acc);
+    out[(size_t)tg * N + m] = acc;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+int g_hpw_override = 0, g_waves_override = 0;
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int check_params(const nssm_layer_params* prm) {
+  if (!prm || !prm->dt_bias || !prm->A || !prm->D) return NSSM_E_NULL;
+  if (prm->N != kN || prm->H <= 0 || prm->G <= 0 || prm->H % prm->G) return NSSM_E_DIMS;
+  if (prm->P <= 0 || prm->P % 16 || prm->P > 256) return NSSM_E_DIMS;
+  if (prm->R && !aligned16(prm->R)) return NSSM_E_ALIGN;
+  return NSSM_OK;
+}
+
+int check_inputs(const nssm_layer_params* prm, const nssm_step_inputs* in, const float* y) {
+  if (!in || !in->x || !in->B || !in->C || !in->dt || !y) return NSSM_E_NULL;
+  if (in->b < 0) return NSSM_E_DIMS;
+  (void)prm;
+  return NSSM_OK;
+}
+
+// largest divisor of n not above cap
+int divisor_at_most(int n, int cap) {
+  for (int d = cap < n ? cap : n; d >= 1; --d)
+    if (n % d == 0) return d;
+  return 1;
+}
+
+struct Launch {
+  int hpw, waves;
+};
+
+int pick_launch(int b, int H, int G, int P, Launch* out) {
+  const int HG = H / G;
+  const int RG = P / 8;
+  int waves = g_waves_override > 0 ? g_waves_override : divisor_at_most(RG, 5);
+  if (waves > kMaxWaves) return NSSM_E_TUNING;
+  int hpw;
+  if (g_hpw_override > 0) {
+    if (HG % g_hpw_override) return NSSM_E_TUNING;
+    hpw = g_hpw_override;
+  } else {
+    // the largest head block that still leaves >= 2048 workgroups (8 per CU)
+    hpw = 1;
+    for (int d = HG; d >= 1; --d)
+      if (HG % d == 0 && (long)b * G * (HG / d) >= 2048) {
+        hpw = d;
+        break;
+      }
+  }
+  out->hpw = hpw;
+  out->waves = waves;
+  return NSSM_OK;
+}
+
+size_t step_lds_bytes(int hpw, int P, int c, int K) {
+  const int NC = kN - K;
+  size_t fl = 4 * kN + (size_t)hpw * P + (size_t)hpw * HD_STRIDE;
+  if (NC > 0) fl += (size_t)c * NC + (size_t)c * P + 3 * (size_t)c;
+  return fl * sizeof(float);
+}
+
+constexpr size_t kMaxLds = 64 * 1024;
+
+template <int K, int COLD>
+int launch_step(const StepArgs& a, int waves, hipStream_t st) {
+  const size_t lds = step_lds_bytes(a.hpw, a.P, a.c, K);
+  if (lds > kMaxLds) return NSSM_E_DIMS;
+  const unsigned grid = (unsigned)a.b * a.G * a.nhb;
+  if (grid == 0) return NSSM_OK;
+  hipLaunchKernelGGL((step_kernel<K, COLD>), dim3(grid), dim3(waves * 64), lds, st, a);
+  return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
+}
+
+void fill_common(StepArgs& a, const nssm_layer_params* prm, const nssm_step_inputs* in, float* y) {
+  a.x = in->x;
+  a.Bm = in->B;
+  a.Cm = in->C;
+  a.dt_raw = in->dt;
+  a.slot_ids = in->slot_ids;
+  a.dt_bias = prm->dt_bias;
+  a.A = prm->A;
+  a.D = prm->D;
+  a.R = prm->R;
+  a.y = y;
+  a.b = in->b;
+  a.H = prm->H;
+  a.P = prm->P;
+  a.G = prm->G;
+  a.HG = prm->H / prm->G;
+  a.dt_min = prm->dt_min;
+}
+
+int check_tier(const nssm_layer_params* prm, const nssm_tier* tr, bool need_ring) {
+  if (!tr || !tr->hot || !tr->cold || !tr->t || !tr->nv || !tr->glog) return NSSM_E_NULL;
+  if (need_ring && (!tr->ring_x || !tr->ring_dt || !tr->ring_b)) return NSSM_E_NULL;
+  if (tr->cold_kind < NSSM_COLD_FP32 || tr->cold_kind > NSSM_COLD_FP8) return NSSM_E_KIND;
+  if (tr->cold_kind != NSSM_COLD_FP32 && !tr->master) return NSSM_E_NULL;
+  if (tr->cold_kind == NSSM_COLD_FP8 && !tr->scale) return NSSM_E_NULL;
+  if (tr->slots <= 0 || tr->c < 1 || tr->c > kMaxC) return NSSM_E_DIMS;
+  if (tr->k_hot != 32 && tr->k_hot != 64 && tr->k_hot != 96) return NSSM_E_DIMS;
+  if (!aligned16(tr->hot) || !aligned16(tr->cold) || (tr->master && !aligned16(tr->master))) return NSSM_E_ALIGN;
+  (void)prm;
+  return NSSM_OK;
+}
+
+void fill_tier(StepArgs& a, const nssm_tier* tr) {
+  a.hot = tr->hot;
+  a.cold = tr->cold;
+  a.scale = tr->scale;
+  a.master = tr->master;
+  a.ring_x = tr->ring_x;
+  a.ring_dt = tr->ring_dt;
+  a.ring_b = tr->ring_b;
+  a.t = tr->t;
+  a.nv = tr->nv;
+  a.glog = tr->glog;
+  a.slots = tr->slots;
+  a.c = tr->c;
+}
+
+template <int K>
+int dispatch_kind(const StepArgs& a, int kind, int waves, hipStream_t st) {
+  switch (kind) {
+    case NSSM_COLD_FP32: return launch_step<K, NSSM_COLD_FP32>(a, waves, st);
+    case NSSM_COLD_BF16: return launch_step<K, NSSM_COLD_BF16>(a, waves, st);
+    case NSSM_COLD_FP8: return launch_step<K, NSSM_COLD_FP8>(a, waves, st);
+  }
+  return NSSM_E_KIND;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+extern "C" {
+
+int nssm_abi_version(void) { return NSSM_ABI_VERSION; }
+
+const char* nssm_strerror(int code) {
+  switch (code) {
+    case NSSM_OK: return "ok";
+    case NSSM_E_NULL: return "a required pointer is NULL";
+    case NSSM_E_DIMS: return "sizes out of the supported range";
+    case NSSM_E_ALIGN: return "a state or parameter pointer is not 16-byte aligned";
+    case NSSM_E_KIND: return "unknown cold storage kind";
+    case NSSM_E_LAUNCH: return "HIP kernel launch failed";
+    case NSSM_E_TUNING: return "launch override does not fit the dimensions";
+  }
+  return "unknown nssm error";
+}
+
+int nssm_tier_sizes(int32_t slots, int32_t H, int32_t P, int32_t N, int32_t G, int32_t k_hot, int32_t c,
+                    int32_t cold_kind, int64_t* sz) {
+  if (!sz) return NSSM_E_NULL;
+  if (slots <= 0 || H <= 0 || P <= 0 || N != kN || G <= 0 || k_hot <= 0 || k_hot >= N || c < 1 || c > kMaxC)
+    return NSSM_E_DIMS;
+  if (cold_kind < NSSM_COLD_FP32 || cold_kind > NSSM_COLD_FP8) return NSSM_E_KIND;
+  const int64_t rows = (int64_t)slots * H * P;
+  const int64_t NC = N - k_hot;
+  const int64_t esz = cold_kind == NSSM_COLD_FP32 ? 4 : cold_kind == NSSM_COLD_BF16 ? 2 : 1;
+  sz[0] = rows * k_hot * 4;
+  sz[1] = rows * NC * esz;
+  sz[2] = cold_kind == NSSM_COLD_FP8 ? rows * 4 : 0;
+  sz[3] = cold_kind == NSSM_COLD_FP32 ? 0 : rows * NC * 4;
+  sz[4] = (int64_t)slots * H * c * P * 2;
+  sz[5] = (int64_t)slots * H * c * 4;
+  sz[6] = (int64_t)slots * G * c * NC * 4;
+  sz[7] = (int64_t)slots * H * 4;
+  sz[8] = (int64_t)slots * H * 4;
+  sz[9] = (int64_t)slots * H * 4;
+  return NSSM_OK;
+}
+
+int nssm_set_launch(int32_t heads_per_wg, int32_t waves_per_wg) {
+  if (heads_per_wg < 0 || waves_per_wg < 0 || waves_per_wg > kMaxWaves) return NSSM_E_TUNING;
+  g_hpw_override = heads_per_wg;
+  g_waves_override = waves_per_wg;
+  return NSSM_OK;
+}
+
+int nssm_fresh_step(const nssm_layer_params* prm, float* state, int32_t slots, const nssm_step_inputs* in,
+                    float* y, void* stream) {
+  int rc = check_params(prm);
+  if (rc) return rc;
+  if ((rc = check_inputs(prm, in, y))) return rc;
+  if (!state) return NSSM_E_NULL;
+  if (!aligned16(state)) return NSSM_E_ALIGN;
+  if (slots <= 0 || (!in->slot_ids && in->b > slots)) return NSSM_E_DIMS;
+  StepArgs a = {};
+  fill_common(a, prm, in, y);
+  a.hot = state;
+  a.slots = slots;
+  a.c = 1;
+  Launch L;
+  if ((rc = pick_launch(in->b, prm->H, prm->G, prm->P, &L))) return rc;
+  a.hpw = L.hpw;
+  a.nhb = a.HG / L.hpw;
+  return launch_step<kN, NSSM_COLD_FP32>(a, L.waves, (hipStream_t)stream);
+}
+
+int nssm_v4_step(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step_inputs* in, float* y,
+                 void* stream) {
+  int rc = check_params(prm);
+  if (rc) return rc;
+  if ((rc = check_inputs(prm, in, y))) return rc;
+  if ((rc = check_tier(prm, tier, true))) return rc;
+  if (!in->slot_ids && in->b > tier->slots) return NSSM_E_DIMS;
+  StepArgs a = {};
+  fill_common(a, prm, in, y);
+  fill_tier(a, tier);
+  Launch L;
+  if ((rc = pick_launch(in->b, prm->H, prm->G, prm->P, &L))) return rc;
+  a.hpw = L.hpw;
+  a.nhb = a.HG / L.hpw;
+  hipStream_t st = (hipStream_t)stream;
+  switch (tier->k_hot) {
+    case 32: return dispatch_kind<32>(a, tier->cold_kind, L.waves, st);
+    case 64: return dispatch_kind<64>(a, tier->cold_kind, L.waves, st);
+    case 96: return dispatch_kind<96>(a, tier->cold_kind, L.waves, st);
+  }
+  return NSSM_E_DIMS;
+}
+
+int nssm_v4_join(const nssm_layer_params* prm, const nssm_tier* tier, const float* state, int32_t b,
+                 const int32_t* slot_ids, const int32_t* phase, void* stream) {
+  int rc = check_params(prm);
+  if (rc) return rc;
+  if ((rc = check_tier(prm, tier, false))) return rc;
+  if (!state) return NSSM_E_NULL;
+  if (b < 0 || (!slot_ids && b > tier->slots)) return NSSM_E_DIMS;
+  if (b == 0) return NSSM_OK;
+  StepArgs a = {};
+  fill_tier(a, tier);
+  a.slot_ids = slot_ids;
+  a.H = prm->H;
+  a.P = prm->P;
+  a.G = prm->G;
+  a.HG = prm->H / prm->G;
+  hipLaunchKernelGGL(join_kernel, dim3((unsigned)b * prm->H), dim3(128), 0, (hipStream_t)stream, a, state, phase,
+                     (int)tier->k_hot, (int)tier->cold_kind);
+  return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
+}
+
+int nssm_v4_materialize(const nssm_layer_params* prm, const nssm_tier* tier, float* state_out, int32_t b,
+                        const int32_t* slot_ids, void* stream) {
+  int rc = check_params(prm);
+  if (rc) return rc;
+  if ((rc = check_tier(prm, tier, true))) return rc;
+  if (!state_out) return NSSM_E_NULL;
+  if (b < 0 || (!slot_ids && b > tier->slots)) return NSSM_E_DIMS;
+  if (b == 0) return NSSM_OK;
+  StepArgs a = {};
+  fill_tier(a, tier);
+  a.slot_ids = slot_ids;
+  a.A = prm->A;
+  a.H = prm->H;
+  a.P = prm->P;
+  a.G = prm->G;
+  a.HG = prm->H / prm->G;
+  hipLaunchKernelGGL(materialize_kernel, dim3((unsigned)b * prm->H), dim3(128), 0, (hipStream_t)stream, a,
+                     state_out, (int)tier->k_hot, (int)tier->cold_kind);
+  return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
+}
+
+int nssm_fp8_readout(const float* q, const uint8_t* s8, const float* scale, float* y, int32_t rows, int32_t nc,
+                     int32_t pd, void* stream) {
+  if (!q || !s8 || !scale || !y) return NSSM_E_NULL;
+  if (rows < 0 || nc <= 0 || pd <= 0) return NSSM_E_DIMS;
+  if (rows == 0) return NSSM_OK;
+  dim3 grid((unsigned)((pd + 127) / 128), (unsigned)rows);
+  hipLaunchKernelGGL(fp8_readout_kernel, grid, dim3(128), 0, (hipStream_t)stream, q, s8, scale, y, rows, nc, pd);
+  return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
+}
+
+int nssm_rotate(const uint16_t* in, const float* R, float* out, int32_t T, int32_t G, int32_t N, void* stream) {
+  if (!in || !R || !out) return NSSM_E_NULL;
+  if (T < 0 || G <= 0 || N <= 0 || N > 1024) return NSSM_E_DIMS;
+  if (T == 0) return NSSM_OK;
+  hipLaunchKernelGGL(rotate_kernel, dim3((unsigned)T * G), dim3(128), N * sizeof(float), (hipStream_t)stream, in,
+                     R, out, G, N);
+  return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
+}
+
+void nssm_host_f32_to_e4m3fn(const float* in, uint8_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = nssm_f32_to_e4m3fn(in[i]);
+}
+void nssm_host_e4m3fn_to_f32(const uint8_t* in, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = nssm_e4m3fn_to_f32(in[i]);
+}
+void nssm_host_f32_to_bf16(const float* in, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = nssm_f32_to_bf16(in[i]);
+}
+
+}  // extern "C"

@@ -1,0 +1,210 @@
+"""Host-side API over the C ABI: torch tensors in, HIP kernels on the current stream.
+
+PyTorch is only the allocator and stream provider here; every state update
+runs in libnssm_hip.so. Nothing in this module has a CPU path: inputs must be
+CUDA (HIP) tensors and the library must be built.
+"""
+import ctypes
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import COLD_KINDS, NssmError, TIER_FIELDS, check, lib
+
+N_STATE = 128
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _need(t: torch.Tensor, name: str, dtype: torch.dtype, shape: tuple):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be on the GPU (got {t.device}); there is no CPU path")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype} (got {t.dtype})")
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)} (got {tuple(t.shape)})")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+@dataclass
+class LayerParams:
+    """Per-layer constants on the GPU: dt_bias, A = -exp(A_log), D [H] fp32, R [G,N,N] fp32."""
+    H: int
+    P: int
+    N: int
+    G: int
+    dt_bias: torch.Tensor
+    A: torch.Tensor
+    D: torch.Tensor
+    R: Optional[torch.Tensor] = None
+    dt_min: float = 0.0
+
+    @classmethod
+    def from_mixer_values(cls, dt_bias, A_log, D, R=None, P=80, G=8, dt_min=0.0, device="cuda"):
+        """Build from the mixer's parameters (A_log as stored by NemotronH)."""
+        f = dict(device=device, dtype=torch.float32)
+        H = dt_bias.numel()
+        A = -torch.exp(A_log.detach().float()).to(**f)
+        Rt = None if R is None else R.detach().to(**f).contiguous()
+        N = N_STATE if Rt is None else Rt.shape[-1]
+        return cls(H, P, N, G, dt_bias.detach().to(**f).contiguous(), A.contiguous(),
+                   D.detach().to(**f).contiguous(), Rt, dt_min)
+
+    def validate(self):
+        if self.N != N_STATE:
+            raise ValueError(f"d_state must be {N_STATE} (got {self.N})")
+        for nm in ("dt_bias", "A", "D"):
+            _need(getattr(self, nm), nm, torch.float32, (self.H,))
+        if self.R is not None:
+            _need(self.R, "R", torch.float32, (self.G, self.N, self.N))
+
+    def c_struct(self) -> _lib.LayerParams:
+        self.validate()
+        return _lib.LayerParams(self.H, self.P, self.N, self.G, _ptr(self.dt_bias), _ptr(self.A),
+                                _ptr(self.D), _ptr(self.R), float(self.dt_min))
+
+
+def _inputs(prm: LayerParams, x, B, C, dt, slot_ids) -> _lib.StepInputs:
+    b = x.shape[0]
+    _need(x, "x", torch.bfloat16, (b, prm.H, prm.P))
+    _need(B, "B", torch.bfloat16, (b, prm.G, prm.N))
+    _need(C, "C", torch.bfloat16, (b, prm.G, prm.N))
+    _need(dt, "dt", torch.bfloat16, (b, prm.H))
+    if slot_ids is not None:
+        _need(slot_ids, "slot_ids", torch.int32, (b,))
+    return _lib.StepInputs(b, _ptr(x), _ptr(B), _ptr(C), _ptr(dt), _ptr(slot_ids))
+
+
+def fresh_step(prm: LayerParams, state: torch.Tensor, x, B, C, dt, y: Optional[torch.Tensor] = None,
+               slot_ids: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Untiered step over state [slots,H,P,N] fp32 (in place); returns y [b,H,P] fp32."""
+    slots = state.shape[0]
+    _need(state, "state", torch.float32, (slots, prm.H, prm.P, prm.N))
+    b = x.shape[0]
+    if y is None:
+        y = torch.empty(b, prm.H, prm.P, device=x.device, dtype=torch.float32)
+    _need(y, "y", torch.float32, (b, prm.H, prm.P))
+    pc, ic = prm.c_struct(), _inputs(prm, x, B, C, dt, slot_ids)
+    check(lib().nssm_fresh_step(ctypes.byref(pc), state.data_ptr(), slots, ctypes.byref(ic), y.data_ptr(),
+                                _stream()), "nssm_fresh_step")
+    return y
+
+
+class V4Tier:
+    """Tiered state of one layer for `slots` sequence slots (hot fp32 [slots,H,P,K],
+    cold fp32/bf16/fp8 [slots,H,P,NC] (+ fp32 master and per-row scale), ring of
+    the last c tokens, per-(slot, head) t / nv / glog). Layout as in include/nssm.h."""
+
+    def __init__(self, slots: int, H: int, P: int, G: int, k_hot: int = 32, c: int = 4, cold: str = "fp32",
+                 device="cuda", N: int = N_STATE):
+        if cold not in COLD_KINDS:
+            raise ValueError(f"cold must be one of {sorted(COLD_KINDS)} (got {cold!r})")
+        self.slots, self.H, self.P, self.G, self.N, self.k, self.c, self.cold = slots, H, P, G, N, k_hot, c, cold
+        self.kind = COLD_KINDS[cold]
+        sizes = (ctypes.c_int64 * 10)()
+        check(lib().nssm_tier_sizes(slots, H, P, N, G, k_hot, c, self.kind, sizes), "nssm_tier_sizes")
+        NC = N - k_hot
+        cold_dt = {"fp32": torch.float32, "bf16": torch.bfloat16, "fp8": torch.uint8}[cold]
+        dev = torch.device(device)
+        e = lambda shape, dt: torch.empty(shape, device=dev, dtype=dt)  # noqa: E731
+        self.hot = e((slots, H, P, k_hot), torch.float32)
+        self.cold_t = e((slots, H, P, NC), cold_dt)
+        self.scale = e((slots, H, P), torch.float32) if cold == "fp8" else None
+        self.master = e((slots, H, P, NC), torch.float32) if cold != "fp32" else None
+        self.ring_x = e((slots, H, c, P), torch.bfloat16)
+        self.ring_dt = e((slots, H, c), torch.float32)
+        self.ring_b = e((slots, G, c, NC), torch.float32)
+        self.t = torch.zeros((slots, H), device=dev, dtype=torch.int32)
+        self.nv = torch.zeros((slots, H), device=dev, dtype=torch.int32)
+        self.glog = torch.zeros((slots, H), device=dev, dtype=torch.float32)
+        got = [self._field(f) for f in TIER_FIELDS]
+        for f, tns, want in zip(TIER_FIELDS, got, sizes):
+            have = 0 if tns is None else tns.numel() * tns.element_size()
+            if have != want:
+                raise NssmError(f"tier buffer {f}: {have} bytes allocated, library expects {want}")
+
+    def _field(self, f):
+        return self.cold_t if f == "cold" else getattr(self, f)
+
+    def nbytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in (self._field(f) for f in TIER_FIELDS) if t is not None)
+
+    def c_struct(self) -> _lib.Tier:
+        return _lib.Tier(self.slots, self.k, self.c, self.kind, *[_ptr(self._field(f)) for f in TIER_FIELDS])
+
+    def join(self, prm: LayerParams, state: torch.Tensor, slot_ids: Optional[torch.Tensor] = None,
+             phase: Optional[torch.Tensor] = None):
+        """Capture full states [b,H,P,N] fp32 into slots (end of prefill)."""
+        b = state.shape[0]
+        _need(state, "state", torch.float32, (b, self.H, self.P, self.N))
+        if slot_ids is not None:
+            _need(slot_ids, "slot_ids", torch.int32, (b,))
+        if phase is not None:
+            _need(phase, "phase", torch.int32, (b,))
+        pc, tc = prm.c_struct(), self.c_struct()
+        check(lib().nssm_v4_join(ctypes.byref(pc), ctypes.byref(tc), state.data_ptr(), b, _ptr(slot_ids),
+                                 _ptr(phase), _stream()), "nssm_v4_join")
+
+    def step(self, prm: LayerParams, x, B, C, dt, y: Optional[torch.Tensor] = None,
+             slot_ids: Optional[torch.Tensor] = None) -> torch.Tensor:
+        b = x.shape[0]
+        if y is None:
+            y = torch.empty(b, prm.H, prm.P, device=x.device, dtype=torch.float32)
+        _need(y, "y", torch.float32, (b, prm.H, prm.P))
+        pc, ic, tc = prm.c_struct(), _inputs(prm, x, B, C, dt, slot_ids), self.c_struct()
+        check(lib().nssm_v4_step(ctypes.byref(pc), ctypes.byref(tc), ctypes.byref(ic), y.data_ptr(), _stream()),
+              "nssm_v4_step")
+        return y
+
+    def materialize(self, prm: LayerParams, slot_ids: Optional[torch.Tensor] = None,
+                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Exact current full state [b,H,P,N] fp32 of the slots (the tier is unchanged)."""
+        b = self.slots if slot_ids is None else slot_ids.shape[0]
+        if out is None:
+            out = torch.empty(b, self.H, self.P, self.N, device=self.hot.device, dtype=torch.float32)
+        _need(out, "out", torch.float32, (b, self.H, self.P, self.N))
+        if slot_ids is not None:
+            _need(slot_ids, "slot_ids", torch.int32, (b,))
+        pc, tc = prm.c_struct(), self.c_struct()
+        check(lib().nssm_v4_materialize(ctypes.byref(pc), ctypes.byref(tc), out.data_ptr(), b, _ptr(slot_ids),
+                                        _stream()), "nssm_v4_materialize")
+        return out
+
+
+def fp8_cold_readout(qc: torch.Tensor, S8: torch.Tensor, scale: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """y[r,p] = sum_n qc[r,n] scale[r,n] fp8(S8[r,n,p]) (scale/bench_v4_decode.py:55-60)."""
+    R_, Nc, Pd = S8.shape
+    s8 = S8.view(torch.uint8) if S8.dtype == torch.float8_e4m3fn else S8
+    _need(qc, "qc", torch.float32, (R_, Nc))
+    _need(s8, "S8", torch.uint8, (R_, Nc, Pd))
+    _need(scale, "scale", torch.float32, (R_, Nc))
+    _need(out, "out", torch.float32, (R_, Pd))
+    check(lib().nssm_fp8_readout(qc.data_ptr(), s8.data_ptr(), scale.data_ptr(), out.data_ptr(), R_, Nc, Pd,
+                                 _stream()), "nssm_fp8_readout")
+    return out
+
+
+def rotate(X: torch.Tensor, R: torch.Tensor) -> torch.Tensor:
+    """out[t,g,m] = sum_n R[g,m,n] X[t,g,n] for bf16 X [T,G,N]; fp32 out."""
+    T, G, N = X.shape
+    _need(X, "X", torch.bfloat16, (T, G, N))
+    _need(R, "R", torch.float32, (G, N, N))
+    out = torch.empty(T, G, N, device=X.device, dtype=torch.float32)
+    check(lib().nssm_rotate(X.data_ptr(), R.data_ptr(), out.data_ptr(), T, G, N, _stream()), "nssm_rotate")
+    return out
+
+
+def set_launch(heads_per_wg: int = 0, waves_per_wg: int = 0) -> None:
+    """Override the step kernels' launch shape (0, 0 = automatic)."""
+    check(lib().nssm_set_launch(heads_per_wg, waves_per_wg), "nssm_set_launch")

@@ -1,0 +1,34 @@
+"""CPU oracle for the Mamba2 v4 tiered decode step — TEST INFRASTRUCTURE ONLY.
+
+This package restates, in plain PyTorch on the CPU, the arithmetic of the
+reference repository's decode step (omin-Kwon/nested_ssm, scale/*.py). It is
+the checker: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+leg may import it, and never as the thing that is measured or shipped. The
+product path (nested_ssm_amd) never imports it and has no CPU fallback.
+
+Precision convention (one fp32 convention for the whole path, as the
+reference's variants disagree on bf16 intermediates):
+  * bf16 inputs (x, B, C, dt) are upcast to fp32 first, as
+    scale/nemo9b_eval.py:35-40 does; every later operation is fp32.
+  * R is applied in fp32 without re-rounding to bf16 (scale/v4_fused_decode.py:47-48
+    rounds to bf16; scale/v4_native_decode.py applies it in bf16) — deviation.
+  * The flush contraction is fp32 (scale/v4_fused_decode.py:80-82 runs it in bf16) — deviation.
+  * glog is per (slot, head) as in scale/v4_fused_decode.py:130 and
+    scale/vllm_v4_patch.py:100 (scale/v4_native_decode.py:241 keeps the same
+    value replicated over P).
+
+Pinning status of each function (how it is checked, in tests/test_oracle.py):
+  rotate            closed form vs fp64 matmul; orthogonality of make_rotation
+  fresh_step        transformers' own mamba2_selective_state_update (fp32
+                    inputs), an fp64 per-element loop, rotation invariance
+  NativeV4          k = N reduces to fresh; c = 1 is one-step stale; state
+                    after every flush equals the fresh state; fp64 brute force
+  TieredV4          equals NativeV4 in fp64 (chunked replay == per-token
+                    recurrence), including ragged phases and join/leave
+  quant_fp8 / read  torch float8_e4m3fn cast; scale = amax/448 + 1e-12 per row
+  fp8_readout       closed form of the reference docstring vs an fp64 loop
+"""
+from .v4_ref import (  # noqa: F401
+    LayerParams, NativeV4, TieredV4, fp8_readout, fresh_step, make_layer_params,
+    make_rotation, make_state, make_step_inputs, quant_fp8, read_fp8, rotate, softplus_dt,
+)

@@ -1,0 +1,284 @@
+"""CPU restatement of the reference decode step (test infrastructure only).
+
+Every function cites the reference file:line it follows (omin-Kwon/nested_ssm).
+Tensors are torch CPU tensors; `dtype` selects fp32 (the parity convention)
+or fp64 (for pinning the fp32 path against exact-ish arithmetic).
+"""
+from dataclasses import dataclass
+import math
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+
+E4M3_MAX = 448.0
+
+
+# ---------------------------------------------------------------------------
+# parameters and synthetic inputs
+@dataclass
+class LayerParams:
+    H: int
+    P: int
+    N: int
+    G: int
+    dt_bias: torch.Tensor  # [H]
+    A: torch.Tensor        # [H] = -exp(A_log)
+    D: torch.Tensor        # [H]
+    R: Optional[torch.Tensor]  # [G, N, N] or None (identity)
+    dt_min: float = 0.0
+
+    def to(self, dtype):
+        return LayerParams(self.H, self.P, self.N, self.G, self.dt_bias.to(dtype), self.A.to(dtype),
+                           self.D.to(dtype), None if self.R is None else self.R.to(dtype), self.dt_min)
+
+
+def make_rotation(G: int, N: int, gen: torch.Generator) -> torch.Tensor:
+    """Q of QR(N(0,1)) with the sign fix Q * sign(diag(R_qr)), as the reference
+    retracts R to orthogonal (scale/nemotron_retrofit.py:359-363)."""
+    W = torch.randn(G, N, N, generator=gen, dtype=torch.float64)
+    Q, Rr = torch.linalg.qr(W)
+    sgn = torch.sign(torch.diagonal(Rr, dim1=-2, dim2=-1))
+    return (Q * sgn[..., None, :]).to(torch.float32)
+
+
+def make_layer_params(H: int, P: int, N: int, G: int, gen: torch.Generator, rotation: bool = True,
+                      dt_min: float = 0.0) -> LayerParams:
+    """Per-head dt_bias = log(expm1(U(1e-3, 1e-1))), A = -exp(U(0, ln 16)), D ~ N(0,1);
+    per-group R (the synthetic distributions of the benchmark configurations)."""
+    u = 1e-3 + (1e-1 - 1e-3) * torch.rand(H, generator=gen, dtype=torch.float64)
+    dt_bias = torch.log(torch.expm1(u)).to(torch.float32)
+    A = -torch.exp(torch.rand(H, generator=gen, dtype=torch.float64) * math.log(16.0)).to(torch.float32)
+    D = torch.randn(H, generator=gen, dtype=torch.float32)
+    R = make_rotation(G, N, gen) if rotation else None
+    return LayerParams(H, P, N, G, dt_bias, A, D, R, dt_min)
+
+
+def make_state(slots: int, H: int, P: int, N: int, gen: torch.Generator, std: float = 0.1) -> torch.Tensor:
+    """fp32 state ~ N(0, std^2) (std read as 0.1)."""
+    return torch.randn(slots, H, P, N, generator=gen, dtype=torch.float32) * std
+
+
+def make_step_inputs(b: int, H: int, P: int, N: int, G: int, gen: torch.Generator):
+    """One decode token: x ~ N(0,1), B, C ~ N(0,1)/sqrt(N), dt_raw ~ N(0,1), all bf16."""
+    x = torch.randn(b, H, P, generator=gen).to(torch.bfloat16)
+    B = (torch.randn(b, G, N, generator=gen) / math.sqrt(N)).to(torch.bfloat16)
+    C = (torch.randn(b, G, N, generator=gen) / math.sqrt(N)).to(torch.bfloat16)
+    dt = torch.randn(b, H, generator=gen).to(torch.bfloat16)
+    return x, B, C, dt
+
+
+# ---------------------------------------------------------------------------
+# building blocks
+def rotate(X: torch.Tensor, R: Optional[torch.Tensor]) -> torch.Tensor:
+    """B' = R_g B per group: einsum('bgn,gmn->bgm') — scale/v4_fused_decode.py:47-48,
+    scale/nemotron_retrofit.py:24-27, scale/vllm_v4_patch.py:41-45."""
+    if R is None:
+        return X
+    return torch.einsum("bgn,gmn->bgm", X, R.to(X.dtype))
+
+
+def softplus_dt(dt_raw: torch.Tensor, dt_bias: torch.Tensor, dt_min: float = 0.0) -> torch.Tensor:
+    """dt = softplus(dt_raw + dt_bias) [b,H], optional clamp(dt, dt_min) —
+    scale/v4_native_decode.py:54-55 (clamp only on that path)."""
+    dt = F.softplus(dt_raw + dt_bias[None, :])
+    if dt_min > 0:
+        dt = torch.clamp(dt, min=dt_min)
+    return dt
+
+
+def _heads(v: torch.Tensor, H: int) -> torch.Tensor:
+    """Group -> head broadcast: head h reads group h // (H/G) — scale/v4_native_decode.py:59-61."""
+    G = v.shape[1]
+    return v.repeat_interleave(H // G, dim=1)
+
+
+def _prep(x, B, C, dt_raw, prm: LayerParams, dtype):
+    xf = x.to(dtype)
+    Bp = _heads(rotate(B.to(dtype), prm.R), prm.H)
+    Cp = _heads(rotate(C.to(dtype), prm.R), prm.H)
+    dt = softplus_dt(dt_raw.to(dtype), prm.dt_bias, prm.dt_min)
+    a = dt * prm.A[None, :]
+    return xf, Bp, Cp, dt, a
+
+
+def quant_fp8(s: torch.Tensor):
+    """Per-row e4m3fn quantization, scale = amax_over_last_dim / 448 + 1e-12 —
+    scale/vllm_v4_patch.py:106-111 (_quant_store). Returns (codes, scale[...,1])."""
+    sc = s.abs().amax(dim=-1, keepdim=True) / E4M3_MAX + 1e-12
+    return (s / sc).to(torch.float8_e4m3fn), sc
+
+
+def read_fp8(q: torch.Tensor, sc: torch.Tensor) -> torch.Tensor:
+    """Dequantized snapshot q.float() * scale — scale/vllm_v4_patch.py:116-120 (_read_snap)."""
+    return q.float() * sc
+
+
+def fp8_readout(q: torch.Tensor, S8: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """y[r,p] = sum_n q[r,n] scale[r,n] fp8(S8[r,n,p]) — the _fp8_matvec docstring,
+    scale/bench_v4_decode.py:33-52."""
+    return torch.einsum("rn,rnp->rp", q.float() * scale.float(), S8.float())
+
+
+# ---------------------------------------------------------------------------
+# fresh (untiered) step
+def fresh_step(S: torch.Tensor, x, B, C, dt_raw, prm: LayerParams, dtype=torch.float32) -> torch.Tensor:
+    """S <- exp(dt A) S + (dt B') x;  y = S C' + D x  (S updated in place, y returned).
+    scale/v4_native_decode.py:49-78 with pb >= N (the R applied by ActRotMask),
+    the same recurrence as transformers' mamba2_selective_state_update."""
+    xf, Bp, Cp, dt, a = _prep(x, B, C, dt_raw, prm, dtype)
+    dA = torch.exp(a)[..., None, None]
+    dB = dt[..., None, None] * Bp[:, :, None, :]
+    S.copy_(S * dA + dB * xf[..., None])
+    y = torch.einsum("bhpn,bhn->bhp", S, Cp)
+    return y + xf * prm.D[None, :, None]
+
+
+# ---------------------------------------------------------------------------
+class NativeV4:
+    """v4 with the full state kept fresh and a stale cold snapshot — the
+    reference semantics: scale/v4_native_decode.py:58-167 (decode) and
+    :234-243 (snapshot at prefill end), with the per-slot phase of
+    scale/vllm_v4_patch.py:123-179 so requests may join and leave.
+
+    cold: "fp32" (snapshot clone), "bf16" (snap.to(bf16).float(),
+    v4_native_decode.py:162-163), "fp8" (per-row scale, vllm_v4_patch.py:106-120).
+    fp8_restore_each_step re-stores the dequantized old snapshot for slots that
+    do not flush, as scale/vllm_v4_patch.py:173-175 does.
+    """
+
+    def __init__(self, slots: int, H: int, P: int, N: int, k: int, c: int, cold: str = "fp32",
+                 dtype=torch.float32, fp8_restore_each_step: bool = True):
+        assert 0 < k <= N and c >= 1 and cold in ("fp32", "bf16", "fp8")
+        self.k, self.c, self.cold, self.dtype = k, c, cold, dtype
+        self.fp8_restore = fp8_restore_each_step
+        self.S = torch.zeros(slots, H, P, N, dtype=dtype)
+        Nc = N - k
+        self.snap = torch.zeros(slots, H, P, Nc, dtype=dtype)          # fp32 / bf16-rounded values
+        self.q8 = torch.zeros(slots, H, P, Nc, dtype=torch.float8_e4m3fn)
+        self.sc8 = torch.ones(slots, H, P, 1, dtype=torch.float32)
+        self.glog = torch.zeros(slots, H, dtype=dtype)
+        self.t = torch.zeros(slots, dtype=torch.int64)
+
+    def _store(self, slots, s_cold):
+        if self.cold == "fp8":
+            q, sc = quant_fp8(s_cold.float())
+            self.q8[slots] = q
+            self.sc8[slots] = sc
+        elif self.cold == "bf16":
+            self.snap[slots] = s_cold.to(torch.bfloat16).to(self.dtype)
+        else:
+            self.snap[slots] = s_cold.clone()
+
+    def _read(self, slots):
+        if self.cold == "fp8":
+            return read_fp8(self.q8[slots], self.sc8[slots]).to(self.dtype)
+        return self.snap[slots]
+
+    def join(self, slots: torch.Tensor, S_new: torch.Tensor, phase: Optional[torch.Tensor] = None):
+        """End of prefill for `slots`: S = S_new, snapshot of its cold columns, glog = 0,
+        t = phase (0 by default) — scale/vllm_v4_patch.py:123-137."""
+        slots = torch.as_tensor(slots, dtype=torch.long)
+        self.S[slots] = S_new.to(self.dtype)
+        self._store(slots, self.S[slots][..., self.k:])
+        self.glog[slots] = 0
+        self.t[slots] = 0 if phase is None else torch.as_tensor(phase, dtype=torch.int64)
+
+    def step(self, x, B, C, dt_raw, prm: LayerParams, slots: Optional[torch.Tensor] = None) -> torch.Tensor:
+        b = x.shape[0]
+        slots = torch.arange(b) if slots is None else torch.as_tensor(slots, dtype=torch.long)
+        k, c = self.k, self.c
+        prm = prm.to(self.dtype)
+        xf, Bp, Cp, dt, a = _prep(x, B, C, dt_raw, prm, self.dtype)
+        S = self.S[slots]
+        S = S * torch.exp(a)[..., None, None] + (dt[..., None, None] * Bp[:, :, None, :]) * xf[..., None]
+        self.S[slots] = S
+        glog = self.glog[slots]
+        y_cold = torch.einsum("bhpn,bhn->bhp", self._read(slots), Cp[..., k:]) * torch.exp(glog)[..., None]
+        y = torch.einsum("bhpn,bhn->bhp", S[..., :k], Cp[..., :k]) + y_cold
+        t = self.t[slots] + 1
+        self.t[slots] = t
+        flush = (t % c == 0)
+        if self.cold == "fp8" and self.fp8_restore:
+            old = self._read(slots)
+            self._store(slots, torch.where(flush[:, None, None, None], S[..., k:], old))
+        elif bool(flush.any()):
+            fs = slots[flush]
+            self._store(fs, S[flush][..., k:])
+        self.glog[slots] = torch.where(flush[:, None], torch.zeros_like(glog), glog + a)
+        return y + xf * prm.D[None, :, None]
+
+
+# ---------------------------------------------------------------------------
+class TieredV4:
+    """v4 with tier-split storage and a chunked flush — scale/v4_fused_decode.py:28-95
+    (hot slice updated every token, stale cold readout with exp(glog), ring of
+    (dt x, B'_cold, dt A), flush = exp(sum a) snap + sum_j exp(sum_{i>j} a_i)
+    (dt_j x_j) (x) B'_j, :76-85), generalised to per-slot phases. The hot/cold
+    split does not hold the full state: the exact cold state exists only right
+    after a flush. materialize() rebuilds it from the pending ring entries."""
+
+    def __init__(self, slots: int, H: int, P: int, N: int, G: int, k: int, c: int, dtype=torch.float32):
+        assert 0 < k < N and c >= 1
+        self.H, self.P, self.N, self.G, self.k, self.c, self.dtype = H, P, N, G, k, c, dtype
+        self.hot = torch.zeros(slots, H, P, k, dtype=dtype)
+        self.cold = torch.zeros(slots, H, P, N - k, dtype=dtype)
+        self.glog = torch.zeros(slots, H, dtype=dtype)
+        self.t = torch.zeros(slots, dtype=torch.int64)
+        self.ring = [[] for _ in range(slots)]  # per slot: list of (dt [H], x [H,P], B'cold [H,Nc])
+
+    def join(self, slots, S_new, phase=None):
+        slots = torch.as_tensor(slots, dtype=torch.long)
+        S_new = S_new.to(self.dtype)
+        self.hot[slots] = S_new[..., :self.k]
+        self.cold[slots] = S_new[..., self.k:]
+        self.glog[slots] = 0
+        self.t[slots] = 0 if phase is None else torch.as_tensor(phase, dtype=torch.int64)
+        for s in slots.tolist():
+            self.ring[s] = []
+
+    def _replay(self, cold0, entries, A):
+        """exp(sum a) cold0 + sum_j exp(sum_{i>j} a_i) dt_j x_j (x) B'_j."""
+        if not entries:
+            return cold0
+        dts = torch.stack([e[0] for e in entries])           # [m,H]
+        a = dts * A[None, :]
+        suf = torch.flip(torch.cumsum(torch.flip(a, [0]), 0), [0]) - a
+        w = torch.exp(suf) * dts                             # [m,H]
+        X = torch.stack([e[1] for e in entries])              # [m,H,P]
+        Bc = torch.stack([e[2] for e in entries])             # [m,H,Nc]
+        upd = torch.einsum("mh,mhp,mhn->hpn", w, X, Bc)
+        return cold0 * torch.exp(a.sum(0))[:, None, None] + upd
+
+    def step(self, x, B, C, dt_raw, prm: LayerParams, slots=None):
+        b = x.shape[0]
+        slots = torch.arange(b) if slots is None else torch.as_tensor(slots, dtype=torch.long)
+        k, c = self.k, self.c
+        prm = prm.to(self.dtype)
+        xf, Bp, Cp, dt, a = _prep(x, B, C, dt_raw, prm, self.dtype)
+        hot = self.hot[slots] * torch.exp(a)[..., None, None] + \
+            (dt[..., None, None] * Bp[:, :, None, :k]) * xf[..., None]
+        self.hot[slots] = hot
+        y = torch.einsum("bhpn,bhn->bhp", hot, Cp[..., :k]) + \
+            torch.einsum("bhpn,bhn->bhp", self.cold[slots], Cp[..., k:]) * torch.exp(self.glog[slots])[..., None]
+        t = self.t[slots] + 1
+        self.t[slots] = t
+        for i, s in enumerate(slots.tolist()):
+            entry = (dt[i], xf[i], Bp[i, :, k:])
+            if int(t[i]) % c == 0:
+                self.cold[s] = self._replay(self.cold[s], self.ring[s] + [entry], prm.A)
+                self.ring[s] = []
+                self.glog[s] = 0
+            else:
+                self.ring[s].append(entry)
+                self.glog[s] = self.glog[s] + a[i]
+        return y + xf * prm.D[None, :, None]
+
+    def materialize(self, slots, prm: LayerParams) -> torch.Tensor:
+        slots = torch.as_tensor(slots, dtype=torch.long)
+        prm = prm.to(self.dtype)
+        out = []
+        for s in slots.tolist():
+            cold = self._replay(self.cold[s], self.ring[s], prm.A)
+            out.append(torch.cat([self.hot[s], cold], dim=-1))
+        return torch.stack(out)

@@ -1,0 +1,35 @@
+"""Shared helpers for the parity tests: seeded inputs built on the CPU (so the
+oracle and the GPU see identical bits) and copied to the device."""
+import torch
+
+import oracle
+from nested_ssm_amd import LayerParams
+
+
+def dev_params(prm: oracle.LayerParams, device="cuda") -> LayerParams:
+    f = dict(device=device, dtype=torch.float32)
+    R = None if prm.R is None else prm.R.to(**f).contiguous()
+    return LayerParams(prm.H, prm.P, prm.N, prm.G, prm.dt_bias.to(**f), prm.A.to(**f), prm.D.to(**f), R,
+                       prm.dt_min)
+
+
+def to_dev(*ts, device="cuda"):
+    return [None if t is None else t.to(device).contiguous() for t in ts]
+
+
+def max_rel(a: torch.Tensor, b: torch.Tensor) -> float:
+    return float((a.double() - b.double()).norm() / b.double().norm().clamp_min(1e-30))
+
+
+def assert_close32(got: torch.Tensor, ref: torch.Tensor, what: str, rtol=1e-5, atol=1e-5):
+    """The fp32 parity bar: |got - ref| <= atol + rtol |ref| elementwise."""
+    got = got.detach().cpu().float()
+    ref = ref.detach().cpu().float()
+    err = (got - ref).abs()
+    bound = atol + rtol * ref.abs()
+    bad = err > bound
+    if bool(bad.any()):
+        i = int(torch.argmax((err - bound).flatten()))
+        raise AssertionError(f"{what}: {int(bad.sum())} of {bad.numel()} elements outside rtol={rtol} "
+                             f"atol={atol}; worst at flat index {i}: got {got.flatten()[i].item():.8g} "
+                             f"ref {ref.flatten()[i].item():.8g} (max abs err {err.max().item():.3g})")
