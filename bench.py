@@ -232,7 +232,19 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the host baseline")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of host work for the baseline")
     ap.add_argument("--only", choices=["v4", "fresh"], default=None, help="profile one path only")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="only run a plain device copy of this many MiB (5 times), for scaling HBM counters")
     args = ap.parse_args()
+
+    if args.copy_calibration_mib:
+        n = args.copy_calibration_mib * (1 << 20) // 4
+        src = torch.randn(n, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_per_dispatch_each_way": n * 4, "dispatches": 5}), flush=True)
+        return
 
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): the tiered state op has no "

@@ -92,41 +92,87 @@ __device__ __forceinline__ float softplus_f(float v) { return v > 20.f ? v : log
 // (stride padded to a multiple of 4 floats so the LDS arrays after it stay 16-byte aligned)
 enum { HD_DT = 0, HD_A, HD_DECAY, HD_EG, HD_D, HD_FLUSH, HD_DTOT, HD_T, HD_NV, HD_STRIDE = 12 };
 
-// Cold-tier row access for one lane: NC/32 segments of 4 columns.
-template <int COLD, int CS>
-struct ColdRead {
-  // read-copy values (what the readout sees)
-  static __device__ __forceinline__ void load(const StepArgs& a, size_t row, int q, float (&v)[CS][4]) {
-    constexpr int NC = CS * 32;
+// Streaming access to the state: non-temporal (the state is touched once per
+// token and is far larger than L2 and the MALL) unless built otherwise.
+#ifndef NSSM_NT_LOAD
+#define NSSM_NT_LOAD 1
+#endif
+#ifndef NSSM_NT_STORE
+#define NSSM_NT_STORE 1
+#endif
+// units (8-row blocks) whose loads a wave keeps in flight together
+#ifndef NSSM_UNROLL
+#define NSSM_UNROLL 2
+#endif
+
+template <class T>
+__device__ __forceinline__ T ld_stream(const T* p) {
+  if constexpr (NSSM_NT_LOAD) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+template <class T>
+__device__ __forceinline__ void st_stream(T v, T* p) {
+  if constexpr (NSSM_NT_STORE) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
+
+// Raw registers of one unit for one lane: HS hot float4 and CS cold segments
+// (float4 / 4 x bf16 / 4 x e4m3 by storage kind).
+template <int K, int COLD>
+struct UnitRaw {
+  static constexpr int HS = K / 32;
+  static constexpr int CS = (kN - K) / 32;
+  static constexpr int CSR = CS > 0 ? CS : 1;
+  f4 hv[HS];
+  f4 cf[COLD == NSSM_COLD_FP32 ? CSR : 1];
+  u2v cb[COLD == NSSM_COLD_BF16 ? CSR : 1];
+  uint32_t c8[COLD == NSSM_COLD_FP8 ? CSR : 1];
+  float sc;
+};
+
+template <int K, int COLD>
+__device__ __forceinline__ void unit_load(const StepArgs& a, size_t row, int q, UnitRaw<K, COLD>& d) {
+  constexpr int HS = K / 32, CS = (kN - K) / 32, NC = kN - K;
+  const f4* hp = reinterpret_cast<const f4*>(a.hot + row * K) + q;
+#pragma unroll
+  for (int s = 0; s < HS; ++s) d.hv[s] = ld_stream(hp + 8 * s);
+  if constexpr (CS > 0) {
     if constexpr (COLD == NSSM_COLD_FP32) {
       const f4* p = reinterpret_cast<const f4*>(static_cast<const float*>(a.cold) + row * NC) + q;
 #pragma unroll
-      for (int s = 0; s < CS; ++s) {
-        f4 t = __builtin_nontemporal_load(p + 8 * s);
-        v[s][0] = t.x; v[s][1] = t.y; v[s][2] = t.z; v[s][3] = t.w;
-      }
+      for (int s = 0; s < CS; ++s) d.cf[s] = ld_stream(p + 8 * s);
     } else if constexpr (COLD == NSSM_COLD_BF16) {
       const u2v* p = reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.cold) + row * NC) + q;
 #pragma unroll
-      for (int s = 0; s < CS; ++s) {
-        u2v t = __builtin_nontemporal_load(p + 8 * s);
-        v[s][0] = __uint_as_float(t.x << 16);
-        v[s][1] = __uint_as_float(t.x & 0xffff0000u);
-        v[s][2] = __uint_as_float(t.y << 16);
-        v[s][3] = __uint_as_float(t.y & 0xffff0000u);
-      }
-    } else {  // FP8: per-row scale
+      for (int s = 0; s < CS; ++s) d.cb[s] = ld_stream(p + 8 * s);
+    } else {
       const uint32_t* p = reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(a.cold) + row * NC) + q;
-      const float sc = a.scale[row];
 #pragma unroll
-      for (int s = 0; s < CS; ++s) {
-        uint32_t t = __builtin_nontemporal_load(p + 8 * s);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[s][e] = nssm_e4m3fn_to_f32((uint8_t)(t >> (8 * e))) * sc;
-      }
+      for (int s = 0; s < CS; ++s) d.c8[s] = ld_stream(p + 8 * s);
+      d.sc = a.scale[row];
     }
   }
-};
+}
+
+// read-copy values the readout sees
+template <int K, int COLD>
+__device__ __forceinline__ void cold_decode(const UnitRaw<K, COLD>& d, float (&v)[UnitRaw<K, COLD>::CSR][4]) {
+  constexpr int CS = UnitRaw<K, COLD>::CS;
+#pragma unroll
+  for (int s = 0; s < CS; ++s) {
+    if constexpr (COLD == NSSM_COLD_FP32) {
+      v[s][0] = d.cf[s].x; v[s][1] = d.cf[s].y; v[s][2] = d.cf[s].z; v[s][3] = d.cf[s].w;
+    } else if constexpr (COLD == NSSM_COLD_BF16) {
+      v[s][0] = __uint_as_float(d.cb[s].x << 16);
+      v[s][1] = __uint_as_float(d.cb[s].x & 0xffff0000u);
+      v[s][2] = __uint_as_float(d.cb[s].y << 16);
+      v[s][3] = __uint_as_float(d.cb[s].y & 0xffff0000u);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[s][e] = nssm_e4m3fn_to_f32((uint8_t)(d.c8[s] >> (8 * e))) * d.sc;
+    }
+  }
+}
 
 // Write the new exact cold values of one row: fp32 copy, or master + read copy.
 template <int COLD, int CS>
@@ -135,11 +181,11 @@ __device__ __forceinline__ void cold_store(const StepArgs& a, size_t row, int q,
   if constexpr (COLD == NSSM_COLD_FP32) {
     f4* p = reinterpret_cast<f4*>(static_cast<float*>(a.cold) + row * NC) + q;
 #pragma unroll
-    for (int s = 0; s < CS; ++s) __builtin_nontemporal_store(f4{v[s][0], v[s][1], v[s][2], v[s][3]}, p + 8 * s);
+    for (int s = 0; s < CS; ++s) st_stream(f4{v[s][0], v[s][1], v[s][2], v[s][3]}, p + 8 * s);
   } else {
     f4* pm = reinterpret_cast<f4*>(a.master + row * NC) + q;
 #pragma unroll
-    for (int s = 0; s < CS; ++s) __builtin_nontemporal_store(f4{v[s][0], v[s][1], v[s][2], v[s][3]}, pm + 8 * s);
+    for (int s = 0; s < CS; ++s) st_stream(f4{v[s][0], v[s][1], v[s][2], v[s][3]}, pm + 8 * s);
     if constexpr (COLD == NSSM_COLD_BF16) {
       u2v* p = reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.cold) + row * NC) + q;
 #pragma unroll
@@ -147,7 +193,7 @@ __device__ __forceinline__ void cold_store(const StepArgs& a, size_t row, int q,
         u2v t;
         t.x = (uint32_t)nssm_f32_to_bf16(v[s][0]) | ((uint32_t)nssm_f32_to_bf16(v[s][1]) << 16);
         t.y = (uint32_t)nssm_f32_to_bf16(v[s][2]) | ((uint32_t)nssm_f32_to_bf16(v[s][3]) << 16);
-        __builtin_nontemporal_store(t, p + 8 * s);
+        st_stream(t, p + 8 * s);
       }
     } else {  // FP8 with per-row amax scale, as scale/vllm_v4_patch.py:106-111
       float am = 0.f;
@@ -163,58 +209,36 @@ __device__ __forceinline__ void cold_store(const StepArgs& a, size_t row, int q,
         uint32_t t = 0;
 #pragma unroll
         for (int e = 0; e < 4; ++e) t |= (uint32_t)nssm_f32_to_e4m3fn(v[s][e] / sc) << (8 * e);
-        __builtin_nontemporal_store(t, p + 8 * s);
+        st_stream(t, p + 8 * s);
       }
       if (q == 0) a.scale[row] = sc;
     }
   }
 }
 
-template <int CS>
-__device__ __forceinline__ void master_load(const StepArgs& a, size_t row, int q, float (&v)[CS][4]) {
-  constexpr int NC = CS * 32;
-  const f4* p = reinterpret_cast<const f4*>(a.master + row * NC) + q;
-#pragma unroll
-  for (int s = 0; s < CS; ++s) {
-    f4 t = __builtin_nontemporal_load(p + 8 * s);
-    v[s][0] = t.x; v[s][1] = t.y; v[s][2] = t.z; v[s][3] = t.w;
-  }
-}
-
-// One unit (8 rows of head j) of the step. FLUSH selects the replay of the
-// buffered window into the cold columns (sU/sBc staged by the caller).
+// Compute and store one unit (8 rows of head j) from its raw registers. FLUSH
+// selects the replay of the buffered window into the cold columns (sU/sBc
+// staged by the caller).
 template <int K, int COLD, bool FLUSH>
-__device__ __forceinline__ void do_unit(const StepArgs& a, int slot, int bi, int h, int j, int p, int q,
-                                        const float (&Bh)[K / 32][4], const float (&Ch)[K / 32][4],
-                                        const float (&Cc)[(kN - K) / 32 > 0 ? (kN - K) / 32 : 1][4],
-                                        const float* sX, const float* sHd, const float* sU, const float* sBc,
-                                        int m) {
+__device__ __forceinline__ void unit_compute(const StepArgs& a, size_t row, int bi, int h, int j, int p, int q,
+                                             UnitRaw<K, COLD>& d, const float (&Bh)[K / 32][4],
+                                             const float (&Ch)[K / 32][4],
+                                             const float (&Cc)[UnitRaw<K, COLD>::CSR][4], const float* sX,
+                                             const float* sHd, const float* sU, const float* sBc, int m) {
   constexpr int HS = K / 32;
   constexpr int NC = kN - K;
   constexpr int CS = NC / 32;
+  constexpr int CSR = UnitRaw<K, COLD>::CSR;
   const int P = a.P;
-  const size_t row = ((size_t)slot * a.H + h) * P + p;
-
-  f4* hp = reinterpret_cast<f4*>(a.hot + row * K) + q;
-  f4 hv[HS];
-#pragma unroll
-  for (int s = 0; s < HS; ++s) hv[s] = __builtin_nontemporal_load(hp + 8 * s);
-
-  float cv[CS > 0 ? CS : 1][4];
-  float mv[CS > 0 ? CS : 1][4];
-  if constexpr (CS > 0) {
-    ColdRead<COLD, CS>::load(a, row, q, cv);
-    if constexpr (FLUSH && COLD != NSSM_COLD_FP32) master_load<CS>(a, row, q, mv);
-  }
-
   const float* hd = sHd + j * HD_STRIDE;
   const float xp = sX[j * P + p];
   const float uu = hd[HD_DT] * xp;
   const float dec = hd[HD_DECAY];
   float ph = 0.f;
+  f4* hp = reinterpret_cast<f4*>(a.hot + row * K) + q;
 #pragma unroll
   for (int s = 0; s < HS; ++s) {
-    f4 v = hv[s];
+    f4 v = d.hv[s];
     v.x = fmaf(v.x, dec, uu * Bh[s][0]);
     v.y = fmaf(v.y, dec, uu * Bh[s][1]);
     v.z = fmaf(v.z, dec, uu * Bh[s][2]);
@@ -223,13 +247,13 @@ __device__ __forceinline__ void do_unit(const StepArgs& a, int slot, int bi, int
     ph = fmaf(v.y, Ch[s][1], ph);
     ph = fmaf(v.z, Ch[s][2], ph);
     ph = fmaf(v.w, Ch[s][3], ph);
-    hv[s] = v;
+    st_stream(v, hp + 8 * s);
   }
-#pragma unroll
-  for (int s = 0; s < HS; ++s) __builtin_nontemporal_store(hv[s], hp + 8 * s);
 
   float part = ph;
   if constexpr (CS > 0) {
+    float cv[CSR][4];
+    cold_decode<K, COLD>(d, cv);
     float pc = 0.f;
 #pragma unroll
     for (int s = 0; s < CS; ++s)
@@ -238,29 +262,40 @@ __device__ __forceinline__ void do_unit(const StepArgs& a, int slot, int bi, int
     part = fmaf(hd[HD_EG], pc, ph);
 
     if constexpr (FLUSH) {
-      if (hd[HD_FLUSH] != 0.f) {
-        // exact cold state at this token: decayed snapshot + decayed replay of
-        // the window (buffered tokens and this one), scale/v4_fused_decode.py:76-85
-        const float dtot = hd[HD_DTOT];
-        float nvv[CS][4];
+      // exact cold state at this token: decayed snapshot + decayed replay of
+      // the window (buffered tokens and this one), scale/v4_fused_decode.py:76-85
+      float nvv[CS][4];
+      if constexpr (COLD == NSSM_COLD_FP32) {
 #pragma unroll
         for (int s = 0; s < CS; ++s)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) nvv[s][e] = dtot * (COLD == NSSM_COLD_FP32 ? cv[s][e] : mv[s][e]);
-        for (int i = 0; i < m; ++i) {
-          const float coef = sU[i * P + p];
-          const float* bc = sBc + i * NC + 4 * q;
+          for (int e = 0; e < 4; ++e) nvv[s][e] = cv[s][e];
+      } else {
+        const f4* pm = reinterpret_cast<const f4*>(a.master + row * NC) + q;
 #pragma unroll
-          for (int s = 0; s < CS; ++s) {
-            const f4 bb = *reinterpret_cast<const f4*>(bc + 32 * s);
-            nvv[s][0] = fmaf(coef, bb.x, nvv[s][0]);
-            nvv[s][1] = fmaf(coef, bb.y, nvv[s][1]);
-            nvv[s][2] = fmaf(coef, bb.z, nvv[s][2]);
-            nvv[s][3] = fmaf(coef, bb.w, nvv[s][3]);
-          }
+        for (int s = 0; s < CS; ++s) {
+          const f4 t = ld_stream(pm + 8 * s);
+          nvv[s][0] = t.x; nvv[s][1] = t.y; nvv[s][2] = t.z; nvv[s][3] = t.w;
         }
-        cold_store<COLD, CS>(a, row, q, nvv);
       }
+      const float dtot = hd[HD_DTOT];
+#pragma unroll
+      for (int s = 0; s < CS; ++s)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) nvv[s][e] *= dtot;
+      for (int i = 0; i < m; ++i) {
+        const float coef = sU[i * P + p];
+        const float* bc = sBc + i * NC + 4 * q;
+#pragma unroll
+        for (int s = 0; s < CS; ++s) {
+          const f4 bb = *reinterpret_cast<const f4*>(bc + 32 * s);
+          nvv[s][0] = fmaf(coef, bb.x, nvv[s][0]);
+          nvv[s][1] = fmaf(coef, bb.y, nvv[s][1]);
+          nvv[s][2] = fmaf(coef, bb.z, nvv[s][2]);
+          nvv[s][3] = fmaf(coef, bb.w, nvv[s][3]);
+        }
+      }
+      cold_store<COLD, CS>(a, row, q, nvv);
     }
   }
   part = sum8(part);
@@ -343,21 +378,35 @@ __global__ void __launch_bounds__(kMaxWaves * 64) step_kernel(StepArgs a) {
     const f4 bv = *reinterpret_cast<const f4*>(sBraw + 4 * hl);
     const f4 cv = *reinterpret_cast<const f4*>(sCraw + 4 * hl);
     const float* Rg = a.R + (size_t)g * kN * kN;
-    for (int mrow = 2 * wave + hw; mrow < kN; mrow += 2 * nw) {
-      const f4 r = *reinterpret_cast<const f4*>(Rg + (size_t)mrow * kN + 4 * hl);
-      float db = r.x * bv.x;
-      db = fmaf(r.y, bv.y, db);
-      db = fmaf(r.z, bv.z, db);
-      db = fmaf(r.w, bv.w, db);
-      float dc = r.x * cv.x;
-      dc = fmaf(r.y, cv.y, dc);
-      dc = fmaf(r.z, cv.z, dc);
-      dc = fmaf(r.w, cv.w, dc);
-      db = sum32(db);
-      dc = sum32(dc);
-      if (hl == 0) {
-        sB[mrow] = db;
-        sC[mrow] = dc;
+    // RB rows of R in flight per half-wave; both half-waves of a wave see the
+    // same trip counts (kN is even), so the reductions run with all lanes active
+    constexpr int RB = 8;
+    for (int m0 = 2 * wave + hw; m0 < kN; m0 += 2 * nw * RB) {
+      f4 r[RB];
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        const int mrow = m0 + 2 * nw * i;
+        if (mrow < kN) r[i] = *reinterpret_cast<const f4*>(Rg + (size_t)mrow * kN + 4 * hl);
+      }
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        const int mrow = m0 + 2 * nw * i;
+        if (mrow < kN) {
+          float db = r[i].x * bv.x;
+          db = fmaf(r[i].y, bv.y, db);
+          db = fmaf(r[i].z, bv.z, db);
+          db = fmaf(r[i].w, bv.w, db);
+          float dc = r[i].x * cv.x;
+          dc = fmaf(r[i].y, cv.y, dc);
+          dc = fmaf(r[i].z, cv.z, dc);
+          dc = fmaf(r[i].w, cv.w, dc);
+          db = sum32(db);
+          dc = sum32(dc);
+          if (hl == 0) {
+            sB[mrow] = db;
+            sC[mrow] = dc;
+          }
+        }
       }
     }
   } else {
@@ -392,11 +441,30 @@ __global__ void __launch_bounds__(kMaxWaves * 64) step_kernel(StepArgs a) {
   }
 
   if (!any_flush) {
+    // U units per wave in flight: all their loads are issued before any compute
+    constexpr int U = NSSM_UNROLL;
     const int units = hpw * RG;
-    for (int u = wave; u < units; u += nw) {
-      const int j = u / RG;
-      const int p = (u - j * RG) * 8 + rr;
-      do_unit<K, COLD, false>(a, slot, bi, h0 + j, j, p, q, Bh, Ch, Cc, sX, sHd, sU, sBc, 0);
+    for (int u0 = wave; u0 < units; u0 += U * nw) {
+      UnitRaw<K, COLD> d[U];
+#pragma unroll
+      for (int i = 0; i < U; ++i) {
+        const int u = u0 + i * nw;
+        if (u < units) {
+          const int j = u / RG;
+          const int p = (u - j * RG) * 8 + rr;
+          unit_load<K, COLD>(a, ((size_t)slot * H + h0 + j) * P + p, q, d[i]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < U; ++i) {
+        const int u = u0 + i * nw;
+        if (u < units) {
+          const int j = u / RG;
+          const int p = (u - j * RG) * 8 + rr;
+          unit_compute<K, COLD, false>(a, ((size_t)slot * H + h0 + j) * P + p, bi, h0 + j, j, p, q, d[i], Bh, Ch,
+                                       Cc, sX, sHd, sU, sBc, 0);
+        }
+      }
     }
   } else if constexpr (TIERED) {
     // window: nv buffered tokens at ring positions [c-1-nv, c-1) plus this one
@@ -439,11 +507,19 @@ __global__ void __launch_bounds__(kMaxWaves * 64) step_kernel(StepArgs a) {
           sU[i] = sW[e] * xv;
         }
         __syncthreads();
-        for (int r = wave; r < RG; r += nw)
-          do_unit<K, COLD, true>(a, slot, bi, h, j, r * 8 + rr, q, Bh, Ch, Cc, sX, sHd, sU, sBc, m);
+        for (int r = wave; r < RG; r += nw) {
+          const size_t row = ((size_t)slot * H + h) * P + r * 8 + rr;
+          UnitRaw<K, COLD> d;
+          unit_load<K, COLD>(a, row, q, d);
+          unit_compute<K, COLD, true>(a, row, bi, h, j, r * 8 + rr, q, d, Bh, Ch, Cc, sX, sHd, sU, sBc, m);
+        }
       } else {
-        for (int r = wave; r < RG; r += nw)
-          do_unit<K, COLD, false>(a, slot, bi, h, j, r * 8 + rr, q, Bh, Ch, Cc, sX, sHd, sU, sBc, 0);
+        for (int r = wave; r < RG; r += nw) {
+          const size_t row = ((size_t)slot * H + h) * P + r * 8 + rr;
+          UnitRaw<K, COLD> d;
+          unit_load<K, COLD>(a, row, q, d);
+          unit_compute<K, COLD, false>(a, row, bi, h, j, r * 8 + rr, q, d, Bh, Ch, Cc, sX, sHd, sU, sBc, 0);
+        }
       }
     }
   }

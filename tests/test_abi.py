@@ -1,0 +1,156 @@
+"""CPU checks of the C ABI (no kernel launches): the library loads, exports
+every entry point include/nssm.h declares, its scalar format conversions are
+bit-identical to torch's casts, and argument validation returns error codes."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import nested_ssm_amd
+from nested_ssm_amd import _lib
+from nested_ssm_amd.ops import LayerParams, V4Tier, _need
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "nssm.h")
+
+
+def header_functions():
+    txt = open(HEADER).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(nssm_[a-z0-9_]+)\s*\(", txt)))
+
+
+def header_defines():
+    return dict(re.findall(r"#define\s+(NSSM_[A-Z0-9_]+)\s+\(?(-?\d+)\)?", open(HEADER).read()))
+
+
+def test_library_loads_and_exports_every_declared_function():
+    L = _lib.lib()
+    names = header_functions()
+    assert len(names) >= 12
+    for nm in names:
+        assert hasattr(L, nm), f"{nm} declared in include/nssm.h but not exported"
+    assert sorted(_lib.EXPORTED) == names
+
+
+def test_abi_version_and_codes_match_header():
+    d = header_defines()
+    L = _lib.lib()
+    assert L.nssm_abi_version() == int(d["NSSM_ABI_VERSION"])
+    assert int(d["NSSM_COLD_FP32"]) == _lib.COLD_FP32
+    assert int(d["NSSM_COLD_BF16"]) == _lib.COLD_BF16
+    assert int(d["NSSM_COLD_FP8"]) == _lib.COLD_FP8
+    for code in ("NSSM_E_NULL", "NSSM_E_DIMS", "NSSM_E_ALIGN", "NSSM_E_KIND", "NSSM_E_LAUNCH", "NSSM_E_TUNING"):
+        msg = L.nssm_strerror(int(d[code])).decode()
+        assert msg and msg != "unknown nssm error"
+    assert L.nssm_strerror(0).decode() == "ok"
+
+
+def _host_f32_to_e4m3(x: torch.Tensor) -> torch.Tensor:
+    x = x.contiguous().float()
+    out = torch.empty(x.numel(), dtype=torch.uint8)
+    _lib.lib().nssm_host_f32_to_e4m3fn(x.data_ptr(), out.data_ptr(), x.numel())
+    return out.view(x.shape)
+
+
+def test_e4m3fn_encode_matches_torch_on_a_dense_sweep():
+    # every fp32 bit pattern with 11 low mantissa bits dropped over |x| in [2^-12, 512):
+    # covers subnormals, every rounding tie class and the overflow edge
+    lo = torch.tensor(2.0 ** -12).view(torch.int32).item()
+    hi = torch.tensor(512.0).view(torch.int32).item()
+    bits = torch.arange(lo, hi, 1 << 11, dtype=torch.int64).to(torch.int32)
+    x = bits.view(torch.float32)
+    x = torch.cat([x, -x, torch.tensor([0.0, -0.0, 448.0, 464.0, 463.9999, 480.0, 2.0 ** -9, 2.0 ** -10,
+                                        1.5 * 2.0 ** -9, 2.0 ** -6, 0.9999 * 2.0 ** -6])])
+    want = x.to(torch.float8_e4m3fn).view(torch.uint8)
+    got = _host_f32_to_e4m3(x)
+    bad = (got != want).nonzero()
+    assert bad.numel() == 0, f"{bad.numel()} mismatches, first x={x[bad[0]].item()!r}"
+
+
+def test_e4m3fn_encode_random_and_nan():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(200000, generator=g) * torch.logspace(-5, 2.6, 200000)
+    assert torch.equal(_host_f32_to_e4m3(x), x.to(torch.float8_e4m3fn).view(torch.uint8))
+    nan = _host_f32_to_e4m3(torch.tensor([float("nan")]))
+    assert int(nan[0]) & 0x7F == 0x7F
+
+
+def test_e4m3fn_decode_all_codes():
+    codes = torch.arange(256, dtype=torch.uint8)
+    out = torch.empty(256, dtype=torch.float32)
+    _lib.lib().nssm_host_e4m3fn_to_f32(codes.data_ptr(), out.data_ptr(), 256)
+    want = codes.view(torch.float8_e4m3fn).float()
+    same = (out == want) | (torch.isnan(out) & torch.isnan(want))
+    assert bool(same.all())
+    assert torch.equal(torch.signbit(out[~torch.isnan(out)]), torch.signbit(want[~torch.isnan(want)]))
+
+
+def test_bf16_rne_matches_torch():
+    g = torch.Generator().manual_seed(1)
+    x = torch.cat([torch.randn(100000, generator=g) * 1e3, torch.randn(100000, generator=g) * 1e-30,
+                   torch.tensor([0.0, -0.0, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, 3.3895e38, -1e-45])])
+    out = torch.empty(x.numel(), dtype=torch.int16)
+    _lib.lib().nssm_host_f32_to_bf16(x.data_ptr(), out.data_ptr(), x.numel())
+    assert torch.equal(out, x.to(torch.bfloat16).view(torch.int16))
+
+
+def test_tier_sizes():
+    L = _lib.lib()
+    sz = (ctypes.c_int64 * 10)()
+    assert L.nssm_tier_sizes(256, 128, 80, 128, 8, 32, 4, _lib.COLD_FP32, sz) == 0
+    rows = 256 * 128 * 80
+    assert sz[0] == rows * 32 * 4 and sz[1] == rows * 96 * 4 and sz[2] == 0 and sz[3] == 0
+    assert sz[4] == 256 * 128 * 4 * 80 * 2 and sz[6] == 256 * 8 * 4 * 96 * 4
+    assert L.nssm_tier_sizes(448, 128, 80, 128, 8, 32, 4, _lib.COLD_FP8, sz) == 0
+    assert sz[1] == 448 * 128 * 80 * 96 and sz[2] == 448 * 128 * 80 * 4 and sz[3] == 448 * 128 * 80 * 96 * 4
+    assert L.nssm_tier_sizes(4, 8, 80, 64, 1, 32, 4, 0, sz) == -2  # d_state must be 128
+    assert L.nssm_tier_sizes(4, 8, 80, 128, 1, 32, 65, 0, sz) == -2  # c above 64
+    assert L.nssm_tier_sizes(4, 8, 80, 128, 1, 32, 4, 7, sz) == -4
+
+
+def test_entry_points_validate_before_launching():
+    """Bad arguments return codes without touching a device (fake pointers never dereferenced)."""
+    L = _lib.lib()
+    fake = 4096
+    prm = _lib.LayerParams(8, 80, 128, 1, fake, fake, fake, None, 0.0)
+    inp = _lib.StepInputs(4, fake, fake, fake, fake, None)
+    assert L.nssm_fresh_step(None, fake, 4, ctypes.byref(inp), fake, None) == -1
+    bad = _lib.LayerParams(8, 80, 64, 1, fake, fake, fake, None, 0.0)
+    assert L.nssm_fresh_step(ctypes.byref(bad), fake, 4, ctypes.byref(inp), fake, None) == -2
+    bad = _lib.LayerParams(8, 72, 128, 1, fake, fake, fake, None, 0.0)  # P not a multiple of 16
+    assert L.nssm_fresh_step(ctypes.byref(bad), fake, 4, ctypes.byref(inp), fake, None) == -2
+    bad = _lib.LayerParams(8, 80, 128, 3, fake, fake, fake, None, 0.0)  # H % G
+    assert L.nssm_fresh_step(ctypes.byref(bad), fake, 4, ctypes.byref(inp), fake, None) == -2
+    assert L.nssm_fresh_step(ctypes.byref(prm), fake + 4, 4, ctypes.byref(inp), fake, None) == -3
+    assert L.nssm_fresh_step(ctypes.byref(prm), fake, 2, ctypes.byref(inp), fake, None) == -2  # b > slots
+    tier = _lib.Tier(4, 32, 4, 9, *([fake] * 10))
+    assert L.nssm_v4_step(ctypes.byref(prm), ctypes.byref(tier), ctypes.byref(inp), fake, None) == -4
+    tier = _lib.Tier(4, 48, 4, 0, *([fake] * 10))  # k_hot not a multiple of 32
+    assert L.nssm_v4_step(ctypes.byref(prm), ctypes.byref(tier), ctypes.byref(inp), fake, None) == -2
+    tier = _lib.Tier(4, 32, 0, 0, *([fake] * 10))  # c = 0
+    assert L.nssm_v4_step(ctypes.byref(prm), ctypes.byref(tier), ctypes.byref(inp), fake, None) == -2
+    tier = _lib.Tier(4, 32, 4, 2, *([fake] * 2 + [None] + [fake] * 7))  # fp8 without a scale buffer
+    assert L.nssm_v4_step(ctypes.byref(prm), ctypes.byref(tier), ctypes.byref(inp), fake, None) == -1
+    assert L.nssm_set_launch(0, 9) == -6
+    assert L.nssm_set_launch(0, 0) == 0
+
+
+def test_python_layer_rejects_cpu_tensors_and_wrong_dtypes():
+    x = torch.zeros(2, 8, 80, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="no CPU path"):
+        _need(x, "x", torch.bfloat16, (2, 8, 80))
+    prm = LayerParams(8, 80, 128, 1, torch.zeros(8), torch.zeros(8), torch.zeros(8))
+    with pytest.raises(ValueError, match="no CPU path"):
+        nested_ssm_amd.fresh_step(prm, torch.zeros(2, 8, 80, 128), x, x, x, x)
+    with pytest.raises(ValueError):
+        V4Tier(2, 8, 80, 1, cold="int4")
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "libnssm_hip.so"))
+    with pytest.raises(_lib.NssmError, match="no CPU fallback"):
+        _lib.lib()

@@ -1,0 +1,298 @@
+"""Pin the CPU oracle (runs without a GPU).
+
+The reference holds no golden vectors for this path, so each oracle function is
+pinned by an independent route: an installed library implementation, an fp64
+per-element loop, a closed form, or an invariant of the mathematics.
+"""
+import math
+
+import pytest
+import torch
+
+import oracle
+from oracle.v4_ref import _heads
+
+N = 128
+
+
+def _small(seed=0, b=3, H=8, P=16, G=2, rotation=True, dt_min=0.0):
+    gen = torch.Generator().manual_seed(seed)
+    prm = oracle.make_layer_params(H, P, N, G, gen, rotation=rotation, dt_min=dt_min)
+    S0 = oracle.make_state(b, H, P, N, gen)
+    return gen, prm, S0
+
+
+# --------------------------------------------------------------------------- rotation
+def test_make_rotation_is_orthogonal_with_positive_qr_diagonal():
+    gen = torch.Generator().manual_seed(3)
+    R = oracle.make_rotation(4, N, gen).double()
+    eye = torch.eye(N, dtype=torch.float64)
+    assert torch.allclose(R @ R.transpose(-1, -2), eye.expand(4, N, N), atol=1e-6)
+    # the sign fix (Q * sign(diag(R_qr))) makes R the Q of the unique QR of the
+    # Gaussian W with a positive triangular diagonal: R^T W is upper triangular, diag > 0
+    W = torch.randn(4, N, N, generator=torch.Generator().manual_seed(3), dtype=torch.float64)
+    T = R.transpose(-1, -2) @ W
+    assert torch.allclose(torch.tril(T, -1), torch.zeros_like(T), atol=1e-5)
+    assert bool((torch.diagonal(T, dim1=-2, dim2=-1) > 0).all())
+
+
+def test_rotate_is_R_times_vector_per_group():
+    gen = torch.Generator().manual_seed(4)
+    R = oracle.make_rotation(3, N, gen)
+    X = torch.randn(5, 3, N, generator=gen)
+    got = oracle.rotate(X, R)
+    for g in range(3):  # B'[m] = sum_n R[g][m][n] B[n]  (a transposed R fails here)
+        want = X[:, g, :].double() @ R[g].double().T
+        assert torch.allclose(got[:, g].double(), want, atol=1e-5)
+    assert oracle.rotate(X, None) is X
+
+
+def test_softplus_dt_closed_form_and_clamp():
+    x = torch.tensor([[-30.0, -2.0, 0.0, 1.5, 19.0, 25.0]])
+    bias = torch.tensor([0.1, -0.2, 0.3, 0.0, 0.5, 1.0])
+    got = oracle.softplus_dt(x, bias)
+    v = (x + bias).double()
+    want = torch.where(v > 20, v, torch.log1p(torch.exp(v)))
+    assert torch.allclose(got.double(), want, rtol=1e-6, atol=1e-12)
+    got2 = oracle.softplus_dt(x, bias, dt_min=0.05)
+    assert float(got2.min()) >= 0.05 and torch.equal(got2[got2 > 0.05], got[got > 0.05])
+
+
+# --------------------------------------------------------------------------- fresh step
+def test_fresh_step_matches_transformers_selective_state_update():
+    """Installed transformers' mamba2_selective_state_update (an independent
+    implementation of the same recurrence), fed fp32-upcast inputs."""
+    M = pytest.importorskip("transformers.models.nemotron_h.modeling_nemotron_h")
+    gen, prm, S0 = _small(seed=5, b=2, H=8, P=16, G=2)
+    b, H, P, G = 2, 8, 16, 2
+    S1, S2 = S0.clone(), S0.clone()
+    for _ in range(6):
+        x, B, C, dt = oracle.make_step_inputs(b, H, P, N, G, gen)
+        y1 = oracle.fresh_step(S1, x, B, C, dt, prm)
+        Bp, Cp = oracle.rotate(B.float(), prm.R), oracle.rotate(C.float(), prm.R)
+        y2 = M.mamba2_selective_state_update(
+            S2, x.float(), dt.float()[..., None].expand(-1, -1, P), prm.A[:, None, None].expand(H, P, N), Bp, Cp,
+            prm.D[:, None].expand(H, P), dt_bias=prm.dt_bias[:, None].expand(H, P), dt_softplus=True)
+        assert torch.allclose(y1, y2, rtol=1e-5, atol=1e-6)
+    assert torch.allclose(S1, S2, rtol=1e-5, atol=1e-7)
+
+
+def test_fresh_step_matches_fp64_elementwise_loop():
+    gen, prm, S0 = _small(seed=6, b=2, H=4, P=8, G=2)
+    b, H, P, G = 2, 4, 8, 2
+    HG = H // G
+    x, B, C, dt = oracle.make_step_inputs(b, H, P, N, G, gen)
+    S = S0.clone().double()
+    y = oracle.fresh_step(S, x, B, C, dt, prm.to(torch.float64), dtype=torch.float64)
+    Sw = S0.double()
+    R = prm.R.double()
+    for i in range(b):
+        for h in range(H):
+            g = h // HG
+            Bp = [sum(float(R[g, m, n]) * float(B[i, g, n]) for n in range(N)) for m in range(N)]
+            Cp = [sum(float(R[g, m, n]) * float(C[i, g, n]) for n in range(N)) for m in range(N)]
+            v = float(dt[i, h]) + float(prm.dt_bias[h])
+            d = math.log1p(math.exp(v))
+            dec = math.exp(d * float(prm.A[h]))
+            for p in range(P):
+                acc = 0.0
+                for n in range(N):
+                    s = float(Sw[i, h, p, n]) * dec + d * Bp[n] * float(x[i, h, p])
+                    assert abs(s - float(S[i, h, p, n])) < 1e-12
+                    acc += s * Cp[n]
+                want = acc + float(prm.D[h]) * float(x[i, h, p])
+                assert abs(want - float(y[i, h, p])) < 1e-10
+
+
+def test_fresh_step_rotation_invariance():
+    """Orthogonal R: B' = R B, C' = R C with S' = S R^T leaves y unchanged and keeps S' = S R^T
+    (the per-head scalar decay commutes with R)."""
+    gen, prm_r, S0 = _small(seed=7, b=2, H=8, P=16, G=2)
+    prm_i = oracle.LayerParams(prm_r.H, prm_r.P, prm_r.N, prm_r.G, prm_r.dt_bias, prm_r.A, prm_r.D, None)
+    f64 = torch.float64
+    Rh = prm_r.R.double().repeat_interleave(8 // 2, dim=0)  # [H, N, N]: head h uses R of group h // HG
+    S_plain = S0.double().clone()
+    S_rot = torch.einsum("bhpn,hmn->bhpm", S_plain, Rh)  # S' = S R^T
+    for _ in range(5):
+        x, B, C, dt = oracle.make_step_inputs(2, 8, 16, N, 2, gen)
+        y_plain = oracle.fresh_step(S_plain, x, B, C, dt, prm_i.to(f64), dtype=f64)
+        y_rot = oracle.fresh_step(S_rot, x, B, C, dt, prm_r.to(f64), dtype=f64)
+        assert torch.allclose(y_plain, y_rot, atol=1e-10)
+    assert torch.allclose(S_rot, torch.einsum("bhpn,hmn->bhpm", S_plain, Rh), atol=1e-10)
+
+
+# --------------------------------------------------------------------------- v4 native
+def _fresh_traj(S0, steps_inputs, prm):
+    """fp64 fresh trajectory: states S_t (after token t) and log decays a_t."""
+    S = S0.double().clone()
+    prm64 = prm.to(torch.float64)
+    traj, ays = [S.clone()], []
+    for (x, B, C, dt) in steps_inputs:
+        oracle.fresh_step(S, x, B, C, dt, prm64, dtype=torch.float64)
+        traj.append(S.clone())
+        ays.append(oracle.softplus_dt(dt.double(), prm64.dt_bias) * prm64.A[None, :])
+    return traj, ays
+
+
+@pytest.mark.parametrize("k,c", [(32, 4), (64, 3), (96, 1), (32, 5)])
+def test_native_v4_equals_stale_readout_closed_form(k, c):
+    """y_t = S_t[:, :k] C'_t[:k] + exp(sum_{s=t0+1}^{t-1} a_s) S_{t0}[:, k:] C'_t[k:] + D x_t
+    with t0 = c * floor((t-1)/c) the last snapshot: the one-token-lagged decay of
+    scale/v4_native_decode.py:159-167. An inclusive decay or a wrong snapshot time fails."""
+    b, H, P, G = 2, 4, 8, 2
+    gen, prm, S0 = _small(seed=10 + k + c, b=b, H=H, P=P, G=G)
+    steps = 3 * c + 2
+    ins = [oracle.make_step_inputs(b, H, P, N, G, gen) for _ in range(steps)]
+    traj, ays = _fresh_traj(S0, ins, prm)
+    nat = oracle.NativeV4(b, H, P, N, k, c, dtype=torch.float64)
+    nat.join(torch.arange(b), S0.double())
+    prm64 = prm.to(torch.float64)
+    for t in range(1, steps + 1):
+        x, B, C, dt = ins[t - 1]
+        y = nat.step(x, B, C, dt, prm)
+        t0 = c * ((t - 1) // c)
+        lag = sum((ays[s - 1] for s in range(t0 + 1, t)), torch.zeros(b, H, dtype=torch.float64))
+        Cp = _heads(oracle.rotate(C.double(), prm64.R), H)
+        want = torch.einsum("bhpn,bhn->bhp", traj[t][..., :k], Cp[..., :k]) + \
+            torch.exp(lag)[..., None] * torch.einsum("bhpn,bhn->bhp", traj[t0][..., k:], Cp[..., k:]) + \
+            x.double() * prm64.D[None, :, None]
+        assert torch.allclose(y, want, atol=1e-11), f"t={t}"
+        if t % c == 0:  # the snapshot after a flush is the fresh cold state
+            assert torch.allclose(nat.snap, traj[t][..., k:], atol=1e-12)
+
+
+def test_native_v4_all_hot_equals_fresh():
+    """k = N reproduces fresh exactly (scale/v4_native_decode.py:16,77-78)."""
+    b, H, P, G = 2, 8, 16, 2
+    gen, prm, S0 = _small(seed=12, b=b, H=H, P=P, G=G)
+    nat = oracle.NativeV4(b, H, P, N, N, 4)
+    nat.join(torch.arange(b), S0)
+    S = S0.clone()
+    for _ in range(7):
+        x, B, C, dt = oracle.make_step_inputs(b, H, P, N, G, gen)
+        assert torch.equal(nat.step(x, B, C, dt, prm), oracle.fresh_step(S, x, B, C, dt, prm))
+
+
+def test_native_v4_dt_min_path():
+    b, H, P, G = 1, 4, 8, 1
+    gen, prm, S0 = _small(seed=13, b=b, H=H, P=P, G=G, dt_min=0.2)
+    nat = oracle.NativeV4(b, H, P, N, N, 4)
+    nat.join(torch.arange(b), S0)
+    S = S0.clone()
+    x, B, C, dt = oracle.make_step_inputs(b, H, P, N, G, gen)
+    y = nat.step(x, B, C, dt, prm)
+    assert torch.equal(y, oracle.fresh_step(S, x, B, C, dt, prm))
+    d = oracle.softplus_dt(dt.float(), prm.dt_bias, 0.2)
+    assert float(d.min()) >= 0.2
+
+
+# --------------------------------------------------------------------------- tiered
+def test_tiered_chunked_replay_equals_native_recurrence_ragged():
+    """The chunked flush (scale/v4_fused_decode.py:76-85) equals the per-token
+    recurrence in fp64, with per-slot phases, partial batches and join/leave."""
+    slots, H, P, G, k, c = 5, 4, 8, 2, 32, 4
+    gen, prm, S0 = _small(seed=14, b=slots, H=H, P=P, G=G)
+    phase = torch.tensor([0, 1, 2, 3, 2])
+    f64 = torch.float64
+    nat = oracle.NativeV4(slots, H, P, N, k, c, dtype=f64)
+    tie = oracle.TieredV4(slots, H, P, N, G, k, c, dtype=f64)
+    nat.join(torch.arange(slots), S0.double(), phase)
+    tie.join(torch.arange(slots), S0.double(), phase)
+    for step in range(30):
+        if step == 13:
+            Sj = oracle.make_state(1, H, P, N, gen).double()
+            nat.join(torch.tensor([2]), Sj, torch.tensor([3]))
+            tie.join(torch.tensor([2]), Sj, torch.tensor([3]))
+        sl = torch.randperm(slots, generator=gen)[:3 + step % 3]
+        x, B, C, dt = oracle.make_step_inputs(len(sl), H, P, N, G, gen)
+        y1 = nat.step(x, B, C, dt, prm, slots=sl)
+        y2 = tie.step(x, B, C, dt, prm, slots=sl)
+        assert torch.allclose(y1, y2, atol=1e-12)
+    assert torch.allclose(tie.materialize(torch.arange(slots), prm), nat.S, atol=1e-12)
+
+
+def test_tiered_flush_weights_detect_a_dropped_decay_term():
+    """A replay that forgets the suffix decay of older tokens disagrees with the
+    recurrence: the closed form is not retyped, it is checked against it."""
+    f64 = torch.float64
+    slots, H, P, G, k, c = 1, 2, 4, 1, 32, 4
+    gen, prm, S0 = _small(seed=15, b=slots, H=H, P=P, G=G)
+    tie = oracle.TieredV4(slots, H, P, N, G, k, c, dtype=f64)
+    tie.join(torch.arange(1), S0.double())
+    nat = oracle.NativeV4(slots, H, P, N, k, c, dtype=f64)
+    nat.join(torch.arange(1), S0.double())
+    for _ in range(c - 1):
+        ins = oracle.make_step_inputs(1, H, P, N, G, gen)
+        tie.step(*ins, prm)
+        nat.step(*ins, prm)
+    entries = tie.ring[0]
+    broken = [(e[0], e[1], e[2]) for e in entries]
+    dts = torch.stack([e[0] for e in broken])
+    X = torch.stack([e[1] for e in broken])
+    Bc = torch.stack([e[2] for e in broken])
+    a = dts * prm.to(f64).A[None, :]
+    no_suffix = tie.cold[0] * torch.exp(a.sum(0))[:, None, None] + torch.einsum("mh,mhp,mhn->hpn", dts, X, Bc)
+    good = tie.materialize(torch.arange(1), prm)[0][..., k:]
+    assert torch.allclose(good, nat.S[0][..., k:], atol=1e-12)
+    assert not torch.allclose(no_suffix, nat.S[0][..., k:], atol=1e-6)
+
+
+# --------------------------------------------------------------------------- fp8 / bf16
+def test_quant_fp8_row_scale_and_error_bound():
+    gen = torch.Generator().manual_seed(16)
+    s = torch.randn(3, 5, 96, generator=gen) * torch.logspace(-4, 1, 5)[None, :, None]
+    q, sc = oracle.quant_fp8(s)
+    assert q.dtype == torch.float8_e4m3fn and sc.shape == (3, 5, 1)
+    amax = s.abs().amax(-1, keepdim=True)
+    assert torch.equal(sc, amax / 448.0 + 1e-12)
+    d = oracle.read_fp8(q, sc)
+    # the row maximum lands on the largest finite code; every element within half an e4m3 ulp
+    assert torch.allclose(d.abs().amax(-1, keepdim=True), amax, rtol=2 ** -4)
+    rel = ((d - s).abs() / s.abs().clamp_min(sc * 2 ** -6)).max()
+    assert float(rel) <= 2 ** -4 + 1e-6
+
+
+def test_native_v4_fp8_tracks_fp32_within_quantisation_error():
+    b, H, P, G, k, c = 2, 8, 16, 2, 32, 4
+    gen, prm, S0 = _small(seed=17, b=b, H=H, P=P, G=G)
+    n32 = oracle.NativeV4(b, H, P, N, k, c, cold="fp32")
+    n8 = oracle.NativeV4(b, H, P, N, k, c, cold="fp8")
+    n8b = oracle.NativeV4(b, H, P, N, k, c, cold="fp8", fp8_restore_each_step=False)
+    for n in (n32, n8, n8b):
+        n.join(torch.arange(b), S0)
+    for _ in range(12):
+        x, B, C, dt = oracle.make_step_inputs(b, H, P, N, G, gen)
+        y32 = n32.step(x, B, C, dt, prm)
+        y8 = n8.step(x, B, C, dt, prm)
+        y8b = n8b.step(x, B, C, dt, prm)
+        rel = float((y8 - y32).norm() / y32.norm())
+        assert 0 < rel < 2e-2
+        # re-storing the dequantized snapshot each step (scale/vllm_v4_patch.py:173-175)
+        # keeps every code; only the row scale drifts (~1e-8 relative per re-store,
+        # from the +1e-12 term), so it matches quantizing at the flush only
+        assert torch.equal(n8.q8.view(torch.uint8), n8b.q8.view(torch.uint8))
+        assert float((n8.sc8 - n8b.sc8).abs().max() / n8b.sc8.abs().max()) < 1e-6
+        assert float((y8 - y8b).norm() / y8b.norm()) < 1e-7
+
+
+def test_native_v4_bf16_snapshot_is_rne_of_fp32():
+    b, H, P, G, k, c = 1, 4, 8, 1, 32, 2
+    gen, prm, S0 = _small(seed=18, b=b, H=H, P=P, G=G)
+    nb = oracle.NativeV4(b, H, P, N, k, c, cold="bf16")
+    nb.join(torch.arange(b), S0)
+    for _ in range(4):
+        nb.step(*oracle.make_step_inputs(b, H, P, N, G, gen), prm)
+    assert torch.equal(nb.snap, nb.S[..., k:].to(torch.bfloat16).float())
+
+
+def test_fp8_readout_matches_fp64_loop():
+    gen = torch.Generator().manual_seed(19)
+    R_, Nc, Pd = 3, 6, 5
+    q = torch.randn(R_, Nc, generator=gen)
+    sc = torch.rand(R_, Nc, generator=gen) + 0.1
+    S8 = torch.randn(R_, Nc, Pd, generator=gen).to(torch.float8_e4m3fn)
+    got = oracle.fp8_readout(q, S8, sc)
+    for r in range(R_):
+        for p in range(Pd):
+            want = sum(float(q[r, n]) * float(sc[r, n]) * float(S8[r, n, p].float()) for n in range(Nc))
+            assert abs(want - float(got[r, p])) < 1e-5
