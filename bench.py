@@ -1,8 +1,9 @@
 """State-op decode benchmark on one MI355X: tiered v4 vs fresh at the
 Nemotron-Nano-9B-v2 mixer shape (27 Mamba2 layers, H=128, P=80, N=128, G=8).
 
-A step is one decode token through the state op of all layers (one kernel
-launch per layer), inputs resident in HBM, synthetic seeded data. Prints one
+A step is one decode token through the state op of all layers (two kernel
+launches per layer: prep and stream), inputs resident in HBM, synthetic
+seeded data. Prints one
 JSON line (the driver contract); progress goes to stderr.
 
     python bench.py [--steps 64] [--warmup 8] [--B 256] [--c 4] [--k 32] [--cold fp32]
@@ -27,7 +28,7 @@ def log(*a):
 
 
 # ---------------------------------------------------------------------------
-# algorithmic byte model (per request per layer-token); see DESIGN.md
+# algorithmic byte model (bytes per request per layer-token)
 def bytes_io():
     # x bf16 + B, C bf16 + dt bf16 in, y fp32 out
     return H * P * 2 + 2 * G * N * 2 + H * 2 + H * P * 4
@@ -218,6 +219,20 @@ def cpu_baseline(args, budget_s):
     }
 
 
+def measured_traffic(key):
+    """HBM bytes per layer-token measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
+    (calibrated against a plain copy) and recorded in profiles/*.md as
+    `traffic[<key>]: <bytes>`; None when no profile covers this workload."""
+    import glob
+    import re
+
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*.md"))):
+        for m in re.finditer(r"traffic\[(.*?)\]:\s*(\d+)", open(path).read()):
+            if m.group(1) == key:
+                return int(m.group(2))
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -248,7 +263,7 @@ def main():
 
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): the tiered state op has no "
-              f"cross-GPU exchange; see DESIGN.md for how it would shard", file=sys.stderr)
+              f"cross-GPU exchange (requests shard across GPUs with no collective)", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
@@ -284,6 +299,8 @@ def main():
     per_launch_bytes = args.B * (bytes_v4_token(args.k, args.c, args.cold) if head == "v4"
                                  else bytes_fresh_token()) + bytes_rotation()
     achieved = per_launch_bytes / (ms_ev * 1e-3) / 1e9
+    tkey = f"v4 B={args.B} k={args.k} c={args.c} {args.cold}" if head == "v4" else f"fresh B={args.B}"
+    traffic = measured_traffic(tkey)
     out = {
         "metric": "state-op tokens/s at 9B shape B=256 (v4-c4 vs fresh); achieved HBM GB/s vs peak",
         "value": round(args.B / ms_step * 1e3, 1),
@@ -309,8 +326,9 @@ def main():
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": None,
-            "kernel": f"step_kernel<{args.k if head == 'v4' else N}, {args.cold if head == 'v4' else 'none'}>",
+            "traffic": traffic,
+            "kernel": (f"prep_kernel + stream_kernel<{args.k if head == 'v4' else N}, "
+                       f"{args.cold if head == 'v4' else 'none'}> (one layer-token, two launches)"),
             "algorithmic_bytes_per_launch": int(per_launch_bytes),
             "avg_launch_us_events": round(ms_ev * 1e3, 2),
             "avg_launch_us_region": round(ms_launch * 1e3, 2),

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define NSSM_ABI_VERSION 1
+#define NSSM_ABI_VERSION 2
 
 /* error codes */
 #define NSSM_OK 0
@@ -49,6 +49,7 @@ extern "C" {
 #define NSSM_E_KIND (-4)        /* unknown cold storage kind             */
 #define NSSM_E_LAUNCH (-5)      /* the HIP launch reported an error      */
 #define NSSM_E_TUNING (-6)      /* launch override does not fit the dims */
+#define NSSM_E_WORKSPACE (-7)   /* workspace NULL or too small           */
 
 /* cold tier storage kinds */
 #define NSSM_COLD_FP32 0 /* one exact fp32 copy, read every token, rewritten at flush */
@@ -109,21 +110,31 @@ typedef struct nssm_tier {
 int nssm_tier_sizes(int32_t slots, int32_t H, int32_t P, int32_t N, int32_t G,
                     int32_t k_hot, int32_t c, int32_t cold_kind, int64_t* sizes_out);
 
+/* Bytes of device workspace a step needs for b requests (c = 0 for the
+ * untiered step), or a negative NSSM_E* code. The workspace holds the rotated
+ * B and C, per-head decay scalars and flush weights of one call; it is
+ * caller-owned, 16-byte aligned, and must not be shared by steps that run
+ * concurrently on different streams. */
+int64_t nssm_step_workspace_bytes(int32_t b, int32_t H, int32_t G, int32_t N, int32_t c);
+
 /* Untiered decode step over the full fp32 state [slots][H][P][N]:
  *   B',C' = R_g B, R_g C;  dt = softplus(dt + dt_bias);  a = dt*A
  *   S <- exp(a) S + (dt x) (x) B';   y = S C' + D x          (y fp32 [b][H][P]) */
 int nssm_fresh_step(const nssm_layer_params* prm, float* state, int32_t slots,
-                    const nssm_step_inputs* in, float* y, void* stream);
+                    const nssm_step_inputs* in, float* y, void* workspace,
+                    int64_t workspace_bytes, void* stream);
 
 /* Tiered decode step (hot fresh, cold stale + decay-corrected, ring append,
- * in-launch flush for requests whose phase wraps):
+ * flush for requests whose phase wraps), two kernels on `stream`:
  *   hot  <- exp(a) hot + (dt x) (x) B'[:K]
  *   y    =  hot C'[:K] + exp(glog) * (cold_read C'[K:]) + D x
- *   t += 1; if t % c == 0: cold <- exact cold state at t (chunked decayed
- *   replay of the ring plus this token), glog <- 0; else glog += a and this
- *   token is appended to the ring. */
+ *   this token (x, dt, B'[K:]) goes to ring position t % c; t += 1;
+ *   if t % c == 0: cold <- exact cold state at t (decayed replay of the nv
+ *   buffered tokens and this one onto the snapshot), nv <- 0, glog <- 0;
+ *   else nv += 1, glog += a. */
 int nssm_v4_step(const nssm_layer_params* prm, const nssm_tier* tier,
-                 const nssm_step_inputs* in, float* y, void* stream);
+                 const nssm_step_inputs* in, float* y, void* workspace,
+                 int64_t workspace_bytes, void* stream);
 
 /* Capture a tier from full fp32 states [b][H][P][N] into slot_ids[b] (NULL =
  * 0..b-1): hot = S[..,:K], cold = S[..,K:] (quantized for BF16/FP8),

@@ -54,8 +54,11 @@ def lib():
     L.nssm_strerror.restype = ctypes.c_char_p
     L.nssm_strerror.argtypes = [ctypes.c_int]
     L.nssm_tier_sizes.argtypes = [c_i32] * 8 + [P_(ctypes.c_int64)]
-    L.nssm_fresh_step.argtypes = [P_(LayerParams), c_vp, c_i32, P_(StepInputs), c_vp, c_vp]
-    L.nssm_v4_step.argtypes = [P_(LayerParams), P_(Tier), P_(StepInputs), c_vp, c_vp]
+    c_i64 = ctypes.c_int64
+    L.nssm_step_workspace_bytes.argtypes = [c_i32] * 5
+    L.nssm_step_workspace_bytes.restype = c_i64
+    L.nssm_fresh_step.argtypes = [P_(LayerParams), c_vp, c_i32, P_(StepInputs), c_vp, c_vp, c_i64, c_vp]
+    L.nssm_v4_step.argtypes = [P_(LayerParams), P_(Tier), P_(StepInputs), c_vp, c_vp, c_i64, c_vp]
     L.nssm_v4_join.argtypes = [P_(LayerParams), P_(Tier), c_vp, c_i32, c_vp, c_vp, c_vp]
     L.nssm_v4_materialize.argtypes = [P_(LayerParams), P_(Tier), c_vp, c_i32, c_vp, c_vp]
     L.nssm_fp8_readout.argtypes = [c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_vp]
@@ -80,7 +83,7 @@ def check(rc: int, what: str) -> None:
 
 
 # symbols include/nssm.h declares (checked by the CPU test-suite)
-EXPORTED = ("nssm_tier_sizes", "nssm_fresh_step", "nssm_v4_step", "nssm_v4_join",
+EXPORTED = ("nssm_tier_sizes", "nssm_step_workspace_bytes", "nssm_fresh_step", "nssm_v4_step", "nssm_v4_join",
             "nssm_v4_materialize", "nssm_fp8_readout", "nssm_rotate", "nssm_set_launch",
             "nssm_host_f32_to_e4m3fn", "nssm_host_e4m3fn_to_f32", "nssm_host_f32_to_bf16",
             "nssm_strerror", "nssm_abi_version")

@@ -1,18 +1,24 @@
 // gfx950 kernels for the Mamba2 decode-step recurrent-state update with
 // nested hot/cold tiering, and the C ABI declared in include/nssm.h.
 //
-// Work decomposition (one launch per layer per decode token):
-//   workgroup = (request i, group g, head block hb) with `hpw` heads of group g.
-//   The workgroup rotates B and C of (i, g) once (B' = R_g B, C' = R_g C, fp32)
-//   into LDS, then its waves stream the heads' state rows.
-//   A "unit" is 8 consecutive headdim rows p of one head. In a unit, lane l owns
-//   row p0 + (l >> 3) and, in every 32-column segment s of the row, the four
-//   columns 32 s + 4 (l & 7) .. +3. One dwordx4 per lane per segment moves
-//   8 rows x 128 B = 1 KB per wave instruction; the C.h readout of a row is a
-//   sum over its 8 lanes (three DPP steps).
-//   Hot columns [0, K) are read and written every token. Cold columns [K, N)
-//   are only read, except at the flush token of the request, when the
-//   workgroup replays the buffered tokens into them.
+// One layer-token is two launches on the caller's stream:
+//
+//  prep    one workgroup per (request, group). Rotates B and C once
+//          (B' = R_g B, C' = R_g C, fp32) into the workspace, computes each
+//          head's dt, decay, the stale-read factor exp(glog), the flush flag
+//          and, at a flush, the decay weights of the buffered window; updates
+//          t, nv, glog; appends this token (x, dt, B' cold columns) to the ring
+//          at position t % c. A flush token sits at c-1, so a flush window is
+//          always ring positions [c-m, c).
+//  stream  one workgroup per (request, head block): streams the state rows.
+//          A "unit" is 8 consecutive headdim rows p of one head. In a unit,
+//          lane l owns row p0 + (l >> 3) and, in every 32-column segment s, the
+//          four columns 32 s + 4 (l & 7) .. +3. One dwordx4 per lane per
+//          segment moves 8 rows x 128 B = 1 KB per wave instruction; the C.h
+//          readout of a row is a sum over its 8 lanes (three DPP steps).
+//          Hot columns [0, K) are read and written every token; cold columns
+//          [K, N) are only read, except at the request's flush token, when the
+//          workgroup replays the staged window into them.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -52,9 +58,24 @@ struct StepArgs {
   const float* D;
   const float* R;
   float* y;
-  int32_t b, slots, H, P, G, HG, c, hpw, nhb;
+  float* ws;  // workspace (see Ws below)
+  int32_t b, slots, H, P, G, HG, c, K, hpw, nhb;
   float dt_min;
 };
+
+// Workspace carve-up for b requests (floats): rotated B and C [b][G][N] each,
+// per-head scalars [b][H][HD_STRIDE], flush weights [b][H][c].
+enum { HD_DT = 0, HD_A, HD_DECAY, HD_EG, HD_D, HD_FLUSH, HD_DTOT, HD_M, HD_POS, HD_STRIDE = 12 };
+struct Ws {
+  float *B, *C, *hd, *w;
+  __host__ __device__ Ws(float* base, int b, int H, int G, int c) {
+    B = base;
+    C = B + (size_t)b * G * kN;
+    hd = C + (size_t)b * G * kN;
+    w = hd + (size_t)b * H * HD_STRIDE;
+  }
+};
+size_t ws_floats(int b, int H, int G, int c) { return (size_t)b * (2 * G * kN + H * HD_STRIDE + H * c); }
 
 __device__ __forceinline__ float bf2f(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
 
@@ -87,11 +108,6 @@ __device__ __forceinline__ float sum32(float v) {
 
 __device__ __forceinline__ float softplus_f(float v) { return v > 20.f ? v : log1pf(expf(v)); }
 
-// ---------------------------------------------------------------------------
-// per-head scalars kept in LDS
-// (stride padded to a multiple of 4 floats so the LDS arrays after it stay 16-byte aligned)
-enum { HD_DT = 0, HD_A, HD_DECAY, HD_EG, HD_D, HD_FLUSH, HD_DTOT, HD_T, HD_NV, HD_STRIDE = 12 };
-
 // Streaming access to the state: non-temporal (the state is touched once per
 // token and is far larger than L2 and the MALL) unless built otherwise.
 #ifndef NSSM_NT_LOAD
@@ -116,8 +132,168 @@ __device__ __forceinline__ void st_stream(T v, T* p) {
   else *p = v;
 }
 
-// Raw registers of one unit for one lane: HS hot float4 and CS cold segments
-// (float4 / 4 x bf16 / 4 x e4m3 by storage kind).
+// ---------------------------------------------------------------------------
+// prep: one workgroup (256 threads = 4 waves) per (request, group). Latency
+// bound: every independent global load is issued before the first barrier.
+constexpr int kPrepThreads = 256;
+
+template <bool TIERED>
+__global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
+  constexpr int NW = kPrepThreads / 64;
+  constexpr int ROWS = kN / (2 * NW);  // rows of R per half-wave
+  constexpr int RB = ROWS / 2;         // rows per batch in flight
+  __shared__ float sBraw[kN], sCraw[kN], sBr[kN];
+  __shared__ int sPos, sFlush;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = blockIdx.x % a.G, bi = blockIdx.x / a.G;
+  const int H = a.H, HG = a.HG, c = a.c;
+  const int slot = a.slot_ids ? a.slot_ids[bi] : bi;
+  if (slot < 0 || slot >= a.slots) return;  // the stream kernel writes NaN rows for it
+  const Ws ws(a.ws, a.b, H, a.G, c);
+  const size_t bgo = ((size_t)bi * a.G + g) * kN;
+  const int hw = lane >> 5, hl = lane & 31;
+  const float* __restrict__ Rg = a.R ? a.R + (size_t)g * kN * kN : nullptr;
+
+  // 1. independent loads: first batch of R rows, B and C, the head's inputs
+  f4 r[RB];
+  if (Rg) {
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+      r[i] = *reinterpret_cast<const f4*>(Rg + (size_t)(2 * wave + hw + 2 * NW * i) * kN + 4 * hl);
+  }
+  if (tid < kN) {
+    sBraw[tid] = bf2f(a.Bm[bgo + tid]);
+    sCraw[tid] = bf2f(a.Cm[bgo + tid]);
+  }
+  const bool head_thread = tid < HG;
+  const int h = g * HG + tid;
+  const size_t o = (size_t)slot * H + h;
+  float draw = 0.f, dtb = 0.f, Ah = 0.f, Dh = 0.f, gl = 0.f;
+  int tt = 0, nvv = 0;
+  if (head_thread) {
+    draw = bf2f(a.dt_raw[(size_t)bi * H + h]);
+    dtb = a.dt_bias[h];
+    Ah = a.A[h];
+    Dh = a.D[h];
+    if constexpr (TIERED) {
+      tt = a.t[o];
+      nvv = a.nv[o];
+      gl = a.glog[o];
+    }
+  }
+  __syncthreads();
+
+  // 2. rotation: a half-wave per row of R (both halves see the same rows
+  // count, so every reduction runs with all lanes active)
+  if (Rg) {
+    const f4 bv = *reinterpret_cast<const f4*>(sBraw + 4 * hl);
+    const f4 cv = *reinterpret_cast<const f4*>(sCraw + 4 * hl);
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      if (half == 1) {
+#pragma unroll
+        for (int i = 0; i < RB; ++i)
+          r[i] = *reinterpret_cast<const f4*>(Rg + (size_t)(2 * wave + hw + 2 * NW * (RB + i)) * kN + 4 * hl);
+      }
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        const int mrow = 2 * wave + hw + 2 * NW * (half * RB + i);
+        float db = r[i].x * bv.x;
+        db = fmaf(r[i].y, bv.y, db);
+        db = fmaf(r[i].z, bv.z, db);
+        db = fmaf(r[i].w, bv.w, db);
+        float dc = r[i].x * cv.x;
+        dc = fmaf(r[i].y, cv.y, dc);
+        dc = fmaf(r[i].z, cv.z, dc);
+        dc = fmaf(r[i].w, cv.w, dc);
+        db = sum32(db);
+        dc = sum32(dc);
+        if (hl == 0) {
+          sBr[mrow] = db;
+          ws.B[bgo + mrow] = db;
+          ws.C[bgo + mrow] = dc;
+        }
+      }
+    }
+  } else if (tid < kN) {
+    sBr[tid] = sBraw[tid];
+    ws.B[bgo + tid] = sBraw[tid];
+    ws.C[bgo + tid] = sCraw[tid];
+  }
+
+  // 3. per-head scalars and bookkeeping: one thread per head of the group
+  if (head_thread) {
+    float dt = softplus_f(draw + dtb);
+    if (a.dt_min > 0.f) dt = fmaxf(dt, a.dt_min);
+    const float av = dt * Ah;
+    float* __restrict__ hd = ws.hd + ((size_t)bi * H + h) * HD_STRIDE;
+    hd[HD_DT] = dt;
+    hd[HD_A] = av;
+    hd[HD_DECAY] = expf(av);
+    hd[HD_D] = Dh;
+    if constexpr (TIERED) {
+      // t >= 0 and 0 <= nv < c hold for every tier these kernels write; the
+      // clamps keep ring indexing inside the buffers even for a corrupted phase
+      tt = max(tt, 0);
+      nvv = min(max(nvv, 0), c - 1);
+      const int pos = tt % c;
+      const bool flush = (tt + 1) % c == 0;  // then pos == c - 1
+      hd[HD_EG] = expf(gl);
+      hd[HD_FLUSH] = flush ? 1.f : 0.f;
+      hd[HD_POS] = (float)pos;
+      if (flush) {
+        // window = the nv buffered tokens at ring [c-m, c-1) and this one:
+        // w_i = exp(sum_{l>i} a_l) dt_i, total decay exp(sum_l a_l)
+        const int m = nvv + 1;
+        const float* __restrict__ rdt = a.ring_dt + o * c + (c - m);
+        float* __restrict__ w = ws.w + ((size_t)bi * H + h) * c;
+        float suf = 0.f;
+        for (int i = m - 1; i >= 0; --i) {
+          const float dti = i == m - 1 ? dt : rdt[i];
+          w[i] = expf(suf) * dti;
+          suf += dti * Ah;
+        }
+        hd[HD_DTOT] = expf(suf);
+        hd[HD_M] = (float)m;
+        a.nv[o] = 0;
+        a.glog[o] = 0.f;
+      } else {
+        hd[HD_DTOT] = 1.f;
+        hd[HD_M] = 0.f;
+        a.ring_dt[o * c + pos] = dt;
+        a.nv[o] = nvv + 1;
+        a.glog[o] = gl + av;
+      }
+      a.t[o] = tt + 1;
+      if (tid == 0) {
+        sPos = pos;
+        sFlush = flush;
+      }
+    } else {
+      hd[HD_EG] = 0.f;
+      hd[HD_FLUSH] = 0.f;
+      hd[HD_DTOT] = 1.f;
+      hd[HD_M] = 0.f;
+      hd[HD_POS] = 0.f;
+    }
+  }
+
+  // 4. ring append of the rotated B cold columns (tokens that do not flush;
+  // a flush token's columns are read from the workspace). x goes to the ring
+  // from the stream kernel.
+  if constexpr (TIERED) {
+    __syncthreads();  // sPos, sFlush, sBr
+    if (!sFlush) {
+      const int NC = kN - a.K;
+      const size_t rb = (((size_t)slot * a.G + g) * c + sPos) * NC;
+      for (int n = tid; n < NC; n += kPrepThreads) a.ring_b[rb + n] = sBr[a.K + n];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// stream: raw registers of one unit for one lane: HS hot float4 and CS cold
+// segments (float4 / 4 x bf16 / 4 x e4m3 by storage kind).
 template <int K, int COLD>
 struct UnitRaw {
   static constexpr int HS = K / 32;
@@ -128,10 +304,12 @@ struct UnitRaw {
   u2v cb[COLD == NSSM_COLD_BF16 ? CSR : 1];
   uint32_t c8[COLD == NSSM_COLD_FP8 ? CSR : 1];
   float sc;
+  float xp;
+  uint16_t xraw;
 };
 
 template <int K, int COLD>
-__device__ __forceinline__ void unit_load(const StepArgs& a, size_t row, int q, UnitRaw<K, COLD>& d) {
+__device__ __forceinline__ void unit_load(const StepArgs& a, size_t row, size_t xrow, int q, UnitRaw<K, COLD>& d) {
   constexpr int HS = K / 32, CS = (kN - K) / 32, NC = kN - K;
   const f4* hp = reinterpret_cast<const f4*>(a.hot + row * K) + q;
 #pragma unroll
@@ -152,6 +330,8 @@ __device__ __forceinline__ void unit_load(const StepArgs& a, size_t row, int q, 
       d.sc = a.scale[row];
     }
   }
+  d.xraw = a.x[xrow];
+  d.xp = bf2f(d.xraw);
 }
 
 // read-copy values the readout sees
@@ -216,22 +396,20 @@ __device__ __forceinline__ void cold_store(const StepArgs& a, size_t row, int q,
   }
 }
 
-// Compute and store one unit (8 rows of head j) from its raw registers. FLUSH
-// selects the replay of the buffered window into the cold columns (sU/sBc
-// staged by the caller).
+// Compute and store one unit (8 rows of head h) from its raw registers. FLUSH
+// selects the replay of the staged window (sU [m][P] of this head, sBc [m][NC]).
 template <int K, int COLD, bool FLUSH>
-__device__ __forceinline__ void unit_compute(const StepArgs& a, size_t row, int bi, int h, int j, int p, int q,
-                                             UnitRaw<K, COLD>& d, const float (&Bh)[K / 32][4],
-                                             const float (&Ch)[K / 32][4],
-                                             const float (&Cc)[UnitRaw<K, COLD>::CSR][4], const float* sX,
-                                             const float* sHd, const float* sU, const float* sBc, int m) {
+__device__ __forceinline__ void unit_compute(const StepArgs& a, size_t row, size_t yrow, int p, int q,
+                                             UnitRaw<K, COLD>& d, uint16_t* rx, const float* __restrict__ hd,
+                                             const float (&Bh)[K / 32][4], const float (&Ch)[K / 32][4],
+                                             const float (&Cc)[UnitRaw<K, COLD>::CSR][4], const float* sU,
+                                             const float* sBc, int m) {
   constexpr int HS = K / 32;
   constexpr int NC = kN - K;
   constexpr int CS = NC / 32;
   constexpr int CSR = UnitRaw<K, COLD>::CSR;
   const int P = a.P;
-  const float* hd = sHd + j * HD_STRIDE;
-  const float xp = sX[j * P + p];
+  const float xp = d.xp;
   const float uu = hd[HD_DT] * xp;
   const float dec = hd[HD_DECAY];
   float ph = 0.f;
@@ -299,151 +477,66 @@ __device__ __forceinline__ void unit_compute(const StepArgs& a, size_t row, int 
     }
   }
   part = sum8(part);
-  if (q == 0) a.y[((size_t)bi * a.H + h) * P + p] = fmaf(hd[HD_D], xp, part);
+  if (q == 0) {
+    a.y[yrow] = fmaf(hd[HD_D], xp, part);
+    if (rx) rx[p] = d.xraw;  // ring append of x (tokens that do not flush)
+  }
 }
 
+// one workgroup per (request, block of hpw heads of one group)
 template <int K, int COLD>
-__global__ void __launch_bounds__(kMaxWaves * 64) step_kernel(StepArgs a) {
+__global__ void __launch_bounds__(kMaxWaves * 64) stream_kernel(StepArgs a) {
   constexpr int HS = K / 32;
   constexpr int NC = kN - K;
   constexpr int CS = NC / 32;
+  constexpr int CSR = CS > 0 ? CS : 1;
   constexpr bool TIERED = NC > 0;
   extern __shared__ float lds[];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
-  const int hb = blockIdx.x % a.nhb;
-  const int bg = blockIdx.x / a.nhb;
-  const int g = bg % a.G;
-  const int bi = bg / a.G;
-  const int P = a.P, H = a.H, hpw = a.hpw;
-  const int h0 = g * a.HG + hb * hpw;
-
-  float* sBraw = lds;
-  float* sCraw = sBraw + kN;
-  float* sB = sCraw + kN;
-  float* sC = sB + kN;
-  float* sX = sC + kN;
-  float* sHd = sX + hpw * P;
-  float* sBc = sHd + hpw * HD_STRIDE;       // [c][NC] rotated B cold columns of the window
-  float* sU = sBc + (TIERED ? a.c * NC : 0);  // [c][P] w_i dt_i x_i
-  float* sLa = sU + (TIERED ? a.c * P : 0);   // [c] log decays a_i
-  float* sDt = sLa + (TIERED ? a.c : 0);      // [c] dt_i
-  float* sW = sDt + (TIERED ? a.c : 0);       // [c] w_i dt_i
-
+  const int hb = blockIdx.x % a.nhb, bi = blockIdx.x / a.nhb;
+  const int H = a.H, P = a.P, hpw = a.hpw, c = a.c;
+  const int h0 = hb * hpw, g = h0 / a.HG;
   const int slot = a.slot_ids ? a.slot_ids[bi] : bi;
   if (slot < 0 || slot >= a.slots) {  // uniform over the workgroup
     for (int i = tid; i < hpw * P; i += blockDim.x) a.y[((size_t)bi * H + h0) * P + i] = __builtin_nanf("");
     return;
   }
-
-  // 1. stage B, C (fp32), x, per-head scalars
-  {
-    const size_t bgo = ((size_t)bi * a.G + g) * kN;
-    for (int i = tid; i < kN; i += blockDim.x) {
-      sBraw[i] = bf2f(a.Bm[bgo + i]);
-      sCraw[i] = bf2f(a.Cm[bgo + i]);
-    }
-    const size_t xo = ((size_t)bi * H + h0) * P;
-    for (int i = tid; i < hpw * P; i += blockDim.x) sX[i] = bf2f(a.x[xo + i]);
-    if (tid < hpw) {
-      const int h = h0 + tid;
-      float dt = softplus_f(bf2f(a.dt_raw[(size_t)bi * H + h]) + a.dt_bias[h]);
-      if (a.dt_min > 0.f) dt = fmaxf(dt, a.dt_min);
-      const float av = dt * a.A[h];
-      float* hd = sHd + tid * HD_STRIDE;
-      hd[HD_DT] = dt;
-      hd[HD_A] = av;
-      hd[HD_DECAY] = expf(av);
-      hd[HD_D] = a.D[h];
-      if constexpr (TIERED) {
-        // t >= 0 and 0 <= nv < c hold for every tier written by these kernels; the
-        // clamps keep ring indexing inside the buffers even for a corrupted phase
-        const int tt = max(a.t[(size_t)slot * H + h], 0);
-        const int nvv = min(max(a.nv[(size_t)slot * H + h], 0), a.c - 1);
-        hd[HD_EG] = expf(a.glog[(size_t)slot * H + h]);
-        hd[HD_FLUSH] = ((tt + 1) % a.c == 0) ? 1.f : 0.f;
-        hd[HD_T] = __int_as_float(tt);
-        hd[HD_NV] = __int_as_float(nvv);
-      } else {
-        hd[HD_EG] = 0.f;
-        hd[HD_FLUSH] = 0.f;
-      }
-    }
-  }
-  __syncthreads();
-
-  // 2. rotation B' = R_g B, C' = R_g C: half-wave per output row of R
-  if (a.R) {
-    const int hw = lane >> 5, hl = lane & 31;
-    const f4 bv = *reinterpret_cast<const f4*>(sBraw + 4 * hl);
-    const f4 cv = *reinterpret_cast<const f4*>(sCraw + 4 * hl);
-    const float* Rg = a.R + (size_t)g * kN * kN;
-    // RB rows of R in flight per half-wave; both half-waves of a wave see the
-    // same trip counts (kN is even), so the reductions run with all lanes active
-    constexpr int RB = 8;
-    for (int m0 = 2 * wave + hw; m0 < kN; m0 += 2 * nw * RB) {
-      f4 r[RB];
-#pragma unroll
-      for (int i = 0; i < RB; ++i) {
-        const int mrow = m0 + 2 * nw * i;
-        if (mrow < kN) r[i] = *reinterpret_cast<const f4*>(Rg + (size_t)mrow * kN + 4 * hl);
-      }
-#pragma unroll
-      for (int i = 0; i < RB; ++i) {
-        const int mrow = m0 + 2 * nw * i;
-        if (mrow < kN) {
-          float db = r[i].x * bv.x;
-          db = fmaf(r[i].y, bv.y, db);
-          db = fmaf(r[i].z, bv.z, db);
-          db = fmaf(r[i].w, bv.w, db);
-          float dc = r[i].x * cv.x;
-          dc = fmaf(r[i].y, cv.y, dc);
-          dc = fmaf(r[i].z, cv.z, dc);
-          dc = fmaf(r[i].w, cv.w, dc);
-          db = sum32(db);
-          dc = sum32(dc);
-          if (hl == 0) {
-            sB[mrow] = db;
-            sC[mrow] = dc;
-          }
-        }
-      }
-    }
-  } else {
-    for (int i = tid; i < kN; i += blockDim.x) {
-      sB[i] = sBraw[i];
-      sC[i] = sCraw[i];
-    }
-  }
-  __syncthreads();
-
-  // 3. per-lane coefficients
+  const Ws ws(a.ws, a.b, H, a.G, c);
   const int q = lane & 7, rr = lane >> 3;
-  float Bh[HS][4], Ch[HS][4];
-  constexpr int CSR = CS > 0 ? CS : 1;
-  float Cc[CSR][4];
-#pragma unroll
-  for (int s = 0; s < HS; ++s)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      Bh[s][e] = sB[32 * s + 4 * q + e];
-      Ch[s][e] = sC[32 * s + 4 * q + e];
-    }
-#pragma unroll
-  for (int s = 0; s < CSR; ++s)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) Cc[s][e] = CS > 0 ? sC[K + 32 * s + 4 * q + e] : 0.f;
 
-  const int RG = P >> 3;
-  bool any_flush = false;
-  if constexpr (TIERED) {
-    for (int j = 0; j < hpw; ++j) any_flush |= sHd[j * HD_STRIDE + HD_FLUSH] != 0.f;
+  // per-lane coefficients of group g (rotated by the prep kernel)
+  const float* wB = ws.B + ((size_t)bi * a.G + g) * kN;
+  const float* wC = ws.C + ((size_t)bi * a.G + g) * kN;
+  float Bh[HS][4], Ch[HS][4], Cc[CSR][4];
+#pragma unroll
+  for (int s = 0; s < HS; ++s) {
+    const f4 tb = *reinterpret_cast<const f4*>(wB + 32 * s + 4 * q);
+    const f4 tc = *reinterpret_cast<const f4*>(wC + 32 * s + 4 * q);
+    Bh[s][0] = tb.x; Bh[s][1] = tb.y; Bh[s][2] = tb.z; Bh[s][3] = tb.w;
+    Ch[s][0] = tc.x; Ch[s][1] = tc.y; Ch[s][2] = tc.z; Ch[s][3] = tc.w;
+  }
+#pragma unroll
+  for (int s = 0; s < CSR; ++s) {
+    if constexpr (CS > 0) {
+      const f4 tc = *reinterpret_cast<const f4*>(wC + K + 32 * s + 4 * q);
+      Cc[s][0] = tc.x; Cc[s][1] = tc.y; Cc[s][2] = tc.z; Cc[s][3] = tc.w;
+    } else {
+      Cc[s][0] = Cc[s][1] = Cc[s][2] = Cc[s][3] = 0.f;
+    }
   }
 
-  if (!any_flush) {
+  const float* hdb = ws.hd + ((size_t)bi * H + h0) * HD_STRIDE;
+  const int RG = P >> 3;
+  const int units = hpw * RG;
+  bool flush = false;
+  if constexpr (TIERED) {
+    for (int j = 0; j < hpw; ++j) flush |= hdb[j * HD_STRIDE + HD_FLUSH] != 0.f;
+  }
+
+  if (!flush) {
     // U units per wave in flight: all their loads are issued before any compute
     constexpr int U = NSSM_UNROLL;
-    const int units = hpw * RG;
     for (int u0 = wave; u0 < units; u0 += U * nw) {
       UnitRaw<K, COLD> d[U];
 #pragma unroll
@@ -452,7 +545,7 @@ __global__ void __launch_bounds__(kMaxWaves * 64) step_kernel(StepArgs a) {
         if (u < units) {
           const int j = u / RG;
           const int p = (u - j * RG) * 8 + rr;
-          unit_load<K, COLD>(a, ((size_t)slot * H + h0 + j) * P + p, q, d[i]);
+          unit_load<K, COLD>(a, ((size_t)slot * H + h0 + j) * P + p, ((size_t)bi * H + h0 + j) * P + p, q, d[i]);
         }
       }
 #pragma unroll
@@ -461,103 +554,64 @@ __global__ void __launch_bounds__(kMaxWaves * 64) step_kernel(StepArgs a) {
         if (u < units) {
           const int j = u / RG;
           const int p = (u - j * RG) * 8 + rr;
-          unit_compute<K, COLD, false>(a, ((size_t)slot * H + h0 + j) * P + p, bi, h0 + j, j, p, q, d[i], Bh, Ch,
-                                       Cc, sX, sHd, sU, sBc, 0);
+          const float* hd = hdb + j * HD_STRIDE;
+          uint16_t* rx = nullptr;
+          if constexpr (TIERED) rx = a.ring_x + (((size_t)slot * H + h0 + j) * c + (int)hd[HD_POS]) * P;
+          unit_compute<K, COLD, false>(a, ((size_t)slot * H + h0 + j) * P + p, ((size_t)bi * H + h0 + j) * P + p,
+                                       p, q, d[i], rx, hd, Bh, Ch, Cc, nullptr, nullptr, 0);
         }
       }
     }
   } else if constexpr (TIERED) {
-    // window: nv buffered tokens at ring positions [c-1-nv, c-1) plus this one
-    const int c = a.c;
-    const int nv0 = __float_as_int(sHd[HD_NV]);
-    const int m = nv0 + 1;
-    {
-      const size_t rb = ((size_t)slot * a.G + g) * c;
-      for (int i = tid; i < (m - 1) * NC; i += blockDim.x) {
-        const int e = i / NC, n = i - e * NC;
-        sBc[i] = a.ring_b[(rb + (c - 1 - nv0 + e)) * NC + n];
+    // the first unit's state loads go out before the window staging
+    UnitRaw<K, COLD> dcur;
+    if (wave < units) {
+      const int j = wave / RG, p = (wave - j * RG) * 8 + rr;
+      unit_load<K, COLD>(a, ((size_t)slot * H + h0 + j) * P + p, ((size_t)bi * H + h0 + j) * P + p, q, dcur);
+    }
+    // stage the flush window, tokens i = 0..m-1 (the last is this token):
+    // rotated B cold columns of the group and w_i dt_i x_i of each head; the
+    // buffered tokens sit at ring positions [c-m, c-1)
+    const int m = min(max((int)hdb[HD_M], 1), c);
+    float* sBc = lds;          // [m][NC]
+    float* sU = lds + c * NC;  // [hpw][m][P]
+    const size_t rb = ((size_t)slot * a.G + g) * c + (c - m);
+    for (int i = tid; i < m * NC; i += blockDim.x) {
+      const int e = i / NC, n = i - e * NC;
+      sBc[i] = e < m - 1 ? a.ring_b[rb * NC + i] : wB[K + n];
+    }
+    for (int i = tid; i < hpw * m * P; i += blockDim.x) {
+      const int j = i / (m * P), r = i - j * m * P, e = r / P, p = r - e * P;
+      const uint16_t xv = e < m - 1 ? a.ring_x[(((size_t)slot * H + h0 + j) * c + (c - m + e)) * P + p]
+                                    : a.x[((size_t)bi * H + h0 + j) * P + p];
+      sU[i] = ws.w[((size_t)bi * H + h0 + j) * c + e] * bf2f(xv);
+    }
+    __syncthreads();
+    // software pipeline: the next unit's loads are in flight during this one's compute
+    for (int u = wave; u < units; u += nw) {
+      UnitRaw<K, COLD> dnext;
+      const int un = u + nw;
+      if (un < units) {
+        const int j = un / RG, p = (un - j * RG) * 8 + rr;
+        unit_load<K, COLD>(a, ((size_t)slot * H + h0 + j) * P + p, ((size_t)bi * H + h0 + j) * P + p, q, dnext);
       }
-      for (int n = tid; n < NC; n += blockDim.x) sBc[(m - 1) * NC + n] = sB[K + n];
-    }
-    for (int j = 0; j < hpw; ++j) {
-      const int h = h0 + j;
-      float* hd = sHd + j * HD_STRIDE;
-      const bool fl = hd[HD_FLUSH] != 0.f;
-      __syncthreads();  // sU / sAw of the previous head consumed
-      if (fl) {
-        const size_t rh = ((size_t)slot * H + h) * c;
-        // log decays a_i and dt_i of the window (token i = 0..m-1, the last is this token)
-        if (tid < m) {
-          const float dti = tid < m - 1 ? a.ring_dt[rh + (c - 1 - nv0 + tid)] : hd[HD_DT];
-          sDt[tid] = dti;
-          sLa[tid] = dti * a.A[h];
-        }
-        __syncthreads();
-        // w_i = exp(sum_{l>i} a_l) * dt_i;  total decay exp(sum_l a_l)
-        if (tid < m) {
-          float suf = 0.f;
-          for (int l = m - 1; l > tid; --l) suf += sLa[l];
-          sW[tid] = expf(suf) * sDt[tid];
-          if (tid == 0) hd[HD_DTOT] = expf(suf + sLa[0]);
-        }
-        __syncthreads();
-        for (int i = tid; i < m * P; i += blockDim.x) {
-          const int e = i / P, p = i - e * P;
-          const float xv = e < m - 1 ? bf2f(a.ring_x[(rh + (c - 1 - nv0 + e)) * P + p]) : sX[j * P + p];
-          sU[i] = sW[e] * xv;
-        }
-        __syncthreads();
-        for (int r = wave; r < RG; r += nw) {
-          const size_t row = ((size_t)slot * H + h) * P + r * 8 + rr;
-          UnitRaw<K, COLD> d;
-          unit_load<K, COLD>(a, row, q, d);
-          unit_compute<K, COLD, true>(a, row, bi, h, j, r * 8 + rr, q, d, Bh, Ch, Cc, sX, sHd, sU, sBc, m);
-        }
-      } else {
-        for (int r = wave; r < RG; r += nw) {
-          const size_t row = ((size_t)slot * H + h) * P + r * 8 + rr;
-          UnitRaw<K, COLD> d;
-          unit_load<K, COLD>(a, row, q, d);
-          unit_compute<K, COLD, false>(a, row, bi, h, j, r * 8 + rr, q, d, Bh, Ch, Cc, sX, sHd, sU, sBc, 0);
-        }
-      }
-    }
-  }
-
-  // 4. ring append (non-flush tokens) and bookkeeping
-  if constexpr (TIERED) {
-    const int c = a.c;
-    for (int j = 0; j < hpw; ++j) {
-      const float* hd = sHd + j * HD_STRIDE;
-      if (hd[HD_FLUSH] != 0.f) continue;
-      const int pos = __float_as_int(hd[HD_T]) % c;
-      const size_t rh = ((size_t)slot * H + h0 + j) * c + pos;
-      const size_t xo = ((size_t)bi * H + h0 + j) * P;
-      for (int p = tid; p < P; p += blockDim.x) a.ring_x[rh * P + p] = a.x[xo + p];
-      if (tid == 0) a.ring_dt[rh] = hd[HD_DT];
-    }
-    if (hb == 0 && sHd[HD_FLUSH] == 0.f) {
-      const int pos = __float_as_int(sHd[HD_T]) % c;
-      const size_t rb = (((size_t)slot * a.G + g) * c + pos) * NC;
-      for (int n = tid; n < NC; n += blockDim.x) a.ring_b[rb + n] = sB[K + n];
-    }
-    if (tid < hpw) {
-      const float* hd = sHd + tid * HD_STRIDE;
-      const size_t o = (size_t)slot * H + h0 + tid;
-      const int tt = __float_as_int(hd[HD_T]);
-      a.t[o] = tt + 1;
+      const int j = u / RG;
+      const int p = (u - j * RG) * 8 + rr;
+      const size_t row = ((size_t)slot * H + h0 + j) * P + p;
+      const size_t yrow = ((size_t)bi * H + h0 + j) * P + p;
+      const float* hd = hdb + j * HD_STRIDE;
       if (hd[HD_FLUSH] != 0.f) {
-        a.nv[o] = 0;
-        a.glog[o] = 0.f;
+        unit_compute<K, COLD, true>(a, row, yrow, p, q, dcur, nullptr, hd, Bh, Ch, Cc, sU + (size_t)j * m * P, sBc,
+                                    m);
       } else {
-        a.nv[o] = __float_as_int(hd[HD_NV]) + 1;
-        a.glog[o] = a.glog[o] + hd[HD_A];
+        uint16_t* rx = a.ring_x + (((size_t)slot * H + h0 + j) * c + (int)hd[HD_POS]) * P;
+        unit_compute<K, COLD, false>(a, row, yrow, p, q, dcur, rx, hd, Bh, Ch, Cc, nullptr, nullptr, 0);
       }
+      dcur = dnext;
     }
   }
 }
 
-// ---------------------------------------------------------------------------
 // join: full state -> tiers; one workgroup per (request, head)
 __global__ void join_kernel(StepArgs a, const float* __restrict__ S, const int32_t* __restrict__ phase, int K,
                             int kind) {
@@ -674,24 +728,32 @@ __global__ void rotate_kernel(const uint16_t* __restrict__ in, const float* __re
   }
 }
 
+
 // ---------------------------------------------------------------------------
 // host side
 int g_hpw_override = 0, g_waves_override = 0;
+constexpr size_t kMaxLds = 64 * 1024;
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 int check_params(const nssm_layer_params* prm) {
   if (!prm || !prm->dt_bias || !prm->A || !prm->D) return NSSM_E_NULL;
-  if (prm->N != kN || prm->H <= 0 || prm->G <= 0 || prm->H % prm->G) return NSSM_E_DIMS;
+  if (prm->N != kN || prm->H <= 0 || prm->G <= 0 || prm->H % prm->G || prm->H / prm->G > 64) return NSSM_E_DIMS;
   if (prm->P <= 0 || prm->P % 16 || prm->P > 256) return NSSM_E_DIMS;
   if (prm->R && !aligned16(prm->R)) return NSSM_E_ALIGN;
   return NSSM_OK;
 }
 
-int check_inputs(const nssm_layer_params* prm, const nssm_step_inputs* in, const float* y) {
+int check_inputs(const nssm_step_inputs* in, const float* y) {
   if (!in || !in->x || !in->B || !in->C || !in->dt || !y) return NSSM_E_NULL;
   if (in->b < 0) return NSSM_E_DIMS;
-  (void)prm;
+  return NSSM_OK;
+}
+
+int check_ws(const nssm_layer_params* prm, int b, int c, const void* ws, int64_t ws_bytes) {
+  if (!ws) return NSSM_E_WORKSPACE;
+  if (!aligned16(ws)) return NSSM_E_ALIGN;
+  if (ws_bytes < (int64_t)(ws_floats(b, prm->H, prm->G, c) * sizeof(float))) return NSSM_E_WORKSPACE;
   return NSSM_OK;
 }
 
@@ -702,53 +764,36 @@ int divisor_at_most(int n, int cap) {
   return 1;
 }
 
+size_t stream_lds_bytes(int hpw, int P, int c, int K) {
+  const int NC = kN - K;
+  return NC > 0 ? ((size_t)c * NC + (size_t)hpw * c * P) * sizeof(float) : 0;
+}
+
 struct Launch {
   int hpw, waves;
 };
 
-int pick_launch(int b, int H, int G, int P, Launch* out) {
-  const int HG = H / G;
-  const int RG = P / 8;
-  int waves = g_waves_override > 0 ? g_waves_override : divisor_at_most(RG, 5);
-  if (waves > kMaxWaves) return NSSM_E_TUNING;
-  int hpw;
+int pick_launch(int H, int G, int P, int K, int c, Launch* out) {
+  const int HG = H / G, RG = P / 8;
+  int hpw = 1;
   if (g_hpw_override > 0) {
     if (HG % g_hpw_override) return NSSM_E_TUNING;
     hpw = g_hpw_override;
-  } else {
-    // the largest head block that still leaves >= 2048 workgroups (8 per CU)
-    hpw = 1;
-    for (int d = HG; d >= 1; --d)
-      if (HG % d == 0 && (long)b * G * (HG / d) >= 2048) {
-        hpw = d;
-        break;
-      }
   }
+  while (hpw > 1 && stream_lds_bytes(hpw, P, c, K) > kMaxLds) hpw = divisor_at_most(HG, hpw - 1);
+  if (stream_lds_bytes(hpw, P, c, K) > kMaxLds) return NSSM_E_DIMS;
+  // measured on MI355X at the 9B shape (P = 80): the untiered stream runs best
+  // with two units per wave (5 waves per head), the tiered one with 4 waves
+  const int waves = g_waves_override > 0 ? g_waves_override
+                    : K < kN             ? (hpw * RG < 4 ? hpw * RG : 4)
+                                         : divisor_at_most(hpw * RG, 5);
+  if (waves > kMaxWaves) return NSSM_E_TUNING;
   out->hpw = hpw;
   out->waves = waves;
   return NSSM_OK;
 }
 
-size_t step_lds_bytes(int hpw, int P, int c, int K) {
-  const int NC = kN - K;
-  size_t fl = 4 * kN + (size_t)hpw * P + (size_t)hpw * HD_STRIDE;
-  if (NC > 0) fl += (size_t)c * NC + (size_t)c * P + 3 * (size_t)c;
-  return fl * sizeof(float);
-}
-
-constexpr size_t kMaxLds = 64 * 1024;
-
-template <int K, int COLD>
-int launch_step(const StepArgs& a, int waves, hipStream_t st) {
-  const size_t lds = step_lds_bytes(a.hpw, a.P, a.c, K);
-  if (lds > kMaxLds) return NSSM_E_DIMS;
-  const unsigned grid = (unsigned)a.b * a.G * a.nhb;
-  if (grid == 0) return NSSM_OK;
-  hipLaunchKernelGGL((step_kernel<K, COLD>), dim3(grid), dim3(waves * 64), lds, st, a);
-  return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
-}
-
-void fill_common(StepArgs& a, const nssm_layer_params* prm, const nssm_step_inputs* in, float* y) {
+void fill_common(StepArgs& a, const nssm_layer_params* prm, const nssm_step_inputs* in, float* y, void* ws) {
   a.x = in->x;
   a.Bm = in->B;
   a.Cm = in->C;
@@ -759,6 +804,7 @@ void fill_common(StepArgs& a, const nssm_layer_params* prm, const nssm_step_inpu
   a.D = prm->D;
   a.R = prm->R;
   a.y = y;
+  a.ws = static_cast<float*>(ws);
   a.b = in->b;
   a.H = prm->H;
   a.P = prm->P;
@@ -767,7 +813,7 @@ void fill_common(StepArgs& a, const nssm_layer_params* prm, const nssm_step_inpu
   a.dt_min = prm->dt_min;
 }
 
-int check_tier(const nssm_layer_params* prm, const nssm_tier* tr, bool need_ring) {
+int check_tier(const nssm_tier* tr, bool need_ring) {
   if (!tr || !tr->hot || !tr->cold || !tr->t || !tr->nv || !tr->glog) return NSSM_E_NULL;
   if (need_ring && (!tr->ring_x || !tr->ring_dt || !tr->ring_b)) return NSSM_E_NULL;
   if (tr->cold_kind < NSSM_COLD_FP32 || tr->cold_kind > NSSM_COLD_FP8) return NSSM_E_KIND;
@@ -776,7 +822,6 @@ int check_tier(const nssm_layer_params* prm, const nssm_tier* tr, bool need_ring
   if (tr->slots <= 0 || tr->c < 1 || tr->c > kMaxC) return NSSM_E_DIMS;
   if (tr->k_hot != 32 && tr->k_hot != 64 && tr->k_hot != 96) return NSSM_E_DIMS;
   if (!aligned16(tr->hot) || !aligned16(tr->cold) || (tr->master && !aligned16(tr->master))) return NSSM_E_ALIGN;
-  (void)prm;
   return NSSM_OK;
 }
 
@@ -793,14 +838,25 @@ void fill_tier(StepArgs& a, const nssm_tier* tr) {
   a.glog = tr->glog;
   a.slots = tr->slots;
   a.c = tr->c;
+  a.K = tr->k_hot;
+}
+
+template <int K, int COLD>
+int launch_pair(const StepArgs& a, int waves, hipStream_t st) {
+  constexpr bool TIERED = K < kN;
+  if (a.b == 0) return NSSM_OK;
+  hipLaunchKernelGGL((prep_kernel<TIERED>), dim3((unsigned)a.b * a.G), dim3(kPrepThreads), 0, st, a);
+  hipLaunchKernelGGL((stream_kernel<K, COLD>), dim3((unsigned)a.b * a.nhb), dim3(waves * 64),
+                     stream_lds_bytes(a.hpw, a.P, a.c, K), st, a);
+  return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
 }
 
 template <int K>
 int dispatch_kind(const StepArgs& a, int kind, int waves, hipStream_t st) {
   switch (kind) {
-    case NSSM_COLD_FP32: return launch_step<K, NSSM_COLD_FP32>(a, waves, st);
-    case NSSM_COLD_BF16: return launch_step<K, NSSM_COLD_BF16>(a, waves, st);
-    case NSSM_COLD_FP8: return launch_step<K, NSSM_COLD_FP8>(a, waves, st);
+    case NSSM_COLD_FP32: return launch_pair<K, NSSM_COLD_FP32>(a, waves, st);
+    case NSSM_COLD_BF16: return launch_pair<K, NSSM_COLD_BF16>(a, waves, st);
+    case NSSM_COLD_FP8: return launch_pair<K, NSSM_COLD_FP8>(a, waves, st);
   }
   return NSSM_E_KIND;
 }
@@ -817,12 +873,18 @@ const char* nssm_strerror(int code) {
     case NSSM_OK: return "ok";
     case NSSM_E_NULL: return "a required pointer is NULL";
     case NSSM_E_DIMS: return "sizes out of the supported range";
-    case NSSM_E_ALIGN: return "a state or parameter pointer is not 16-byte aligned";
+    case NSSM_E_ALIGN: return "a state, parameter or workspace pointer is not 16-byte aligned";
     case NSSM_E_KIND: return "unknown cold storage kind";
     case NSSM_E_LAUNCH: return "HIP kernel launch failed";
     case NSSM_E_TUNING: return "launch override does not fit the dimensions";
+    case NSSM_E_WORKSPACE: return "workspace missing or smaller than nssm_step_workspace_bytes()";
   }
   return "unknown nssm error";
+}
+
+int64_t nssm_step_workspace_bytes(int32_t b, int32_t H, int32_t G, int32_t N, int32_t c) {
+  if (b < 0 || H <= 0 || G <= 0 || H % G || N != kN || c < 0 || c > kMaxC) return NSSM_E_DIMS;
+  return (int64_t)(ws_floats(b, H, G, c) * sizeof(float));
 }
 
 int nssm_tier_sizes(int32_t slots, int32_t H, int32_t P, int32_t N, int32_t G, int32_t k_hot, int32_t c,
@@ -855,39 +917,42 @@ int nssm_set_launch(int32_t heads_per_wg, int32_t waves_per_wg) {
 }
 
 int nssm_fresh_step(const nssm_layer_params* prm, float* state, int32_t slots, const nssm_step_inputs* in,
-                    float* y, void* stream) {
+                    float* y, void* workspace, int64_t workspace_bytes, void* stream) {
   int rc = check_params(prm);
   if (rc) return rc;
-  if ((rc = check_inputs(prm, in, y))) return rc;
+  if ((rc = check_inputs(in, y))) return rc;
   if (!state) return NSSM_E_NULL;
   if (!aligned16(state)) return NSSM_E_ALIGN;
   if (slots <= 0 || (!in->slot_ids && in->b > slots)) return NSSM_E_DIMS;
+  if ((rc = check_ws(prm, in->b, 0, workspace, workspace_bytes))) return rc;
   StepArgs a = {};
-  fill_common(a, prm, in, y);
+  fill_common(a, prm, in, y, workspace);
   a.hot = state;
   a.slots = slots;
-  a.c = 1;
+  a.c = 0;
+  a.K = kN;
   Launch L;
-  if ((rc = pick_launch(in->b, prm->H, prm->G, prm->P, &L))) return rc;
+  if ((rc = pick_launch(prm->H, prm->G, prm->P, kN, 0, &L))) return rc;
   a.hpw = L.hpw;
-  a.nhb = a.HG / L.hpw;
-  return launch_step<kN, NSSM_COLD_FP32>(a, L.waves, (hipStream_t)stream);
+  a.nhb = prm->H / L.hpw;
+  return launch_pair<kN, NSSM_COLD_FP32>(a, L.waves, (hipStream_t)stream);
 }
 
 int nssm_v4_step(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step_inputs* in, float* y,
-                 void* stream) {
+                 void* workspace, int64_t workspace_bytes, void* stream) {
   int rc = check_params(prm);
   if (rc) return rc;
-  if ((rc = check_inputs(prm, in, y))) return rc;
-  if ((rc = check_tier(prm, tier, true))) return rc;
+  if ((rc = check_inputs(in, y))) return rc;
+  if ((rc = check_tier(tier, true))) return rc;
   if (!in->slot_ids && in->b > tier->slots) return NSSM_E_DIMS;
+  if ((rc = check_ws(prm, in->b, tier->c, workspace, workspace_bytes))) return rc;
   StepArgs a = {};
-  fill_common(a, prm, in, y);
+  fill_common(a, prm, in, y, workspace);
   fill_tier(a, tier);
   Launch L;
-  if ((rc = pick_launch(in->b, prm->H, prm->G, prm->P, &L))) return rc;
+  if ((rc = pick_launch(prm->H, prm->G, prm->P, tier->k_hot, tier->c, &L))) return rc;
   a.hpw = L.hpw;
-  a.nhb = a.HG / L.hpw;
+  a.nhb = prm->H / L.hpw;
   hipStream_t st = (hipStream_t)stream;
   switch (tier->k_hot) {
     case 32: return dispatch_kind<32>(a, tier->cold_kind, L.waves, st);
@@ -901,7 +966,7 @@ int nssm_v4_join(const nssm_layer_params* prm, const nssm_tier* tier, const floa
                  const int32_t* slot_ids, const int32_t* phase, void* stream) {
   int rc = check_params(prm);
   if (rc) return rc;
-  if ((rc = check_tier(prm, tier, false))) return rc;
+  if ((rc = check_tier(tier, false))) return rc;
   if (!state) return NSSM_E_NULL;
   if (b < 0 || (!slot_ids && b > tier->slots)) return NSSM_E_DIMS;
   if (b == 0) return NSSM_OK;
@@ -921,7 +986,7 @@ int nssm_v4_materialize(const nssm_layer_params* prm, const nssm_tier* tier, flo
                         const int32_t* slot_ids, void* stream) {
   int rc = check_params(prm);
   if (rc) return rc;
-  if ((rc = check_tier(prm, tier, true))) return rc;
+  if ((rc = check_tier(tier, true))) return rc;
   if (!state_out) return NSSM_E_NULL;
   if (b < 0 || (!slot_ids && b > tier->slots)) return NSSM_E_DIMS;
   if (b == 0) return NSSM_OK;

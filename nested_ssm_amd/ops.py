@@ -20,6 +20,24 @@ def _stream() -> int:
     return torch.cuda.current_stream().cuda_stream
 
 
+_WORKSPACES = {}
+
+
+def step_workspace(b: int, H: int, G: int, c: int, device=None) -> torch.Tensor:
+    """Workspace for one step call on the current stream of `device` (cached per
+    device and stream, grown on demand; calls on one stream run in order)."""
+    need = lib().nssm_step_workspace_bytes(b, H, G, N_STATE, c)
+    if need < 0:
+        check(int(need), "nssm_step_workspace_bytes")
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(max(int(need), 256), device=dev, dtype=torch.uint8)
+        _WORKSPACES[key] = ws
+    return ws
+
+
 def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
@@ -96,8 +114,9 @@ def fresh_step(prm: LayerParams, state: torch.Tensor, x, B, C, dt, y: Optional[t
         y = torch.empty(b, prm.H, prm.P, device=x.device, dtype=torch.float32)
     _need(y, "y", torch.float32, (b, prm.H, prm.P))
     pc, ic = prm.c_struct(), _inputs(prm, x, B, C, dt, slot_ids)
+    ws = step_workspace(b, prm.H, prm.G, 0, x.device)
     check(lib().nssm_fresh_step(ctypes.byref(pc), state.data_ptr(), slots, ctypes.byref(ic), y.data_ptr(),
-                                _stream()), "nssm_fresh_step")
+                                ws.data_ptr(), ws.numel(), _stream()), "nssm_fresh_step")
     return y
 
 
@@ -163,8 +182,9 @@ class V4Tier:
             y = torch.empty(b, prm.H, prm.P, device=x.device, dtype=torch.float32)
         _need(y, "y", torch.float32, (b, prm.H, prm.P))
         pc, ic, tc = prm.c_struct(), _inputs(prm, x, B, C, dt, slot_ids), self.c_struct()
-        check(lib().nssm_v4_step(ctypes.byref(pc), ctypes.byref(tc), ctypes.byref(ic), y.data_ptr(), _stream()),
-              "nssm_v4_step")
+        ws = step_workspace(b, prm.H, prm.G, self.c, x.device)
+        check(lib().nssm_v4_step(ctypes.byref(pc), ctypes.byref(tc), ctypes.byref(ic), y.data_ptr(),
+                                 ws.data_ptr(), ws.numel(), _stream()), "nssm_v4_step")
         return y
 
     def materialize(self, prm: LayerParams, slot_ids: Optional[torch.Tensor] = None,

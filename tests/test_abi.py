@@ -42,7 +42,8 @@ def test_abi_version_and_codes_match_header():
     assert int(d["NSSM_COLD_FP32"]) == _lib.COLD_FP32
     assert int(d["NSSM_COLD_BF16"]) == _lib.COLD_BF16
     assert int(d["NSSM_COLD_FP8"]) == _lib.COLD_FP8
-    for code in ("NSSM_E_NULL", "NSSM_E_DIMS", "NSSM_E_ALIGN", "NSSM_E_KIND", "NSSM_E_LAUNCH", "NSSM_E_TUNING"):
+    for code in ("NSSM_E_NULL", "NSSM_E_DIMS", "NSSM_E_ALIGN", "NSSM_E_KIND", "NSSM_E_LAUNCH", "NSSM_E_TUNING",
+                 "NSSM_E_WORKSPACE"):
         msg = L.nssm_strerror(int(d[code])).decode()
         assert msg and msg != "unknown nssm error"
     assert L.nssm_strerror(0).decode() == "ok"
@@ -117,23 +118,31 @@ def test_entry_points_validate_before_launching():
     fake = 4096
     prm = _lib.LayerParams(8, 80, 128, 1, fake, fake, fake, None, 0.0)
     inp = _lib.StepInputs(4, fake, fake, fake, fake, None)
-    assert L.nssm_fresh_step(None, fake, 4, ctypes.byref(inp), fake, None) == -1
+    assert L.nssm_fresh_step(None, fake, 4, ctypes.byref(inp), fake, fake, 1 << 30, None) == -1
     bad = _lib.LayerParams(8, 80, 64, 1, fake, fake, fake, None, 0.0)
-    assert L.nssm_fresh_step(ctypes.byref(bad), fake, 4, ctypes.byref(inp), fake, None) == -2
+    assert L.nssm_fresh_step(ctypes.byref(bad), fake, 4, ctypes.byref(inp), fake, fake, 1 << 30, None) == -2
     bad = _lib.LayerParams(8, 72, 128, 1, fake, fake, fake, None, 0.0)  # P not a multiple of 16
-    assert L.nssm_fresh_step(ctypes.byref(bad), fake, 4, ctypes.byref(inp), fake, None) == -2
+    assert L.nssm_fresh_step(ctypes.byref(bad), fake, 4, ctypes.byref(inp), fake, fake, 1 << 30, None) == -2
     bad = _lib.LayerParams(8, 80, 128, 3, fake, fake, fake, None, 0.0)  # H % G
-    assert L.nssm_fresh_step(ctypes.byref(bad), fake, 4, ctypes.byref(inp), fake, None) == -2
-    assert L.nssm_fresh_step(ctypes.byref(prm), fake + 4, 4, ctypes.byref(inp), fake, None) == -3
-    assert L.nssm_fresh_step(ctypes.byref(prm), fake, 2, ctypes.byref(inp), fake, None) == -2  # b > slots
+    assert L.nssm_fresh_step(ctypes.byref(bad), fake, 4, ctypes.byref(inp), fake, fake, 1 << 30, None) == -2
+    assert L.nssm_fresh_step(ctypes.byref(prm), fake + 4, 4, ctypes.byref(inp), fake, fake, 1 << 30, None) == -3
+    assert L.nssm_fresh_step(ctypes.byref(prm), fake, 2, ctypes.byref(inp), fake, fake, 1 << 30, None) == -2  # b > slots
     tier = _lib.Tier(4, 32, 4, 9, *([fake] * 10))
-    assert L.nssm_v4_step(ctypes.byref(prm), ctypes.byref(tier), ctypes.byref(inp), fake, None) == -4
+    assert L.nssm_v4_step(ctypes.byref(prm), ctypes.byref(tier), ctypes.byref(inp), fake, fake, 1 << 30, None) == -4
     tier = _lib.Tier(4, 48, 4, 0, *([fake] * 10))  # k_hot not a multiple of 32
-    assert L.nssm_v4_step(ctypes.byref(prm), ctypes.byref(tier), ctypes.byref(inp), fake, None) == -2
+    assert L.nssm_v4_step(ctypes.byref(prm), ctypes.byref(tier), ctypes.byref(inp), fake, fake, 1 << 30, None) == -2
     tier = _lib.Tier(4, 32, 0, 0, *([fake] * 10))  # c = 0
-    assert L.nssm_v4_step(ctypes.byref(prm), ctypes.byref(tier), ctypes.byref(inp), fake, None) == -2
+    assert L.nssm_v4_step(ctypes.byref(prm), ctypes.byref(tier), ctypes.byref(inp), fake, fake, 1 << 30, None) == -2
     tier = _lib.Tier(4, 32, 4, 2, *([fake] * 2 + [None] + [fake] * 7))  # fp8 without a scale buffer
-    assert L.nssm_v4_step(ctypes.byref(prm), ctypes.byref(tier), ctypes.byref(inp), fake, None) == -1
+    assert L.nssm_v4_step(ctypes.byref(prm), ctypes.byref(tier), ctypes.byref(inp), fake, fake, 1 << 30, None) == -1
+    # workspace: NULL, too small, misaligned
+    need = L.nssm_step_workspace_bytes(4, 8, 1, 128, 0)
+    assert need == 4 * (2 * 128 + 12 * 8) * 4
+    assert L.nssm_step_workspace_bytes(4, 8, 1, 128, 4) == need + 4 * 8 * 4 * 4
+    assert L.nssm_step_workspace_bytes(4, 8, 3, 128, 4) == -2
+    assert L.nssm_fresh_step(ctypes.byref(prm), fake, 4, ctypes.byref(inp), fake, None, need, None) == -7
+    assert L.nssm_fresh_step(ctypes.byref(prm), fake, 4, ctypes.byref(inp), fake, fake, need - 4, None) == -7
+    assert L.nssm_fresh_step(ctypes.byref(prm), fake, 4, ctypes.byref(inp), fake, fake + 8, need, None) == -3
     assert L.nssm_set_launch(0, 9) == -6
     assert L.nssm_set_launch(0, 0) == 0
 
