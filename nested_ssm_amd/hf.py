@@ -1,0 +1,232 @@
+"""Transformers NemotronH integration of the MI355X decode-step kernels.
+
+Shared engine of the two drop-in modules v4_native_decode and v4_fused_decode.
+A patched NemotronHMamba2Mixer runs prefill through the stock transformers
+forward, then captures the state into a V4Tier (join); every single-token
+decode call then runs
+
+    prologue  in_proj, causal conv1d update + SiLU      (stock torch ops)
+    state op  nssm_v4_step / nssm_fresh_step            (HIP, libnssm_hip.so)
+    epilogue  gated RMSNorm, out_proj                   (stock torch ops)
+
+Rotation: the installed transformers (5.15) mixer never calls `self.act`, so a
+rotation wrapper on `act` (ActRotMask, scale/nemotron_retrofit.py:15-56) would
+not rotate B and C in prefill. Because the per-head decay is a scalar, the
+model is invariant under an orthogonal rotation of the state basis
+(S' = S R^T, y' = y): prefill runs unrotated and the captured state is rotated
+once, S' = S R^T, before the tiers are filled; decode then rotates B and C
+inside the kernels. Before any multi-token call that continues a decoded
+sequence, the exact current state is rebuilt from the tiers (materialize) and
+rotated back, so the stock forward sees the state it expects.
+"""
+import torch
+from torch import nn
+
+from . import ops
+from .ops import N_STATE, LayerParams, V4Tier
+
+MIXER = "NemotronHMamba2Mixer"
+
+
+def _modeling():
+    from transformers.models.nemotron_h import modeling_nemotron_h as M
+
+    return M
+
+
+# ---------------------------------------------------------------------------
+class ActRotMask(nn.Module):
+    """Container for the per-group rotation R of a mixer, identity-initialised
+    (scale/nemotron_retrofit.py:15-56): `m.act = ActRotMask(m.act, inter,
+    ngroups, dstate)` then `m.act.R.data.copy_(R_i)`. forward() keeps the
+    reference's training-path semantics (activation, then rotation and width
+    mask of the B and C slices); the decode kernels read `R` directly."""
+
+    def __init__(self, act, inter, ngroups, dstate):
+        super().__init__()
+        self.act = act
+        self.inter, self.ng, self.ds = inter, ngroups, dstate
+        self.conv_dim = inter + 2 * ngroups * dstate
+        self.R = nn.Parameter(torch.eye(dstate).repeat(ngroups, 1, 1))
+        self.width = dstate
+
+    def _rot(self, x):  # (B, T, G*N) -> (B, T, G, N) rotated, einsum('btgn,gmn->btgm')
+        b, t, _ = x.shape
+        return torch.einsum("btgn,gmn->btgm", x.view(b, t, self.ng, self.ds), self.R.to(x.dtype))
+
+    def _mask(self, x):
+        b, t = x.shape[:2]
+        if self.width < self.ds:
+            x = torch.cat([x[..., :self.width], torch.zeros_like(x[..., self.width:])], -1)
+        return x.reshape(b, t, self.ng * self.ds)
+
+    def rotmask(self, x):
+        return self._mask(self._rot(x))
+
+    def forward(self, x):
+        x = self.act(x)
+        if x.dim() == 3 and x.shape[-1] == self.conv_dim:
+            h, B, C = torch.split(x, [self.inter, self.ng * self.ds, self.ng * self.ds], dim=-1)
+            x = torch.cat([h, self._mask(self._rot(B)), self._mask(self._rot(C))], dim=-1)
+        return x
+
+
+def mixer_rotation(m):
+    """R [G, N, N] attached to a mixer by any of the reference's conventions:
+    ActRotMask (m.act.R), the fused install (m._v4R) or the vLLM port (m.v4R)."""
+    for R in (getattr(m.act, "R", None), getattr(m, "_v4R", None), getattr(m, "v4R", None)):
+        if R is not None:
+            return R.detach()
+    return None
+
+
+def layer_params(m, dt_min: float) -> LayerParams:
+    dev = m.A_log.device
+    return LayerParams.from_mixer_values(m.dt_bias, m.A_log, m.D, mixer_rotation(m), P=m.head_dim,
+                                         G=m.n_groups, dt_min=dt_min, device=dev)
+
+
+def rotate_state(S: torch.Tensor, R: torch.Tensor, inverse: bool = False) -> torch.Tensor:
+    """S R^T per head (the head's group rotation); inverse: S R. fp32."""
+    H, G = S.shape[1], R.shape[0]
+    Rh = R.float().repeat_interleave(H // G, dim=0)  # [H, N, N]
+    if inverse:
+        return torch.einsum("bhpm,hmn->bhpn", S.float(), Rh.contiguous())
+    return torch.einsum("bhpn,hmn->bhpm", S.float(), Rh.contiguous())
+
+
+class V4State(dict):
+    """Per-mixer decode state (`m._v4state`). Keys: "tier" (V4Tier or None for
+    the untiered path), "params" (LayerParams), "pb", "c". Item "t" reads and
+    writes the decode phase kept on the device (callers reset it between
+    prompts, scale/probe_selfspec_policy.py:127-128)."""
+
+    def __getitem__(self, key):
+        if key == "t":
+            tier = dict.get(self, "tier")
+            return int(tier.t[0, 0].item()) if tier is not None else dict.get(self, "t_fresh", 0)
+        return dict.__getitem__(self, key)
+
+    def __setitem__(self, key, value):
+        if key == "t":
+            tier = dict.get(self, "tier")
+            if tier is not None:
+                tier.t.fill_(int(value))
+            else:
+                dict.__setitem__(self, "t_fresh", int(value))
+            return
+        dict.__setitem__(self, key, value)
+
+
+# ---------------------------------------------------------------------------
+def decode_inputs(m, hidden_states, cache_params, attention_mask):
+    """One decode token through in_proj and the causal conv1d update + SiLU
+    (transformers' own functions): gate [b,1,I] and x [b,H,P], B, C [b,G,N],
+    dt [b,H] in bf16, as the kernels take them."""
+    M = _modeling()
+    b = hidden_states.shape[0]
+    H, P, G, N = m.num_heads, m.head_dim, m.n_groups, m.ssm_state_size
+    hidden_states = M.apply_mask_to_padding_states(hidden_states, attention_mask)
+    proj = m.in_proj(hidden_states)
+    gate, hbc, dt = proj.split([m.intermediate_size, m.conv_dim, H], dim=-1)
+    conv_state = cache_params.layers[m.layer_idx].conv_states[0]
+    hbc = M.causal_conv1d_update(hbc.transpose(1, 2), conv_state, m.conv1d.weight.squeeze(1), m.conv1d.bias,
+                                 activation=m.activation).transpose(1, 2)
+    hbc = M.apply_mask_to_padding_states(hbc, attention_mask)
+    x, B, C = torch.split(hbc, [m.intermediate_size, G * N, G * N], dim=-1)
+    bf = torch.bfloat16
+    return (gate, x.reshape(b, H, P).to(bf).contiguous(), B.reshape(b, G, N).to(bf).contiguous(),
+            C.reshape(b, G, N).to(bf).contiguous(), dt.reshape(b, H).to(bf).contiguous())
+
+
+def decode_epilogue(m, y, gate, dtype):
+    """y [b,H,P] fp32 (D x included) -> gated RMSNorm -> out_proj."""
+    b = y.shape[0]
+    out = m.norm(y.to(dtype).reshape(b, 1, -1), gate)
+    return m.out_proj(out.to(dtype))
+
+
+def decode_step(m, hidden_states, cache_params, attention_mask):
+    """The tiered (or untiered, pb >= N) decode step of one mixer."""
+    st = m._v4state
+    gate, x, B, C, dt = decode_inputs(m, hidden_states, cache_params, attention_mask)
+    prm = st["params"]
+    tier = dict.get(st, "tier")
+    if tier is None:
+        S = cache_params.layers[m.layer_idx].recurrent_states[0]
+        y = ops.fresh_step(prm, S, x, B, C, dt)
+    else:
+        y = tier.step(prm, x, B, C, dt)
+    return decode_epilogue(m, y, gate, hidden_states.dtype)
+
+
+def _cold_kind(cfg) -> str:
+    if "cold" in cfg:
+        return cfg["cold"]
+    return "bf16" if cfg.get("cold_bf16") else "fp32"
+
+
+def capture(m, cache_params, dt_min: float):
+    """End of prefill: tiers from the cache's fp32 state (rotated into R's basis)."""
+    cfg = m.v4cfg
+    pb, c = int(cfg["pb"]), int(cfg["c"])
+    for key in ("corr", "coldoff", "qgate", "ktop"):
+        if cfg.get(key):
+            raise NotImplementedError(f"v4cfg[{key!r}] is not implemented by the MI355X kernels")
+    layer = cache_params.layers[m.layer_idx]
+    S = layer.recurrent_states[0]
+    prm = layer_params(m, dt_min)
+    Srot = rotate_state(S, prm.R) if prm.R is not None else S.float()
+    b = S.shape[0]
+    if pb >= m.ssm_state_size:
+        if prm.R is not None:
+            layer.recurrent_states[0].copy_(Srot)
+        m._v4state = V4State(tier=None, params=prm, pb=pb, c=c, rotated=prm.R is not None)
+        return
+    kind = _cold_kind(cfg)
+    if kind == "off":
+        raise NotImplementedError("cold='off' (hot-only readout) is not implemented by the MI355X kernels")
+    tier = V4Tier(b, m.num_heads, m.head_dim, m.n_groups, k_hot=pb, c=c, cold=kind, device=S.device)
+    tier.join(prm, Srot.contiguous())
+    m._v4state = V4State(tier=tier, params=prm, pb=pb, c=c, rotated=prm.R is not None)
+
+
+def restore_cache(m, cache_params):
+    """Exact current state back into the cache, in the unrotated basis, before a
+    stock multi-token forward continues a decoded sequence."""
+    st = m._v4state
+    layer = cache_params.layers[m.layer_idx]
+    prm = st["params"]
+    tier = dict.get(st, "tier")
+    S = tier.materialize(prm) if tier is not None else layer.recurrent_states[0].float()
+    if prm.R is not None:
+        S = rotate_state(S, prm.R, inverse=True)
+    layer.recurrent_states[0].copy_(S)
+    m._v4state = None
+
+
+def dispatch(m, hidden_states, cache_params, attention_mask, kw, orig_forward, dt_min, decode_fn):
+    """Body of a patched mixer forward: single-token decode through `decode_fn`
+    (the tiered step) once a tier exists; anything else through the stock
+    forward, after which the tier is (re)captured."""
+    seq_len = hidden_states.shape[1]
+    has_prev = cache_params is not None and cache_params.has_previous_state(m.layer_idx)
+    if has_prev and m._v4state is not None:
+        if seq_len == 1 and not cache_params.layers[m.layer_idx].record_past:
+            return decode_fn(m, hidden_states, cache_params, attention_mask)
+        restore_cache(m, cache_params)
+    out = orig_forward(m, hidden_states, cache_params=cache_params, attention_mask=attention_mask, **kw)
+    if cache_params is not None:
+        capture(m, cache_params, dt_min)
+    return out
+
+
+def mixers(model):
+    return [m for m in model.modules() if type(m).__name__ == MIXER]
+
+
+def check_mixer_shape(m):
+    if m.ssm_state_size != N_STATE:
+        raise ValueError(f"the MI355X kernels need d_state = {N_STATE} (mixer has {m.ssm_state_size})")
+    if m.head_dim % 16:
+        raise ValueError(f"the MI355X kernels need head_dim % 16 == 0 (mixer has {m.head_dim})")

@@ -1,0 +1,231 @@
+"""GPU: the transformers drop-in modules (v4_native_decode / v4_fused_decode)
+on a tiny random-init NemotronH (fp32 weights; the mixers hand bf16 x, B, C,
+dt to the kernels as the 9B model does).
+
+The adapters' state handling is checked against the oracle: every decode call
+records the kernel inputs and the kernel's y, the prefill state the tier was
+built from is recorded, and the oracle replays the same sequence (fp32 bar,
+rtol = atol = 1e-5)."""
+import pytest
+import torch
+
+import oracle
+from helpers import assert_close32
+
+pytestmark = pytest.mark.gpu
+
+N = 128
+
+
+def _tiny_model(seed=0, rotated=True):
+    from transformers import NemotronHConfig, NemotronHForCausalLM
+
+    from nested_ssm_amd import hf
+
+    torch.manual_seed(seed)
+    cfg = NemotronHConfig(vocab_size=96, hidden_size=128, layers_block_type=["mamba", "attention", "mamba"],
+                          num_attention_heads=4, num_key_value_heads=2, head_dim=32, intermediate_size=256,
+                          ssm_state_size=N, mamba_num_heads=8, mamba_head_dim=16, n_groups=2, conv_kernel=4,
+                          chunk_size=16, use_mamba_kernels=False, attn_implementation="eager")
+    model = NemotronHForCausalLM(cfg).to("cuda", torch.float32).eval()
+    gen = torch.Generator().manual_seed(seed + 1)
+    rgen = torch.Generator().manual_seed(seed + 2)  # R draws do not shift the other parameters
+    for m in hf.mixers(model):
+        with torch.no_grad():  # spread decays and skips so the test sees varied heads
+            m.A_log.copy_(torch.rand(m.num_heads, generator=gen) * 2.7)
+            m.dt_bias.copy_(torch.log(torch.expm1(0.001 + 0.099 * torch.rand(m.num_heads, generator=gen))))
+            m.D.copy_(torch.randn(m.num_heads, generator=gen))
+        if rotated:
+            m.act = hf.ActRotMask(m.act, m.intermediate_size, m.n_groups, m.ssm_state_size).cuda()
+            with torch.no_grad():
+                m.act.R.copy_(oracle.make_rotation(m.n_groups, N, rgen))
+    return model
+
+
+class Recorder:
+    """Wraps the adapter's capture / decode_inputs / decode_epilogue."""
+
+    def __init__(self, monkeypatch):
+        from nested_ssm_amd import hf
+
+        self.states, self.inputs, self.ys = {}, {}, {}
+        orig_capture, orig_inputs, orig_epi = hf.capture, hf.decode_inputs, hf.decode_epilogue
+
+        def capture(m, cache_params, dt_min):
+            self.states[m.layer_idx] = cache_params.layers[m.layer_idx].recurrent_states[0].detach().clone().cpu()
+            self.inputs[m.layer_idx], self.ys[m.layer_idx] = [], []
+            return orig_capture(m, cache_params, dt_min)
+
+        def decode_inputs(m, *a):
+            out = orig_inputs(m, *a)
+            self.inputs[m.layer_idx].append([t.detach().clone().cpu() for t in out[1:]])
+            return out
+
+        def decode_epilogue(m, y, gate, dtype):
+            self.ys[m.layer_idx].append(y.detach().clone().cpu())
+            return orig_epi(m, y, gate, dtype)
+
+        monkeypatch.setattr(hf, "capture", capture)
+        monkeypatch.setattr(hf, "decode_inputs", decode_inputs)
+        monkeypatch.setattr(hf, "decode_epilogue", decode_epilogue)
+
+
+def _oracle_params(m, dt_min):
+    from nested_ssm_amd import hf
+
+    R = hf.mixer_rotation(m)
+    return oracle.LayerParams(m.num_heads, m.head_dim, N, m.n_groups, m.dt_bias.detach().float().cpu(),
+                              -torch.exp(m.A_log.detach().float()).cpu(), m.D.detach().float().cpu(),
+                              None if R is None else R.float().cpu(), dt_min)
+
+
+def _rot(S, R, H):
+    Rh = R.double().repeat_interleave(H // R.shape[0], dim=0)
+    return torch.einsum("bhpn,hmn->bhpm", S.double(), Rh).float()
+
+
+def _replay_and_check(model, rec, pb, c, cold, dt_min_of):
+    from nested_ssm_amd import hf
+
+    for m in hf.mixers(model):
+        li = m.layer_idx
+        prm = _oracle_params(m, dt_min_of(m))
+        S0 = rec.states[li]
+        if prm.R is not None:
+            S0 = _rot(S0, prm.R, m.num_heads)
+        b = S0.shape[0]
+        k = min(pb, N)
+        ref = oracle.NativeV4(b, m.num_heads, m.head_dim, N, k, c, cold=cold)
+        ref.join(torch.arange(b), S0)
+        assert len(rec.inputs[li]) > 0
+        for step, ((x, B, C, dt), y) in enumerate(zip(rec.inputs[li], rec.ys[li])):
+            y_ref = ref.step(x, B, C, dt, prm)
+            if cold == "fp32":
+                assert_close32(y, y_ref, f"layer {li} step {step} (pb={pb}, c={c})")
+            else:
+                assert float((y - y_ref).norm() / y_ref.norm()) < 1e-4
+        yield m, ref
+
+
+def _prefill_decode(model, ids, n_decode):
+    out = model(ids, use_cache=True)
+    pkv = out.past_key_values
+    logits = [out.logits[:, -1].float()]
+    tok = out.logits[:, -1:].argmax(-1)
+    for _ in range(n_decode):
+        out = model(tok, past_key_values=pkv, use_cache=True)
+        logits.append(out.logits[:, -1].float())
+        tok = out.logits[:, -1:].argmax(-1)
+    return torch.stack(logits, 1), pkv
+
+
+@pytest.mark.parametrize("pb,c,cold_bf16", [(128, 16, 0), (32, 4, 0), (64, 3, 1)])
+def test_native_install_matches_oracle(monkeypatch, pb, c, cold_bf16):
+    from nested_ssm_amd import v4_native_decode as V
+
+    V.M.is_fast_path_available = False  # the reference's callers set it; it must stay assignable
+    model = _tiny_model(seed=3)
+    assert V.install(model, pb=pb, c=c, cold_bf16=cold_bf16) == 2
+    rec = Recorder(monkeypatch)
+    ids = torch.randint(0, 96, (3, 9), generator=torch.Generator().manual_seed(4)).cuda()
+    with torch.no_grad():
+        _prefill_decode(model, ids, n_decode=2 * c + 1 if c < 16 else 6)
+    cold = "bf16" if cold_bf16 and pb < N else "fp32"
+    dt_min_of = lambda m: float(m.time_step_limit[0])  # noqa: E731
+    for m, ref in _replay_and_check(model, rec, pb, c, cold, dt_min_of):
+        st = m._v4state
+        assert st["pb"] == pb and st["c"] == c
+        if pb < N:
+            assert st["t"] == int(ref.t[0])
+
+
+def test_fused_install_fp8_matches_oracle(monkeypatch):
+    from nested_ssm_amd import v4_fused_decode as F
+
+    model = _tiny_model(seed=5)
+    assert F.install(model, pb=32, c=4, cold="fp8") == 2
+    for m in model.modules():
+        if type(m).__name__ == "NemotronHMamba2Mixer":
+            assert m._v4R is not None and m._v4R.dtype == torch.float32
+    rec = Recorder(monkeypatch)
+    ids = torch.randint(0, 96, (2, 6), generator=torch.Generator().manual_seed(6)).cuda()
+    with torch.no_grad():
+        _prefill_decode(model, ids, n_decode=9)
+    from nested_ssm_amd import hf
+
+    for m in hf.mixers(model):
+        li = m.layer_idx
+        prm = _oracle_params(m, 0.0)
+        ref = oracle.NativeV4(2, m.num_heads, m.head_dim, N, 32, 4, cold="fp8")
+        ref.join(torch.arange(2), _rot(rec.states[li], prm.R, m.num_heads))
+        for (x, B, C, dt), y in zip(rec.inputs[li], rec.ys[li]):
+            y_ref = ref.step(x, B, C, dt, prm)
+            assert float((y - y_ref).norm() / y_ref.norm()) <= 2e-2
+
+
+def test_all_hot_install_is_rotation_invariant_and_tracks_stock():
+    """pb = N with a random orthogonal R gives the stock (unrotated) model's outputs:
+    exactly up to fp32 rounding against the same install with R = I, and within
+    the bf16 cast of the kernel inputs against the stock fp32 forward."""
+    from nested_ssm_amd import v4_native_decode as V
+
+    ids = torch.randint(0, 96, (2, 8), generator=torch.Generator().manual_seed(7)).cuda()
+    with torch.no_grad():
+        stock, _ = _prefill_decode(_tiny_model(seed=8, rotated=False), ids, 5)
+        m_id = _tiny_model(seed=8, rotated=False)
+        V.install(m_id, pb=128, c=16, cold_bf16=0)
+        l_id, _ = _prefill_decode(m_id, ids, 5)
+        m_rot = _tiny_model(seed=8, rotated=True)
+        V.install(m_rot, pb=128, c=16, cold_bf16=0)
+        l_rot, _ = _prefill_decode(m_rot, ids, 5)
+    scale = stock.abs().max()
+    assert float((l_rot - l_id).abs().max() / scale) < 1e-4
+    assert float((l_id - stock).abs().max() / scale) < 2e-2
+    assert torch.equal(l_id[:, 0], stock[:, 0])  # the prefill logits come from the stock forward
+
+
+def test_restore_after_decode_gives_exact_state(monkeypatch):
+    """A multi-token call after tiered decode tokens rebuilds the exact state
+    (rotated back to the stock basis) in the cache before the stock forward."""
+    from nested_ssm_amd import hf
+    from nested_ssm_amd import v4_native_decode as V
+
+    model = _tiny_model(seed=9)
+    V.install(model, pb=32, c=4, cold_bf16=0)
+    rec = Recorder(monkeypatch)
+    restored = {}
+    orig_restore = hf.restore_cache
+
+    def restore(m, cache_params):
+        orig_restore(m, cache_params)
+        restored[m.layer_idx] = cache_params.layers[m.layer_idx].recurrent_states[0].detach().clone().cpu()
+
+    monkeypatch.setattr(hf, "restore_cache", restore)
+    ids = torch.randint(0, 96, (2, 5), generator=torch.Generator().manual_seed(10)).cuda()
+    with torch.no_grad():
+        _, pkv = _prefill_decode(model, ids, n_decode=6)
+        rec_inputs = {k: list(v) for k, v in rec.inputs.items()}
+        rec_states = dict(rec.states)
+        model(ids[:, :2], past_key_values=pkv, use_cache=True)  # two tokens continue the sequence
+    for m in hf.mixers(model):
+        li = m.layer_idx
+        prm = _oracle_params(m, float(m.time_step_limit[0]))
+        ref = oracle.NativeV4(2, m.num_heads, m.head_dim, N, 32, 4)
+        ref.join(torch.arange(2), _rot(rec_states[li], prm.R, m.num_heads))
+        for x, B, C, dt in rec_inputs[li]:
+            ref.step(x, B, C, dt, prm)
+        Rh = prm.R.double().repeat_interleave(m.num_heads // m.n_groups, dim=0)
+        want = torch.einsum("bhpm,hmn->bhpn", ref.S.double(), Rh).float()  # back to the stock basis
+        assert_close32(restored[li], want, f"restored state layer {li}")
+
+
+def test_generate_runs_with_tiered_decode():
+    from nested_ssm_amd import v4_native_decode as V
+
+    model = _tiny_model(seed=11)
+    V.install(model, pb=32, c=4, cold_bf16=1)
+    ids = torch.randint(0, 96, (2, 6), generator=torch.Generator().manual_seed(12)).cuda()
+    with torch.no_grad():
+        g1 = model.generate(ids, max_new_tokens=9, do_sample=False)
+        g2 = model.generate(ids, max_new_tokens=9, do_sample=False)
+    assert g1.shape == (2, 15) and torch.equal(g1, g2)
