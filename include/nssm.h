@@ -56,6 +56,8 @@ extern "C" {
 #define NSSM_COLD_BF16 1 /* bf16 read copy (RNE of the master) + exact fp32 master */
 #define NSSM_COLD_FP8 2  /* e4m3fn read copy, fp32 scale per (slot,head,p) row
                             (amax/448 + 1e-12), + exact fp32 master */
+#define NSSM_COLD_NONE 3 /* hot tier only: the cold columns are dropped (never stored,
+                            read or flushed); cold, scale, master and the ring may be NULL */
 
 /* Per-layer constants. Mirrors the mixer attributes the reference reads:
  * dt_bias, A = -exp(A_log), D, time_step_min, and the ActRotMask R. */

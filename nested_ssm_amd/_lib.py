@@ -8,8 +8,8 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libnssm_hip.so")
 
-COLD_FP32, COLD_BF16, COLD_FP8 = 0, 1, 2
-COLD_KINDS = {"fp32": COLD_FP32, "bf16": COLD_BF16, "fp8": COLD_FP8}
+COLD_FP32, COLD_BF16, COLD_FP8, COLD_NONE = 0, 1, 2, 3
+COLD_KINDS = {"fp32": COLD_FP32, "bf16": COLD_BF16, "fp8": COLD_FP8, "off": COLD_NONE}
 
 TIER_FIELDS = ("hot", "cold", "scale", "master", "ring_x", "ring_dt", "ring_b", "t", "nv", "glog")
 

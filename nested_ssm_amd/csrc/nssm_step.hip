@@ -297,7 +297,7 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
 template <int K, int COLD>
 struct UnitRaw {
   static constexpr int HS = K / 32;
-  static constexpr int CS = (kN - K) / 32;
+  static constexpr int CS = COLD == NSSM_COLD_NONE ? 0 : (kN - K) / 32;
   static constexpr int CSR = CS > 0 ? CS : 1;
   f4 hv[HS];
   f4 cf[COLD == NSSM_COLD_FP32 ? CSR : 1];
@@ -310,7 +310,7 @@ struct UnitRaw {
 
 template <int K, int COLD>
 __device__ __forceinline__ void unit_load(const StepArgs& a, size_t row, size_t xrow, int q, UnitRaw<K, COLD>& d) {
-  constexpr int HS = K / 32, CS = (kN - K) / 32, NC = kN - K;
+  constexpr int HS = K / 32, CS = UnitRaw<K, COLD>::CS, NC = kN - K;
   const f4* hp = reinterpret_cast<const f4*>(a.hot + row * K) + q;
 #pragma unroll
   for (int s = 0; s < HS; ++s) d.hv[s] = ld_stream(hp + 8 * s);
@@ -406,7 +406,7 @@ __device__ __forceinline__ void unit_compute(const StepArgs& a, size_t row, size
                                              const float* sBc, int m) {
   constexpr int HS = K / 32;
   constexpr int NC = kN - K;
-  constexpr int CS = NC / 32;
+  constexpr int CS = UnitRaw<K, COLD>::CS;
   constexpr int CSR = UnitRaw<K, COLD>::CSR;
   const int P = a.P;
   const float xp = d.xp;
@@ -488,9 +488,9 @@ template <int K, int COLD>
 __global__ void __launch_bounds__(kMaxWaves * 64) stream_kernel(StepArgs a) {
   constexpr int HS = K / 32;
   constexpr int NC = kN - K;
-  constexpr int CS = NC / 32;
+  constexpr int CS = UnitRaw<K, COLD>::CS;
   constexpr int CSR = CS > 0 ? CS : 1;
-  constexpr bool TIERED = NC > 0;
+  constexpr bool TIERED = CS > 0;  // a cold tier with ring and flushes
   extern __shared__ float lds[];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
@@ -627,7 +627,7 @@ __global__ void join_kernel(StepArgs a, const float* __restrict__ S, const int32
     const float v = src[i];
     if (n < K) {
       a.hot[(row0 + p) * K + n] = v;
-    } else {
+    } else if (kind != NSSM_COLD_NONE) {
       float* dst = kind == NSSM_COLD_FP32 ? static_cast<float*>(a.cold) : a.master;
       dst[(row0 + p) * NC + (n - K)] = v;
       if (kind == NSSM_COLD_BF16) static_cast<uint16_t*>(a.cold)[(row0 + p) * NC + (n - K)] = nssm_f32_to_bf16(v);
@@ -764,28 +764,28 @@ int divisor_at_most(int n, int cap) {
   return 1;
 }
 
-size_t stream_lds_bytes(int hpw, int P, int c, int K) {
+size_t stream_lds_bytes(int hpw, int P, int c, int K, int kind = NSSM_COLD_FP32) {
   const int NC = kN - K;
-  return NC > 0 ? ((size_t)c * NC + (size_t)hpw * c * P) * sizeof(float) : 0;
+  return NC > 0 && kind != NSSM_COLD_NONE ? ((size_t)c * NC + (size_t)hpw * c * P) * sizeof(float) : 0;
 }
 
 struct Launch {
   int hpw, waves;
 };
 
-int pick_launch(int H, int G, int P, int K, int c, Launch* out) {
+int pick_launch(int H, int G, int P, int K, int c, Launch* out, int kind = NSSM_COLD_FP32) {
   const int HG = H / G, RG = P / 8;
   int hpw = 1;
   if (g_hpw_override > 0) {
     if (HG % g_hpw_override) return NSSM_E_TUNING;
     hpw = g_hpw_override;
   }
-  while (hpw > 1 && stream_lds_bytes(hpw, P, c, K) > kMaxLds) hpw = divisor_at_most(HG, hpw - 1);
-  if (stream_lds_bytes(hpw, P, c, K) > kMaxLds) return NSSM_E_DIMS;
+  while (hpw > 1 && stream_lds_bytes(hpw, P, c, K, kind) > kMaxLds) hpw = divisor_at_most(HG, hpw - 1);
+  if (stream_lds_bytes(hpw, P, c, K, kind) > kMaxLds) return NSSM_E_DIMS;
   // measured on MI355X at the 9B shape (P = 80): the untiered stream runs best
   // with two units per wave (5 waves per head), the tiered one with 4 waves
   const int waves = g_waves_override > 0 ? g_waves_override
-                    : K < kN             ? (hpw * RG < 4 ? hpw * RG : 4)
+                    : K < kN && kind != NSSM_COLD_NONE ? (hpw * RG < 4 ? hpw * RG : 4)
                                          : divisor_at_most(hpw * RG, 5);
   if (waves > kMaxWaves) return NSSM_E_TUNING;
   out->hpw = hpw;
@@ -814,14 +814,17 @@ void fill_common(StepArgs& a, const nssm_layer_params* prm, const nssm_step_inpu
 }
 
 int check_tier(const nssm_tier* tr, bool need_ring) {
-  if (!tr || !tr->hot || !tr->cold || !tr->t || !tr->nv || !tr->glog) return NSSM_E_NULL;
-  if (need_ring && (!tr->ring_x || !tr->ring_dt || !tr->ring_b)) return NSSM_E_NULL;
-  if (tr->cold_kind < NSSM_COLD_FP32 || tr->cold_kind > NSSM_COLD_FP8) return NSSM_E_KIND;
-  if (tr->cold_kind != NSSM_COLD_FP32 && !tr->master) return NSSM_E_NULL;
+  if (!tr) return NSSM_E_NULL;
+  if (tr->cold_kind < NSSM_COLD_FP32 || tr->cold_kind > NSSM_COLD_NONE) return NSSM_E_KIND;
+  const bool cold = tr->cold_kind != NSSM_COLD_NONE;
+  if (!tr->hot || !tr->t || !tr->nv || !tr->glog || (cold && !tr->cold)) return NSSM_E_NULL;
+  if (cold && need_ring && (!tr->ring_x || !tr->ring_dt || !tr->ring_b)) return NSSM_E_NULL;
+  if ((tr->cold_kind == NSSM_COLD_BF16 || tr->cold_kind == NSSM_COLD_FP8) && !tr->master) return NSSM_E_NULL;
   if (tr->cold_kind == NSSM_COLD_FP8 && !tr->scale) return NSSM_E_NULL;
   if (tr->slots <= 0 || tr->c < 1 || tr->c > kMaxC) return NSSM_E_DIMS;
   if (tr->k_hot != 32 && tr->k_hot != 64 && tr->k_hot != 96) return NSSM_E_DIMS;
-  if (!aligned16(tr->hot) || !aligned16(tr->cold) || (tr->master && !aligned16(tr->master))) return NSSM_E_ALIGN;
+  if (!aligned16(tr->hot) || (cold && !aligned16(tr->cold)) || (tr->master && !aligned16(tr->master)))
+    return NSSM_E_ALIGN;
   return NSSM_OK;
 }
 
@@ -843,11 +846,11 @@ void fill_tier(StepArgs& a, const nssm_tier* tr) {
 
 template <int K, int COLD>
 int launch_pair(const StepArgs& a, int waves, hipStream_t st) {
-  constexpr bool TIERED = K < kN;
+  constexpr bool TIERED = K < kN && COLD != NSSM_COLD_NONE;
   if (a.b == 0) return NSSM_OK;
   hipLaunchKernelGGL((prep_kernel<TIERED>), dim3((unsigned)a.b * a.G), dim3(kPrepThreads), 0, st, a);
   hipLaunchKernelGGL((stream_kernel<K, COLD>), dim3((unsigned)a.b * a.nhb), dim3(waves * 64),
-                     stream_lds_bytes(a.hpw, a.P, a.c, K), st, a);
+                     stream_lds_bytes(a.hpw, a.P, a.c, K, COLD), st, a);
   return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
 }
 
@@ -857,6 +860,7 @@ int dispatch_kind(const StepArgs& a, int kind, int waves, hipStream_t st) {
     case NSSM_COLD_FP32: return launch_pair<K, NSSM_COLD_FP32>(a, waves, st);
     case NSSM_COLD_BF16: return launch_pair<K, NSSM_COLD_BF16>(a, waves, st);
     case NSSM_COLD_FP8: return launch_pair<K, NSSM_COLD_FP8>(a, waves, st);
+    case NSSM_COLD_NONE: return launch_pair<K, NSSM_COLD_NONE>(a, waves, st);
   }
   return NSSM_E_KIND;
 }
@@ -892,17 +896,18 @@ int nssm_tier_sizes(int32_t slots, int32_t H, int32_t P, int32_t N, int32_t G, i
   if (!sz) return NSSM_E_NULL;
   if (slots <= 0 || H <= 0 || P <= 0 || N != kN || G <= 0 || k_hot <= 0 || k_hot >= N || c < 1 || c > kMaxC)
     return NSSM_E_DIMS;
-  if (cold_kind < NSSM_COLD_FP32 || cold_kind > NSSM_COLD_FP8) return NSSM_E_KIND;
+  if (cold_kind < NSSM_COLD_FP32 || cold_kind > NSSM_COLD_NONE) return NSSM_E_KIND;
   const int64_t rows = (int64_t)slots * H * P;
   const int64_t NC = N - k_hot;
-  const int64_t esz = cold_kind == NSSM_COLD_FP32 ? 4 : cold_kind == NSSM_COLD_BF16 ? 2 : 1;
+  const int64_t esz = cold_kind == NSSM_COLD_FP32 ? 4 : cold_kind == NSSM_COLD_BF16 ? 2 : cold_kind == NSSM_COLD_FP8 ? 1 : 0;
+  const int64_t ring = cold_kind == NSSM_COLD_NONE ? 0 : 1;
   sz[0] = rows * k_hot * 4;
   sz[1] = rows * NC * esz;
   sz[2] = cold_kind == NSSM_COLD_FP8 ? rows * 4 : 0;
-  sz[3] = cold_kind == NSSM_COLD_FP32 ? 0 : rows * NC * 4;
-  sz[4] = (int64_t)slots * H * c * P * 2;
-  sz[5] = (int64_t)slots * H * c * 4;
-  sz[6] = (int64_t)slots * G * c * NC * 4;
+  sz[3] = cold_kind == NSSM_COLD_BF16 || cold_kind == NSSM_COLD_FP8 ? rows * NC * 4 : 0;
+  sz[4] = ring * slots * H * c * P * 2;
+  sz[5] = ring * slots * H * c * 4;
+  sz[6] = ring * slots * G * c * NC * 4;
   sz[7] = (int64_t)slots * H * 4;
   sz[8] = (int64_t)slots * H * 4;
   sz[9] = (int64_t)slots * H * 4;
@@ -950,7 +955,7 @@ int nssm_v4_step(const nssm_layer_params* prm, const nssm_tier* tier, const nssm
   fill_common(a, prm, in, y, workspace);
   fill_tier(a, tier);
   Launch L;
-  if ((rc = pick_launch(prm->H, prm->G, prm->P, tier->k_hot, tier->c, &L))) return rc;
+  if ((rc = pick_launch(prm->H, prm->G, prm->P, tier->k_hot, tier->c, &L, tier->cold_kind))) return rc;
   a.hpw = L.hpw;
   a.nhb = prm->H / L.hpw;
   hipStream_t st = (hipStream_t)stream;
@@ -987,6 +992,7 @@ int nssm_v4_materialize(const nssm_layer_params* prm, const nssm_tier* tier, flo
   int rc = check_params(prm);
   if (rc) return rc;
   if ((rc = check_tier(tier, true))) return rc;
+  if (tier->cold_kind == NSSM_COLD_NONE) return NSSM_E_KIND;  // the cold columns were dropped
   if (!state_out) return NSSM_E_NULL;
   if (b < 0 || (!slot_ids && b > tier->slots)) return NSSM_E_DIMS;
   if (b == 0) return NSSM_OK;

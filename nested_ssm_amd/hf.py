@@ -184,8 +184,6 @@ def capture(m, cache_params, dt_min: float):
         m._v4state = V4State(tier=None, params=prm, pb=pb, c=c, rotated=prm.R is not None)
         return
     kind = _cold_kind(cfg)
-    if kind == "off":
-        raise NotImplementedError("cold='off' (hot-only readout) is not implemented by the MI355X kernels")
     tier = V4Tier(b, m.num_heads, m.head_dim, m.n_groups, k_hot=pb, c=c, cold=kind, device=S.device)
     tier.join(prm, Srot.contiguous())
     m._v4state = V4State(tier=tier, params=prm, pb=pb, c=c, rotated=prm.R is not None)
@@ -198,6 +196,9 @@ def restore_cache(m, cache_params):
     layer = cache_params.layers[m.layer_idx]
     prm = st["params"]
     tier = dict.get(st, "tier")
+    if tier is not None and tier.cold == "off":
+        raise NotImplementedError("cold='off' drops the cold columns: a multi-token call cannot continue "
+                                  "from a hot-only decoded sequence")
     S = tier.materialize(prm) if tier is not None else layer.recurrent_states[0].float()
     if prm.R is not None:
         S = rotate_state(S, prm.R, inverse=True)

@@ -134,16 +134,17 @@ class V4Tier:
         sizes = (ctypes.c_int64 * 10)()
         check(lib().nssm_tier_sizes(slots, H, P, N, G, k_hot, c, self.kind, sizes), "nssm_tier_sizes")
         NC = N - k_hot
-        cold_dt = {"fp32": torch.float32, "bf16": torch.bfloat16, "fp8": torch.uint8}[cold]
         dev = torch.device(device)
         e = lambda shape, dt: torch.empty(shape, device=dev, dtype=dt)  # noqa: E731
         self.hot = e((slots, H, P, k_hot), torch.float32)
-        self.cold_t = e((slots, H, P, NC), cold_dt)
+        tiered = cold != "off"  # "off": hot tier only, the cold columns are dropped
+        cold_dt = {"fp32": torch.float32, "bf16": torch.bfloat16, "fp8": torch.uint8, "off": None}[cold]
+        self.cold_t = e((slots, H, P, NC), cold_dt) if tiered else None
         self.scale = e((slots, H, P), torch.float32) if cold == "fp8" else None
-        self.master = e((slots, H, P, NC), torch.float32) if cold != "fp32" else None
-        self.ring_x = e((slots, H, c, P), torch.bfloat16)
-        self.ring_dt = e((slots, H, c), torch.float32)
-        self.ring_b = e((slots, G, c, NC), torch.float32)
+        self.master = e((slots, H, P, NC), torch.float32) if cold in ("bf16", "fp8") else None
+        self.ring_x = e((slots, H, c, P), torch.bfloat16) if tiered else None
+        self.ring_dt = e((slots, H, c), torch.float32) if tiered else None
+        self.ring_b = e((slots, G, c, NC), torch.float32) if tiered else None
         self.t = torch.zeros((slots, H), device=dev, dtype=torch.int32)
         self.nv = torch.zeros((slots, H), device=dev, dtype=torch.int32)
         self.glog = torch.zeros((slots, H), device=dev, dtype=torch.float32)

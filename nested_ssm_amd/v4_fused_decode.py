@@ -1,14 +1,14 @@
 """Drop-in for scale/v4_fused_decode.py on the MI355X kernels.
 
 Same module surface: `install(model, pb=32, c=16, cold="bf16") -> int`
-(scale/v4_fused_decode.py:163-175) with cold in {"bf16", "fp32", "fp8"}, the
+(scale/v4_fused_decode.py:163-175) with cold in {"bf16", "fp32", "fp8", "off"}, the
 rotation read from an ActRotMask-wrapped `m.act.R` into `m._v4R`, and the
 module-level `_v4_fused_decode(self, hidden_states, cache_params,
 attention_mask)` (scale/v4_fused_decode.py:28-95). Prefill runs the stock
 forward and the tier is captured at its end (scale/v4_fused_decode.py:109-160).
 No dt clamp, as the reference's fused kernel path. The reference keeps a bf16
 master for its bf16/fp8 cold snapshots; here the master is exact fp32.
-cold="off" raises NotImplementedError at capture.
+cold="off" keeps the hot tier only (the cold columns are dropped).
 """
 from transformers.models.nemotron_h import modeling_nemotron_h as M
 

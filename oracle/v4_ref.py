@@ -39,7 +39,7 @@ def make_rotation(G: int, N: int, gen: torch.Generator) -> torch.Tensor:
     W = torch.randn(G, N, N, generator=gen, dtype=torch.float64)
     Q, Rr = torch.linalg.qr(W)
     sgn = torch.sign(torch.diagonal(Rr, dim1=-2, dim2=-1))
-    return (Q * sgn[..., None, :]).to(torch.float32)
+    return (Q * sgn[..., None, :]).to(torch.float32).contiguous()
 
 
 def make_layer_params(H: int, P: int, N: int, G: int, gen: torch.Generator, rotation: bool = True,
@@ -132,6 +132,16 @@ def fresh_step(S: torch.Tensor, x, B, C, dt_raw, prm: LayerParams, dtype=torch.f
     S.copy_(S * dA + dB * xf[..., None])
     y = torch.einsum("bhpn,bhn->bhp", S, Cp)
     return y + xf * prm.D[None, :, None]
+
+
+def hot_only_step(S_hot: torch.Tensor, x, B, C, dt_raw, prm: LayerParams, dtype=torch.float32) -> torch.Tensor:
+    """Hot tier only, cold columns dropped (cold == "off"): the update and readout
+    of the first k = S_hot.shape[-1] rotated columns, scale/v4_fused_decode.py:52-56
+    and :140-142. S_hot updated in place; y = S_hot C'[:k] + D x."""
+    k = S_hot.shape[-1]
+    xf, Bp, Cp, dt, a = _prep(x, B, C, dt_raw, prm, dtype)
+    S_hot.copy_(S_hot * torch.exp(a)[..., None, None] + (dt[..., None, None] * Bp[:, :, None, :k]) * xf[..., None])
+    return torch.einsum("bhpn,bhn->bhp", S_hot, Cp[..., :k]) + xf * prm.D[None, :, None]
 
 
 # ---------------------------------------------------------------------------

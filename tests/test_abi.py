@@ -110,6 +110,8 @@ def test_tier_sizes():
     assert L.nssm_tier_sizes(4, 8, 80, 64, 1, 32, 4, 0, sz) == -2  # d_state must be 128
     assert L.nssm_tier_sizes(4, 8, 80, 128, 1, 32, 65, 0, sz) == -2  # c above 64
     assert L.nssm_tier_sizes(4, 8, 80, 128, 1, 32, 4, 7, sz) == -4
+    assert L.nssm_tier_sizes(4, 8, 80, 128, 1, 32, 4, 3, sz) == 0  # hot only
+    assert sz[0] == 4 * 8 * 80 * 32 * 4 and all(sz[i] == 0 for i in range(1, 7))
 
 
 def test_entry_points_validate_before_launching():

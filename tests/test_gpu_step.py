@@ -177,3 +177,56 @@ def test_out_of_range_slot_gives_nan_rows():
     y = fresh_step(dprm, S_dev, *to_dev(x, B, C, dt), slot_ids=sl)
     assert torch.isnan(y[1]).all() and not torch.isnan(y[0]).any()
     assert torch.equal(S_dev[0].cpu(), S0[0])  # slot 0 untouched
+
+
+@pytest.mark.parametrize("k", [32, 64, 96])
+def test_hot_only_tier(k):
+    b, H, G, P = 3, 8, 2, 80
+    gen, prm, S0 = _setup(b, H, P, G, seed=31 + k)
+    dprm = dev_params(prm)
+    tier = V4Tier(b, H, P, G, k_hot=k, c=4, cold="off")
+    assert tier.cold_t is None and tier.ring_x is None
+    tier.join(dprm, *to_dev(S0))
+    Sh = S0[..., :k].clone()
+    for step in range(10):
+        x, B, C, dt = oracle.make_step_inputs(b, H, P, 128, G, gen)
+        y_ref = oracle.hot_only_step(Sh, x, B, C, dt, prm)
+        y = tier.step(dprm, *to_dev(x, B, C, dt))
+        assert_close32(y, y_ref, f"hot-only k={k} y step {step}", **FP32_TOL)
+    assert_close32(tier.hot, Sh, "hot-only state", **FP32_TOL)
+    with pytest.raises(Exception, match="kind"):
+        tier.materialize(dprm)
+
+
+def test_bench_v4_decode_dropin_smoke(tmp_path):
+    """The bench drop-in runs its smoke point and writes the reference's JSON keys."""
+    from nested_ssm_amd import bench_v4_decode as BV
+
+    out = BV.main(["--Bs", "8", "--cs", "4", "--out", str(tmp_path / "b.json")])
+    r = out["points"][0]
+    for key in ("fresh_ms", "v4_ms", "v4async_ms", "v4bf16_ms", "v4fp8_ms", "hotonly_ms", "eager3_ms",
+                "fresh_ssu_ms", "v4ssu_ms", "fresh_toks", "v4_toks", "speedup_vs_fresh", "speedup_bf16",
+                "speedup_fp8", "fresh_bw_tbs", "state_gb", "B", "pb", "c"):
+        assert key in r, key
+    assert r["B"] == 8 and r["c"] == 4 and r["v4_ms"] > 0 and r["fresh_ms"] > 0
+
+
+def test_fp8_cold_readout_matches_oracle():
+    gen = torch.Generator().manual_seed(2)
+    R_, Nc, Pd = 37, 96, 80
+    q = torch.randn(R_, Nc, generator=gen)
+    sc = torch.rand(R_, Nc, generator=gen) + 0.05
+    S8 = (torch.randn(R_, Nc, Pd, generator=gen) * 50).to(torch.float8_e4m3fn)
+    want = oracle.fp8_readout(q, S8, sc)
+    from nested_ssm_amd import fp8_cold_readout
+    out = torch.empty(R_, Pd, device="cuda")
+    got = fp8_cold_readout(q.cuda(), S8.cuda(), sc.cuda(), out)
+    assert_close32(got, want, "fp8 readout", rtol=1e-5, atol=1e-4)
+
+
+def test_rotate_matches_oracle():
+    from nested_ssm_amd import rotate
+    gen = torch.Generator().manual_seed(3)
+    R = oracle.make_rotation(8, 128, gen)
+    X = torch.randn(5, 8, 128, generator=gen).to(torch.bfloat16)
+    assert_close32(rotate(X.cuda(), R.cuda()), oracle.rotate(X.float(), R), "rotate", rtol=1e-5, atol=1e-6)

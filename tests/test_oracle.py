@@ -296,3 +296,18 @@ def test_fp8_readout_matches_fp64_loop():
         for p in range(Pd):
             want = sum(float(q[r, n]) * float(sc[r, n]) * float(S8[r, n, p].float()) for n in range(Nc))
             assert abs(want - float(got[r, p])) < 1e-5
+
+
+def test_hot_only_step_is_the_fresh_trajectory_restricted_to_hot_columns():
+    b, H, P, G, k = 2, 4, 8, 2, 32
+    gen, prm, S0 = _small(seed=20, b=b, H=H, P=P, G=G)
+    ins = [oracle.make_step_inputs(b, H, P, N, G, gen) for _ in range(5)]
+    traj, _ = _fresh_traj(S0, ins, prm)
+    Sh = S0[..., :k].double().clone()
+    prm64 = prm.to(torch.float64)
+    for t, (x, B, C, dt) in enumerate(ins, start=1):
+        y = oracle.hot_only_step(Sh, x, B, C, dt, prm64, dtype=torch.float64)
+        Cp = _heads(oracle.rotate(C.double(), prm64.R), H)
+        want = torch.einsum("bhpn,bhn->bhp", traj[t][..., :k], Cp[..., :k]) + x.double() * prm64.D[None, :, None]
+        assert torch.allclose(y, want, atol=1e-11)
+        assert torch.allclose(Sh, traj[t][..., :k], atol=1e-12)
