@@ -22,9 +22,12 @@ def max_rel(a: torch.Tensor, b: torch.Tensor) -> float:
 
 
 def assert_close32(got: torch.Tensor, ref: torch.Tensor, what: str, rtol=1e-5, atol=1e-5):
-    """The fp32 parity bar: |got - ref| <= atol + rtol |ref| elementwise."""
-    got = got.detach().cpu().float()
-    ref = ref.detach().cpu().float()
+    """The fp32 parity bar: |got - ref| <= atol + rtol |ref| elementwise (computed on
+    the device of `ref`, or the CPU when the two differ)."""
+    if got.device != ref.device:
+        got, ref = got.detach().cpu(), ref.detach().cpu()
+    got = got.detach().float()
+    ref = ref.detach().float()
     err = (got - ref).abs()
     bound = atol + rtol * ref.abs()
     bad = err > bound

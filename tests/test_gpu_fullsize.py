@@ -1,0 +1,136 @@
+"""GPU: the benchmark configurations at their full per-layer sizes (9B head shape
+H=128, P=80, N=128, G=8), checked by properties that do not need the CPU oracle:
+
+  * the v4 tier's hot columns equal an untiered (fresh) run's hot columns;
+  * the tier's materialized state (snapshot + pending ring replay) equals the
+    fresh state, and its cold copy equals the fresh cold columns right after a
+    flush;
+  * y equals the stale-readout closed form built on the GPU in plain fp32 torch
+    from the fresh trajectory: hot C' + exp(glog) (snapshot C') + D x, where the
+    snapshot is the fresh state at the request's last flush (for fp8: torch's
+    own e4m3fn cast of it with the per-row amax / 448 + 1e-12 scale).
+
+fp32 bar rtol = atol = 1e-5; fp8 y: ||dy|| / ||y|| <= 2e-2 per step."""
+import pytest
+import torch
+
+from helpers import assert_close32
+from nested_ssm_amd import LayerParams, V4Tier, fresh_step
+
+pytestmark = pytest.mark.gpu
+
+H, P, N, G = 128, 80, 128, 8
+DEV = "cuda"
+
+
+def _params(seed):
+    gen = torch.Generator().manual_seed(seed)
+    f = dict(device=DEV, dtype=torch.float32)
+    u = 1e-3 + (1e-1 - 1e-3) * torch.rand(H, generator=gen, dtype=torch.float64)
+    A = -torch.exp(torch.rand(H, generator=gen, dtype=torch.float64) * 2.772588722239781)
+    Q, Rr = torch.linalg.qr(torch.randn(G, N, N, generator=gen, dtype=torch.float64))
+    R = Q * torch.sign(torch.diagonal(Rr, dim1=-2, dim2=-1))[..., None, :]
+    return LayerParams(H, P, N, G, torch.log(torch.expm1(u)).to(**f), A.to(**f),
+                       torch.randn(H, generator=gen, dtype=torch.float64).to(**f), R.to(**f).contiguous())
+
+
+def _inputs(b, g):
+    x = torch.randn(b, H, P, device=DEV, generator=g).to(torch.bfloat16)
+    B = (torch.randn(b, G, N, device=DEV, generator=g) / N ** 0.5).to(torch.bfloat16)
+    C = (torch.randn(b, G, N, device=DEV, generator=g) / N ** 0.5).to(torch.bfloat16)
+    dt = torch.randn(b, H, device=DEV, generator=g).to(torch.bfloat16)
+    return x, B, C, dt
+
+
+def _rotated_C(prm, C):
+    Cp = torch.einsum("bgn,gmn->bgm", C.float(), prm.R)  # R[g][m][n]
+    return Cp.repeat_interleave(H // G, dim=1)
+
+
+def _log_decay(prm, dt):
+    d = torch.nn.functional.softplus(dt.float() + prm.dt_bias[None, :])
+    return d * prm.A[None, :]
+
+
+def _quant_rt(s):
+    sc = s.abs().amax(-1, keepdim=True) / 448.0 + 1e-12
+    return (s / sc).to(torch.float8_e4m3fn).float() * sc
+
+
+def _run(b, k, c, cold, steps, seed, slot_events=None, check_y=True):
+    prm = _params(seed)
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    S = torch.randn(b, H, P, N, device=DEV, generator=g).mul_(0.1)
+    phase = torch.randint(0, c, (b,), device=DEV, generator=g, dtype=torch.int32)
+    tier = V4Tier(b, H, P, G, k_hot=k, c=c, cold=cold)
+    tier.join(prm, S, phase=phase)
+    t = phase.clone().long()
+    snap = S[..., k:].clone()  # fresh cold columns at each slot's last snapshot
+    glog = torch.zeros(b, H, device=DEV)
+    worst = 0.0
+    for step in range(steps):
+        if slot_events is not None:
+            ev = slot_events(step, g)
+            if ev is not None:  # requests leave, new ones join those slots with a new state and phase
+                sl, Snew, ph = ev
+                S[sl.long()] = Snew
+                tier.join(prm, Snew, slot_ids=sl, phase=ph)
+                t[sl.long()] = ph.long()
+                snap[sl.long()] = Snew[..., k:]
+                glog[sl.long()] = 0
+        x, B, C, dt = _inputs(b, g)
+        y = tier.step(prm, x, B, C, dt)
+        yf = fresh_step(prm, S, x, B, C, dt)
+        assert_close32(tier.hot, S[..., :k], f"hot columns step {step}")
+        if check_y:
+            Cp = _rotated_C(prm, C)
+            read = _quant_rt(snap) if cold == "fp8" else snap
+            cold_part = torch.einsum("bhpn,bhn->bhp", read, Cp[..., k:]) * torch.exp(glog)[..., None]
+            y_ref = yf - torch.einsum("bhpn,bhn->bhp", S[..., k:], Cp[..., k:]) + cold_part
+            if cold == "fp8":
+                r = float((y - y_ref).norm() / y_ref.norm())
+                worst = max(worst, r)
+                assert r <= 2e-2, f"fp8 y step {step}: {r:.3g}"
+            else:
+                assert_close32(y, y_ref, f"y step {step}", rtol=1e-5, atol=2e-5)
+        a = _log_decay(prm, dt)
+        t += 1
+        flush = (t % c == 0)
+        glog = torch.where(flush[:, None], torch.zeros_like(glog), glog + a)
+        if bool(flush.any()):
+            snap[flush] = S[flush][..., k:]
+    assert_close32(tier.materialize(prm), S, "materialized state")
+    if cold == "fp32":
+        done = (t % c == 0)
+        if bool(done.any()):
+            assert_close32(tier.cold_t[done], S[done][..., k:], "cold copy after flush")
+    assert torch.equal(tier.t[:, 0].long(), t)
+    return worst
+
+
+def test_full_size_v4_tracks_fresh():
+    """Config 2 at its per-layer size: B=256, k=32, c=4, fp32 cold (random phases)."""
+    _run(256, 32, 4, "fp32", steps=12, seed=1)
+
+
+def test_full_size_fp8_b448():
+    """Config 3 at its per-layer size: B=448, fp8 cold with per-row scale, c=4, 128 steps."""
+    worst = _run(448, 32, 4, "fp8", steps=128, seed=2)
+    assert worst > 0
+
+
+@pytest.mark.parametrize("c,k", [(8, 32), (16, 32), (64, 32), (8, 64), (16, 64), (64, 64)])
+def test_full_size_ragged_config4(c, k):
+    """Config 4: 384 slots, random phases, 48 requests leave and new ones join every 8 steps."""
+    b = 384
+
+    def events(step, g):
+        if step == 0 or step % 8:
+            return None
+        sl = torch.randperm(b, device=DEV, generator=g)[:48].to(torch.int32)
+        Snew = torch.randn(48, H, P, N, device=DEV, generator=g).mul_(0.1)
+        ph = torch.randint(0, c, (48,), device=DEV, generator=g, dtype=torch.int32)
+        return sl, Snew, ph
+
+    _run(b, k, c, "fp32", steps=256 if c == 64 else 64, seed=10 + c + k, slot_events=events,
+         check_y=(c != 64))
