@@ -31,6 +31,7 @@ namespace {
 constexpr int kN = 128;  // d_state handled by these kernels
 constexpr int kMaxC = 64;
 constexpr int kMaxWaves = 8;
+constexpr int kMfmaTiles = 8;  // 16 x 16 flush-contraction tiles a wave keeps in registers
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2v __attribute__((ext_vector_type(2)));
@@ -403,7 +404,7 @@ __device__ __forceinline__ void unit_compute(const StepArgs& a, size_t row, size
                                              UnitRaw<K, COLD>& d, uint16_t* rx, const float* __restrict__ hd,
                                              const float (&Bh)[K / 32][4], const float (&Ch)[K / 32][4],
                                              const float (&Cc)[UnitRaw<K, COLD>::CSR][4], const float* sU,
-                                             const float* sBc, int m) {
+                                             const float* sBc, int m, const float* dS = nullptr) {
   constexpr int HS = K / 32;
   constexpr int NC = kN - K;
   constexpr int CS = UnitRaw<K, COLD>::CS;
@@ -461,16 +462,28 @@ __device__ __forceinline__ void unit_compute(const StepArgs& a, size_t row, size
       for (int s = 0; s < CS; ++s)
 #pragma unroll
         for (int e = 0; e < 4; ++e) nvv[s][e] *= dtot;
-      for (int i = 0; i < m; ++i) {
-        const float coef = sU[i * P + p];
-        const float* bc = sBc + i * NC + 4 * q;
+      if (dS) {  // window contraction done on the matrix cores, rows of stride NC + 4
+        const float* dr = dS + p * (NC + 4) + 4 * q;
 #pragma unroll
         for (int s = 0; s < CS; ++s) {
-          const f4 bb = *reinterpret_cast<const f4*>(bc + 32 * s);
-          nvv[s][0] = fmaf(coef, bb.x, nvv[s][0]);
-          nvv[s][1] = fmaf(coef, bb.y, nvv[s][1]);
-          nvv[s][2] = fmaf(coef, bb.z, nvv[s][2]);
-          nvv[s][3] = fmaf(coef, bb.w, nvv[s][3]);
+          const f4 dd = *reinterpret_cast<const f4*>(dr + 32 * s);
+          nvv[s][0] += dd.x;
+          nvv[s][1] += dd.y;
+          nvv[s][2] += dd.z;
+          nvv[s][3] += dd.w;
+        }
+      } else {
+        for (int i = 0; i < m; ++i) {
+          const float coef = sU[i * P + p];
+          const float* bc = sBc + i * NC + 4 * q;
+#pragma unroll
+          for (int s = 0; s < CS; ++s) {
+            const f4 bb = *reinterpret_cast<const f4*>(bc + 32 * s);
+            nvv[s][0] = fmaf(coef, bb.x, nvv[s][0]);
+            nvv[s][1] = fmaf(coef, bb.y, nvv[s][1]);
+            nvv[s][2] = fmaf(coef, bb.z, nvv[s][2]);
+            nvv[s][3] = fmaf(coef, bb.w, nvv[s][3]);
+          }
         }
       }
       cold_store<COLD, CS>(a, row, q, nvv);
@@ -587,6 +600,46 @@ __global__ void __launch_bounds__(kMaxWaves * 64) stream_kernel(StepArgs a) {
       sU[i] = ws.w[((size_t)bi * H + h0 + j) * c + e] * bf2f(xv);
     }
     __syncthreads();
+    // c >= 16: the window contraction Delta[p][n] = sum_i sU[i][p] sBc[i][n] runs on the
+    // matrix cores (v_mfma_f32_16x16x4_f32: A = sBc^T 16 n x 4 tokens, B = sU 4 tokens
+    // x 16 p, K = window tokens, zero past m). Each wave keeps up to kMfmaTiles 16 x 16
+    // output tiles in registers; after a barrier they go to LDS (rows of stride
+    // NC + 4, over the staging area) for the streaming-layout apply below.
+    const float* dS = nullptr;
+    constexpr int NT = NC / 16;
+    const int ntiles = (P / 16) * NT;
+    if (c >= 16 && hpw == 1 && ntiles <= nw * kMfmaTiles) {
+      const int li = lane & 15, lk = lane >> 4;
+      f4 acc[kMfmaTiles];
+#pragma unroll
+      for (int i = 0; i < kMfmaTiles; ++i) {
+        acc[i] = f4{0.f, 0.f, 0.f, 0.f};
+        const int tt = wave + i * nw;
+        if (tt < ntiles) {
+          const int pt = tt / NT, nt = tt - pt * NT;
+          for (int k0 = 0; k0 < m; k0 += 4) {
+            const int kk = k0 + lk;
+            const int kc = kk < m ? kk : m - 1;
+            float av = sBc[kc * NC + nt * 16 + li];
+            float bv = sU[kc * P + pt * 16 + li];
+            if (kk >= m) av = bv = 0.f;
+            acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[i], 0, 0, 0);
+          }
+        }
+      }
+      __syncthreads();  // every wave is done reading sBc / sU
+      float* dW = lds;  // [P][NC + 4]
+#pragma unroll
+      for (int i = 0; i < kMfmaTiles; ++i) {
+        const int tt = wave + i * nw;
+        if (tt < ntiles) {  // lane holds Delta[p0 + li][n0 + 4 lk .. +3]
+          const int pt = tt / NT, nt = tt - pt * NT;
+          *reinterpret_cast<f4*>(dW + (pt * 16 + li) * (NC + 4) + nt * 16 + 4 * lk) = acc[i];
+        }
+      }
+      __syncthreads();
+      dS = dW;
+    }
     // software pipeline: the next unit's loads are in flight during this one's compute
     for (int u = wave; u < units; u += nw) {
       UnitRaw<K, COLD> dnext;
@@ -602,7 +655,7 @@ __global__ void __launch_bounds__(kMaxWaves * 64) stream_kernel(StepArgs a) {
       const float* hd = hdb + j * HD_STRIDE;
       if (hd[HD_FLUSH] != 0.f) {
         unit_compute<K, COLD, true>(a, row, yrow, p, q, dcur, nullptr, hd, Bh, Ch, Cc, sU + (size_t)j * m * P, sBc,
-                                    m);
+                                    m, dS);
       } else {
         uint16_t* rx = a.ring_x + (((size_t)slot * H + h0 + j) * c + (int)hd[HD_POS]) * P;
         unit_compute<K, COLD, false>(a, row, yrow, p, q, dcur, rx, hd, Bh, Ch, Cc, nullptr, nullptr, 0);
@@ -766,7 +819,10 @@ int divisor_at_most(int n, int cap) {
 
 size_t stream_lds_bytes(int hpw, int P, int c, int K, int kind = NSSM_COLD_FP32) {
   const int NC = kN - K;
-  return NC > 0 && kind != NSSM_COLD_NONE ? ((size_t)c * NC + (size_t)hpw * c * P) * sizeof(float) : 0;
+  if (NC <= 0 || kind == NSSM_COLD_NONE) return 0;
+  size_t fl = (size_t)c * NC + (size_t)hpw * c * P;  // window staging
+  if (c >= 16 && hpw == 1) fl = fl > (size_t)P * (NC + 4) ? fl : (size_t)P * (NC + 4);  // MFMA exchange
+  return fl * sizeof(float);
 }
 
 struct Launch {

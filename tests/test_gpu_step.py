@@ -230,3 +230,13 @@ def test_rotate_matches_oracle():
     R = oracle.make_rotation(8, 128, gen)
     X = torch.randn(5, 8, 128, generator=gen).to(torch.bfloat16)
     assert_close32(rotate(X.cuda(), R.cuda()), oracle.rotate(X.float(), R), "rotate", rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("c", [16, 33, 64])
+@pytest.mark.parametrize("hpw", [1, 2])
+def test_flush_contraction_mfma_and_valu_paths(c, hpw):
+    """c >= 16 with one head per workgroup contracts the flush window on the matrix
+    cores; two heads per workgroup take the VALU replay. Both match the oracle."""
+    b, H, G, P, k = 2, 8, 2, 80, 32
+    set_launch(hpw, 4)
+    _run_v4(b, H, G, P, k, c, "fp32", steps=2 * c + 3, seed=40 + c + hpw, check_state_every=c)
