@@ -45,7 +45,7 @@ extern "C" {
 #define NSSM_OK 0
 #define NSSM_E_NULL (-1)        /* a required pointer is NULL            */
 #define NSSM_E_DIMS (-2)        /* sizes out of the supported range      */
-#define NSSM_E_ALIGN (-3)       /* a pointer is not 16-byte aligned      */
+#define NSSM_E_ALIGN (-3)       /* a pointer is not aligned as required  */
 #define NSSM_E_KIND (-4)        /* unknown cold storage kind             */
 #define NSSM_E_LAUNCH (-5)      /* the HIP launch reported an error      */
 #define NSSM_E_TUNING (-6)      /* launch override does not fit the dims */
@@ -73,7 +73,7 @@ typedef struct nssm_layer_params {
 /* One decode token for b requests (all bf16, as the model emits them). */
 typedef struct nssm_step_inputs {
   int32_t b;
-  const uint16_t* x;        /* [b][H][P] bf16 conv/SiLU output, head view */
+  const uint16_t* x;        /* [b][H][P] bf16 conv/SiLU output, head view; 8-byte aligned */
   const uint16_t* B;        /* [b][G][N] bf16, before rotation */
   const uint16_t* C;        /* [b][G][N] bf16, before rotation */
   const uint16_t* dt;       /* [b][H] bf16, before dt_bias and softplus */
@@ -92,7 +92,8 @@ typedef struct nssm_step_inputs {
  *   t        int32 [slots][H]           decode steps (phase = t % c)
  *   nv       int32 [slots][H]           buffered tokens since the last snapshot
  *   glog     fp32 [slots][H]            log-decay since the snapshot, one token lagged
- * All heads of a slot carry equal t and nv. */
+ * All heads of a slot carry equal t and nv. hot, cold, master and ring_b are
+ * 16-byte aligned, ring_x 8-byte aligned. */
 typedef struct nssm_tier {
   int32_t slots, k_hot, c, cold_kind;
   float* hot;

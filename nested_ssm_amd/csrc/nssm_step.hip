@@ -1,7 +1,8 @@
 // gfx950 kernels for the Mamba2 decode-step recurrent-state update with
 // nested hot/cold tiering, and the C ABI declared in include/nssm.h.
 //
-// One layer-token is two launches on the caller's stream:
+// A tiered layer-token is three launches on the caller's stream (the untiered
+// step: prep and stream):
 //
 //  prep    one workgroup per (request, group). Rotates B and C once
 //          (B' = R_g B, C' = R_g C, fp32) into the workspace, computes each
@@ -11,14 +12,13 @@
 //          at position t % c. A flush token sits at c-1, so a flush window is
 //          always ring positions [c-m, c).
 //  stream  one workgroup per (request, head block): streams the state rows.
-//          A "unit" is 8 consecutive headdim rows p of one head. In a unit,
-//          lane l owns row p0 + (l >> 3) and, in every 32-column segment s, the
-//          four columns 32 s + 4 (l & 7) .. +3. One dwordx4 per lane per
-//          segment moves 8 rows x 128 B = 1 KB per wave instruction; the C.h
-//          readout of a row is a sum over its 8 lanes (three DPP steps).
-//          Hot columns [0, K) are read and written every token; cold columns
-//          [K, N) are only read, except at the request's flush token, when the
-//          workgroup replays the staged window into them.
+//          A "unit" is 8 consecutive headdim rows p of one head; lane l works
+//          on row p0 + (l >> 3), and a row's C.h readout is a sum over its 8
+//          lanes (three DPP steps). Hot columns [0, K) are read and written
+//          every token; cold columns [K, N) are only read (the stale readout),
+//          and not at all for a head that flushes at this token.
+//  flush   the cold columns of the heads that flush: decayed snapshot plus the
+//          window contraction on the matrix cores, and their stale readout.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -30,8 +30,9 @@ namespace {
 
 constexpr int kN = 128;  // d_state handled by these kernels
 constexpr int kMaxC = 64;
+constexpr int kMaxHG = 64;  // heads per group
 constexpr int kMaxWaves = 8;
-constexpr int kMfmaTiles = 8;  // 16 x 16 flush-contraction tiles a wave keeps in registers
+constexpr int kMfmaTiles = 4;  // 16 x 16 flush-contraction tiles a wave keeps in registers
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2v __attribute__((ext_vector_type(2)));
@@ -144,6 +145,8 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
   constexpr int ROWS = kN / (2 * NW);  // rows of R per half-wave
   constexpr int RB = ROWS / 2;         // rows per batch in flight
   __shared__ float sBraw[kN], sCraw[kN], sBr[kN];
+  __shared__ float sRdt[TIERED ? kMaxHG * kMaxC : 1];  // window dt of flushing heads [HG][c]
+  __shared__ int sT[TIERED ? kMaxHG : 1], sNv[TIERED ? kMaxHG : 1];
   __shared__ int sPos, sFlush;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = blockIdx.x % a.G, bi = blockIdx.x / a.G;
@@ -177,12 +180,26 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
     Ah = a.A[h];
     Dh = a.D[h];
     if constexpr (TIERED) {
-      tt = a.t[o];
-      nvv = a.nv[o];
+      // t >= 0 and 0 <= nv < c hold for every tier these kernels write; the
+      // clamps keep ring indexing inside the buffers even for a corrupted phase
+      tt = max(a.t[o], 0);
+      nvv = min(max(a.nv[o], 0), c - 1);
       gl = a.glog[o];
+      sT[tid] = tt;
+      sNv[tid] = nvv;
     }
   }
   __syncthreads();
+
+  // 1b. a flushing head's window dt (ring positions [c-1-nv, c-1)), loaded by all threads
+  if constexpr (TIERED) {
+#pragma unroll 4
+    for (int idx = tid; idx < HG * c; idx += kPrepThreads) {
+      const int hh = idx / c, i = idx - hh * c;
+      if ((sT[hh] + 1) % c == 0 && i >= c - 1 - sNv[hh] && i < c - 1)
+        sRdt[idx] = a.ring_dt[((size_t)slot * H + g * HG + hh) * c + i];
+    }
+  }
 
   // 2. rotation: a half-wave per row of R (both halves see the same rows
   // count, so every reduction runs with all lanes active)
@@ -222,6 +239,8 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
     ws.C[bgo + tid] = sCraw[tid];
   }
 
+  if constexpr (TIERED) __syncthreads();  // sRdt
+
   // 3. per-head scalars and bookkeeping: one thread per head of the group
   if (head_thread) {
     float dt = softplus_f(draw + dtb);
@@ -233,10 +252,6 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
     hd[HD_DECAY] = expf(av);
     hd[HD_D] = Dh;
     if constexpr (TIERED) {
-      // t >= 0 and 0 <= nv < c hold for every tier these kernels write; the
-      // clamps keep ring indexing inside the buffers even for a corrupted phase
-      tt = max(tt, 0);
-      nvv = min(max(nvv, 0), c - 1);
       const int pos = tt % c;
       const bool flush = (tt + 1) % c == 0;  // then pos == c - 1
       hd[HD_EG] = expf(gl);
@@ -246,7 +261,7 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
         // window = the nv buffered tokens at ring [c-m, c-1) and this one:
         // w_i = exp(sum_{l>i} a_l) dt_i, total decay exp(sum_l a_l)
         const int m = nvv + 1;
-        const float* __restrict__ rdt = a.ring_dt + o * c + (c - m);
+        const float* rdt = sRdt + tid * c + (c - m);
         float* __restrict__ w = ws.w + ((size_t)bi * H + h) * c;
         float suf = 0.f;
         for (int i = m - 1; i >= 0; --i) {
@@ -293,69 +308,189 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// stream: raw registers of one unit for one lane: HS hot float4 and CS cold
-// segments (float4 / 4 x bf16 / 4 x e4m3 by storage kind).
+// stream kernel
+//
+// Lane mappings inside a unit (8 rows p0..p0+7 of one head); lane l, rr = l >> 3, q = l & 7:
+//   segment     columns 32 s + 4 q + e of row p0 + rr (segment s, e = 0..3): hot columns, the
+//               fp32 cold copy and the fp32 master. One dwordx4 per segment moves 8 rows x 128 B
+//               (whole cache lines) per wave instruction.
+//   contiguous  columns CW q .. CW q + CW - 1 (CW = NC / 8) of row p0 + rr: the bf16 / e4m3 read
+//               copies, so a lane's bytes are one contiguous dwordx3 (e4m3, k = 32) load.
+//   mfma        flush at c >= 16: lane (li = l & 15, lk = l >> 4) of a 16 x 16 tile holds row
+//               p0 + li, columns n0 + 4 lk .. +3: the accumulator layout of v_mfma_f32_16x16x4_f32.
+// Both unit mappings group a row's lanes as 8 consecutive lanes, so a row's dot product is
+// sum8 (three DPP steps).
+
+template <int K, int COLD>
+struct Cfg {
+  static constexpr int HS = K / 32;
+  static constexpr int NC = kN - K;
+  static constexpr bool TIERED = COLD != NSSM_COLD_NONE && NC > 0;
+  static constexpr int CS = TIERED ? NC / 32 : 0;                // cold segments per row
+  static constexpr int CSR = CS > 0 ? CS : 1;
+  static constexpr int CW = NC / 8;                              // contiguous columns per lane
+  static constexpr int WORDS = COLD == NSSM_COLD_FP8 ? CW / 4 : COLD == NSSM_COLD_BF16 ? CW / 2 : 0;
+  static constexpr int WR = WORDS > 0 ? WORDS : 1;
+  static constexpr int CWR = (COLD == NSSM_COLD_FP8 || COLD == NSSM_COLD_BF16) ? CW : 1;
+  static constexpr int NT = NC / 16;                             // 16-column tiles of a row
+};
+
+// e4m3fn <-> fp32 on gfx950's conversion instructions (OCP e4m3fn, round to nearest even;
+// bit-identical to nssm_f32_to_e4m3fn / nssm_e4m3fn_to_f32 for the |v| <= 448 range the
+// kernels produce)
+__device__ __forceinline__ void fp8x4_to_f32(uint32_t w, float (&v)[4]) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  const f2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  const f2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  v[0] = lo.x; v[1] = lo.y; v[2] = hi.x; v[3] = hi.y;
+}
+__device__ __forceinline__ uint32_t f32x4_to_fp8(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return (uint32_t)w;
+}
+
+template <int N>
+__device__ __forceinline__ void ld_words(const uint32_t* p, uint32_t (&w)[N]) {
+  if constexpr (N == 1) {
+    w[0] = ld_stream(p);
+  } else if constexpr (N == 2) {
+    const u2v t = ld_stream(reinterpret_cast<const u2v*>(p));
+    w[0] = t.x; w[1] = t.y;
+  } else if constexpr (N == 3) {  // 12 bytes at 4-byte alignment
+    w[0] = ld_stream(p);
+    w[1] = ld_stream(p + 1);
+    w[2] = ld_stream(p + 2);
+  } else {
+    static_assert(N % 2 == 0, "word count");
+#pragma unroll
+    for (int i = 0; i < N; i += 2) {
+      const u2v t = ld_stream(reinterpret_cast<const u2v*>(p + i));
+      w[i] = t.x; w[i + 1] = t.y;
+    }
+  }
+}
+
+// Raw registers of one unit for one lane.
 template <int K, int COLD>
 struct UnitRaw {
-  static constexpr int HS = K / 32;
-  static constexpr int CS = COLD == NSSM_COLD_NONE ? 0 : (kN - K) / 32;
-  static constexpr int CSR = CS > 0 ? CS : 1;
-  f4 hv[HS];
-  f4 cf[COLD == NSSM_COLD_FP32 ? CSR : 1];
-  u2v cb[COLD == NSSM_COLD_BF16 ? CSR : 1];
-  uint32_t c8[COLD == NSSM_COLD_FP8 ? CSR : 1];
-  float sc;
+  using C = Cfg<K, COLD>;
+  f4 hv[C::HS];
+  f4 cf[COLD == NSSM_COLD_FP32 ? C::CSR : 1];  // fp32 cold copy, segment mapping
+  uint32_t cw[C::WR];                           // bf16 / e4m3 read copy, contiguous mapping
+  float sc;                                     // e4m3 row scale
   float xp;
   uint16_t xraw;
 };
 
 template <int K, int COLD>
-__device__ __forceinline__ void unit_load(const StepArgs& a, size_t row, size_t xrow, int q, UnitRaw<K, COLD>& d) {
-  constexpr int HS = K / 32, CS = UnitRaw<K, COLD>::CS, NC = kN - K;
+__device__ __forceinline__ void unit_load(const StepArgs& a, size_t row, size_t xrow, int q, UnitRaw<K, COLD>& d,
+                                          bool hot_only = false) {
+  using C = Cfg<K, COLD>;
   const f4* hp = reinterpret_cast<const f4*>(a.hot + row * K) + q;
 #pragma unroll
-  for (int s = 0; s < HS; ++s) d.hv[s] = ld_stream(hp + 8 * s);
-  if constexpr (CS > 0) {
-    if constexpr (COLD == NSSM_COLD_FP32) {
-      const f4* p = reinterpret_cast<const f4*>(static_cast<const float*>(a.cold) + row * NC) + q;
+  for (int s = 0; s < C::HS; ++s) d.hv[s] = ld_stream(hp + 8 * s);
+  if constexpr (C::TIERED) {
+    if (!hot_only) {
+      if constexpr (COLD == NSSM_COLD_FP32) {
+        const f4* p = reinterpret_cast<const f4*>(static_cast<const float*>(a.cold) + row * C::NC) + q;
 #pragma unroll
-      for (int s = 0; s < CS; ++s) d.cf[s] = ld_stream(p + 8 * s);
-    } else if constexpr (COLD == NSSM_COLD_BF16) {
-      const u2v* p = reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.cold) + row * NC) + q;
-#pragma unroll
-      for (int s = 0; s < CS; ++s) d.cb[s] = ld_stream(p + 8 * s);
-    } else {
-      const uint32_t* p = reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(a.cold) + row * NC) + q;
-#pragma unroll
-      for (int s = 0; s < CS; ++s) d.c8[s] = ld_stream(p + 8 * s);
-      d.sc = a.scale[row];
+        for (int s = 0; s < C::CS; ++s) d.cf[s] = ld_stream(p + 8 * s);
+      } else if constexpr (COLD == NSSM_COLD_BF16) {
+        ld_words<C::WORDS>(
+            reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(a.cold) + row * C::NC + C::CW * q), d.cw);
+      } else {
+        ld_words<C::WORDS>(
+            reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(a.cold) + row * C::NC + C::CW * q), d.cw);
+        d.sc = a.scale[row];
+      }
     }
   }
   d.xraw = a.x[xrow];
   d.xp = bf2f(d.xraw);
 }
 
-// read-copy values the readout sees
+// stale readout partial of one lane from its read-copy registers (times the row scale for e4m3)
 template <int K, int COLD>
-__device__ __forceinline__ void cold_decode(const UnitRaw<K, COLD>& d, float (&v)[UnitRaw<K, COLD>::CSR][4]) {
-  constexpr int CS = UnitRaw<K, COLD>::CS;
+__device__ __forceinline__ float cold_partial(const UnitRaw<K, COLD>& d, const float (&Cc)[Cfg<K, COLD>::CSR][4],
+                                              const float (&Cq)[Cfg<K, COLD>::CWR]) {
+  using C = Cfg<K, COLD>;
+  float pc = 0.f;
+  if constexpr (COLD == NSSM_COLD_FP32) {
 #pragma unroll
-  for (int s = 0; s < CS; ++s) {
-    if constexpr (COLD == NSSM_COLD_FP32) {
-      v[s][0] = d.cf[s].x; v[s][1] = d.cf[s].y; v[s][2] = d.cf[s].z; v[s][3] = d.cf[s].w;
-    } else if constexpr (COLD == NSSM_COLD_BF16) {
-      v[s][0] = __uint_as_float(d.cb[s].x << 16);
-      v[s][1] = __uint_as_float(d.cb[s].x & 0xffff0000u);
-      v[s][2] = __uint_as_float(d.cb[s].y << 16);
-      v[s][3] = __uint_as_float(d.cb[s].y & 0xffff0000u);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[s][e] = nssm_e4m3fn_to_f32((uint8_t)(d.c8[s] >> (8 * e))) * d.sc;
+    for (int s = 0; s < C::CS; ++s) {
+      pc = fmaf(d.cf[s].x, Cc[s][0], pc);
+      pc = fmaf(d.cf[s].y, Cc[s][1], pc);
+      pc = fmaf(d.cf[s].z, Cc[s][2], pc);
+      pc = fmaf(d.cf[s].w, Cc[s][3], pc);
     }
+  } else if constexpr (COLD == NSSM_COLD_BF16) {
+#pragma unroll
+    for (int i = 0; i < C::WORDS; ++i) {
+      pc = fmaf(__uint_as_float(d.cw[i] << 16), Cq[2 * i], pc);
+      pc = fmaf(__uint_as_float(d.cw[i] & 0xffff0000u), Cq[2 * i + 1], pc);
+    }
+  } else if constexpr (COLD == NSSM_COLD_FP8) {
+#pragma unroll
+    for (int i = 0; i < C::WORDS; ++i) {
+      float v[4];
+      fp8x4_to_f32(d.cw[i], v);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pc = fmaf(v[e], Cq[4 * i + e], pc);
+    }
+    pc *= d.sc;
+  }
+  return pc;
+}
+
+// Hot columns of one unit: decay-and-update in registers, store, and the lane's
+// readout partial.
+template <int K, int COLD>
+__device__ __forceinline__ float hot_update(const StepArgs& a, size_t row, int q, UnitRaw<K, COLD>& d,
+                                            const float* __restrict__ hd, const float (&Bh)[K / 32][4],
+                                            const float (&Ch)[K / 32][4]) {
+  const float uu = hd[HD_DT] * d.xp;
+  const float dec = hd[HD_DECAY];
+  float ph = 0.f;
+  f4* hp = reinterpret_cast<f4*>(a.hot + row * K) + q;
+#pragma unroll
+  for (int s = 0; s < K / 32; ++s) {
+    f4 v = d.hv[s];
+    v.x = fmaf(v.x, dec, uu * Bh[s][0]);
+    v.y = fmaf(v.y, dec, uu * Bh[s][1]);
+    v.z = fmaf(v.z, dec, uu * Bh[s][2]);
+    v.w = fmaf(v.w, dec, uu * Bh[s][3]);
+    ph = fmaf(v.x, Ch[s][0], ph);
+    ph = fmaf(v.y, Ch[s][1], ph);
+    ph = fmaf(v.z, Ch[s][2], ph);
+    ph = fmaf(v.w, Ch[s][3], ph);
+    st_stream(v, hp + 8 * s);
+  }
+  return ph;
+}
+
+// One unit of one token: hot columns, and (a head that does not flush at this token)
+// the stale readout of its cold read copy and the ring append of x. A flushing head's
+// cold columns are left to the flush kernel, which adds their readout to y.
+template <int K, int COLD>
+__device__ __forceinline__ void unit_compute(const StepArgs& a, size_t row, size_t yrow, int p, int q,
+                                             UnitRaw<K, COLD>& d, uint16_t* rx, bool cold, const float* __restrict__ hd,
+                                             const float (&Bh)[K / 32][4], const float (&Ch)[K / 32][4],
+                                             const float (&Cc)[Cfg<K, COLD>::CSR][4],
+                                             const float (&Cq)[Cfg<K, COLD>::CWR]) {
+  float part = hot_update<K, COLD>(a, row, q, d, hd, Bh, Ch);
+  if constexpr (Cfg<K, COLD>::TIERED) {
+    if (cold) part = fmaf(hd[HD_EG], cold_partial<K, COLD>(d, Cc, Cq), part);
+  }
+  part = sum8(part);
+  if (q == 0) {
+    a.y[yrow] = fmaf(hd[HD_D], d.xp, part);
+    if (rx) rx[p] = d.xraw;  // ring append of x (tokens that do not flush)
   }
 }
 
-// Write the new exact cold values of one row: fp32 copy, or master + read copy.
+// Write the new exact cold values of one row in the segment mapping: fp32 copy, or
+// master + bf16 / e4m3 read copy.
 template <int COLD, int CS>
 __device__ __forceinline__ void cold_store(const StepArgs& a, size_t row, int q, const float (&v)[CS][4]) {
   constexpr int NC = CS * 32;
@@ -376,7 +511,7 @@ __device__ __forceinline__ void cold_store(const StepArgs& a, size_t row, int q,
         t.y = (uint32_t)nssm_f32_to_bf16(v[s][2]) | ((uint32_t)nssm_f32_to_bf16(v[s][3]) << 16);
         st_stream(t, p + 8 * s);
       }
-    } else {  // FP8 with per-row amax scale, as scale/vllm_v4_patch.py:106-111
+    } else {  // e4m3 with the per-row amax scale of scale/vllm_v4_patch.py:106-111
       float am = 0.f;
 #pragma unroll
       for (int s = 0; s < CS; ++s)
@@ -386,125 +521,157 @@ __device__ __forceinline__ void cold_store(const StepArgs& a, size_t row, int q,
       const float sc = am / 448.0f + 1e-12f;
       uint32_t* p = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.cold) + row * NC) + q;
 #pragma unroll
-      for (int s = 0; s < CS; ++s) {
-        uint32_t t = 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) t |= (uint32_t)nssm_f32_to_e4m3fn(v[s][e] / sc) << (8 * e);
-        st_stream(t, p + 8 * s);
-      }
+      for (int s = 0; s < CS; ++s)
+        st_stream(f32x4_to_fp8(v[s][0] / sc, v[s][1] / sc, v[s][2] / sc, v[s][3] / sc), p + 8 * s);
       if (q == 0) a.scale[row] = sc;
     }
   }
 }
 
-// Compute and store one unit (8 rows of head h) from its raw registers. FLUSH
-// selects the replay of the staged window (sU [m][P] of this head, sBc [m][NC]).
-template <int K, int COLD, bool FLUSH>
-__device__ __forceinline__ void unit_compute(const StepArgs& a, size_t row, size_t yrow, int p, int q,
-                                             UnitRaw<K, COLD>& d, uint16_t* rx, const float* __restrict__ hd,
-                                             const float (&Bh)[K / 32][4], const float (&Ch)[K / 32][4],
-                                             const float (&Cc)[UnitRaw<K, COLD>::CSR][4], const float* sU,
-                                             const float* sBc, int m, const float* dS = nullptr) {
-  constexpr int HS = K / 32;
-  constexpr int NC = kN - K;
-  constexpr int CS = UnitRaw<K, COLD>::CS;
-  constexpr int CSR = UnitRaw<K, COLD>::CSR;
+// One unit of a head that flushes at this token, in the stream kernel (short windows):
+// hot columns, the stale readout, and the exact cold state at this token, the decayed
+// snapshot plus the VALU replay of the staged window (sU [m][P] of this head,
+// sBc [m][NC]), scale/v4_fused_decode.py:76-85.
+template <int K, int COLD>
+__device__ __forceinline__ void unit_compute_flush(const StepArgs& a, size_t row, size_t yrow, int p, int q,
+                                                   UnitRaw<K, COLD>& d, const float* __restrict__ hd,
+                                                   const float (&Bh)[K / 32][4], const float (&Ch)[K / 32][4],
+                                                   const float (&Cc)[Cfg<K, COLD>::CSR][4],
+                                                   const float (&Cq)[Cfg<K, COLD>::CWR], const float* sU,
+                                                   const float* sBc, int m) {
+  using C = Cfg<K, COLD>;
+  constexpr int NC = C::NC, CS = C::CS;
+  float part = hot_update<K, COLD>(a, row, q, d, hd, Bh, Ch);
+  part = fmaf(hd[HD_EG], cold_partial<K, COLD>(d, Cc, Cq), part);
   const int P = a.P;
-  const float xp = d.xp;
-  const float uu = hd[HD_DT] * xp;
-  const float dec = hd[HD_DECAY];
-  float ph = 0.f;
-  f4* hp = reinterpret_cast<f4*>(a.hot + row * K) + q;
+  const float dtot = hd[HD_DTOT];
+  float nvv[CS][4];
+  const f4* pm = reinterpret_cast<const f4*>(a.master + row * NC) + q;  // bf16 / e4m3: fp32 master
 #pragma unroll
-  for (int s = 0; s < HS; ++s) {
-    f4 v = d.hv[s];
-    v.x = fmaf(v.x, dec, uu * Bh[s][0]);
-    v.y = fmaf(v.y, dec, uu * Bh[s][1]);
-    v.z = fmaf(v.z, dec, uu * Bh[s][2]);
-    v.w = fmaf(v.w, dec, uu * Bh[s][3]);
-    ph = fmaf(v.x, Ch[s][0], ph);
-    ph = fmaf(v.y, Ch[s][1], ph);
-    ph = fmaf(v.z, Ch[s][2], ph);
-    ph = fmaf(v.w, Ch[s][3], ph);
-    st_stream(v, hp + 8 * s);
+  for (int s = 0; s < CS; ++s) {
+    f4 t;
+    if constexpr (COLD == NSSM_COLD_FP32) t = d.cf[s];
+    else t = ld_stream(pm + 8 * s);
+    nvv[s][0] = t.x * dtot; nvv[s][1] = t.y * dtot; nvv[s][2] = t.z * dtot; nvv[s][3] = t.w * dtot;
   }
-
-  float part = ph;
-  if constexpr (CS > 0) {
-    float cv[CSR][4];
-    cold_decode<K, COLD>(d, cv);
-    float pc = 0.f;
+  for (int i = 0; i < m; ++i) {
+    const float coef = sU[i * P + p];
+    const float* bc = sBc + i * NC + 4 * q;
 #pragma unroll
-    for (int s = 0; s < CS; ++s)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) pc = fmaf(cv[s][e], Cc[s][e], pc);
-    part = fmaf(hd[HD_EG], pc, ph);
-
-    if constexpr (FLUSH) {
-      // exact cold state at this token: decayed snapshot + decayed replay of
-      // the window (buffered tokens and this one), scale/v4_fused_decode.py:76-85
-      float nvv[CS][4];
-      if constexpr (COLD == NSSM_COLD_FP32) {
-#pragma unroll
-        for (int s = 0; s < CS; ++s)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) nvv[s][e] = cv[s][e];
-      } else {
-        const f4* pm = reinterpret_cast<const f4*>(a.master + row * NC) + q;
-#pragma unroll
-        for (int s = 0; s < CS; ++s) {
-          const f4 t = ld_stream(pm + 8 * s);
-          nvv[s][0] = t.x; nvv[s][1] = t.y; nvv[s][2] = t.z; nvv[s][3] = t.w;
-        }
-      }
-      const float dtot = hd[HD_DTOT];
-#pragma unroll
-      for (int s = 0; s < CS; ++s)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) nvv[s][e] *= dtot;
-      if (dS) {  // window contraction done on the matrix cores, rows of stride NC + 4
-        const float* dr = dS + p * (NC + 4) + 4 * q;
-#pragma unroll
-        for (int s = 0; s < CS; ++s) {
-          const f4 dd = *reinterpret_cast<const f4*>(dr + 32 * s);
-          nvv[s][0] += dd.x;
-          nvv[s][1] += dd.y;
-          nvv[s][2] += dd.z;
-          nvv[s][3] += dd.w;
-        }
-      } else {
-        for (int i = 0; i < m; ++i) {
-          const float coef = sU[i * P + p];
-          const float* bc = sBc + i * NC + 4 * q;
-#pragma unroll
-          for (int s = 0; s < CS; ++s) {
-            const f4 bb = *reinterpret_cast<const f4*>(bc + 32 * s);
-            nvv[s][0] = fmaf(coef, bb.x, nvv[s][0]);
-            nvv[s][1] = fmaf(coef, bb.y, nvv[s][1]);
-            nvv[s][2] = fmaf(coef, bb.z, nvv[s][2]);
-            nvv[s][3] = fmaf(coef, bb.w, nvv[s][3]);
-          }
-        }
-      }
-      cold_store<COLD, CS>(a, row, q, nvv);
+    for (int s = 0; s < CS; ++s) {
+      const f4 bb = *reinterpret_cast<const f4*>(bc + 32 * s);
+      nvv[s][0] = fmaf(coef, bb.x, nvv[s][0]);
+      nvv[s][1] = fmaf(coef, bb.y, nvv[s][1]);
+      nvv[s][2] = fmaf(coef, bb.z, nvv[s][2]);
+      nvv[s][3] = fmaf(coef, bb.w, nvv[s][3]);
     }
   }
+  cold_store<COLD, CS>(a, row, q, nvv);
   part = sum8(part);
-  if (q == 0) {
-    a.y[yrow] = fmaf(hd[HD_D], xp, part);
-    if (rx) rx[p] = d.xraw;  // ring append of x (tokens that do not flush)
+  if (q == 0) a.y[yrow] = fmaf(hd[HD_D], d.xp, part);
+}
+
+// Stage window tokens [k0, k0 + kn) of one head into LDS: sB[e][n] = B'_tok[K + n]
+// (when with_b) and sU[e][p] = w_tok x_tok[p]. Window token m - 1 is this token (B'
+// from the workspace, x from the inputs); token tok < m - 1 sits at ring position
+// c - m + tok (rb0 and rx0 point at the ring rows of window token 0). A thread issues
+// all R loads of a round before its LDS stores.
+template <int NC, int R>
+__device__ __forceinline__ void stage_window(float* sB, float* sU, int k0, int kn, int m, int P,
+                                             const float* rb0, const float* bcur, const uint16_t* rx0,
+                                             const uint16_t* xcur, const float* wgt, bool with_b, int tid,
+                                             int nthr) {
+  constexpr int NB4 = NC / 4;  // float4 per token of B'
+  const int P4 = P >> 2;        // 4 x bf16 per token of x
+  const int nb = with_b ? kn * NB4 : 0, tot = nb + kn * P4;
+  for (int base = 0; base < tot; base += R * nthr) {
+    f4 vb[R];
+    u2v vx[R];
+    float wv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int i = base + tid + r * nthr;
+      if (i < nb) {
+        const int e = i / NB4, tok = k0 + e;
+        const float* src = tok < m - 1 ? rb0 + (size_t)tok * NC : bcur;
+        vb[r] = *reinterpret_cast<const f4*>(src + 4 * (i - e * NB4));
+      } else if (i < tot) {
+        const int j = i - nb, e = j / P4, tok = k0 + e;
+        const uint16_t* src = tok < m - 1 ? rx0 + (size_t)tok * P : xcur;
+        vx[r] = *reinterpret_cast<const u2v*>(src + 4 * (j - e * P4));
+        wv[r] = wgt[tok];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int i = base + tid + r * nthr;
+      if (i < nb) {
+        *reinterpret_cast<f4*>(sB + 4 * i) = vb[r];
+      } else if (i < tot) {
+        const u2v v = vx[r];
+        f4 u;
+        u.x = wv[r] * __uint_as_float(v.x << 16);
+        u.y = wv[r] * __uint_as_float(v.x & 0xffff0000u);
+        u.z = wv[r] * __uint_as_float(v.y << 16);
+        u.w = wv[r] * __uint_as_float(v.y & 0xffff0000u);
+        *reinterpret_cast<f4*>(sU + 4 * (i - nb)) = u;
+      }
+    }
   }
 }
 
-// one workgroup per (request, block of hpw heads of one group)
-template <int K, int COLD>
+
+// The units of one workgroup, U per wave in flight (all their loads issued before any
+// compute). MIXED: some head of the block flushes at this token, so each unit checks
+// its head's flag (a flushing head's cold columns are neither read nor appended to).
+template <int K, int COLD, bool MIXED>
+__device__ __forceinline__ void stream_units(const StepArgs& a, int slot, int bi, int h0, int units, int RG, int wave,
+                                             int nw, int q, int rr, const float* __restrict__ hdb,
+                                             const float (&Bh)[K / 32][4], const float (&Ch)[K / 32][4],
+                                             const float (&Cc)[Cfg<K, COLD>::CSR][4],
+                                             const float (&Cq)[Cfg<K, COLD>::CWR]) {
+  constexpr bool TIERED = Cfg<K, COLD>::TIERED;
+  constexpr int U = NSSM_UNROLL;
+  const int H = a.H, P = a.P, c = a.c;
+  for (int u0 = wave; u0 < units; u0 += U * nw) {
+    UnitRaw<K, COLD> d[U];
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      const int u = u0 + i * nw;
+      if (u < units) {
+        const int j = u / RG;
+        const int p = (u - j * RG) * 8 + rr;
+        const bool flushing = MIXED && hdb[j * HD_STRIDE + HD_FLUSH] != 0.f;
+        unit_load<K, COLD>(a, ((size_t)slot * H + h0 + j) * P + p, ((size_t)bi * H + h0 + j) * P + p, q, d[i],
+                           flushing);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      const int u = u0 + i * nw;
+      if (u < units) {
+        const int j = u / RG;
+        const int p = (u - j * RG) * 8 + rr;
+        const float* hd = hdb + j * HD_STRIDE;
+        const bool flushing = MIXED && hd[HD_FLUSH] != 0.f;
+        uint16_t* rx = nullptr;
+        if constexpr (TIERED) {
+          if (!flushing) rx = a.ring_x + (((size_t)slot * H + h0 + j) * c + (int)hd[HD_POS]) * P;
+        }
+        unit_compute<K, COLD>(a, ((size_t)slot * H + h0 + j) * P + p, ((size_t)bi * H + h0 + j) * P + p, p, q,
+                              d[i], rx, !flushing, hd, Bh, Ch, Cc, Cq);
+      }
+    }
+  }
+}
+
+// one workgroup per (request, block of hpw heads of one group). FUSED (short windows):
+// a flushing head's cold columns are flushed here; otherwise by the flush kernel.
+template <int K, int COLD, bool FUSED>
 __global__ void __launch_bounds__(kMaxWaves * 64) stream_kernel(StepArgs a) {
-  constexpr int HS = K / 32;
-  constexpr int NC = kN - K;
-  constexpr int CS = UnitRaw<K, COLD>::CS;
-  constexpr int CSR = CS > 0 ? CS : 1;
-  constexpr bool TIERED = CS > 0;  // a cold tier with ring and flushes
-  extern __shared__ float lds[];
+  using C = Cfg<K, COLD>;
+  constexpr int HS = C::HS, CS = C::CS, CSR = C::CSR, CWR = C::CWR;
+  constexpr bool TIERED = C::TIERED;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
   const int hb = blockIdx.x % a.nhb, bi = blockIdx.x / a.nhb;
@@ -521,7 +688,7 @@ __global__ void __launch_bounds__(kMaxWaves * 64) stream_kernel(StepArgs a) {
   // per-lane coefficients of group g (rotated by the prep kernel)
   const float* wB = ws.B + ((size_t)bi * a.G + g) * kN;
   const float* wC = ws.C + ((size_t)bi * a.G + g) * kN;
-  float Bh[HS][4], Ch[HS][4], Cc[CSR][4];
+  float Bh[HS][4], Ch[HS][4], Cc[CSR][4], Cq[CWR];
 #pragma unroll
   for (int s = 0; s < HS; ++s) {
     const f4 tb = *reinterpret_cast<const f4*>(wB + 32 * s + 4 * q);
@@ -531,115 +698,50 @@ __global__ void __launch_bounds__(kMaxWaves * 64) stream_kernel(StepArgs a) {
   }
 #pragma unroll
   for (int s = 0; s < CSR; ++s) {
-    if constexpr (CS > 0) {
+    if constexpr (COLD == NSSM_COLD_FP32 && CS > 0) {
       const f4 tc = *reinterpret_cast<const f4*>(wC + K + 32 * s + 4 * q);
       Cc[s][0] = tc.x; Cc[s][1] = tc.y; Cc[s][2] = tc.z; Cc[s][3] = tc.w;
     } else {
       Cc[s][0] = Cc[s][1] = Cc[s][2] = Cc[s][3] = 0.f;
     }
   }
+#pragma unroll
+  for (int i = 0; i < CWR; ++i) {
+    if constexpr (COLD == NSSM_COLD_FP8 || COLD == NSSM_COLD_BF16) Cq[i] = wC[K + C::CW * q + i];
+    else Cq[i] = 0.f;
+  }
 
   const float* hdb = ws.hd + ((size_t)bi * H + h0) * HD_STRIDE;
   const int RG = P >> 3;
   const int units = hpw * RG;
-  bool flush = false;
+  bool any_flush = false;
   if constexpr (TIERED) {
-    for (int j = 0; j < hpw; ++j) flush |= hdb[j * HD_STRIDE + HD_FLUSH] != 0.f;
+    for (int j = 0; j < hpw; ++j) any_flush |= hdb[j * HD_STRIDE + HD_FLUSH] != 0.f;
   }
-
-  if (!flush) {
-    // U units per wave in flight: all their loads are issued before any compute
-    constexpr int U = NSSM_UNROLL;
-    for (int u0 = wave; u0 < units; u0 += U * nw) {
-      UnitRaw<K, COLD> d[U];
-#pragma unroll
-      for (int i = 0; i < U; ++i) {
-        const int u = u0 + i * nw;
-        if (u < units) {
-          const int j = u / RG;
-          const int p = (u - j * RG) * 8 + rr;
-          unit_load<K, COLD>(a, ((size_t)slot * H + h0 + j) * P + p, ((size_t)bi * H + h0 + j) * P + p, q, d[i]);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < U; ++i) {
-        const int u = u0 + i * nw;
-        if (u < units) {
-          const int j = u / RG;
-          const int p = (u - j * RG) * 8 + rr;
-          const float* hd = hdb + j * HD_STRIDE;
-          uint16_t* rx = nullptr;
-          if constexpr (TIERED) rx = a.ring_x + (((size_t)slot * H + h0 + j) * c + (int)hd[HD_POS]) * P;
-          unit_compute<K, COLD, false>(a, ((size_t)slot * H + h0 + j) * P + p, ((size_t)bi * H + h0 + j) * P + p,
-                                       p, q, d[i], rx, hd, Bh, Ch, Cc, nullptr, nullptr, 0);
-        }
-      }
-    }
+  if (!any_flush) {
+    stream_units<K, COLD, false>(a, slot, bi, h0, units, RG, wave, nw, q, rr, hdb, Bh, Ch, Cc, Cq);
+  } else if constexpr (TIERED && !FUSED) {
+    stream_units<K, COLD, true>(a, slot, bi, h0, units, RG, wave, nw, q, rr, hdb, Bh, Ch, Cc, Cq);
   } else if constexpr (TIERED) {
-    // the first unit's state loads go out before the window staging
+    extern __shared__ float lds[];
+    constexpr int NC = C::NC;
+    // the first unit's loads go out before the window staging
     UnitRaw<K, COLD> dcur;
     if (wave < units) {
       const int j = wave / RG, p = (wave - j * RG) * 8 + rr;
       unit_load<K, COLD>(a, ((size_t)slot * H + h0 + j) * P + p, ((size_t)bi * H + h0 + j) * P + p, q, dcur);
     }
-    // stage the flush window, tokens i = 0..m-1 (the last is this token):
-    // rotated B cold columns of the group and w_i dt_i x_i of each head; the
-    // buffered tokens sit at ring positions [c-m, c-1)
+    // the window of every head of the block: B' cold columns of the group and
+    // w_i x_i of each head (all heads of a slot share t, so they share m)
     const int m = min(max((int)hdb[HD_M], 1), c);
+    const size_t rb = ((size_t)slot * a.G + g) * c + (c - m);
     float* sBc = lds;          // [m][NC]
     float* sU = lds + c * NC;  // [hpw][m][P]
-    const size_t rb = ((size_t)slot * a.G + g) * c + (c - m);
-    for (int i = tid; i < m * NC; i += blockDim.x) {
-      const int e = i / NC, n = i - e * NC;
-      sBc[i] = e < m - 1 ? a.ring_b[rb * NC + i] : wB[K + n];
-    }
-    for (int i = tid; i < hpw * m * P; i += blockDim.x) {
-      const int j = i / (m * P), r = i - j * m * P, e = r / P, p = r - e * P;
-      const uint16_t xv = e < m - 1 ? a.ring_x[(((size_t)slot * H + h0 + j) * c + (c - m + e)) * P + p]
-                                    : a.x[((size_t)bi * H + h0 + j) * P + p];
-      sU[i] = ws.w[((size_t)bi * H + h0 + j) * c + e] * bf2f(xv);
-    }
+    for (int j = 0; j < hpw; ++j)
+      stage_window<NC, 2>(sBc, sU + (size_t)j * m * P, 0, m, m, P, a.ring_b + rb * NC, wB + K,
+                          a.ring_x + (((size_t)slot * H + h0 + j) * c + (c - m)) * P, a.x + ((size_t)bi * H + h0 + j) * P,
+                          ws.w + ((size_t)bi * H + h0 + j) * c, j == 0, tid, blockDim.x);
     __syncthreads();
-    // c >= 16: the window contraction Delta[p][n] = sum_i sU[i][p] sBc[i][n] runs on the
-    // matrix cores (v_mfma_f32_16x16x4_f32: A = sBc^T 16 n x 4 tokens, B = sU 4 tokens
-    // x 16 p, K = window tokens, zero past m). Each wave keeps up to kMfmaTiles 16 x 16
-    // output tiles in registers; after a barrier they go to LDS (rows of stride
-    // NC + 4, over the staging area) for the streaming-layout apply below.
-    const float* dS = nullptr;
-    constexpr int NT = NC / 16;
-    const int ntiles = (P / 16) * NT;
-    if (c >= 16 && hpw == 1 && ntiles <= nw * kMfmaTiles) {
-      const int li = lane & 15, lk = lane >> 4;
-      f4 acc[kMfmaTiles];
-#pragma unroll
-      for (int i = 0; i < kMfmaTiles; ++i) {
-        acc[i] = f4{0.f, 0.f, 0.f, 0.f};
-        const int tt = wave + i * nw;
-        if (tt < ntiles) {
-          const int pt = tt / NT, nt = tt - pt * NT;
-          for (int k0 = 0; k0 < m; k0 += 4) {
-            const int kk = k0 + lk;
-            const int kc = kk < m ? kk : m - 1;
-            float av = sBc[kc * NC + nt * 16 + li];
-            float bv = sU[kc * P + pt * 16 + li];
-            if (kk >= m) av = bv = 0.f;
-            acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[i], 0, 0, 0);
-          }
-        }
-      }
-      __syncthreads();  // every wave is done reading sBc / sU
-      float* dW = lds;  // [P][NC + 4]
-#pragma unroll
-      for (int i = 0; i < kMfmaTiles; ++i) {
-        const int tt = wave + i * nw;
-        if (tt < ntiles) {  // lane holds Delta[p0 + li][n0 + 4 lk .. +3]
-          const int pt = tt / NT, nt = tt - pt * NT;
-          *reinterpret_cast<f4*>(dW + (pt * 16 + li) * (NC + 4) + nt * 16 + 4 * lk) = acc[i];
-        }
-      }
-      __syncthreads();
-      dS = dW;
-    }
     // software pipeline: the next unit's loads are in flight during this one's compute
     for (int u = wave; u < units; u += nw) {
       UnitRaw<K, COLD> dnext;
@@ -654,14 +756,228 @@ __global__ void __launch_bounds__(kMaxWaves * 64) stream_kernel(StepArgs a) {
       const size_t yrow = ((size_t)bi * H + h0 + j) * P + p;
       const float* hd = hdb + j * HD_STRIDE;
       if (hd[HD_FLUSH] != 0.f) {
-        unit_compute<K, COLD, true>(a, row, yrow, p, q, dcur, nullptr, hd, Bh, Ch, Cc, sU + (size_t)j * m * P, sBc,
-                                    m, dS);
+        unit_compute_flush<K, COLD>(a, row, yrow, p, q, dcur, hd, Bh, Ch, Cc, Cq, sU + (size_t)j * m * P, sBc, m);
       } else {
         uint16_t* rx = a.ring_x + (((size_t)slot * H + h0 + j) * c + (int)hd[HD_POS]) * P;
-        unit_compute<K, COLD, false>(a, row, yrow, p, q, dcur, rx, hd, Bh, Ch, Cc, nullptr, nullptr, 0);
+        unit_compute<K, COLD>(a, row, yrow, p, q, dcur, rx, true, hd, Bh, Ch, Cc, Cq);
       }
       dcur = dnext;
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// flush: the cold tier of every (request, head) whose phase wraps at this token.
+// A workgroup walks a strided set of items and takes the flushing ones. Per item:
+//   cold <- exp(sum a) cold + Delta,  Delta[p][n] = sum_i w_i x_i[p] B'_i[n]
+// over the window (the buffered tokens and this one), scale/v4_fused_decode.py:76-85,
+// and y += exp(glog) (stale read copy . C'[K:]) — the stream kernel wrote the hot part
+// and D x of these heads' y and left their cold columns alone.
+//
+// Delta is contracted on the matrix cores as 16 x 16 tiles (p-tile pt, n-tile nt) of
+// v_mfma_f32_16x16x4_f32: A = B'^T (16 n x 4 tokens), B = w x (4 tokens x 16 p), the
+// window staged in LDS in chunks of 16 tokens (zero past its end). Lane (li, lk) of a
+// tile holds Delta[pt*16 + li][nt*16 + 4 lk .. +3]; the state is read and written in
+// that mapping. Each wave holds kMfmaTiles tiles, in pairs that cover whole 128-byte
+// row segments (flush_tile); a pass covers as many tiles as the waves hold, for e4m3
+// whole rows only (the row scale needs all of a row's tiles). When an item takes one
+// pass, the next item's state tiles are loaded while this one contracts and stores.
+// Per-tile readout partials and row maxima go through LDS and are summed in a fixed
+// order.
+constexpr int kFlushWaves = 8;
+constexpr int kFlushGrid = 2048;  // workgroups of a flush launch (at most)
+
+
+template <int K, int COLD>
+__global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
+  using C = Cfg<K, COLD>;
+  constexpr int NC = C::NC, NT = C::NT, nw = kFlushWaves;
+  constexpr int TPP = COLD == NSSM_COLD_FP8 ? (nw * kMfmaTiles / NT) * NT : nw * kMfmaTiles;  // tiles per pass
+  static_assert(TPP >= NT, "a pass must hold a whole row");
+  extern __shared__ float lds[];
+  // the round's flushing items and their scalars (loaded in parallel by the thread
+  // that finds the item)
+  __shared__ int sItem[kFlushWaves * 64], sSlot[kFlushWaves * 64], sM[kFlushWaves * 64];
+  __shared__ float sDtot[kFlushWaves * 64], sEg[kFlushWaves * 64];
+  __shared__ int sCount;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, lk = lane >> 4;
+  const int H = a.H, P = a.P, c = a.c;
+  const int items = a.b * H;
+  const Ws ws(a.ws, a.b, H, a.G, c);
+  float* sBc = lds;              // [16][NC]
+  float* sU = sBc + 16 * NC;     // [16][P]
+  float* sPart = sU + 16 * P;    // [P][NT] readout partials of the old read copy
+  float* sAmx = sPart + P * NT;  // [P][NT] row maxima of the new values (e4m3 only)
+  const int ntot = (P / 16) * NT;
+
+  for (int r0 = blockIdx.x; r0 < items; r0 += gridDim.x * blockDim.x) {
+    // this round's items: r0 + tid * gridDim.x; keep the flushing ones
+    if (tid == 0) sCount = 0;
+    __syncthreads();
+    {
+      const int it = r0 + tid * gridDim.x;
+      if (it < items) {
+        const int bi = it / H;
+        const int slot = a.slot_ids ? a.slot_ids[bi] : bi;
+        const float* hd = ws.hd + (size_t)it * HD_STRIDE;
+        const float fl = hd[HD_FLUSH], mm = hd[HD_M], dt = hd[HD_DTOT], eg = hd[HD_EG];
+        if (slot >= 0 && slot < a.slots && fl != 0.f) {
+          const int k = atomicAdd(&sCount, 1);
+          sItem[k] = it;
+          sSlot[k] = slot;
+          sM[k] = min(max((int)mm, 1), c);
+          sDtot[k] = dt;
+          sEg[k] = eg;
+        }
+      }
+    }
+    __syncthreads();
+    const int n_items = sCount;
+    for (int k = 0; k < n_items; ++k) {
+      const int it = sItem[k], slot = sSlot[k], m = sM[k];
+      const float dtot = sDtot[k], eg = sEg[k];
+      const int bi = it / H, h = it - bi * H, g = h / a.HG;
+      float yv = 0.f;  // this head's y (hot part and D x, from the stream kernel)
+      if (tid < P) yv = a.y[(size_t)it * P + tid];
+      const float* bcur = ws.B + ((size_t)bi * a.G + g) * kN + K;  // this token's B'[K:]
+      const float* cq0 = ws.C + ((size_t)bi * a.G + g) * kN + K;   // C'[K:]
+      const float* rb0 = a.ring_b + (((size_t)slot * a.G + g) * c + (c - m)) * NC;
+      const uint16_t* rx0 = a.ring_x + (((size_t)slot * H + h) * c + (c - m)) * P;
+      const uint16_t* xcur = a.x + (size_t)it * P;
+      const float* wgt = ws.w + (size_t)it * c;
+      const size_t row0 = ((size_t)slot * H + h) * P;
+      const float* src = COLD == NSSM_COLD_FP32 ? static_cast<const float*>(a.cold) : a.master;
+
+      for (int t0 = 0; t0 < ntot; t0 += TPP) {
+        const int ntile = min(TPP, ntot - t0);
+        // the pass's state tiles are loaded before the window work
+        f4 old[kMfmaTiles];
+        u2v rb16[COLD == NSSM_COLD_BF16 ? kMfmaTiles : 1];
+        uint32_t r8[COLD == NSSM_COLD_FP8 ? kMfmaTiles : 1];
+        float rsc[COLD == NSSM_COLD_FP8 ? kMfmaTiles : 1];
+#pragma unroll
+        for (int i = 0; i < kMfmaTiles; ++i) {
+          const int tt = t0 + wave + i * nw;
+          if (wave + i * nw < ntile) {
+            const size_t row = row0 + (tt / NT) * 16 + li;
+            const int col = (tt % NT) * 16 + 4 * lk;
+            old[i] = ld_stream(reinterpret_cast<const f4*>(src + row * NC + col));
+            if constexpr (COLD == NSSM_COLD_BF16)
+              rb16[i] = ld_stream(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.cold) + row * NC + col));
+            if constexpr (COLD == NSSM_COLD_FP8) {
+              r8[i] = ld_stream(reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(a.cold) + row * NC + col));
+              rsc[i] = a.scale[row];
+            }
+          }
+        }
+        f4 acc[kMfmaTiles];
+#pragma unroll
+        for (int i = 0; i < kMfmaTiles; ++i) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
+        for (int k0 = 0; k0 < m; k0 += 16) {
+          const int kn = min(16, m - k0);
+          __syncthreads();  // the previous chunk (or item) is consumed
+          stage_window<NC, 2>(sBc, sU, k0, kn, m, P, rb0, bcur, rx0, xcur, wgt, true, tid, blockDim.x);
+          __syncthreads();
+#pragma unroll
+          for (int i = 0; i < kMfmaTiles; ++i) {
+            if (wave + i * nw < ntile) {  // wave-uniform
+              const int tt = t0 + wave + i * nw;
+              const int pt = tt / NT, nt = tt % NT;
+              for (int kk0 = 0; kk0 < kn; kk0 += 4) {
+                const int kk = kk0 + lk;
+                const int kc = kk < kn ? kk : kn - 1;
+                float av = sBc[kc * NC + nt * 16 + li];
+                float bv = sU[kc * P + pt * 16 + li];
+                if (kk >= kn) av = bv = 0.f;
+                acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[i], 0, 0, 0);
+              }
+            }
+          }
+        }
+        // new = total decay x old + Delta; readout partial of the old read copy
+#pragma unroll
+        for (int i = 0; i < kMfmaTiles; ++i) {
+          if (wave + i * nw < ntile) {
+            const int tt = t0 + wave + i * nw;
+            const int pt = tt / NT, nt = tt % NT;
+            const int p = pt * 16 + li, col = nt * 16 + 4 * lk;
+            const size_t row = row0 + p;
+            const f4 cq = *reinterpret_cast<const f4*>(cq0 + col);
+            float rd[4];
+            float rscale = 1.f;
+            if constexpr (COLD == NSSM_COLD_FP32) {
+              rd[0] = old[i].x; rd[1] = old[i].y; rd[2] = old[i].z; rd[3] = old[i].w;
+            } else if constexpr (COLD == NSSM_COLD_BF16) {
+              rd[0] = __uint_as_float(rb16[i].x << 16); rd[1] = __uint_as_float(rb16[i].x & 0xffff0000u);
+              rd[2] = __uint_as_float(rb16[i].y << 16); rd[3] = __uint_as_float(rb16[i].y & 0xffff0000u);
+            } else {
+              fp8x4_to_f32(r8[i], rd);
+              rscale = rsc[i];
+            }
+            float pc = rd[0] * cq.x;
+            pc = fmaf(rd[1], cq.y, pc);
+            pc = fmaf(rd[2], cq.z, pc);
+            pc = fmaf(rd[3], cq.w, pc);
+            pc += __shfl_xor(pc, 16);
+            pc += __shfl_xor(pc, 32);
+            f4 nv = acc[i];
+            nv.x = fmaf(dtot, old[i].x, nv.x);
+            nv.y = fmaf(dtot, old[i].y, nv.y);
+            nv.z = fmaf(dtot, old[i].z, nv.z);
+            nv.w = fmaf(dtot, old[i].w, nv.w);
+            acc[i] = nv;
+            if constexpr (COLD == NSSM_COLD_FP32) {
+              st_stream(nv, reinterpret_cast<f4*>(static_cast<float*>(a.cold) + row * NC + col));
+            } else {
+              st_stream(nv, reinterpret_cast<f4*>(a.master + row * NC + col));
+            }
+            if constexpr (COLD == NSSM_COLD_BF16) {
+              u2v t;
+              t.x = (uint32_t)nssm_f32_to_bf16(nv.x) | ((uint32_t)nssm_f32_to_bf16(nv.y) << 16);
+              t.y = (uint32_t)nssm_f32_to_bf16(nv.z) | ((uint32_t)nssm_f32_to_bf16(nv.w) << 16);
+              st_stream(t, reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.cold) + row * NC + col));
+            }
+            if (lk == 0) sPart[p * NT + nt] = pc * rscale;
+            if constexpr (COLD == NSSM_COLD_FP8) {
+              float am = fmaxf(fmaxf(fabsf(nv.x), fabsf(nv.y)), fmaxf(fabsf(nv.z), fabsf(nv.w)));
+              am = fmaxf(am, __shfl_xor(am, 16));
+              am = fmaxf(am, __shfl_xor(am, 32));
+              if (lk == 0) sAmx[p * NT + nt] = am;
+            }
+          }
+        }
+        __syncthreads();  // partials and row maxima of this pass's tiles
+        if constexpr (COLD == NSSM_COLD_FP8) {
+#pragma unroll
+          for (int i = 0; i < kMfmaTiles; ++i) {
+            if (wave + i * nw < ntile) {
+              const int tt = t0 + wave + i * nw;
+              const int pt = tt / NT, nt = tt % NT;
+              const int p = pt * 16 + li;
+              const size_t row = row0 + p;
+              float am = 0.f;
+#pragma unroll
+              for (int t2 = 0; t2 < NT; ++t2) am = fmaxf(am, sAmx[p * NT + t2]);
+              const float sc = am / 448.0f + 1e-12f;  // scale/vllm_v4_patch.py:106-111
+              const f4 nv = acc[i];
+              st_stream(f32x4_to_fp8(nv.x / sc, nv.y / sc, nv.z / sc, nv.w / sc),
+                        reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.cold) + row * NC + nt * 16 + 4 * lk));
+              if (nt == 0 && lk == 0) a.scale[row] = sc;
+            }
+          }
+        }
+      }
+      // y += exp(glog) (stale cold readout); the next item's first barrier orders
+      // these reads before sPart is written again
+      if (tid < P) {
+        float pc = 0.f;
+#pragma unroll
+        for (int t2 = 0; t2 < NT; ++t2) pc += sPart[tid * NT + t2];
+        a.y[(size_t)it * P + tid] = fmaf(eg, pc, yv);
+      }
+    }
+    __syncthreads();  // sItem and sCount are rewritten by the next round
   }
 }
 
@@ -788,10 +1104,11 @@ int g_hpw_override = 0, g_waves_override = 0;
 constexpr size_t kMaxLds = 64 * 1024;
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+bool aligned8(const void* p) { return ((uintptr_t)p & 7u) == 0; }
 
 int check_params(const nssm_layer_params* prm) {
   if (!prm || !prm->dt_bias || !prm->A || !prm->D) return NSSM_E_NULL;
-  if (prm->N != kN || prm->H <= 0 || prm->G <= 0 || prm->H % prm->G || prm->H / prm->G > 64) return NSSM_E_DIMS;
+  if (prm->N != kN || prm->H <= 0 || prm->G <= 0 || prm->H % prm->G || prm->H / prm->G > kMaxHG) return NSSM_E_DIMS;
   if (prm->P <= 0 || prm->P % 16 || prm->P > 256) return NSSM_E_DIMS;
   if (prm->R && !aligned16(prm->R)) return NSSM_E_ALIGN;
   return NSSM_OK;
@@ -800,6 +1117,7 @@ int check_params(const nssm_layer_params* prm) {
 int check_inputs(const nssm_step_inputs* in, const float* y) {
   if (!in || !in->x || !in->B || !in->C || !in->dt || !y) return NSSM_E_NULL;
   if (in->b < 0) return NSSM_E_DIMS;
+  if (!aligned8(in->x)) return NSSM_E_ALIGN;
   return NSSM_OK;
 }
 
@@ -817,16 +1135,31 @@ int divisor_at_most(int n, int cap) {
   return 1;
 }
 
-size_t stream_lds_bytes(int hpw, int P, int c, int K, int kind = NSSM_COLD_FP32) {
+// flush kernel LDS: 16-token window chunk, per-tile readout partials (+ e4m3 row maxima)
+size_t flush_lds_bytes(int P, int K, int kind) {
   const int NC = kN - K;
-  if (NC <= 0 || kind == NSSM_COLD_NONE) return 0;
-  size_t fl = (size_t)c * NC + (size_t)hpw * c * P;  // window staging
-  if (c >= 16 && hpw == 1) fl = fl > (size_t)P * (NC + 4) ? fl : (size_t)P * (NC + 4);  // MFMA exchange
-  return fl * sizeof(float);
+  const size_t tiles = (size_t)P * (NC / 16);
+  return ((size_t)16 * NC + (size_t)16 * P + tiles * (kind == NSSM_COLD_FP8 ? 2 : 1)) * sizeof(float);
+}
+
+// windows shorter than this are flushed by the stream kernel (VALU replay of the window
+// staged in LDS); longer ones by the flush kernel (matrix cores). Measured on MI355X at
+// the 9B shape, B = 256, 27 layers, fp32 / bf16 / e4m3 cold, ms per step:
+//   c =  4  fused  9.4 / 10.2 / 8.2   split 11.6 / 12.3 / 11.4
+//   c = 16  fused  8.6 /  8.0 / 6.3   split  9.0 /  8.1 /  7.0
+//   c = 32  fused  8.5 /  7.7 / 6.0   split  8.7 /  7.4 /  6.3
+//   c = 64  fused  9.3 /  8.6 / 7.4   split  8.5 /  7.2 /  6.0
+constexpr int kFuseMaxC = 33;
+
+// stream kernel LDS: the whole window of the block's heads when it flushes (fused)
+size_t fused_lds_bytes(int hpw, int P, int c, int K) {
+  return ((size_t)c * (kN - K) + (size_t)hpw * c * P) * sizeof(float);
 }
 
 struct Launch {
   int hpw, waves;
+  bool fused;
+  size_t lds;
 };
 
 int pick_launch(int H, int G, int P, int K, int c, Launch* out, int kind = NSSM_COLD_FP32) {
@@ -836,16 +1169,21 @@ int pick_launch(int H, int G, int P, int K, int c, Launch* out, int kind = NSSM_
     if (HG % g_hpw_override) return NSSM_E_TUNING;
     hpw = g_hpw_override;
   }
-  while (hpw > 1 && stream_lds_bytes(hpw, P, c, K, kind) > kMaxLds) hpw = divisor_at_most(HG, hpw - 1);
-  if (stream_lds_bytes(hpw, P, c, K, kind) > kMaxLds) return NSSM_E_DIMS;
+  const bool tiered = K < kN && kind != NSSM_COLD_NONE;
+  const bool fused = tiered && c < kFuseMaxC;
+  while (fused && hpw > 1 && fused_lds_bytes(hpw, P, c, K) > kMaxLds) hpw = divisor_at_most(HG, hpw - 1);
   // measured on MI355X at the 9B shape (P = 80): the untiered stream runs best
   // with two units per wave (5 waves per head), the tiered one with 4 waves
   const int waves = g_waves_override > 0 ? g_waves_override
                     : K < kN && kind != NSSM_COLD_NONE ? (hpw * RG < 4 ? hpw * RG : 4)
                                          : divisor_at_most(hpw * RG, 5);
   if (waves > kMaxWaves) return NSSM_E_TUNING;
+  const size_t lds = fused ? fused_lds_bytes(hpw, P, c, K) : 0;
+  if (lds > kMaxLds || (tiered && !fused && flush_lds_bytes(P, K, kind) > kMaxLds)) return NSSM_E_DIMS;
   out->hpw = hpw;
   out->waves = waves;
+  out->fused = fused;
+  out->lds = lds;
   return NSSM_OK;
 }
 
@@ -881,6 +1219,7 @@ int check_tier(const nssm_tier* tr, bool need_ring) {
   if (tr->k_hot != 32 && tr->k_hot != 64 && tr->k_hot != 96) return NSSM_E_DIMS;
   if (!aligned16(tr->hot) || (cold && !aligned16(tr->cold)) || (tr->master && !aligned16(tr->master)))
     return NSSM_E_ALIGN;
+  if (cold && need_ring && (!aligned8(tr->ring_x) || !aligned16(tr->ring_b))) return NSSM_E_ALIGN;
   return NSSM_OK;
 }
 
@@ -901,22 +1240,32 @@ void fill_tier(StepArgs& a, const nssm_tier* tr) {
 }
 
 template <int K, int COLD>
-int launch_pair(const StepArgs& a, int waves, hipStream_t st) {
+int launch_pair(const StepArgs& a, const Launch& L, hipStream_t st) {
   constexpr bool TIERED = K < kN && COLD != NSSM_COLD_NONE;
   if (a.b == 0) return NSSM_OK;
   hipLaunchKernelGGL((prep_kernel<TIERED>), dim3((unsigned)a.b * a.G), dim3(kPrepThreads), 0, st, a);
-  hipLaunchKernelGGL((stream_kernel<K, COLD>), dim3((unsigned)a.b * a.nhb), dim3(waves * 64),
-                     stream_lds_bytes(a.hpw, a.P, a.c, K, COLD), st, a);
+  if (L.fused) {
+    if constexpr (TIERED)
+      hipLaunchKernelGGL((stream_kernel<K, COLD, true>), dim3((unsigned)a.b * a.nhb), dim3(L.waves * 64), L.lds, st, a);
+    return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
+  }
+  hipLaunchKernelGGL((stream_kernel<K, COLD, false>), dim3((unsigned)a.b * a.nhb), dim3(L.waves * 64), 0, st, a);
+  if constexpr (TIERED) {
+    const int items = a.b * a.H;
+    const int grid = items < kFlushGrid ? items : kFlushGrid;
+    hipLaunchKernelGGL((flush_kernel<K, COLD>), dim3((unsigned)grid), dim3(kFlushWaves * 64),
+                       flush_lds_bytes(a.P, K, COLD), st, a);
+  }
   return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
 }
 
 template <int K>
-int dispatch_kind(const StepArgs& a, int kind, int waves, hipStream_t st) {
+int dispatch_kind(const StepArgs& a, int kind, const Launch& L, hipStream_t st) {
   switch (kind) {
-    case NSSM_COLD_FP32: return launch_pair<K, NSSM_COLD_FP32>(a, waves, st);
-    case NSSM_COLD_BF16: return launch_pair<K, NSSM_COLD_BF16>(a, waves, st);
-    case NSSM_COLD_FP8: return launch_pair<K, NSSM_COLD_FP8>(a, waves, st);
-    case NSSM_COLD_NONE: return launch_pair<K, NSSM_COLD_NONE>(a, waves, st);
+    case NSSM_COLD_FP32: return launch_pair<K, NSSM_COLD_FP32>(a, L, st);
+    case NSSM_COLD_BF16: return launch_pair<K, NSSM_COLD_BF16>(a, L, st);
+    case NSSM_COLD_FP8: return launch_pair<K, NSSM_COLD_FP8>(a, L, st);
+    case NSSM_COLD_NONE: return launch_pair<K, NSSM_COLD_NONE>(a, L, st);
   }
   return NSSM_E_KIND;
 }
@@ -933,7 +1282,7 @@ const char* nssm_strerror(int code) {
     case NSSM_OK: return "ok";
     case NSSM_E_NULL: return "a required pointer is NULL";
     case NSSM_E_DIMS: return "sizes out of the supported range";
-    case NSSM_E_ALIGN: return "a state, parameter or workspace pointer is not 16-byte aligned";
+    case NSSM_E_ALIGN: return "a pointer is not aligned as required (state, parameters, workspace, ring_b: 16 bytes; x, ring_x: 8)";
     case NSSM_E_KIND: return "unknown cold storage kind";
     case NSSM_E_LAUNCH: return "HIP kernel launch failed";
     case NSSM_E_TUNING: return "launch override does not fit the dimensions";
@@ -996,7 +1345,7 @@ int nssm_fresh_step(const nssm_layer_params* prm, float* state, int32_t slots, c
   if ((rc = pick_launch(prm->H, prm->G, prm->P, kN, 0, &L))) return rc;
   a.hpw = L.hpw;
   a.nhb = prm->H / L.hpw;
-  return launch_pair<kN, NSSM_COLD_FP32>(a, L.waves, (hipStream_t)stream);
+  return launch_pair<kN, NSSM_COLD_FP32>(a, L, (hipStream_t)stream);
 }
 
 int nssm_v4_step(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step_inputs* in, float* y,
@@ -1016,9 +1365,9 @@ int nssm_v4_step(const nssm_layer_params* prm, const nssm_tier* tier, const nssm
   a.nhb = prm->H / L.hpw;
   hipStream_t st = (hipStream_t)stream;
   switch (tier->k_hot) {
-    case 32: return dispatch_kind<32>(a, tier->cold_kind, L.waves, st);
-    case 64: return dispatch_kind<64>(a, tier->cold_kind, L.waves, st);
-    case 96: return dispatch_kind<96>(a, tier->cold_kind, L.waves, st);
+    case 32: return dispatch_kind<32>(a, tier->cold_kind, L, st);
+    case 64: return dispatch_kind<64>(a, tier->cold_kind, L, st);
+    case 96: return dispatch_kind<96>(a, tier->cold_kind, L, st);
   }
   return NSSM_E_DIMS;
 }
