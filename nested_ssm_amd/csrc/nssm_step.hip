@@ -62,6 +62,7 @@ struct StepArgs {
   float* y;
   float* ws;  // workspace (see Ws below)
   int32_t b, slots, H, P, G, HG, c, K, hpw, nhb;
+  int32_t prb;  // requests per prep workgroup
   float dt_min;
 };
 
@@ -86,7 +87,7 @@ __device__ __forceinline__ float dpp(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
 }
 // DPP controls: quad_perm [1,0,3,2] = 0xB1, quad_perm [2,3,0,1] = 0x4E,
-// row_half_mirror (lane i <-> 7-i within 8) = 0x141, row_mirror (within 16) = 0x140.
+// row_half_mirror (lane i <-> 7-i within 8) = 0x141.
 __device__ __forceinline__ float sum8(float v) {
   v += dpp<0xB1>(v);
   v += dpp<0x4E>(v);
@@ -97,14 +98,6 @@ __device__ __forceinline__ float max8(float v) {
   v = fmaxf(v, dpp<0xB1>(v));
   v = fmaxf(v, dpp<0x4E>(v));
   v = fmaxf(v, dpp<0x141>(v));
-  return v;
-}
-__device__ __forceinline__ float sum32(float v) {
-  v += dpp<0xB1>(v);
-  v += dpp<0x4E>(v);
-  v += dpp<0x141>(v);
-  v += dpp<0x140>(v);
-  v += __shfl_xor(v, 16);
   return v;
 }
 
@@ -135,46 +128,63 @@ __device__ __forceinline__ void st_stream(T v, T* p) {
 }
 
 // ---------------------------------------------------------------------------
-// prep: one workgroup (256 threads = 4 waves) per (request, group). Latency
-// bound: every independent global load is issued before the first barrier.
+// prep: one workgroup (256 threads) per (group g, block of prb <= 8 requests).
+//  * rotation: [B' C'] = R_g [B C] for the block, a 128 x 128 by 128 x 16 product on
+//    the matrix cores (v_mfma_f32_16x16x4_f32, fp32 products and sums): columns
+//    j < 8 are B of request j, j >= 8 C of request j - 8 (staged in LDS); wave w owns
+//    the output row tiles w and w + 4. A lane loads R as float4 (R[m][k..k+3]); the
+//    four MFMA steps of a 16-wide k block take the float4's elements in turn, and the
+//    B operand takes the same k order, so each step pairs equal k. The group's R is
+//    read once per block;
+//  * one thread per (request, head) of the block computes the head's dt, decay,
+//    stale-read factor, flush flag and, at a flush, the window weights; updates t,
+//    nv, glog; appends dt and (rotation lanes) the B' cold columns to the ring at
+//    position t % c. A flush token sits at c-1, so a flush window is always ring
+//    positions [c-m, c).
+// Latency bound: every independent global load is issued before the first barrier.
 constexpr int kPrepThreads = 256;
+constexpr int kPrepReq = 8;  // requests per prep workgroup (at most)
 
 template <bool TIERED>
 __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
-  constexpr int NW = kPrepThreads / 64;
-  constexpr int ROWS = kN / (2 * NW);  // rows of R per half-wave
-  constexpr int RB = ROWS / 2;         // rows per batch in flight
-  __shared__ float sBraw[kN], sCraw[kN], sBr[kN];
-  __shared__ float sRdt[TIERED ? kMaxHG * kMaxC : 1];  // window dt of flushing heads [HG][c]
-  __shared__ int sT[TIERED ? kMaxHG : 1], sNv[TIERED ? kMaxHG : 1];
-  __shared__ int sPos, sFlush;
+  __shared__ float sX[2 * kPrepReq][kN];  // B (j < 8) and C (j >= 8) of the block's requests
+  __shared__ int sSlot[kPrepReq], sTr[kPrepReq];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int g = blockIdx.x % a.G, bi = blockIdx.x / a.G;
-  const int H = a.H, HG = a.HG, c = a.c;
-  const int slot = a.slot_ids ? a.slot_ids[bi] : bi;
-  if (slot < 0 || slot >= a.slots) return;  // the stream kernel writes NaN rows for it
-  const Ws ws(a.ws, a.b, H, a.G, c);
-  const size_t bgo = ((size_t)bi * a.G + g) * kN;
-  const int hw = lane >> 5, hl = lane & 31;
-  const float* __restrict__ Rg = a.R ? a.R + (size_t)g * kN * kN : nullptr;
+  const int li = lane & 15, lk = lane >> 4;
+  const int G = a.G, H = a.H, HG = a.HG, c = a.c;
+  const int g = blockIdx.x % G, r0 = (blockIdx.x / G) * a.prb;
+  const int nreq = min(a.prb, a.b - r0);
+  const Ws ws(a.ws, a.b, H, G, c);
 
-  // 1. independent loads: first batch of R rows, B and C, the head's inputs
-  f4 r[RB];
+  // 1. independent loads: B and C of the block (zero past the last request), R, the
+  // head inputs
+  for (int i = tid; i < kPrepReq * kN; i += kPrepThreads) {
+    const int r = i / kN, n = i - r * kN;
+    float bv = 0.f, cv = 0.f;
+    if (r < nreq) {
+      const size_t o = ((size_t)(r0 + r) * G + g) * kN + n;
+      bv = bf2f(a.Bm[o]);
+      cv = bf2f(a.Cm[o]);
+    }
+    sX[r][n] = bv;
+    sX[kPrepReq + r][n] = cv;
+  }
+  const float* __restrict__ Rg = a.R ? a.R + (size_t)g * kN * kN : nullptr;
+  f4 ra[2][kN / 16];  // this lane's R operands of its two row tiles
   if (Rg) {
 #pragma unroll
-    for (int i = 0; i < RB; ++i)
-      r[i] = *reinterpret_cast<const f4*>(Rg + (size_t)(2 * wave + hw + 2 * NW * i) * kN + 4 * hl);
+    for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+      for (int kb = 0; kb < kN / 16; ++kb)
+        ra[t2][kb] = *reinterpret_cast<const f4*>(Rg + (size_t)((wave + 4 * t2) * 16 + li) * kN + kb * 16 + 4 * lk);
   }
-  if (tid < kN) {
-    sBraw[tid] = bf2f(a.Bm[bgo + tid]);
-    sCraw[tid] = bf2f(a.Cm[bgo + tid]);
-  }
-  const bool head_thread = tid < HG;
-  const int h = g * HG + tid;
-  const size_t o = (size_t)slot * H + h;
+  const int hr = tid / HG, hh = tid - hr * HG;  // the head thread's request and head
+  const bool head_thread = tid < nreq * HG;
+  const int h = g * HG + hh, bi = r0 + hr;
+  int slot = -1, tt = 0, nvv = 0;
   float draw = 0.f, dtb = 0.f, Ah = 0.f, Dh = 0.f, gl = 0.f;
-  int tt = 0, nvv = 0;
   if (head_thread) {
+    slot = a.slot_ids ? a.slot_ids[bi] : bi;
     draw = bf2f(a.dt_raw[(size_t)bi * H + h]);
     dtb = a.dt_bias[h];
     Ah = a.A[h];
@@ -182,67 +192,67 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
     if constexpr (TIERED) {
       // t >= 0 and 0 <= nv < c hold for every tier these kernels write; the
       // clamps keep ring indexing inside the buffers even for a corrupted phase
-      tt = max(a.t[o], 0);
-      nvv = min(max(a.nv[o], 0), c - 1);
-      gl = a.glog[o];
-      sT[tid] = tt;
-      sNv[tid] = nvv;
+      if (slot >= 0 && slot < a.slots) {
+        const size_t o = (size_t)slot * H + h;
+        tt = max(a.t[o], 0);
+        nvv = min(max(a.nv[o], 0), c - 1);
+        gl = a.glog[o];
+      }
+    }
+    if (hh == 0) {
+      sSlot[hr] = slot;
+      sTr[hr] = tt;
     }
   }
   __syncthreads();
 
-  // 1b. a flushing head's window dt (ring positions [c-1-nv, c-1)), loaded by all threads
-  if constexpr (TIERED) {
-#pragma unroll 4
-    for (int idx = tid; idx < HG * c; idx += kPrepThreads) {
-      const int hh = idx / c, i = idx - hh * c;
-      if ((sT[hh] + 1) % c == 0 && i >= c - 1 - sNv[hh] && i < c - 1)
-        sRdt[idx] = a.ring_dt[((size_t)slot * H + g * HG + hh) * c + i];
-    }
-  }
-
-  // 2. rotation: a half-wave per row of R (both halves see the same rows
-  // count, so every reduction runs with all lanes active)
+  // 2. rotation and its stores
   if (Rg) {
-    const f4 bv = *reinterpret_cast<const f4*>(sBraw + 4 * hl);
-    const f4 cv = *reinterpret_cast<const f4*>(sCraw + 4 * hl);
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      if (half == 1) {
+    for (int t2 = 0; t2 < 2; ++t2) {
+      f4 acc = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < RB; ++i)
-          r[i] = *reinterpret_cast<const f4*>(Rg + (size_t)(2 * wave + hw + 2 * NW * (RB + i)) * kN + 4 * hl);
+      for (int kb = 0; kb < kN / 16; ++kb) {
+        const f4 xb = *reinterpret_cast<const f4*>(&sX[li][kb * 16 + 4 * lk]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ra[t2][kb].x, xb.x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ra[t2][kb].y, xb.y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ra[t2][kb].z, xb.z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ra[t2][kb].w, xb.w, acc, 0, 0, 0);
       }
-#pragma unroll
-      for (int i = 0; i < RB; ++i) {
-        const int mrow = 2 * wave + hw + 2 * NW * (half * RB + i);
-        float db = r[i].x * bv.x;
-        db = fmaf(r[i].y, bv.y, db);
-        db = fmaf(r[i].z, bv.z, db);
-        db = fmaf(r[i].w, bv.w, db);
-        float dc = r[i].x * cv.x;
-        dc = fmaf(r[i].y, cv.y, dc);
-        dc = fmaf(r[i].z, cv.z, dc);
-        dc = fmaf(r[i].w, cv.w, dc);
-        db = sum32(db);
-        dc = sum32(dc);
-        if (hl == 0) {
-          sBr[mrow] = db;
-          ws.B[bgo + mrow] = db;
-          ws.C[bgo + mrow] = dc;
+      // lane (li, lk) holds rows m0 + 4 lk .. +3 of column li
+      const int m0 = (wave + 4 * t2) * 16 + 4 * lk;
+      const int r = li & (kPrepReq - 1), which = li >> 3;
+      const int sl = r < nreq ? sSlot[r] : -1;
+      if (sl >= 0 && sl < a.slots) {
+        *reinterpret_cast<f4*>((which ? ws.C : ws.B) + ((size_t)(r0 + r) * G + g) * kN + m0) = acc;
+        if constexpr (TIERED) {
+          // ring append of the B' cold columns (tokens that do not flush; a flush
+          // token's columns are read from the workspace). x goes to the ring from
+          // the stream kernel.
+          const int tr = sTr[r];
+          if (which == 0 && m0 >= a.K && (tr + 1) % c != 0)
+            *reinterpret_cast<f4*>(a.ring_b + (((size_t)sl * G + g) * c + tr % c) * (kN - a.K) + (m0 - a.K)) = acc;
         }
       }
     }
-  } else if (tid < kN) {
-    sBr[tid] = sBraw[tid];
-    ws.B[bgo + tid] = sBraw[tid];
-    ws.C[bgo + tid] = sCraw[tid];
+  } else {  // identity rotation
+    for (int i = tid; i < nreq * kN; i += kPrepThreads) {
+      const int r = i / kN, n = i - r * kN;
+      const int sl = sSlot[r];
+      if (sl < 0 || sl >= a.slots) continue;
+      const size_t o = ((size_t)(r0 + r) * G + g) * kN + n;
+      ws.B[o] = sX[r][n];
+      ws.C[o] = sX[kPrepReq + r][n];
+      if constexpr (TIERED) {
+        const int tr = sTr[r];
+        if (n >= a.K && (tr + 1) % c != 0)
+          a.ring_b[(((size_t)sl * G + g) * c + tr % c) * (kN - a.K) + (n - a.K)] = sX[r][n];
+      }
+    }
   }
 
-  if constexpr (TIERED) __syncthreads();  // sRdt
-
-  // 3. per-head scalars and bookkeeping: one thread per head of the group
-  if (head_thread) {
+  // 3. per-head scalars and bookkeeping
+  if (head_thread && slot >= 0 && slot < a.slots) {
     float dt = softplus_f(draw + dtb);
     if (a.dt_min > 0.f) dt = fmaxf(dt, a.dt_min);
     const float av = dt * Ah;
@@ -252,6 +262,7 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
     hd[HD_DECAY] = expf(av);
     hd[HD_D] = Dh;
     if constexpr (TIERED) {
+      const size_t o = (size_t)slot * H + h;
       const int pos = tt % c;
       const bool flush = (tt + 1) % c == 0;  // then pos == c - 1
       hd[HD_EG] = expf(gl);
@@ -259,18 +270,27 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
       hd[HD_POS] = (float)pos;
       if (flush) {
         // window = the nv buffered tokens at ring [c-m, c-1) and this one:
-        // w_i = exp(sum_{l>i} a_l) dt_i, total decay exp(sum_l a_l)
-        const int m = nvv + 1;
-        const float* rdt = sRdt + tid * c + (c - m);
+        // w_i = exp(sum_{l>i} a_l) dt_i, total decay exp(sum_l a_l); the buffered
+        // dt are loaded 16 at a time
+        const int mw = nvv + 1;
+        const float* __restrict__ rdt = a.ring_dt + o * c + (c - mw);
         float* __restrict__ w = ws.w + ((size_t)bi * H + h) * c;
-        float suf = 0.f;
-        for (int i = m - 1; i >= 0; --i) {
-          const float dti = i == m - 1 ? dt : rdt[i];
-          w[i] = expf(suf) * dti;
-          suf += dti * Ah;
+        w[mw - 1] = dt;
+        float suf = dt * Ah;
+        for (int i0 = mw - 2; i0 >= 0; i0 -= 16) {
+          float v[16];
+#pragma unroll
+          for (int u = 0; u < 16; ++u) v[u] = i0 - u >= 0 ? rdt[i0 - u] : 0.f;
+#pragma unroll
+          for (int u = 0; u < 16; ++u) {
+            if (i0 - u >= 0) {
+              w[i0 - u] = expf(suf) * v[u];
+              suf += v[u] * Ah;
+            }
+          }
         }
         hd[HD_DTOT] = expf(suf);
-        hd[HD_M] = (float)m;
+        hd[HD_M] = (float)mw;
         a.nv[o] = 0;
         a.glog[o] = 0.f;
       } else {
@@ -281,28 +301,12 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
         a.glog[o] = gl + av;
       }
       a.t[o] = tt + 1;
-      if (tid == 0) {
-        sPos = pos;
-        sFlush = flush;
-      }
     } else {
       hd[HD_EG] = 0.f;
       hd[HD_FLUSH] = 0.f;
       hd[HD_DTOT] = 1.f;
       hd[HD_M] = 0.f;
       hd[HD_POS] = 0.f;
-    }
-  }
-
-  // 4. ring append of the rotated B cold columns (tokens that do not flush;
-  // a flush token's columns are read from the workspace). x goes to the ring
-  // from the stream kernel.
-  if constexpr (TIERED) {
-    __syncthreads();  // sPos, sFlush, sBr
-    if (!sFlush) {
-      const int NC = kN - a.K;
-      const size_t rb = (((size_t)slot * a.G + g) * c + sPos) * NC;
-      for (int n = tid; n < NC; n += kPrepThreads) a.ring_b[rb + n] = sBr[a.K + n];
     }
   }
 }
@@ -1151,6 +1155,12 @@ size_t flush_lds_bytes(int P, int K, int kind) {
 //   c = 64  fused  9.3 /  8.6 / 7.4   split  8.5 /  7.2 /  6.0
 constexpr int kFuseMaxC = 33;
 
+// requests per prep workgroup: one head thread per (request, head)
+int prep_requests(int HG) {
+  const int r = kPrepThreads / HG;
+  return r < 1 ? 1 : r > kPrepReq ? kPrepReq : r;
+}
+
 // stream kernel LDS: the whole window of the block's heads when it flushes (fused)
 size_t fused_lds_bytes(int hpw, int P, int c, int K) {
   return ((size_t)c * (kN - K) + (size_t)hpw * c * P) * sizeof(float);
@@ -1243,7 +1253,10 @@ template <int K, int COLD>
 int launch_pair(const StepArgs& a, const Launch& L, hipStream_t st) {
   constexpr bool TIERED = K < kN && COLD != NSSM_COLD_NONE;
   if (a.b == 0) return NSSM_OK;
-  hipLaunchKernelGGL((prep_kernel<TIERED>), dim3((unsigned)a.b * a.G), dim3(kPrepThreads), 0, st, a);
+  StepArgs ap = a;
+  ap.prb = prep_requests(a.HG);
+  const unsigned pgrid = (unsigned)((a.b + ap.prb - 1) / ap.prb) * a.G;
+  hipLaunchKernelGGL((prep_kernel<TIERED>), dim3(pgrid), dim3(kPrepThreads), 0, st, ap);
   if (L.fused) {
     if constexpr (TIERED)
       hipLaunchKernelGGL((stream_kernel<K, COLD, true>), dim3((unsigned)a.b * a.nhb), dim3(L.waves * 64), L.lds, st, a);
