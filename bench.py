@@ -1,9 +1,10 @@
 """State-op decode benchmark on one MI355X: tiered v4 vs fresh at the
 Nemotron-Nano-9B-v2 mixer shape (27 Mamba2 layers, H=128, P=80, N=128, G=8).
 
-A step is one decode token through the state op of all layers (two kernel
-launches per layer: prep and stream), inputs resident in HBM, synthetic
-seeded data. Prints one
+A step is one decode token through the state op of all layers, inputs resident
+in HBM, synthetic seeded data. Per layer-token the tiered path launches prep and
+stream (windows up to 32 tokens are flushed inside the stream kernel) or prep,
+stream and flush (longer windows); the untiered path prep and stream. Prints one
 JSON line (the driver contract); progress goes to stderr.
 
     python bench.py [--steps 64] [--warmup 8] [--B 256] [--c 4] [--k 32] [--cold fp32]
@@ -233,6 +234,17 @@ def measured_traffic(key):
     return None
 
 
+def kernel_label(head, args):
+    """The launches of one layer-token (the unit the roofline is measured on)."""
+    if head == "fresh":
+        return "prep_kernel<false> + stream_kernel<128, fp32, all> (one layer-token, two launches)"
+    if args.c <= 32:
+        return (f"prep_kernel<true> + stream_kernel<{args.k}, {args.cold}, fused flush> "
+                f"(one layer-token, two launches)")
+    return (f"prep_kernel<true> + stream_kernel<{args.k}, {args.cold}> + flush_kernel<{args.k}, {args.cold}> "
+            f"(one layer-token, three launches)")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -327,8 +339,7 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": traffic,
-            "kernel": (f"prep_kernel + stream_kernel<{args.k if head == 'v4' else N}, "
-                       f"{args.cold if head == 'v4' else 'none'}> (one layer-token, two launches)"),
+            "kernel": kernel_label(head, args),
             "algorithmic_bytes_per_launch": int(per_launch_bytes),
             "avg_launch_us_events": round(ms_ev * 1e3, 2),
             "avg_launch_us_region": round(ms_launch * 1e3, 2),
