@@ -165,7 +165,7 @@ def bench_v4(args, layers, inputs, dev):
     def step(i):
         inp = inputs[i % len(inputs)]
         for l in range(args.layers):
-            tiers[l].step(layers[l], *inp[l], y=ys[l])
+            tiers[l].step(layers[l], *inp[l], y=ys[l], exact=args.exact)
 
     # warmup is rounded to whole flush windows so the timed steps start phase-aligned
     warm = ((args.warmup + args.c - 1) // args.c) * args.c
@@ -179,7 +179,7 @@ def bench_v4(args, layers, inputs, dev):
 
     def one(i):
         tok, l = seq[i % len(seq)]
-        tiers[l].step(layers[l], *inputs[tok % len(inputs)][l], y=ys[l])
+        tiers[l].step(layers[l], *inputs[tok % len(inputs)][l], y=ys[l], exact=args.exact)
 
     ms_ev = per_launch_ms(one, len(seq) * max(1, 108 // len(seq)))
     tier_gb = sum(t.nbytes() for t in tiers) / 1e9
@@ -198,7 +198,7 @@ def cpu_baseline(args, budget_s):
     gen = torch.Generator().manual_seed(args.seed)
     prm = oracle.make_layer_params(H, P, N, G, gen)
     B = args.B
-    ref = oracle.NativeV4(B, H, P, N, args.k, args.c, cold=args.cold)
+    ref = oracle.NativeV4(B, H, P, N, args.k, args.c, cold=args.cold, exact=args.exact)
     ref.join(torch.arange(B), oracle.make_state(B, H, P, N, gen))
     x, Bm, Cm, dt = oracle.make_step_inputs(B, H, P, N, G, gen)
     ref.step(x, Bm, Cm, dt, prm)  # warm
@@ -215,7 +215,8 @@ def cpu_baseline(args, budget_s):
         "unit": "state-op tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"oracle NativeV4 step ({args.cold} cold, k={args.k}, c={args.c}), 1 layer x B={B} x {n} tokens "
+        "sample": f"oracle NativeV4 step ({args.cold} cold, k={args.k}, c={args.c}"
+                  f"{', exact readout' if args.exact else ''}), 1 layer x B={B} x {n} tokens "
                   f"on the host, {t_layer * 1e3:.0f} ms/layer-token, scaled to {args.layers} layers",
     }
 
@@ -255,6 +256,7 @@ def main():
     ap.add_argument("--k", type=int, default=32)
     ap.add_argument("--c", type=int, default=4)
     ap.add_argument("--cold", default="fp32", choices=["fp32", "bf16", "fp8"])
+    ap.add_argument("--exact", action="store_true", help="v4 with the rank-c exact correction readout (corr=1)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the host baseline")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of host work for the baseline")
@@ -328,9 +330,10 @@ def main():
         "data": "synthetic (seeded; bf16 x/B/C/dt, fp32 state ~N(0,0.1^2), random orthogonal R per layer-group)",
         "config": {
             "workload": (f"{head} state op, Nemotron-Nano-9B-v2 mixer shape, {args.layers} layers, B={args.B}"
-                         + (f", k_hot={args.k}, c={args.c}, {args.cold} cold, phase-aligned" if head == "v4" else "")),
+                         + (f", k_hot={args.k}, c={args.c}, {args.cold} cold, phase-aligned" if head == "v4" else "")
+                         + (", exact (corr=1) readout" if head == "v4" and args.exact else "")),
             "layers": args.layers, "B": args.B, "H": H, "P": P, "N": N, "G": G,
-            "k_hot": args.k, "c": args.c, "cold": args.cold,
+            "k_hot": args.k, "c": args.c, "cold": args.cold, "readout": "exact" if args.exact else "stale",
         },
         "roofline": {
             "bound": "hbm",

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define NSSM_ABI_VERSION 2
+#define NSSM_ABI_VERSION 3
 
 /* error codes */
 #define NSSM_OK 0
@@ -138,6 +138,19 @@ int nssm_fresh_step(const nssm_layer_params* prm, float* state, int32_t slots,
 int nssm_v4_step(const nssm_layer_params* prm, const nssm_tier* tier,
                  const nssm_step_inputs* in, float* y, void* workspace,
                  int64_t workspace_bytes, void* stream);
+
+/* nssm_v4_step with the rank-c exact correction readout instead of the stale
+ * one: replaces `_v4_decode` with v4cfg["corr"] = 1 (scale/v4_native_decode.py:81-117).
+ * With G = glog + a (inclusive of this token) and the window j = 0..nv (the
+ * buffered tokens, then this one),
+ *   y = hot C'[:K] + exp(G) (cold_read C'[K:])
+ *       + sum_j exp(sum_{i>j} a_i) dt_j (C'[K:] . B'_j[K:]) x_j + D x,
+ * which is the current cold state's readout for an fp32 cold tier. The tier
+ * bookkeeping (ring, t, nv, glog, flush) is nssm_v4_step's, so calls of the two
+ * may alternate on one tier. NSSM_E_KIND for NSSM_COLD_NONE (no cold tier). */
+int nssm_v4_step_exact(const nssm_layer_params* prm, const nssm_tier* tier,
+                       const nssm_step_inputs* in, float* y, void* workspace,
+                       int64_t workspace_bytes, void* stream);
 
 /* Capture a tier from full fp32 states [b][H][P][N] into slot_ids[b] (NULL =
  * 0..b-1): hot = S[..,:K], cold = S[..,K:] (quantized for BF16/FP8),

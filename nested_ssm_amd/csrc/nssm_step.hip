@@ -62,23 +62,28 @@ struct StepArgs {
   float* y;
   float* ws;  // workspace (see Ws below)
   int32_t b, slots, H, P, G, HG, c, K, hpw, nhb;
-  int32_t prb;  // requests per prep workgroup
+  int32_t prb;    // requests per prep workgroup
+  int32_t exact;  // rank-c exact correction readout instead of the stale one
   float dt_min;
 };
 
 // Workspace carve-up for b requests (floats): rotated B and C [b][G][N] each,
-// per-head scalars [b][H][HD_STRIDE], flush weights [b][H][c].
-enum { HD_DT = 0, HD_A, HD_DECAY, HD_EG, HD_D, HD_FLUSH, HD_DTOT, HD_M, HD_POS, HD_STRIDE = 12 };
+// per-head scalars [b][H][HD_STRIDE], window weights [b][H][c] (flush) and
+// correction coefficients [b][H][c] (exact readout).
+// HD_SNAPF is the factor of the snapshot readout: exp(glog) (stale, the decay up
+// to the previous token) or exp(glog + a) (exact, inclusive of this token).
+enum { HD_DT = 0, HD_A, HD_DECAY, HD_SNAPF, HD_D, HD_FLUSH, HD_DTOT, HD_M, HD_POS, HD_STRIDE = 12 };
 struct Ws {
-  float *B, *C, *hd, *w;
+  float *B, *C, *hd, *w, *cw;
   __host__ __device__ Ws(float* base, int b, int H, int G, int c) {
     B = base;
     C = B + (size_t)b * G * kN;
     hd = C + (size_t)b * G * kN;
     w = hd + (size_t)b * H * HD_STRIDE;
+    cw = w + (size_t)b * H * c;
   }
 };
-size_t ws_floats(int b, int H, int G, int c) { return (size_t)b * (2 * G * kN + H * HD_STRIDE + H * c); }
+size_t ws_floats(int b, int H, int G, int c) { return (size_t)b * (2 * G * kN + H * HD_STRIDE + 2 * H * c); }
 
 __device__ __forceinline__ float bf2f(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
 
@@ -148,7 +153,10 @@ constexpr int kPrepReq = 8;  // requests per prep workgroup (at most)
 template <bool TIERED>
 __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
   __shared__ float sX[2 * kPrepReq][kN];  // B (j < 8) and C (j >= 8) of the block's requests
-  __shared__ int sSlot[kPrepReq], sTr[kPrepReq];
+  __shared__ int sSlot[kPrepReq], sTr[kPrepReq], sNvr[kPrepReq];
+  // exact readout: B', C' of the block and s_j = C'_cold . B'_j over each window
+  __shared__ float sRot[TIERED ? 2 * kPrepReq : 1][TIERED ? kN : 1];
+  __shared__ float sS[TIERED ? kPrepReq : 1][TIERED ? kMaxC : 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, lk = lane >> 4;
   const int G = a.G, H = a.H, HG = a.HG, c = a.c;
@@ -202,6 +210,7 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
     if (hh == 0) {
       sSlot[hr] = slot;
       sTr[hr] = tt;
+      sNvr[hr] = nvv;
     }
   }
   __syncthreads();
@@ -222,6 +231,9 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
       // lane (li, lk) holds rows m0 + 4 lk .. +3 of column li
       const int m0 = (wave + 4 * t2) * 16 + 4 * lk;
       const int r = li & (kPrepReq - 1), which = li >> 3;
+      if constexpr (TIERED) {
+        if (a.exact) *reinterpret_cast<f4*>(&sRot[li][m0]) = acc;
+      }
       const int sl = r < nreq ? sSlot[r] : -1;
       if (sl >= 0 && sl < a.slots) {
         *reinterpret_cast<f4*>((which ? ws.C : ws.B) + ((size_t)(r0 + r) * G + g) * kN + m0) = acc;
@@ -244,10 +256,42 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
       ws.B[o] = sX[r][n];
       ws.C[o] = sX[kPrepReq + r][n];
       if constexpr (TIERED) {
+        if (a.exact) {
+          sRot[r][n] = sX[r][n];
+          sRot[kPrepReq + r][n] = sX[kPrepReq + r][n];
+        }
         const int tr = sTr[r];
         if (n >= a.K && (tr + 1) % c != 0)
           a.ring_b[(((size_t)sl * G + g) * c + tr % c) * (kN - a.K) + (n - a.K)] = sX[r][n];
       }
+    }
+  }
+
+  // 2b. exact readout: s_j = C'_cold . B'_j for each request's window, j = 0 .. nv
+  // (buffered tokens at ring positions t % c - nv + j, then this token)
+  if constexpr (TIERED) {
+    if (a.exact) {
+      __syncthreads();  // sRot
+      const int NC = kN - a.K;
+      for (int pi = tid; pi < nreq * c; pi += kPrepThreads) {
+        const int r = pi / c, j = pi - r * c;
+        const int sl = sSlot[r], nv = sNvr[r];
+        if (sl < 0 || sl >= a.slots || j > nv) continue;
+        const float* bj = j < nv ? a.ring_b + (((size_t)sl * G + g) * c + (sTr[r] % c - nv + j)) * NC
+                                 : &sRot[r][a.K];
+        const float* cq = &sRot[kPrepReq + r][a.K];
+        float acc = 0.f;
+        for (int n = 0; n < NC; n += 4) {
+          const f4 bv = *reinterpret_cast<const f4*>(bj + n);
+          const f4 cv = *reinterpret_cast<const f4*>(cq + n);
+          acc = fmaf(bv.x, cv.x, acc);
+          acc = fmaf(bv.y, cv.y, acc);
+          acc = fmaf(bv.z, cv.z, acc);
+          acc = fmaf(bv.w, cv.w, acc);
+        }
+        sS[r][j] = acc;
+      }
+      __syncthreads();  // sS
     }
   }
 
@@ -265,17 +309,23 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
       const size_t o = (size_t)slot * H + h;
       const int pos = tt % c;
       const bool flush = (tt + 1) % c == 0;  // then pos == c - 1
-      hd[HD_EG] = expf(gl);
+      const bool exact = a.exact != 0;
+      // stale: exp(glog), the decay up to the previous token (one-token lag);
+      // exact: exp(glog + a), inclusive of this token (scale/v4_native_decode.py:89)
+      hd[HD_SNAPF] = expf(exact ? gl + av : gl);
       hd[HD_FLUSH] = flush ? 1.f : 0.f;
       hd[HD_POS] = (float)pos;
-      if (flush) {
-        // window = the nv buffered tokens at ring [c-m, c-1) and this one:
-        // w_i = exp(sum_{l>i} a_l) dt_i, total decay exp(sum_l a_l); the buffered
-        // dt are loaded 16 at a time
+      if (flush || exact) {
+        // window = the nv buffered tokens at ring [pos-nv, pos) and this one (at a
+        // flush pos = c-1): w_i = exp(sum_{l>i} a_l) dt_i, total decay exp(sum_l a_l);
+        // the exact readout's coefficients are w_i s_i. The buffered dt are loaded
+        // 16 at a time.
         const int mw = nvv + 1;
-        const float* __restrict__ rdt = a.ring_dt + o * c + (c - mw);
+        const float* __restrict__ rdt = a.ring_dt + o * c + (pos - nvv);
         float* __restrict__ w = ws.w + ((size_t)bi * H + h) * c;
-        w[mw - 1] = dt;
+        float* __restrict__ cw = ws.cw + ((size_t)bi * H + h) * c;
+        if (flush) w[mw - 1] = dt;
+        if (exact) cw[mw - 1] = dt * sS[hr][mw - 1];
         float suf = dt * Ah;
         for (int i0 = mw - 2; i0 >= 0; i0 -= 16) {
           float v[16];
@@ -284,25 +334,30 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
 #pragma unroll
           for (int u = 0; u < 16; ++u) {
             if (i0 - u >= 0) {
-              w[i0 - u] = expf(suf) * v[u];
+              const float wi = expf(suf) * v[u];
+              if (flush) w[i0 - u] = wi;
+              if (exact) cw[i0 - u] = wi * sS[hr][i0 - u];
               suf += v[u] * Ah;
             }
           }
         }
         hd[HD_DTOT] = expf(suf);
         hd[HD_M] = (float)mw;
-        a.nv[o] = 0;
-        a.glog[o] = 0.f;
       } else {
         hd[HD_DTOT] = 1.f;
         hd[HD_M] = 0.f;
+      }
+      if (flush) {
+        a.nv[o] = 0;
+        a.glog[o] = 0.f;
+      } else {
         a.ring_dt[o * c + pos] = dt;
         a.nv[o] = nvv + 1;
         a.glog[o] = gl + av;
       }
       a.t[o] = tt + 1;
     } else {
-      hd[HD_EG] = 0.f;
+      hd[HD_SNAPF] = 0.f;
       hd[HD_FLUSH] = 0.f;
       hd[HD_DTOT] = 1.f;
       hd[HD_M] = 0.f;
@@ -473,18 +528,36 @@ __device__ __forceinline__ float hot_update(const StepArgs& a, size_t row, int q
   return ph;
 }
 
+// The exact readout's correction for row p of head (slot sh, request rh):
+// sum_j cw_j x_j[p] over the window j = 0 .. m-1, the buffered tokens at ring positions
+// pos - (m-1) + j and, last, this token (x = xcur); cw_j = w_j (C'_cold . B'_j) from the
+// prep kernel, scale/v4_native_decode.py:98-104. Lane q takes j = q, q + 8, ...; the
+// row's 8 lanes are summed with the rest of the readout. (Issuing these loads with the
+// unit's state loads costs more registers than the latency it hides.)
+__device__ __forceinline__ float corr_partial(const StepArgs& a, const float* __restrict__ hd, size_t sh, size_t rh,
+                                              int p, int q, float xcur) {
+  const int m = (int)hd[HD_M], P = a.P, c = a.c;
+  const uint16_t* rx0 = a.ring_x + (sh * c + ((int)hd[HD_POS] - (m - 1))) * P + p;
+  const float* cw = Ws(a.ws, a.b, a.H, a.G, c).cw + rh * c;
+  float s = 0.f;
+  for (int j = q; j < m; j += 8) s = fmaf(cw[j], j < m - 1 ? bf2f(rx0[(size_t)j * P]) : xcur, s);
+  return s;
+}
+
 // One unit of one token: hot columns, and (a head that does not flush at this token)
 // the stale readout of its cold read copy and the ring append of x. A flushing head's
 // cold columns are left to the flush kernel, which adds their readout to y.
-template <int K, int COLD>
-__device__ __forceinline__ void unit_compute(const StepArgs& a, size_t row, size_t yrow, int p, int q,
+template <int K, int COLD, bool EXACT>
+__device__ __forceinline__ void unit_compute(const StepArgs& a, size_t sh, size_t rh, int p, int q,
                                              UnitRaw<K, COLD>& d, uint16_t* rx, bool cold, const float* __restrict__ hd,
                                              const float (&Bh)[K / 32][4], const float (&Ch)[K / 32][4],
                                              const float (&Cc)[Cfg<K, COLD>::CSR][4],
                                              const float (&Cq)[Cfg<K, COLD>::CWR]) {
+  const size_t row = sh * a.P + p, yrow = rh * a.P + p;
   float part = hot_update<K, COLD>(a, row, q, d, hd, Bh, Ch);
   if constexpr (Cfg<K, COLD>::TIERED) {
-    if (cold) part = fmaf(hd[HD_EG], cold_partial<K, COLD>(d, Cc, Cq), part);
+    if (cold) part = fmaf(hd[HD_SNAPF], cold_partial<K, COLD>(d, Cc, Cq), part);
+    if constexpr (EXACT) part += corr_partial(a, hd, sh, rh, p, q, d.xp);
   }
   part = sum8(part);
   if (q == 0) {
@@ -536,8 +609,8 @@ __device__ __forceinline__ void cold_store(const StepArgs& a, size_t row, int q,
 // hot columns, the stale readout, and the exact cold state at this token, the decayed
 // snapshot plus the VALU replay of the staged window (sU [m][P] of this head,
 // sBc [m][NC]), scale/v4_fused_decode.py:76-85.
-template <int K, int COLD>
-__device__ __forceinline__ void unit_compute_flush(const StepArgs& a, size_t row, size_t yrow, int p, int q,
+template <int K, int COLD, bool EXACT>
+__device__ __forceinline__ void unit_compute_flush(const StepArgs& a, size_t sh, size_t rh, int p, int q,
                                                    UnitRaw<K, COLD>& d, const float* __restrict__ hd,
                                                    const float (&Bh)[K / 32][4], const float (&Ch)[K / 32][4],
                                                    const float (&Cc)[Cfg<K, COLD>::CSR][4],
@@ -545,8 +618,10 @@ __device__ __forceinline__ void unit_compute_flush(const StepArgs& a, size_t row
                                                    const float* sBc, int m) {
   using C = Cfg<K, COLD>;
   constexpr int NC = C::NC, CS = C::CS;
+  const size_t row = sh * a.P + p, yrow = rh * a.P + p;
   float part = hot_update<K, COLD>(a, row, q, d, hd, Bh, Ch);
-  part = fmaf(hd[HD_EG], cold_partial<K, COLD>(d, Cc, Cq), part);
+  part = fmaf(hd[HD_SNAPF], cold_partial<K, COLD>(d, Cc, Cq), part);
+  if constexpr (EXACT) part += corr_partial(a, hd, sh, rh, p, q, d.xp);
   const int P = a.P;
   const float dtot = hd[HD_DTOT];
   float nvv[CS][4];
@@ -628,7 +703,7 @@ __device__ __forceinline__ void stage_window(float* sB, float* sU, int k0, int k
 // The units of one workgroup, U per wave in flight (all their loads issued before any
 // compute). MIXED: some head of the block flushes at this token, so each unit checks
 // its head's flag (a flushing head's cold columns are neither read nor appended to).
-template <int K, int COLD, bool MIXED>
+template <int K, int COLD, bool MIXED, bool EXACT>
 __device__ __forceinline__ void stream_units(const StepArgs& a, int slot, int bi, int h0, int units, int RG, int wave,
                                              int nw, int q, int rr, const float* __restrict__ hdb,
                                              const float (&Bh)[K / 32][4], const float (&Ch)[K / 32][4],
@@ -662,8 +737,8 @@ __device__ __forceinline__ void stream_units(const StepArgs& a, int slot, int bi
         if constexpr (TIERED) {
           if (!flushing) rx = a.ring_x + (((size_t)slot * H + h0 + j) * c + (int)hd[HD_POS]) * P;
         }
-        unit_compute<K, COLD>(a, ((size_t)slot * H + h0 + j) * P + p, ((size_t)bi * H + h0 + j) * P + p, p, q,
-                              d[i], rx, !flushing, hd, Bh, Ch, Cc, Cq);
+        unit_compute<K, COLD, EXACT>(a, (size_t)slot * H + h0 + j, (size_t)bi * H + h0 + j, p, q, d[i], rx, !flushing,
+                                     hd, Bh, Ch, Cc, Cq);
       }
     }
   }
@@ -671,7 +746,7 @@ __device__ __forceinline__ void stream_units(const StepArgs& a, int slot, int bi
 
 // one workgroup per (request, block of hpw heads of one group). FUSED (short windows):
 // a flushing head's cold columns are flushed here; otherwise by the flush kernel.
-template <int K, int COLD, bool FUSED>
+template <int K, int COLD, bool FUSED, bool EXACT>
 __global__ void __launch_bounds__(kMaxWaves * 64) stream_kernel(StepArgs a) {
   using C = Cfg<K, COLD>;
   constexpr int HS = C::HS, CS = C::CS, CSR = C::CSR, CWR = C::CWR;
@@ -723,9 +798,9 @@ __global__ void __launch_bounds__(kMaxWaves * 64) stream_kernel(StepArgs a) {
     for (int j = 0; j < hpw; ++j) any_flush |= hdb[j * HD_STRIDE + HD_FLUSH] != 0.f;
   }
   if (!any_flush) {
-    stream_units<K, COLD, false>(a, slot, bi, h0, units, RG, wave, nw, q, rr, hdb, Bh, Ch, Cc, Cq);
+    stream_units<K, COLD, false, EXACT>(a, slot, bi, h0, units, RG, wave, nw, q, rr, hdb, Bh, Ch, Cc, Cq);
   } else if constexpr (TIERED && !FUSED) {
-    stream_units<K, COLD, true>(a, slot, bi, h0, units, RG, wave, nw, q, rr, hdb, Bh, Ch, Cc, Cq);
+    stream_units<K, COLD, true, EXACT>(a, slot, bi, h0, units, RG, wave, nw, q, rr, hdb, Bh, Ch, Cc, Cq);
   } else if constexpr (TIERED) {
     extern __shared__ float lds[];
     constexpr int NC = C::NC;
@@ -756,14 +831,14 @@ __global__ void __launch_bounds__(kMaxWaves * 64) stream_kernel(StepArgs a) {
       }
       const int j = u / RG;
       const int p = (u - j * RG) * 8 + rr;
-      const size_t row = ((size_t)slot * H + h0 + j) * P + p;
-      const size_t yrow = ((size_t)bi * H + h0 + j) * P + p;
+      const size_t sh = (size_t)slot * H + h0 + j, rh = (size_t)bi * H + h0 + j;
       const float* hd = hdb + j * HD_STRIDE;
       if (hd[HD_FLUSH] != 0.f) {
-        unit_compute_flush<K, COLD>(a, row, yrow, p, q, dcur, hd, Bh, Ch, Cc, Cq, sU + (size_t)j * m * P, sBc, m);
+        unit_compute_flush<K, COLD, EXACT>(a, sh, rh, p, q, dcur, hd, Bh, Ch, Cc, Cq, sU + (size_t)j * m * P, sBc,
+                                           m);
       } else {
-        uint16_t* rx = a.ring_x + (((size_t)slot * H + h0 + j) * c + (int)hd[HD_POS]) * P;
-        unit_compute<K, COLD>(a, row, yrow, p, q, dcur, rx, true, hd, Bh, Ch, Cc, Cq);
+        uint16_t* rx = a.ring_x + (sh * c + (int)hd[HD_POS]) * P;
+        unit_compute<K, COLD, EXACT>(a, sh, rh, p, q, dcur, rx, true, hd, Bh, Ch, Cc, Cq);
       }
       dcur = dnext;
     }
@@ -825,7 +900,7 @@ __global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
         const int bi = it / H;
         const int slot = a.slot_ids ? a.slot_ids[bi] : bi;
         const float* hd = ws.hd + (size_t)it * HD_STRIDE;
-        const float fl = hd[HD_FLUSH], mm = hd[HD_M], dt = hd[HD_DTOT], eg = hd[HD_EG];
+        const float fl = hd[HD_FLUSH], mm = hd[HD_M], dt = hd[HD_DTOT], eg = hd[HD_SNAPF];
         if (slot >= 0 && slot < a.slots && fl != 0.f) {
           const int k = atomicAdd(&sCount, 1);
           sItem[k] = it;
@@ -1257,12 +1332,16 @@ int launch_pair(const StepArgs& a, const Launch& L, hipStream_t st) {
   ap.prb = prep_requests(a.HG);
   const unsigned pgrid = (unsigned)((a.b + ap.prb - 1) / ap.prb) * a.G;
   hipLaunchKernelGGL((prep_kernel<TIERED>), dim3(pgrid), dim3(kPrepThreads), 0, st, ap);
+  const dim3 sgrid((unsigned)a.b * a.nhb), sblock(L.waves * 64);
   if (L.fused) {
-    if constexpr (TIERED)
-      hipLaunchKernelGGL((stream_kernel<K, COLD, true>), dim3((unsigned)a.b * a.nhb), dim3(L.waves * 64), L.lds, st, a);
+    if constexpr (TIERED) {
+      if (a.exact) hipLaunchKernelGGL((stream_kernel<K, COLD, true, true>), sgrid, sblock, L.lds, st, a);
+      else hipLaunchKernelGGL((stream_kernel<K, COLD, true, false>), sgrid, sblock, L.lds, st, a);
+    }
     return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
   }
-  hipLaunchKernelGGL((stream_kernel<K, COLD, false>), dim3((unsigned)a.b * a.nhb), dim3(L.waves * 64), 0, st, a);
+  if (TIERED && a.exact) hipLaunchKernelGGL((stream_kernel<K, COLD, false, TIERED>), sgrid, sblock, 0, st, a);
+  else hipLaunchKernelGGL((stream_kernel<K, COLD, false, false>), sgrid, sblock, 0, st, a);
   if constexpr (TIERED) {
     const int items = a.b * a.H;
     const int grid = items < kFlushGrid ? items : kFlushGrid;
@@ -1281,6 +1360,32 @@ int dispatch_kind(const StepArgs& a, int kind, const Launch& L, hipStream_t st) 
     case NSSM_COLD_NONE: return launch_pair<K, NSSM_COLD_NONE>(a, L, st);
   }
   return NSSM_E_KIND;
+}
+
+int v4_step(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step_inputs* in, float* y,
+            void* workspace, int64_t workspace_bytes, void* stream, int exact) {
+  int rc = check_params(prm);
+  if (rc) return rc;
+  if ((rc = check_inputs(in, y))) return rc;
+  if ((rc = check_tier(tier, true))) return rc;
+  if (exact && tier->cold_kind == NSSM_COLD_NONE) return NSSM_E_KIND;  // the correction needs the cold tier
+  if (!in->slot_ids && in->b > tier->slots) return NSSM_E_DIMS;
+  if ((rc = check_ws(prm, in->b, tier->c, workspace, workspace_bytes))) return rc;
+  StepArgs a = {};
+  fill_common(a, prm, in, y, workspace);
+  fill_tier(a, tier);
+  a.exact = exact;
+  Launch L;
+  if ((rc = pick_launch(prm->H, prm->G, prm->P, tier->k_hot, tier->c, &L, tier->cold_kind))) return rc;
+  a.hpw = L.hpw;
+  a.nhb = prm->H / L.hpw;
+  hipStream_t st = (hipStream_t)stream;
+  switch (tier->k_hot) {
+    case 32: return dispatch_kind<32>(a, tier->cold_kind, L, st);
+    case 64: return dispatch_kind<64>(a, tier->cold_kind, L, st);
+    case 96: return dispatch_kind<96>(a, tier->cold_kind, L, st);
+  }
+  return NSSM_E_DIMS;
 }
 
 }  // namespace
@@ -1363,26 +1468,12 @@ int nssm_fresh_step(const nssm_layer_params* prm, float* state, int32_t slots, c
 
 int nssm_v4_step(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step_inputs* in, float* y,
                  void* workspace, int64_t workspace_bytes, void* stream) {
-  int rc = check_params(prm);
-  if (rc) return rc;
-  if ((rc = check_inputs(in, y))) return rc;
-  if ((rc = check_tier(tier, true))) return rc;
-  if (!in->slot_ids && in->b > tier->slots) return NSSM_E_DIMS;
-  if ((rc = check_ws(prm, in->b, tier->c, workspace, workspace_bytes))) return rc;
-  StepArgs a = {};
-  fill_common(a, prm, in, y, workspace);
-  fill_tier(a, tier);
-  Launch L;
-  if ((rc = pick_launch(prm->H, prm->G, prm->P, tier->k_hot, tier->c, &L, tier->cold_kind))) return rc;
-  a.hpw = L.hpw;
-  a.nhb = prm->H / L.hpw;
-  hipStream_t st = (hipStream_t)stream;
-  switch (tier->k_hot) {
-    case 32: return dispatch_kind<32>(a, tier->cold_kind, L, st);
-    case 64: return dispatch_kind<64>(a, tier->cold_kind, L, st);
-    case 96: return dispatch_kind<96>(a, tier->cold_kind, L, st);
-  }
-  return NSSM_E_DIMS;
+  return v4_step(prm, tier, in, y, workspace, workspace_bytes, stream, 0);
+}
+
+int nssm_v4_step_exact(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step_inputs* in, float* y,
+                       void* workspace, int64_t workspace_bytes, void* stream) {
+  return v4_step(prm, tier, in, y, workspace, workspace_bytes, stream, 1);
 }
 
 int nssm_v4_join(const nssm_layer_params* prm, const nssm_tier* tier, const float* state, int32_t b,

@@ -156,7 +156,9 @@ def decode_step(m, hidden_states, cache_params, attention_mask):
         S = cache_params.layers[m.layer_idx].recurrent_states[0]
         y = ops.fresh_step(prm, S, x, B, C, dt)
     else:
-        y = tier.step(prm, x, B, C, dt)
+        # v4cfg["corr"] is read per token (callers may switch it at run time): the
+        # rank-c exact correction readout, scale/v4_native_decode.py:81-117
+        y = tier.step(prm, x, B, C, dt, exact=bool(m.v4cfg.get("corr")))
     return decode_epilogue(m, y, gate, hidden_states.dtype)
 
 
@@ -170,7 +172,7 @@ def capture(m, cache_params, dt_min: float):
     """End of prefill: tiers from the cache's fp32 state (rotated into R's basis)."""
     cfg = m.v4cfg
     pb, c = int(cfg["pb"]), int(cfg["c"])
-    for key in ("corr", "coldoff", "qgate", "ktop"):
+    for key in ("coldoff", "qgate", "ktop"):
         if cfg.get(key):
             raise NotImplementedError(f"v4cfg[{key!r}] is not implemented by the MI355X kernels")
     layer = cache_params.layers[m.layer_idx]

@@ -177,15 +177,20 @@ class V4Tier:
                                  _ptr(phase), _stream()), "nssm_v4_join")
 
     def step(self, prm: LayerParams, x, B, C, dt, y: Optional[torch.Tensor] = None,
-             slot_ids: Optional[torch.Tensor] = None) -> torch.Tensor:
+             slot_ids: Optional[torch.Tensor] = None, exact: bool = False) -> torch.Tensor:
+        """One decode token for b requests (slot_ids: their slots, default 0..b-1).
+        exact=True reads the cold tier with the rank-c exact correction (corr=1,
+        scale/v4_native_decode.py:81-117) instead of the stale readout; the tier
+        evolves the same way either way."""
         b = x.shape[0]
         if y is None:
             y = torch.empty(b, prm.H, prm.P, device=x.device, dtype=torch.float32)
         _need(y, "y", torch.float32, (b, prm.H, prm.P))
         pc, ic, tc = prm.c_struct(), _inputs(prm, x, B, C, dt, slot_ids), self.c_struct()
         ws = step_workspace(b, prm.H, prm.G, self.c, x.device)
-        check(lib().nssm_v4_step(ctypes.byref(pc), ctypes.byref(tc), ctypes.byref(ic), y.data_ptr(),
-                                 ws.data_ptr(), ws.numel(), _stream()), "nssm_v4_step")
+        fn, name = (lib().nssm_v4_step_exact, "nssm_v4_step_exact") if exact else (lib().nssm_v4_step, "nssm_v4_step")
+        check(fn(ctypes.byref(pc), ctypes.byref(tc), ctypes.byref(ic), y.data_ptr(), ws.data_ptr(), ws.numel(),
+                 _stream()), name)
         return y
 
     def materialize(self, prm: LayerParams, slot_ids: Optional[torch.Tensor] = None,

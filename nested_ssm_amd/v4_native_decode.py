@@ -12,8 +12,10 @@ clamped at the mixer's time_step_min (scale/v4_native_decode.py:55), and the
 cold snapshot is bf16 when cold_bf16=1 (an exact fp32 master is kept beside
 it) or an exact fp32 copy otherwise.
 
-The installed transformers has no `torch_forward`; the mixer's `forward` is
-patched instead. corr=1 and coldoff=1 raise NotImplementedError at capture.
+corr=1 selects the rank-c exact correction readout
+(scale/v4_native_decode.py:81-117), read from v4cfg at every token. The installed
+transformers has no `torch_forward`; the mixer's `forward` is patched instead.
+coldoff=1 raises NotImplementedError at capture.
 """
 from transformers.models.nemotron_h import modeling_nemotron_h as M
 

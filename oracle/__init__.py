@@ -23,6 +23,10 @@ Pinning status of each function (how it is checked, in tests/test_oracle.py):
                     inputs), an fp64 per-element loop, rotation invariance
   NativeV4          k = N reduces to fresh; c = 1 is one-step stale; state
                     after every flush equals the fresh state; fp64 brute force
+  NativeV4 exact    (corr=1) y equals the fresh trajectory's y in fp64 with ragged
+                    phases and join/leave (the stale readout and a buffer missing
+                    this token's term fail it); with an e4m3 snapshot, fresh y plus
+                    the closed-form quantisation term exp(G_t) (q sc - snap) . C'
   TieredV4          equals NativeV4 in fp64 (chunked replay == per-token
                     recurrence), including ragged phases and join/leave
   quant_fp8 / read  torch float8_e4m3fn cast; scale = amax/448 + 1e-12 per row

@@ -155,13 +155,22 @@ class NativeV4:
     v4_native_decode.py:162-163), "fp8" (per-row scale, vllm_v4_patch.py:106-120).
     fp8_restore_each_step re-stores the dequantized old snapshot for slots that
     do not flush, as scale/vllm_v4_patch.py:173-175 does.
+
+    exact=True is the rank-c exact correction readout (corr=1,
+    scale/v4_native_decode.py:81-117): the log-decay G_t includes this token, this
+    token's (B'_cold, dt x, G_t) is buffered before the readout, and
+      y_cold = exp(G_t) (snap . C'_cold) + sum_j exp(G_t - G_j) (C'_cold . B'_j) (dt_j x_j)
+    over the buffer since the snapshot; the bookkeeping (t, glog, snapshot) is the
+    stale path's.
     """
 
     def __init__(self, slots: int, H: int, P: int, N: int, k: int, c: int, cold: str = "fp32",
-                 dtype=torch.float32, fp8_restore_each_step: bool = True):
+                 dtype=torch.float32, fp8_restore_each_step: bool = True, exact: bool = False):
         assert 0 < k <= N and c >= 1 and cold in ("fp32", "bf16", "fp8")
         self.k, self.c, self.cold, self.dtype = k, c, cold, dtype
         self.fp8_restore = fp8_restore_each_step
+        self.exact = exact
+        self.buf = [[] for _ in range(slots)]  # exact readout: per slot (B'_cold [H,Nc], dt x [H,P], G [H])
         self.S = torch.zeros(slots, H, P, N, dtype=dtype)
         Nc = N - k
         self.snap = torch.zeros(slots, H, P, Nc, dtype=dtype)          # fp32 / bf16-rounded values
@@ -193,6 +202,8 @@ class NativeV4:
         self._store(slots, self.S[slots][..., self.k:])
         self.glog[slots] = 0
         self.t[slots] = 0 if phase is None else torch.as_tensor(phase, dtype=torch.int64)
+        for s in slots.tolist():
+            self.buf[s] = []
 
     def step(self, x, B, C, dt_raw, prm: LayerParams, slots: Optional[torch.Tensor] = None) -> torch.Tensor:
         b = x.shape[0]
@@ -204,7 +215,19 @@ class NativeV4:
         S = S * torch.exp(a)[..., None, None] + (dt[..., None, None] * Bp[:, :, None, :]) * xf[..., None]
         self.S[slots] = S
         glog = self.glog[slots]
-        y_cold = torch.einsum("bhpn,bhn->bhp", self._read(slots), Cp[..., k:]) * torch.exp(glog)[..., None]
+        if self.exact:
+            g1 = glog + a  # G_t, inclusive of this token
+            y_cold = torch.einsum("bhpn,bhn->bhp", self._read(slots), Cp[..., k:]) * torch.exp(g1)[..., None]
+            for i, s in enumerate(slots.tolist()):
+                self.buf[s].append((Bp[i, :, k:].clone(), dt[i][:, None] * xf[i], g1[i].clone()))
+                Bs = torch.stack([e[0] for e in self.buf[s]])   # [j,H,Nc]
+                Xs = torch.stack([e[1] for e in self.buf[s]])   # [j,H,P]
+                Gs = torch.stack([e[2] for e in self.buf[s]])   # [j,H]
+                sj = torch.einsum("jhn,hn->jh", Bs, Cp[i, :, k:])
+                w = torch.exp(g1[i][None] - Gs) * sj
+                y_cold[i] = y_cold[i] + torch.einsum("jh,jhp->hp", w, Xs)
+        else:
+            y_cold = torch.einsum("bhpn,bhn->bhp", self._read(slots), Cp[..., k:]) * torch.exp(glog)[..., None]
         y = torch.einsum("bhpn,bhn->bhp", S[..., :k], Cp[..., :k]) + y_cold
         t = self.t[slots] + 1
         self.t[slots] = t
@@ -215,6 +238,10 @@ class NativeV4:
         elif bool(flush.any()):
             fs = slots[flush]
             self._store(fs, S[flush][..., k:])
+        if self.exact:
+            for i, s in enumerate(slots.tolist()):
+                if bool(flush[i]):
+                    self.buf[s] = []
         self.glog[slots] = torch.where(flush[:, None], torch.zeros_like(glog), glog + a)
         return y + xf * prm.D[None, :, None]
 

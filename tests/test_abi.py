@@ -140,11 +140,19 @@ def test_entry_points_validate_before_launching():
     # workspace: NULL, too small, misaligned
     need = L.nssm_step_workspace_bytes(4, 8, 1, 128, 0)
     assert need == 4 * (2 * 128 + 12 * 8) * 4
-    assert L.nssm_step_workspace_bytes(4, 8, 1, 128, 4) == need + 4 * 8 * 4 * 4
+    # tiered: plus window weights and exact-readout coefficients [b][H][c] each
+    assert L.nssm_step_workspace_bytes(4, 8, 1, 128, 4) == need + 2 * 4 * 8 * 4 * 4
     assert L.nssm_step_workspace_bytes(4, 8, 3, 128, 4) == -2
     assert L.nssm_fresh_step(ctypes.byref(prm), fake, 4, ctypes.byref(inp), fake, None, need, None) == -7
     assert L.nssm_fresh_step(ctypes.byref(prm), fake, 4, ctypes.byref(inp), fake, fake, need - 4, None) == -7
     assert L.nssm_fresh_step(ctypes.byref(prm), fake, 4, ctypes.byref(inp), fake, fake + 8, need, None) == -3
+    # the exact readout needs a cold tier; x must be 8-byte aligned
+    tier = _lib.Tier(4, 32, 4, _lib.COLD_KINDS["off"], *([fake] * 10))
+    assert L.nssm_v4_step_exact(ctypes.byref(prm), ctypes.byref(tier), ctypes.byref(inp), fake, fake, 1 << 30,
+                                None) == -4
+    odd = _lib.StepInputs(4, fake + 2, fake, fake, fake, None)
+    assert L.nssm_v4_step_exact(ctypes.byref(prm), ctypes.byref(tier), ctypes.byref(odd), fake, fake, 1 << 30,
+                                None) == -3
     assert L.nssm_set_launch(0, 9) == -6
     assert L.nssm_set_launch(0, 0) == 0
 

@@ -84,7 +84,7 @@ def _rot(S, R, H):
     return torch.einsum("bhpn,hmn->bhpm", S.double(), Rh).float()
 
 
-def _replay_and_check(model, rec, pb, c, cold, dt_min_of):
+def _replay_and_check(model, rec, pb, c, cold, dt_min_of, exact=False):
     from nested_ssm_amd import hf
 
     for m in hf.mixers(model):
@@ -95,7 +95,7 @@ def _replay_and_check(model, rec, pb, c, cold, dt_min_of):
             S0 = _rot(S0, prm.R, m.num_heads)
         b = S0.shape[0]
         k = min(pb, N)
-        ref = oracle.NativeV4(b, m.num_heads, m.head_dim, N, k, c, cold=cold)
+        ref = oracle.NativeV4(b, m.num_heads, m.head_dim, N, k, c, cold=cold, exact=exact)
         ref.join(torch.arange(b), S0)
         assert len(rec.inputs[li]) > 0
         for step, ((x, B, C, dt), y) in enumerate(zip(rec.inputs[li], rec.ys[li])):
@@ -137,6 +137,44 @@ def test_native_install_matches_oracle(monkeypatch, pb, c, cold_bf16):
         assert st["pb"] == pb and st["c"] == c
         if pb < N:
             assert st["t"] == int(ref.t[0])
+
+
+@pytest.mark.parametrize("pb,c,cold_bf16", [(32, 4, 0), (64, 16, 1)])
+def test_native_install_corr_matches_oracle(monkeypatch, pb, c, cold_bf16):
+    """install(..., corr=1): the rank-c exact correction readout
+    (scale/v4_native_decode.py:81-117) against the oracle's exact mode."""
+    from nested_ssm_amd import v4_native_decode as V
+
+    model = _tiny_model(seed=11)
+    assert V.install(model, pb=pb, c=c, cold_bf16=cold_bf16, corr=1) == 2
+    rec = Recorder(monkeypatch)
+    ids = torch.randint(0, 96, (3, 7), generator=torch.Generator().manual_seed(12)).cuda()
+    with torch.no_grad():
+        _prefill_decode(model, ids, n_decode=2 * c + 1)
+    cold = "bf16" if cold_bf16 else "fp32"
+    for m, ref in _replay_and_check(model, rec, pb, c, cold, lambda m: float(m.time_step_limit[0]), exact=True):
+        assert m._v4state["t"] == int(ref.t[0])
+
+
+def test_native_install_corr_gives_the_untiered_model():
+    """With an fp32 cold tier, corr=1 reads the current cold state exactly, so the
+    tiered model's logits equal the untiered (pb = N) install's up to fp32 rounding."""
+    from nested_ssm_amd import v4_native_decode as V
+
+    ids = torch.randint(0, 96, (2, 8), generator=torch.Generator().manual_seed(13)).cuda()
+    with torch.no_grad():
+        m_full = _tiny_model(seed=14)
+        V.install(m_full, pb=128, c=4, cold_bf16=0)
+        l_full, _ = _prefill_decode(m_full, ids, 9)
+        m_corr = _tiny_model(seed=14)
+        V.install(m_corr, pb=32, c=4, cold_bf16=0, corr=1)
+        l_corr, _ = _prefill_decode(m_corr, ids, 9)
+        m_stale = _tiny_model(seed=14)
+        V.install(m_stale, pb=32, c=4, cold_bf16=0)
+        l_stale, _ = _prefill_decode(m_stale, ids, 9)
+    scale = l_full.abs().max()
+    assert float((l_corr - l_full).abs().max() / scale) < 1e-4
+    assert float((l_stale - l_full).abs().max() / scale) > 1e-4  # the stale readout is not exact
 
 
 def test_fused_install_fp8_matches_oracle(monkeypatch):

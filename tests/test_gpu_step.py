@@ -56,10 +56,10 @@ def test_fresh_dt_min_and_identity_rotation():
     assert_close32(S_dev, S_ref, "fresh(dt_min) state", **FP32_TOL)
 
 
-def _run_v4(b, H, G, P, k, c, cold, steps, seed, slots=None, phase=None, check_state_every=1):
+def _run_v4(b, H, G, P, k, c, cold, steps, seed, slots=None, phase=None, check_state_every=1, exact=False):
     gen, prm, S0 = _setup(b, H, P, G, seed)
     dprm = dev_params(prm)
-    ref = oracle.NativeV4(b, H, P, 128, k, c, cold=cold)
+    ref = oracle.NativeV4(b, H, P, 128, k, c, cold=cold, exact=exact)
     ph = None if phase is None else torch.as_tensor(phase, dtype=torch.int32)
     ref.join(torch.arange(b), S0, phase=None if ph is None else ph.long())
     tier = V4Tier(b, H, P, G, k_hot=k, c=c, cold=cold)
@@ -68,7 +68,7 @@ def _run_v4(b, H, G, P, k, c, cold, steps, seed, slots=None, phase=None, check_s
     for step in range(steps):
         x, B, C, dt = oracle.make_step_inputs(b, H, P, 128, G, gen)
         y_ref = ref.step(x, B, C, dt, prm)
-        y = tier.step(dprm, *to_dev(x, B, C, dt))
+        y = tier.step(dprm, *to_dev(x, B, C, dt), exact=exact)
         if cold == "fp8":
             r = max_rel(y.cpu(), y_ref)
             worst = max(worst, r)
@@ -262,3 +262,43 @@ def test_flush_contraction_kinds_and_passes(cold, k, c, P, waves):
         # the scale is amax / 448 of an fp32 state row built in another summation
         # order (matrix cores vs per-token recurrence): the fp32 state bar applies
         assert_close32(tier.scale.cpu(), ref.sc8[..., 0], "fp8 scale", rtol=1e-5, atol=0)
+
+
+@pytest.mark.parametrize("cold,k,c,phase", [
+    ("fp32", 32, 4, None), ("fp32", 32, 4, [0, 1, 2, 3]), ("fp32", 64, 16, [3, 9, 15, 0]), ("fp32", 32, 40, [0, 7, 39, 20]),
+    ("bf16", 32, 4, [1, 2, 3, 0]), ("fp8", 32, 4, None), ("fp8", 96, 33, [5, 0, 32, 17])])
+def test_v4_exact_readout_matches_oracle(cold, k, c, phase):
+    """The rank-c exact correction readout (corr=1) through nssm_v4_step_exact against
+    the oracle's exact mode, on the fused (c <= 32) and flush-kernel (c > 32) paths,
+    with per-request phases."""
+    steps = 2 * c + 5
+    _run_v4(4, 8, 2, 80, k, c, cold, steps=steps, seed=80 + k + c, phase=phase, check_state_every=max(1, c // 2),
+            exact=True)
+
+
+def test_v4_exact_readout_equals_fresh_at_9b_shape_alternating_modes():
+    """fp32 cold at the 9B head shape (H=128, G=8, B=64): steps alternate between the
+    stale and the exact readout on one tier (the tier evolves the same way). Every
+    exact y equals the fresh path's y (computed on the GPU by nssm_fresh_step from the
+    same start); hot columns and the materialized state track fresh; random phases."""
+    import torch as T
+    b, H, P, G, k, c = 64, 128, 80, 8, 32, 4
+    gen, prm, _ = _setup(1, H, P, G, seed=91)
+    dprm = dev_params(prm)
+    g = T.Generator(device="cuda").manual_seed(5)
+    S = T.randn(b, H, P, 128, device="cuda", generator=g).mul_(0.1)
+    phase = T.randint(0, c, (b,), device="cuda", generator=g, dtype=T.int32)
+    tier = V4Tier(b, H, P, G, k_hot=k, c=c, cold="fp32")
+    tier.join(dprm, S, phase=phase)
+    for step in range(4 * c + 1):
+        x = T.randn(b, H, P, device="cuda", generator=g).to(T.bfloat16)
+        B = (T.randn(b, G, 128, device="cuda", generator=g) / 128 ** 0.5).to(T.bfloat16)
+        C = (T.randn(b, G, 128, device="cuda", generator=g) / 128 ** 0.5).to(T.bfloat16)
+        dt = T.randn(b, H, device="cuda", generator=g).to(T.bfloat16)
+        exact = step % 2 == 1
+        y = tier.step(dprm, x, B, C, dt, exact=exact)
+        y_fresh = fresh_step(dprm, S, x, B, C, dt)
+        if exact:
+            assert_close32(y, y_fresh, f"exact y step {step}", rtol=1e-5, atol=2e-5)
+        assert_close32(tier.hot, S[..., :k], f"hot step {step}")
+    assert_close32(tier.materialize(dprm), S, "materialized state")

@@ -186,6 +186,69 @@ def test_native_v4_dt_min_path():
     assert float(d.min()) >= 0.2
 
 
+@pytest.mark.parametrize("k,c", [(32, 4), (96, 1), (64, 7)])
+def test_native_v4_exact_readout_equals_fresh_readout(k, c):
+    """The rank-c exact correction (corr=1, scale/v4_native_decode.py:81-117) reads
+    exp(G_t) snap + the buffered rank-1 terms, which is the current cold state: its y
+    equals the fresh trajectory's y in fp64, with ragged phases and join/leave. The
+    stale readout (the lagged decay, no correction) is checked to fail the same test,
+    and so is a buffer that misses this token's term."""
+    b, H, P, G = 3, 4, 8, 2
+    gen, prm, S0 = _small(seed=40 + k + c, b=b, H=H, P=P, G=G)
+    f64 = torch.float64
+    prm64 = prm.to(f64)
+    phase = torch.tensor([0, c // 2, c - 1])
+    ex = oracle.NativeV4(b, H, P, N, k, c, dtype=f64, exact=True)
+    st = oracle.NativeV4(b, H, P, N, k, c, dtype=f64)
+    for m in (ex, st):
+        m.join(torch.arange(b), S0.double(), phase)
+    S = S0.double().clone()
+    stale_differs = False
+    for step in range(3 * c + 5):
+        if step == c + 1:  # slot 1 leaves, a new request joins it mid-window
+            Sj = oracle.make_state(1, H, P, N, gen).double()
+            S[1] = Sj[0]
+            for m in (ex, st):
+                m.join(torch.tensor([1]), Sj, torch.tensor([1 % c]))
+        x, B, C, dt = oracle.make_step_inputs(b, H, P, N, G, gen)
+        y_fresh = oracle.fresh_step(S, x, B, C, dt, prm64, dtype=f64)
+        y_ex = ex.step(x, B, C, dt, prm)
+        y_st = st.step(x, B, C, dt, prm)
+        assert torch.allclose(y_ex, y_fresh, atol=1e-11), f"step {step}"
+        stale_differs |= not torch.allclose(y_st, y_fresh, atol=1e-6)
+        # without this token's term (dt x)_t (C'_cold . B'_t) the readout is off
+        xf, Bp, Cp, dtv, a = oracle.v4_ref._prep(x, B, C, dt, prm64, f64)
+        own = dtv[..., None] * xf * torch.einsum("bhn,bhn->bh", Bp[..., k:], Cp[..., k:])[..., None]
+        assert not torch.allclose(y_ex - own, y_fresh, atol=1e-6)
+    assert stale_differs
+
+
+def test_native_v4_exact_fp8_is_fresh_plus_snapshot_quantisation():
+    """exact readout with an e4m3 snapshot = fresh readout + exp(G_t) ((q sc - snap) . C'_cold),
+    the snapshot being the fresh cold state at the last flush (one quantisation, no re-store)."""
+    b, H, P, G, k, c = 2, 4, 8, 2, 32, 4
+    gen, prm, S0 = _small(seed=47, b=b, H=H, P=P, G=G)
+    f64 = torch.float64
+    prm64 = prm.to(f64)
+    ex = oracle.NativeV4(b, H, P, N, k, c, cold="fp8", dtype=f64, fp8_restore_each_step=False, exact=True)
+    ex.join(torch.arange(b), S0.double())
+    S = S0.double().clone()
+    snap = S[..., k:].clone()
+    G_t = torch.zeros(b, H, dtype=f64)
+    for t in range(1, 3 * c + 2):
+        x, B, C, dt = oracle.make_step_inputs(b, H, P, N, G, gen)
+        q, sc = oracle.quant_fp8(snap.float())
+        err = oracle.read_fp8(q, sc).double() - snap
+        xf, Bp, Cp, dtv, a = oracle.v4_ref._prep(x, B, C, dt, prm64, f64)
+        G_t = G_t + a
+        y_fresh = oracle.fresh_step(S, x, B, C, dt, prm64, dtype=f64)
+        want = y_fresh + torch.exp(G_t)[..., None] * torch.einsum("bhpn,bhn->bhp", err, Cp[..., k:])
+        assert torch.allclose(ex.step(x, B, C, dt, prm), want, atol=1e-10), f"t={t}"
+        if t % c == 0:
+            snap = S[..., k:].clone()
+            G_t = torch.zeros_like(G_t)
+
+
 # --------------------------------------------------------------------------- tiered
 def test_tiered_chunked_replay_equals_native_recurrence_ragged():
     """The chunked flush (scale/v4_fused_decode.py:76-85) equals the per-token
