@@ -747,7 +747,7 @@ __device__ __forceinline__ void stream_units(const StepArgs& a, int slot, int bi
 // one workgroup per (request, block of hpw heads of one group). FUSED (short windows):
 // a flushing head's cold columns are flushed here; otherwise by the flush kernel.
 template <int K, int COLD, bool FUSED, bool EXACT>
-__global__ void __launch_bounds__(kMaxWaves * 64) stream_kernel(StepArgs a) {
+__device__ __forceinline__ void stream_body(const StepArgs& a) {
   using C = Cfg<K, COLD>;
   constexpr int HS = C::HS, CS = C::CS, CSR = C::CSR, CWR = C::CWR;
   constexpr bool TIERED = C::TIERED;
@@ -843,6 +843,30 @@ __global__ void __launch_bounds__(kMaxWaves * 64) stream_kernel(StepArgs a) {
       dcur = dnext;
     }
   }
+}
+
+// The k_hot = 32 stream kernels are compiled for at least 5 waves per SIMD (measured on
+// MI355X, B = 256, 27 layers: bf16 cold c = 4 10.1 -> 9.5 ms, c = 16 7.9 -> 7.3 ms per
+// step, fp32 and e4m3 unchanged or better); wider hot tiers spill under that bound and
+// keep the compiler's choice, as does the untiered kernel (it spills: 12.2 -> 12.8 ms).
+template <int K, int COLD, bool FUSED, bool EXACT>
+__global__ void __launch_bounds__(kMaxWaves * 64) __attribute__((amdgpu_waves_per_eu(5))) stream_kernel_o5(StepArgs a) {
+  stream_body<K, COLD, FUSED, EXACT>(a);
+}
+
+template <int K, int COLD, bool FUSED, bool EXACT>
+__global__ void __launch_bounds__(kMaxWaves * 64) stream_kernel(StepArgs a) {
+  stream_body<K, COLD, FUSED, EXACT>(a);
+}
+
+template <int K, int COLD, bool FUSED, bool EXACT>
+void launch_stream(dim3 grid, dim3 block, size_t lds, hipStream_t st, const StepArgs& a) {
+  if constexpr (K == 32) hipLaunchKernelGGL((stream_kernel_o5<K, COLD, FUSED, EXACT>), grid, block, lds, st, a);
+  else hipLaunchKernelGGL((stream_kernel<K, COLD, FUSED, EXACT>), grid, block, lds, st, a);
+}
+
+__global__ void __launch_bounds__(kMaxWaves * 64) fresh_stream_kernel(StepArgs a) {
+  stream_body<kN, NSSM_COLD_FP32, false, false>(a);
 }
 
 // ---------------------------------------------------------------------------
@@ -1335,13 +1359,14 @@ int launch_pair(const StepArgs& a, const Launch& L, hipStream_t st) {
   const dim3 sgrid((unsigned)a.b * a.nhb), sblock(L.waves * 64);
   if (L.fused) {
     if constexpr (TIERED) {
-      if (a.exact) hipLaunchKernelGGL((stream_kernel<K, COLD, true, true>), sgrid, sblock, L.lds, st, a);
-      else hipLaunchKernelGGL((stream_kernel<K, COLD, true, false>), sgrid, sblock, L.lds, st, a);
+      if (a.exact) launch_stream<K, COLD, true, true>(sgrid, sblock, L.lds, st, a);
+      else launch_stream<K, COLD, true, false>(sgrid, sblock, L.lds, st, a);
     }
     return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
   }
-  if (TIERED && a.exact) hipLaunchKernelGGL((stream_kernel<K, COLD, false, TIERED>), sgrid, sblock, 0, st, a);
-  else hipLaunchKernelGGL((stream_kernel<K, COLD, false, false>), sgrid, sblock, 0, st, a);
+  if constexpr (K == kN) hipLaunchKernelGGL(fresh_stream_kernel, sgrid, sblock, 0, st, a);
+  else if (TIERED && a.exact) launch_stream<K, COLD, false, TIERED>(sgrid, sblock, 0, st, a);
+  else launch_stream<K, COLD, false, false>(sgrid, sblock, 0, st, a);
   if constexpr (TIERED) {
     const int items = a.b * a.H;
     const int grid = items < kFlushGrid ? items : kFlushGrid;
