@@ -112,6 +112,27 @@ def timed(step_fn, steps, warmup, launches_per_step):
     return ms / steps, ms / (steps * launches_per_step)
 
 
+def graphed(step_fn, n_inputs):
+    """One HIP graph per input set, each capturing a whole step (all layers), after a
+    first call on the capture stream has sized its workspace; returns a step function
+    that replays them in turn. The state ops allocate nothing, issue no memset and keep
+    their phase on the device, so the replays do what the eager steps do."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step_fn(0)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graphs = []
+    for i in range(n_inputs):
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr, stream=s):
+            step_fn(i)
+        graphs.append(gr)
+    torch.cuda.synchronize()
+    return lambda i: graphs[i % n_inputs].replay()
+
+
 def per_launch_ms(launch_fn, n):
     """Average duration of n launches, each bracketed by its own event pair."""
     st = torch.cuda.current_stream()
@@ -136,7 +157,8 @@ def bench_fresh(args, layers, inputs, dev):
         for l in range(args.layers):
             fresh_step(layers[l], states[l], *inp[l], y=ys[l])
 
-    ms_step, ms_launch = timed(step, args.steps, args.warmup, args.layers)
+    run = graphed(step, len(inputs)) if args.graph else step
+    ms_step, ms_launch = timed(run, args.steps, args.warmup, args.layers)
 
     def one(i):
         l = i % args.layers
@@ -168,8 +190,13 @@ def bench_v4(args, layers, inputs, dev):
             tiers[l].step(layers[l], *inp[l], y=ys[l], exact=args.exact)
 
     # warmup is rounded to whole flush windows so the timed steps start phase-aligned
+    # (with --graph the capture's sizing call advances the phase by one token)
     warm = ((args.warmup + args.c - 1) // args.c) * args.c
-    ms_step, ms_launch = timed(step, args.steps, warm, args.layers)
+    run = step
+    if args.graph:
+        run = graphed(step, len(inputs))
+        warm = max(warm, args.c) - 1
+    ms_step, ms_launch = timed(run, args.steps, warm, args.layers)
 
     # per-launch events over whole flush windows (c tokens of layer 0 .. L-1)
     seq = []
@@ -257,6 +284,7 @@ def main():
     ap.add_argument("--c", type=int, default=4)
     ap.add_argument("--cold", default="fp32", choices=["fp32", "bf16", "fp8"])
     ap.add_argument("--exact", action="store_true", help="v4 with the rank-c exact correction readout (corr=1)")
+    ap.add_argument("--graph", action="store_true", help="time HIP graph replays of whole steps (all layers)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the host baseline")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of host work for the baseline")
@@ -331,7 +359,8 @@ def main():
         "config": {
             "workload": (f"{head} state op, Nemotron-Nano-9B-v2 mixer shape, {args.layers} layers, B={args.B}"
                          + (f", k_hot={args.k}, c={args.c}, {args.cold} cold, phase-aligned" if head == "v4" else "")
-                         + (", exact (corr=1) readout" if head == "v4" and args.exact else "")),
+                         + (", exact (corr=1) readout" if head == "v4" and args.exact else "")
+                         + (", HIP graph replay" if args.graph else "")),
             "layers": args.layers, "B": args.B, "H": H, "P": P, "N": N, "G": G,
             "k_hot": args.k, "c": args.c, "cold": args.cold, "readout": "exact" if args.exact else "stale",
         },
