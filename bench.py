@@ -215,6 +215,45 @@ def bench_v4(args, layers, inputs, dev):
     return ms_step, ms_launch, ms_ev, tier_gb
 
 
+def bench_prologue(args, dev):
+    """The mixer's conv prologue at the 9B shape (conv_dim 12288 = x 10240 + B, C 2 x 1024,
+    width 4, bf16): nssm_conv_update (one launch: state shift, conv, SiLU, x/B/C split)
+    vs transformers' causal_conv1d_update + split + bf16 casts (the adapter's path when
+    a padding mask is given). Microseconds per layer-token and GB/s of algorithmic bytes."""
+    from transformers.models.nemotron_h import modeling_nemotron_h as M
+
+    from nested_ssm_amd import conv_update
+
+    I, gn, W = H * P, G * N, 4
+    dim = I + 2 * gn
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(args.seed + 3)
+    proj = torch.randn(args.B, I + dim + H, device=dev, generator=g).to(bf)
+    hbc = proj[:, I:I + dim]
+    st = torch.randn(args.B, dim, W, device=dev, generator=g).to(bf)
+    w = (torch.randn(dim, W, device=dev, generator=g) * 0.5).to(bf)
+    bias = torch.randn(dim, device=dev, generator=g).to(bf)
+
+    def ours(_):
+        conv_update(hbc, st, w, bias, I, gn)
+
+    def stock(_):
+        o = M.causal_conv1d_update(hbc[..., None], st, w, bias, activation="silu")[..., 0]
+        x, B, C = torch.split(o, [I, gn, gn], dim=-1)
+        x.to(bf).contiguous(), B.to(bf).contiguous(), C.to(bf).contiguous()
+
+    n = 200
+    res = {}
+    for name, fn in (("nssm_conv_update", ours), ("torch_causal_conv1d_update", stock)):
+        ms, _ = timed(fn, n, 20, 1)
+        res[name + "_us"] = round(ms * 1e3, 2)
+    nbytes = args.B * (dim * 2 + 2 * dim * W * 2 + dim * 2) + dim * W * 2 + dim * 2
+    res["algorithmic_bytes"] = nbytes
+    res["nssm_conv_update_gbs"] = round(nbytes / (res["nssm_conv_update_us"] * 1e-6) / 1e9, 1)
+    res["shape"] = f"B={args.B}, conv_dim={dim} (x {I}, B/C {gn} each), width {W}, bf16"
+    return res
+
+
 def cpu_baseline(args, budget_s):
     """The oracle's reference step (full fp32 state updated every token, stale
     cold readout, scale/v4_native_decode.py semantics) on the host, one layer at
@@ -336,6 +375,13 @@ def main():
         log(f"v4: {v_step:.3f} ms/step, {args.B / v_step * 1e3:,.0f} tok/s, launch {v_ev * 1e3:.1f} us "
             f"-> {vb / (v_ev * 1e-3) / 1e9:,.0f} GB/s (tiers {tier_gb:.1f} GB)")
 
+    prologue = None
+    if args.only is None:
+        log("conv prologue ...")
+        prologue = bench_prologue(args, dev)
+        log(f"prologue: nssm_conv_update {prologue['nssm_conv_update_us']} us "
+            f"({prologue['nssm_conv_update_gbs']} GB/s), torch {prologue['torch_causal_conv1d_update_us']} us")
+
     head = "v4" if "v4" in res else "fresh"
     ms_step, ms_launch, ms_ev = res[head]
     per_launch_bytes = args.B * (bytes_v4_token(args.k, args.c, args.cold) if head == "v4"
@@ -383,6 +429,8 @@ def main():
         fb = args.B * bytes_fresh_token() + bytes_rotation()
         out["fresh_achieved_gbs"] = round(fb / (res["fresh"][2] * 1e-3) / 1e9, 1)
         out["speedup_v4_vs_fresh"] = round(res["fresh"][0] / res["v4"][0], 3)
+    if prologue is not None:
+        out["conv_prologue"] = prologue
     if not args.no_cpu:
         log("cpu baseline ...")
         out["cpu_baseline"] = cpu_baseline(args, args.cpu_budget)

@@ -28,6 +28,10 @@
  *                        fp8_cold_readout)
  *   nssm_rotate          scale/nemotron_retrofit.py:24-27 (ActRotMask._rot),
  *                        scale/vllm_v4_patch.py:41-45 (rot_flat)
+ *   nssm_conv_update     scale/v4_fused_decode.py:37-44 (causal_conv1d_update
+ *                        with SiLU and the x / B / C split; causal-conv1d
+ *                        1.6.2.post1, restated by transformers'
+ *                        modeling_nemotron_h.causal_conv1d_update)
  */
 #ifndef NSSM_H_
 #define NSSM_H_
@@ -39,7 +43,7 @@
 extern "C" {
 #endif
 
-#define NSSM_ABI_VERSION 3
+#define NSSM_ABI_VERSION 4
 
 /* error codes */
 #define NSSM_OK 0
@@ -50,6 +54,10 @@ extern "C" {
 #define NSSM_E_LAUNCH (-5)      /* the HIP launch reported an error      */
 #define NSSM_E_TUNING (-6)      /* launch override does not fit the dims */
 #define NSSM_E_WORKSPACE (-7)   /* workspace NULL or too small           */
+
+/* model dtypes of the conv prologue's tensors */
+#define NSSM_DT_F32 0
+#define NSSM_DT_BF16 1
 
 /* cold tier storage kinds */
 #define NSSM_COLD_FP32 0 /* one exact fp32 copy, read every token, rewritten at flush */
@@ -171,6 +179,21 @@ int nssm_fp8_readout(const float* q, const uint8_t* s8, const float* scale, floa
 /* out[t][g][m] = sum_n R[g][m][n] * in[t][g][n]; in bf16, out fp32. */
 int nssm_rotate(const uint16_t* in, const float* R, float* out, int32_t T, int32_t G, int32_t N,
                 void* stream);
+
+/* One decode token's causal depthwise conv1d update + SiLU (the mixer's
+ * prologue before the state op) and the x / B / C split, one launch:
+ *   conv_state[r][c] <- [conv_state[r][c][1:], hbc[r][c]]          (width W <= 8)
+ *   u[r][c] = silu(bias[c] + sum_w conv_state[r][c][w] weight[c][w]) (* mask[r])
+ *   x_out = u[:, :I] [b][I], B_out = u[:, I:I+GN], C_out = u[:, I+GN:] [b][GN], bf16
+ * hbc, conv_state [b][dim][W], weight [dim][W] and bias [dim] (NULL: none) are in
+ * `dtype` (NSSM_DT_F32 / NSSM_DT_BF16; in bf16 the conv and the SiLU outputs are
+ * rounded to bf16, as torch computes them in that dtype); hbc rows are hbc_stride
+ * elements apart (a slice of the in_proj output); mask NULL = 1; dim = I + 2 GN.
+ * Width 4: conv_state and weight 16-byte (fp32) / 8-byte (bf16) aligned. */
+int nssm_conv_update(int32_t b, int32_t dim, int32_t width, int32_t dtype, const void* hbc,
+                     int64_t hbc_stride, void* conv_state, const void* weight, const void* bias,
+                     const float* mask, int32_t I, int32_t GN, uint16_t* x_out, uint16_t* B_out,
+                     uint16_t* C_out, void* stream);
 
 /* Launch-shape override for the step kernels (0, 0 = automatic): heads per
  * workgroup and waves per workgroup. Process-wide; for tuning sweeps. */

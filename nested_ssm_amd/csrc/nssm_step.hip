@@ -1200,6 +1200,99 @@ __global__ void rotate_kernel(const uint16_t* __restrict__ in, const float* __re
   }
 }
 
+// ---------------------------------------------------------------------------
+// conv prologue: causal depthwise conv1d update of one decode token + SiLU, one
+// thread per (request, channel). DT: model dtype of hbc, state, weight, bias
+// (0 fp32, 1 bf16; in bf16 the conv and the SiLU outputs are rounded to bf16, as
+// torch computes them in that dtype).
+constexpr int kMaxConvW = 8;
+
+struct ConvArgs {
+  const void* hbc;
+  void* state;
+  const void* w;
+  const void* bias;
+  const float* mask;
+  uint16_t *x, *B, *C;
+  int64_t hbc_stride;
+  int32_t b, dim, W, I, GN;
+};
+
+template <int DT>
+__device__ __forceinline__ float ld_dt(const void* p, size_t i) {
+  if constexpr (DT == 0) return static_cast<const float*>(p)[i];
+  else return bf2f(static_cast<const uint16_t*>(p)[i]);
+}
+template <int DT>
+__device__ __forceinline__ void st_dt(void* p, size_t i, float v) {
+  if constexpr (DT == 0) static_cast<float*>(p)[i] = v;
+  else static_cast<uint16_t*>(p)[i] = nssm_f32_to_bf16(v);  // v is a bf16 value: exact
+}
+template <int DT>
+__device__ __forceinline__ float round_dt(float v) {
+  if constexpr (DT == 0) return v;
+  else return bf2f(nssm_f32_to_bf16(v));
+}
+
+template <int DT>
+__global__ void __launch_bounds__(256) conv_update_kernel(ConvArgs a) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)a.b * a.dim) return;
+  const int r = (int)(i / a.dim), ch = (int)(i - (int64_t)r * a.dim);
+  const int W = a.W;
+  const size_t so = ((size_t)r * a.dim + ch) * W;
+  const float xin = ld_dt<DT>(a.hbc, (size_t)r * a.hbc_stride + ch);
+  float acc = a.bias ? ld_dt<DT>(a.bias, ch) : 0.f;
+  if (W == 4) {  // the usual width: the state row and the weights as one vector each
+    float s[4], w[4];
+    if constexpr (DT == 0) {
+      const f4 sv = *reinterpret_cast<const f4*>(static_cast<const float*>(a.state) + so);
+      const f4 wv = *reinterpret_cast<const f4*>(static_cast<const float*>(a.w) + (size_t)ch * 4);
+      s[0] = sv.x; s[1] = sv.y; s[2] = sv.z; s[3] = sv.w;
+      w[0] = wv.x; w[1] = wv.y; w[2] = wv.z; w[3] = wv.w;
+      *reinterpret_cast<f4*>(static_cast<float*>(a.state) + so) = f4{s[1], s[2], s[3], xin};
+    } else {
+      const u2v sv = *reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.state) + so);
+      const u2v wv = *reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.w) + (size_t)ch * 4);
+      s[0] = __uint_as_float(sv.x << 16); s[1] = __uint_as_float(sv.x & 0xffff0000u);
+      s[2] = __uint_as_float(sv.y << 16); s[3] = __uint_as_float(sv.y & 0xffff0000u);
+      w[0] = __uint_as_float(wv.x << 16); w[1] = __uint_as_float(wv.x & 0xffff0000u);
+      w[2] = __uint_as_float(wv.y << 16); w[3] = __uint_as_float(wv.y & 0xffff0000u);
+      const uint32_t xb = nssm_f32_to_bf16(xin);
+      *reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.state) + so) =
+          u2v{(sv.x >> 16) | (sv.y << 16), (sv.y >> 16) | (xb << 16)};
+    }
+    acc = fmaf(s[1], w[0], acc);
+    acc = fmaf(s[2], w[1], acc);
+    acc = fmaf(s[3], w[2], acc);
+    acc = fmaf(xin, w[3], acc);
+  } else {
+    float s[kMaxConvW], w[kMaxConvW];
+#pragma unroll
+    for (int k = 0; k < kMaxConvW; ++k) {
+      if (k < W) {
+        s[k] = ld_dt<DT>(a.state, so + k);
+        w[k] = ld_dt<DT>(a.w, (size_t)ch * W + k);
+      }
+    }
+    // shift in the new input; out = bias + sum_w state'[w] weight[w] (cross-correlation)
+#pragma unroll
+    for (int k = 0; k < kMaxConvW; ++k) {
+      if (k < W) {
+        const float v = k < W - 1 ? s[k + 1] : xin;
+        st_dt<DT>(a.state, so + k, v);
+        acc = fmaf(v, w[k], acc);
+      }
+    }
+  }
+  float u = round_dt<DT>(acc);
+  u = round_dt<DT>(u / (1.f + expf(-u)));  // SiLU
+  if (a.mask) u = round_dt<DT>(u * a.mask[r]);
+  const uint16_t o = nssm_f32_to_bf16(u);
+  if (ch < a.I) a.x[(size_t)r * a.I + ch] = o;
+  else if (ch < a.I + a.GN) a.B[(size_t)r * a.GN + (ch - a.I)] = o;
+  else a.C[(size_t)r * a.GN + (ch - a.I - a.GN)] = o;
+}
 
 // ---------------------------------------------------------------------------
 // host side
@@ -1559,6 +1652,27 @@ int nssm_rotate(const uint16_t* in, const float* R, float* out, int32_t T, int32
   if (T == 0) return NSSM_OK;
   hipLaunchKernelGGL(rotate_kernel, dim3((unsigned)T * G), dim3(128), N * sizeof(float), (hipStream_t)stream, in,
                      R, out, G, N);
+  return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
+}
+
+int nssm_conv_update(int32_t b, int32_t dim, int32_t width, int32_t dtype, const void* hbc, int64_t hbc_stride,
+                     void* conv_state, const void* weight, const void* bias, const float* mask, int32_t I,
+                     int32_t GN, uint16_t* x_out, uint16_t* B_out, uint16_t* C_out, void* stream) {
+  if (!hbc || !conv_state || !weight || !x_out || !B_out || !C_out) return NSSM_E_NULL;
+  if (b < 0 || width < 1 || width > kMaxConvW || I < 0 || GN < 0 || dim != I + 2 * GN || hbc_stride < dim)
+    return NSSM_E_DIMS;
+  // width 4 moves a state row and a weight row as one vector each
+  if (width == 4 && (!(dtype == NSSM_DT_F32 ? aligned16(conv_state) && aligned16(weight)
+                                             : aligned8(conv_state) && aligned8(weight))))
+    return NSSM_E_ALIGN;
+  if (dtype != NSSM_DT_F32 && dtype != NSSM_DT_BF16) return NSSM_E_KIND;
+  if (b == 0 || dim == 0) return NSSM_OK;
+  ConvArgs a{hbc, conv_state, weight, bias, mask, x_out, B_out, C_out, hbc_stride, b, dim, width, I, GN};
+  const unsigned grid = (unsigned)(((int64_t)b * dim + 255) / 256);
+  if (dtype == NSSM_DT_F32)
+    hipLaunchKernelGGL(conv_update_kernel<0>, dim3(grid), dim3(256), 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(conv_update_kernel<1>, dim3(grid), dim3(256), 0, (hipStream_t)stream, a);
   return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
 }
 

@@ -120,9 +120,10 @@ class V4State(dict):
 
 # ---------------------------------------------------------------------------
 def decode_inputs(m, hidden_states, cache_params, attention_mask):
-    """One decode token through in_proj and the causal conv1d update + SiLU
-    (transformers' own functions): gate [b,1,I] and x [b,H,P], B, C [b,G,N],
-    dt [b,H] in bf16, as the kernels take them."""
+    """One decode token through in_proj and the causal conv1d update + SiLU (one
+    nssm_conv_update launch; transformers' own functions when a padding mask is
+    given): gate [b,1,I] and x [b,H,P], B, C [b,G,N], dt [b,H] in bf16, as the
+    kernels take them."""
     M = _modeling()
     b = hidden_states.shape[0]
     H, P, G, N = m.num_heads, m.head_dim, m.n_groups, m.ssm_state_size
@@ -130,11 +131,18 @@ def decode_inputs(m, hidden_states, cache_params, attention_mask):
     proj = m.in_proj(hidden_states)
     gate, hbc, dt = proj.split([m.intermediate_size, m.conv_dim, H], dim=-1)
     conv_state = cache_params.layers[m.layer_idx].conv_states[0]
-    hbc = M.causal_conv1d_update(hbc.transpose(1, 2), conv_state, m.conv1d.weight.squeeze(1), m.conv1d.bias,
-                                 activation=m.activation).transpose(1, 2)
-    hbc = M.apply_mask_to_padding_states(hbc, attention_mask)
-    x, B, C = torch.split(hbc, [m.intermediate_size, G * N, G * N], dim=-1)
     bf = torch.bfloat16
+    w = m.conv1d.weight.squeeze(1)
+    if (attention_mask is None and m.activation in ("silu", "swish") and hbc.dtype in (torch.float32, bf)
+            and conv_state.dtype == hbc.dtype and w.dtype == hbc.dtype and conv_state.is_contiguous()):
+        # conv update + SiLU + split in one HIP launch (scale/v4_fused_decode.py:42-44)
+        x, B, C = ops.conv_update(hbc[:, 0], conv_state, w.contiguous(), m.conv1d.bias, m.intermediate_size,
+                                  G * N)
+    else:
+        hbc = M.causal_conv1d_update(hbc.transpose(1, 2), conv_state, w, m.conv1d.bias,
+                                     activation=m.activation).transpose(1, 2)
+        hbc = M.apply_mask_to_padding_states(hbc, attention_mask)
+        x, B, C = torch.split(hbc, [m.intermediate_size, G * N, G * N], dim=-1)
     return (gate, x.reshape(b, H, P).to(bf).contiguous(), B.reshape(b, G, N).to(bf).contiguous(),
             C.reshape(b, G, N).to(bf).contiguous(), dt.reshape(b, H).to(bf).contiguous())
 

@@ -231,6 +231,37 @@ def rotate(X: torch.Tensor, R: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def conv_update(hbc: torch.Tensor, conv_state: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor],
+                intermediate: int, gn: int, mask: Optional[torch.Tensor] = None):
+    """One decode token's causal conv1d update + SiLU and the x / B / C split, on the
+    GPU in one launch: conv_state [b,dim,W] is updated in place; returns bf16
+    x [b, intermediate], B [b, gn], C [b, gn]. hbc [b, dim] may be a row-strided slice
+    (unit stride over channels); hbc, conv_state, weight [dim, W], bias [dim] share
+    the model dtype (fp32 or bf16). Replaces causal_conv1d_update(..., "silu") and the
+    split at scale/v4_fused_decode.py:42-44."""
+    b, dim = hbc.shape
+    W = conv_state.shape[-1]
+    dt = {torch.float32: _lib.DT_F32, torch.bfloat16: _lib.DT_BF16}.get(hbc.dtype)
+    if dt is None:
+        raise NssmError(f"conv_update: model dtype {hbc.dtype} is not fp32 or bf16")
+    if not hbc.is_cuda or hbc.stride(1) != 1:
+        raise NssmError("conv_update: hbc must be a CUDA tensor with unit stride over channels")
+    _need(conv_state, "conv_state", hbc.dtype, (b, dim, W))
+    _need(weight, "weight", hbc.dtype, (dim, W))
+    if bias is not None:
+        _need(bias, "bias", hbc.dtype, (dim,))
+    if mask is not None:
+        _need(mask, "mask", torch.float32, (b,))
+    bf = torch.bfloat16
+    x = torch.empty(b, intermediate, device=hbc.device, dtype=bf)
+    B = torch.empty(b, gn, device=hbc.device, dtype=bf)
+    C = torch.empty(b, gn, device=hbc.device, dtype=bf)
+    check(lib().nssm_conv_update(b, dim, W, dt, hbc.data_ptr(), hbc.stride(0), conv_state.data_ptr(),
+                                 weight.data_ptr(), _ptr(bias), _ptr(mask), intermediate, gn, x.data_ptr(),
+                                 B.data_ptr(), C.data_ptr(), _stream()), "nssm_conv_update")
+    return x, B, C
+
+
 def set_launch(heads_per_wg: int = 0, waves_per_wg: int = 0) -> None:
     """Override the step kernels' launch shape (0, 0 = automatic)."""
     check(lib().nssm_set_launch(heads_per_wg, waves_per_wg), "nssm_set_launch")

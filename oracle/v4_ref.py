@@ -121,6 +121,31 @@ def fp8_readout(q: torch.Tensor, S8: torch.Tensor, scale: torch.Tensor) -> torch
 
 
 # ---------------------------------------------------------------------------
+# conv prologue
+def conv_update(hbc: torch.Tensor, conv_state: torch.Tensor, weight: torch.Tensor, bias, intermediate: int,
+                gn: int, mask=None):
+    """One decode token's causal depthwise conv1d update + SiLU and the x / B / C
+    split (scale/v4_fused_decode.py:42-44 via causal-conv1d 1.6.2.post1
+    causal_conv1d_update, restated by transformers' modeling_nemotron_h):
+      state <- [state[..., 1:], hbc];  u = silu(bias + sum_w state[..., w] weight[:, w])
+    computed in the model dtype (bf16: the conv and the SiLU outputs rounded to bf16),
+    times mask[b] if given; returns bf16 x [b, I], B [b, gn], C [b, gn]; conv_state is
+    updated in place."""
+    dt = hbc.dtype
+    new = torch.cat([conv_state[..., 1:], hbc[..., None]], dim=-1)
+    conv_state.copy_(new)
+    acc = (new.float() * weight.float()[None]).sum(-1)
+    if bias is not None:
+        acc = acc + bias.float()[None]
+    u = acc.to(dt).float()
+    u = (u / (1.0 + torch.exp(-u))).to(dt).float()
+    if mask is not None:
+        u = (u * mask.float()[:, None]).to(dt).float()
+    u = u.to(torch.bfloat16)
+    return u[:, :intermediate], u[:, intermediate:intermediate + gn], u[:, intermediate + gn:]
+
+
+# ---------------------------------------------------------------------------
 # fresh (untiered) step
 def fresh_step(S: torch.Tensor, x, B, C, dt_raw, prm: LayerParams, dtype=torch.float32) -> torch.Tensor:
     """S <- exp(dt A) S + (dt B') x;  y = S C' + D x  (S updated in place, y returned).

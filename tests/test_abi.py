@@ -42,6 +42,7 @@ def test_abi_version_and_codes_match_header():
     assert int(d["NSSM_COLD_FP32"]) == _lib.COLD_FP32
     assert int(d["NSSM_COLD_BF16"]) == _lib.COLD_BF16
     assert int(d["NSSM_COLD_FP8"]) == _lib.COLD_FP8
+    assert (int(d["NSSM_DT_F32"]), int(d["NSSM_DT_BF16"])) == (_lib.DT_F32, _lib.DT_BF16)
     for code in ("NSSM_E_NULL", "NSSM_E_DIMS", "NSSM_E_ALIGN", "NSSM_E_KIND", "NSSM_E_LAUNCH", "NSSM_E_TUNING",
                  "NSSM_E_WORKSPACE"):
         msg = L.nssm_strerror(int(d[code])).decode()
@@ -146,6 +147,12 @@ def test_entry_points_validate_before_launching():
     assert L.nssm_fresh_step(ctypes.byref(prm), fake, 4, ctypes.byref(inp), fake, None, need, None) == -7
     assert L.nssm_fresh_step(ctypes.byref(prm), fake, 4, ctypes.byref(inp), fake, fake, need - 4, None) == -7
     assert L.nssm_fresh_step(ctypes.byref(prm), fake, 4, ctypes.byref(inp), fake, fake + 8, need, None) == -3
+    # conv prologue: dim = I + 2 GN, width <= 8, dtype fp32 / bf16
+    assert L.nssm_conv_update(2, 10, 4, 0, fake, 10, fake, fake, None, None, 4, 2, fake, fake, fake, None) == -2
+    assert L.nssm_conv_update(2, 8, 9, 0, fake, 8, fake, fake, None, None, 4, 2, fake, fake, fake, None) == -2
+    assert L.nssm_conv_update(2, 8, 4, 5, fake, 8, fake, fake, None, None, 4, 2, fake, fake, fake, None) == -4
+    assert L.nssm_conv_update(2, 8, 4, 0, None, 8, fake, fake, None, None, 4, 2, fake, fake, fake, None) == -1
+    assert L.nssm_conv_update(0, 8, 4, 0, fake, 8, fake, fake, None, None, 4, 2, fake, fake, fake, None) == 0
     # the exact readout needs a cold tier; x must be 8-byte aligned
     tier = _lib.Tier(4, 32, 4, _lib.COLD_KINDS["off"], *([fake] * 10))
     assert L.nssm_v4_step_exact(ctypes.byref(prm), ctypes.byref(tier), ctypes.byref(inp), fake, fake, 1 << 30,

@@ -1,0 +1,37 @@
+"""GPU: the conv prologue (nssm_conv_update) against the oracle's conv_update on the
+same inputs: the conv state update bit for bit; x / B / C (bf16) equal up to a
+one-ulp bf16 flip in at most 1% of the elements (the fp32 sum of the window runs
+in another order than the oracle's)."""
+import pytest
+import torch
+
+import oracle
+from nested_ssm_amd import conv_update
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dtype,b,I,gn,W,with_bias,with_mask", [
+    (torch.float32, 4, 128, 32, 4, True, False), (torch.bfloat16, 4, 128, 32, 4, True, True),
+    (torch.bfloat16, 64, 10240, 1024, 4, True, False), (torch.float32, 3, 64, 16, 2, False, True)])
+def test_conv_update_matches_oracle(dtype, b, I, gn, W, with_bias, with_mask):
+    gen = torch.Generator().manual_seed(b + I + W)
+    dim = I + 2 * gn
+    extra = 24  # hbc is a slice of a wider in_proj output (row stride dim + 2 extra)
+    proj = torch.randn(b, dim + 2 * extra, generator=gen).to(dtype)
+    hbc = proj[:, extra:extra + dim]
+    st = torch.randn(b, dim, W, generator=gen).to(dtype)
+    w = (torch.randn(dim, W, generator=gen) * 0.5).to(dtype)
+    bias = torch.randn(dim, generator=gen).to(dtype) if with_bias else None
+    mask = (torch.arange(b) % 3 != 1).float() if with_mask else None
+    st_ref = st.clone()
+    xr, Br, Cr = oracle.conv_update(hbc.clone(), st_ref, w, bias, I, gn, mask=mask)
+    proj_d = proj.cuda()
+    st_d = st.cuda()
+    x, B, C = conv_update(proj_d[:, extra:extra + dim], st_d, w.cuda(), None if bias is None else bias.cuda(), I, gn,
+                          mask=None if mask is None else mask.cuda())
+    assert torch.equal(st_d.cpu(), st_ref)
+    got = torch.cat([x, B, C], dim=-1).cpu().float()
+    want = torch.cat([xr, Br, Cr], dim=-1).float()
+    assert torch.allclose(got, want, rtol=2 ** -7, atol=1e-6)
+    assert float((got != want).float().mean()) <= 0.01

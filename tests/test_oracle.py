@@ -374,3 +374,49 @@ def test_hot_only_step_is_the_fresh_trajectory_restricted_to_hot_columns():
         want = torch.einsum("bhpn,bhn->bhp", traj[t][..., :k], Cp[..., :k]) + x.double() * prm64.D[None, :, None]
         assert torch.allclose(y, want, atol=1e-11)
         assert torch.allclose(Sh, traj[t][..., :k], atol=1e-12)
+
+
+# --------------------------------------------------------------------------- conv prologue
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_conv_update_matches_transformers_causal_conv1d_update(dtype):
+    """The conv prologue against transformers' causal_conv1d_update (the installed
+    library's restatement of causal-conv1d's kernel) with SiLU, in the model dtype;
+    the state update is bit-exact, the outputs agree to the bf16 cast."""
+    from transformers.models.nemotron_h import modeling_nemotron_h as M
+
+    gen = torch.Generator().manual_seed(50)
+    b, I, gn, W = 3, 40, 16, 4
+    dim = I + 2 * gn
+    hbc = torch.randn(b, dim, generator=gen).to(dtype)
+    st = torch.randn(b, dim, W, generator=gen).to(dtype)
+    w = (torch.randn(dim, W, generator=gen) * 0.5).to(dtype)
+    bias = torch.randn(dim, generator=gen).to(dtype)
+    st_ref = st.clone()
+    out = M.causal_conv1d_update(hbc[..., None], st_ref, w, bias, activation="silu")[..., 0]
+    st_me = st.clone()
+    x, B, C = oracle.conv_update(hbc, st_me, w, bias, I, gn)
+    assert torch.equal(st_me, st_ref)
+    got = torch.cat([x, B, C], dim=-1).float()
+    want = out.to(torch.bfloat16).float()
+    assert torch.allclose(got, want, rtol=2 ** -7, atol=1e-6)
+    assert float((got != want).float().mean()) < 0.02
+
+
+def test_conv_update_matches_fp64_window_loop():
+    gen = torch.Generator().manual_seed(51)
+    b, I, gn, W = 2, 8, 4, 3
+    dim = I + 2 * gn
+    hbc = torch.randn(b, dim, generator=gen)
+    st = torch.randn(b, dim, W, generator=gen)
+    w = torch.randn(dim, W, generator=gen)
+    bias = torch.randn(dim, generator=gen)
+    mask = torch.tensor([1.0, 0.0])
+    want = torch.zeros(b, dim, dtype=torch.float64)
+    for r in range(b):
+        for ch in range(dim):
+            win = [float(st[r, ch, k]) for k in range(1, W)] + [float(hbc[r, ch])]
+            v = float(bias[ch]) + sum(win[k] * float(w[ch, k]) for k in range(W))
+            want[r, ch] = v / (1.0 + math.exp(-v)) * float(mask[r])
+    x, B, C = oracle.conv_update(hbc, st.clone(), w, bias, I, gn, mask=mask)
+    got = torch.cat([x, B, C], dim=-1).double()
+    assert torch.allclose(got, want.to(torch.bfloat16).double(), rtol=2 ** -7, atol=1e-6)
