@@ -242,15 +242,33 @@ def bench_prologue(args, dev):
         x, B, C = torch.split(o, [I, gn, gn], dim=-1)
         x.to(bf).contiguous(), B.to(bf).contiguous(), C.to(bf).contiguous()
 
+    # the epilogue norm: y fp32 [B, I], gate a bf16 slice of the in_proj output, group 1280
+    from nested_ssm_amd import gated_rmsnorm
+
+    y = torch.randn(args.B, I, device=dev, generator=g)
+    gate = proj[:, :I]
+    norm = M.Zamba2RMSNormGated(I, group_size=I // G, eps=1e-5).to(dev, bf)
+
+    def ours_norm(_):
+        gated_rmsnorm(y, gate, norm.weight, I // G, 1e-5)
+
+    def stock_norm(_):
+        norm(y.to(bf)[:, None], gate[:, None])
+
     n = 200
     res = {}
-    for name, fn in (("nssm_conv_update", ours), ("torch_causal_conv1d_update", stock)):
+    for name, fn in (("nssm_conv_update", ours), ("torch_causal_conv1d_update", stock),
+                     ("nssm_gated_rmsnorm", ours_norm), ("torch_Zamba2RMSNormGated", stock_norm)):
         ms, _ = timed(fn, n, 20, 1)
         res[name + "_us"] = round(ms * 1e3, 2)
     nbytes = args.B * (dim * 2 + 2 * dim * W * 2 + dim * 2) + dim * W * 2 + dim * 2
     res["algorithmic_bytes"] = nbytes
     res["nssm_conv_update_gbs"] = round(nbytes / (res["nssm_conv_update_us"] * 1e-6) / 1e9, 1)
-    res["shape"] = f"B={args.B}, conv_dim={dim} (x {I}, B/C {gn} each), width {W}, bf16"
+    nb_norm = args.B * I * (4 + 2 + 2) + I * 2
+    res["norm_algorithmic_bytes"] = nb_norm
+    res["nssm_gated_rmsnorm_gbs"] = round(nb_norm / (res["nssm_gated_rmsnorm_us"] * 1e-6) / 1e9, 1)
+    res["shape"] = (f"B={args.B}, conv_dim={dim} (x {I}, B/C {gn} each), width {W}; norm over {I} channels "
+                    f"in groups of {I // G}; bf16")
     return res
 
 
@@ -380,7 +398,9 @@ def main():
         log("conv prologue ...")
         prologue = bench_prologue(args, dev)
         log(f"prologue: nssm_conv_update {prologue['nssm_conv_update_us']} us "
-            f"({prologue['nssm_conv_update_gbs']} GB/s), torch {prologue['torch_causal_conv1d_update_us']} us")
+            f"({prologue['nssm_conv_update_gbs']} GB/s), torch {prologue['torch_causal_conv1d_update_us']} us; "
+            f"epilogue norm: nssm_gated_rmsnorm {prologue['nssm_gated_rmsnorm_us']} us "
+            f"({prologue['nssm_gated_rmsnorm_gbs']} GB/s), torch {prologue['torch_Zamba2RMSNormGated_us']} us")
 
     head = "v4" if "v4" in res else "fresh"
     ms_step, ms_launch, ms_ev = res[head]
@@ -430,7 +450,7 @@ def main():
         out["fresh_achieved_gbs"] = round(fb / (res["fresh"][2] * 1e-3) / 1e9, 1)
         out["speedup_v4_vs_fresh"] = round(res["fresh"][0] / res["v4"][0], 3)
     if prologue is not None:
-        out["conv_prologue"] = prologue
+        out["prologue_epilogue"] = prologue
     if not args.no_cpu:
         log("cpu baseline ...")
         out["cpu_baseline"] = cpu_baseline(args, args.cpu_budget)

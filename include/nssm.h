@@ -28,6 +28,8 @@
  *                        fp8_cold_readout)
  *   nssm_rotate          scale/nemotron_retrofit.py:24-27 (ActRotMask._rot),
  *                        scale/vllm_v4_patch.py:41-45 (rot_flat)
+ *   nssm_gated_rmsnorm   scale/v4_native_decode.py:170-171 (self.norm(y, gate):
+ *                        transformers' Zamba2RMSNormGated of the mixer)
  *   nssm_conv_update     scale/v4_fused_decode.py:37-44 (causal_conv1d_update
  *                        with SiLU and the x / B / C split; causal-conv1d
  *                        1.6.2.post1, restated by transformers'
@@ -43,7 +45,7 @@
 extern "C" {
 #endif
 
-#define NSSM_ABI_VERSION 4
+#define NSSM_ABI_VERSION 5
 
 /* error codes */
 #define NSSM_OK 0
@@ -194,6 +196,16 @@ int nssm_conv_update(int32_t b, int32_t dim, int32_t width, int32_t dtype, const
                      int64_t hbc_stride, void* conv_state, const void* weight, const void* bias,
                      const float* mask, int32_t I, int32_t GN, uint16_t* x_out, uint16_t* B_out,
                      uint16_t* C_out, void* stream);
+
+/* The mixer's epilogue before out_proj, one launch: y (fp32 [b][I], D x included)
+ * cast to the model dtype, gated by silu(gate), RMS-normalised per group of gs
+ * channels and scaled by weight (transformers' Zamba2RMSNormGated):
+ *   v = dtype(y) * silu(gate)  (fp32);  out = weight * dtype(v * rsqrt(mean_group(v^2) + eps))
+ * gate rows are gate_stride elements apart (a slice of the in_proj output); gate,
+ * weight [I] and out [b][I] in `dtype` (NSSM_DT_F32 / NSSM_DT_BF16); gs <= 2048. */
+int nssm_gated_rmsnorm(int32_t b, int32_t I, int32_t gs, int32_t dtype, const float* y,
+                       const void* gate, int64_t gate_stride, const void* weight, float eps,
+                       void* out, void* stream);
 
 /* Launch-shape override for the step kernels (0, 0 = automatic): heads per
  * workgroup and waves per workgroup. Process-wide; for tuning sweeps. */

@@ -7,6 +7,8 @@ The kernels live in libnssm_hip.so (C ABI: include/nssm.h), built in-tree by
 `python -m nested_ssm_amd.build`. There is no CPU fallback.
 """
 from ._lib import COLD_KINDS, NssmError, lib  # noqa: F401
-from .ops import LayerParams, V4Tier, conv_update, fp8_cold_readout, fresh_step, rotate, set_launch  # noqa: F401
+from .ops import (  # noqa: F401
+    LayerParams, V4Tier, conv_update, fp8_cold_readout, fresh_step, gated_rmsnorm, rotate, set_launch,
+)
 
 __version__ = "0.1.0"

@@ -65,6 +65,7 @@ def lib():
     L.nssm_v4_materialize.argtypes = [P_(LayerParams), P_(Tier), c_vp, c_i32, c_vp, c_vp]
     L.nssm_fp8_readout.argtypes = [c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_vp]
     L.nssm_rotate.argtypes = [c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_vp]
+    L.nssm_gated_rmsnorm.argtypes = [c_i32, c_i32, c_i32, c_i32, c_vp, c_vp, c_i64, c_vp, ctypes.c_float, c_vp, c_vp]
     L.nssm_conv_update.argtypes = [c_i32, c_i32, c_i32, c_i32, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32,
                                    c_vp, c_vp, c_vp, c_vp]
     L.nssm_set_launch.argtypes = [c_i32, c_i32]
@@ -72,7 +73,8 @@ def lib():
     L.nssm_host_e4m3fn_to_f32.argtypes = [c_vp, c_vp, ctypes.c_int64]
     L.nssm_host_f32_to_bf16.argtypes = [c_vp, c_vp, ctypes.c_int64]
     for fn in ("nssm_fresh_step", "nssm_v4_step", "nssm_v4_step_exact", "nssm_v4_join", "nssm_v4_materialize",
-               "nssm_fp8_readout", "nssm_rotate", "nssm_conv_update", "nssm_set_launch", "nssm_tier_sizes"):
+               "nssm_fp8_readout", "nssm_rotate", "nssm_conv_update", "nssm_gated_rmsnorm", "nssm_set_launch",
+               "nssm_tier_sizes"):
         getattr(L, fn).restype = ctypes.c_int
     for fn in ("nssm_host_f32_to_e4m3fn", "nssm_host_e4m3fn_to_f32", "nssm_host_f32_to_bf16"):
         getattr(L, fn).restype = None
@@ -89,6 +91,7 @@ def check(rc: int, what: str) -> None:
 # symbols include/nssm.h declares (checked by the CPU test-suite)
 EXPORTED = ("nssm_tier_sizes", "nssm_step_workspace_bytes", "nssm_fresh_step", "nssm_v4_step", "nssm_v4_step_exact",
             "nssm_v4_join",
-            "nssm_v4_materialize", "nssm_fp8_readout", "nssm_rotate", "nssm_conv_update", "nssm_set_launch",
+            "nssm_v4_materialize", "nssm_fp8_readout", "nssm_rotate", "nssm_conv_update", "nssm_gated_rmsnorm",
+            "nssm_set_launch",
             "nssm_host_f32_to_e4m3fn", "nssm_host_e4m3fn_to_f32", "nssm_host_f32_to_bf16",
             "nssm_strerror", "nssm_abi_version")

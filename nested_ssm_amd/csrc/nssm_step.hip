@@ -1295,6 +1295,66 @@ __global__ void __launch_bounds__(256) conv_update_kernel(ConvArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// epilogue: gated RMSNorm of the mixer output, one workgroup (256 threads) per
+// (request, group of gs channels); DT: model dtype of gate, weight and out.
+constexpr int kNormThreads = 256;
+constexpr int kNormPer = 8;  // channels per thread: gs <= 2048
+
+struct NormArgs {
+  const float* y;
+  const void* gate;
+  const void* w;
+  void* out;
+  int64_t gate_stride;
+  int32_t I, gs;
+  float eps;
+};
+
+template <int DT>
+__global__ void __launch_bounds__(kNormThreads) gated_norm_kernel(NormArgs a) {
+  __shared__ float sRed[kNormThreads / 64];
+  const int ng = a.I / a.gs;
+  const int r = blockIdx.x / ng, grp = blockIdx.x - r * ng;
+  const int tid = threadIdx.x;
+  const size_t c0 = (size_t)grp * a.gs;
+  float v[kNormPer];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < kNormPer; ++k) {
+    const int i = tid + k * kNormThreads;
+    v[k] = 0.f;
+    if (i < a.gs) {
+      const float yv = round_dt<DT>(a.y[(size_t)r * a.I + c0 + i]);  // y in the model dtype
+      const float gv = ld_dt<DT>(a.gate, (size_t)r * a.gate_stride + c0 + i);
+      v[k] = yv * (gv / (1.f + expf(-gv)));  // y * silu(gate), fp32
+      ss = fmaf(v[k], v[k], ss);
+    }
+  }
+  // group sum of squares: wave (DPP + cross-row shuffles), then across the waves
+  ss += dpp<0xB1>(ss);
+  ss += dpp<0x4E>(ss);
+  ss += dpp<0x141>(ss);
+  ss += __shfl_xor(ss, 8);
+  ss += __shfl_xor(ss, 16);
+  ss += __shfl_xor(ss, 32);
+  if ((tid & 63) == 0) sRed[tid >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormThreads / 64; ++i) tot += sRed[i];
+  const float rs = 1.f / sqrtf(tot / (float)a.gs + a.eps);
+#pragma unroll
+  for (int k = 0; k < kNormPer; ++k) {
+    const int i = tid + k * kNormThreads;
+    if (i < a.gs) {
+      const float o = ld_dt<DT>(a.w, c0 + i) * round_dt<DT>(v[k] * rs);
+      if constexpr (DT == 0) static_cast<float*>(a.out)[(size_t)r * a.I + c0 + i] = o;
+      else static_cast<uint16_t*>(a.out)[(size_t)r * a.I + c0 + i] = nssm_f32_to_bf16(o);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host side
 int g_hpw_override = 0, g_waves_override = 0;
 constexpr size_t kMaxLds = 64 * 1024;
@@ -1673,6 +1733,21 @@ int nssm_conv_update(int32_t b, int32_t dim, int32_t width, int32_t dtype, const
     hipLaunchKernelGGL(conv_update_kernel<0>, dim3(grid), dim3(256), 0, (hipStream_t)stream, a);
   else
     hipLaunchKernelGGL(conv_update_kernel<1>, dim3(grid), dim3(256), 0, (hipStream_t)stream, a);
+  return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
+}
+
+int nssm_gated_rmsnorm(int32_t b, int32_t I, int32_t gs, int32_t dtype, const float* y, const void* gate,
+                       int64_t gate_stride, const void* weight, float eps, void* out, void* stream) {
+  if (!y || !gate || !weight || !out) return NSSM_E_NULL;
+  if (b < 0 || I <= 0 || gs <= 0 || I % gs || gs > kNormThreads * kNormPer || gate_stride < I) return NSSM_E_DIMS;
+  if (dtype != NSSM_DT_F32 && dtype != NSSM_DT_BF16) return NSSM_E_KIND;
+  if (b == 0) return NSSM_OK;
+  NormArgs a{y, gate, weight, out, gate_stride, I, gs, eps};
+  const dim3 grid((unsigned)b * (unsigned)(I / gs));
+  if (dtype == NSSM_DT_F32)
+    hipLaunchKernelGGL(gated_norm_kernel<0>, grid, dim3(kNormThreads), 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(gated_norm_kernel<1>, grid, dim3(kNormThreads), 0, (hipStream_t)stream, a);
   return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
 }
 

@@ -148,9 +148,16 @@ def decode_inputs(m, hidden_states, cache_params, attention_mask):
 
 
 def decode_epilogue(m, y, gate, dtype):
-    """y [b,H,P] fp32 (D x included) -> gated RMSNorm -> out_proj."""
+    """y [b,H,P] fp32 (D x included) -> gated RMSNorm (one nssm_gated_rmsnorm launch for
+    the mixer's Zamba2RMSNormGated) -> out_proj."""
     b = y.shape[0]
-    out = m.norm(y.to(dtype).reshape(b, 1, -1), gate)
+    norm = m.norm
+    g = gate[:, 0]
+    if (type(norm).__name__ == "Zamba2RMSNormGated" and g.dtype == dtype and norm.weight.dtype == dtype
+            and dtype in (torch.float32, torch.bfloat16) and g.stride(-1) == 1):
+        out = ops.gated_rmsnorm(y.reshape(b, -1), g, norm.weight, norm.group_size, norm.variance_epsilon)
+        return m.out_proj(out.reshape(b, 1, -1))
+    out = norm(y.to(dtype).reshape(b, 1, -1), gate)
     return m.out_proj(out.to(dtype))
 
 

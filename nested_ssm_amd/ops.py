@@ -262,6 +262,29 @@ def conv_update(hbc: torch.Tensor, conv_state: torch.Tensor, weight: torch.Tenso
     return x, B, C
 
 
+def gated_rmsnorm(y: torch.Tensor, gate: torch.Tensor, weight: torch.Tensor, group_size: int, eps: float,
+                  out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The mixer's epilogue norm on the GPU in one launch: y [b, I] fp32 (D x included)
+    cast to the model dtype, times silu(gate), RMS-normalised per group of group_size
+    channels, times weight (transformers' Zamba2RMSNormGated; self.norm(y, gate) at
+    scale/v4_native_decode.py:170-171). gate [b, I] may be a row-strided slice; gate,
+    weight [I] and the returned out [b, I] share the model dtype (fp32 or bf16)."""
+    b, I = y.shape
+    dt = {torch.float32: _lib.DT_F32, torch.bfloat16: _lib.DT_BF16}.get(gate.dtype)
+    if dt is None:
+        raise NssmError(f"gated_rmsnorm: model dtype {gate.dtype} is not fp32 or bf16")
+    _need(y, "y", torch.float32, (b, I))
+    _need(weight, "weight", gate.dtype, (I,))
+    if not gate.is_cuda or gate.stride(1) != 1 or tuple(gate.shape) != (b, I):
+        raise NssmError("gated_rmsnorm: gate must be a CUDA [b, I] tensor with unit stride over channels")
+    if out is None:
+        out = torch.empty(b, I, device=y.device, dtype=gate.dtype)
+    _need(out, "out", gate.dtype, (b, I))
+    check(lib().nssm_gated_rmsnorm(b, I, group_size, dt, y.data_ptr(), gate.data_ptr(), gate.stride(0),
+                                   weight.data_ptr(), float(eps), out.data_ptr(), _stream()), "nssm_gated_rmsnorm")
+    return out
+
+
 def set_launch(heads_per_wg: int = 0, waves_per_wg: int = 0) -> None:
     """Override the step kernels' launch shape (0, 0 = automatic)."""
     check(lib().nssm_set_launch(heads_per_wg, waves_per_wg), "nssm_set_launch")

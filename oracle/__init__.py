@@ -34,8 +34,11 @@ Pinning status of each function (how it is checked, in tests/test_oracle.py):
   hot_only_step     the hot columns of an fp64 fresh trajectory (they never read the cold ones)
   conv_update       transformers' own causal_conv1d_update (silu) in fp32 and bf16, and an
                     fp64 loop over the shifted window
+  gated_rmsnorm     transformers' own Zamba2RMSNormGated module in fp32 and bf16, and an
+                    fp64 per-group loop
 """
 from .v4_ref import (  # noqa: F401
-    LayerParams, NativeV4, TieredV4, conv_update, fp8_readout, fresh_step, hot_only_step, make_layer_params,
+    LayerParams, NativeV4, TieredV4, conv_update, fp8_readout, fresh_step, gated_rmsnorm, hot_only_step,
+    make_layer_params,
     make_rotation, make_state, make_step_inputs, quant_fp8, read_fp8, rotate, softplus_dt,
 )

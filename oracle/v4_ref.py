@@ -145,6 +145,18 @@ def conv_update(hbc: torch.Tensor, conv_state: torch.Tensor, weight: torch.Tenso
     return u[:, :intermediate], u[:, intermediate:intermediate + gn], u[:, intermediate + gn:]
 
 
+def gated_rmsnorm(y: torch.Tensor, gate: torch.Tensor, weight: torch.Tensor, group_size: int, eps: float):
+    """The mixer's epilogue norm (transformers' Zamba2RMSNormGated, applied as
+    self.norm(y.to(dtype), gate) at scale/v4_native_decode.py:170-171): y cast to the
+    model dtype, times silu(gate) in fp32, RMS-normalised per group, cast back, times weight."""
+    dt = gate.dtype
+    v = y.to(dt).float() * torch.nn.functional.silu(gate.float())
+    b, I = v.shape
+    vg = v.view(b, I // group_size, group_size)
+    vg = vg * torch.rsqrt(vg.pow(2).mean(-1, keepdim=True) + eps)
+    return weight * vg.view(b, I).to(dt)
+
+
 # ---------------------------------------------------------------------------
 # fresh (untiered) step
 def fresh_step(S: torch.Tensor, x, B, C, dt_raw, prm: LayerParams, dtype=torch.float32) -> torch.Tensor:

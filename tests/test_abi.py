@@ -153,6 +153,11 @@ def test_entry_points_validate_before_launching():
     assert L.nssm_conv_update(2, 8, 4, 5, fake, 8, fake, fake, None, None, 4, 2, fake, fake, fake, None) == -4
     assert L.nssm_conv_update(2, 8, 4, 0, None, 8, fake, fake, None, None, 4, 2, fake, fake, fake, None) == -1
     assert L.nssm_conv_update(0, 8, 4, 0, fake, 8, fake, fake, None, None, 4, 2, fake, fake, fake, None) == 0
+    # epilogue norm: I a multiple of gs, gs <= 2048, dtype fp32 / bf16
+    assert L.nssm_gated_rmsnorm(2, 100, 30, 0, fake, fake, 100, fake, ctypes.c_float(1e-5), fake, None) == -2
+    assert L.nssm_gated_rmsnorm(2, 4096, 4096, 0, fake, fake, 4096, fake, ctypes.c_float(1e-5), fake, None) == -2
+    assert L.nssm_gated_rmsnorm(2, 128, 64, 3, fake, fake, 128, fake, ctypes.c_float(1e-5), fake, None) == -4
+    assert L.nssm_gated_rmsnorm(2, 128, 64, 0, None, fake, 128, fake, ctypes.c_float(1e-5), fake, None) == -1
     # the exact readout needs a cold tier; x must be 8-byte aligned
     tier = _lib.Tier(4, 32, 4, _lib.COLD_KINDS["off"], *([fake] * 10))
     assert L.nssm_v4_step_exact(ctypes.byref(prm), ctypes.byref(tier), ctypes.byref(inp), fake, fake, 1 << 30,

@@ -420,3 +420,37 @@ def test_conv_update_matches_fp64_window_loop():
     x, B, C = oracle.conv_update(hbc, st.clone(), w, bias, I, gn, mask=mask)
     got = torch.cat([x, B, C], dim=-1).double()
     assert torch.allclose(got, want.to(torch.bfloat16).double(), rtol=2 ** -7, atol=1e-6)
+
+
+# --------------------------------------------------------------------------- epilogue
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_gated_rmsnorm_matches_transformers_module(dtype):
+    from transformers.models.nemotron_h import modeling_nemotron_h as M
+
+    gen = torch.Generator().manual_seed(60)
+    b, I, gs = 3, 96, 32
+    norm = M.Zamba2RMSNormGated(I, group_size=gs, eps=1e-5).to(dtype)
+    with torch.no_grad():
+        norm.weight.copy_(torch.randn(I, generator=gen).to(dtype))
+    y = torch.randn(b, I, generator=gen)
+    gate = torch.randn(b, I, generator=gen).to(dtype)
+    with torch.no_grad():
+        want = norm(y.to(dtype), gate)
+    got = oracle.gated_rmsnorm(y, gate, norm.weight.detach(), gs, 1e-5)
+    assert got.dtype == want.dtype
+    assert torch.equal(got, want)
+
+
+def test_gated_rmsnorm_matches_fp64_group_loop():
+    gen = torch.Generator().manual_seed(61)
+    b, I, gs = 2, 12, 4
+    y, gate, w = torch.randn(b, I, generator=gen), torch.randn(b, I, generator=gen), torch.randn(I, generator=gen)
+    want = torch.zeros(b, I, dtype=torch.float64)
+    for r in range(b):
+        for g0 in range(0, I, gs):
+            v = [float(y[r, i]) * float(gate[r, i]) / (1 + math.exp(-float(gate[r, i]))) for i in range(g0, g0 + gs)]
+            rs = 1 / math.sqrt(sum(t * t for t in v) / gs + 1e-6)
+            for j, i in enumerate(range(g0, g0 + gs)):
+                want[r, i] = float(w[i]) * v[j] * rs
+    got = oracle.gated_rmsnorm(y, gate, w, gs, 1e-6)
+    assert torch.allclose(got.double(), want, rtol=1e-6, atol=1e-7)
