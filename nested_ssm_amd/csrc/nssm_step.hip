@@ -1084,43 +1084,57 @@ __global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
   }
 }
 
-// join: full state -> tiers; one workgroup per (request, head)
-__global__ void join_kernel(StepArgs a, const float* __restrict__ S, const int32_t* __restrict__ phase, int K,
-                            int kind) {
+// join: full state -> tiers; one workgroup (4 waves) per (request, head). Rows go in
+// units of 8 in the stream kernel's segment mapping (float4 per lane per 32-column
+// segment): hot columns stored as they are, cold columns through cold_store (the fp32
+// copy, or the fp32 master and the bf16 / e4m3 read copy with its row amax scale,
+// scale/vllm_v4_patch.py:106-111).
+template <int K, int COLD>
+__global__ void __launch_bounds__(256) join_kernel(StepArgs a, const float* __restrict__ S,
+                                                   const int32_t* __restrict__ phase) {
+  constexpr int HS = K / 32;
+  constexpr int CS = COLD == NSSM_COLD_NONE ? 0 : (kN - K) / 32;
   const int bi = blockIdx.x / a.H, h = blockIdx.x % a.H;
   const int slot = a.slot_ids ? a.slot_ids[bi] : bi;
   if (slot < 0 || slot >= a.slots) return;
-  const int NC = kN - K;
-  const float* src = S + ((size_t)bi * a.H + h) * a.P * kN;
-  const size_t row0 = ((size_t)slot * a.H + h) * a.P;
-  // element pass (coalesced): hot columns, and the fp32 cold copy or master
-  for (int i = threadIdx.x; i < a.P * kN; i += blockDim.x) {
-    const int p = i / kN, n = i - p * kN;
-    const float v = src[i];
-    if (n < K) {
-      a.hot[(row0 + p) * K + n] = v;
-    } else if (kind != NSSM_COLD_NONE) {
-      float* dst = kind == NSSM_COLD_FP32 ? static_cast<float*>(a.cold) : a.master;
-      dst[(row0 + p) * NC + (n - K)] = v;
-      if (kind == NSSM_COLD_BF16) static_cast<uint16_t*>(a.cold)[(row0 + p) * NC + (n - K)] = nssm_f32_to_bf16(v);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+  const int q = lane & 7, rr = lane >> 3;
+  for (int u = wave; u < (a.P >> 3); u += nw) {
+    const int p = u * 8 + rr;
+    const size_t row = ((size_t)slot * a.H + h) * a.P + p;
+    const f4* src = reinterpret_cast<const f4*>(S + (((size_t)bi * a.H + h) * a.P + p) * kN) + q;
+    f4 hv[HS];
+#pragma unroll
+    for (int s2 = 0; s2 < HS; ++s2) hv[s2] = ld_stream(src + 8 * s2);
+    if constexpr (CS > 0) {
+      float v[CS][4];
+#pragma unroll
+      for (int s2 = 0; s2 < CS; ++s2) {
+        const f4 t = ld_stream(src + 8 * (HS + s2));
+        v[s2][0] = t.x; v[s2][1] = t.y; v[s2][2] = t.z; v[s2][3] = t.w;
+      }
+      cold_store<COLD, CS>(a, row, q, v);
     }
+    f4* hp = reinterpret_cast<f4*>(a.hot + row * K) + q;
+#pragma unroll
+    for (int s2 = 0; s2 < HS; ++s2) st_stream(hv[s2], hp + 8 * s2);
   }
-  if (kind == NSSM_COLD_FP8) {  // row pass: per-row amax scale, scale/vllm_v4_patch.py:106-111
-    for (int p = threadIdx.x; p < a.P; p += blockDim.x) {
-      const float* r = src + (size_t)p * kN + K;
-      float am = 0.f;
-      for (int n = 0; n < NC; ++n) am = fmaxf(am, fabsf(r[n]));
-      const float sc = am / 448.0f + 1e-12f;
-      uint8_t* d8 = static_cast<uint8_t*>(a.cold) + (row0 + p) * NC;
-      for (int n = 0; n < NC; ++n) d8[n] = nssm_f32_to_e4m3fn(r[n] / sc);
-      a.scale[row0 + p] = sc;
-    }
-  }
-  if (threadIdx.x == 0) {
+  if (tid == 0) {
     const size_t o = (size_t)slot * a.H + h;
     a.t[o] = phase ? phase[bi] : 0;
     a.nv[o] = 0;
     a.glog[o] = 0.f;
+  }
+}
+
+template <int K>
+void launch_join(const StepArgs& a, int kind, const float* state, const int32_t* phase, unsigned grid,
+                 hipStream_t st) {
+  switch (kind) {
+    case NSSM_COLD_FP32: hipLaunchKernelGGL((join_kernel<K, NSSM_COLD_FP32>), dim3(grid), dim3(256), 0, st, a, state, phase); break;
+    case NSSM_COLD_BF16: hipLaunchKernelGGL((join_kernel<K, NSSM_COLD_BF16>), dim3(grid), dim3(256), 0, st, a, state, phase); break;
+    case NSSM_COLD_FP8: hipLaunchKernelGGL((join_kernel<K, NSSM_COLD_FP8>), dim3(grid), dim3(256), 0, st, a, state, phase); break;
+    default: hipLaunchKernelGGL((join_kernel<K, NSSM_COLD_NONE>), dim3(grid), dim3(256), 0, st, a, state, phase); break;
   }
 }
 
@@ -1660,6 +1674,7 @@ int nssm_v4_join(const nssm_layer_params* prm, const nssm_tier* tier, const floa
   if (rc) return rc;
   if ((rc = check_tier(tier, false))) return rc;
   if (!state) return NSSM_E_NULL;
+  if (!aligned16(state)) return NSSM_E_ALIGN;
   if (b < 0 || (!slot_ids && b > tier->slots)) return NSSM_E_DIMS;
   if (b == 0) return NSSM_OK;
   StepArgs a = {};
@@ -1669,8 +1684,12 @@ int nssm_v4_join(const nssm_layer_params* prm, const nssm_tier* tier, const floa
   a.P = prm->P;
   a.G = prm->G;
   a.HG = prm->H / prm->G;
-  hipLaunchKernelGGL(join_kernel, dim3((unsigned)b * prm->H), dim3(128), 0, (hipStream_t)stream, a, state, phase,
-                     (int)tier->k_hot, (int)tier->cold_kind);
+  const unsigned grid = (unsigned)b * prm->H;
+  switch (tier->k_hot) {
+    case 32: launch_join<32>(a, tier->cold_kind, state, phase, grid, (hipStream_t)stream); break;
+    case 64: launch_join<64>(a, tier->cold_kind, state, phase, grid, (hipStream_t)stream); break;
+    default: launch_join<96>(a, tier->cold_kind, state, phase, grid, (hipStream_t)stream); break;
+  }
   return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
 }
 
