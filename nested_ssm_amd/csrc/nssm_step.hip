@@ -116,9 +116,15 @@ __device__ __forceinline__ float softplus_f(float v) { return v > 20.f ? v : log
 #ifndef NSSM_NT_STORE
 #define NSSM_NT_STORE 1
 #endif
-// units (8-row blocks) whose loads a wave keeps in flight together
+// units (8-row blocks) whose loads a wave keeps in flight together. Measured on
+// MI355X (B = 256, 27 layers, k_hot = 32, ms per step at c = 4 / 16): bf16 cold 2 units
+// 9.80 / 7.33, 3 units 9.42 / 7.21, 4 units 10.02 / 8.19; fp32 and e4m3 best with 2
+// (fp32 with 3: 10.28 / 9.27).
 #ifndef NSSM_UNROLL
 #define NSSM_UNROLL 2
+#endif
+#ifndef NSSM_UNROLL_BF16
+#define NSSM_UNROLL_BF16 3
 #endif
 
 template <class T>
@@ -710,7 +716,7 @@ __device__ __forceinline__ void stream_units(const StepArgs& a, int slot, int bi
                                              const float (&Cc)[Cfg<K, COLD>::CSR][4],
                                              const float (&Cq)[Cfg<K, COLD>::CWR]) {
   constexpr bool TIERED = Cfg<K, COLD>::TIERED;
-  constexpr int U = NSSM_UNROLL;
+  constexpr int U = COLD == NSSM_COLD_BF16 ? NSSM_UNROLL_BF16 : NSSM_UNROLL;
   const int H = a.H, P = a.P, c = a.c;
   for (int u0 = wave; u0 < units; u0 += U * nw) {
     UnitRaw<K, COLD> d[U];
@@ -804,12 +810,6 @@ __device__ __forceinline__ void stream_body(const StepArgs& a) {
   } else if constexpr (TIERED) {
     extern __shared__ float lds[];
     constexpr int NC = C::NC;
-    // the first unit's loads go out before the window staging
-    UnitRaw<K, COLD> dcur;
-    if (wave < units) {
-      const int j = wave / RG, p = (wave - j * RG) * 8 + rr;
-      unit_load<K, COLD>(a, ((size_t)slot * H + h0 + j) * P + p, ((size_t)bi * H + h0 + j) * P + p, q, dcur);
-    }
     // the window of every head of the block: B' cold columns of the group and
     // w_i x_i of each head (all heads of a slot share t, so they share m)
     const int m = min(max((int)hdb[HD_M], 1), c);
@@ -821,13 +821,13 @@ __device__ __forceinline__ void stream_body(const StepArgs& a) {
                           a.ring_x + (((size_t)slot * H + h0 + j) * c + (c - m)) * P, a.x + ((size_t)bi * H + h0 + j) * P,
                           ws.w + ((size_t)bi * H + h0 + j) * c, j == 0, tid, blockDim.x);
     __syncthreads();
-    // software pipeline: the next unit's loads are in flight during this one's compute
+    // one unit at a time: loading the next unit during this one's replay needs more
+    // registers than the 5 waves per SIMD leave, and spills (measured slower)
     for (int u = wave; u < units; u += nw) {
-      UnitRaw<K, COLD> dnext;
-      const int un = u + nw;
-      if (un < units) {
-        const int j = un / RG, p = (un - j * RG) * 8 + rr;
-        unit_load<K, COLD>(a, ((size_t)slot * H + h0 + j) * P + p, ((size_t)bi * H + h0 + j) * P + p, q, dnext);
+      UnitRaw<K, COLD> dcur;
+      {
+        const int j = u / RG, p = (u - j * RG) * 8 + rr;
+        unit_load<K, COLD>(a, ((size_t)slot * H + h0 + j) * P + p, ((size_t)bi * H + h0 + j) * P + p, q, dcur);
       }
       const int j = u / RG;
       const int p = (u - j * RG) * 8 + rr;
@@ -840,7 +840,6 @@ __device__ __forceinline__ void stream_body(const StepArgs& a) {
         uint16_t* rx = a.ring_x + (sh * c + (int)hd[HD_POS]) * P;
         unit_compute<K, COLD, EXACT>(a, sh, rh, p, q, dcur, rx, true, hd, Bh, Ch, Cc, Cq);
       }
-      dcur = dnext;
     }
   }
 }
