@@ -126,6 +126,9 @@ __device__ __forceinline__ float softplus_f(float v) { return v > 20.f ? v : log
 #ifndef NSSM_UNROLL_BF16
 #define NSSM_UNROLL_BF16 3
 #endif
+#ifndef NSSM_UNROLL_FP8
+#define NSSM_UNROLL_FP8 2
+#endif
 
 template <class T>
 __device__ __forceinline__ T ld_stream(const T* p) {
@@ -716,7 +719,7 @@ __device__ __forceinline__ void stream_units(const StepArgs& a, int slot, int bi
                                              const float (&Cc)[Cfg<K, COLD>::CSR][4],
                                              const float (&Cq)[Cfg<K, COLD>::CWR]) {
   constexpr bool TIERED = Cfg<K, COLD>::TIERED;
-  constexpr int U = COLD == NSSM_COLD_BF16 ? NSSM_UNROLL_BF16 : NSSM_UNROLL;
+  constexpr int U = COLD == NSSM_COLD_BF16 ? NSSM_UNROLL_BF16 : COLD == NSSM_COLD_FP8 ? NSSM_UNROLL_FP8 : NSSM_UNROLL;
   const int H = a.H, P = a.P, c = a.c;
   for (int u0 = wave; u0 < units; u0 += U * nw) {
     UnitRaw<K, COLD> d[U];
@@ -1439,7 +1442,10 @@ struct Launch {
 
 int pick_launch(int H, int G, int P, int K, int c, Launch* out, int kind = NSSM_COLD_FP32) {
   const int HG = H / G, RG = P / 8;
-  int hpw = 1;
+  // heads per stream workgroup, measured on MI355X (B = 256, 27 layers, k_hot = 32, ms per
+  // step at c = 4 / 16): fp32 cold 1 head 9.02 / 8.09, 2 heads 9.50 / 8.35; bf16 9.68 / 7.22
+  // vs 9.48 / 7.10; e4m3 8.01 / 6.14 vs 7.98 / 5.75
+  int hpw = (kind == NSSM_COLD_BF16 || kind == NSSM_COLD_FP8) && K < kN && HG % 2 == 0 ? 2 : 1;
   if (g_hpw_override > 0) {
     if (HG % g_hpw_override) return NSSM_E_TUNING;
     hpw = g_hpw_override;
