@@ -178,7 +178,9 @@ def bench_v4(args, layers, inputs, dev):
     for l in range(args.layers):
         t = V4Tier(args.B, H, P, G, k_hot=args.k, c=args.c, cold=args.cold, device=dev)
         S0 = rand_state(args.B, dev, g)
-        t.join(layers[l], S0)
+        phase = (torch.randint(0, args.c, (args.B,), device=dev, generator=g, dtype=torch.int32)
+                 if args.ragged else None)
+        t.join(layers[l], S0, phase=phase)
         del S0
         tiers.append(t)
         ys.append(torch.empty(args.B, H, P, device=dev))
@@ -342,6 +344,8 @@ def main():
     ap.add_argument("--cold", default="fp32", choices=["fp32", "bf16", "fp8"])
     ap.add_argument("--exact", action="store_true", help="v4 with the rank-c exact correction readout (corr=1)")
     ap.add_argument("--graph", action="store_true", help="time HIP graph replays of whole steps (all layers)")
+    ap.add_argument("--ragged", action="store_true",
+                    help="v4 requests join with random phases (each token flushes about B/c of them)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the host baseline")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of host work for the baseline")
@@ -424,7 +428,8 @@ def main():
         "data": "synthetic (seeded; bf16 x/B/C/dt, fp32 state ~N(0,0.1^2), random orthogonal R per layer-group)",
         "config": {
             "workload": (f"{head} state op, Nemotron-Nano-9B-v2 mixer shape, {args.layers} layers, B={args.B}"
-                         + (f", k_hot={args.k}, c={args.c}, {args.cold} cold, phase-aligned" if head == "v4" else "")
+                         + (f", k_hot={args.k}, c={args.c}, {args.cold} cold, "
+                            f"{'random phases' if args.ragged else 'phase-aligned'}" if head == "v4" else "")
                          + (", exact (corr=1) readout" if head == "v4" and args.exact else "")
                          + (", HIP graph replay" if args.graph else "")),
             "layers": args.layers, "B": args.B, "H": H, "P": P, "N": N, "G": G,
