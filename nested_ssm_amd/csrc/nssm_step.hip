@@ -64,26 +64,36 @@ struct StepArgs {
   int32_t b, slots, H, P, G, HG, c, K, hpw, nhb;
   int32_t prb;    // requests per prep workgroup
   int32_t exact;  // rank-c exact correction readout instead of the stale one
+  int32_t split;  // the flush kernel runs after the stream kernel (prep writes the pair flags)
+  int32_t fch;    // window tokens the flush kernel stages in LDS at a time (multiple of 4)
   float dt_min;
 };
 
 // Workspace carve-up for b requests (floats): rotated B and C [b][G][N] each,
-// per-head scalars [b][H][HD_STRIDE], window weights [b][H][c] (flush) and
-// correction coefficients [b][H][c] (exact readout).
+// per-head scalars [b][H][HD_STRIDE]; tiered steps (c > 0) add the per-(request,
+// group) flush flags [b][G] (int32, padded to a multiple of 4), window weights
+// [b][H][c] (flush) and correction coefficients [b][H][c] (exact readout).
 // HD_SNAPF is the factor of the snapshot readout: exp(glog) (stale, the decay up
 // to the previous token) or exp(glog + a) (exact, inclusive of this token).
 enum { HD_DT = 0, HD_A, HD_DECAY, HD_SNAPF, HD_D, HD_FLUSH, HD_DTOT, HD_M, HD_POS, HD_STRIDE = 12 };
+__host__ __device__ constexpr size_t flag_words(int b, int G, int c) {
+  return c > 0 ? (((size_t)b * G + 3) & ~(size_t)3) : 0;
+}
 struct Ws {
   float *B, *C, *hd, *w, *cw;
+  int* fg;
   __host__ __device__ Ws(float* base, int b, int H, int G, int c) {
     B = base;
     C = B + (size_t)b * G * kN;
     hd = C + (size_t)b * G * kN;
-    w = hd + (size_t)b * H * HD_STRIDE;
+    fg = reinterpret_cast<int*>(hd + (size_t)b * H * HD_STRIDE);
+    w = hd + (size_t)b * H * HD_STRIDE + flag_words(b, G, c);
     cw = w + (size_t)b * H * c;
   }
 };
-size_t ws_floats(int b, int H, int G, int c) { return (size_t)b * (2 * G * kN + H * HD_STRIDE + 2 * H * c); }
+size_t ws_floats(int b, int H, int G, int c) {
+  return (size_t)b * (2 * G * kN + H * HD_STRIDE + 2 * H * c) + flag_words(b, G, c);
+}
 
 __device__ __forceinline__ float bf2f(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
 
@@ -162,7 +172,7 @@ constexpr int kPrepReq = 8;  // requests per prep workgroup (at most)
 template <bool TIERED>
 __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
   __shared__ float sX[2 * kPrepReq][kN];  // B (j < 8) and C (j >= 8) of the block's requests
-  __shared__ int sSlot[kPrepReq], sTr[kPrepReq], sNvr[kPrepReq];
+  __shared__ int sSlot[kPrepReq], sTr[kPrepReq], sNvr[kPrepReq], sFl[kPrepReq];
   // exact readout: B', C' of the block and s_j = C'_cold . B'_j over each window
   __shared__ float sRot[TIERED ? 2 * kPrepReq : 1][TIERED ? kN : 1];
   __shared__ float sS[TIERED ? kPrepReq : 1][TIERED ? kMaxC : 1];
@@ -195,6 +205,7 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
       for (int kb = 0; kb < kN / 16; ++kb)
         ra[t2][kb] = *reinterpret_cast<const f4*>(Rg + (size_t)((wave + 4 * t2) * 16 + li) * kN + kb * 16 + 4 * lk);
   }
+  if (tid < kPrepReq) sFl[tid] = 0;
   const int hr = tid / HG, hh = tid - hr * HG;  // the head thread's request and head
   const bool head_thread = tid < nreq * HG;
   const int h = g * HG + hh, bi = r0 + hr;
@@ -324,6 +335,7 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
       hd[HD_SNAPF] = expf(exact ? gl + av : gl);
       hd[HD_FLUSH] = flush ? 1.f : 0.f;
       hd[HD_POS] = (float)pos;
+      if (flush) sFl[hr] = 1;
       if (flush || exact) {
         // window = the nv buffered tokens at ring [pos-nv, pos) and this one (at a
         // flush pos = c-1): w_i = exp(sum_{l>i} a_l) dt_i, total decay exp(sum_l a_l);
@@ -371,6 +383,14 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
       hd[HD_DTOT] = 1.f;
       hd[HD_M] = 0.f;
       hd[HD_POS] = 0.f;
+    }
+  }
+  // 4. the flush kernel's per-(request, group) flags: some head of the pair flushes
+  // (every pair of the block is written, so no flag survives from an earlier token)
+  if constexpr (TIERED) {
+    if (a.split) {
+      __syncthreads();
+      if (tid < nreq) ws.fg[(size_t)(r0 + tid) * G + g] = sFl[tid];
     }
   }
 }
@@ -873,90 +893,175 @@ __global__ void __launch_bounds__(kMaxWaves * 64) fresh_stream_kernel(StepArgs a
 
 // ---------------------------------------------------------------------------
 // flush: the cold tier of every (request, head) whose phase wraps at this token.
-// A workgroup walks a strided set of items and takes the flushing ones. Per item:
+// Per item:
 //   cold <- exp(sum a) cold + Delta,  Delta[p][n] = sum_i w_i x_i[p] B'_i[n]
 // over the window (the buffered tokens and this one), scale/v4_fused_decode.py:76-85,
 // and y += exp(glog) (stale read copy . C'[K:]) — the stream kernel wrote the hot part
 // and D x of these heads' y and left their cold columns alone.
 //
+// Work split: prep flags each (request, group) pair with a flushing head. Every
+// workgroup ranks the flagged pairs (a block-wide prefix count over the flags) and
+// takes the flushing items j * gridDim.x + blockIdx.x of the ranked order (pair rank
+// r covers items r HG .. r HG + HG - 1, one per head), so F flushing heads spread
+// over min(F, grid) workgroups whatever the requests' phases.
+//
 // Delta is contracted on the matrix cores as 16 x 16 tiles (p-tile pt, n-tile nt) of
-// v_mfma_f32_16x16x4_f32: A = B'^T (16 n x 4 tokens), B = w x (4 tokens x 16 p), the
-// window staged in LDS in chunks of 16 tokens (zero past its end). Lane (li, lk) of a
-// tile holds Delta[pt*16 + li][nt*16 + 4 lk .. +3]; the state is read and written in
-// that mapping. Each wave holds kMfmaTiles tiles, in pairs that cover whole 128-byte
-// row segments (flush_tile); a pass covers as many tiles as the waves hold, for e4m3
-// whole rows only (the row scale needs all of a row's tiles). When an item takes one
-// pass, the next item's state tiles are loaded while this one contracts and stores.
-// Per-tile readout partials and row maxima go through LDS and are summed in a fixed
-// order.
+// v_mfma_f32_16x16x4_f32: A = B'^T (16 n x 4 tokens), B = w x (4 tokens x 16 p). The
+// window is staged in LDS by DMA fch tokens at a time (the whole window when it fits,
+// all its loads in flight together; zero past its end). Lane (li, lk) of a tile holds
+// Delta[pt*16 + li][nt*16 + 4 lk .. +3]; the state is read and written in that mapping,
+// its loads issued before the window's. Each wave holds kMfmaTiles tiles; a pass covers
+// as many tiles as the waves hold (e4m3: whole rows only, the row scale needs all of a
+// row's tiles). Per-tile readout partials and row maxima go through LDS and are summed
+// in a fixed order.
 constexpr int kFlushWaves = 8;
-constexpr int kFlushGrid = 2048;  // workgroups of a flush launch (at most)
+constexpr int kFlushPerCU = 2;  // flush workgroups per CU (the kernel's occupancy: 4 waves per SIMD)
+constexpr int kFlushList = 64;  // items a workgroup lists at a time
 
+#define NSSM_GLOBAL(p) ((const __attribute__((address_space(1))) void*)(p))
+#define NSSM_LOCAL(p) ((__attribute__((address_space(3))) void*)(p))
+
+// Stage window tokens [k0, k0 + kn) of one head into LDS with gfx950's LDS DMA
+// (global_load_lds: lane L of a wave instruction writes its granule at base + L * size,
+// no registers in between): sB[e][n] = B'_tok[K + n] (16-byte granules), sX[e][p] =
+// x_tok[p] as bf16 (4-byte granules), sW[e] = w_tok. Window token m - 1 is this token
+// (B' from the workspace, x from the inputs); token tok < m - 1 sits at ring position
+// c - m + tok (rb0 and rx0 point at the ring rows of window token 0). Wave w issues the
+// instructions w, w + nw, ... of each block; the caller waits (vmcnt) and barriers.
+template <int NC>
+__device__ __forceinline__ void stage_window_dma(float* sB, uint16_t* sX, float* sW, int k0, int kn, int m, int P,
+                                                 const float* rb0, const float* bcur, const uint16_t* rx0,
+                                                 const uint16_t* xcur, const float* wgt, int wave, int lane,
+                                                 int nw) {
+  constexpr int NB4 = NC / 4;  // 16-byte granules per token of B'
+  const int nb = kn * NB4;
+  for (int q = wave; q * 64 < nb; q += nw) {
+    const int gi = q * 64 + lane;
+    if (gi < nb) {
+      const int e = gi / NB4, tok = k0 + e;
+      const float* src = (tok < m - 1 ? rb0 + (size_t)tok * NC : bcur) + 4 * (gi - e * NB4);
+      __builtin_amdgcn_global_load_lds(NSSM_GLOBAL(src), NSSM_LOCAL(sB + q * 256), 16, 0, 0);
+    }
+  }
+  const int P2 = P >> 1, nx = kn * P2;  // 4-byte granules (2 x bf16) per token of x
+  for (int q = wave; q * 64 < nx; q += nw) {
+    const int gi = q * 64 + lane;
+    if (gi < nx) {
+      const int e = gi / P2, tok = k0 + e;
+      const uint16_t* src = (tok < m - 1 ? rx0 + (size_t)tok * P : xcur) + 2 * (gi - e * P2);
+      __builtin_amdgcn_global_load_lds(NSSM_GLOBAL(src), NSSM_LOCAL(sX + q * 128), 4, 0, 0);
+    }
+  }
+  if (wave == nw - 1 && lane < kn)
+    __builtin_amdgcn_global_load_lds(NSSM_GLOBAL(wgt + k0 + lane), NSSM_LOCAL(sW), 4, 0, 0);
+}
 
 template <int K, int COLD>
 __global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
   using C = Cfg<K, COLD>;
-  constexpr int NC = C::NC, NT = C::NT, nw = kFlushWaves;
+  constexpr int NC = C::NC, NT = C::NT, nw = kFlushWaves, nthr = kFlushWaves * 64;
   constexpr int TPP = COLD == NSSM_COLD_FP8 ? (nw * kMfmaTiles / NT) * NT : nw * kMfmaTiles;  // tiles per pass
   static_assert(TPP >= NT, "a pass must hold a whole row");
   extern __shared__ float lds[];
-  // the round's flushing items and their scalars (loaded in parallel by the thread
-  // that finds the item)
-  __shared__ int sItem[kFlushWaves * 64], sSlot[kFlushWaves * 64], sM[kFlushWaves * 64];
-  __shared__ float sDtot[kFlushWaves * 64], sEg[kFlushWaves * 64];
-  __shared__ int sCount;
+  // this workgroup's listed items and their scalars (loaded by the thread that lists
+  // the item); sM = 0 marks an item with nothing to flush
+  __shared__ int sItem[kFlushList], sSlot[kFlushList], sM[kFlushList];
+  __shared__ float sDtot[kFlushList], sEg[kFlushList];
+  __shared__ int sWave[kFlushWaves];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, lk = lane >> 4;
-  const int H = a.H, P = a.P, c = a.c;
-  const int items = a.b * H;
-  const Ws ws(a.ws, a.b, H, a.G, c);
-  float* sBc = lds;              // [16][NC]
-  float* sU = sBc + 16 * NC;     // [16][P]
-  float* sPart = sU + 16 * P;    // [P][NT] readout partials of the old read copy
+  const int H = a.H, P = a.P, c = a.c, G = a.G, HG = a.HG, fch = a.fch;
+  const Ws ws(a.ws, a.b, H, G, c);
+  float* sBc = lds;                                             // [fch][NC] B'
+  uint16_t* sX = reinterpret_cast<uint16_t*>(sBc + fch * NC);   // [fch][P] x (bf16)
+  float* sW = sBc + fch * NC + fch * P / 2;                     // [fch] window weights
+  float* sPart = sW + fch;       // [P][NT] readout partials of the old read copy
   float* sAmx = sPart + P * NT;  // [P][NT] row maxima of the new values (e4m3 only)
   const int ntot = (P / 16) * NT;
 
-  for (int r0 = blockIdx.x; r0 < items; r0 += gridDim.x * blockDim.x) {
-    // this round's items: r0 + tid * gridDim.x; keep the flushing ones
-    if (tid == 0) sCount = 0;
-    __syncthreads();
-    {
-      const int it = r0 + tid * gridDim.x;
-      if (it < items) {
-        const int bi = it / H;
-        const int slot = a.slot_ids ? a.slot_ids[bi] : bi;
-        const float* hd = ws.hd + (size_t)it * HD_STRIDE;
-        const float fl = hd[HD_FLUSH], mm = hd[HD_M], dt = hd[HD_DTOT], eg = hd[HD_SNAPF];
-        if (slot >= 0 && slot < a.slots && fl != 0.f) {
-          const int k = atomicAdd(&sCount, 1);
+  // 1. rank the flagged pairs: thread tid counts pairs [p0, p1) (whole int4 words of
+  // the flag array, which is padded to a multiple of 4), then a block-wide exclusive
+  // prefix of the counts
+  const int npair = a.b * G;
+  const int per = (((npair + nthr - 1) / nthr) + 3) & ~3;
+  const int p0 = min(tid * per, npair), p1 = min(p0 + per, npair);
+  int cnt = 0;
+  for (int p = p0; p < p1; p += 4) {
+    const int4 f = *reinterpret_cast<const int4*>(ws.fg + p);
+    cnt += (f.x != 0) + (p + 1 < p1 && f.y != 0) + (p + 2 < p1 && f.z != 0) + (p + 3 < p1 && f.w != 0);
+  }
+  int incl = cnt;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int v = __shfl_up(incl, o);
+    if (lane >= o) incl += v;
+  }
+  if (lane == 63) sWave[wave] = incl;
+  __syncthreads();
+  int rank0 = incl - cnt, total = 0;
+#pragma unroll
+  for (int w2 = 0; w2 < nw; ++w2) {
+    const int s = sWave[w2];
+    rank0 += w2 < wave ? s : 0;
+    total += s;
+  }
+  const int64_t fitems = (int64_t)total * HG;  // heads of flagged pairs
+  const int bx = blockIdx.x, grid = gridDim.x;  // grid >= HG (host)
+  const int nmine = fitems > bx ? (int)((fitems - bx + grid - 1) / grid) : 0;
+
+  for (int j0 = 0; j0 < nmine; j0 += kFlushList) {
+    const int jn = min(kFlushList, nmine - j0);
+    __syncthreads();  // the previous list is consumed
+    // 2. list items j0 .. j0 + jn - 1: pair rank r holds item j when
+    // r HG <= j grid + bx < (r + 1) HG (at most one j per rank, as grid >= HG)
+    if (cnt > 0) {
+      int r = rank0;
+      for (int p = p0; p < p1; ++p) {
+        if (ws.fg[p] == 0) continue;
+        const int64_t lo = (int64_t)r * HG - bx;
+        const int64_t j = lo <= 0 ? 0 : (lo + grid - 1) / grid;
+        const int64_t ci = j * grid + bx;
+        if (ci < (int64_t)(r + 1) * HG && j >= j0 && j < j0 + jn) {
+          const int hh = (int)(ci - (int64_t)r * HG);
+          const int bi = p / G, g = p - bi * G;
+          const int it = bi * H + g * HG + hh;
+          const int slot = a.slot_ids ? a.slot_ids[bi] : bi;
+          const float* hd = ws.hd + (size_t)it * HD_STRIDE;
+          const int k = (int)(j - j0);
+          const bool ok = slot >= 0 && slot < a.slots && hd[HD_FLUSH] != 0.f;
           sItem[k] = it;
           sSlot[k] = slot;
-          sM[k] = min(max((int)mm, 1), c);
-          sDtot[k] = dt;
-          sEg[k] = eg;
+          sM[k] = ok ? min(max((int)hd[HD_M], 1), c) : 0;
+          sDtot[k] = hd[HD_DTOT];
+          sEg[k] = hd[HD_SNAPF];
         }
+        ++r;
       }
     }
     __syncthreads();
-    const int n_items = sCount;
-    for (int k = 0; k < n_items; ++k) {
-      const int it = sItem[k], slot = sSlot[k], m = sM[k];
+
+    // 3. the listed items
+    for (int k = 0; k < jn; ++k) {
+      const int m = sM[k];
+      if (m == 0) continue;  // workgroup-uniform
+      const int it = sItem[k], slot = sSlot[k];
       const float dtot = sDtot[k], eg = sEg[k];
-      const int bi = it / H, h = it - bi * H, g = h / a.HG;
+      const int bi = it / H, h = it - bi * H, g = h / HG;
       float yv = 0.f;  // this head's y (hot part and D x, from the stream kernel)
       if (tid < P) yv = a.y[(size_t)it * P + tid];
-      const float* bcur = ws.B + ((size_t)bi * a.G + g) * kN + K;  // this token's B'[K:]
-      const float* cq0 = ws.C + ((size_t)bi * a.G + g) * kN + K;   // C'[K:]
-      const float* rb0 = a.ring_b + (((size_t)slot * a.G + g) * c + (c - m)) * NC;
+      const float* bcur = ws.B + ((size_t)bi * G + g) * kN + K;  // this token's B'[K:]
+      const float* cq0 = ws.C + ((size_t)bi * G + g) * kN + K;   // C'[K:]
+      const float* rb0 = a.ring_b + (((size_t)slot * G + g) * c + (c - m)) * NC;
       const uint16_t* rx0 = a.ring_x + (((size_t)slot * H + h) * c + (c - m)) * P;
       const uint16_t* xcur = a.x + (size_t)it * P;
       const float* wgt = ws.w + (size_t)it * c;
       const size_t row0 = ((size_t)slot * H + h) * P;
       const float* src = COLD == NSSM_COLD_FP32 ? static_cast<const float*>(a.cold) : a.master;
+      const bool whole = m <= fch;  // the window fits in LDS: staged once
 
       for (int t0 = 0; t0 < ntot; t0 += TPP) {
         const int ntile = min(TPP, ntot - t0);
-        // the pass's state tiles are loaded before the window work
+        // the pass's state tiles are loaded before the window
         f4 old[kMfmaTiles];
         u2v rb16[COLD == NSSM_COLD_BF16 ? kMfmaTiles : 1];
         uint32_t r8[COLD == NSSM_COLD_FP8 ? kMfmaTiles : 1];
@@ -979,25 +1084,34 @@ __global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
         f4 acc[kMfmaTiles];
 #pragma unroll
         for (int i = 0; i < kMfmaTiles; ++i) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
-        for (int k0 = 0; k0 < m; k0 += 16) {
-          const int kn = min(16, m - k0);
-          __syncthreads();  // the previous chunk (or item) is consumed
-          stage_window<NC, 2>(sBc, sU, k0, kn, m, P, rb0, bcur, rx0, xcur, wgt, true, tid, blockDim.x);
-          __syncthreads();
+        for (int k0 = 0; k0 < m; k0 += fch) {
+          const int kn = min(fch, m - k0);
+          if (!whole || t0 == 0) {  // a whole window is staged once, in the first pass
+            __syncthreads();  // the previous chunk (or item: window and partials) is consumed
+            stage_window_dma<NC>(sBc, sX, sW, k0, kn, m, P, rb0, bcur, rx0, xcur, wgt, wave, lane, nw);
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA has landed in LDS
+            __syncthreads();
+          }
+          // k-step s pairs token kk0 + lk of A = B'^T (16 n x 4 tokens) with the same token
+          // of B = w x (4 tokens x 16 p); the tiles' steps are independent
+          for (int kk0 = 0; kk0 < kn; kk0 += 4) {
+            const int kk = kk0 + lk;
+            const bool live = kk < kn;
+            const int kc = live ? kk : kn - 1;
+            const float wk = sW[kc];
+            float av[kMfmaTiles], bv[kMfmaTiles];
 #pragma unroll
-          for (int i = 0; i < kMfmaTiles; ++i) {
-            if (wave + i * nw < ntile) {  // wave-uniform
-              const int tt = t0 + wave + i * nw;
-              const int pt = tt / NT, nt = tt % NT;
-              for (int kk0 = 0; kk0 < kn; kk0 += 4) {
-                const int kk = kk0 + lk;
-                const int kc = kk < kn ? kk : kn - 1;
-                float av = sBc[kc * NC + nt * 16 + li];
-                float bv = sU[kc * P + pt * 16 + li];
-                if (kk >= kn) av = bv = 0.f;
-                acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[i], 0, 0, 0);
+            for (int i = 0; i < kMfmaTiles; ++i) {
+              if (wave + i * nw < ntile) {  // wave-uniform
+                const int tt = t0 + wave + i * nw;
+                const int pt = tt / NT, nt = tt % NT;
+                av[i] = live ? sBc[kc * NC + nt * 16 + li] : 0.f;
+                bv[i] = live ? wk * bf2f(sX[kc * P + pt * 16 + li]) : 0.f;
               }
             }
+#pragma unroll
+            for (int i = 0; i < kMfmaTiles; ++i)
+              if (wave + i * nw < ntile) acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], bv[i], acc[i], 0, 0, 0);
           }
         }
         // new = total decay x old + Delta; readout partial of the old read copy
@@ -1082,7 +1196,6 @@ __global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
         a.y[(size_t)it * P + tid] = fmaf(eg, pc, yv);
       }
     }
-    __syncthreads();  // sItem and sCount are rewritten by the next round
   }
 }
 
@@ -1400,6 +1513,19 @@ int check_ws(const nssm_layer_params* prm, int b, int c, const void* ws, int64_t
   return NSSM_OK;
 }
 
+// compute units of the current device (cached per device)
+int cu_count() {
+  static int cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
 // largest divisor of n not above cap
 int divisor_at_most(int n, int cap) {
   for (int d = cap < n ? cap : n; d >= 1; --d)
@@ -1407,11 +1533,21 @@ int divisor_at_most(int n, int cap) {
   return 1;
 }
 
-// flush kernel LDS: 16-token window chunk, per-tile readout partials (+ e4m3 row maxima)
-size_t flush_lds_bytes(int P, int K, int kind) {
+// flush kernel LDS: a window chunk of fch tokens (B' fp32, x bf16, weights), per-tile
+// readout partials (+ e4m3 row maxima); the kernel's own lists take under 2 KB more
+size_t flush_lds_bytes(int P, int K, int kind, int fch) {
   const int NC = kN - K;
   const size_t tiles = (size_t)P * (NC / 16);
-  return ((size_t)16 * NC + (size_t)16 * P + tiles * (kind == NSSM_COLD_FP8 ? 2 : 1)) * sizeof(float);
+  return ((size_t)fch * NC + (size_t)fch * P / 2 + fch + tiles * (kind == NSSM_COLD_FP8 ? 2 : 1)) * sizeof(float);
+}
+// window tokens the flush kernel stages at a time: the whole window (c rounded up to the
+// matrix-core step of 4 tokens) when it fits, else the most that fit (0: none fit)
+int flush_chunk(int P, int K, int kind, int c) {
+  const size_t budget = kMaxLds - 2048;
+  const size_t fixed = flush_lds_bytes(P, K, kind, 0), per_tok = (size_t)(kN - K + P / 2 + 1) * sizeof(float);
+  const int fit = fixed >= budget ? 0 : (int)((budget - fixed) / per_tok) & ~3;
+  const int want = (c + 3) & ~3;
+  return want < fit ? want : fit;
 }
 
 // windows shorter than this are flushed by the stream kernel (VALU replay of the window
@@ -1460,7 +1596,7 @@ int pick_launch(int H, int G, int P, int K, int c, Launch* out, int kind = NSSM_
                                          : divisor_at_most(hpw * RG, 5);
   if (waves > kMaxWaves) return NSSM_E_TUNING;
   const size_t lds = fused ? fused_lds_bytes(hpw, P, c, K) : 0;
-  if (lds > kMaxLds || (tiered && !fused && flush_lds_bytes(P, K, kind) > kMaxLds)) return NSSM_E_DIMS;
+  if (lds > kMaxLds || (tiered && !fused && flush_chunk(P, K, kind, c) < 4)) return NSSM_E_DIMS;
   out->hpw = hpw;
   out->waves = waves;
   out->fused = fused;
@@ -1540,10 +1676,13 @@ int launch_pair(const StepArgs& a, const Launch& L, hipStream_t st) {
   else if (TIERED && a.exact) launch_stream<K, COLD, false, TIERED>(sgrid, sblock, 0, st, a);
   else launch_stream<K, COLD, false, false>(sgrid, sblock, 0, st, a);
   if constexpr (TIERED) {
-    const int items = a.b * a.H;
-    const int grid = items < kFlushGrid ? items : kFlushGrid;
+    // one resident round of workgroups: an empty launch dispatches no more than that,
+    // and a full flush keeps every workgroup busy to the end
+    const int items = a.b * a.H, cap = kFlushPerCU * cu_count();
+    int grid = items < cap ? items : cap;
+    if (grid < a.HG) grid = a.HG;  // the kernel's listing needs grid >= HG (items >= HG)
     hipLaunchKernelGGL((flush_kernel<K, COLD>), dim3((unsigned)grid), dim3(kFlushWaves * 64),
-                       flush_lds_bytes(a.P, K, COLD), st, a);
+                       flush_lds_bytes(a.P, K, COLD, a.fch), st, a);
   }
   return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
 }
@@ -1576,6 +1715,8 @@ int v4_step(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step
   if ((rc = pick_launch(prm->H, prm->G, prm->P, tier->k_hot, tier->c, &L, tier->cold_kind))) return rc;
   a.hpw = L.hpw;
   a.nhb = prm->H / L.hpw;
+  a.split = !L.fused && tier->cold_kind != NSSM_COLD_NONE;
+  a.fch = a.split ? flush_chunk(prm->P, tier->k_hot, tier->cold_kind, tier->c) : 0;
   hipStream_t st = (hipStream_t)stream;
   switch (tier->k_hot) {
     case 32: return dispatch_kind<32>(a, tier->cold_kind, L, st);

@@ -141,8 +141,10 @@ def test_entry_points_validate_before_launching():
     # workspace: NULL, too small, misaligned
     need = L.nssm_step_workspace_bytes(4, 8, 1, 128, 0)
     assert need == 4 * (2 * 128 + 12 * 8) * 4
-    # tiered: plus window weights and exact-readout coefficients [b][H][c] each
-    assert L.nssm_step_workspace_bytes(4, 8, 1, 128, 4) == need + 2 * 4 * 8 * 4 * 4
+    # tiered: plus per-(request, group) flush flags [b][G] (padded to a multiple of 4),
+    # window weights and exact-readout coefficients [b][H][c] each
+    assert L.nssm_step_workspace_bytes(4, 8, 1, 128, 4) == need + 4 * 4 + 2 * 4 * 8 * 4 * 4
+    assert L.nssm_step_workspace_bytes(3, 8, 2, 128, 4) == 4 * (3 * (2 * 2 * 128 + 12 * 8 + 2 * 8 * 4) + 8)
     assert L.nssm_step_workspace_bytes(4, 8, 3, 128, 4) == -2
     assert L.nssm_fresh_step(ctypes.byref(prm), fake, 4, ctypes.byref(inp), fake, None, need, None) == -7
     assert L.nssm_fresh_step(ctypes.byref(prm), fake, 4, ctypes.byref(inp), fake, fake, need - 4, None) == -7
