@@ -39,15 +39,16 @@ def bytes_fresh_token():
     return 2 * H * P * N * 4 + bytes_io()
 
 
-def bytes_v4_token(k, c, cold):
+def bytes_v4_token(k, c, cold, master="fp32"):
     nc = N - k
     esz = {"fp32": 4, "bf16": 2, "fp8": 1}[cold]
     hot = 2 * H * P * k * 4
     read = H * P * nc * esz + (H * P * 4 if cold == "fp8" else 0)
-    if cold == "fp32":
-        flush = H * P * nc * 4  # rewrite of the single copy
+    if cold == "fp32" or (cold == "bf16" and master == "bf16"):
+        flush = H * P * nc * esz  # rewrite of the single copy (its read is the stale read)
     else:  # master read + master write + read-copy write (+ scale)
-        flush = H * P * nc * (4 + 4 + esz) + (H * P * 4 if cold == "fp8" else 0)
+        msz = 4 if master == "fp32" else 2
+        flush = H * P * nc * (2 * msz + esz) + (H * P * 4 if cold == "fp8" else 0)
     ring_entry = H * P * 2 + H * 4 + G * nc * 4  # x bf16, dt, B' cold
     ring = (c - 1) / c * 2 * ring_entry  # written by c-1 of c tokens, read once at the flush
     return hot + read + flush / c + ring + bytes_io()
@@ -176,7 +177,7 @@ def bench_v4(args, layers, inputs, dev):
     g = torch.Generator(device=dev).manual_seed(args.seed + 1)
     tiers, ys = [], []
     for l in range(args.layers):
-        t = V4Tier(args.B, H, P, G, k_hot=args.k, c=args.c, cold=args.cold, device=dev)
+        t = V4Tier(args.B, H, P, G, k_hot=args.k, c=args.c, cold=args.cold, device=dev, master=args.master)
         S0 = rand_state(args.B, dev, g)
         phase = (torch.randint(0, args.c, (args.B,), device=dev, generator=g, dtype=torch.int32)
                  if args.ragged else None)
@@ -284,7 +285,7 @@ def cpu_baseline(args, budget_s):
     gen = torch.Generator().manual_seed(args.seed)
     prm = oracle.make_layer_params(H, P, N, G, gen)
     B = args.B
-    ref = oracle.NativeV4(B, H, P, N, args.k, args.c, cold=args.cold, exact=args.exact)
+    ref = oracle.NativeV4(B, H, P, N, args.k, args.c, cold=args.cold, exact=args.exact, master=args.master)
     ref.join(torch.arange(B), oracle.make_state(B, H, P, N, gen))
     x, Bm, Cm, dt = oracle.make_step_inputs(B, H, P, N, G, gen)
     ref.step(x, Bm, Cm, dt, prm)  # warm
@@ -342,6 +343,9 @@ def main():
     ap.add_argument("--k", type=int, default=32)
     ap.add_argument("--c", type=int, default=4)
     ap.add_argument("--cold", default="fp32", choices=["fp32", "bf16", "fp8"])
+    ap.add_argument("--master", default="fp32", choices=["fp32", "bf16"],
+                    help="precision of the cold master for bf16 / fp8 cold (bf16: the reference fused "
+                         "path's bf16 master; bf16 cold is then a single copy)")
     ap.add_argument("--exact", action="store_true", help="v4 with the rank-c exact correction readout (corr=1)")
     ap.add_argument("--graph", action="store_true", help="time HIP graph replays of whole steps (all layers)")
     ap.add_argument("--ragged", action="store_true",
@@ -353,6 +357,8 @@ def main():
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (5 times), for scaling HBM counters")
     args = ap.parse_args()
+    if args.cold == "fp32":
+        args.master = "fp32"  # fp32 cold is its own master
 
     if args.copy_calibration_mib:
         n = args.copy_calibration_mib * (1 << 20) // 4
@@ -393,7 +399,7 @@ def main():
         log("v4 ...")
         v_step, v_launch, v_ev, tier_gb = bench_v4(args, layers, inputs, dev)
         res["v4"] = (v_step, v_launch, v_ev)
-        vb = args.B * bytes_v4_token(args.k, args.c, args.cold) + bytes_rotation()
+        vb = args.B * bytes_v4_token(args.k, args.c, args.cold, args.master) + bytes_rotation()
         log(f"v4: {v_step:.3f} ms/step, {args.B / v_step * 1e3:,.0f} tok/s, launch {v_ev * 1e3:.1f} us "
             f"-> {vb / (v_ev * 1e-3) / 1e9:,.0f} GB/s (tiers {tier_gb:.1f} GB)")
 
@@ -408,10 +414,11 @@ def main():
 
     head = "v4" if "v4" in res else "fresh"
     ms_step, ms_launch, ms_ev = res[head]
-    per_launch_bytes = args.B * (bytes_v4_token(args.k, args.c, args.cold) if head == "v4"
+    per_launch_bytes = args.B * (bytes_v4_token(args.k, args.c, args.cold, args.master) if head == "v4"
                                  else bytes_fresh_token()) + bytes_rotation()
     achieved = per_launch_bytes / (ms_ev * 1e-3) / 1e9
-    tkey = f"v4 B={args.B} k={args.k} c={args.c} {args.cold}" if head == "v4" else f"fresh B={args.B}"
+    tkey = (f"v4 B={args.B} k={args.k} c={args.c} {args.cold}" + (" bf16-master" if args.master == "bf16" else "")
+            if head == "v4" else f"fresh B={args.B}")
     traffic = measured_traffic(tkey)
     out = {
         "metric": "state-op tokens/s at 9B shape B=256 (v4-c4 vs fresh); achieved HBM GB/s vs peak",
@@ -428,12 +435,14 @@ def main():
         "data": "synthetic (seeded; bf16 x/B/C/dt, fp32 state ~N(0,0.1^2), random orthogonal R per layer-group)",
         "config": {
             "workload": (f"{head} state op, Nemotron-Nano-9B-v2 mixer shape, {args.layers} layers, B={args.B}"
-                         + (f", k_hot={args.k}, c={args.c}, {args.cold} cold, "
+                         + (f", k_hot={args.k}, c={args.c}, {args.cold} cold"
+                            + (", bf16 master" if args.master == "bf16" and args.cold != "fp32" else "") + ", "
                             f"{'random phases' if args.ragged else 'phase-aligned'}" if head == "v4" else "")
                          + (", exact (corr=1) readout" if head == "v4" and args.exact else "")
                          + (", HIP graph replay" if args.graph else "")),
             "layers": args.layers, "B": args.B, "H": H, "P": P, "N": N, "G": G,
             "k_hot": args.k, "c": args.c, "cold": args.cold, "readout": "exact" if args.exact else "stale",
+            "master": args.master if args.cold != "fp32" else "fp32",
         },
         "roofline": {
             "bound": "hbm",

@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define NSSM_ABI_VERSION 5
+#define NSSM_ABI_VERSION 6
 
 /* error codes */
 #define NSSM_OK 0
@@ -68,6 +68,13 @@ extern "C" {
                             (amax/448 + 1e-12), + exact fp32 master */
 #define NSSM_COLD_NONE 3 /* hot tier only: the cold columns are dropped (never stored,
                             read or flushed); cold, scale, master and the ring may be NULL */
+#define NSSM_COLD_BF16_SINGLE 4 /* one bf16 copy, read every token and rewritten at flush
+                                   with the RNE of the fp32 flush (the bf16 snapshot master of
+                                   scale/v4_fused_decode.py:156-158 and the bf16 arm of
+                                   scale/bench_v4_decode.py:160-175); no master */
+#define NSSM_COLD_FP8_BF16M 5 /* e4m3fn read copy with the per-row scale of NSSM_COLD_FP8,
+                                 quantized from a bf16 master (RNE of the fp32 flush): the
+                                 bf16 shadow master of scale/v4_fused_decode.py:149 */
 
 /* Per-layer constants. Mirrors the mixer attributes the reference reads:
  * dt_bias, A = -exp(A_log), D, time_step_min, and the ActRotMask R. */
@@ -94,8 +101,9 @@ typedef struct nssm_step_inputs {
  * owned by the caller). Layouts, all row-major:
  *   hot      fp32 [slots][H][P][K]
  *   cold     [slots][H][P][NC]   fp32 | bf16 | e4m3fn bytes, by cold_kind
- *   scale    fp32 [slots][H][P]         (NSSM_COLD_FP8 only, else NULL)
- *   master   fp32 [slots][H][P][NC]     (BF16/FP8 only, else NULL)
+ *   scale    fp32 [slots][H][P]         (FP8 and FP8_BF16M, else NULL)
+ *   master   [slots][H][P][NC]          fp32 for BF16 / FP8, bf16 for FP8_BF16M,
+ *                                       else NULL
  *   ring_x   bf16 [slots][H][c][P]      x of buffered tokens
  *   ring_dt  fp32 [slots][H][c]         softplus'd dt of buffered tokens
  *   ring_b   fp32 [slots][G][c][NC]     rotated B cold columns of buffered tokens
@@ -109,7 +117,7 @@ typedef struct nssm_tier {
   float* hot;
   void* cold;
   float* scale;
-  float* master;
+  void* master;
   uint16_t* ring_x;
   float* ring_dt;
   float* ring_b;
@@ -163,7 +171,8 @@ int nssm_v4_step_exact(const nssm_layer_params* prm, const nssm_tier* tier,
                        int64_t workspace_bytes, void* stream);
 
 /* Capture a tier from full fp32 states [b][H][P][N] into slot_ids[b] (NULL =
- * 0..b-1): hot = S[..,:K], cold = S[..,K:] (quantized for BF16/FP8),
+ * 0..b-1): hot = S[..,:K], cold = S[..,K:] (rounded to the master's precision,
+ * then quantized to the read copy),
  * t = phase[i] (NULL = 0), nv = 0, glog = 0. */
 int nssm_v4_join(const nssm_layer_params* prm, const nssm_tier* tier, const float* state,
                  int32_t b, const int32_t* slot_ids, const int32_t* phase, void* stream);

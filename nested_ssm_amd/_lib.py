@@ -9,7 +9,11 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libnssm_hip.so")
 
 COLD_FP32, COLD_BF16, COLD_FP8, COLD_NONE = 0, 1, 2, 3
+COLD_BF16_SINGLE, COLD_FP8_BF16M = 4, 5  # bf16 masters (NSSM_COLD_BF16_SINGLE / NSSM_COLD_FP8_BF16M)
 COLD_KINDS = {"fp32": COLD_FP32, "bf16": COLD_BF16, "fp8": COLD_FP8, "off": COLD_NONE}
+# (cold read copy, master precision) -> storage kind
+STORAGE_KINDS = {("fp32", "fp32"): COLD_FP32, ("bf16", "fp32"): COLD_BF16, ("fp8", "fp32"): COLD_FP8,
+                 ("bf16", "bf16"): COLD_BF16_SINGLE, ("fp8", "bf16"): COLD_FP8_BF16M}
 DT_F32, DT_BF16 = 0, 1  # model dtypes of nssm_conv_update (NSSM_DT_*)
 
 TIER_FIELDS = ("hot", "cold", "scale", "master", "ring_x", "ring_dt", "ring_b", "t", "nv", "glog")

@@ -11,8 +11,10 @@ with random synthetic values, 27 layers per step:
 
   fresh / fresh_ssu   untiered state op (nssm_fresh_step)
   v4                  tiered, fp32 cold (one exact copy)
-  v4bf16 / v4ssu      tiered, bf16 cold read copy + exact fp32 master
+  v4bf16 / v4ssu      tiered, one bf16 cold copy (the reference's SnapH / SnapM bf16
+                      snapshot masters, scale/bench_v4_decode.py:160-175, 258-276)
   v4fp8               tiered, e4m3 cold read copy (per-row scale) + fp32 master
+                      (the reference's fp32 acc_cold, :196-221)
   hotonly             hot tier only, cold columns dropped
   eager3              the untiered recurrence in plain torch ops (unfused engine)
   v4async             not run (the reference measured the side-stream variant
@@ -80,10 +82,10 @@ def run_point(B, pb, c, device, iters=20, warmup=5):
     res["fresh_ms"] = timed(fresh, iters, warmup)
     res["fresh_ssu_ms"] = res["fresh_ms"]
 
-    def tiered(cold, k):
+    def tiered(cold, k, master="fp32"):
         tiers = []
         for l in range(L):
-            t = V4Tier(B, H, P, G, k_hot=k, c=c, cold=cold, device=device)
+            t = V4Tier(B, H, P, G, k_hot=k, c=c, cold=cold, device=device, master=master)
             t.join(prms[l], S[l])
             tiers.append(t)
 
@@ -99,7 +101,7 @@ def run_point(B, pb, c, device, iters=20, warmup=5):
     res["hotonly_ms"] = tiered("off", pb) if pb < N else res["fresh_ms"]
     if pb < N:
         res["v4_ms"] = tiered("fp32", pb)
-        res["v4bf16_ms"] = tiered("bf16", pb)
+        res["v4bf16_ms"] = tiered("bf16", pb, master="bf16")
         res["v4fp8_ms"] = tiered("fp8", pb)
     else:
         res["v4_ms"] = res["v4bf16_ms"] = res["v4fp8_ms"] = res["fresh_ms"]

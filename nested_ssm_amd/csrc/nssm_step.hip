@@ -42,7 +42,7 @@ struct StepArgs {
   float* hot;
   void* cold;
   float* scale;
-  float* master;
+  void* master;  // fp32 (bf16 / e4m3 read copies) or bf16 (NSSM_COLD_FP8_BF16M)
   uint16_t* ring_x;
   float* ring_dt;
   float* ring_b;
@@ -138,6 +138,9 @@ __device__ __forceinline__ float softplus_f(float v) { return v > 20.f ? v : log
 #endif
 #ifndef NSSM_UNROLL_FP8
 #define NSSM_UNROLL_FP8 2
+#endif
+#ifndef NSSM_UNROLL_BF16S
+#define NSSM_UNROLL_BF16S 3
 #endif
 
 template <class T>
@@ -409,6 +412,15 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
 // Both unit mappings group a row's lanes as 8 consecutive lanes, so a row's dot product is
 // sum8 (three DPP steps).
 
+// Cold storage kinds (include/nssm.h) by read copy and master:
+//   kind            read copy (mapping)          master
+//   FP32            fp32 (segment)               the read copy
+//   BF16_SINGLE     bf16 (segment)               the read copy
+//   BF16            bf16 (contiguous)            fp32
+//   FP8             e4m3 + row scale (contig.)   fp32
+//   FP8_BF16M       e4m3 + row scale (contig.)   bf16
+// A single copy is read in the segment mapping so a flushing head replays onto the
+// values it read; a master beside a read copy is loaded only by flushing heads.
 template <int K, int COLD>
 struct Cfg {
   static constexpr int HS = K / 32;
@@ -416,10 +428,15 @@ struct Cfg {
   static constexpr bool TIERED = COLD != NSSM_COLD_NONE && NC > 0;
   static constexpr int CS = TIERED ? NC / 32 : 0;                // cold segments per row
   static constexpr int CSR = CS > 0 ? CS : 1;
+  static constexpr bool E4M3 = COLD == NSSM_COLD_FP8 || COLD == NSSM_COLD_FP8_BF16M;  // e4m3 read copy
+  static constexpr bool SEG = COLD == NSSM_COLD_FP32 || COLD == NSSM_COLD_BF16_SINGLE;  // segment read
+  static constexpr bool CONTIG = COLD == NSSM_COLD_BF16 || E4M3;                        // contiguous read
+  static constexpr bool MASTER32 = COLD == NSSM_COLD_BF16 || COLD == NSSM_COLD_FP8;    // fp32 master
+  static constexpr bool MASTER16 = COLD == NSSM_COLD_FP8_BF16M;                        // bf16 master
   static constexpr int CW = NC / 8;                              // contiguous columns per lane
-  static constexpr int WORDS = COLD == NSSM_COLD_FP8 ? CW / 4 : COLD == NSSM_COLD_BF16 ? CW / 2 : 0;
+  static constexpr int WORDS = E4M3 ? CW / 4 : COLD == NSSM_COLD_BF16 ? CW / 2 : 0;
   static constexpr int WR = WORDS > 0 ? WORDS : 1;
-  static constexpr int CWR = (COLD == NSSM_COLD_FP8 || COLD == NSSM_COLD_BF16) ? CW : 1;
+  static constexpr int CWR = CONTIG ? CW : 1;
   static constexpr int NT = NC / 16;                             // 16-column tiles of a row
 };
 
@@ -464,8 +481,9 @@ template <int K, int COLD>
 struct UnitRaw {
   using C = Cfg<K, COLD>;
   f4 hv[C::HS];
-  f4 cf[COLD == NSSM_COLD_FP32 ? C::CSR : 1];  // fp32 cold copy, segment mapping
-  uint32_t cw[C::WR];                           // bf16 / e4m3 read copy, contiguous mapping
+  f4 cf[COLD == NSSM_COLD_FP32 ? C::CSR : 1];               // fp32 cold copy, segment mapping
+  u2v cb[COLD == NSSM_COLD_BF16_SINGLE ? C::CSR : 1];       // single bf16 copy, segment mapping
+  uint32_t cw[C::WR];                                        // bf16 / e4m3 read copy, contiguous mapping
   float sc;                                     // e4m3 row scale
   float xp;
   uint16_t xraw;
@@ -484,6 +502,10 @@ __device__ __forceinline__ void unit_load(const StepArgs& a, size_t row, size_t 
         const f4* p = reinterpret_cast<const f4*>(static_cast<const float*>(a.cold) + row * C::NC) + q;
 #pragma unroll
         for (int s = 0; s < C::CS; ++s) d.cf[s] = ld_stream(p + 8 * s);
+      } else if constexpr (COLD == NSSM_COLD_BF16_SINGLE) {
+        const u2v* p = reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.cold) + row * C::NC) + q;
+#pragma unroll
+        for (int s = 0; s < C::CS; ++s) d.cb[s] = ld_stream(p + 8 * s);
       } else if constexpr (COLD == NSSM_COLD_BF16) {
         ld_words<C::WORDS>(
             reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(a.cold) + row * C::NC + C::CW * q), d.cw);
@@ -496,6 +518,19 @@ __device__ __forceinline__ void unit_load(const StepArgs& a, size_t row, size_t 
   }
   d.xraw = a.x[xrow];
   d.xp = bf2f(d.xraw);
+}
+
+__device__ __forceinline__ void bf16x4_to_f32(u2v w, float (&v)[4]) {
+  v[0] = __uint_as_float(w.x << 16);
+  v[1] = __uint_as_float(w.x & 0xffff0000u);
+  v[2] = __uint_as_float(w.y << 16);
+  v[3] = __uint_as_float(w.y & 0xffff0000u);
+}
+__device__ __forceinline__ u2v f32x4_to_bf16(float a, float b, float c, float d) {
+  u2v t;
+  t.x = (uint32_t)nssm_f32_to_bf16(a) | ((uint32_t)nssm_f32_to_bf16(b) << 16);
+  t.y = (uint32_t)nssm_f32_to_bf16(c) | ((uint32_t)nssm_f32_to_bf16(d) << 16);
+  return t;
 }
 
 // stale readout partial of one lane from its read-copy registers (times the row scale for e4m3)
@@ -512,13 +547,21 @@ __device__ __forceinline__ float cold_partial(const UnitRaw<K, COLD>& d, const f
       pc = fmaf(d.cf[s].z, Cc[s][2], pc);
       pc = fmaf(d.cf[s].w, Cc[s][3], pc);
     }
+  } else if constexpr (COLD == NSSM_COLD_BF16_SINGLE) {
+#pragma unroll
+    for (int s = 0; s < C::CS; ++s) {
+      float v[4];
+      bf16x4_to_f32(d.cb[s], v);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pc = fmaf(v[e], Cc[s][e], pc);
+    }
   } else if constexpr (COLD == NSSM_COLD_BF16) {
 #pragma unroll
     for (int i = 0; i < C::WORDS; ++i) {
       pc = fmaf(__uint_as_float(d.cw[i] << 16), Cq[2 * i], pc);
       pc = fmaf(__uint_as_float(d.cw[i] & 0xffff0000u), Cq[2 * i + 1], pc);
     }
-  } else if constexpr (COLD == NSSM_COLD_FP8) {
+  } else if constexpr (C::E4M3) {
 #pragma unroll
     for (int i = 0; i < C::WORDS; ++i) {
       float v[4];
@@ -595,8 +638,9 @@ __device__ __forceinline__ void unit_compute(const StepArgs& a, size_t sh, size_
   }
 }
 
-// Write the new exact cold values of one row in the segment mapping: fp32 copy, or
-// master + bf16 / e4m3 read copy.
+// Write the new cold values of one row in the segment mapping: the fp32 copy, the single
+// bf16 copy (RNE), or the master (fp32, or bf16 by RNE) and the bf16 / e4m3 read copy
+// quantized from the master's values.
 template <int COLD, int CS>
 __device__ __forceinline__ void cold_store(const StepArgs& a, size_t row, int q, const float (&v)[CS][4]) {
   constexpr int NC = CS * 32;
@@ -604,31 +648,45 @@ __device__ __forceinline__ void cold_store(const StepArgs& a, size_t row, int q,
     f4* p = reinterpret_cast<f4*>(static_cast<float*>(a.cold) + row * NC) + q;
 #pragma unroll
     for (int s = 0; s < CS; ++s) st_stream(f4{v[s][0], v[s][1], v[s][2], v[s][3]}, p + 8 * s);
-  } else {
-    f4* pm = reinterpret_cast<f4*>(a.master + row * NC) + q;
+  } else if constexpr (COLD == NSSM_COLD_BF16_SINGLE) {
+    u2v* p = reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.cold) + row * NC) + q;
 #pragma unroll
-    for (int s = 0; s < CS; ++s) st_stream(f4{v[s][0], v[s][1], v[s][2], v[s][3]}, pm + 8 * s);
+    for (int s = 0; s < CS; ++s) st_stream(f32x4_to_bf16(v[s][0], v[s][1], v[s][2], v[s][3]), p + 8 * s);
+  } else {
+    float w[CS][4];  // the master's values
+    if constexpr (COLD == NSSM_COLD_FP8_BF16M) {
+      u2v* pm = reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.master) + row * NC) + q;
+#pragma unroll
+      for (int s = 0; s < CS; ++s) {
+        const u2v t = f32x4_to_bf16(v[s][0], v[s][1], v[s][2], v[s][3]);
+        st_stream(t, pm + 8 * s);
+        bf16x4_to_f32(t, w[s]);
+      }
+    } else {
+      f4* pm = reinterpret_cast<f4*>(static_cast<float*>(a.master) + row * NC) + q;
+#pragma unroll
+      for (int s = 0; s < CS; ++s) {
+        st_stream(f4{v[s][0], v[s][1], v[s][2], v[s][3]}, pm + 8 * s);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[s][e] = v[s][e];
+      }
+    }
     if constexpr (COLD == NSSM_COLD_BF16) {
       u2v* p = reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.cold) + row * NC) + q;
 #pragma unroll
-      for (int s = 0; s < CS; ++s) {
-        u2v t;
-        t.x = (uint32_t)nssm_f32_to_bf16(v[s][0]) | ((uint32_t)nssm_f32_to_bf16(v[s][1]) << 16);
-        t.y = (uint32_t)nssm_f32_to_bf16(v[s][2]) | ((uint32_t)nssm_f32_to_bf16(v[s][3]) << 16);
-        st_stream(t, p + 8 * s);
-      }
+      for (int s = 0; s < CS; ++s) st_stream(f32x4_to_bf16(w[s][0], w[s][1], w[s][2], w[s][3]), p + 8 * s);
     } else {  // e4m3 with the per-row amax scale of scale/vllm_v4_patch.py:106-111
       float am = 0.f;
 #pragma unroll
       for (int s = 0; s < CS; ++s)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) am = fmaxf(am, fabsf(v[s][e]));
+        for (int e = 0; e < 4; ++e) am = fmaxf(am, fabsf(w[s][e]));
       am = max8(am);
       const float sc = am / 448.0f + 1e-12f;
       uint32_t* p = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.cold) + row * NC) + q;
 #pragma unroll
       for (int s = 0; s < CS; ++s)
-        st_stream(f32x4_to_fp8(v[s][0] / sc, v[s][1] / sc, v[s][2] / sc, v[s][3] / sc), p + 8 * s);
+        st_stream(f32x4_to_fp8(w[s][0] / sc, w[s][1] / sc, w[s][2] / sc, w[s][3] / sc), p + 8 * s);
       if (q == 0) a.scale[row] = sc;
     }
   }
@@ -654,13 +712,21 @@ __device__ __forceinline__ void unit_compute_flush(const StepArgs& a, size_t sh,
   const int P = a.P;
   const float dtot = hd[HD_DTOT];
   float nvv[CS][4];
-  const f4* pm = reinterpret_cast<const f4*>(a.master + row * NC) + q;  // bf16 / e4m3: fp32 master
 #pragma unroll
   for (int s = 0; s < CS; ++s) {
-    f4 t;
-    if constexpr (COLD == NSSM_COLD_FP32) t = d.cf[s];
-    else t = ld_stream(pm + 8 * s);
-    nvv[s][0] = t.x * dtot; nvv[s][1] = t.y * dtot; nvv[s][2] = t.z * dtot; nvv[s][3] = t.w * dtot;
+    float t[4];
+    if constexpr (COLD == NSSM_COLD_FP32) {
+      t[0] = d.cf[s].x; t[1] = d.cf[s].y; t[2] = d.cf[s].z; t[3] = d.cf[s].w;
+    } else if constexpr (COLD == NSSM_COLD_BF16_SINGLE) {
+      bf16x4_to_f32(d.cb[s], t);
+    } else if constexpr (C::MASTER16) {
+      bf16x4_to_f32(ld_stream(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.master) + row * NC) + q + 8 * s), t);
+    } else {  // fp32 master
+      const f4 m4 = ld_stream(reinterpret_cast<const f4*>(static_cast<const float*>(a.master) + row * NC) + q + 8 * s);
+      t[0] = m4.x; t[1] = m4.y; t[2] = m4.z; t[3] = m4.w;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) nvv[s][e] = t[e] * dtot;
   }
   for (int i = 0; i < m; ++i) {
     const float coef = sU[i * P + p];
@@ -739,7 +805,10 @@ __device__ __forceinline__ void stream_units(const StepArgs& a, int slot, int bi
                                              const float (&Cc)[Cfg<K, COLD>::CSR][4],
                                              const float (&Cq)[Cfg<K, COLD>::CWR]) {
   constexpr bool TIERED = Cfg<K, COLD>::TIERED;
-  constexpr int U = COLD == NSSM_COLD_BF16 ? NSSM_UNROLL_BF16 : COLD == NSSM_COLD_FP8 ? NSSM_UNROLL_FP8 : NSSM_UNROLL;
+  constexpr int U = COLD == NSSM_COLD_BF16          ? NSSM_UNROLL_BF16
+                    : COLD == NSSM_COLD_BF16_SINGLE ? NSSM_UNROLL_BF16S
+                    : Cfg<K, COLD>::E4M3            ? NSSM_UNROLL_FP8
+                                                    : NSSM_UNROLL;
   const int H = a.H, P = a.P, c = a.c;
   for (int u0 = wave; u0 < units; u0 += U * nw) {
     UnitRaw<K, COLD> d[U];
@@ -806,7 +875,7 @@ __device__ __forceinline__ void stream_body(const StepArgs& a) {
   }
 #pragma unroll
   for (int s = 0; s < CSR; ++s) {
-    if constexpr (COLD == NSSM_COLD_FP32 && CS > 0) {
+    if constexpr (C::SEG && CS > 0) {
       const f4 tc = *reinterpret_cast<const f4*>(wC + K + 32 * s + 4 * q);
       Cc[s][0] = tc.x; Cc[s][1] = tc.y; Cc[s][2] = tc.z; Cc[s][3] = tc.w;
     } else {
@@ -815,7 +884,7 @@ __device__ __forceinline__ void stream_body(const StepArgs& a) {
   }
 #pragma unroll
   for (int i = 0; i < CWR; ++i) {
-    if constexpr (COLD == NSSM_COLD_FP8 || COLD == NSSM_COLD_BF16) Cq[i] = wC[K + C::CW * q + i];
+    if constexpr (C::CONTIG) Cq[i] = wC[K + C::CW * q + i];
     else Cq[i] = 0.f;
   }
 
@@ -960,7 +1029,7 @@ template <int K, int COLD>
 __global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
   using C = Cfg<K, COLD>;
   constexpr int NC = C::NC, NT = C::NT, nw = kFlushWaves, nthr = kFlushWaves * 64;
-  constexpr int TPP = COLD == NSSM_COLD_FP8 ? (nw * kMfmaTiles / NT) * NT : nw * kMfmaTiles;  // tiles per pass
+  constexpr int TPP = C::E4M3 ? (nw * kMfmaTiles / NT) * NT : nw * kMfmaTiles;  // tiles per pass
   static_assert(TPP >= NT, "a pass must hold a whole row");
   extern __shared__ float lds[];
   // this workgroup's listed items and their scalars (loaded by the thread that lists
@@ -1056,26 +1125,32 @@ __global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
       const uint16_t* xcur = a.x + (size_t)it * P;
       const float* wgt = ws.w + (size_t)it * c;
       const size_t row0 = ((size_t)slot * H + h) * P;
-      const float* src = COLD == NSSM_COLD_FP32 ? static_cast<const float*>(a.cold) : a.master;
+      // the values the flush starts from: the single copy, or the master (fp32 or bf16)
+      const void* src = C::SEG ? static_cast<const void*>(a.cold) : static_cast<const void*>(a.master);
+      constexpr bool SRC16 = COLD == NSSM_COLD_BF16_SINGLE || C::MASTER16;
       const bool whole = m <= fch;  // the window fits in LDS: staged once
 
       for (int t0 = 0; t0 < ntot; t0 += TPP) {
         const int ntile = min(TPP, ntot - t0);
         // the pass's state tiles are loaded before the window
         f4 old[kMfmaTiles];
+        u2v old16[SRC16 ? kMfmaTiles : 1];
         u2v rb16[COLD == NSSM_COLD_BF16 ? kMfmaTiles : 1];
-        uint32_t r8[COLD == NSSM_COLD_FP8 ? kMfmaTiles : 1];
-        float rsc[COLD == NSSM_COLD_FP8 ? kMfmaTiles : 1];
+        uint32_t r8[C::E4M3 ? kMfmaTiles : 1];
+        float rsc[C::E4M3 ? kMfmaTiles : 1];
 #pragma unroll
         for (int i = 0; i < kMfmaTiles; ++i) {
           const int tt = t0 + wave + i * nw;
           if (wave + i * nw < ntile) {
             const size_t row = row0 + (tt / NT) * 16 + li;
             const int col = (tt % NT) * 16 + 4 * lk;
-            old[i] = ld_stream(reinterpret_cast<const f4*>(src + row * NC + col));
+            if constexpr (SRC16)
+              old16[i] = ld_stream(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(src) + row * NC + col));
+            else
+              old[i] = ld_stream(reinterpret_cast<const f4*>(static_cast<const float*>(src) + row * NC + col));
             if constexpr (COLD == NSSM_COLD_BF16)
               rb16[i] = ld_stream(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.cold) + row * NC + col));
-            if constexpr (COLD == NSSM_COLD_FP8) {
+            if constexpr (C::E4M3) {
               r8[i] = ld_stream(reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(a.cold) + row * NC + col));
               rsc[i] = a.scale[row];
             }
@@ -1123,9 +1198,14 @@ __global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
             const int p = pt * 16 + li, col = nt * 16 + 4 * lk;
             const size_t row = row0 + p;
             const f4 cq = *reinterpret_cast<const f4*>(cq0 + col);
+            if constexpr (SRC16) {
+              float o4[4];
+              bf16x4_to_f32(old16[i], o4);
+              old[i] = f4{o4[0], o4[1], o4[2], o4[3]};
+            }
             float rd[4];
             float rscale = 1.f;
-            if constexpr (COLD == NSSM_COLD_FP32) {
+            if constexpr (C::SEG) {  // the single copy is the read copy
               rd[0] = old[i].x; rd[1] = old[i].y; rd[2] = old[i].z; rd[3] = old[i].w;
             } else if constexpr (COLD == NSSM_COLD_BF16) {
               rd[0] = __uint_as_float(rb16[i].x << 16); rd[1] = __uint_as_float(rb16[i].x & 0xffff0000u);
@@ -1145,20 +1225,24 @@ __global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
             nv.y = fmaf(dtot, old[i].y, nv.y);
             nv.z = fmaf(dtot, old[i].z, nv.z);
             nv.w = fmaf(dtot, old[i].w, nv.w);
-            acc[i] = nv;
             if constexpr (COLD == NSSM_COLD_FP32) {
               st_stream(nv, reinterpret_cast<f4*>(static_cast<float*>(a.cold) + row * NC + col));
+            } else if constexpr (SRC16) {  // bf16 single copy or bf16 master: RNE, and the
+              // e4m3 copy is quantized from the rounded values
+              const u2v t = f32x4_to_bf16(nv.x, nv.y, nv.z, nv.w);
+              st_stream(t, reinterpret_cast<u2v*>(static_cast<uint16_t*>(C::SEG ? a.cold : a.master) + row * NC + col));
+              float r4[4];
+              bf16x4_to_f32(t, r4);
+              nv = f4{r4[0], r4[1], r4[2], r4[3]};
             } else {
-              st_stream(nv, reinterpret_cast<f4*>(a.master + row * NC + col));
+              st_stream(nv, reinterpret_cast<f4*>(static_cast<float*>(a.master) + row * NC + col));
             }
-            if constexpr (COLD == NSSM_COLD_BF16) {
-              u2v t;
-              t.x = (uint32_t)nssm_f32_to_bf16(nv.x) | ((uint32_t)nssm_f32_to_bf16(nv.y) << 16);
-              t.y = (uint32_t)nssm_f32_to_bf16(nv.z) | ((uint32_t)nssm_f32_to_bf16(nv.w) << 16);
-              st_stream(t, reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.cold) + row * NC + col));
-            }
+            acc[i] = nv;
+            if constexpr (COLD == NSSM_COLD_BF16)
+              st_stream(f32x4_to_bf16(nv.x, nv.y, nv.z, nv.w),
+                        reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.cold) + row * NC + col));
             if (lk == 0) sPart[p * NT + nt] = pc * rscale;
-            if constexpr (COLD == NSSM_COLD_FP8) {
+            if constexpr (C::E4M3) {
               float am = fmaxf(fmaxf(fabsf(nv.x), fabsf(nv.y)), fmaxf(fabsf(nv.z), fabsf(nv.w)));
               am = fmaxf(am, __shfl_xor(am, 16));
               am = fmaxf(am, __shfl_xor(am, 32));
@@ -1167,7 +1251,7 @@ __global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
           }
         }
         __syncthreads();  // partials and row maxima of this pass's tiles
-        if constexpr (COLD == NSSM_COLD_FP8) {
+        if constexpr (C::E4M3) {
 #pragma unroll
           for (int i = 0; i < kMfmaTiles; ++i) {
             if (wave + i * nw < ntile) {
@@ -1249,6 +1333,8 @@ void launch_join(const StepArgs& a, int kind, const float* state, const int32_t*
     case NSSM_COLD_FP32: hipLaunchKernelGGL((join_kernel<K, NSSM_COLD_FP32>), dim3(grid), dim3(256), 0, st, a, state, phase); break;
     case NSSM_COLD_BF16: hipLaunchKernelGGL((join_kernel<K, NSSM_COLD_BF16>), dim3(grid), dim3(256), 0, st, a, state, phase); break;
     case NSSM_COLD_FP8: hipLaunchKernelGGL((join_kernel<K, NSSM_COLD_FP8>), dim3(grid), dim3(256), 0, st, a, state, phase); break;
+    case NSSM_COLD_BF16_SINGLE: hipLaunchKernelGGL((join_kernel<K, NSSM_COLD_BF16_SINGLE>), dim3(grid), dim3(256), 0, st, a, state, phase); break;
+    case NSSM_COLD_FP8_BF16M: hipLaunchKernelGGL((join_kernel<K, NSSM_COLD_FP8_BF16M>), dim3(grid), dim3(256), 0, st, a, state, phase); break;
     default: hipLaunchKernelGGL((join_kernel<K, NSSM_COLD_NONE>), dim3(grid), dim3(256), 0, st, a, state, phase); break;
   }
 }
@@ -1285,9 +1371,13 @@ __global__ void materialize_kernel(StepArgs a, float* __restrict__ S, int K, int
     const size_t row = o * a.P + p;
     float* dst = S + (((size_t)bi * a.H + h) * a.P + p) * kN;
     for (int n = 0; n < K; ++n) dst[n] = a.hot[row * K + n];
-    const float* cm = kind == NSSM_COLD_FP32 ? static_cast<const float*>(a.cold) + row * NC : a.master + row * NC;
+    // the snapshot values: fp32 (the copy or the master) or bf16 (the single copy or the master)
+    const bool m16 = kind == NSSM_COLD_BF16_SINGLE || kind == NSSM_COLD_FP8_BF16M;
+    const void* cbase = kind == NSSM_COLD_FP32 || kind == NSSM_COLD_BF16_SINGLE ? a.cold : a.master;
     for (int n = 0; n < NC; ++n) {
-      float v = dtot * cm[n];
+      const float snap = m16 ? bf2f(static_cast<const uint16_t*>(cbase)[row * NC + n])
+                             : static_cast<const float*>(cbase)[row * NC + n];
+      float v = dtot * snap;
       for (int i = 0; i < nv; ++i) {
         const int pos = (t0 + i) % c;
         const float u = w[i] * bf2f(a.ring_x[(rh + pos) * a.P + p]);
@@ -1538,7 +1628,8 @@ int divisor_at_most(int n, int cap) {
 size_t flush_lds_bytes(int P, int K, int kind, int fch) {
   const int NC = kN - K;
   const size_t tiles = (size_t)P * (NC / 16);
-  return ((size_t)fch * NC + (size_t)fch * P / 2 + fch + tiles * (kind == NSSM_COLD_FP8 ? 2 : 1)) * sizeof(float);
+  const bool e4m3 = kind == NSSM_COLD_FP8 || kind == NSSM_COLD_FP8_BF16M;  // + row maxima
+  return ((size_t)fch * NC + (size_t)fch * P / 2 + fch + tiles * (e4m3 ? 2 : 1)) * sizeof(float);
 }
 // window tokens the flush kernel stages at a time: the whole window (c rounded up to the
 // matrix-core step of 4 tokens) when it fits, else the most that fit (0: none fit)
@@ -1581,7 +1672,9 @@ int pick_launch(int H, int G, int P, int K, int c, Launch* out, int kind = NSSM_
   // heads per stream workgroup, measured on MI355X (B = 256, 27 layers, k_hot = 32, ms per
   // step at c = 4 / 16): fp32 cold 1 head 9.02 / 8.09, 2 heads 9.50 / 8.35; bf16 9.68 / 7.22
   // vs 9.48 / 7.10; e4m3 8.01 / 6.14 vs 7.98 / 5.75
-  int hpw = (kind == NSSM_COLD_BF16 || kind == NSSM_COLD_FP8) && K < kN && HG % 2 == 0 ? 2 : 1;
+  const bool narrow = kind == NSSM_COLD_BF16 || kind == NSSM_COLD_FP8 || kind == NSSM_COLD_FP8_BF16M ||
+                      kind == NSSM_COLD_BF16_SINGLE;  // 16- or 8-bit read copies
+  int hpw = narrow && K < kN && HG % 2 == 0 ? 2 : 1;
   if (g_hpw_override > 0) {
     if (HG % g_hpw_override) return NSSM_E_TUNING;
     hpw = g_hpw_override;
@@ -1626,12 +1719,13 @@ void fill_common(StepArgs& a, const nssm_layer_params* prm, const nssm_step_inpu
 
 int check_tier(const nssm_tier* tr, bool need_ring) {
   if (!tr) return NSSM_E_NULL;
-  if (tr->cold_kind < NSSM_COLD_FP32 || tr->cold_kind > NSSM_COLD_NONE) return NSSM_E_KIND;
+  if (tr->cold_kind < NSSM_COLD_FP32 || tr->cold_kind > NSSM_COLD_FP8_BF16M) return NSSM_E_KIND;
   const bool cold = tr->cold_kind != NSSM_COLD_NONE;
   if (!tr->hot || !tr->t || !tr->nv || !tr->glog || (cold && !tr->cold)) return NSSM_E_NULL;
   if (cold && need_ring && (!tr->ring_x || !tr->ring_dt || !tr->ring_b)) return NSSM_E_NULL;
-  if ((tr->cold_kind == NSSM_COLD_BF16 || tr->cold_kind == NSSM_COLD_FP8) && !tr->master) return NSSM_E_NULL;
-  if (tr->cold_kind == NSSM_COLD_FP8 && !tr->scale) return NSSM_E_NULL;
+  const bool e4m3 = tr->cold_kind == NSSM_COLD_FP8 || tr->cold_kind == NSSM_COLD_FP8_BF16M;
+  if ((tr->cold_kind == NSSM_COLD_BF16 || e4m3) && !tr->master) return NSSM_E_NULL;
+  if (e4m3 && !tr->scale) return NSSM_E_NULL;
   if (tr->slots <= 0 || tr->c < 1 || tr->c > kMaxC) return NSSM_E_DIMS;
   if (tr->k_hot != 32 && tr->k_hot != 64 && tr->k_hot != 96) return NSSM_E_DIMS;
   if (!aligned16(tr->hot) || (cold && !aligned16(tr->cold)) || (tr->master && !aligned16(tr->master)))
@@ -1694,6 +1788,8 @@ int dispatch_kind(const StepArgs& a, int kind, const Launch& L, hipStream_t st) 
     case NSSM_COLD_BF16: return launch_pair<K, NSSM_COLD_BF16>(a, L, st);
     case NSSM_COLD_FP8: return launch_pair<K, NSSM_COLD_FP8>(a, L, st);
     case NSSM_COLD_NONE: return launch_pair<K, NSSM_COLD_NONE>(a, L, st);
+    case NSSM_COLD_BF16_SINGLE: return launch_pair<K, NSSM_COLD_BF16_SINGLE>(a, L, st);
+    case NSSM_COLD_FP8_BF16M: return launch_pair<K, NSSM_COLD_FP8_BF16M>(a, L, st);
   }
   return NSSM_E_KIND;
 }
@@ -1757,15 +1853,23 @@ int nssm_tier_sizes(int32_t slots, int32_t H, int32_t P, int32_t N, int32_t G, i
   if (!sz) return NSSM_E_NULL;
   if (slots <= 0 || H <= 0 || P <= 0 || N != kN || G <= 0 || k_hot <= 0 || k_hot >= N || c < 1 || c > kMaxC)
     return NSSM_E_DIMS;
-  if (cold_kind < NSSM_COLD_FP32 || cold_kind > NSSM_COLD_NONE) return NSSM_E_KIND;
+  if (cold_kind < NSSM_COLD_FP32 || cold_kind > NSSM_COLD_FP8_BF16M) return NSSM_E_KIND;
   const int64_t rows = (int64_t)slots * H * P;
   const int64_t NC = N - k_hot;
-  const int64_t esz = cold_kind == NSSM_COLD_FP32 ? 4 : cold_kind == NSSM_COLD_BF16 ? 2 : cold_kind == NSSM_COLD_FP8 ? 1 : 0;
+  int64_t esz = 0, msz = 0;  // bytes per element of the cold copy and of the master
+  switch (cold_kind) {
+    case NSSM_COLD_FP32: esz = 4; break;
+    case NSSM_COLD_BF16: esz = 2; msz = 4; break;
+    case NSSM_COLD_FP8: esz = 1; msz = 4; break;
+    case NSSM_COLD_BF16_SINGLE: esz = 2; break;
+    case NSSM_COLD_FP8_BF16M: esz = 1; msz = 2; break;
+  }
+  const bool e4m3 = cold_kind == NSSM_COLD_FP8 || cold_kind == NSSM_COLD_FP8_BF16M;
   const int64_t ring = cold_kind == NSSM_COLD_NONE ? 0 : 1;
   sz[0] = rows * k_hot * 4;
   sz[1] = rows * NC * esz;
-  sz[2] = cold_kind == NSSM_COLD_FP8 ? rows * 4 : 0;
-  sz[3] = cold_kind == NSSM_COLD_BF16 || cold_kind == NSSM_COLD_FP8 ? rows * NC * 4 : 0;
+  sz[2] = e4m3 ? rows * 4 : 0;
+  sz[3] = rows * NC * msz;
   sz[4] = ring * slots * H * c * P * 2;
   sz[5] = ring * slots * H * c * 4;
   sz[6] = ring * slots * G * c * NC * 4;

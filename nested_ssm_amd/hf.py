@@ -201,7 +201,9 @@ def capture(m, cache_params, dt_min: float):
         m._v4state = V4State(tier=None, params=prm, pb=pb, c=c, rotated=prm.R is not None)
         return
     kind = _cold_kind(cfg)
-    tier = V4Tier(b, m.num_heads, m.head_dim, m.n_groups, k_hot=pb, c=c, cold=kind, device=S.device)
+    master = cfg.get("master", "fp32") if kind in ("bf16", "fp8") else "fp32"
+    tier = V4Tier(b, m.num_heads, m.head_dim, m.n_groups, k_hot=pb, c=c, cold=kind, device=S.device,
+                  master=master)
     tier.join(prm, Srot.contiguous())
     m._v4state = V4State(tier=tier, params=prm, pb=pb, c=c, rotated=prm.R is not None)
 

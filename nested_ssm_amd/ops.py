@@ -122,15 +122,26 @@ def fresh_step(prm: LayerParams, state: torch.Tensor, x, B, C, dt, y: Optional[t
 
 class V4Tier:
     """Tiered state of one layer for `slots` sequence slots (hot fp32 [slots,H,P,K],
-    cold fp32/bf16/fp8 [slots,H,P,NC] (+ fp32 master and per-row scale), ring of
-    the last c tokens, per-(slot, head) t / nv / glog). Layout as in include/nssm.h."""
+    cold fp32/bf16/fp8 [slots,H,P,NC] (+ master and per-row scale), ring of the last
+    c tokens, per-(slot, head) t / nv / glog). Layout as in include/nssm.h.
+
+    master: the precision the cold state is kept in between flushes. "fp32" (the
+    default): an exact fp32 master beside a bf16 / e4m3 read copy (the native and
+    vLLM paths keep the full fp32 state, scale/v4_native_decode.py:65-67). "bf16":
+    the fused path's bf16 master (scale/v4_fused_decode.py:149,156-158): bf16 cold
+    is then one bf16 copy, rewritten with the RNE of each flush; fp8 cold keeps a
+    bf16 master beside the e4m3 copy. fp32 cold is its own fp32 master."""
 
     def __init__(self, slots: int, H: int, P: int, G: int, k_hot: int = 32, c: int = 4, cold: str = "fp32",
-                 device="cuda", N: int = N_STATE):
+                 device="cuda", N: int = N_STATE, master: str = "fp32"):
         if cold not in COLD_KINDS:
             raise ValueError(f"cold must be one of {sorted(COLD_KINDS)} (got {cold!r})")
+        if cold != "off" and (cold, master) not in _lib.STORAGE_KINDS:
+            raise ValueError(f"cold={cold!r} cannot be kept with master={master!r} "
+                             f"(supported: {sorted(_lib.STORAGE_KINDS)})")
         self.slots, self.H, self.P, self.G, self.N, self.k, self.c, self.cold = slots, H, P, G, N, k_hot, c, cold
-        self.kind = COLD_KINDS[cold]
+        self.master_dtype = master if cold != "off" else None
+        self.kind = COLD_KINDS["off"] if cold == "off" else _lib.STORAGE_KINDS[(cold, master)]
         sizes = (ctypes.c_int64 * 10)()
         check(lib().nssm_tier_sizes(slots, H, P, N, G, k_hot, c, self.kind, sizes), "nssm_tier_sizes")
         NC = N - k_hot
@@ -141,7 +152,9 @@ class V4Tier:
         cold_dt = {"fp32": torch.float32, "bf16": torch.bfloat16, "fp8": torch.uint8, "off": None}[cold]
         self.cold_t = e((slots, H, P, NC), cold_dt) if tiered else None
         self.scale = e((slots, H, P), torch.float32) if cold == "fp8" else None
-        self.master = e((slots, H, P, NC), torch.float32) if cold in ("bf16", "fp8") else None
+        master_dt = {_lib.COLD_BF16: torch.float32, _lib.COLD_FP8: torch.float32,
+                     _lib.COLD_FP8_BF16M: torch.bfloat16}.get(self.kind)
+        self.master = e((slots, H, P, NC), master_dt) if master_dt is not None else None
         self.ring_x = e((slots, H, c, P), torch.bfloat16) if tiered else None
         self.ring_dt = e((slots, H, c), torch.float32) if tiered else None
         self.ring_b = e((slots, G, c, NC), torch.float32) if tiered else None

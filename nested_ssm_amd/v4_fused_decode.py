@@ -6,9 +6,11 @@ rotation read from an ActRotMask-wrapped `m.act.R` into `m._v4R`, and the
 module-level `_v4_fused_decode(self, hidden_states, cache_params,
 attention_mask)` (scale/v4_fused_decode.py:28-95). Prefill runs the stock
 forward and the tier is captured at its end (scale/v4_fused_decode.py:109-160).
-No dt clamp, as the reference's fused kernel path. The reference keeps a bf16
-master for its bf16/fp8 cold snapshots; here the master is exact fp32.
-cold="off" keeps the hot tier only (the cold columns are dropped).
+No dt clamp, as the reference's fused kernel path. The cold tier is kept over the
+reference's bf16 master by default (master="bf16": bf16 cold is one bf16 copy, fp8
+cold an e4m3 copy beside a bf16 shadow master, scale/v4_fused_decode.py:149,156-158);
+master="fp32" keeps an exact fp32 master instead. cold="off" keeps the hot tier only
+(the cold columns are dropped).
 """
 from transformers.models.nemotron_h import modeling_nemotron_h as M
 
@@ -26,11 +28,11 @@ def _dispatch(self, hidden_states, cache_params=None, attention_mask=None, **kw)
                        lambda *a: _v4_fused_decode(*a))
 
 
-def install(model, pb=32, c=16, cold="bf16"):
+def install(model, pb=32, c=16, cold="bf16", master="bf16"):
     n = 0
     for m in hf.mixers(model):
         hf.check_mixer_shape(m)
-        m.v4cfg = dict(pb=pb, c=c, cold=cold)
+        m.v4cfg = dict(pb=pb, c=c, cold=cold, master=master if cold in ("bf16", "fp8") else "fp32")
         m._v4state = None
         m._v4R = m.act.R.detach().float() if hasattr(m.act, "R") else None
         m.forward = _dispatch.__get__(m)

@@ -29,6 +29,11 @@ Pinning status of each function (how it is checked, in tests/test_oracle.py):
                     the closed-form quantisation term exp(G_t) (q sc - snap) . C'
   TieredV4          equals NativeV4 in fp64 (chunked replay == per-token
                     recurrence), including ragged phases and join/leave
+  master="bf16"     (NativeV4, TieredV4) the fp64 fresh recurrence with the cold
+                    columns rounded to bf16 at the join and after every flush
+                    (rounding at every token, never, or quantizing the e4m3 copy
+                    from the unrounded state each fails); TieredV4 == NativeV4
+                    with ragged phases and join/leave
   quant_fp8 / read  torch float8_e4m3fn cast; scale = amax/448 + 1e-12 per row
   fp8_readout       closed form of the reference docstring vs an fp64 loop
   hot_only_step     the hot columns of an fp64 fresh trajectory (they never read the cold ones)

@@ -193,6 +193,16 @@ class NativeV4:
     fp8_restore_each_step re-stores the dequantized old snapshot for slots that
     do not flush, as scale/vllm_v4_patch.py:173-175 does.
 
+    master: the precision the cold state is kept in between flushes. "fp32": the
+    exact state (the native and vLLM paths keep the full fp32 state). "bf16": the
+    fused path's bf16 master, scale/v4_fused_decode.py:149,156-158 (bf16 cold: the
+    snapshot is the master; fp8 cold: a bf16 shadow master beside the e4m3 copy)
+    and the bf16 arm of scale/bench_v4_decode.py:160-175: the cold columns are
+    rounded to bf16 (RNE) at the join and at every flush and evolve in fp32 in
+    between; the read copy is taken from the rounded values. (The reference rounds
+    the decay product and the window update separately, :79-84; one rounding of the
+    fp32 result is this convention.)
+
     exact=True is the rank-c exact correction readout (corr=1,
     scale/v4_native_decode.py:81-117): the log-decay G_t includes this token, this
     token's (B'_cold, dt x, G_t) is buffered before the readout, and
@@ -202,9 +212,11 @@ class NativeV4:
     """
 
     def __init__(self, slots: int, H: int, P: int, N: int, k: int, c: int, cold: str = "fp32",
-                 dtype=torch.float32, fp8_restore_each_step: bool = True, exact: bool = False):
+                 dtype=torch.float32, fp8_restore_each_step: bool = True, exact: bool = False,
+                 master: str = "fp32"):
         assert 0 < k <= N and c >= 1 and cold in ("fp32", "bf16", "fp8")
-        self.k, self.c, self.cold, self.dtype = k, c, cold, dtype
+        assert master in ("fp32", "bf16") and not (cold == "fp32" and master == "bf16")
+        self.k, self.c, self.cold, self.dtype, self.master = k, c, cold, dtype, master
         self.fp8_restore = fp8_restore_each_step
         self.exact = exact
         self.buf = [[] for _ in range(slots)]  # exact readout: per slot (B'_cold [H,Nc], dt x [H,P], G [H])
@@ -231,11 +243,18 @@ class NativeV4:
             return read_fp8(self.q8[slots], self.sc8[slots]).to(self.dtype)
         return self.snap[slots]
 
+    def _round_master(self, S: torch.Tensor) -> torch.Tensor:
+        """S with its cold columns rounded to the master precision."""
+        if self.master == "fp32":
+            return S
+        k = self.k
+        return torch.cat([S[..., :k], S[..., k:].to(torch.bfloat16).to(S.dtype)], dim=-1)
+
     def join(self, slots: torch.Tensor, S_new: torch.Tensor, phase: Optional[torch.Tensor] = None):
         """End of prefill for `slots`: S = S_new, snapshot of its cold columns, glog = 0,
         t = phase (0 by default) — scale/vllm_v4_patch.py:123-137."""
         slots = torch.as_tensor(slots, dtype=torch.long)
-        self.S[slots] = S_new.to(self.dtype)
+        self.S[slots] = self._round_master(S_new.to(self.dtype))
         self._store(slots, self.S[slots][..., self.k:])
         self.glog[slots] = 0
         self.t[slots] = 0 if phase is None else torch.as_tensor(phase, dtype=torch.int64)
@@ -269,6 +288,9 @@ class NativeV4:
         t = self.t[slots] + 1
         self.t[slots] = t
         flush = (t % c == 0)
+        if self.master != "fp32" and bool(flush.any()):
+            S = torch.where(flush[:, None, None, None], self._round_master(S), S)
+            self.S[slots] = S
         if self.cold == "fp8" and self.fp8_restore:
             old = self._read(slots)
             self._store(slots, torch.where(flush[:, None, None, None], S[..., k:], old))
@@ -292,9 +314,12 @@ class TieredV4:
     split does not hold the full state: the exact cold state exists only right
     after a flush. materialize() rebuilds it from the pending ring entries."""
 
-    def __init__(self, slots: int, H: int, P: int, N: int, G: int, k: int, c: int, dtype=torch.float32):
-        assert 0 < k < N and c >= 1
+    def __init__(self, slots: int, H: int, P: int, N: int, G: int, k: int, c: int, dtype=torch.float32,
+                 master: str = "fp32"):
+        assert 0 < k < N and c >= 1 and master in ("fp32", "bf16")
         self.H, self.P, self.N, self.G, self.k, self.c, self.dtype = H, P, N, G, k, c, dtype
+        # "bf16": the cold tier is a bf16 master, rounded at join and at every flush
+        self.master = master
         self.hot = torch.zeros(slots, H, P, k, dtype=dtype)
         self.cold = torch.zeros(slots, H, P, N - k, dtype=dtype)
         self.glog = torch.zeros(slots, H, dtype=dtype)
@@ -305,11 +330,14 @@ class TieredV4:
         slots = torch.as_tensor(slots, dtype=torch.long)
         S_new = S_new.to(self.dtype)
         self.hot[slots] = S_new[..., :self.k]
-        self.cold[slots] = S_new[..., self.k:]
+        self.cold[slots] = self._round(S_new[..., self.k:])
         self.glog[slots] = 0
         self.t[slots] = 0 if phase is None else torch.as_tensor(phase, dtype=torch.int64)
         for s in slots.tolist():
             self.ring[s] = []
+
+    def _round(self, cold):
+        return cold if self.master == "fp32" else cold.to(torch.bfloat16).to(self.dtype)
 
     def _replay(self, cold0, entries, A):
         """exp(sum a) cold0 + sum_j exp(sum_{i>j} a_i) dt_j x_j (x) B'_j."""
@@ -340,7 +368,7 @@ class TieredV4:
         for i, s in enumerate(slots.tolist()):
             entry = (dt[i], xf[i], Bp[i, :, k:])
             if int(t[i]) % c == 0:
-                self.cold[s] = self._replay(self.cold[s], self.ring[s] + [entry], prm.A)
+                self.cold[s] = self._round(self._replay(self.cold[s], self.ring[s] + [entry], prm.A))
                 self.ring[s] = []
                 self.glog[s] = 0
             else:

@@ -42,6 +42,9 @@ def test_abi_version_and_codes_match_header():
     assert int(d["NSSM_COLD_FP32"]) == _lib.COLD_FP32
     assert int(d["NSSM_COLD_BF16"]) == _lib.COLD_BF16
     assert int(d["NSSM_COLD_FP8"]) == _lib.COLD_FP8
+    assert int(d["NSSM_COLD_NONE"]) == _lib.COLD_NONE
+    assert int(d["NSSM_COLD_BF16_SINGLE"]) == _lib.COLD_BF16_SINGLE
+    assert int(d["NSSM_COLD_FP8_BF16M"]) == _lib.COLD_FP8_BF16M
     assert (int(d["NSSM_DT_F32"]), int(d["NSSM_DT_BF16"])) == (_lib.DT_F32, _lib.DT_BF16)
     for code in ("NSSM_E_NULL", "NSSM_E_DIMS", "NSSM_E_ALIGN", "NSSM_E_KIND", "NSSM_E_LAUNCH", "NSSM_E_TUNING",
                  "NSSM_E_WORKSPACE"):
@@ -108,6 +111,12 @@ def test_tier_sizes():
     assert sz[4] == 256 * 128 * 4 * 80 * 2 and sz[6] == 256 * 8 * 4 * 96 * 4
     assert L.nssm_tier_sizes(448, 128, 80, 128, 8, 32, 4, _lib.COLD_FP8, sz) == 0
     assert sz[1] == 448 * 128 * 80 * 96 and sz[2] == 448 * 128 * 80 * 4 and sz[3] == 448 * 128 * 80 * 96 * 4
+    # bf16 masters: one bf16 copy (no master); e4m3 copy + row scale + bf16 master
+    assert L.nssm_tier_sizes(256, 128, 80, 128, 8, 32, 4, _lib.COLD_BF16_SINGLE, sz) == 0
+    assert sz[1] == rows * 96 * 2 and sz[2] == 0 and sz[3] == 0 and sz[6] == 256 * 8 * 4 * 96 * 4
+    assert L.nssm_tier_sizes(448, 128, 80, 128, 8, 32, 4, _lib.COLD_FP8_BF16M, sz) == 0
+    assert sz[1] == 448 * 128 * 80 * 96 and sz[2] == 448 * 128 * 80 * 4 and sz[3] == 448 * 128 * 80 * 96 * 2
+    assert L.nssm_tier_sizes(4, 8, 80, 128, 1, 32, 4, 6, sz) == -4
     assert L.nssm_tier_sizes(4, 8, 80, 64, 1, 32, 4, 0, sz) == -2  # d_state must be 128
     assert L.nssm_tier_sizes(4, 8, 80, 128, 1, 32, 65, 0, sz) == -2  # c above 64
     assert L.nssm_tier_sizes(4, 8, 80, 128, 1, 32, 4, 7, sz) == -4

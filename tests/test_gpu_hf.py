@@ -177,11 +177,16 @@ def test_native_install_corr_gives_the_untiered_model():
     assert float((l_stale - l_full).abs().max() / scale) > 1e-4  # the stale readout is not exact
 
 
-def test_fused_install_fp8_matches_oracle(monkeypatch):
+@pytest.mark.parametrize("master", ["bf16", "fp32"])
+def test_fused_install_fp8_matches_oracle(monkeypatch, master):
+    """install(cold="fp8") over the fused path's bf16 shadow master (the default) or an
+    fp32 master: y within 2e-2 of the reference's fp8 emulation over the exact fp32
+    state, and within 1e-4 of the oracle with the same master."""
     from nested_ssm_amd import v4_fused_decode as F
 
     model = _tiny_model(seed=5)
-    assert F.install(model, pb=32, c=4, cold="fp8") == 2
+    kw = {} if master == "bf16" else dict(master=master)
+    assert F.install(model, pb=32, c=4, cold="fp8", **kw) == 2
     for m in model.modules():
         if type(m).__name__ == "NemotronHMamba2Mixer":
             assert m._v4R is not None and m._v4R.dtype == torch.float32
@@ -195,10 +200,15 @@ def test_fused_install_fp8_matches_oracle(monkeypatch):
         li = m.layer_idx
         prm = _oracle_params(m, 0.0)
         ref = oracle.NativeV4(2, m.num_heads, m.head_dim, N, 32, 4, cold="fp8")
-        ref.join(torch.arange(2), _rot(rec.states[li], prm.R, m.num_heads))
+        same = oracle.NativeV4(2, m.num_heads, m.head_dim, N, 32, 4, cold="fp8", master=master)
+        S0 = _rot(rec.states[li], prm.R, m.num_heads)
+        ref.join(torch.arange(2), S0)
+        same.join(torch.arange(2), S0)
         for (x, B, C, dt), y in zip(rec.inputs[li], rec.ys[li]):
             y_ref = ref.step(x, B, C, dt, prm)
+            y_same = same.step(x, B, C, dt, prm)
             assert float((y - y_ref).norm() / y_ref.norm()) <= 2e-2
+            assert float((y - y_same).norm() / y_same.norm()) <= 1e-4
 
 
 def test_all_hot_install_is_rotation_invariant_and_tracks_stock():

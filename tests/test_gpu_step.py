@@ -5,7 +5,7 @@ import pytest
 import torch
 
 import oracle
-from helpers import assert_close32, dev_params, max_rel, to_dev
+from helpers import assert_close_flips, assert_close32, dev_params, max_rel, to_dev
 from nested_ssm_amd import V4Tier, fresh_step, set_launch
 
 pytestmark = pytest.mark.gpu
@@ -56,13 +56,14 @@ def test_fresh_dt_min_and_identity_rotation():
     assert_close32(S_dev, S_ref, "fresh(dt_min) state", **FP32_TOL)
 
 
-def _run_v4(b, H, G, P, k, c, cold, steps, seed, slots=None, phase=None, check_state_every=1, exact=False):
+def _run_v4(b, H, G, P, k, c, cold, steps, seed, slots=None, phase=None, check_state_every=1, exact=False,
+            master="fp32"):
     gen, prm, S0 = _setup(b, H, P, G, seed)
     dprm = dev_params(prm)
-    ref = oracle.NativeV4(b, H, P, 128, k, c, cold=cold, exact=exact)
+    ref = oracle.NativeV4(b, H, P, 128, k, c, cold=cold, exact=exact, master=master)
     ph = None if phase is None else torch.as_tensor(phase, dtype=torch.int32)
     ref.join(torch.arange(b), S0, phase=None if ph is None else ph.long())
-    tier = V4Tier(b, H, P, G, k_hot=k, c=c, cold=cold)
+    tier = V4Tier(b, H, P, G, k_hot=k, c=c, cold=cold, master=master)
     tier.join(dprm, *to_dev(S0), phase=None if ph is None else ph.cuda())
     worst = 0.0
     for step in range(steps):
@@ -89,7 +90,10 @@ def _run_v4(b, H, G, P, k, c, cold, steps, seed, slots=None, phase=None, check_s
             assert_close32(y, y_ref, f"v4[{cold},k{k},c{c}] y step {step}", **FP32_TOL)
         if check_state_every and (step + 1) % check_state_every == 0:
             assert_close32(tier.hot, ref.S[..., :k], f"hot step {step}", **FP32_TOL)
-            assert_close32(tier.materialize(dprm), ref.S, f"materialized state step {step}", **FP32_TOL)
+            if master == "fp32":
+                assert_close32(tier.materialize(dprm), ref.S, f"materialized state step {step}", **FP32_TOL)
+            else:  # a bf16 master: isolated one-ulp rounding flips (see assert_close_flips)
+                assert_close_flips(tier.materialize(dprm), ref.S, f"materialized state step {step}")
     return tier, ref, worst
 
 
@@ -302,3 +306,92 @@ def test_v4_exact_readout_equals_fresh_at_9b_shape_alternating_modes():
             assert_close32(y, y_fresh, f"exact y step {step}", rtol=1e-5, atol=2e-5)
         assert_close32(tier.hot, S[..., :k], f"hot step {step}")
     assert_close32(tier.materialize(dprm), S, "materialized state")
+
+
+# --------------------------------------------------------------------------- bf16 masters
+@pytest.mark.parametrize("cold,k,c,P", [
+    ("bf16", 32, 4, 80), ("fp8", 32, 4, 80), ("bf16", 32, 16, 80), ("fp8", 64, 33, 48), ("bf16", 96, 40, 80),
+    ("fp8", 32, 64, 256), ("bf16", 64, 1, 80), ("fp8", 32, 17, 80)])
+def test_v4_bf16_master_matches_oracle(cold, k, c, P):
+    """The fused path's bf16 masters (scale/v4_fused_decode.py:149,156-158): one bf16
+    copy (bf16 cold) or a bf16 master beside the e4m3 copy (fp8 cold), rounded at the
+    join and every flush, against the oracle's master="bf16" step; windows replayed in
+    the stream kernel (c <= 32) and on the matrix cores (c > 32)."""
+    b, H, G = 3, 8, 2
+    tier, ref, worst = _run_v4(b, H, G, P, k, c, cold, steps=2 * c + 5, seed=120 + k + c + P,
+                               check_state_every=max(1, c // 2), master="bf16")
+    if cold == "bf16":  # the single copy equals the oracle's rounded master up to isolated flips
+        # (a flip is one bf16 ulp of the value at that flush and persists in the master,
+        # decaying, so it is bounded norm-wise, not relative to the element's value now)
+        got = tier.cold_t.cpu().float()
+        assert float((got != ref.snap).float().mean()) < 1e-3
+        assert_close_flips(got, ref.snap, "bf16 single copy", frac_max=1e-3)
+        assert tier.master is None
+    else:
+        assert tier.master.dtype == torch.bfloat16
+        assert float((tier.cold_t.cpu() != ref.q8.view(torch.uint8)).float().mean()) < 1e-3
+        assert_close32(tier.scale.cpu(), ref.sc8[..., 0], "fp8 scale", rtol=2.0 ** -7, atol=0)
+        assert 0 < worst <= 2e-2
+
+
+def test_fp8_bf16_master_within_the_reference_fp8_emulation():
+    """Config-3 storage (e4m3 read copy, per-row scale) kept over a bf16 master, against
+    the reference's fp8-cold emulation with the exact fp32 state
+    (scale/vllm_v4_patch.py:106-120, 164-179): y within 2e-2 relative at every one of
+    128 steps, random phases."""
+    b, H, G, P, k, c = 4, 16, 2, 80, 32, 4
+    gen, prm, S0 = _setup(b, H, P, G, seed=131)
+    dprm = dev_params(prm)
+    ref = oracle.NativeV4(b, H, P, 128, k, c, cold="fp8")
+    phase = torch.tensor([0, 3, 1, 2], dtype=torch.int32)
+    ref.join(torch.arange(b), S0, phase=phase.long())
+    tier = V4Tier(b, H, P, G, k_hot=k, c=c, cold="fp8", master="bf16")
+    tier.join(dprm, *to_dev(S0), phase=phase.cuda())
+    worst = 0.0
+    for step in range(128):
+        x, B, C, dt = oracle.make_step_inputs(b, H, P, 128, G, gen)
+        y_ref = ref.step(x, B, C, dt, prm)
+        y = tier.step(dprm, *to_dev(x, B, C, dt))
+        r = max_rel(y.cpu(), y_ref)
+        worst = max(worst, r)
+        assert r <= 2e-2, f"step {step}: rel err {r:.3g} against the fp32-state fp8 emulation"
+    assert worst > 0
+
+
+@pytest.mark.parametrize("cold", ["bf16", "fp8"])
+def test_v4_bf16_master_ragged_phases_and_slots(cold):
+    """bf16 masters with requests in a subset of slots, their own phases, and join/leave."""
+    slots, H, G, P, k, c = 6, 8, 2, 48, 32, 4
+    gen, prm, S0 = _setup(slots, H, P, G, seed=141)
+    dprm = dev_params(prm)
+    ref = oracle.NativeV4(slots, H, P, 128, k, c, cold=cold, master="bf16")
+    tier = V4Tier(slots, H, P, G, k_hot=k, c=c, cold=cold, master="bf16")
+    phase = torch.tensor([0, 1, 2, 3, 1, 2], dtype=torch.int32)
+    ref.join(torch.arange(slots), S0, phase=phase.long())
+    tier.join(dprm, *to_dev(S0), phase=phase.cuda())
+    for step in range(40):
+        if step % 8 == 7:
+            leave = step % slots
+            Snew = oracle.make_state(1, H, P, 128, gen)
+            ph = torch.randint(0, c, (1,), generator=gen, dtype=torch.int32)
+            ref.join(torch.tensor([leave]), Snew, phase=ph.long())
+            tier.join(dprm, *to_dev(Snew), slot_ids=torch.tensor([leave], dtype=torch.int32).cuda(),
+                      phase=ph.cuda())
+        sl = torch.randperm(slots, generator=gen)[: 4 + step % 3].to(torch.int32)
+        x, B, C, dt = oracle.make_step_inputs(len(sl), H, P, 128, G, gen)
+        y_ref = ref.step(x, B, C, dt, prm, slots=sl.long())
+        y = tier.step(dprm, *to_dev(x, B, C, dt), slot_ids=sl.cuda())
+        if cold == "fp8":
+            assert max_rel(y.cpu(), y_ref) <= 2e-2
+        else:
+            assert_close_flips(y, y_ref, f"ragged bf16 single y step {step}")
+    assert_close_flips(tier.materialize(dprm), ref.S, "ragged materialized state")
+    assert torch.equal(tier.t[:, 0].cpu().long(), ref.t)
+
+
+@pytest.mark.parametrize("cold,k,c", [("bf16", 32, 4), ("fp8", 32, 4), ("bf16", 32, 40), ("fp8", 64, 33)])
+def test_v4_bf16_master_exact_readout(cold, k, c):
+    """The exact (corr=1) readout over bf16 masters: exact with respect to the rounded
+    snapshot, as the oracle's exact mode with master="bf16"."""
+    _run_v4(4, 8, 2, 80, k, c, cold, steps=2 * c + 5, seed=150 + k + c, phase=[0, 1, c - 1, c // 2],
+            check_state_every=max(1, c // 2), exact=True, master="bf16")

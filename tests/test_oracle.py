@@ -348,6 +348,76 @@ def test_native_v4_bf16_snapshot_is_rne_of_fp32():
     assert torch.equal(nb.snap, nb.S[..., k:].to(torch.bfloat16).float())
 
 
+def _bf16(v: torch.Tensor) -> torch.Tensor:
+    return v.to(torch.bfloat16).to(v.dtype)
+
+
+@pytest.mark.parametrize("cold", ["bf16", "fp8"])
+def test_native_v4_bf16_master_is_fresh_recurrence_rounded_at_each_flush(cold):
+    """master="bf16" (the fused path's bf16 master, scale/v4_fused_decode.py:149,156-158)
+    against a brute-force restatement built from fresh_step in fp64: the state is the
+    fresh recurrence whose cold columns are rounded to bf16 at the join and after every
+    flush token, and the read copy comes from those rounded values (bf16: the same
+    values, a single copy; e4m3: quant_fp8 of them). Rounding at every token, never, or
+    quantizing the unrounded state each fails one of the checks."""
+    b, H, P, G, k, c = 2, 8, 16, 2, 32, 4
+    gen, prm, S0 = _small(seed=41, b=b, H=H, P=P, G=G)
+    f64 = torch.float64
+    nat = oracle.NativeV4(b, H, P, N, k, c, cold=cold, dtype=f64, master="bf16")
+    exact = oracle.NativeV4(b, H, P, N, k, c, cold=cold, dtype=f64)  # fp32 (unrounded) master
+    nat.join(torch.arange(b), S0.double())
+    exact.join(torch.arange(b), S0.double())
+    S = S0.double().clone()
+    S[..., k:] = _bf16(S[..., k:])
+    every = S.clone()  # rounded at every token: a plausible mistake
+    prm64 = prm.to(f64)
+    for step in range(3 * c):
+        ins = oracle.make_step_inputs(b, H, P, N, G, gen)
+        nat.step(*ins, prm)
+        exact.step(*ins, prm)
+        oracle.fresh_step(S, *ins, prm64, dtype=f64)
+        oracle.fresh_step(every, *ins, prm64, dtype=f64)
+        every[..., k:] = _bf16(every[..., k:])
+        if (step + 1) % c == 0:
+            S[..., k:] = _bf16(S[..., k:])
+            if cold == "bf16":  # single copy: the read copy is the master
+                assert torch.equal(nat.snap, S[..., k:])
+            else:
+                q, sc = oracle.quant_fp8(S[..., k:].float())
+                assert torch.equal(nat.q8.view(torch.uint8), q.view(torch.uint8))
+                assert torch.equal(nat.sc8, sc)
+                q_unrounded, _ = oracle.quant_fp8(exact.S[..., k:].float())
+                assert not torch.equal(q.view(torch.uint8), q_unrounded.view(torch.uint8))
+        assert torch.allclose(nat.S, S, rtol=0, atol=1e-12)
+    assert not torch.allclose(every, S, rtol=0, atol=1e-6)
+    assert not torch.allclose(exact.S, S, rtol=0, atol=1e-6)
+
+
+def test_tiered_bf16_master_equals_native_bf16_master_ragged():
+    """The chunked replay into a bf16 master (round the replayed window once) equals
+    the per-token recurrence rounded at the flush, in fp64, with per-slot phases,
+    partial batches and join/leave."""
+    slots, H, P, G, k, c = 5, 4, 8, 2, 32, 4
+    gen, prm, S0 = _small(seed=42, b=slots, H=H, P=P, G=G)
+    phase = torch.tensor([0, 1, 2, 3, 2])
+    f64 = torch.float64
+    nat = oracle.NativeV4(slots, H, P, N, k, c, cold="bf16", dtype=f64, master="bf16")
+    tie = oracle.TieredV4(slots, H, P, N, G, k, c, dtype=f64, master="bf16")
+    nat.join(torch.arange(slots), S0.double(), phase)
+    tie.join(torch.arange(slots), S0.double(), phase)
+    for step in range(30):
+        if step == 13:
+            Sj = oracle.make_state(1, H, P, N, gen).double()
+            nat.join(torch.tensor([2]), Sj, torch.tensor([3]))
+            tie.join(torch.tensor([2]), Sj, torch.tensor([3]))
+        sl = torch.randperm(slots, generator=gen)[:3 + step % 3]
+        x, B, C, dt = oracle.make_step_inputs(len(sl), H, P, N, G, gen)
+        y1 = nat.step(x, B, C, dt, prm, slots=sl)
+        y2 = tie.step(x, B, C, dt, prm, slots=sl)
+        assert torch.allclose(y1, y2, atol=1e-12)
+    assert torch.allclose(tie.materialize(torch.arange(slots), prm), nat.S, atol=1e-12)
+
+
 def test_fp8_readout_matches_fp64_loop():
     gen = torch.Generator().manual_seed(19)
     R_, Nc, Pd = 3, 6, 5
