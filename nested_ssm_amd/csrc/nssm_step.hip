@@ -816,7 +816,7 @@ __device__ __forceinline__ void stream_units(const StepArgs& a, int slot, int bi
     for (int i = 0; i < U; ++i) {
       const int u = u0 + i * nw;
       if (u < units) {
-        const int j = u / RG;
+        const int j = __builtin_amdgcn_readfirstlane(u / RG);  // wave-uniform
         const int p = (u - j * RG) * 8 + rr;
         const bool flushing = MIXED && hdb[j * HD_STRIDE + HD_FLUSH] != 0.f;
         unit_load<K, COLD>(a, ((size_t)slot * H + h0 + j) * P + p, ((size_t)bi * H + h0 + j) * P + p, q, d[i],
@@ -827,7 +827,7 @@ __device__ __forceinline__ void stream_units(const StepArgs& a, int slot, int bi
     for (int i = 0; i < U; ++i) {
       const int u = u0 + i * nw;
       if (u < units) {
-        const int j = u / RG;
+        const int j = __builtin_amdgcn_readfirstlane(u / RG);  // wave-uniform
         const int p = (u - j * RG) * 8 + rr;
         const float* hd = hdb + j * HD_STRIDE;
         const bool flushing = MIXED && hd[HD_FLUSH] != 0.f;
@@ -845,7 +845,7 @@ __device__ __forceinline__ void stream_units(const StepArgs& a, int slot, int bi
 // one workgroup per (request, block of hpw heads of one group). FUSED (short windows):
 // a flushing head's cold columns are flushed here; otherwise by the flush kernel.
 template <int K, int COLD, bool FUSED, bool EXACT>
-__device__ __forceinline__ void stream_body(const StepArgs& a) {
+__device__ __forceinline__ void stream_body(const StepArgs& a, const float* __restrict__ hd_ro) {
   using C = Cfg<K, COLD>;
   constexpr int HS = C::HS, CS = C::CS, CSR = C::CSR, CWR = C::CWR;
   constexpr bool TIERED = C::TIERED;
@@ -888,7 +888,14 @@ __device__ __forceinline__ void stream_body(const StepArgs& a) {
     else Cq[i] = 0.f;
   }
 
-  const float* hdb = ws.hd + ((size_t)bi * H + h0) * HD_STRIDE;
+  // Per-head scalars. A wave's head index is uniform (readfirstlane) and, read through
+  // the kernel's hd_ro argument (noalias: no kernel writes the workspace it reads), they
+  // become scalar loads instead of one vector load per unit. Measured on MI355X, 27
+  // layers, ms per step: e4m3 cold over a bf16 master, B = 448, c = 4: 12.2 -> 11.75;
+  // single bf16 copy, c = 4: 7.41 -> 6.94; fresh 12.27 -> 12.00. The fp32 cold tier was
+  // slower with them (c = 4: 9.11 -> 9.60; c = 64: 8.21 -> 8.56) and keeps vector loads.
+  const float* __restrict__ hdb =
+      (COLD == NSSM_COLD_FP32 && TIERED ? static_cast<const float*>(ws.hd) : hd_ro) + ((size_t)bi * H + h0) * HD_STRIDE;
   const int RG = P >> 3;
   const int units = hpw * RG;
   bool any_flush = false;
@@ -918,10 +925,10 @@ __device__ __forceinline__ void stream_body(const StepArgs& a) {
     for (int u = wave; u < units; u += nw) {
       UnitRaw<K, COLD> dcur;
       {
-        const int j = u / RG, p = (u - j * RG) * 8 + rr;
+        const int j = __builtin_amdgcn_readfirstlane(u / RG), p = (u - j * RG) * 8 + rr;
         unit_load<K, COLD>(a, ((size_t)slot * H + h0 + j) * P + p, ((size_t)bi * H + h0 + j) * P + p, q, dcur);
       }
-      const int j = u / RG;
+      const int j = __builtin_amdgcn_readfirstlane(u / RG);
       const int p = (u - j * RG) * 8 + rr;
       const size_t sh = (size_t)slot * H + h0 + j, rh = (size_t)bi * H + h0 + j;
       const float* hd = hdb + j * HD_STRIDE;
@@ -941,23 +948,24 @@ __device__ __forceinline__ void stream_body(const StepArgs& a) {
 // step, fp32 and e4m3 unchanged or better); wider hot tiers spill under that bound and
 // keep the compiler's choice, as does the untiered kernel (it spills: 12.2 -> 12.8 ms).
 template <int K, int COLD, bool FUSED, bool EXACT>
-__global__ void __launch_bounds__(kMaxWaves * 64) __attribute__((amdgpu_waves_per_eu(5))) stream_kernel_o5(StepArgs a) {
-  stream_body<K, COLD, FUSED, EXACT>(a);
+__global__ void __launch_bounds__(kMaxWaves * 64) __attribute__((amdgpu_waves_per_eu(5))) stream_kernel_o5(StepArgs a, const float* __restrict__ hd_ro) {
+  stream_body<K, COLD, FUSED, EXACT>(a, hd_ro);
 }
 
 template <int K, int COLD, bool FUSED, bool EXACT>
-__global__ void __launch_bounds__(kMaxWaves * 64) stream_kernel(StepArgs a) {
-  stream_body<K, COLD, FUSED, EXACT>(a);
+__global__ void __launch_bounds__(kMaxWaves * 64) stream_kernel(StepArgs a, const float* __restrict__ hd_ro) {
+  stream_body<K, COLD, FUSED, EXACT>(a, hd_ro);
 }
 
 template <int K, int COLD, bool FUSED, bool EXACT>
 void launch_stream(dim3 grid, dim3 block, size_t lds, hipStream_t st, const StepArgs& a) {
-  if constexpr (K == 32) hipLaunchKernelGGL((stream_kernel_o5<K, COLD, FUSED, EXACT>), grid, block, lds, st, a);
-  else hipLaunchKernelGGL((stream_kernel<K, COLD, FUSED, EXACT>), grid, block, lds, st, a);
+  const float* hd_ro = Ws(a.ws, a.b, a.H, a.G, a.c).hd;  // the per-head scalars prep wrote
+  if constexpr (K == 32) hipLaunchKernelGGL((stream_kernel_o5<K, COLD, FUSED, EXACT>), grid, block, lds, st, a, hd_ro);
+  else hipLaunchKernelGGL((stream_kernel<K, COLD, FUSED, EXACT>), grid, block, lds, st, a, hd_ro);
 }
 
-__global__ void __launch_bounds__(kMaxWaves * 64) fresh_stream_kernel(StepArgs a) {
-  stream_body<kN, NSSM_COLD_FP32, false, false>(a);
+__global__ void __launch_bounds__(kMaxWaves * 64) fresh_stream_kernel(StepArgs a, const float* __restrict__ hd_ro) {
+  stream_body<kN, NSSM_COLD_FP32, false, false>(a, hd_ro);
 }
 
 // ---------------------------------------------------------------------------
@@ -1766,7 +1774,7 @@ int launch_pair(const StepArgs& a, const Launch& L, hipStream_t st) {
     }
     return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
   }
-  if constexpr (K == kN) hipLaunchKernelGGL(fresh_stream_kernel, sgrid, sblock, 0, st, a);
+  if constexpr (K == kN) hipLaunchKernelGGL(fresh_stream_kernel, sgrid, sblock, 0, st, a, Ws(a.ws, a.b, a.H, a.G, a.c).hd);
   else if (TIERED && a.exact) launch_stream<K, COLD, false, TIERED>(sgrid, sblock, 0, st, a);
   else launch_stream<K, COLD, false, false>(sgrid, sblock, 0, st, a);
   if constexpr (TIERED) {
