@@ -325,11 +325,11 @@ def measured_traffic(key):
 def kernel_label(head, args):
     """The launches of one layer-token (the unit the roofline is measured on)."""
     if head == "fresh":
-        return "prep_kernel<false> + stream_kernel<128, fp32, all> (one layer-token, two launches)"
+        return "prep_kernel<false> + unit_kernel<128, fp32> (one layer-token, two launches)"
     if args.c <= 32:
-        return (f"prep_kernel<true> + stream_kernel<{args.k}, {args.cold}, fused flush> "
+        return (f"prep_kernel<true> + unit_kernel<{args.k}, {args.cold}, fused flush> "
                 f"(one layer-token, two launches)")
-    return (f"prep_kernel<true> + stream_kernel<{args.k}, {args.cold}> + flush_kernel<{args.k}, {args.cold}> "
+    return (f"prep_kernel<true> + unit_kernel<{args.k}, {args.cold}> + flush_kernel<{args.k}, {args.cold}> "
             f"(one layer-token, three launches)")
 
 

@@ -216,9 +216,10 @@ int nssm_gated_rmsnorm(int32_t b, int32_t I, int32_t gs, int32_t dtype, const fl
                        const void* gate, int64_t gate_stride, const void* weight, float eps,
                        void* out, void* stream);
 
-/* Launch-shape override for the step kernels (0, 0 = automatic): heads per
- * workgroup and waves per workgroup. Process-wide; for tuning sweeps. */
-int nssm_set_launch(int32_t heads_per_wg, int32_t waves_per_wg);
+/* Launch-shape override for the stream kernel (0 = automatic): units (waves, each
+ * streaming 8 headdim rows of one head) per workgroup, at most 4; a step returns
+ * NSSM_E_TUNING when it does not divide P/8. Process-wide; for tuning sweeps. */
+int nssm_set_launch(int32_t units_per_wg);
 
 /* Host-side (CPU) conversions used by the kernels, exported so the CPU test
  * suite can compare them bit for bit with torch's casts. */

@@ -72,7 +72,7 @@ def lib():
     L.nssm_gated_rmsnorm.argtypes = [c_i32, c_i32, c_i32, c_i32, c_vp, c_vp, c_i64, c_vp, ctypes.c_float, c_vp, c_vp]
     L.nssm_conv_update.argtypes = [c_i32, c_i32, c_i32, c_i32, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32,
                                    c_vp, c_vp, c_vp, c_vp]
-    L.nssm_set_launch.argtypes = [c_i32, c_i32]
+    L.nssm_set_launch.argtypes = [c_i32]
     L.nssm_host_f32_to_e4m3fn.argtypes = [c_vp, c_vp, ctypes.c_int64]
     L.nssm_host_e4m3fn_to_f32.argtypes = [c_vp, c_vp, ctypes.c_int64]
     L.nssm_host_f32_to_bf16.argtypes = [c_vp, c_vp, ctypes.c_int64]

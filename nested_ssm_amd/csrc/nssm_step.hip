@@ -1,24 +1,26 @@
 // gfx950 kernels for the Mamba2 decode-step recurrent-state update with
 // nested hot/cold tiering, and the C ABI declared in include/nssm.h.
 //
-// A tiered layer-token is three launches on the caller's stream (the untiered
-// step: prep and stream):
+// A tiered layer-token is two launches on the caller's stream when the flush window
+// is at most 32 tokens (prep, stream), three beyond (prep, stream, flush); the
+// untiered step is prep and stream:
 //
-//  prep    one workgroup per (request, group). Rotates B and C once
+//  prep    one workgroup per (group, block of requests). Rotates B and C once
 //          (B' = R_g B, C' = R_g C, fp32) into the workspace, computes each
 //          head's dt, decay, the stale-read factor exp(glog), the flush flag
 //          and, at a flush, the decay weights of the buffered window; updates
-//          t, nv, glog; appends this token (x, dt, B' cold columns) to the ring
+//          t, nv, glog; appends this token (dt, B' cold columns) to the ring
 //          at position t % c. A flush token sits at c-1, so a flush window is
 //          always ring positions [c-m, c).
-//  stream  one workgroup per (request, head block): streams the state rows.
-//          A "unit" is 8 consecutive headdim rows p of one head; lane l works
-//          on row p0 + (l >> 3), and a row's C.h readout is a sum over its 8
-//          lanes (three DPP steps). Hot columns [0, K) are read and written
-//          every token; cold columns [K, N) are only read (the stale readout),
-//          and not at all for a head that flushes at this token.
-//  flush   the cold columns of the heads that flush: decayed snapshot plus the
-//          window contraction on the matrix cores, and their stale readout.
+//  stream  one wave per "unit", 8 consecutive headdim rows p of one head (lane l
+//          works on row p0 + (l >> 3), and a row's C.h readout is a sum over its
+//          8 lanes, three DPP steps), a few units of one head per workgroup. Hot
+//          columns [0, K) are read and written every token; cold columns [K, N)
+//          are only read (the stale readout) except by a head that flushes at
+//          this token, whose short window is replayed here.
+//  flush   (windows over 32 tokens) the cold columns of the heads that flush:
+//          decayed snapshot plus the window contraction on the matrix cores,
+//          and their stale readout.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -31,7 +33,7 @@ namespace {
 constexpr int kN = 128;  // d_state handled by these kernels
 constexpr int kMaxC = 64;
 constexpr int kMaxHG = 64;  // heads per group
-constexpr int kMaxWaves = 8;
+constexpr int kMaxUnitsPerWg = 4;  // waves (units) per stream workgroup
 constexpr int kMfmaTiles = 4;  // 16 x 16 flush-contraction tiles a wave keeps in registers
 
 typedef float f4 __attribute__((ext_vector_type(4)));
@@ -61,7 +63,7 @@ struct StepArgs {
   const float* R;
   float* y;
   float* ws;  // workspace (see Ws below)
-  int32_t b, slots, H, P, G, HG, c, K, hpw, nhb;
+  int32_t b, slots, H, P, G, HG, c, K;
   int32_t prb;    // requests per prep workgroup
   int32_t exact;  // rank-c exact correction readout instead of the stale one
   int32_t split;  // the flush kernel runs after the stream kernel (prep writes the pair flags)
@@ -126,23 +128,6 @@ __device__ __forceinline__ float softplus_f(float v) { return v > 20.f ? v : log
 #ifndef NSSM_NT_STORE
 #define NSSM_NT_STORE 1
 #endif
-// units (8-row blocks) whose loads a wave keeps in flight together. Measured on
-// MI355X (B = 256, 27 layers, k_hot = 32, ms per step at c = 4 / 16): bf16 cold 2 units
-// 9.80 / 7.33, 3 units 9.42 / 7.21, 4 units 10.02 / 8.19; fp32 and e4m3 best with 2
-// (fp32 with 3: 10.28 / 9.27).
-#ifndef NSSM_UNROLL
-#define NSSM_UNROLL 2
-#endif
-#ifndef NSSM_UNROLL_BF16
-#define NSSM_UNROLL_BF16 3
-#endif
-#ifndef NSSM_UNROLL_FP8
-#define NSSM_UNROLL_FP8 2
-#endif
-#ifndef NSSM_UNROLL_BF16S
-#define NSSM_UNROLL_BF16S 3
-#endif
-
 template <class T>
 __device__ __forceinline__ T ld_stream(const T* p) {
   if constexpr (NSSM_NT_LOAD) return __builtin_nontemporal_load(p);
@@ -702,14 +687,13 @@ __device__ __forceinline__ void unit_compute_flush(const StepArgs& a, size_t sh,
                                                    const float (&Bh)[K / 32][4], const float (&Ch)[K / 32][4],
                                                    const float (&Cc)[Cfg<K, COLD>::CSR][4],
                                                    const float (&Cq)[Cfg<K, COLD>::CWR], const float* sU,
-                                                   const float* sBc, int m) {
+                                                   const float* sBc, int m, int ldu, int pofs) {
   using C = Cfg<K, COLD>;
   constexpr int NC = C::NC, CS = C::CS;
   const size_t row = sh * a.P + p, yrow = rh * a.P + p;
   float part = hot_update<K, COLD>(a, row, q, d, hd, Bh, Ch);
   part = fmaf(hd[HD_SNAPF], cold_partial<K, COLD>(d, Cc, Cq), part);
   if constexpr (EXACT) part += corr_partial(a, hd, sh, rh, p, q, d.xp);
-  const int P = a.P;
   const float dtot = hd[HD_DTOT];
   float nvv[CS][4];
 #pragma unroll
@@ -729,7 +713,7 @@ __device__ __forceinline__ void unit_compute_flush(const StepArgs& a, size_t sh,
     for (int e = 0; e < 4; ++e) nvv[s][e] = t[e] * dtot;
   }
   for (int i = 0; i < m; ++i) {
-    const float coef = sU[i * P + p];
+    const float coef = sU[i * ldu + (p - pofs)];
     const float* bc = sBc + i * NC + 4 * q;
 #pragma unroll
     for (int s = 0; s < CS; ++s) {
@@ -745,124 +729,69 @@ __device__ __forceinline__ void unit_compute_flush(const StepArgs& a, size_t sh,
   if (q == 0) a.y[yrow] = fmaf(hd[HD_D], d.xp, part);
 }
 
-// Stage window tokens [k0, k0 + kn) of one head into LDS: sB[e][n] = B'_tok[K + n]
-// (when with_b) and sU[e][p] = w_tok x_tok[p]. Window token m - 1 is this token (B'
-// from the workspace, x from the inputs); token tok < m - 1 sits at ring position
-// c - m + tok (rb0 and rx0 point at the ring rows of window token 0). A thread issues
-// all R loads of a round before its LDS stores.
-template <int NC, int R>
-__device__ __forceinline__ void stage_window(float* sB, float* sU, int k0, int kn, int m, int P,
-                                             const float* rb0, const float* bcur, const uint16_t* rx0,
-                                             const uint16_t* xcur, const float* wgt, bool with_b, int tid,
-                                             int nthr) {
-  constexpr int NB4 = NC / 4;  // float4 per token of B'
-  const int P4 = P >> 2;        // 4 x bf16 per token of x
-  const int nb = with_b ? kn * NB4 : 0, tot = nb + kn * P4;
-  for (int base = 0; base < tot; base += R * nthr) {
-    f4 vb[R];
-    u2v vx[R];
-    float wv[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int i = base + tid + r * nthr;
-      if (i < nb) {
-        const int e = i / NB4, tok = k0 + e;
-        const float* src = tok < m - 1 ? rb0 + (size_t)tok * NC : bcur;
-        vb[r] = *reinterpret_cast<const f4*>(src + 4 * (i - e * NB4));
-      } else if (i < tot) {
-        const int j = i - nb, e = j / P4, tok = k0 + e;
-        const uint16_t* src = tok < m - 1 ? rx0 + (size_t)tok * P : xcur;
-        vx[r] = *reinterpret_cast<const u2v*>(src + 4 * (j - e * P4));
-        wv[r] = wgt[tok];
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int i = base + tid + r * nthr;
-      if (i < nb) {
-        *reinterpret_cast<f4*>(sB + 4 * i) = vb[r];
-      } else if (i < tot) {
-        const u2v v = vx[r];
-        f4 u;
-        u.x = wv[r] * __uint_as_float(v.x << 16);
-        u.y = wv[r] * __uint_as_float(v.x & 0xffff0000u);
-        u.z = wv[r] * __uint_as_float(v.y << 16);
-        u.w = wv[r] * __uint_as_float(v.y & 0xffff0000u);
-        *reinterpret_cast<f4*>(sU + 4 * (i - nb)) = u;
-      }
-    }
+// Window of one head for the rows [p0, p0 + nr) of a unit workgroup, in LDS:
+// sB[i][n] = B'_i[K + n] (the group's cold columns) and sU[i][r] = w_i x_i[p0 + r]; window
+// token m - 1 is this token (B' from the workspace, x from the inputs), token i < m - 1 sits
+// at ring position c - m + i (rb0 and rx0 point at the ring rows of window token 0).
+template <int NC>
+__device__ __forceinline__ void stage_unit_window(float* sB, float* sU, int m, int P, int p0, int nr,
+                                                  const float* rb0, const float* bcur, const uint16_t* rx0,
+                                                  const uint16_t* xcur, const float* wgt, int tid, int nthr) {
+  constexpr int NB4 = NC / 4;
+  for (int i = tid; i < m * NB4; i += nthr) {
+    const int e = i / NB4;
+    const float* src = e < m - 1 ? rb0 + (size_t)e * NC : bcur;
+    reinterpret_cast<f4*>(sB)[i] = *reinterpret_cast<const f4*>(src + 4 * (i - e * NB4));
+  }
+  for (int i = tid; i < m * nr; i += nthr) {
+    const int e = i / nr, r = i - e * nr;
+    const uint16_t xs = e < m - 1 ? rx0[(size_t)e * P + p0 + r] : xcur[p0 + r];
+    sU[i] = wgt[e] * bf2f(xs);
   }
 }
 
-
-// The units of one workgroup, U per wave in flight (all their loads issued before any
-// compute). MIXED: some head of the block flushes at this token, so each unit checks
-// its head's flag (a flushing head's cold columns are neither read nor appended to).
-template <int K, int COLD, bool MIXED, bool EXACT>
-__device__ __forceinline__ void stream_units(const StepArgs& a, int slot, int bi, int h0, int units, int RG, int wave,
-                                             int nw, int q, int rr, const float* __restrict__ hdb,
-                                             const float (&Bh)[K / 32][4], const float (&Ch)[K / 32][4],
-                                             const float (&Cc)[Cfg<K, COLD>::CSR][4],
-                                             const float (&Cq)[Cfg<K, COLD>::CWR]) {
-  constexpr bool TIERED = Cfg<K, COLD>::TIERED;
-  constexpr int U = COLD == NSSM_COLD_BF16          ? NSSM_UNROLL_BF16
-                    : COLD == NSSM_COLD_BF16_SINGLE ? NSSM_UNROLL_BF16S
-                    : Cfg<K, COLD>::E4M3            ? NSSM_UNROLL_FP8
-                                                    : NSSM_UNROLL;
-  const int H = a.H, P = a.P, c = a.c;
-  for (int u0 = wave; u0 < units; u0 += U * nw) {
-    UnitRaw<K, COLD> d[U];
-#pragma unroll
-    for (int i = 0; i < U; ++i) {
-      const int u = u0 + i * nw;
-      if (u < units) {
-        const int j = __builtin_amdgcn_readfirstlane(u / RG);  // wave-uniform
-        const int p = (u - j * RG) * 8 + rr;
-        const bool flushing = MIXED && hdb[j * HD_STRIDE + HD_FLUSH] != 0.f;
-        unit_load<K, COLD>(a, ((size_t)slot * H + h0 + j) * P + p, ((size_t)bi * H + h0 + j) * P + p, q, d[i],
-                           flushing);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < U; ++i) {
-      const int u = u0 + i * nw;
-      if (u < units) {
-        const int j = __builtin_amdgcn_readfirstlane(u / RG);  // wave-uniform
-        const int p = (u - j * RG) * 8 + rr;
-        const float* hd = hdb + j * HD_STRIDE;
-        const bool flushing = MIXED && hd[HD_FLUSH] != 0.f;
-        uint16_t* rx = nullptr;
-        if constexpr (TIERED) {
-          if (!flushing) rx = a.ring_x + (((size_t)slot * H + h0 + j) * c + (int)hd[HD_POS]) * P;
-        }
-        unit_compute<K, COLD, EXACT>(a, (size_t)slot * H + h0 + j, (size_t)bi * H + h0 + j, p, q, d[i], rx, !flushing,
-                                     hd, Bh, Ch, Cc, Cq);
-      }
-    }
-  }
+// Stream kernel: one unit (8 headdim rows of one head) per wave; a workgroup is UW waves
+// on consecutive units of one head (UW divides P / 8), workgroups in request-major, head,
+// row order, so the resident waves stream a compact window of the state. FUSED (short
+// windows): a flushing head's cold columns are replayed here from an LDS copy of the
+// window (the group's B' columns and w_i x_i of the workgroup's rows); otherwise the flush
+// kernel does them and this kernel leaves them alone.
+// Occupancy bound of the stream kernel (waves per SIMD it is compiled for). Without one
+// the fused replay's registers leave 4 waves per SIMD for every launch; measured on MI355X
+// (B = 256, 27 layers, ms per step): fp32 cold c = 4 at 8 waves 8.57 (at 6: 8.59); e4m3
+// over a bf16 master (B = 448) spills at 8 (12.66) and runs 11.62 at 6; wider hot tiers
+// spill above 6 (k_hot = 64) and 5 (k_hot = 96).
+template <int K, int COLD>
+constexpr int unit_waves_per_eu() {
+  return K == 32 ? (Cfg<K, COLD>::E4M3 ? 6 : 8) : K == kN ? 8 : K == 64 ? 6 : 5;
 }
 
-// one workgroup per (request, block of hpw heads of one group). FUSED (short windows):
-// a flushing head's cold columns are flushed here; otherwise by the flush kernel.
 template <int K, int COLD, bool FUSED, bool EXACT>
-__device__ __forceinline__ void stream_body(const StepArgs& a, const float* __restrict__ hd_ro) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(unit_waves_per_eu<K, COLD>()))) unit_kernel(StepArgs a, const float* __restrict__ hd_ro) {
   using C = Cfg<K, COLD>;
-  constexpr int HS = C::HS, CS = C::CS, CSR = C::CSR, CWR = C::CWR;
+  constexpr int HS = C::HS, CS = C::CS, CSR = C::CSR, CWR = C::CWR, NC = C::NC;
   constexpr bool TIERED = C::TIERED;
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
-  const int hb = blockIdx.x % a.nhb, bi = blockIdx.x / a.nhb;
-  const int H = a.H, P = a.P, hpw = a.hpw, c = a.c;
-  const int h0 = hb * hpw, g = h0 / a.HG;
+  const int tid = threadIdx.x, lane = tid & 63, q = lane & 7, rr = lane >> 3;
+  const int uw = blockDim.x >> 6, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int H = a.H, P = a.P, c = a.c, nub = (P >> 3) / uw;
+  const int ub = blockIdx.x % nub, hb = blockIdx.x / nub, h = hb % H, bi = hb / H, g = h / a.HG;
+  const int p0 = ub * uw * 8, p = p0 + wave * 8 + rr;
   const int slot = a.slot_ids ? a.slot_ids[bi] : bi;
+  const size_t rh = (size_t)bi * H + h;
   if (slot < 0 || slot >= a.slots) {  // uniform over the workgroup
-    for (int i = tid; i < hpw * P; i += blockDim.x) a.y[((size_t)bi * H + h0) * P + i] = __builtin_nanf("");
+    if (q == 0) a.y[rh * P + p] = __builtin_nanf("");
     return;
   }
+  const size_t sh = (size_t)slot * H + h, row = sh * P + p;
   const Ws ws(a.ws, a.b, H, a.G, c);
-  const int q = lane & 7, rr = lane >> 3;
+  // per-head scalars through the noalias argument (scalar loads), except over fp32 cold
+  const float* __restrict__ hd = (COLD == NSSM_COLD_FP32 && TIERED ? static_cast<const float*>(ws.hd) : hd_ro) +
+                                 rh * HD_STRIDE;
+  const bool flushing = TIERED && hd[HD_FLUSH] != 0.f;  // uniform over the workgroup
+  UnitRaw<K, COLD> d;
+  // a flushing head's cold columns are needed here only when the replay is fused
+  unit_load<K, COLD>(a, row, rh * P + p, q, d, !FUSED && flushing);
 
-  // per-lane coefficients of group g (rotated by the prep kernel)
   const float* wB = ws.B + ((size_t)bi * a.G + g) * kN;
   const float* wC = ws.C + ((size_t)bi * a.G + g) * kN;
   float Bh[HS][4], Ch[HS][4], Cc[CSR][4], Cq[CWR];
@@ -888,84 +817,25 @@ __device__ __forceinline__ void stream_body(const StepArgs& a, const float* __re
     else Cq[i] = 0.f;
   }
 
-  // Per-head scalars. A wave's head index is uniform (readfirstlane) and, read through
-  // the kernel's hd_ro argument (noalias: no kernel writes the workspace it reads), they
-  // become scalar loads instead of one vector load per unit. Measured on MI355X, 27
-  // layers, ms per step: e4m3 cold over a bf16 master, B = 448, c = 4: 12.2 -> 11.75;
-  // single bf16 copy, c = 4: 7.41 -> 6.94; fresh 12.27 -> 12.00. The fp32 cold tier was
-  // slower with them (c = 4: 9.11 -> 9.60; c = 64: 8.21 -> 8.56) and keeps vector loads.
-  const float* __restrict__ hdb =
-      (COLD == NSSM_COLD_FP32 && TIERED ? static_cast<const float*>(ws.hd) : hd_ro) + ((size_t)bi * H + h0) * HD_STRIDE;
-  const int RG = P >> 3;
-  const int units = hpw * RG;
-  bool any_flush = false;
-  if constexpr (TIERED) {
-    for (int j = 0; j < hpw; ++j) any_flush |= hdb[j * HD_STRIDE + HD_FLUSH] != 0.f;
-  }
-  if (!any_flush) {
-    stream_units<K, COLD, false, EXACT>(a, slot, bi, h0, units, RG, wave, nw, q, rr, hdb, Bh, Ch, Cc, Cq);
-  } else if constexpr (TIERED && !FUSED) {
-    stream_units<K, COLD, true, EXACT>(a, slot, bi, h0, units, RG, wave, nw, q, rr, hdb, Bh, Ch, Cc, Cq);
-  } else if constexpr (TIERED) {
-    extern __shared__ float lds[];
-    constexpr int NC = C::NC;
-    // the window of every head of the block: B' cold columns of the group and
-    // w_i x_i of each head (all heads of a slot share t, so they share m)
-    const int m = min(max((int)hdb[HD_M], 1), c);
-    const size_t rb = ((size_t)slot * a.G + g) * c + (c - m);
-    float* sBc = lds;          // [m][NC]
-    float* sU = lds + c * NC;  // [hpw][m][P]
-    for (int j = 0; j < hpw; ++j)
-      stage_window<NC, 2>(sBc, sU + (size_t)j * m * P, 0, m, m, P, a.ring_b + rb * NC, wB + K,
-                          a.ring_x + (((size_t)slot * H + h0 + j) * c + (c - m)) * P, a.x + ((size_t)bi * H + h0 + j) * P,
-                          ws.w + ((size_t)bi * H + h0 + j) * c, j == 0, tid, blockDim.x);
-    __syncthreads();
-    // one unit at a time: loading the next unit during this one's replay needs more
-    // registers than the 5 waves per SIMD leave, and spills (measured slower)
-    for (int u = wave; u < units; u += nw) {
-      UnitRaw<K, COLD> dcur;
-      {
-        const int j = __builtin_amdgcn_readfirstlane(u / RG), p = (u - j * RG) * 8 + rr;
-        unit_load<K, COLD>(a, ((size_t)slot * H + h0 + j) * P + p, ((size_t)bi * H + h0 + j) * P + p, q, dcur);
-      }
-      const int j = __builtin_amdgcn_readfirstlane(u / RG);
-      const int p = (u - j * RG) * 8 + rr;
-      const size_t sh = (size_t)slot * H + h0 + j, rh = (size_t)bi * H + h0 + j;
-      const float* hd = hdb + j * HD_STRIDE;
-      if (hd[HD_FLUSH] != 0.f) {
-        unit_compute_flush<K, COLD, EXACT>(a, sh, rh, p, q, dcur, hd, Bh, Ch, Cc, Cq, sU + (size_t)j * m * P, sBc,
-                                           m);
-      } else {
-        uint16_t* rx = a.ring_x + (sh * c + (int)hd[HD_POS]) * P;
-        unit_compute<K, COLD, EXACT>(a, sh, rh, p, q, dcur, rx, true, hd, Bh, Ch, Cc, Cq);
-      }
+  if constexpr (FUSED && TIERED) {
+    if (flushing) {
+      extern __shared__ float lds[];
+      const int m = min(max((int)hd[HD_M], 1), c);
+      const int nr = uw * 8;
+      float* sBc = lds;           // [m][NC]
+      float* sU = lds + c * NC;   // [m][nr]
+      stage_unit_window<NC>(sBc, sU, m, P, p0, nr, a.ring_b + (((size_t)slot * a.G + g) * c + (c - m)) * NC, wB + K,
+                            a.ring_x + (sh * c + (c - m)) * P, a.x + rh * P, ws.w + rh * c, tid, blockDim.x);
+      __syncthreads();
+      unit_compute_flush<K, COLD, EXACT>(a, sh, rh, p, q, d, hd, Bh, Ch, Cc, Cq, sU, sBc, m, nr, p0);
+      return;
     }
   }
-}
-
-// The k_hot = 32 stream kernels are compiled for at least 5 waves per SIMD (measured on
-// MI355X, B = 256, 27 layers: bf16 cold c = 4 10.1 -> 9.5 ms, c = 16 7.9 -> 7.3 ms per
-// step, fp32 and e4m3 unchanged or better); wider hot tiers spill under that bound and
-// keep the compiler's choice, as does the untiered kernel (it spills: 12.2 -> 12.8 ms).
-template <int K, int COLD, bool FUSED, bool EXACT>
-__global__ void __launch_bounds__(kMaxWaves * 64) __attribute__((amdgpu_waves_per_eu(5))) stream_kernel_o5(StepArgs a, const float* __restrict__ hd_ro) {
-  stream_body<K, COLD, FUSED, EXACT>(a, hd_ro);
-}
-
-template <int K, int COLD, bool FUSED, bool EXACT>
-__global__ void __launch_bounds__(kMaxWaves * 64) stream_kernel(StepArgs a, const float* __restrict__ hd_ro) {
-  stream_body<K, COLD, FUSED, EXACT>(a, hd_ro);
-}
-
-template <int K, int COLD, bool FUSED, bool EXACT>
-void launch_stream(dim3 grid, dim3 block, size_t lds, hipStream_t st, const StepArgs& a) {
-  const float* hd_ro = Ws(a.ws, a.b, a.H, a.G, a.c).hd;  // the per-head scalars prep wrote
-  if constexpr (K == 32) hipLaunchKernelGGL((stream_kernel_o5<K, COLD, FUSED, EXACT>), grid, block, lds, st, a, hd_ro);
-  else hipLaunchKernelGGL((stream_kernel<K, COLD, FUSED, EXACT>), grid, block, lds, st, a, hd_ro);
-}
-
-__global__ void __launch_bounds__(kMaxWaves * 64) fresh_stream_kernel(StepArgs a, const float* __restrict__ hd_ro) {
-  stream_body<kN, NSSM_COLD_FP32, false, false>(a, hd_ro);
+  uint16_t* rx = nullptr;
+  if constexpr (TIERED) {
+    if (!flushing) rx = a.ring_x + (sh * c + (int)hd[HD_POS]) * P;
+  }
+  unit_compute<K, COLD, EXACT>(a, sh, rh, p, q, d, rx, !flushing, hd, Bh, Ch, Cc, Cq);
 }
 
 // ---------------------------------------------------------------------------
@@ -1583,7 +1453,7 @@ __global__ void __launch_bounds__(kNormThreads) gated_norm_kernel(NormArgs a) {
 
 // ---------------------------------------------------------------------------
 // host side
-int g_hpw_override = 0, g_waves_override = 0;
+int g_units_override = 0;  // units (waves) per stream workgroup, 0 = automatic
 constexpr size_t kMaxLds = 64 * 1024;
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -1624,12 +1494,6 @@ int cu_count() {
   return cache[dev];
 }
 
-// largest divisor of n not above cap
-int divisor_at_most(int n, int cap) {
-  for (int d = cap < n ? cap : n; d >= 1; --d)
-    if (n % d == 0) return d;
-  return 1;
-}
 
 // flush kernel LDS: a window chunk of fch tokens (B' fp32, x bf16, weights), per-tile
 // readout partials (+ e4m3 row maxima); the kernel's own lists take under 2 KB more
@@ -1664,42 +1528,25 @@ int prep_requests(int HG) {
   return r < 1 ? 1 : r > kPrepReq ? kPrepReq : r;
 }
 
-// stream kernel LDS: the whole window of the block's heads when it flushes (fused)
-size_t fused_lds_bytes(int hpw, int P, int c, int K) {
-  return ((size_t)c * (kN - K) + (size_t)hpw * c * P) * sizeof(float);
-}
-
 struct Launch {
-  int hpw, waves;
-  bool fused;
-  size_t lds;
+  int uw;      // units (waves) per stream workgroup
+  bool fused;  // flush windows replayed in the stream kernel
+  size_t lds;  // its LDS bytes (the fused window)
 };
 
-int pick_launch(int H, int G, int P, int K, int c, Launch* out, int kind = NSSM_COLD_FP32) {
-  const int HG = H / G, RG = P / 8;
-  // heads per stream workgroup, measured on MI355X (B = 256, 27 layers, k_hot = 32, ms per
-  // step at c = 4 / 16): fp32 cold 1 head 9.02 / 8.09, 2 heads 9.50 / 8.35; bf16 9.68 / 7.22
-  // vs 9.48 / 7.10; e4m3 8.01 / 6.14 vs 7.98 / 5.75
-  const bool narrow = kind == NSSM_COLD_BF16 || kind == NSSM_COLD_FP8 || kind == NSSM_COLD_FP8_BF16M ||
-                      kind == NSSM_COLD_BF16_SINGLE;  // 16- or 8-bit read copies
-  int hpw = narrow && K < kN && HG % 2 == 0 ? 2 : 1;
-  if (g_hpw_override > 0) {
-    if (HG % g_hpw_override) return NSSM_E_TUNING;
-    hpw = g_hpw_override;
-  }
+// Stream launch shape, measured on MI355X at the 9B shape (B = 256, 27 layers, ms per
+// step): fresh 1 unit per workgroup 11.95, 2 units 12.09; k_hot = 32 tiered 2 units (fp32
+// cold c = 4 8.57, 1 unit 8.78; e4m3 over a bf16 master at B = 448 11.62, 1 unit 11.80).
+int pick_launch(int P, int K, int c, Launch* out, int kind = NSSM_COLD_FP32) {
+  const int RG = P / 8;
   const bool tiered = K < kN && kind != NSSM_COLD_NONE;
+  int uw = tiered ? 2 : 1;
+  if (g_units_override > 0) uw = g_units_override;
+  if (uw > kMaxUnitsPerWg || RG % uw) return NSSM_E_TUNING;
   const bool fused = tiered && c < kFuseMaxC;
-  while (fused && hpw > 1 && fused_lds_bytes(hpw, P, c, K) > kMaxLds) hpw = divisor_at_most(HG, hpw - 1);
-  // measured on MI355X at the 9B shape (P = 80): the untiered stream runs best
-  // with two units per wave (5 waves per head), the tiered one with 4 waves
-  const int waves = g_waves_override > 0 ? g_waves_override
-                    : K < kN && kind != NSSM_COLD_NONE ? (hpw * RG < 4 ? hpw * RG : 4)
-                                         : divisor_at_most(hpw * RG, 5);
-  if (waves > kMaxWaves) return NSSM_E_TUNING;
-  const size_t lds = fused ? fused_lds_bytes(hpw, P, c, K) : 0;
+  const size_t lds = fused ? ((size_t)c * (kN - K) + (size_t)c * uw * 8) * sizeof(float) : 0;
   if (lds > kMaxLds || (tiered && !fused && flush_chunk(P, K, kind, c) < 4)) return NSSM_E_DIMS;
-  out->hpw = hpw;
-  out->waves = waves;
+  out->uw = uw;
   out->fused = fused;
   out->lds = lds;
   return NSSM_OK;
@@ -1766,18 +1613,16 @@ int launch_pair(const StepArgs& a, const Launch& L, hipStream_t st) {
   ap.prb = prep_requests(a.HG);
   const unsigned pgrid = (unsigned)((a.b + ap.prb - 1) / ap.prb) * a.G;
   hipLaunchKernelGGL((prep_kernel<TIERED>), dim3(pgrid), dim3(kPrepThreads), 0, st, ap);
-  const dim3 sgrid((unsigned)a.b * a.nhb), sblock(L.waves * 64);
-  if (L.fused) {
-    if constexpr (TIERED) {
-      if (a.exact) launch_stream<K, COLD, true, true>(sgrid, sblock, L.lds, st, a);
-      else launch_stream<K, COLD, true, false>(sgrid, sblock, L.lds, st, a);
-    }
-    return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
-  }
-  if constexpr (K == kN) hipLaunchKernelGGL(fresh_stream_kernel, sgrid, sblock, 0, st, a, Ws(a.ws, a.b, a.H, a.G, a.c).hd);
-  else if (TIERED && a.exact) launch_stream<K, COLD, false, TIERED>(sgrid, sblock, 0, st, a);
-  else launch_stream<K, COLD, false, false>(sgrid, sblock, 0, st, a);
+  const dim3 ugrid((unsigned)((size_t)a.b * a.H * (a.P / 8 / L.uw))), ublock(L.uw * 64);
+  const float* hd_ro = Ws(a.ws, a.b, a.H, a.G, a.c).hd;  // the per-head scalars prep wrote
   if constexpr (TIERED) {
+    if (L.fused) {
+      if (a.exact) hipLaunchKernelGGL((unit_kernel<K, COLD, true, true>), ugrid, ublock, L.lds, st, a, hd_ro);
+      else hipLaunchKernelGGL((unit_kernel<K, COLD, true, false>), ugrid, ublock, L.lds, st, a, hd_ro);
+      return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
+    }
+    if (a.exact) hipLaunchKernelGGL((unit_kernel<K, COLD, false, true>), ugrid, ublock, 0, st, a, hd_ro);
+    else hipLaunchKernelGGL((unit_kernel<K, COLD, false, false>), ugrid, ublock, 0, st, a, hd_ro);
     // one resident round of workgroups: an empty launch dispatches no more than that,
     // and a full flush keeps every workgroup busy to the end
     const int items = a.b * a.H, cap = kFlushPerCU * cu_count();
@@ -1785,6 +1630,8 @@ int launch_pair(const StepArgs& a, const Launch& L, hipStream_t st) {
     if (grid < a.HG) grid = a.HG;  // the kernel's listing needs grid >= HG (items >= HG)
     hipLaunchKernelGGL((flush_kernel<K, COLD>), dim3((unsigned)grid), dim3(kFlushWaves * 64),
                        flush_lds_bytes(a.P, K, COLD, a.fch), st, a);
+  } else {
+    hipLaunchKernelGGL((unit_kernel<K, COLD, false, false>), ugrid, ublock, 0, st, a, hd_ro);
   }
   return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
 }
@@ -1816,9 +1663,7 @@ int v4_step(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step
   fill_tier(a, tier);
   a.exact = exact;
   Launch L;
-  if ((rc = pick_launch(prm->H, prm->G, prm->P, tier->k_hot, tier->c, &L, tier->cold_kind))) return rc;
-  a.hpw = L.hpw;
-  a.nhb = prm->H / L.hpw;
+  if ((rc = pick_launch(prm->P, tier->k_hot, tier->c, &L, tier->cold_kind))) return rc;
   a.split = !L.fused && tier->cold_kind != NSSM_COLD_NONE;
   a.fch = a.split ? flush_chunk(prm->P, tier->k_hot, tier->cold_kind, tier->c) : 0;
   hipStream_t st = (hipStream_t)stream;
@@ -1887,10 +1732,9 @@ int nssm_tier_sizes(int32_t slots, int32_t H, int32_t P, int32_t N, int32_t G, i
   return NSSM_OK;
 }
 
-int nssm_set_launch(int32_t heads_per_wg, int32_t waves_per_wg) {
-  if (heads_per_wg < 0 || waves_per_wg < 0 || waves_per_wg > kMaxWaves) return NSSM_E_TUNING;
-  g_hpw_override = heads_per_wg;
-  g_waves_override = waves_per_wg;
+int nssm_set_launch(int32_t units_per_wg) {
+  if (units_per_wg < 0 || units_per_wg > kMaxUnitsPerWg) return NSSM_E_TUNING;
+  g_units_override = units_per_wg;
   return NSSM_OK;
 }
 
@@ -1910,9 +1754,7 @@ int nssm_fresh_step(const nssm_layer_params* prm, float* state, int32_t slots, c
   a.c = 0;
   a.K = kN;
   Launch L;
-  if ((rc = pick_launch(prm->H, prm->G, prm->P, kN, 0, &L))) return rc;
-  a.hpw = L.hpw;
-  a.nhb = prm->H / L.hpw;
+  if ((rc = pick_launch(prm->P, kN, 0, &L))) return rc;
   return launch_pair<kN, NSSM_COLD_FP32>(a, L, (hipStream_t)stream);
 }
 

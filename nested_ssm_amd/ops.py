@@ -298,6 +298,7 @@ def gated_rmsnorm(y: torch.Tensor, gate: torch.Tensor, weight: torch.Tensor, gro
     return out
 
 
-def set_launch(heads_per_wg: int = 0, waves_per_wg: int = 0) -> None:
-    """Override the step kernels' launch shape (0, 0 = automatic)."""
-    check(lib().nssm_set_launch(heads_per_wg, waves_per_wg), "nssm_set_launch")
+def set_launch(units_per_wg: int = 0) -> None:
+    """Override the stream kernel's units (waves of 8 headdim rows) per workgroup
+    (0 = automatic; at most 4, and a step raises when it does not divide P / 8)."""
+    check(lib().nssm_set_launch(units_per_wg), "nssm_set_launch")

@@ -176,8 +176,13 @@ def test_entry_points_validate_before_launching():
     odd = _lib.StepInputs(4, fake + 2, fake, fake, fake, None)
     assert L.nssm_v4_step_exact(ctypes.byref(prm), ctypes.byref(tier), ctypes.byref(odd), fake, fake, 1 << 30,
                                 None) == -3
-    assert L.nssm_set_launch(0, 9) == -6
-    assert L.nssm_set_launch(0, 0) == 0
+    assert L.nssm_set_launch(5) == -6
+    assert L.nssm_set_launch(-1) == -6
+    # 4 units per workgroup do not divide P / 8 = 10 rows blocks: refused before any launch
+    assert L.nssm_set_launch(4) == 0
+    t32 = _lib.Tier(4, 32, 4, _lib.COLD_FP32, *([fake] * 10))
+    assert L.nssm_v4_step(ctypes.byref(prm), ctypes.byref(t32), ctypes.byref(inp), fake, fake, 1 << 30, None) == -6
+    assert L.nssm_set_launch(0) == 0
 
 
 def test_python_layer_rejects_cpu_tensors_and_wrong_dtypes():

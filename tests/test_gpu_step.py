@@ -15,9 +15,9 @@ FP32_TOL = dict(rtol=1e-5, atol=1e-5)
 
 @pytest.fixture(autouse=True)
 def _auto_launch():
-    set_launch(0, 0)
+    set_launch(0)
     yield
-    set_launch(0, 0)
+    set_launch(0)
 
 
 def _setup(b, H, P, G, seed, dt_min=0.0, rotation=True):
@@ -155,10 +155,11 @@ def test_v4_ragged_phases_and_slots():
     assert torch.equal(tier.t[:, 0].cpu().long(), ref.t)
 
 
-@pytest.mark.parametrize("hpw,waves", [(1, 1), (2, 2), (4, 5), (8, 8)])
-def test_launch_shapes_agree(hpw, waves):
-    b, H, G, P, k, c = 2, 16, 2, 80, 32, 4
-    set_launch(hpw, waves)
+@pytest.mark.parametrize("units,P", [(1, 80), (2, 80), (4, 64), (2, 48)])
+def test_launch_shapes_agree(units, P):
+    """1, 2 and 4 units (waves) per stream workgroup, tiered and fresh."""
+    b, H, G, k, c = 2, 16, 2, 32, 4
+    set_launch(units)
     _run_v4(b, H, G, P, k, c, "fp32", steps=9, seed=4, check_state_every=3)
     gen, prm, S0 = _setup(b, H, P, G, seed=8)
     dprm = dev_params(prm)
@@ -168,7 +169,7 @@ def test_launch_shapes_agree(hpw, waves):
         x, B, C, dt = oracle.make_step_inputs(b, H, P, 128, G, gen)
         y_ref = oracle.fresh_step(S_ref, x, B, C, dt, prm)
         y = fresh_step(dprm, S_dev, *to_dev(x, B, C, dt))
-        assert_close32(y, y_ref, f"fresh launch {hpw}x{waves} step {step}", **FP32_TOL)
+        assert_close32(y, y_ref, f"fresh launch {units} units P={P} step {step}", **FP32_TOL)
 
 
 def test_out_of_range_slot_gives_nan_rows():
@@ -237,27 +238,29 @@ def test_rotate_matches_oracle():
 
 
 @pytest.mark.parametrize("c", [16, 33, 64])
-@pytest.mark.parametrize("hpw", [1, 2])
-def test_flush_windows_and_head_blocks(c, hpw):
-    """Long flush windows (16, 33, 64 tokens: one, three and four staged chunks) with
-    one and two heads per stream workgroup match the oracle."""
+@pytest.mark.parametrize("units", [1, 2])
+def test_flush_windows_and_head_blocks(c, units):
+    """Long flush windows (16 tokens replayed in the stream kernel; 33 and 64 on the
+    flush kernel: three and four staged chunks) with one and two units per stream
+    workgroup match the oracle."""
     b, H, G, P, k = 2, 8, 2, 80, 32
-    set_launch(hpw, 4)
-    _run_v4(b, H, G, P, k, c, "fp32", steps=2 * c + 3, seed=40 + c + hpw, check_state_every=c)
+    set_launch(units)
+    _run_v4(b, H, G, P, k, c, "fp32", steps=2 * c + 3, seed=40 + c + units, check_state_every=c)
 
 
-@pytest.mark.parametrize("cold,k,c,P,waves", [
-    ("bf16", 32, 16, 80, 4), ("fp8", 32, 16, 80, 4), ("fp8", 64, 33, 48, 4), ("fp32", 96, 20, 80, 4),
-    ("fp32", 32, 17, 256, 4), ("fp8", 32, 40, 256, 4), ("bf16", 64, 64, 256, 8), ("fp8", 32, 16, 80, 2),
-    ("fp8", 32, 16, 80, 1), ("bf16", 32, 48, 80, 4), ("fp32", 64, 40, 80, 4)])
-def test_flush_contraction_kinds_and_passes(cold, k, c, P, waves):
+@pytest.mark.parametrize("cold,k,c,P,units", [
+    ("bf16", 32, 16, 80, 2), ("fp8", 32, 16, 80, 2), ("fp8", 64, 33, 48, 2), ("fp32", 96, 20, 80, 2),
+    ("fp32", 32, 17, 256, 4), ("fp8", 32, 40, 256, 4), ("bf16", 64, 64, 256, 4), ("fp8", 32, 16, 80, 1),
+    ("fp8", 32, 32, 256, 4), ("bf16", 32, 48, 80, 2), ("fp32", 64, 40, 80, 1)])
+def test_flush_contraction_kinds_and_passes(cold, k, c, P, units):
     """Flushes for every cold storage kind, hot width and headdim. Windows up to 32
-    tokens are replayed in the stream kernel; longer ones go to the matrix-core flush
-    kernel, where P = 256 needs several passes over the accumulator tiles (e4m3: whole
-    rows per pass). The stream kernel runs with 8, 4, 2 and 1 waves."""
+    tokens are replayed in the stream kernel (the window of a workgroup's rows in LDS);
+    longer ones go to the matrix-core flush kernel, where P = 256 needs several passes
+    over the accumulator tiles (e4m3: whole rows per pass). The stream kernel runs with
+    1, 2 and 4 units per workgroup."""
     b, H, G = 2, 4, 1
-    set_launch(1, waves)
-    tier, ref, worst = _run_v4(b, H, G, P, k, c, cold, steps=2 * c + 3, seed=60 + c + k + P + waves,
+    set_launch(units)
+    tier, ref, worst = _run_v4(b, H, G, P, k, c, cold, steps=2 * c + 3, seed=60 + c + k + P + units,
                                check_state_every=c)
     if cold == "fp8":
         assert 0 < worst <= 2e-2
