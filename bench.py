@@ -3,7 +3,7 @@ Nemotron-Nano-9B-v2 mixer shape (27 Mamba2 layers, H=128, P=80, N=128, G=8).
 
 A step is one decode token through the state op of all layers, inputs resident
 in HBM, synthetic seeded data. Per layer-token the tiered path launches prep and
-stream (windows up to 32 tokens are flushed inside the stream kernel) or prep,
+stream (windows up to 16 tokens, 32 for a single bf16 copy, are flushed inside the stream kernel) or prep,
 stream and flush (longer windows); the untiered path prep and stream. Prints one
 JSON line (the driver contract); progress goes to stderr.
 
@@ -326,7 +326,7 @@ def kernel_label(head, args):
     """The launches of one layer-token (the unit the roofline is measured on)."""
     if head == "fresh":
         return "prep_kernel<false> + unit_kernel<128, fp32> (one layer-token, two launches)"
-    if args.c <= 32:
+    if args.c <= (32 if args.cold == "bf16" and args.master == "bf16" else 16):
         return (f"prep_kernel<true> + unit_kernel<{args.k}, {args.cold}, fused flush> "
                 f"(one layer-token, two launches)")
     return (f"prep_kernel<true> + unit_kernel<{args.k}, {args.cold}> + flush_kernel<{args.k}, {args.cold}> "

@@ -146,7 +146,8 @@ int nssm_fresh_step(const nssm_layer_params* prm, float* state, int32_t slots,
                     int64_t workspace_bytes, void* stream);
 
 /* Tiered decode step (hot fresh, cold stale + decay-corrected, ring append,
- * flush for requests whose phase wraps), two kernels on `stream` (three when c > 32):
+ * flush for requests whose phase wraps), two kernels on `stream` (three when c > 16,
+ * or c > 32 for NSSM_COLD_BF16_SINGLE):
  *   hot  <- exp(a) hot + (dt x) (x) B'[:K]
  *   y    =  hot C'[:K] + exp(glog) * (cold_read C'[K:]) + D x
  *   this token (x, dt, B'[K:]) goes to ring position t % c; t += 1;

@@ -2,7 +2,8 @@
 // nested hot/cold tiering, and the C ABI declared in include/nssm.h.
 //
 // A tiered layer-token is two launches on the caller's stream when the flush window
-// is at most 32 tokens (prep, stream), three beyond (prep, stream, flush); the
+// is at most 16 tokens (32 for a single bf16 copy: prep, stream), three beyond (prep,
+// stream, flush); the
 // untiered step is prep and stream:
 //
 //  prep    one workgroup per (group, block of requests). Rotates B and C once
@@ -18,7 +19,7 @@
 //          columns [0, K) are read and written every token; cold columns [K, N)
 //          are only read (the stale readout) except by a head that flushes at
 //          this token, whose short window is replayed here.
-//  flush   (windows over 32 tokens) the cold columns of the heads that flush:
+//  flush   (longer windows) the cold columns of the heads that flush:
 //          decayed snapshot plus the window contraction on the matrix cores,
 //          and their stale readout.
 #include <hip/hip_runtime.h>
@@ -1513,14 +1514,13 @@ int flush_chunk(int P, int K, int kind, int c) {
   return want < fit ? want : fit;
 }
 
-// windows shorter than this are flushed by the stream kernel (VALU replay of the window
-// staged in LDS); longer ones by the flush kernel (matrix cores). Measured on MI355X at
-// the 9B shape, B = 256, 27 layers, fp32 / bf16 / e4m3 cold, ms per step:
-//   c =  4  fused  9.4 / 10.2 / 8.2   split 11.6 / 12.3 / 11.4
-//   c = 16  fused  8.6 /  8.0 / 6.3   split  9.0 /  8.1 /  7.0
-//   c = 32  fused  8.5 /  7.7 / 6.0   split  8.7 /  7.4 /  6.3
-//   c = 64  fused  9.3 /  8.6 / 7.4   split  8.5 /  7.2 /  6.0
-constexpr int kFuseMaxC = 33;
+// Longest window the stream kernel replays itself (VALU, window in LDS); longer ones go to
+// the flush kernel (matrix cores). Measured on MI355X at the 9B shape, B = 256, 27 layers,
+// ms per step, fused / split:
+//   fp32 cold           c = 16  7.82 / 8.28   c = 32  8.58 / 7.94   c = 64 10.46 / 7.88
+//   e4m3, bf16 master   c = 16  5.32 / 6.22   c = 32  5.62 / 5.53   c = 64  8.23 / 5.24
+//   single bf16 copy    c = 16  6.25 / 6.73   c = 32  6.34 / 6.44   c = 64  8.81 / 6.31
+int fuse_max_window(int kind) { return kind == NSSM_COLD_BF16_SINGLE ? 32 : 16; }
 
 // requests per prep workgroup: one head thread per (request, head)
 int prep_requests(int HG) {
@@ -1543,7 +1543,7 @@ int pick_launch(int P, int K, int c, Launch* out, int kind = NSSM_COLD_FP32) {
   int uw = tiered ? 2 : 1;
   if (g_units_override > 0) uw = g_units_override;
   if (uw > kMaxUnitsPerWg || RG % uw) return NSSM_E_TUNING;
-  const bool fused = tiered && c < kFuseMaxC;
+  const bool fused = tiered && c <= fuse_max_window(kind);
   const size_t lds = fused ? ((size_t)c * (kN - K) + (size_t)c * uw * 8) * sizeof(float) : 0;
   if (lds > kMaxLds || (tiered && !fused && flush_chunk(P, K, kind, c) < 4)) return NSSM_E_DIMS;
   out->uw = uw;

@@ -253,7 +253,7 @@ def test_flush_windows_and_head_blocks(c, units):
     ("fp32", 32, 17, 256, 4), ("fp8", 32, 40, 256, 4), ("bf16", 64, 64, 256, 4), ("fp8", 32, 16, 80, 1),
     ("fp8", 32, 32, 256, 4), ("bf16", 32, 48, 80, 2), ("fp32", 64, 40, 80, 1)])
 def test_flush_contraction_kinds_and_passes(cold, k, c, P, units):
-    """Flushes for every cold storage kind, hot width and headdim. Windows up to 32
+    """Flushes for every cold storage kind, hot width and headdim. Windows up to 16
     tokens are replayed in the stream kernel (the window of a workgroup's rows in LDS);
     longer ones go to the matrix-core flush kernel, where P = 256 needs several passes
     over the accumulator tiles (e4m3: whole rows per pass). The stream kernel runs with
@@ -276,7 +276,7 @@ def test_flush_contraction_kinds_and_passes(cold, k, c, P, units):
     ("bf16", 32, 4, [1, 2, 3, 0]), ("fp8", 32, 4, None), ("fp8", 96, 33, [5, 0, 32, 17])])
 def test_v4_exact_readout_matches_oracle(cold, k, c, phase):
     """The rank-c exact correction readout (corr=1) through nssm_v4_step_exact against
-    the oracle's exact mode, on the fused (c <= 32) and flush-kernel (c > 32) paths,
+    the oracle's exact mode, on the fused (c <= 16) and flush-kernel (c > 16) paths,
     with per-request phases."""
     steps = 2 * c + 5
     _run_v4(4, 8, 2, 80, k, c, cold, steps=steps, seed=80 + k + c, phase=phase, check_state_every=max(1, c // 2),
@@ -314,12 +314,12 @@ def test_v4_exact_readout_equals_fresh_at_9b_shape_alternating_modes():
 # --------------------------------------------------------------------------- bf16 masters
 @pytest.mark.parametrize("cold,k,c,P", [
     ("bf16", 32, 4, 80), ("fp8", 32, 4, 80), ("bf16", 32, 16, 80), ("fp8", 64, 33, 48), ("bf16", 96, 40, 80),
-    ("fp8", 32, 64, 256), ("bf16", 64, 1, 80), ("fp8", 32, 17, 80)])
+    ("fp8", 32, 64, 256), ("bf16", 64, 1, 80), ("fp8", 32, 17, 80), ("bf16", 32, 32, 80)])
 def test_v4_bf16_master_matches_oracle(cold, k, c, P):
     """The fused path's bf16 masters (scale/v4_fused_decode.py:149,156-158): one bf16
     copy (bf16 cold) or a bf16 master beside the e4m3 copy (fp8 cold), rounded at the
     join and every flush, against the oracle's master="bf16" step; windows replayed in
-    the stream kernel (c <= 32) and on the matrix cores (c > 32)."""
+    the stream kernel (c <= 16; single bf16 copy c <= 32) and on the matrix cores."""
     b, H, G = 3, 8, 2
     tier, ref, worst = _run_v4(b, H, G, P, k, c, cold, steps=2 * c + 5, seed=120 + k + c + P,
                                check_state_every=max(1, c // 2), master="bf16")
