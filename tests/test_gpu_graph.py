@@ -31,16 +31,17 @@ def _inputs(b, n, g):
              torch.randn(b, H, device="cuda", generator=g).to(torch.bfloat16)) for _ in range(n)]
 
 
-@pytest.mark.parametrize("c,cold,exact", [(4, "fp32", False), (4, "fp8", True), (40, "fp32", False),
-                                          (40, "bf16", True)])
-def test_v4_step_graph_replays_match_eager(c, cold, exact):
+@pytest.mark.parametrize("c,cold,exact,master", [(4, "fp32", False, "fp32"), (4, "fp8", True, "fp32"),
+                                                 (40, "fp32", False, "fp32"), (40, "bf16", True, "fp32"),
+                                                 (4, "fp8", False, "bf16"), (40, "bf16", False, "bf16")])
+def test_v4_step_graph_replays_match_eager(c, cold, exact, master):
     b, nl, k = 6, 3, 32
     layers = _layers(nl, seed=c)
     g = torch.Generator(device="cuda").manual_seed(1)
     S0 = [torch.randn(b, H, P, N, device="cuda", generator=g).mul_(0.1) for _ in range(nl)]
     phase = torch.randint(0, c, (b,), device="cuda", generator=g, dtype=torch.int32)
-    tg = [V4Tier(b, H, P, G, k_hot=k, c=c, cold=cold) for _ in range(nl)]
-    te = [V4Tier(b, H, P, G, k_hot=k, c=c, cold=cold) for _ in range(nl)]
+    tg = [V4Tier(b, H, P, G, k_hot=k, c=c, cold=cold, master=master) for _ in range(nl)]
+    te = [V4Tier(b, H, P, G, k_hot=k, c=c, cold=cold, master=master) for _ in range(nl)]
     for l in range(nl):
         tg[l].join(layers[l], S0[l], phase=phase)
         te[l].join(layers[l], S0[l], phase=phase)
@@ -54,7 +55,7 @@ def test_v4_step_graph_replays_match_eager(c, cold, exact):
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):  # first call on the capture stream sizes its workspace
-        token([V4Tier(b, H, P, G, k_hot=k, c=c, cold=cold) for _ in range(nl)], static,
+        token([V4Tier(b, H, P, G, k_hot=k, c=c, cold=cold, master=master) for _ in range(nl)], static,
               [torch.empty_like(y) for y in ys])
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
