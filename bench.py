@@ -39,11 +39,13 @@ def bytes_fresh_token():
     return 2 * H * P * N * 4 + bytes_io()
 
 
-def bytes_v4_token(k, c, cold, master="fp32"):
+def bytes_v4_token(k, c, cold, master="fp32", skip=0.0):
+    """skip: fraction of heads whose cold term a gated readout drops; such a head reads
+    no cold column on the c - 1 tokens of a window that do not flush."""
     nc = N - k
     esz = {"fp32": 4, "bf16": 2, "fp8": 1}[cold]
     hot = 2 * H * P * k * 4
-    read = H * P * nc * esz + (H * P * 4 if cold == "fp8" else 0)
+    read = (H * P * nc * esz + (H * P * 4 if cold == "fp8" else 0)) * (1.0 - skip * (c - 1) / c)
     if cold == "fp32" or (cold == "bf16" and master == "bf16"):
         flush = H * P * nc * esz  # rewrite of the single copy (its read is the stale read)
     else:  # master read + master write + read-copy write (+ scale)
@@ -187,10 +189,13 @@ def bench_v4(args, layers, inputs, dev):
         ys.append(torch.empty(args.B, H, P, device=dev))
     torch.cuda.synchronize()
 
+    counts = torch.zeros(args.layers, 2, dtype=torch.int64, device=dev) if args.qgate > 0 else None
+    rd = dict(exact=args.exact, hot_only=args.coldoff, qgate=args.qgate)
+
     def step(i):
         inp = inputs[i % len(inputs)]
         for l in range(args.layers):
-            tiers[l].step(layers[l], *inp[l], y=ys[l], exact=args.exact)
+            tiers[l].step(layers[l], *inp[l], y=ys[l], counts=None if counts is None else counts[l], **rd)
 
     # warmup is rounded to whole flush windows so the timed steps start phase-aligned
     # (with --graph the capture's sizing call advances the phase by one token)
@@ -209,10 +214,17 @@ def bench_v4(args, layers, inputs, dev):
 
     def one(i):
         tok, l = seq[i % len(seq)]
-        tiers[l].step(layers[l], *inputs[tok % len(inputs)][l], y=ys[l], exact=args.exact)
+        tiers[l].step(layers[l], *inputs[tok % len(inputs)][l], y=ys[l],
+                      counts=None if counts is None else counts[l], **rd)
 
     ms_ev = per_launch_ms(one, len(seq) * max(1, 108 // len(seq)))
     tier_gb = sum(t.nbytes() for t in tiers) / 1e9
+    # fraction of heads whose cold term the readout dropped
+    if args.coldoff:
+        args.skip = 1.0
+    elif counts is not None:
+        n, kept = counts.sum(0).tolist()
+        args.skip = 1.0 - kept / n if n else 0.0
     del tiers
     torch.cuda.empty_cache()
     return ms_step, ms_launch, ms_ev, tier_gb
@@ -288,11 +300,12 @@ def cpu_baseline(args, budget_s):
     ref = oracle.NativeV4(B, H, P, N, args.k, args.c, cold=args.cold, exact=args.exact, master=args.master)
     ref.join(torch.arange(B), oracle.make_state(B, H, P, N, gen))
     x, Bm, Cm, dt = oracle.make_step_inputs(B, H, P, N, G, gen)
-    ref.step(x, Bm, Cm, dt, prm)  # warm
+    rd = dict(hot_only=args.coldoff, qgate=args.qgate)
+    ref.step(x, Bm, Cm, dt, prm, **rd)  # warm
     t0 = time.perf_counter()
     n = 0
     while True:
-        ref.step(x, Bm, Cm, dt, prm)
+        ref.step(x, Bm, Cm, dt, prm, **rd)
         n += 1
         if time.perf_counter() - t0 > budget_s or n >= 16:
             break
@@ -303,7 +316,8 @@ def cpu_baseline(args, budget_s):
         "cores": threads,
         "kind": "port",
         "sample": f"oracle NativeV4 step ({args.cold} cold, k={args.k}, c={args.c}"
-                  f"{', exact readout' if args.exact else ''}), 1 layer x B={B} x {n} tokens "
+                  f"{', exact readout' if args.exact else ''}{', hot-only readout' if args.coldoff else ''}"
+                  f"{f', query gate {args.qgate:g}' if args.qgate > 0 else ''}), 1 layer x B={B} x {n} tokens "
                   f"on the host, {t_layer * 1e3:.0f} ms/layer-token, scaled to {args.layers} layers",
     }
 
@@ -347,6 +361,9 @@ def main():
                     help="precision of the cold master for bf16 / fp8 cold (bf16: the reference fused "
                          "path's bf16 master; bf16 cold is then a single copy)")
     ap.add_argument("--exact", action="store_true", help="v4 with the rank-c exact correction readout (corr=1)")
+    ap.add_argument("--coldoff", action="store_true", help="v4 with the hot-only readout (coldoff=1)")
+    ap.add_argument("--qgate", type=float, default=0.0,
+                    help="v4 with the query-gated stale readout at this threshold (qgate=tau)")
     ap.add_argument("--graph", action="store_true", help="time HIP graph replays of whole steps (all layers)")
     ap.add_argument("--ragged", action="store_true",
                     help="v4 requests join with random phases (each token flushes about B/c of them)")
@@ -359,6 +376,9 @@ def main():
     args = ap.parse_args()
     if args.cold == "fp32":
         args.master = "fp32"  # fp32 cold is its own master
+    if args.exact and (args.coldoff or args.qgate > 0):
+        ap.error("--exact cannot be combined with --coldoff or --qgate")
+    args.skip = 0.0
 
     if args.copy_calibration_mib:
         n = args.copy_calibration_mib * (1 << 20) // 4
@@ -399,7 +419,7 @@ def main():
         log("v4 ...")
         v_step, v_launch, v_ev, tier_gb = bench_v4(args, layers, inputs, dev)
         res["v4"] = (v_step, v_launch, v_ev)
-        vb = args.B * bytes_v4_token(args.k, args.c, args.cold, args.master) + bytes_rotation()
+        vb = args.B * bytes_v4_token(args.k, args.c, args.cold, args.master, args.skip) + bytes_rotation()
         log(f"v4: {v_step:.3f} ms/step, {args.B / v_step * 1e3:,.0f} tok/s, launch {v_ev * 1e3:.1f} us "
             f"-> {vb / (v_ev * 1e-3) / 1e9:,.0f} GB/s (tiers {tier_gb:.1f} GB)")
 
@@ -414,11 +434,13 @@ def main():
 
     head = "v4" if "v4" in res else "fresh"
     ms_step, ms_launch, ms_ev = res[head]
-    per_launch_bytes = args.B * (bytes_v4_token(args.k, args.c, args.cold, args.master) if head == "v4"
+    per_launch_bytes = args.B * (bytes_v4_token(args.k, args.c, args.cold, args.master, args.skip) if head == "v4"
                                  else bytes_fresh_token()) + bytes_rotation()
     achieved = per_launch_bytes / (ms_ev * 1e-3) / 1e9
+    readout = ("exact" if args.exact else "hot-only" if args.coldoff
+               else f"query-gated tau={args.qgate:g}" if args.qgate > 0 else "stale")
     tkey = (f"v4 B={args.B} k={args.k} c={args.c} {args.cold}" + (" bf16-master" if args.master == "bf16" else "")
-            if head == "v4" else f"fresh B={args.B}")
+            + ("" if readout == "stale" else f" {readout}") if head == "v4" else f"fresh B={args.B}")
     traffic = measured_traffic(tkey)
     out = {
         "metric": "state-op tokens/s at 9B shape B=256 (v4-c4 vs fresh); achieved HBM GB/s vs peak",
@@ -438,12 +460,13 @@ def main():
                          + (f", k_hot={args.k}, c={args.c}, {args.cold} cold"
                             + (", bf16 master" if args.master == "bf16" and args.cold != "fp32" else "") + ", "
                             f"{'random phases' if args.ragged else 'phase-aligned'}" if head == "v4" else "")
-                         + (", exact (corr=1) readout" if head == "v4" and args.exact else "")
+                         + (f", {readout} readout" if head == "v4" and readout != "stale" else "")
                          + (", HIP graph replay" if args.graph else "")),
             "layers": args.layers, "B": args.B, "H": H, "P": P, "N": N, "G": G,
-            "k_hot": args.k, "c": args.c, "cold": args.cold, "readout": "exact" if args.exact else "stale",
+            "k_hot": args.k, "c": args.c, "cold": args.cold, "readout": readout,
             "master": args.master if args.cold != "fp32" else "fp32",
         },
+        **({"cold_skip_frac": round(args.skip, 4)} if head == "v4" and readout not in ("stale", "exact") else {}),
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),

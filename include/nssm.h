@@ -18,6 +18,8 @@
  *   nssm_v4_step         scale/v4_fused_decode.py:28-95 (_v4_fused_decode),
  *                        scale/v4_native_decode.py:58-167 (_v4_decode state
  *                        part), scale/vllm_v4_patch.py:140-179 (decode_readout)
+ *   nssm_v4_step_gated   scale/v4_native_decode.py:118-127 (coldoff) and
+ *                        :147-156 (qgate) of _v4_decode
  *   nssm_v4_join         scale/vllm_v4_patch.py:123-137 (prefill_snapshot),
  *                        scale/v4_native_decode.py:234-243,
  *                        scale/v4_fused_decode.py:121-159 (prefill capture)
@@ -45,7 +47,7 @@
 extern "C" {
 #endif
 
-#define NSSM_ABI_VERSION 6
+#define NSSM_ABI_VERSION 7
 
 /* error codes */
 #define NSSM_OK 0
@@ -170,6 +172,22 @@ int nssm_v4_step(const nssm_layer_params* prm, const nssm_tier* tier,
 int nssm_v4_step_exact(const nssm_layer_params* prm, const nssm_tier* tier,
                        const nssm_step_inputs* in, float* y, void* workspace,
                        int64_t workspace_bytes, void* stream);
+
+/* nssm_v4_step with a gated stale readout: a skipped head's y is hot C'[:K] + D x
+ * (no cold term) and, when it does not flush at this token, its cold columns are not
+ * read. hot_only != 0 skips every head: the draft readout of v4cfg["coldoff"] = 1
+ * (scale/v4_native_decode.py:118-127). Otherwise qgate_tau > 0 skips the heads with
+ *   rho = sum_{n>=K} C'_n^2 / max(sum_n C'_n^2, 1e-9) < qgate_tau
+ * (v4cfg["qgate"], scale/v4_native_decode.py:147-156), and when counts (device, two
+ * int64, 8-byte aligned) is not NULL, counts[0] += the gated heads (b H) and counts[1]
+ * += the heads that kept the cold term, by device atomics in stream order. hot_only = 0
+ * and qgate_tau = 0 is nssm_v4_step. The tier's bookkeeping is nssm_v4_step's in every
+ * case (the reference's coldoff branch advances only t). NSSM_E_DIMS for a NaN or
+ * infinite qgate_tau (a negative one gates nothing). */
+int nssm_v4_step_gated(const nssm_layer_params* prm, const nssm_tier* tier,
+                       const nssm_step_inputs* in, float* y, void* workspace,
+                       int64_t workspace_bytes, int32_t hot_only, float qgate_tau,
+                       int64_t* counts, void* stream);
 
 /* Capture a tier from full fp32 states [b][H][P][N] into slot_ids[b] (NULL =
  * 0..b-1): hot = S[..,:K], cold = S[..,K:] (rounded to the master's precision,

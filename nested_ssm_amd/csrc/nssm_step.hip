@@ -70,6 +70,12 @@ struct StepArgs {
   int32_t split;  // the flush kernel runs after the stream kernel (prep writes the pair flags)
   int32_t fch;    // window tokens the flush kernel stages in LDS at a time (multiple of 4)
   float dt_min;
+  // gated stale readout (no cold term for a skipped head): every head (hot_only), or the
+  // heads whose query puts less than qgate_tau of its energy on the cold columns;
+  // qcounts[0] / [1] (NULL: not counted) accumulate gated heads / heads that kept the term
+  int32_t hot_only;
+  float qgate_tau;
+  unsigned long long* qcounts;
 };
 
 // Workspace carve-up for b requests (floats): rotated B and C [b][G][N] each,
@@ -77,8 +83,9 @@ struct StepArgs {
 // group) flush flags [b][G] (int32, padded to a multiple of 4), window weights
 // [b][H][c] (flush) and correction coefficients [b][H][c] (exact readout).
 // HD_SNAPF is the factor of the snapshot readout: exp(glog) (stale, the decay up
-// to the previous token) or exp(glog + a) (exact, inclusive of this token).
-enum { HD_DT = 0, HD_A, HD_DECAY, HD_SNAPF, HD_D, HD_FLUSH, HD_DTOT, HD_M, HD_POS, HD_STRIDE = 12 };
+// to the previous token), exp(glog + a) (exact, inclusive of this token) or 0 (a head
+// whose cold term the gated readout drops; HD_SKIP = 1 then).
+enum { HD_DT = 0, HD_A, HD_DECAY, HD_SNAPF, HD_D, HD_FLUSH, HD_DTOT, HD_M, HD_POS, HD_SKIP, HD_STRIDE = 12 };
 __host__ __device__ constexpr size_t flag_words(int b, int G, int c) {
   return c > 0 ? (((size_t)b * G + 3) & ~(size_t)3) : 0;
 }
@@ -162,15 +169,20 @@ template <bool TIERED>
 __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
   __shared__ float sX[2 * kPrepReq][kN];  // B (j < 8) and C (j >= 8) of the block's requests
   __shared__ int sSlot[kPrepReq], sTr[kPrepReq], sNvr[kPrepReq], sFl[kPrepReq];
-  // exact readout: B', C' of the block and s_j = C'_cold . B'_j over each window
+  // exact readout and query gate: B', C' of the block; s_j = C'_cold . B'_j over each
+  // window; each request's cold energy fraction; gated / kept head counts
   __shared__ float sRot[TIERED ? 2 * kPrepReq : 1][TIERED ? kN : 1];
   __shared__ float sS[TIERED ? kPrepReq : 1][TIERED ? kMaxC : 1];
+  __shared__ float sRho[kPrepReq];
+  __shared__ int sQc[2];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, lk = lane >> 4;
   const int G = a.G, H = a.H, HG = a.HG, c = a.c;
   const int g = blockIdx.x % G, r0 = (blockIdx.x / G) * a.prb;
   const int nreq = min(a.prb, a.b - r0);
   const Ws ws(a.ws, a.b, H, G, c);
+  const bool gate = TIERED && a.qgate_tau > 0.f && !a.hot_only;  // query gate (uniform)
+  const bool rot_lds = TIERED && (a.exact || gate);              // B', C' kept in LDS
 
   // 1. independent loads: B and C of the block (zero past the last request), R, the
   // head inputs
@@ -195,6 +207,7 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
         ra[t2][kb] = *reinterpret_cast<const f4*>(Rg + (size_t)((wave + 4 * t2) * 16 + li) * kN + kb * 16 + 4 * lk);
   }
   if (tid < kPrepReq) sFl[tid] = 0;
+  if (tid < 2) sQc[tid] = 0;
   const int hr = tid / HG, hh = tid - hr * HG;  // the head thread's request and head
   const bool head_thread = tid < nreq * HG;
   const int h = g * HG + hh, bi = r0 + hr;
@@ -241,7 +254,7 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
       const int m0 = (wave + 4 * t2) * 16 + 4 * lk;
       const int r = li & (kPrepReq - 1), which = li >> 3;
       if constexpr (TIERED) {
-        if (a.exact) *reinterpret_cast<f4*>(&sRot[li][m0]) = acc;
+        if (rot_lds) *reinterpret_cast<f4*>(&sRot[li][m0]) = acc;
       }
       const int sl = r < nreq ? sSlot[r] : -1;
       if (sl >= 0 && sl < a.slots) {
@@ -265,7 +278,7 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
       ws.B[o] = sX[r][n];
       ws.C[o] = sX[kPrepReq + r][n];
       if constexpr (TIERED) {
-        if (a.exact) {
+        if (rot_lds) {
           sRot[r][n] = sX[r][n];
           sRot[kPrepReq + r][n] = sX[kPrepReq + r][n];
         }
@@ -304,6 +317,29 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
     }
   }
 
+  // 2c. query gate: rho_r = sum_{n>=K} C'_n^2 / max(sum_n C'_n^2, 1e-9) of each request
+  // (scale/v4_native_decode.py:147-156); wave 0, 8 lanes per request
+  if constexpr (TIERED) {
+    if (gate) {
+      __syncthreads();  // sRot
+      if (wave == 0) {
+        const int r = lane >> 3, j = lane & 7;
+        float ea = 0.f, ec = 0.f;
+        for (int n = 4 * j; n < kN; n += 32) {  // K is a multiple of 32: a float4 is hot or cold
+          const f4 v = *reinterpret_cast<const f4*>(&sRot[kPrepReq + r][n]);
+          const float e = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+          ea += e;
+          if (n >= a.K) ec += e;
+        }
+        ea = sum8(ea);
+        ec = sum8(ec);
+        // clamp(min=1e-9) keeps a NaN energy NaN, so its head is dropped
+        if (j == 0) sRho[r] = ec / (ea < 1e-9f ? 1e-9f : ea);
+      }
+      __syncthreads();  // sRho
+    }
+  }
+
   // 3. per-head scalars and bookkeeping
   if (head_thread && slot >= 0 && slot < a.slots) {
     float dt = softplus_f(draw + dtb);
@@ -319,9 +355,21 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
       const int pos = tt % c;
       const bool flush = (tt + 1) % c == 0;  // then pos == c - 1
       const bool exact = a.exact != 0;
+      // gated readout: coldoff drops every head's cold term (scale/v4_native_decode.py:118-127),
+      // the query gate a head whose rho < tau (:147-156); the tier evolves as without it
+      bool skip = !exact && a.hot_only;
+      if (gate) {
+        const bool keep = sRho[hr] >= a.qgate_tau;
+        skip = !keep;
+        if (a.qcounts) {
+          atomicAdd(&sQc[0], 1);
+          if (keep) atomicAdd(&sQc[1], 1);
+        }
+      }
       // stale: exp(glog), the decay up to the previous token (one-token lag);
       // exact: exp(glog + a), inclusive of this token (scale/v4_native_decode.py:89)
-      hd[HD_SNAPF] = expf(exact ? gl + av : gl);
+      hd[HD_SNAPF] = skip ? 0.f : expf(exact ? gl + av : gl);
+      hd[HD_SKIP] = skip ? 1.f : 0.f;
       hd[HD_FLUSH] = flush ? 1.f : 0.f;
       hd[HD_POS] = (float)pos;
       if (flush) sFl[hr] = 1;
@@ -377,9 +425,13 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
   // 4. the flush kernel's per-(request, group) flags: some head of the pair flushes
   // (every pair of the block is written, so no flag survives from an earlier token)
   if constexpr (TIERED) {
-    if (a.split) {
+    if (a.split || (gate && a.qcounts)) {
       __syncthreads();
-      if (tid < nreq) ws.fg[(size_t)(r0 + tid) * G + g] = sFl[tid];
+      if (a.split && tid < nreq) ws.fg[(size_t)(r0 + tid) * G + g] = sFl[tid];
+      if (gate && a.qcounts && tid == 0) {
+        atomicAdd(a.qcounts, (unsigned long long)sQc[0]);
+        atomicAdd(a.qcounts + 1, (unsigned long long)sQc[1]);
+      }
     }
   }
 }
@@ -751,6 +803,28 @@ __device__ __forceinline__ void stage_unit_window(float* sB, float* sU, int m, i
   }
 }
 
+// One unit of a head that does not flush and whose cold term the gated readout drops:
+// hot columns, y = hot C'[:K] + D x, and the ring append of x; no cold column is read.
+template <int K, int COLD>
+__device__ __forceinline__ void unit_hot_only(const StepArgs& a, const float* __restrict__ hd, const Ws& ws, size_t sh,
+                                           size_t rh, size_t pair, int p, int q) {
+  using C = Cfg<K, COLD>;
+  UnitRaw<K, COLD> d;
+  unit_load<K, COLD>(a, sh * a.P + p, rh * a.P + p, q, d, true);
+  const float* wB = ws.B + pair * kN;
+  const float* wC = ws.C + pair * kN;
+  float Bh[K / 32][4], Ch[K / 32][4], Cc[C::CSR][4] = {}, Cq[C::CWR] = {};
+#pragma unroll
+  for (int s = 0; s < K / 32; ++s) {
+    const f4 tb = *reinterpret_cast<const f4*>(wB + 32 * s + 4 * q);
+    const f4 tc = *reinterpret_cast<const f4*>(wC + 32 * s + 4 * q);
+    Bh[s][0] = tb.x; Bh[s][1] = tb.y; Bh[s][2] = tb.z; Bh[s][3] = tb.w;
+    Ch[s][0] = tc.x; Ch[s][1] = tc.y; Ch[s][2] = tc.z; Ch[s][3] = tc.w;
+  }
+  uint16_t* rx = a.ring_x + (sh * a.c + (int)hd[HD_POS]) * a.P;
+  unit_compute<K, COLD, false>(a, sh, rh, p, q, d, rx, false, hd, Bh, Ch, Cc, Cq);
+}
+
 // Stream kernel: one unit (8 headdim rows of one head) per wave; a workgroup is UW waves
 // on consecutive units of one head (UW divides P / 8), workgroups in request-major, head,
 // row order, so the resident waves stream a compact window of the state. FUSED (short
@@ -767,8 +841,11 @@ constexpr int unit_waves_per_eu() {
   return K == 32 ? (Cfg<K, COLD>::E4M3 ? 6 : 8) : K == kN ? 8 : K == 64 ? 6 : 5;
 }
 
-template <int K, int COLD, bool FUSED, bool EXACT>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(unit_waves_per_eu<K, COLD>()))) unit_kernel(StepArgs a, const float* __restrict__ hd_ro) {
+// GATED: the gated readout's variant, in which a head that prep marked HD_SKIP and that
+// does not flush takes the hot-only path (the other variants never wait for that flag
+// before their state loads).
+template <int K, int COLD, bool FUSED, bool EXACT, bool GATED>
+__device__ __forceinline__ void unit_body(const StepArgs& a, const float* __restrict__ hd_ro) {
   using C = Cfg<K, COLD>;
   constexpr int HS = C::HS, CS = C::CS, CSR = C::CSR, CWR = C::CWR, NC = C::NC;
   constexpr bool TIERED = C::TIERED;
@@ -789,6 +866,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(unit_w
   const float* __restrict__ hd = (COLD == NSSM_COLD_FP32 && TIERED ? static_cast<const float*>(ws.hd) : hd_ro) +
                                  rh * HD_STRIDE;
   const bool flushing = TIERED && hd[HD_FLUSH] != 0.f;  // uniform over the workgroup
+  if constexpr (TIERED && GATED) {
+    // a head whose cold term the gated readout drops reads no cold columns unless it
+    // flushes (its own path, so the common one keeps its unconditional loads)
+    if (!flushing && hd[HD_SKIP] != 0.f) {
+      unit_hot_only<K, COLD>(a, hd, ws, sh, rh, (size_t)bi * a.G + g, p, q);
+      return;
+    }
+  }
   UnitRaw<K, COLD> d;
   // a flushing head's cold columns are needed here only when the replay is fused
   unit_load<K, COLD>(a, row, rh * P + p, q, d, !FUSED && flushing);
@@ -837,6 +922,15 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(unit_w
     if (!flushing) rx = a.ring_x + (sh * c + (int)hd[HD_POS]) * P;
   }
   unit_compute<K, COLD, EXACT>(a, sh, rh, p, q, d, rx, !flushing, hd, Bh, Ch, Cc, Cq);
+}
+
+template <int K, int COLD, bool FUSED, bool EXACT>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(unit_waves_per_eu<K, COLD>()))) unit_kernel(StepArgs a, const float* __restrict__ hd_ro) {
+  unit_body<K, COLD, FUSED, EXACT, false>(a, hd_ro);
+}
+template <int K, int COLD, bool FUSED>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(unit_waves_per_eu<K, COLD>()))) unit_kernel_gated(StepArgs a, const float* __restrict__ hd_ro) {
+  unit_body<K, COLD, FUSED, false, true>(a, hd_ro);
 }
 
 // ---------------------------------------------------------------------------
@@ -1616,12 +1710,15 @@ int launch_pair(const StepArgs& a, const Launch& L, hipStream_t st) {
   const dim3 ugrid((unsigned)((size_t)a.b * a.H * (a.P / 8 / L.uw))), ublock(L.uw * 64);
   const float* hd_ro = Ws(a.ws, a.b, a.H, a.G, a.c).hd;  // the per-head scalars prep wrote
   if constexpr (TIERED) {
+    const bool gated = a.hot_only || a.qgate_tau > 0.f;
     if (L.fused) {
       if (a.exact) hipLaunchKernelGGL((unit_kernel<K, COLD, true, true>), ugrid, ublock, L.lds, st, a, hd_ro);
+      else if (gated) hipLaunchKernelGGL((unit_kernel_gated<K, COLD, true>), ugrid, ublock, L.lds, st, a, hd_ro);
       else hipLaunchKernelGGL((unit_kernel<K, COLD, true, false>), ugrid, ublock, L.lds, st, a, hd_ro);
       return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
     }
     if (a.exact) hipLaunchKernelGGL((unit_kernel<K, COLD, false, true>), ugrid, ublock, 0, st, a, hd_ro);
+    else if (gated) hipLaunchKernelGGL((unit_kernel_gated<K, COLD, false>), ugrid, ublock, 0, st, a, hd_ro);
     else hipLaunchKernelGGL((unit_kernel<K, COLD, false, false>), ugrid, ublock, 0, st, a, hd_ro);
     // one resident round of workgroups: an empty launch dispatches no more than that,
     // and a full flush keeps every workgroup busy to the end
@@ -1650,18 +1747,24 @@ int dispatch_kind(const StepArgs& a, int kind, const Launch& L, hipStream_t st) 
 }
 
 int v4_step(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step_inputs* in, float* y,
-            void* workspace, int64_t workspace_bytes, void* stream, int exact) {
+            void* workspace, int64_t workspace_bytes, void* stream, int exact, int hot_only = 0,
+            float qgate_tau = 0.f, int64_t* qcounts = nullptr) {
   int rc = check_params(prm);
   if (rc) return rc;
   if ((rc = check_inputs(in, y))) return rc;
   if ((rc = check_tier(tier, true))) return rc;
   if (exact && tier->cold_kind == NSSM_COLD_NONE) return NSSM_E_KIND;  // the correction needs the cold tier
+  if (!(fabsf(qgate_tau) <= 3.0e38f)) return NSSM_E_DIMS;  // NaN or infinite threshold
+  if (qcounts && (reinterpret_cast<uintptr_t>(qcounts) & 7)) return NSSM_E_ALIGN;
   if (!in->slot_ids && in->b > tier->slots) return NSSM_E_DIMS;
   if ((rc = check_ws(prm, in->b, tier->c, workspace, workspace_bytes))) return rc;
   StepArgs a = {};
   fill_common(a, prm, in, y, workspace);
   fill_tier(a, tier);
   a.exact = exact;
+  a.hot_only = hot_only != 0;
+  a.qgate_tau = qgate_tau;
+  a.qcounts = reinterpret_cast<unsigned long long*>(qcounts);
   Launch L;
   if ((rc = pick_launch(prm->P, tier->k_hot, tier->c, &L, tier->cold_kind))) return rc;
   a.split = !L.fused && tier->cold_kind != NSSM_COLD_NONE;
@@ -1766,6 +1869,12 @@ int nssm_v4_step(const nssm_layer_params* prm, const nssm_tier* tier, const nssm
 int nssm_v4_step_exact(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step_inputs* in, float* y,
                        void* workspace, int64_t workspace_bytes, void* stream) {
   return v4_step(prm, tier, in, y, workspace, workspace_bytes, stream, 1);
+}
+
+int nssm_v4_step_gated(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step_inputs* in, float* y,
+                       void* workspace, int64_t workspace_bytes, int32_t hot_only, float qgate_tau,
+                       int64_t* counts, void* stream) {
+  return v4_step(prm, tier, in, y, workspace, workspace_bytes, stream, 0, hot_only, qgate_tau, counts);
 }
 
 int nssm_v4_join(const nssm_layer_params* prm, const nssm_tier* tier, const float* state, int32_t b,

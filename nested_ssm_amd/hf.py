@@ -95,17 +95,39 @@ def rotate_state(S: torch.Tensor, R: torch.Tensor, inverse: bool = False) -> tor
     return torch.einsum("bhpn,hmn->bhpm", S.float(), Rh.contiguous())
 
 
+_QGATE_KEYS = ("qgate_n", "qgate_kept")
+
+
 class V4State(dict):
     """Per-mixer decode state (`m._v4state`). Keys: "tier" (V4Tier or None for
     the untiered path), "params" (LayerParams), "pb", "c". Item "t" reads and
     writes the decode phase kept on the device (callers reset it between
-    prompts, scale/probe_selfspec_policy.py:127-128)."""
+    prompts, scale/probe_selfspec_policy.py:127-128). Items "qgate_n" and
+    "qgate_kept" (present once a query-gated token has run, as in
+    scale/v4_native_decode.py:153-154) read the gated and kept head counts kept
+    on the device (scale/run_recall_native.py:116-118 reads them with .get)."""
 
     def __getitem__(self, key):
         if key == "t":
             tier = dict.get(self, "tier")
             return int(tier.t[0, 0].item()) if tier is not None else dict.get(self, "t_fresh", 0)
+        if key in _QGATE_KEYS:
+            qc = dict.get(self, "qcounts")
+            if qc is None:
+                raise KeyError(key)
+            return int(qc[_QGATE_KEYS.index(key)].item())
         return dict.__getitem__(self, key)
+
+    def get(self, key, default=None):
+        try:
+            return self[key]
+        except KeyError:
+            return default
+
+    def __contains__(self, key):
+        if key in _QGATE_KEYS:
+            return dict.get(self, "qcounts") is not None
+        return key == "t" or dict.__contains__(self, key)
 
     def __setitem__(self, key, value):
         if key == "t":
@@ -167,14 +189,44 @@ def decode_step(m, hidden_states, cache_params, attention_mask):
     gate, x, B, C, dt = decode_inputs(m, hidden_states, cache_params, attention_mask)
     prm = st["params"]
     tier = dict.get(st, "tier")
+    check_readout_cfg(m.v4cfg, st["pb"], m.ssm_state_size)
     if tier is None:
         S = cache_params.layers[m.layer_idx].recurrent_states[0]
         y = ops.fresh_step(prm, S, x, B, C, dt)
     else:
-        # v4cfg["corr"] is read per token (callers may switch it at run time): the
-        # rank-c exact correction readout, scale/v4_native_decode.py:81-117
-        y = tier.step(prm, x, B, C, dt, exact=bool(m.v4cfg.get("corr")))
+        # the readout keys are read per token (callers switch them at run time), in the
+        # reference's order: corr (rank-c exact correction, scale/v4_native_decode.py:81-117),
+        # else coldoff (hot-only draft readout, :118-127), else the stale readout,
+        # query-gated when qgate > 0 (:147-156)
+        cfg = m.v4cfg
+        exact = bool(cfg.get("corr"))
+        hot_only = not exact and bool(cfg.get("coldoff"))
+        tau = 0.0 if exact or hot_only else float(cfg.get("qgate") or 0.0)
+        if not hot_only and int(cfg["c"]) != tier.c:
+            raise NotImplementedError(f"window c={cfg['c']} exceeds the kernels' {ops.MAX_WINDOW}: it is "
+                                      "supported with the hot-only readout (coldoff=1) only")
+        counts = None
+        if tau > 0:
+            counts = dict.get(st, "qcounts")
+            if counts is None:
+                counts = torch.zeros(2, dtype=torch.int64, device=x.device)
+                dict.__setitem__(st, "qcounts", counts)
+        y = tier.step(prm, x, B, C, dt, exact=exact, hot_only=hot_only, qgate=tau, counts=counts)
     return decode_epilogue(m, y, gate, hidden_states.dtype)
+
+
+def check_readout_cfg(cfg, pb: int, N: int):
+    """Readout keys the kernels do not serve: a hot/cold split changed after capture
+    (the tier's split is fixed when it is captured) and the top-k cold column gather
+    (ktop < N - pb, scale/v4_native_decode.py:129-143: a data-dependent gather of cold
+    columns, not a tier readout)."""
+    if min(int(cfg["pb"]), N) != min(pb, N):
+        raise NotImplementedError(f"v4cfg['pb'] changed from {pb} to {cfg['pb']} after capture; the tier's "
+                                  "hot/cold split is fixed at capture")
+    ktop = int(cfg.get("ktop") or 0)
+    if pb < N and 0 < ktop < N - pb and not cfg.get("corr") and not cfg.get("coldoff"):
+        raise NotImplementedError("v4cfg['ktop'] (top-k cold column gather) is not implemented by the "
+                                  "MI355X kernels")
 
 
 def _cold_kind(cfg) -> str:
@@ -187,9 +239,14 @@ def capture(m, cache_params, dt_min: float):
     """End of prefill: tiers from the cache's fp32 state (rotated into R's basis)."""
     cfg = m.v4cfg
     pb, c = int(cfg["pb"]), int(cfg["c"])
-    for key in ("coldoff", "qgate", "ktop"):
-        if cfg.get(key):
-            raise NotImplementedError(f"v4cfg[{key!r}] is not implemented by the MI355X kernels")
+    check_readout_cfg(cfg, pb, m.ssm_state_size)
+    if c > ops.MAX_WINDOW and pb < m.ssm_state_size:
+        # the hot-only readout never reads the cold tier, which evolves exactly at any
+        # window: it runs on the largest window the kernels take
+        if not cfg.get("coldoff"):
+            raise NotImplementedError(f"window c={c} exceeds the kernels' {ops.MAX_WINDOW} (supported with "
+                                      "coldoff=1 only)")
+        c = ops.MAX_WINDOW
     layer = cache_params.layers[m.layer_idx]
     S = layer.recurrent_states[0]
     prm = layer_params(m, dt_min)

@@ -14,6 +14,7 @@ from . import _lib
 from ._lib import COLD_KINDS, NssmError, TIER_FIELDS, check, lib
 
 N_STATE = 128
+MAX_WINDOW = 64  # largest flush window c the kernels take
 
 
 def _stream() -> int:
@@ -190,20 +191,34 @@ class V4Tier:
                                  _ptr(phase), _stream()), "nssm_v4_join")
 
     def step(self, prm: LayerParams, x, B, C, dt, y: Optional[torch.Tensor] = None,
-             slot_ids: Optional[torch.Tensor] = None, exact: bool = False) -> torch.Tensor:
+             slot_ids: Optional[torch.Tensor] = None, exact: bool = False, hot_only: bool = False,
+             qgate: float = 0.0, counts: Optional[torch.Tensor] = None) -> torch.Tensor:
         """One decode token for b requests (slot_ids: their slots, default 0..b-1).
         exact=True reads the cold tier with the rank-c exact correction (corr=1,
-        scale/v4_native_decode.py:81-117) instead of the stale readout; the tier
-        evolves the same way either way."""
+        scale/v4_native_decode.py:81-117) instead of the stale readout. hot_only=True is
+        the hot-only draft readout (coldoff=1, scale/v4_native_decode.py:118-127);
+        qgate=tau > 0 drops the cold term of the heads whose query puts less than tau of
+        its energy on the cold columns (scale/v4_native_decode.py:147-156), and adds the
+        gated and kept head counts to counts (int64 [2] on the GPU) when given. The tier
+        evolves the same way in every case."""
         b = x.shape[0]
+        gated = hot_only or qgate > 0
+        if exact and gated:
+            raise ValueError("exact readout cannot be combined with hot_only or qgate")
         if y is None:
             y = torch.empty(b, prm.H, prm.P, device=x.device, dtype=torch.float32)
         _need(y, "y", torch.float32, (b, prm.H, prm.P))
+        if counts is not None:
+            _need(counts, "counts", torch.int64, (2,))
         pc, ic, tc = prm.c_struct(), _inputs(prm, x, B, C, dt, slot_ids), self.c_struct()
         ws = step_workspace(b, prm.H, prm.G, self.c, x.device)
-        fn, name = (lib().nssm_v4_step_exact, "nssm_v4_step_exact") if exact else (lib().nssm_v4_step, "nssm_v4_step")
-        check(fn(ctypes.byref(pc), ctypes.byref(tc), ctypes.byref(ic), y.data_ptr(), ws.data_ptr(), ws.numel(),
-                 _stream()), name)
+        args = (ctypes.byref(pc), ctypes.byref(tc), ctypes.byref(ic), y.data_ptr(), ws.data_ptr(), ws.numel())
+        if gated:
+            check(lib().nssm_v4_step_gated(*args, int(hot_only), float(qgate), _ptr(counts), _stream()),
+                  "nssm_v4_step_gated")
+        else:
+            fn, name = (lib().nssm_v4_step_exact, "nssm_v4_step_exact") if exact else (lib().nssm_v4_step, "nssm_v4_step")
+            check(fn(*args, _stream()), name)
         return y
 
     def materialize(self, prm: LayerParams, slot_ids: Optional[torch.Tensor] = None,

@@ -12,10 +12,15 @@ clamped at the mixer's time_step_min (scale/v4_native_decode.py:55), and the
 cold snapshot is bf16 when cold_bf16=1 (an exact fp32 master is kept beside
 it) or an exact fp32 copy otherwise.
 
-corr=1 selects the rank-c exact correction readout
-(scale/v4_native_decode.py:81-117), read from v4cfg at every token. The installed
-transformers has no `torch_forward`; the mixer's `forward` is patched instead.
-coldoff=1 raises NotImplementedError at capture.
+The readout keys are read from v4cfg at every token, in the reference's order:
+corr=1 the rank-c exact correction readout (scale/v4_native_decode.py:81-117), else
+coldoff=1 the hot-only draft readout (:118-127), else the stale readout, query-gated when
+v4cfg["qgate"] > 0 (:147-156; `_v4state.get("qgate_n")` / `get("qgate_kept")` count the
+gated and kept heads since the prompt's capture). Under coldoff the tier evolves exactly
+(the reference advances only t). A window beyond the kernels' 64 tokens (c=1<<30,
+scale/probe_selfspec_alpha.py:59) runs on a 64-token window while coldoff=1 and raises on
+a stale readout; ktop > 0 raises NotImplementedError. The installed transformers has no
+`torch_forward`; the mixer's `forward` is patched instead.
 """
 from transformers.models.nemotron_h import modeling_nemotron_h as M
 

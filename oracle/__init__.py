@@ -34,6 +34,10 @@ Pinning status of each function (how it is checked, in tests/test_oracle.py):
                     (rounding at every token, never, or quantizing the e4m3 copy
                     from the unrounded state each fails); TieredV4 == NativeV4
                     with ragged phases and join/leave
+  NativeV4 gated    (hot_only, qgate) hot_only y = the hot part of the stale y with D x;
+                    qgate on constructed queries C = R^T e_n (all energy on one column):
+                    a cold column is kept, a hot one dropped at any tau, and the counters
+                    count heads; the state is the ungated one's in every mode
   quant_fp8 / read  torch float8_e4m3fn cast; scale = amax/448 + 1e-12 per row
   fp8_readout       closed form of the reference docstring vs an fp64 loop
   hot_only_step     the hot columns of an fp64 fresh trajectory (they never read the cold ones)

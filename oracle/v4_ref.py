@@ -203,6 +203,13 @@ class NativeV4:
     the decay product and the window update separately, :79-84; one rounding of the
     fp32 result is this convention.)
 
+    step(..., hot_only=True) is the draft readout of coldoff=1
+    (scale/v4_native_decode.py:118-127): y from the hot columns only. step(..., qgate=tau)
+    is the query-gated cold skip (scale/v4_native_decode.py:147-156): a head's cold term is
+    dropped when sum_{n>=k} C'_n^2 / max(sum_n C'_n^2, 1e-9) < tau; qgate_n / qgate_kept
+    count heads and kept heads. In both the tier's bookkeeping (t, glog, snapshot) runs as
+    in the stale readout (the reference's coldoff branch skips it, :118-127).
+
     exact=True is the rank-c exact correction readout (corr=1,
     scale/v4_native_decode.py:81-117): the log-decay G_t includes this token, this
     token's (B'_cold, dt x, G_t) is buffered before the readout, and
@@ -227,6 +234,8 @@ class NativeV4:
         self.sc8 = torch.ones(slots, H, P, 1, dtype=torch.float32)
         self.glog = torch.zeros(slots, H, dtype=dtype)
         self.t = torch.zeros(slots, dtype=torch.int64)
+        self.qgate_n = 0
+        self.qgate_kept = 0
 
     def _store(self, slots, s_cold):
         if self.cold == "fp8":
@@ -261,7 +270,9 @@ class NativeV4:
         for s in slots.tolist():
             self.buf[s] = []
 
-    def step(self, x, B, C, dt_raw, prm: LayerParams, slots: Optional[torch.Tensor] = None) -> torch.Tensor:
+    def step(self, x, B, C, dt_raw, prm: LayerParams, slots: Optional[torch.Tensor] = None,
+             hot_only: bool = False, qgate: float = 0.0) -> torch.Tensor:
+        assert not (self.exact and (hot_only or qgate > 0)), "the exact readout takes precedence"
         b = x.shape[0]
         slots = torch.arange(b) if slots is None else torch.as_tensor(slots, dtype=torch.long)
         k, c = self.k, self.c
@@ -284,6 +295,15 @@ class NativeV4:
                 y_cold[i] = y_cold[i] + torch.einsum("jh,jhp->hp", w, Xs)
         else:
             y_cold = torch.einsum("bhpn,bhn->bhp", self._read(slots), Cp[..., k:]) * torch.exp(glog)[..., None]
+            if hot_only:
+                y_cold = torch.zeros_like(y_cold)
+            elif qgate > 0:
+                e = Cp * Cp
+                rho = e[..., k:].sum(-1) / e.sum(-1).clamp(min=1e-9)  # [b,H]
+                keep = rho >= qgate
+                self.qgate_n += keep.numel()
+                self.qgate_kept += int(keep.sum())
+                y_cold = y_cold * keep[..., None].to(y_cold.dtype)
         y = torch.einsum("bhpn,bhn->bhp", S[..., :k], Cp[..., :k]) + y_cold
         t = self.t[slots] + 1
         self.t[slots] = t

@@ -176,6 +176,13 @@ def test_entry_points_validate_before_launching():
     odd = _lib.StepInputs(4, fake + 2, fake, fake, fake, None)
     assert L.nssm_v4_step_exact(ctypes.byref(prm), ctypes.byref(tier), ctypes.byref(odd), fake, fake, 1 << 30,
                                 None) == -3
+    # gated readout: the threshold must be a finite number, the counters 8-byte aligned
+    t32 = _lib.Tier(4, 32, 4, _lib.COLD_FP32, *([fake] * 10))
+    gargs = (ctypes.byref(prm), ctypes.byref(t32), ctypes.byref(inp), fake, fake, 1 << 30)
+    assert L.nssm_v4_step_gated(*gargs, 0, float("nan"), None, None) == -2
+    assert L.nssm_v4_step_gated(*gargs, 0, float("inf"), None, None) == -2
+    assert L.nssm_v4_step_gated(*gargs, 0, 0.5, fake + 4, None) == -3
+    assert L.nssm_v4_step_gated(*gargs[:1], None, *gargs[2:], 1, 0.0, None, None) == -1
     assert L.nssm_set_launch(5) == -6
     assert L.nssm_set_launch(-1) == -6
     # 4 units per workgroup do not divide P / 8 = 10 rows blocks: refused before any launch

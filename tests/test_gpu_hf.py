@@ -84,7 +84,7 @@ def _rot(S, R, H):
     return torch.einsum("bhpn,hmn->bhpm", S.double(), Rh).float()
 
 
-def _replay_and_check(model, rec, pb, c, cold, dt_min_of, exact=False):
+def _replay_and_check(model, rec, pb, c, cold, dt_min_of, exact=False, modes=None):
     from nested_ssm_amd import hf
 
     for m in hf.mixers(model):
@@ -99,7 +99,7 @@ def _replay_and_check(model, rec, pb, c, cold, dt_min_of, exact=False):
         ref.join(torch.arange(b), S0)
         assert len(rec.inputs[li]) > 0
         for step, ((x, B, C, dt), y) in enumerate(zip(rec.inputs[li], rec.ys[li])):
-            y_ref = ref.step(x, B, C, dt, prm)
+            y_ref = ref.step(x, B, C, dt, prm, **(modes[step] if modes else {}))
             if cold == "fp32":
                 assert_close32(y, y_ref, f"layer {li} step {step} (pb={pb}, c={c})")
             else:
@@ -277,3 +277,76 @@ def test_generate_runs_with_tiered_decode():
         g1 = model.generate(ids, max_new_tokens=9, do_sample=False)
         g2 = model.generate(ids, max_new_tokens=9, do_sample=False)
     assert g1.shape == (2, 15) and torch.equal(g1, g2)
+
+
+def _decode_with_modes(model, ids, modes):
+    """Prefill, then one decode token per entry of modes, switching the mixers'
+    v4cfg["coldoff"] / v4cfg["qgate"] before each (as scale/probe_selfspec_policy.py:125-136
+    and scale/run_recall_native.py:85-89 mutate them)."""
+    from nested_ssm_amd import hf
+
+    out = model(ids, use_cache=True)
+    pkv = out.past_key_values
+    tok = out.logits[:, -1:].argmax(-1)
+    for md in modes:
+        for m in hf.mixers(model):
+            m.v4cfg["coldoff"] = int(md.get("hot_only", False))
+            m.v4cfg["qgate"] = md.get("qgate", 0.0)
+        out = model(tok, past_key_values=pkv, use_cache=True)
+        tok = out.logits[:, -1:].argmax(-1)
+    return pkv
+
+
+@pytest.mark.parametrize("cold_bf16", [0, 1])
+def test_native_install_gated_readouts_match_oracle(monkeypatch, cold_bf16):
+    """coldoff and qgate switched per token on the installed mixers against the oracle's
+    gated readouts; the qgate counters read as scale/run_recall_native.py:116-118 does."""
+    from nested_ssm_amd import hf
+    from nested_ssm_amd import v4_native_decode as V
+
+    pb, c = 32, 4
+    model = _tiny_model(seed=21)
+    assert V.install(model, pb=pb, c=c, cold_bf16=cold_bf16) == 2
+    rec = Recorder(monkeypatch)
+    ids = torch.randint(0, 96, (3, 7), generator=torch.Generator().manual_seed(22)).cuda()
+    tau = (N - pb) / N
+    modes = [[{}, dict(hot_only=True), dict(qgate=tau)][i % 3] for i in range(2 * c + 4)]
+    with torch.no_grad():
+        _decode_with_modes(model, ids, modes)
+    cold = "bf16" if cold_bf16 else "fp32"
+    for m, ref in _replay_and_check(model, rec, pb, c, cold, lambda m: float(m.time_step_limit[0]), modes=modes):
+        st = m._v4state
+        assert "qgate_n" in st and ref.qgate_n > 0
+        assert st.get("qgate_n", 0) == ref.qgate_n and st.get("qgate_kept", 0) == ref.qgate_kept
+        assert st["t"] == int(ref.t[0])
+    with torch.no_grad():  # a new prompt's capture starts the counters again
+        model(ids, use_cache=True)
+    for m in hf.mixers(model):
+        assert "qgate_n" not in m._v4state and m._v4state.get("qgate_kept", 0) == 0
+
+
+def test_native_install_coldoff_with_an_unbounded_window(monkeypatch):
+    """install(..., c=1 << 30, coldoff=1) (scale/probe_selfspec_alpha.py:59): the hot-only
+    readout runs on the kernels' largest window, which it never reads, the state stays
+    exact, and switching to the stale readout on that window is refused."""
+    from nested_ssm_amd import v4_native_decode as V
+
+    pb, c = 32, 1 << 30
+    model = _tiny_model(seed=25)
+    assert V.install(model, pb=pb, c=c, cold_bf16=0, coldoff=1) == 2
+    rec = Recorder(monkeypatch)
+    ids = torch.randint(0, 96, (2, 6), generator=torch.Generator().manual_seed(26)).cuda()
+    modes = [dict(hot_only=True)] * 70  # past one 64-token window
+    with torch.no_grad():
+        pkv = _decode_with_modes(model, ids, modes)
+    for m, ref in _replay_and_check(model, rec, pb, c, "fp32", lambda m: float(m.time_step_limit[0]),
+                                    modes=modes):
+        st = m._v4state
+        assert dict.get(st, "tier").c == 64 and st["t"] == int(ref.t[0]) == len(modes)
+        S = dict.get(st, "tier").materialize(st["params"]).cpu()
+        assert_close32(S, ref.S, f"layer {m.layer_idx} state")
+        assert st.get("qgate_n", 0) == 0 and "qgate_n" not in st
+        m.v4cfg["coldoff"] = 0
+    tok = torch.zeros(2, 1, dtype=torch.long, device="cuda")
+    with torch.no_grad(), pytest.raises(NotImplementedError, match="coldoff"):
+        model(tok, past_key_values=pkv, use_cache=True)

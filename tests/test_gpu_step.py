@@ -57,7 +57,7 @@ def test_fresh_dt_min_and_identity_rotation():
 
 
 def _run_v4(b, H, G, P, k, c, cold, steps, seed, slots=None, phase=None, check_state_every=1, exact=False,
-            master="fp32"):
+            master="fp32", modes=None, counts=None):
     gen, prm, S0 = _setup(b, H, P, G, seed)
     dprm = dev_params(prm)
     ref = oracle.NativeV4(b, H, P, 128, k, c, cold=cold, exact=exact, master=master)
@@ -68,8 +68,9 @@ def _run_v4(b, H, G, P, k, c, cold, steps, seed, slots=None, phase=None, check_s
     worst = 0.0
     for step in range(steps):
         x, B, C, dt = oracle.make_step_inputs(b, H, P, 128, G, gen)
-        y_ref = ref.step(x, B, C, dt, prm)
-        y = tier.step(dprm, *to_dev(x, B, C, dt), exact=exact)
+        md = modes(step) if modes else {}
+        y_ref = ref.step(x, B, C, dt, prm, **md)
+        y = tier.step(dprm, *to_dev(x, B, C, dt), exact=exact, counts=counts, **md)
         if cold == "fp8":
             r = max_rel(y.cpu(), y_ref)
             worst = max(worst, r)
@@ -398,3 +399,71 @@ def test_v4_bf16_master_exact_readout(cold, k, c):
     snapshot, as the oracle's exact mode with master="bf16"."""
     _run_v4(4, 8, 2, 80, k, c, cold, steps=2 * c + 5, seed=150 + k + c, phase=[0, 1, c - 1, c // 2],
             check_state_every=max(1, c // 2), exact=True, master="bf16")
+
+
+def _gate_modes(k):
+    """Readout per token: hot-only on every third token, a plain stale readout on every
+    fifth of the rest, else the query gate at the median cold energy fraction of an
+    isotropic query, (N - k) / N, so that it splits the heads."""
+    tau = (128 - k) / 128
+
+    def modes(step):
+        if step % 3 == 2:
+            return dict(hot_only=True)
+        if step % 5 == 4:
+            return {}
+        return dict(qgate=tau)
+    return modes
+
+
+@pytest.mark.parametrize("cold,k,c,P,master", [
+    ("fp32", 32, 4, 80, "fp32"),   # flush replay inside the stream kernel
+    ("fp32", 64, 24, 48, "fp32"),  # flush kernel
+    ("bf16", 32, 4, 80, "fp32"),
+    ("bf16", 32, 40, 80, "bf16"),  # one bf16 copy, flush kernel
+    ("fp8", 32, 4, 80, "fp32"),
+    ("fp8", 96, 20, 80, "bf16"),
+])
+def test_v4_gated_readout_matches_oracle(cold, k, c, P, master):
+    """coldoff (hot-only) and qgate readouts, switched per token, against the oracle's
+    (scale/v4_native_decode.py:118-127, :147-156): y, the gated and kept head counts,
+    and the exact state, with phases that put flushes on gated tokens."""
+    counts = torch.zeros(2, dtype=torch.int64, device="cuda")
+    tier, ref, _ = _run_v4(4, 8, 2, P, k, c, cold, steps=2 * c + 7, seed=170 + k + c, phase=[0, 1, c - 1, c // 2],
+                           check_state_every=max(1, c // 2), master=master, modes=_gate_modes(k), counts=counts)
+    n, kept = counts.tolist()
+    assert (n, kept) == (ref.qgate_n, ref.qgate_kept)
+    assert 0 < kept < n, "the gate kept all or none of the heads"
+    assert torch.equal(tier.t[:, 0].cpu().long(), ref.t)
+
+
+def test_hot_only_readout_reads_no_cold_column():
+    """A head that takes the hot-only readout and does not flush never reads its cold read
+    copy: with that copy NaN, y stays finite and equal to the oracle's until the window's
+    flush, and the state (master and ring) is untouched by it."""
+    b, H, G, P, k, c = 3, 8, 2, 80, 32, 8
+    gen, prm, S0 = _setup(b, H, P, G, seed=181)
+    dprm = dev_params(prm)
+    ref = oracle.NativeV4(b, H, P, 128, k, c, cold="bf16")
+    ref.join(torch.arange(b), S0)
+    tier = V4Tier(b, H, P, G, k_hot=k, c=c, cold="bf16")
+    tier.join(dprm, *to_dev(S0))
+    tier.cold_t.fill_(float("nan"))
+    for step in range(c - 1):
+        x, B, C, dt = oracle.make_step_inputs(b, H, P, 128, G, gen)
+        y_ref = ref.step(x, B, C, dt, prm, hot_only=True)
+        y = tier.step(dprm, *to_dev(x, B, C, dt), hot_only=True)
+        assert bool(torch.isfinite(y).all()), f"step {step}: the hot-only readout read the cold copy"
+        assert_close32(y, y_ref, f"hot-only y step {step}", **FP32_TOL)
+    assert_close32(tier.materialize(dprm), ref.S, "materialized state", **FP32_TOL)
+
+
+def test_gated_readout_rejects_the_exact_one():
+    b, H, G, P = 2, 8, 1, 80
+    gen, prm, S0 = _setup(b, H, P, G, seed=5)
+    dprm = dev_params(prm)
+    tier = V4Tier(b, H, P, G, k_hot=32, c=4, cold="fp32")
+    tier.join(dprm, *to_dev(S0))
+    x, B, C, dt = oracle.make_step_inputs(b, H, P, 128, G, gen)
+    with pytest.raises(ValueError, match="exact"):
+        tier.step(dprm, *to_dev(x, B, C, dt), exact=True, hot_only=True)

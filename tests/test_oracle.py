@@ -348,6 +348,64 @@ def test_native_v4_bf16_snapshot_is_rne_of_fp32():
     assert torch.equal(nb.snap, nb.S[..., k:].to(torch.bfloat16).float())
 
 
+def test_native_v4_hot_only_and_qgate_readouts():
+    """coldoff=1 (hot-only draft readout) and the query-gated cold skip, against an fp64
+    restatement built from the stale readout and the hot columns of a fresh trajectory:
+    hot_only y = hot C'[:k] + D x; qgate y = stale y for kept heads, hot-only y for the
+    others, keep computed from the rotated C of each group (a head inherits its group's C');
+    tau = 0 is the stale readout, tau above 1 the hot-only one; the state evolves as in the
+    stale readout either way."""
+    b, H, P, G, k, c = 3, 8, 16, 2, 32, 4
+    gen, prm, S0 = _small(seed=43, b=b, H=H, P=P, G=G)
+    f64 = torch.float64
+    stale = oracle.NativeV4(b, H, P, N, k, c, dtype=f64)
+    gated = oracle.NativeV4(b, H, P, N, k, c, dtype=f64)
+    hot = oracle.NativeV4(b, H, P, N, k, c, dtype=f64)
+    for n in (stale, gated, hot):
+        n.join(torch.arange(b), S0.double())
+    S = S0.double().clone()
+    prm64 = prm.to(f64)
+    tau = 0.75  # the cold fraction of |C'|^2 is about 96/128 for random C: about half the heads kept
+    kept_total = 0
+    for step in range(2 * c + 1):
+        x, B, C, dt = oracle.make_step_inputs(b, H, P, N, G, gen)
+        y_s = stale.step(x, B, C, dt, prm)
+        y_g = gated.step(x, B, C, dt, prm, qgate=tau)
+        y_h = hot.step(x, B, C, dt, prm, hot_only=True)
+        oracle.fresh_step(S, x, B, C, dt, prm64, dtype=f64)
+        Cp = _heads(oracle.rotate(C.double(), prm64.R), H)
+        y_hot_ref = torch.einsum("bhpn,bhn->bhp", S[..., :k], Cp[..., :k]) + x.double() * prm64.D[None, :, None]
+        assert torch.allclose(y_h, y_hot_ref, atol=1e-12)
+        rho = (Cp[..., k:] ** 2).sum(-1) / (Cp ** 2).sum(-1)
+        keep = rho >= tau
+        kept_total += int(keep.sum())
+        assert 0 < int(keep.sum()) < keep.numel()
+        want = torch.where(keep[..., None], y_s, y_h)
+        assert torch.allclose(y_g, want, atol=1e-12)
+    assert gated.qgate_n == (2 * c + 1) * b * H and gated.qgate_kept == kept_total
+    # the bookkeeping runs as in the stale readout
+    for n in (gated, hot):
+        assert torch.equal(n.S, stale.S) and torch.equal(n.snap, stale.snap) and torch.equal(n.glog, stale.glog)
+    # tau = 0 is the stale readout; tau above 1 the hot-only one
+    a0, a1, a2, a3 = (oracle.NativeV4(b, H, P, N, k, c, dtype=f64) for _ in range(4))
+    for n in (a0, a1, a2, a3):
+        n.join(torch.arange(b), S0.double())
+    ins = oracle.make_step_inputs(b, H, P, N, G, gen)
+    assert torch.equal(a0.step(*ins, prm, qgate=0.0), a1.step(*ins, prm))
+    assert torch.equal(a2.step(*ins, prm, qgate=1.5), a3.step(*ins, prm, hot_only=True))
+    # a query whose rotated C' lies in one cold column (C = R^T e_n, n >= k) has rho = 1 and
+    # is kept for tau = 0.95; one in a hot column (n < k) has rho ~ 0 and is dropped for
+    # tau = 0.05 (a swapped fraction or a transposed R fails this)
+    for col, tau_, kept in ((k + 7, 0.95, True), (3, 0.05, False)):
+        Cq = torch.zeros(b, G, N, dtype=f64)
+        Cq[..., col] = 1.0
+        Cq = torch.einsum("gmn,bgm->bgn", prm64.R, Cq).to(torch.bfloat16)  # R^T e_col per group
+        n_ = oracle.NativeV4(b, H, P, N, k, c, dtype=f64)
+        n_.join(torch.arange(b), S0.double())
+        n_.step(ins[0], ins[1], Cq, ins[3], prm, qgate=tau_)
+        assert n_.qgate_kept == (b * H if kept else 0)
+
+
 def _bf16(v: torch.Tensor) -> torch.Tensor:
     return v.to(torch.bfloat16).to(v.dtype)
 
