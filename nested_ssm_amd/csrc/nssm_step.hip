@@ -146,6 +146,19 @@ __device__ __forceinline__ void st_stream(T v, T* p) {
   if constexpr (NSSM_NT_STORE) __builtin_nontemporal_store(v, p);
   else *p = v;
 }
+// 16-bit arrays in the segment mapping (8 bytes per lane, half a cache line per row per
+// wave instruction): plain accesses, so the two halves of a line meet in L2
+#ifndef NSSM_NT_HALF
+#define NSSM_NT_HALF 0
+#endif
+__device__ __forceinline__ u2v ld_half(const u2v* p) {
+  if constexpr (NSSM_NT_HALF) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+__device__ __forceinline__ void st_half(u2v v, u2v* p) {
+  if constexpr (NSSM_NT_HALF) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
 
 // ---------------------------------------------------------------------------
 // prep: one workgroup (256 threads) per (group g, block of prb <= 8 requests).
@@ -543,7 +556,7 @@ __device__ __forceinline__ void unit_load(const StepArgs& a, size_t row, size_t 
       } else if constexpr (COLD == NSSM_COLD_BF16_SINGLE) {
         const u2v* p = reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.cold) + row * C::NC) + q;
 #pragma unroll
-        for (int s = 0; s < C::CS; ++s) d.cb[s] = ld_stream(p + 8 * s);
+        for (int s = 0; s < C::CS; ++s) d.cb[s] = ld_half(p + 8 * s);
       } else if constexpr (COLD == NSSM_COLD_BF16) {
         ld_words<C::WORDS>(
             reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(a.cold) + row * C::NC + C::CW * q), d.cw);
@@ -564,12 +577,42 @@ __device__ __forceinline__ void bf16x4_to_f32(u2v w, float (&v)[4]) {
   v[2] = __uint_as_float(w.y << 16);
   v[3] = __uint_as_float(w.y & 0xffff0000u);
 }
+#ifndef NSSM_HW_BF16
+#define NSSM_HW_BF16 1
+#endif
 __device__ __forceinline__ u2v f32x4_to_bf16(float a, float b, float c, float d) {
   u2v t;
-  t.x = (uint32_t)nssm_f32_to_bf16(a) | ((uint32_t)nssm_f32_to_bf16(b) << 16);
-  t.y = (uint32_t)nssm_f32_to_bf16(c) | ((uint32_t)nssm_f32_to_bf16(d) << 16);
+  if constexpr (NSSM_HW_BF16) {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    t.x = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{a, b}), b2));
+    t.y = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{c, d}), b2));
+  } else {
+    t.x = (uint32_t)nssm_f32_to_bf16(a) | ((uint32_t)nssm_f32_to_bf16(b) << 16);
+    t.y = (uint32_t)nssm_f32_to_bf16(c) | ((uint32_t)nssm_f32_to_bf16(d) << 16);
+  }
   return t;
 }
+
+#ifndef NSSM_FAST_QDIV
+#define NSSM_FAST_QDIV 1
+#endif
+// w / sc rounded to nearest for sc > 0: one correctly rounded reciprocal per row, then
+// q = w inv and one correction step q + (w - q sc) inv (Markstein: correctly rounded when
+// inv is and no intermediate over- or underflows); the sign of w restores -0 (the
+// correction step sums +0 and -0 to +0)
+struct QDiv {
+  float sc, inv;
+  __device__ __forceinline__ explicit QDiv(float s) : sc(s), inv(1.0f / s) {}
+  __device__ __forceinline__ float operator()(float w) const {
+    if constexpr (NSSM_FAST_QDIV) {
+      const float q = w * inv;
+      return copysignf(fmaf(fmaf(-q, sc, w), inv, q), w);
+    } else {
+      return w / sc;
+    }
+  }
+};
 
 // stale readout partial of one lane from its read-copy registers (times the row scale for e4m3)
 template <int K, int COLD>
@@ -689,7 +732,7 @@ __device__ __forceinline__ void cold_store(const StepArgs& a, size_t row, int q,
   } else if constexpr (COLD == NSSM_COLD_BF16_SINGLE) {
     u2v* p = reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.cold) + row * NC) + q;
 #pragma unroll
-    for (int s = 0; s < CS; ++s) st_stream(f32x4_to_bf16(v[s][0], v[s][1], v[s][2], v[s][3]), p + 8 * s);
+    for (int s = 0; s < CS; ++s) st_half(f32x4_to_bf16(v[s][0], v[s][1], v[s][2], v[s][3]), p + 8 * s);
   } else {
     float w[CS][4];  // the master's values
     if constexpr (COLD == NSSM_COLD_FP8_BF16M) {
@@ -697,7 +740,7 @@ __device__ __forceinline__ void cold_store(const StepArgs& a, size_t row, int q,
 #pragma unroll
       for (int s = 0; s < CS; ++s) {
         const u2v t = f32x4_to_bf16(v[s][0], v[s][1], v[s][2], v[s][3]);
-        st_stream(t, pm + 8 * s);
+        st_half(t, pm + 8 * s);
         bf16x4_to_f32(t, w[s]);
       }
     } else {
@@ -712,7 +755,7 @@ __device__ __forceinline__ void cold_store(const StepArgs& a, size_t row, int q,
     if constexpr (COLD == NSSM_COLD_BF16) {
       u2v* p = reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.cold) + row * NC) + q;
 #pragma unroll
-      for (int s = 0; s < CS; ++s) st_stream(f32x4_to_bf16(w[s][0], w[s][1], w[s][2], w[s][3]), p + 8 * s);
+      for (int s = 0; s < CS; ++s) st_half(f32x4_to_bf16(w[s][0], w[s][1], w[s][2], w[s][3]), p + 8 * s);
     } else {  // e4m3 with the per-row amax scale of scale/vllm_v4_patch.py:106-111
       float am = 0.f;
 #pragma unroll
@@ -721,10 +764,11 @@ __device__ __forceinline__ void cold_store(const StepArgs& a, size_t row, int q,
         for (int e = 0; e < 4; ++e) am = fmaxf(am, fabsf(w[s][e]));
       am = max8(am);
       const float sc = am / 448.0f + 1e-12f;
+      const QDiv qd(sc);
       uint32_t* p = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.cold) + row * NC) + q;
 #pragma unroll
       for (int s = 0; s < CS; ++s)
-        st_stream(f32x4_to_fp8(w[s][0] / sc, w[s][1] / sc, w[s][2] / sc, w[s][3] / sc), p + 8 * s);
+        st_stream(f32x4_to_fp8(qd(w[s][0]), qd(w[s][1]), qd(w[s][2]), qd(w[s][3])), p + 8 * s);
       if (q == 0) a.scale[row] = sc;
     }
   }
@@ -757,7 +801,7 @@ __device__ __forceinline__ void unit_compute_flush(const StepArgs& a, size_t sh,
     } else if constexpr (COLD == NSSM_COLD_BF16_SINGLE) {
       bf16x4_to_f32(d.cb[s], t);
     } else if constexpr (C::MASTER16) {
-      bf16x4_to_f32(ld_stream(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.master) + row * NC) + q + 8 * s), t);
+      bf16x4_to_f32(ld_half(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.master) + row * NC) + q + 8 * s), t);
     } else {  // fp32 master
       const f4 m4 = ld_stream(reinterpret_cast<const f4*>(static_cast<const float*>(a.master) + row * NC) + q + 8 * s);
       t[0] = m4.x; t[1] = m4.y; t[2] = m4.z; t[3] = m4.w;
@@ -1118,11 +1162,11 @@ __global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
             const size_t row = row0 + (tt / NT) * 16 + li;
             const int col = (tt % NT) * 16 + 4 * lk;
             if constexpr (SRC16)
-              old16[i] = ld_stream(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(src) + row * NC + col));
+              old16[i] = ld_half(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(src) + row * NC + col));
             else
               old[i] = ld_stream(reinterpret_cast<const f4*>(static_cast<const float*>(src) + row * NC + col));
             if constexpr (COLD == NSSM_COLD_BF16)
-              rb16[i] = ld_stream(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.cold) + row * NC + col));
+              rb16[i] = ld_half(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.cold) + row * NC + col));
             if constexpr (C::E4M3) {
               r8[i] = ld_stream(reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(a.cold) + row * NC + col));
               rsc[i] = a.scale[row];
@@ -1203,7 +1247,7 @@ __global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
             } else if constexpr (SRC16) {  // bf16 single copy or bf16 master: RNE, and the
               // e4m3 copy is quantized from the rounded values
               const u2v t = f32x4_to_bf16(nv.x, nv.y, nv.z, nv.w);
-              st_stream(t, reinterpret_cast<u2v*>(static_cast<uint16_t*>(C::SEG ? a.cold : a.master) + row * NC + col));
+              st_half(t, reinterpret_cast<u2v*>(static_cast<uint16_t*>(C::SEG ? a.cold : a.master) + row * NC + col));
               float r4[4];
               bf16x4_to_f32(t, r4);
               nv = f4{r4[0], r4[1], r4[2], r4[3]};
@@ -1212,8 +1256,8 @@ __global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
             }
             acc[i] = nv;
             if constexpr (COLD == NSSM_COLD_BF16)
-              st_stream(f32x4_to_bf16(nv.x, nv.y, nv.z, nv.w),
-                        reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.cold) + row * NC + col));
+              st_half(f32x4_to_bf16(nv.x, nv.y, nv.z, nv.w),
+                      reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.cold) + row * NC + col));
             if (lk == 0) sPart[p * NT + nt] = pc * rscale;
             if constexpr (C::E4M3) {
               float am = fmaxf(fmaxf(fabsf(nv.x), fabsf(nv.y)), fmaxf(fabsf(nv.z), fabsf(nv.w)));
@@ -1236,8 +1280,9 @@ __global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
 #pragma unroll
               for (int t2 = 0; t2 < NT; ++t2) am = fmaxf(am, sAmx[p * NT + t2]);
               const float sc = am / 448.0f + 1e-12f;  // scale/vllm_v4_patch.py:106-111
+              const QDiv qd(sc);
               const f4 nv = acc[i];
-              st_stream(f32x4_to_fp8(nv.x / sc, nv.y / sc, nv.z / sc, nv.w / sc),
+              st_stream(f32x4_to_fp8(qd(nv.x), qd(nv.y), qd(nv.z), qd(nv.w)),
                         reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.cold) + row * NC + nt * 16 + 4 * lk));
               if (nt == 0 && lk == 0) a.scale[row] = sc;
             }

@@ -467,3 +467,48 @@ def test_gated_readout_rejects_the_exact_one():
     x, B, C, dt = oracle.make_step_inputs(b, H, P, 128, G, gen)
     with pytest.raises(ValueError, match="exact"):
         tier.step(dprm, *to_dev(x, B, C, dt), exact=True, hot_only=True)
+
+
+def _rounding_state(b, H, P, gen):
+    """fp32 states that exercise every rounding path: magnitudes over 10^-6 .. 10^3 per
+    row, exact bf16 halfway cases (the low 16 bits 0x8000, RNE picks the even neighbour),
+    fp32 subnormals, signed zeros and one element per row at the row maximum's value."""
+    S = torch.randn(b, H, P, 128, generator=gen) * torch.pow(10.0, torch.empty(b, H, P, 1).uniform_(-6, 3, generator=gen))
+    bits = S.view(torch.int32)
+    tie = torch.rand(S.shape, generator=gen) < 0.25
+    bits = torch.where(tie, (bits & ~0xFFFF) | 0x8000, bits)
+    S = bits.view(torch.float32)
+    sub = torch.rand(S.shape, generator=gen) < 0.02
+    S = torch.where(sub, torch.randn(S.shape, generator=gen) * 1e-39, S)
+    S[..., 5] = 0.0
+    S[..., 6] = -0.0
+    return S.contiguous()
+
+
+@pytest.mark.parametrize("cold,master", [("bf16", "bf16"), ("bf16", "fp32"), ("fp8", "fp32"), ("fp8", "bf16")])
+def test_join_quantization_is_bit_exact(cold, master):
+    """The tier's cold copies at the join against torch's own casts on the CPU, bit for
+    bit: bf16 by round-to-nearest-even (the kernels use gfx950's packed conversion), the
+    e4m3 row scale amax / 448 + 1e-12 and codes (v / scale).to(float8_e4m3fn) (the kernels
+    divide by a reciprocal and one correction step), of the master's values."""
+    b, H, G, P, k = 3, 8, 2, 80, 32
+    gen = torch.Generator().manual_seed(190)
+    S = _rounding_state(b, H, P, gen)
+    prm = oracle.make_layer_params(H, P, 128, G, gen)
+    dprm = dev_params(prm)
+    tier = V4Tier(b, H, P, G, k_hot=k, c=4, cold=cold, master=master)
+    tier.join(dprm, S.cuda())
+    torch.cuda.synchronize()
+    Sc = S[..., k:]
+    assert torch.equal(tier.hot.cpu().view(torch.int32), S[..., :k].contiguous().view(torch.int32))
+    ref_master = Sc.to(torch.bfloat16) if master == "bf16" else Sc
+    if tier.master is not None:
+        assert torch.equal(tier.master.cpu().view(torch.int16 if master == "bf16" else torch.int32),
+                           ref_master.contiguous().view(torch.int16 if master == "bf16" else torch.int32))
+    mv = ref_master.float()
+    if cold == "bf16":
+        assert torch.equal(tier.cold_t.cpu().view(torch.int16), mv.to(torch.bfloat16).view(torch.int16))
+    else:
+        q, sc = oracle.quant_fp8(mv)
+        assert torch.equal(tier.scale.cpu().view(torch.int32), sc[..., 0].contiguous().view(torch.int32))
+        assert torch.equal(tier.cold_t.cpu(), q.view(torch.uint8))
