@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define NSSM_ABI_VERSION 7
+#define NSSM_ABI_VERSION 8
 
 /* error codes */
 #define NSSM_OK 0
@@ -100,12 +100,13 @@ typedef struct nssm_step_inputs {
 } nssm_step_inputs;
 
 /* Tiered state of one layer for `slots` sequence slots (all buffers are
- * owned by the caller). Layouts, all row-major:
+ * owned by the caller). Layouts, row-major unless noted:
  *   hot      fp32 [slots][H][P][K]
  *   cold     [slots][H][P][NC]   fp32 | bf16 | e4m3fn bytes, by cold_kind
+ *                                (BF16_SINGLE: unit-blocked, below)
  *   scale    fp32 [slots][H][P]         (FP8 and FP8_BF16M, else NULL)
- *   master   [slots][H][P][NC]          fp32 for BF16 / FP8, bf16 for FP8_BF16M,
- *                                       else NULL
+ *   master   [slots][H][P][NC]          fp32 for BF16 / FP8, bf16 for FP8_BF16M
+ *                                       (unit-blocked, below), else NULL
  *   ring_x   bf16 [slots][H][c][P]      x of buffered tokens
  *   ring_dt  fp32 [slots][H][c]         softplus'd dt of buffered tokens
  *   ring_b   fp32 [slots][G][c][NC]     rotated B cold columns of buffered tokens
@@ -113,7 +114,11 @@ typedef struct nssm_step_inputs {
  *   nv       int32 [slots][H]           buffered tokens since the last snapshot
  *   glog     fp32 [slots][H]            log-decay since the snapshot, one token lagged
  * All heads of a slot carry equal t and nv. hot, cold, master and ring_b are
- * 16-byte aligned, ring_x 8-byte aligned. */
+ * 16-byte aligned, ring_x 8-byte aligned.
+ * Unit-blocked (the single bf16 copy, the bf16 master): with row = (slot H + h) P + p,
+ * element (row, col) sits at (row / 8) 8 NC + (col / 32) 256 + (row % 8) 32 + col % 32:
+ * the 8 rows of a unit form one block, 32-column segment by segment, so a wave moves
+ * whole cache lines of it (the sizes are those of [slots][H][P][NC]). */
 typedef struct nssm_tier {
   int32_t slots, k_hot, c, cold_kind;
   float* hot;

@@ -159,6 +159,15 @@ __device__ __forceinline__ void st_half(u2v v, u2v* p) {
   if constexpr (NSSM_NT_HALF) __builtin_nontemporal_store(v, p);
   else *p = v;
 }
+// The single bf16 copy and the bf16 master are kept unit-blocked: the 8 rows of a unit
+// (rows 8u .. 8u+7 of the [slots][H][P] row order) are one block of 8 NC elements,
+// segment-major ([NC / 32][8 rows][32 columns]), so one wave instruction over a segment of
+// a unit moves 512 contiguous bytes (whole cache lines) instead of 64 bytes of each of 8
+// rows. Element (row, col) of such an array sits at blk16(row, col, NC); NC is a multiple of 32.
+__host__ __device__ constexpr size_t blk16(size_t row, int col, int NC) {
+  return (row >> 3) * (size_t)(8 * NC) + (size_t)(col >> 5) * 256 + (row & 7) * 32 + (size_t)(col & 31);
+}
+constexpr int kBlkSeg = 64;  // u2v (4 bf16) between consecutive segments of a blocked row
 
 // ---------------------------------------------------------------------------
 // prep: one workgroup (256 threads) per (group g, block of prb <= 8 requests).
@@ -554,9 +563,9 @@ __device__ __forceinline__ void unit_load(const StepArgs& a, size_t row, size_t 
 #pragma unroll
         for (int s = 0; s < C::CS; ++s) d.cf[s] = ld_stream(p + 8 * s);
       } else if constexpr (COLD == NSSM_COLD_BF16_SINGLE) {
-        const u2v* p = reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.cold) + row * C::NC) + q;
+        const u2v* p = reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.cold) + blk16(row, 4 * q, C::NC));
 #pragma unroll
-        for (int s = 0; s < C::CS; ++s) d.cb[s] = ld_half(p + 8 * s);
+        for (int s = 0; s < C::CS; ++s) d.cb[s] = ld_stream(p + kBlkSeg * s);
       } else if constexpr (COLD == NSSM_COLD_BF16) {
         ld_words<C::WORDS>(
             reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(a.cold) + row * C::NC + C::CW * q), d.cw);
@@ -730,17 +739,17 @@ __device__ __forceinline__ void cold_store(const StepArgs& a, size_t row, int q,
 #pragma unroll
     for (int s = 0; s < CS; ++s) st_stream(f4{v[s][0], v[s][1], v[s][2], v[s][3]}, p + 8 * s);
   } else if constexpr (COLD == NSSM_COLD_BF16_SINGLE) {
-    u2v* p = reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.cold) + row * NC) + q;
+    u2v* p = reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.cold) + blk16(row, 4 * q, NC));
 #pragma unroll
-    for (int s = 0; s < CS; ++s) st_half(f32x4_to_bf16(v[s][0], v[s][1], v[s][2], v[s][3]), p + 8 * s);
+    for (int s = 0; s < CS; ++s) st_stream(f32x4_to_bf16(v[s][0], v[s][1], v[s][2], v[s][3]), p + kBlkSeg * s);
   } else {
     float w[CS][4];  // the master's values
     if constexpr (COLD == NSSM_COLD_FP8_BF16M) {
-      u2v* pm = reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.master) + row * NC) + q;
+      u2v* pm = reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.master) + blk16(row, 4 * q, NC));
 #pragma unroll
       for (int s = 0; s < CS; ++s) {
         const u2v t = f32x4_to_bf16(v[s][0], v[s][1], v[s][2], v[s][3]);
-        st_half(t, pm + 8 * s);
+        st_stream(t, pm + kBlkSeg * s);
         bf16x4_to_f32(t, w[s]);
       }
     } else {
@@ -801,7 +810,7 @@ __device__ __forceinline__ void unit_compute_flush(const StepArgs& a, size_t sh,
     } else if constexpr (COLD == NSSM_COLD_BF16_SINGLE) {
       bf16x4_to_f32(d.cb[s], t);
     } else if constexpr (C::MASTER16) {
-      bf16x4_to_f32(ld_half(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.master) + row * NC) + q + 8 * s), t);
+      bf16x4_to_f32(ld_stream(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.master) + blk16(row, 4 * q, NC)) + kBlkSeg * s), t);
     } else {  // fp32 master
       const f4 m4 = ld_stream(reinterpret_cast<const f4*>(static_cast<const float*>(a.master) + row * NC) + q + 8 * s);
       t[0] = m4.x; t[1] = m4.y; t[2] = m4.z; t[3] = m4.w;
@@ -1162,7 +1171,7 @@ __global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
             const size_t row = row0 + (tt / NT) * 16 + li;
             const int col = (tt % NT) * 16 + 4 * lk;
             if constexpr (SRC16)
-              old16[i] = ld_half(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(src) + row * NC + col));
+              old16[i] = ld_stream(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(src) + blk16(row, col, NC)));
             else
               old[i] = ld_stream(reinterpret_cast<const f4*>(static_cast<const float*>(src) + row * NC + col));
             if constexpr (COLD == NSSM_COLD_BF16)
@@ -1247,7 +1256,7 @@ __global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
             } else if constexpr (SRC16) {  // bf16 single copy or bf16 master: RNE, and the
               // e4m3 copy is quantized from the rounded values
               const u2v t = f32x4_to_bf16(nv.x, nv.y, nv.z, nv.w);
-              st_half(t, reinterpret_cast<u2v*>(static_cast<uint16_t*>(C::SEG ? a.cold : a.master) + row * NC + col));
+              st_stream(t, reinterpret_cast<u2v*>(static_cast<uint16_t*>(C::SEG ? a.cold : a.master) + blk16(row, col, NC)));
               float r4[4];
               bf16x4_to_f32(t, r4);
               nv = f4{r4[0], r4[1], r4[2], r4[3]};
@@ -1393,7 +1402,7 @@ __global__ void materialize_kernel(StepArgs a, float* __restrict__ S, int K, int
     const bool m16 = kind == NSSM_COLD_BF16_SINGLE || kind == NSSM_COLD_FP8_BF16M;
     const void* cbase = kind == NSSM_COLD_FP32 || kind == NSSM_COLD_BF16_SINGLE ? a.cold : a.master;
     for (int n = 0; n < NC; ++n) {
-      const float snap = m16 ? bf2f(static_cast<const uint16_t*>(cbase)[row * NC + n])
+      const float snap = m16 ? bf2f(static_cast<const uint16_t*>(cbase)[blk16(row, n, NC)])
                              : static_cast<const float*>(cbase)[row * NC + n];
       float v = dtot * snap;
       for (int i = 0; i < nv; ++i) {

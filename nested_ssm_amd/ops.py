@@ -171,6 +171,23 @@ class V4Tier:
     def _field(self, f):
         return self.cold_t if f == "cold" else getattr(self, f)
 
+    def _rows(self, t: Optional[torch.Tensor], blocked: bool) -> Optional[torch.Tensor]:
+        """[slots, H, P, NC] in row order. The single bf16 copy and the bf16 master are
+        stored unit-blocked (8 rows of a unit segment-major: [NC/32][8][32] per unit), which
+        this unpacks (a copy); other arrays are returned as they are."""
+        if t is None or not blocked:
+            return t
+        S, H, P, NC = t.shape
+        return t.reshape(S * H * P // 8, NC // 32, 8, 32).transpose(1, 2).reshape(S, H, P, NC)
+
+    def cold_rows(self) -> Optional[torch.Tensor]:
+        """The cold copy [slots, H, P, NC] in row order."""
+        return self._rows(self.cold_t, self.kind == _lib.COLD_BF16_SINGLE)
+
+    def master_rows(self) -> Optional[torch.Tensor]:
+        """The cold master [slots, H, P, NC] in row order (None without a separate master)."""
+        return self._rows(self.master, self.kind == _lib.COLD_FP8_BF16M)
+
     def nbytes(self) -> int:
         return sum(t.numel() * t.element_size() for t in (self._field(f) for f in TIER_FIELDS) if t is not None)
 

@@ -208,3 +208,25 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "libnssm_hip.so"))
     with pytest.raises(_lib.NssmError, match="no CPU fallback"):
         _lib.lib()
+
+
+@pytest.mark.parametrize("NC", [96, 64, 32])
+def test_blocked_16bit_layout_unpacks_to_row_order(NC):
+    """The single bf16 copy and the bf16 master are stored unit-blocked: element (row, col)
+    at (row // 8) * 8 NC + (col // 32) * 256 + (row % 8) * 32 + col % 32 (include/nssm.h).
+    V4Tier.cold_rows / master_rows unpack that order (checked here on the CPU against the
+    formula; the GPU join test checks the kernels through them)."""
+    from nested_ssm_amd.ops import V4Tier
+
+    S, H, P = 2, 3, 16
+    rows = S * H * P
+    flat = torch.empty(rows * NC, dtype=torch.int64)
+    for r in range(rows):
+        for cidx in range(NC):
+            off = (r // 8) * 8 * NC + (cidx // 32) * 256 + (r % 8) * 32 + cidx % 32
+            flat[off] = r * 1000 + cidx
+    got = V4Tier._rows(None, flat.view(S, H, P, NC), True)
+    want = (torch.arange(rows)[:, None] * 1000 + torch.arange(NC)[None, :]).view(S, H, P, NC)
+    assert torch.equal(got, want)
+    if NC == 32:  # one segment: the blocked order is the row order
+        assert torch.equal(flat.view(S, H, P, NC), want)

@@ -327,7 +327,7 @@ def test_v4_bf16_master_matches_oracle(cold, k, c, P):
     if cold == "bf16":  # the single copy equals the oracle's rounded master up to isolated flips
         # (a flip is one bf16 ulp of the value at that flush and persists in the master,
         # decaying, so it is bounded norm-wise, not relative to the element's value now)
-        got = tier.cold_t.cpu().float()
+        got = tier.cold_rows().cpu().float()
         assert float((got != ref.snap).float().mean()) < 1e-3
         assert_close_flips(got, ref.snap, "bf16 single copy", frac_max=1e-3)
         assert tier.master is None
@@ -502,12 +502,12 @@ def test_join_quantization_is_bit_exact(cold, master):
     Sc = S[..., k:]
     assert torch.equal(tier.hot.cpu().view(torch.int32), S[..., :k].contiguous().view(torch.int32))
     ref_master = Sc.to(torch.bfloat16) if master == "bf16" else Sc
-    if tier.master is not None:
-        assert torch.equal(tier.master.cpu().view(torch.int16 if master == "bf16" else torch.int32),
+    if tier.master is not None:  # in row order (a bf16 master is stored unit-blocked)
+        assert torch.equal(tier.master_rows().cpu().view(torch.int16 if master == "bf16" else torch.int32),
                            ref_master.contiguous().view(torch.int16 if master == "bf16" else torch.int32))
     mv = ref_master.float()
     if cold == "bf16":
-        assert torch.equal(tier.cold_t.cpu().view(torch.int16), mv.to(torch.bfloat16).view(torch.int16))
+        assert torch.equal(tier.cold_rows().cpu().view(torch.int16), mv.to(torch.bfloat16).view(torch.int16))
     else:
         q, sc = oracle.quant_fp8(mv)
         assert torch.equal(tier.scale.cpu().view(torch.int32), sc[..., 0].contiguous().view(torch.int32))
