@@ -33,6 +33,7 @@ namespace {
 
 constexpr int kN = 128;  // d_state handled by these kernels
 constexpr int kMaxC = 64;
+constexpr int kFusedMaxWindow = 32;  // longest window the stream kernel replays itself
 constexpr int kMaxHG = 64;  // heads per group
 constexpr int kMaxUnitsPerWg = 4;  // waves (units) per stream workgroup
 constexpr int kMfmaTiles = 4;  // 16 x 16 flush-contraction tiles a wave keeps in registers
@@ -316,24 +317,39 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
   if constexpr (TIERED) {
     if (a.exact) {
       __syncthreads();  // sRot
-      const int NC = kN - a.K;
-      for (int pi = tid; pi < nreq * c; pi += kPrepThreads) {
-        const int r = pi / c, j = pi - r * c;
+      // 8 lanes per (request, window token): lane k of the group takes columns K + 32 i + 4 k
+      // (float4 each, all loads at once), then a DPP sum over the group's 8 lanes. The loop
+      // bound is uniform over each aligned 8-lane group, so every group's lanes sum together.
+      const int NC = kN - a.K, k8 = tid & 7;
+      for (int it = tid >> 3; it < nreq * c; it += kPrepThreads / 8) {
+        const int r = it / c, j = it - r * c;
         const int sl = sSlot[r], nv = sNvr[r];
-        if (sl < 0 || sl >= a.slots || j > nv) continue;
-        const float* bj = j < nv ? a.ring_b + (((size_t)sl * G + g) * c + (sTr[r] % c - nv + j)) * NC
-                                 : &sRot[r][a.K];
-        const float* cq = &sRot[kPrepReq + r][a.K];
+        const bool live = sl >= 0 && sl < a.slots && j <= nv;
         float acc = 0.f;
-        for (int n = 0; n < NC; n += 4) {
-          const f4 bv = *reinterpret_cast<const f4*>(bj + n);
-          const f4 cv = *reinterpret_cast<const f4*>(cq + n);
-          acc = fmaf(bv.x, cv.x, acc);
-          acc = fmaf(bv.y, cv.y, acc);
-          acc = fmaf(bv.z, cv.z, acc);
-          acc = fmaf(bv.w, cv.w, acc);
+        if (live) {
+          const float* bj = j < nv ? a.ring_b + (((size_t)sl * G + g) * c + (sTr[r] % c - nv + j)) * NC
+                                   : &sRot[r][a.K];
+          const float* cq = &sRot[kPrepReq + r][a.K];
+          f4 bv[kN / 32], cv[kN / 32];
+#pragma unroll
+          for (int i = 0; i < kN / 32; ++i) {
+            if (32 * i < NC) {
+              bv[i] = *reinterpret_cast<const f4*>(bj + 32 * i + 4 * k8);
+              cv[i] = *reinterpret_cast<const f4*>(cq + 32 * i + 4 * k8);
+            }
+          }
+#pragma unroll
+          for (int i = 0; i < kN / 32; ++i) {
+            if (32 * i < NC) {
+              acc = fmaf(bv[i].x, cv[i].x, acc);
+              acc = fmaf(bv[i].y, cv[i].y, acc);
+              acc = fmaf(bv[i].z, cv[i].z, acc);
+              acc = fmaf(bv[i].w, cv[i].w, acc);
+            }
+          }
         }
-        sS[r][j] = acc;
+        acc = sum8(acc);
+        if (live && k8 == 0) sS[r][j] = acc;
       }
       __syncthreads();  // sS
     }
@@ -696,30 +712,61 @@ __device__ __forceinline__ float hot_update(const StepArgs& a, size_t row, int q
 // prep kernel, scale/v4_native_decode.py:98-104. Lane q takes j = q, q + 8, ...; the
 // row's 8 lanes are summed with the rest of the readout. (Issuing these loads with the
 // unit's state loads costs more registers than the latency it hides.)
-__device__ __forceinline__ float corr_partial(const StepArgs& a, const float* __restrict__ hd, size_t sh, size_t rh,
-                                              int p, int q, float xcur) {
+// KU: window tokens per lane at most (the window is at most 8 KU long). The loads and the
+// sum are separate so a kernel with registers to spare issues the loads with its state loads.
+template <int KU>
+struct CorrRaw {
+  float wv[KU], xv[KU];
+};
+template <int KU>
+__device__ __forceinline__ void corr_load(const StepArgs& a, const float* __restrict__ hd, size_t sh, size_t rh,
+                                          int p, int q, CorrRaw<KU>& cr) {
   const int m = (int)hd[HD_M], P = a.P, c = a.c;
+  // window token j sits at ring position pos - (m - 1) + j
   const uint16_t* rx0 = a.ring_x + (sh * c + ((int)hd[HD_POS] - (m - 1))) * P + p;
   const float* cw = Ws(a.ws, a.b, a.H, a.G, c).cw + rh * c;
+#pragma unroll
+  for (int u = 0; u < KU; ++u) {
+    const int j = q + 8 * u;
+    cr.wv[u] = j < m ? cw[j] : 0.f;
+    cr.xv[u] = j < m - 1 ? bf2f(rx0[(size_t)j * P]) : 0.f;
+  }
+}
+template <int KU>
+__device__ __forceinline__ float corr_sum(const float* __restrict__ hd, int q, const CorrRaw<KU>& cr, float xcur) {
+  const int m = (int)hd[HD_M];
   float s = 0.f;
-  for (int j = q; j < m; j += 8) s = fmaf(cw[j], j < m - 1 ? bf2f(rx0[(size_t)j * P]) : xcur, s);
+#pragma unroll
+  for (int u = 0; u < KU; ++u) s = fmaf(cr.wv[u], q + 8 * u < m - 1 ? cr.xv[u] : xcur, s);
   return s;
+}
+template <int KU>
+__device__ __forceinline__ float corr_partial(const StepArgs& a, const float* __restrict__ hd, size_t sh, size_t rh,
+                                              int p, int q, float xcur) {
+  CorrRaw<KU> cr;
+  corr_load<KU>(a, hd, sh, rh, p, q, cr);
+  return corr_sum<KU>(hd, q, cr, xcur);
 }
 
 // One unit of one token: hot columns, and (a head that does not flush at this token)
 // the stale readout of its cold read copy and the ring append of x. A flushing head's
 // cold columns are left to the flush kernel, which adds their readout to y.
-template <int K, int COLD, bool EXACT>
+// PRE: the exact readout's correction loads were issued with the state (cr), else here.
+template <int K, int COLD, bool EXACT, int KU = kMaxC / 8, bool PRE = false>
 __device__ __forceinline__ void unit_compute(const StepArgs& a, size_t sh, size_t rh, int p, int q,
                                              UnitRaw<K, COLD>& d, uint16_t* rx, bool cold, const float* __restrict__ hd,
                                              const float (&Bh)[K / 32][4], const float (&Ch)[K / 32][4],
                                              const float (&Cc)[Cfg<K, COLD>::CSR][4],
-                                             const float (&Cq)[Cfg<K, COLD>::CWR]) {
+                                             const float (&Cq)[Cfg<K, COLD>::CWR],
+                                             const CorrRaw<KU>* cr = nullptr) {
   const size_t row = sh * a.P + p, yrow = rh * a.P + p;
   float part = hot_update<K, COLD>(a, row, q, d, hd, Bh, Ch);
   if constexpr (Cfg<K, COLD>::TIERED) {
     if (cold) part = fmaf(hd[HD_SNAPF], cold_partial<K, COLD>(d, Cc, Cq), part);
-    if constexpr (EXACT) part += corr_partial(a, hd, sh, rh, p, q, d.xp);
+    if constexpr (EXACT) {
+      if constexpr (PRE) part += corr_sum<KU>(hd, q, *cr, d.xp);
+      else part += corr_partial<KU>(a, hd, sh, rh, p, q, d.xp);
+    }
   }
   part = sum8(part);
   if (q == 0) {
@@ -799,7 +846,6 @@ __device__ __forceinline__ void unit_compute_flush(const StepArgs& a, size_t sh,
   const size_t row = sh * a.P + p, yrow = rh * a.P + p;
   float part = hot_update<K, COLD>(a, row, q, d, hd, Bh, Ch);
   part = fmaf(hd[HD_SNAPF], cold_partial<K, COLD>(d, Cc, Cq), part);
-  if constexpr (EXACT) part += corr_partial(a, hd, sh, rh, p, q, d.xp);
   const float dtot = hd[HD_DTOT];
   float nvv[CS][4];
 #pragma unroll
@@ -831,6 +877,9 @@ __device__ __forceinline__ void unit_compute_flush(const StepArgs& a, size_t sh,
     }
   }
   cold_store<COLD, CS>(a, row, q, nvv);
+  // the exact readout's correction, once the replay's registers are free (nothing else
+  // adds to part in between, so the sum is the same)
+  if constexpr (EXACT) part += corr_partial<kFusedMaxWindow / 8>(a, hd, sh, rh, p, q, d.xp);
   part = sum8(part);
   if (q == 0) a.y[yrow] = fmaf(hd[HD_D], d.xp, part);
 }
@@ -915,9 +964,12 @@ __device__ __forceinline__ void unit_body(const StepArgs& a, const float* __rest
   }
   const size_t sh = (size_t)slot * H + h, row = sh * P + p;
   const Ws ws(a.ws, a.b, H, a.G, c);
-  // per-head scalars through the noalias argument (scalar loads), except over fp32 cold
-  const float* __restrict__ hd = (COLD == NSSM_COLD_FP32 && TIERED ? static_cast<const float*>(ws.hd) : hd_ro) +
-                                 rh * HD_STRIDE;
+  // per-head scalars through the noalias argument (scalar loads), except for the stale
+  // readout over fp32 cold (vector loads measured faster there). The exact readout's
+  // buffered-x addresses depend on them, and a vector load in front of those costs every
+  // wave a second dependent memory round trip.
+  constexpr bool kVecHd = COLD == NSSM_COLD_FP32 && TIERED && !EXACT;
+  const float* __restrict__ hd = (kVecHd ? static_cast<const float*>(ws.hd) : hd_ro) + rh * HD_STRIDE;
   const bool flushing = TIERED && hd[HD_FLUSH] != 0.f;  // uniform over the workgroup
   if constexpr (TIERED && GATED) {
     // a head whose cold term the gated readout drops reads no cold columns unless it
@@ -930,6 +982,12 @@ __device__ __forceinline__ void unit_body(const StepArgs& a, const float* __rest
   UnitRaw<K, COLD> d;
   // a flushing head's cold columns are needed here only when the replay is fused
   unit_load<K, COLD>(a, row, rh * P + p, q, d, !FUSED && flushing);
+  // the exact readout's correction: without the fused replay there are registers to issue
+  // its loads now, beside the state's, instead of a second round trip after them
+  constexpr int kCorrU = (FUSED ? kFusedMaxWindow : kMaxC) / 8;
+  constexpr bool kCorrPre = EXACT && !FUSED && TIERED;
+  CorrRaw<kCorrPre ? kCorrU : 1> cr;
+  if constexpr (kCorrPre) corr_load<kCorrU>(a, hd, sh, rh, p, q, cr);
 
   const float* wB = ws.B + ((size_t)bi * a.G + g) * kN;
   const float* wC = ws.C + ((size_t)bi * a.G + g) * kN;
@@ -974,7 +1032,12 @@ __device__ __forceinline__ void unit_body(const StepArgs& a, const float* __rest
   if constexpr (TIERED) {
     if (!flushing) rx = a.ring_x + (sh * c + (int)hd[HD_POS]) * P;
   }
-  unit_compute<K, COLD, EXACT>(a, sh, rh, p, q, d, rx, !flushing, hd, Bh, Ch, Cc, Cq);
+  // the stream kernel replays windows of at most kFusedMaxWindow tokens itself; the exact
+  // readout's correction then covers at most that many
+  if constexpr (kCorrPre)
+    unit_compute<K, COLD, EXACT, kCorrU, true>(a, sh, rh, p, q, d, rx, !flushing, hd, Bh, Ch, Cc, Cq, &cr);
+  else
+    unit_compute<K, COLD, EXACT, kCorrU>(a, sh, rh, p, q, d, rx, !flushing, hd, Bh, Ch, Cc, Cq);
 }
 
 template <int K, int COLD, bool FUSED, bool EXACT>
@@ -1668,7 +1731,7 @@ int flush_chunk(int P, int K, int kind, int c) {
 //   fp32 cold           c = 16  7.82 / 8.28   c = 32  8.58 / 7.94   c = 64 10.46 / 7.88
 //   e4m3, bf16 master   c = 16  5.32 / 6.22   c = 32  5.62 / 5.53   c = 64  8.23 / 5.24
 //   single bf16 copy    c = 16  6.25 / 6.73   c = 32  6.34 / 6.44   c = 64  8.81 / 6.31
-int fuse_max_window(int kind) { return kind == NSSM_COLD_BF16_SINGLE ? 32 : 16; }
+int fuse_max_window(int kind) { return kind == NSSM_COLD_BF16_SINGLE ? kFusedMaxWindow : 16; }
 
 // requests per prep workgroup: one head thread per (request, head)
 int prep_requests(int HG) {
@@ -1691,7 +1754,8 @@ int pick_launch(int P, int K, int c, Launch* out, int kind = NSSM_COLD_FP32) {
   int uw = tiered ? 2 : 1;
   if (g_units_override > 0) uw = g_units_override;
   if (uw > kMaxUnitsPerWg || RG % uw) return NSSM_E_TUNING;
-  const bool fused = tiered && c <= fuse_max_window(kind);
+  // (the fused kernels' exact-readout correction is sized for kFusedMaxWindow tokens)
+  const bool fused = tiered && c <= fuse_max_window(kind) && c <= kFusedMaxWindow;
   const size_t lds = fused ? ((size_t)c * (kN - K) + (size_t)c * uw * 8) * sizeof(float) : 0;
   if (lds > kMaxLds || (tiered && !fused && flush_chunk(P, K, kind, c) < 4)) return NSSM_E_DIMS;
   out->uw = uw;
