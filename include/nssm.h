@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define NSSM_ABI_VERSION 8
+#define NSSM_ABI_VERSION 9
 
 /* error codes */
 #define NSSM_OK 0
@@ -103,7 +103,7 @@ typedef struct nssm_step_inputs {
  * owned by the caller). Layouts, row-major unless noted:
  *   hot      fp32 [slots][H][P][K]
  *   cold     [slots][H][P][NC]   fp32 | bf16 | e4m3fn bytes, by cold_kind
- *                                (BF16_SINGLE: unit-blocked, below)
+ *                                (bf16: unit-blocked, below)
  *   scale    fp32 [slots][H][P]         (FP8 and FP8_BF16M, else NULL)
  *   master   [slots][H][P][NC]          fp32 for BF16 / FP8, bf16 for FP8_BF16M
  *                                       (unit-blocked, below), else NULL
@@ -115,7 +115,7 @@ typedef struct nssm_step_inputs {
  *   glog     fp32 [slots][H]            log-decay since the snapshot, one token lagged
  * All heads of a slot carry equal t and nv. hot, cold, master and ring_b are
  * 16-byte aligned, ring_x 8-byte aligned.
- * Unit-blocked (the single bf16 copy, the bf16 master): with row = (slot H + h) P + p,
+ * Unit-blocked (the bf16 read copies, the bf16 master): with row = (slot H + h) P + p,
  * element (row, col) sits at (row / 8) 8 NC + (col / 32) 256 + (row % 8) 32 + col % 32:
  * the 8 rows of a unit form one block, 32-column segment by segment, so a wave moves
  * whole cache lines of it (the sizes are those of [slots][H][P][NC]). */

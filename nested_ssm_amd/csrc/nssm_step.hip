@@ -147,21 +147,8 @@ __device__ __forceinline__ void st_stream(T v, T* p) {
   if constexpr (NSSM_NT_STORE) __builtin_nontemporal_store(v, p);
   else *p = v;
 }
-// 16-bit arrays in the segment mapping (8 bytes per lane, half a cache line per row per
-// wave instruction): plain accesses, so the two halves of a line meet in L2
-#ifndef NSSM_NT_HALF
-#define NSSM_NT_HALF 0
-#endif
-__device__ __forceinline__ u2v ld_half(const u2v* p) {
-  if constexpr (NSSM_NT_HALF) return __builtin_nontemporal_load(p);
-  else return *p;
-}
-__device__ __forceinline__ void st_half(u2v v, u2v* p) {
-  if constexpr (NSSM_NT_HALF) __builtin_nontemporal_store(v, p);
-  else *p = v;
-}
-// The single bf16 copy and the bf16 master are kept unit-blocked: the 8 rows of a unit
-// (rows 8u .. 8u+7 of the [slots][H][P] row order) are one block of 8 NC elements,
+// The 16-bit arrays (the bf16 read copies and the bf16 master) are kept unit-blocked: the
+// 8 rows of a unit (rows 8u .. 8u+7 of the [slots][H][P] row order) are one block of 8 NC elements,
 // segment-major ([NC / 32][8 rows][32 columns]), so one wave instruction over a segment of
 // a unit moves 512 contiguous bytes (whole cache lines) instead of 64 bytes of each of 8
 // rows. Element (row, col) of such an array sits at blk16(row, col, NC); NC is a multiple of 32.
@@ -492,11 +479,12 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
 //   kind            read copy (mapping)          master
 //   FP32            fp32 (segment)               the read copy
 //   BF16_SINGLE     bf16 (segment)               the read copy
-//   BF16            bf16 (contiguous)            fp32
+//   BF16            bf16 (segment)               fp32
 //   FP8             e4m3 + row scale (contig.)   fp32
 //   FP8_BF16M       e4m3 + row scale (contig.)   bf16
 // A single copy is read in the segment mapping so a flushing head replays onto the
-// values it read; a master beside a read copy is loaded only by flushing heads.
+// values it read; a master beside a read copy is loaded only by flushing heads. The 16-bit
+// copies are unit-blocked (blk16); the e4m3 copies row-major, read contiguously.
 template <int K, int COLD>
 struct Cfg {
   static constexpr int HS = K / 32;
@@ -505,12 +493,14 @@ struct Cfg {
   static constexpr int CS = TIERED ? NC / 32 : 0;                // cold segments per row
   static constexpr int CSR = CS > 0 ? CS : 1;
   static constexpr bool E4M3 = COLD == NSSM_COLD_FP8 || COLD == NSSM_COLD_FP8_BF16M;  // e4m3 read copy
-  static constexpr bool SEG = COLD == NSSM_COLD_FP32 || COLD == NSSM_COLD_BF16_SINGLE;  // segment read
-  static constexpr bool CONTIG = COLD == NSSM_COLD_BF16 || E4M3;                        // contiguous read
+  static constexpr bool SEG = COLD == NSSM_COLD_FP32 || COLD == NSSM_COLD_BF16_SINGLE;  // single copy
+  static constexpr bool B16 = COLD == NSSM_COLD_BF16 || COLD == NSSM_COLD_BF16_SINGLE;  // bf16 read copy
+  static constexpr bool SEGREAD = SEG || B16;                                           // segment read
+  static constexpr bool CONTIG = E4M3;                                                  // contiguous read
   static constexpr bool MASTER32 = COLD == NSSM_COLD_BF16 || COLD == NSSM_COLD_FP8;    // fp32 master
   static constexpr bool MASTER16 = COLD == NSSM_COLD_FP8_BF16M;                        // bf16 master
   static constexpr int CW = NC / 8;                              // contiguous columns per lane
-  static constexpr int WORDS = E4M3 ? CW / 4 : COLD == NSSM_COLD_BF16 ? CW / 2 : 0;
+  static constexpr int WORDS = E4M3 ? CW / 4 : 0;
   static constexpr int WR = WORDS > 0 ? WORDS : 1;
   static constexpr int CWR = CONTIG ? CW : 1;
   static constexpr int NT = NC / 16;                             // 16-column tiles of a row
@@ -558,8 +548,8 @@ struct UnitRaw {
   using C = Cfg<K, COLD>;
   f4 hv[C::HS];
   f4 cf[COLD == NSSM_COLD_FP32 ? C::CSR : 1];               // fp32 cold copy, segment mapping
-  u2v cb[COLD == NSSM_COLD_BF16_SINGLE ? C::CSR : 1];       // single bf16 copy, segment mapping
-  uint32_t cw[C::WR];                                        // bf16 / e4m3 read copy, contiguous mapping
+  u2v cb[C::B16 ? C::CSR : 1];                              // bf16 read copy, segment mapping
+  uint32_t cw[C::WR];                                        // e4m3 read copy, contiguous mapping
   float sc;                                     // e4m3 row scale
   float xp;
   uint16_t xraw;
@@ -578,13 +568,10 @@ __device__ __forceinline__ void unit_load(const StepArgs& a, size_t row, size_t 
         const f4* p = reinterpret_cast<const f4*>(static_cast<const float*>(a.cold) + row * C::NC) + q;
 #pragma unroll
         for (int s = 0; s < C::CS; ++s) d.cf[s] = ld_stream(p + 8 * s);
-      } else if constexpr (COLD == NSSM_COLD_BF16_SINGLE) {
+      } else if constexpr (C::B16) {
         const u2v* p = reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.cold) + blk16(row, 4 * q, C::NC));
 #pragma unroll
         for (int s = 0; s < C::CS; ++s) d.cb[s] = ld_stream(p + kBlkSeg * s);
-      } else if constexpr (COLD == NSSM_COLD_BF16) {
-        ld_words<C::WORDS>(
-            reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(a.cold) + row * C::NC + C::CW * q), d.cw);
       } else {
         ld_words<C::WORDS>(
             reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(a.cold) + row * C::NC + C::CW * q), d.cw);
@@ -653,19 +640,13 @@ __device__ __forceinline__ float cold_partial(const UnitRaw<K, COLD>& d, const f
       pc = fmaf(d.cf[s].z, Cc[s][2], pc);
       pc = fmaf(d.cf[s].w, Cc[s][3], pc);
     }
-  } else if constexpr (COLD == NSSM_COLD_BF16_SINGLE) {
+  } else if constexpr (C::B16) {
 #pragma unroll
     for (int s = 0; s < C::CS; ++s) {
       float v[4];
       bf16x4_to_f32(d.cb[s], v);
 #pragma unroll
       for (int e = 0; e < 4; ++e) pc = fmaf(v[e], Cc[s][e], pc);
-    }
-  } else if constexpr (COLD == NSSM_COLD_BF16) {
-#pragma unroll
-    for (int i = 0; i < C::WORDS; ++i) {
-      pc = fmaf(__uint_as_float(d.cw[i] << 16), Cq[2 * i], pc);
-      pc = fmaf(__uint_as_float(d.cw[i] & 0xffff0000u), Cq[2 * i + 1], pc);
     }
   } else if constexpr (C::E4M3) {
 #pragma unroll
@@ -809,9 +790,9 @@ __device__ __forceinline__ void cold_store(const StepArgs& a, size_t row, int q,
       }
     }
     if constexpr (COLD == NSSM_COLD_BF16) {
-      u2v* p = reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.cold) + row * NC) + q;
+      u2v* p = reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.cold) + blk16(row, 4 * q, NC));
 #pragma unroll
-      for (int s = 0; s < CS; ++s) st_half(f32x4_to_bf16(w[s][0], w[s][1], w[s][2], w[s][3]), p + 8 * s);
+      for (int s = 0; s < CS; ++s) st_stream(f32x4_to_bf16(w[s][0], w[s][1], w[s][2], w[s][3]), p + kBlkSeg * s);
     } else {  // e4m3 with the per-row amax scale of scale/vllm_v4_patch.py:106-111
       float am = 0.f;
 #pragma unroll
@@ -1001,7 +982,7 @@ __device__ __forceinline__ void unit_body(const StepArgs& a, const float* __rest
   }
 #pragma unroll
   for (int s = 0; s < CSR; ++s) {
-    if constexpr (C::SEG && CS > 0) {
+    if constexpr (C::SEGREAD && CS > 0) {
       const f4 tc = *reinterpret_cast<const f4*>(wC + K + 32 * s + 4 * q);
       Cc[s][0] = tc.x; Cc[s][1] = tc.y; Cc[s][2] = tc.z; Cc[s][3] = tc.w;
     } else {
@@ -1238,7 +1219,7 @@ __global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
             else
               old[i] = ld_stream(reinterpret_cast<const f4*>(static_cast<const float*>(src) + row * NC + col));
             if constexpr (COLD == NSSM_COLD_BF16)
-              rb16[i] = ld_half(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.cold) + row * NC + col));
+              rb16[i] = ld_stream(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.cold) + blk16(row, col, NC)));
             if constexpr (C::E4M3) {
               r8[i] = ld_stream(reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(a.cold) + row * NC + col));
               rsc[i] = a.scale[row];
@@ -1328,8 +1309,8 @@ __global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
             }
             acc[i] = nv;
             if constexpr (COLD == NSSM_COLD_BF16)
-              st_half(f32x4_to_bf16(nv.x, nv.y, nv.z, nv.w),
-                      reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.cold) + row * NC + col));
+              st_stream(f32x4_to_bf16(nv.x, nv.y, nv.z, nv.w),
+                        reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.cold) + blk16(row, col, NC)));
             if (lk == 0) sPart[p * NT + nt] = pc * rscale;
             if constexpr (C::E4M3) {
               float am = fmaxf(fmaxf(fabsf(nv.x), fabsf(nv.y)), fmaxf(fabsf(nv.z), fabsf(nv.w)));

@@ -172,7 +172,7 @@ class V4Tier:
         return self.cold_t if f == "cold" else getattr(self, f)
 
     def _rows(self, t: Optional[torch.Tensor], blocked: bool) -> Optional[torch.Tensor]:
-        """[slots, H, P, NC] in row order. The single bf16 copy and the bf16 master are
+        """[slots, H, P, NC] in row order. The bf16 read copies and the bf16 master are
         stored unit-blocked (8 rows of a unit segment-major: [NC/32][8][32] per unit), which
         this unpacks (a copy); other arrays are returned as they are."""
         if t is None or not blocked:
@@ -182,7 +182,7 @@ class V4Tier:
 
     def cold_rows(self) -> Optional[torch.Tensor]:
         """The cold copy [slots, H, P, NC] in row order."""
-        return self._rows(self.cold_t, self.kind == _lib.COLD_BF16_SINGLE)
+        return self._rows(self.cold_t, self.kind in (_lib.COLD_BF16_SINGLE, _lib.COLD_BF16))
 
     def master_rows(self) -> Optional[torch.Tensor]:
         """The cold master [slots, H, P, NC] in row order (None without a separate master)."""

@@ -212,7 +212,7 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
 
 @pytest.mark.parametrize("NC", [96, 64, 32])
 def test_blocked_16bit_layout_unpacks_to_row_order(NC):
-    """The single bf16 copy and the bf16 master are stored unit-blocked: element (row, col)
+    """The bf16 read copies and the bf16 master are stored unit-blocked: element (row, col)
     at (row // 8) * 8 NC + (col // 32) * 256 + (row % 8) * 32 + col % 32 (include/nssm.h).
     V4Tier.cold_rows / master_rows unpack that order (checked here on the CPU against the
     formula; the GPU join test checks the kernels through them)."""

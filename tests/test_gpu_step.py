@@ -117,7 +117,7 @@ def test_v4_low_precision_cold(cold):
     tier, ref, worst = _run_v4(b, H, G, P, k, c, cold, steps=64, seed=77)
     # the read copy after the last flush equals the reference's quantized snapshot
     if cold == "bf16":  # equal up to isolated one-ulp rounding flips (see above)
-        got = tier.cold_t.cpu().float()
+        got = tier.cold_rows().cpu().float()
         assert float((got != ref.snap).float().mean()) < 1e-3
         assert_close32(got, ref.snap, "bf16 read copy", rtol=2.0 ** -7, atol=1e-6)
     else:
