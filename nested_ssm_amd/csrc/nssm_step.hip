@@ -466,10 +466,11 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
 //
 // Lane mappings inside a unit (8 rows p0..p0+7 of one head); lane l, rr = l >> 3, q = l & 7:
 //   segment     columns 32 s + 4 q + e of row p0 + rr (segment s, e = 0..3): hot columns, the
-//               fp32 cold copy and the fp32 master. One dwordx4 per segment moves 8 rows x 128 B
-//               (whole cache lines) per wave instruction.
-//   contiguous  columns CW q .. CW q + CW - 1 (CW = NC / 8) of row p0 + rr: the bf16 / e4m3 read
-//               copies, so a lane's bytes are one contiguous dwordx3 (e4m3, k = 32) load.
+//               fp32 cold copy, the fp32 master (one dwordx4 per segment moves 8 rows x 128 B,
+//               whole cache lines, per wave instruction), the bf16 read copies and the bf16
+//               master (unit-blocked, one dwordx2 per segment: 512 contiguous bytes).
+//   contiguous  columns CW q .. CW q + CW - 1 (CW = NC / 8) of row p0 + rr: the e4m3 read
+//               copies, so a lane's bytes are one contiguous dwordx3 (k = 32) load.
 //   mfma        flush at c >= 16: lane (li = l & 15, lk = l >> 4) of a 16 x 16 tile holds row
 //               p0 + li, columns n0 + 4 lk .. +3: the accumulator layout of v_mfma_f32_16x16x4_f32.
 // Both unit mappings group a row's lanes as 8 consecutive lanes, so a row's dot product is
