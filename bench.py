@@ -230,6 +230,41 @@ def bench_v4(args, layers, inputs, dev):
     return ms_step, ms_launch, ms_ev, tier_gb
 
 
+def bench_deploy(args, layers, inputs, dev, fresh_ms_256):
+    """The v4-c4 storage points beyond the fp32 headline, each against fresh at its own batch
+    size: one bf16 copy at B=256 (the bf16 snapshot master of scale/v4_fused_decode.py:149 and
+    the reference bench's bf16 arm) and e4m3 cold over a bf16 master at B=448 (the fp8
+    deployment point). Same layers, seeds and timing as the headline."""
+    import copy
+
+    points = [("v4 k32 c4 single bf16 copy, B=256", dict(B=256, cold="bf16", master="bf16")),
+              ("v4 k32 c4 e4m3 cold + bf16 master, B=448", dict(B=448, cold="fp8", master="bf16"))]
+    out = {}
+    for name, kw in points:
+        a = copy.copy(args)
+        a.__dict__.update(kw)
+        a.skip = 0.0
+        if a.B == 256:
+            inp, f_ms = inputs, fresh_ms_256
+        else:
+            inp = make_inputs(a.layers, a.B, dev, a.seed + 7)
+            log(f"deploy: fresh B={a.B} ...")
+            f_ms = bench_fresh(a, layers, inp, dev)[0]
+        log(f"deploy: {name} ...")
+        v_step, _, v_ev, _ = bench_v4(a, layers, inp, dev)
+        vb = a.B * bytes_v4_token(a.k, a.c, a.cold, a.master) + bytes_rotation()
+        out[name] = {"value": round(a.B / v_step * 1e3, 1), "unit": "state-op tokens/s",
+                     "ms_per_step": round(v_step, 4), "fresh_ms_per_step": round(f_ms, 4),
+                     "speedup_vs_fresh": round(f_ms / v_step, 3),
+                     "achieved_gbs": round(vb / (v_ev * 1e-3) / 1e9, 1),
+                     "frac": round(vb / (v_ev * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                     "algorithmic_bytes_per_launch": int(vb), "avg_launch_us_events": round(v_ev * 1e3, 2)}
+        log(f"deploy: {name}: {v_step:.3f} ms/step, {out[name]['speedup_vs_fresh']}x fresh")
+        del inp
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_prologue(args, dev):
     """The mixer's conv prologue at the 9B shape (conv_dim 12288 = x 10240 + B, C 2 x 1024,
     width 4, bf16): nssm_conv_update (one launch: state shift, conv, SiLU, x/B/C split)
@@ -369,6 +404,8 @@ def main():
                     help="v4 requests join with random phases (each token flushes about B/c of them)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the host baseline")
+    ap.add_argument("--no-deploy", action="store_true",
+                    help="skip the bf16 / e4m3 storage points measured beside the default headline")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of host work for the baseline")
     ap.add_argument("--only", choices=["v4", "fresh"], default=None, help="profile one path only")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -422,6 +459,12 @@ def main():
         vb = args.B * bytes_v4_token(args.k, args.c, args.cold, args.master, args.skip) + bytes_rotation()
         log(f"v4: {v_step:.3f} ms/step, {args.B / v_step * 1e3:,.0f} tok/s, launch {v_ev * 1e3:.1f} us "
             f"-> {vb / (v_ev * 1e-3) / 1e9:,.0f} GB/s (tiers {tier_gb:.1f} GB)")
+
+    deploy = None
+    headline_default = (args.B == 256 and args.c == 4 and args.k == 32 and args.cold == "fp32" and not args.exact
+                        and not args.coldoff and args.qgate <= 0 and not args.ragged and not args.graph)
+    if args.only is None and headline_default and not args.no_deploy:
+        deploy = bench_deploy(args, layers, inputs, dev, res["fresh"][0])
 
     prologue = None
     if args.only is None:
@@ -486,6 +529,8 @@ def main():
         fb = args.B * bytes_fresh_token() + bytes_rotation()
         out["fresh_achieved_gbs"] = round(fb / (res["fresh"][2] * 1e-3) / 1e9, 1)
         out["speedup_v4_vs_fresh"] = round(res["fresh"][0] / res["v4"][0], 3)
+    if deploy is not None:
+        out["deployment_points"] = deploy
     if prologue is not None:
         out["prologue_epilogue"] = prologue
     if not args.no_cpu:
