@@ -95,14 +95,16 @@ def _run(b, k, c, cold, steps, seed, slot_events=None, check_y=True, master="fp3
         assert_close32(tier.hot, S[..., :k], f"hot columns step {step}")
         if check_y:
             Cp = _rotated_C(prm, C)
-            read = _quant_rt(snap) if cold == "fp8" else snap
+            # the read copy: e4m3 of the snapshot, its bf16 rounding (bf16 cold; a no-op over a
+            # bf16 master, whose snapshot is already rounded), or the fp32 snapshot itself
+            read = _quant_rt(snap) if cold == "fp8" else snap.to(torch.bfloat16).float() if cold == "bf16" else snap
             cold_part = torch.einsum("bhpn,bhn->bhp", read, Cp[..., k:]) * torch.exp(glog)[..., None]
             y_ref = yf - torch.einsum("bhpn,bhn->bhp", S[..., k:], Cp[..., k:]) + cold_part
             if cold == "fp8":
                 r = float((y - y_ref).norm() / y_ref.norm())
                 worst = max(worst, r)
                 assert r <= 2e-2, f"fp8 y step {step}: {r:.3g}"
-            elif master == "bf16":
+            elif master == "bf16" or cold == "bf16":
                 worst = max(worst, assert_close_flips(y, y_ref, f"y step {step}"))
             else:
                 assert_close32(y, y_ref, f"y step {step}", rtol=1e-5, atol=2e-5)
@@ -148,6 +150,14 @@ def test_full_size_bf16_single_copy_b256():
     """One bf16 cold copy (the reference bench's bf16 arm) at B=256, k=32, c=4 and c=16."""
     _run(256, 32, 4, "bf16", steps=24, seed=4, master="bf16")
     _run(256, 32, 16, "bf16", steps=40, seed=5, master="bf16")
+
+
+@pytest.mark.parametrize("c", [4, 64])
+def test_full_size_bf16_read_copy_fp32_master_b256(c):
+    """The native adapter's default storage (cold_bf16=1): a bf16 read copy (RNE of the
+    snapshot) beside an exact fp32 master, B=256, k=32, random phases; c=4 replays in the
+    stream kernel, c=64 on the matrix cores. The state stays exact fp32."""
+    _run(256, 32, c, "bf16", steps=24 if c == 4 else 130, seed=6 + c)
 
 
 @pytest.mark.parametrize("c,k", [(8, 32), (16, 32), (64, 32), (8, 64), (16, 64), (64, 64)])
