@@ -374,7 +374,7 @@ def measured_traffic(key):
 def kernel_label(head, args):
     """The launches of one layer-token (the unit the roofline is measured on)."""
     if head == "fresh":
-        return "prep_kernel<false> + unit_kernel<128, fp32> (one layer-token, two launches)"
+        return "prep_kernel<false> + fresh_kernel (one layer-token, two launches)"
     if args.c <= (32 if args.cold == "bf16" and args.master == "bf16" else 16):
         return (f"prep_kernel<true> + unit_kernel<{args.k}, {args.cold}, fused flush> "
                 f"(one layer-token, two launches)")

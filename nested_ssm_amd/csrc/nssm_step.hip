@@ -1020,6 +1020,48 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(unit_w
   unit_body<K, COLD, FUSED, false, true>(a, hd_ro);
 }
 
+// Untiered step (the full fp32 state is the hot tier, K = N): one one-wave workgroup per 2
+// headdim rows of one head, one float4 of state per lane (lane l: row p0 + (l >> 5),
+// columns 4 (l & 31) .. +3); a row's C.h readout is a sum over its 32 lanes (three DPP steps
+// within 8, a row mirror within 16, one swizzle across the two 16-lane halves). In-place RMW
+// at this shape ran 6.73 TB/s in a skeleton over a 1.34 GB buffer, against 6.40 with four
+// float4 per lane (the unit kernel's shape at K = N). Workgroups in request, head, row
+// order. The arithmetic per element is the hot update's.
+__global__ void __launch_bounds__(64) fresh_kernel(StepArgs a, const float* __restrict__ hd_ro) {
+  const int lane = threadIdx.x, cl = lane & 31;
+  const int H = a.H, P = a.P, np = P >> 1;
+  const int pp = blockIdx.x % np, hb = blockIdx.x / np, h = hb % H, bi = hb / H, g = h / a.HG;
+  const int p = 2 * pp + (lane >> 5);
+  const int slot = a.slot_ids ? a.slot_ids[bi] : bi;
+  const size_t rh = (size_t)bi * H + h;
+  if (slot < 0 || slot >= a.slots) {  // uniform over the workgroup
+    if (cl == 0) a.y[rh * P + p] = __builtin_nanf("");
+    return;
+  }
+  f4* sp = reinterpret_cast<f4*>(a.hot + (((size_t)slot * H + h) * P + p) * kN) + cl;
+  f4 v = ld_stream(sp);
+  const float* __restrict__ hd = hd_ro + rh * HD_STRIDE;
+  const Ws ws(a.ws, a.b, H, a.G, 0);
+  const size_t pair = (size_t)bi * a.G + g;
+  const f4 bv = *reinterpret_cast<const f4*>(ws.B + pair * kN + 4 * cl);
+  const f4 cv = *reinterpret_cast<const f4*>(ws.C + pair * kN + 4 * cl);
+  const float xp = bf2f(a.x[rh * P + p]);
+  const float uu = hd[HD_DT] * xp, dec = hd[HD_DECAY];
+  v.x = fmaf(v.x, dec, uu * bv.x);
+  v.y = fmaf(v.y, dec, uu * bv.y);
+  v.z = fmaf(v.z, dec, uu * bv.z);
+  v.w = fmaf(v.w, dec, uu * bv.w);
+  float part = v.x * cv.x;
+  part = fmaf(v.y, cv.y, part);
+  part = fmaf(v.z, cv.z, part);
+  part = fmaf(v.w, cv.w, part);
+  st_stream(v, sp);
+  part = sum8(part);
+  part += dpp<0x140>(part);       // row_mirror: lane i <-> 15 - i, the other 8 of the 16
+  part += __shfl_xor(part, 16);   // the row's other 16 lanes
+  if (cl == 0) a.y[rh * P + p] = fmaf(hd[HD_D], xp, part);
+}
+
 // ---------------------------------------------------------------------------
 // flush: the cold tier of every (request, head) whose phase wraps at this token.
 // Per item:
@@ -1816,6 +1858,8 @@ int launch_pair(const StepArgs& a, const Launch& L, hipStream_t st) {
     if (grid < a.HG) grid = a.HG;  // the kernel's listing needs grid >= HG (items >= HG)
     hipLaunchKernelGGL((flush_kernel<K, COLD>), dim3((unsigned)grid), dim3(kFlushWaves * 64),
                        flush_lds_bytes(a.P, K, COLD, a.fch), st, a);
+  } else if constexpr (K == kN) {  // untiered
+    hipLaunchKernelGGL(fresh_kernel, dim3((unsigned)((size_t)a.b * a.H * (a.P / 2))), dim3(64), 0, st, a, hd_ro);
   } else {
     hipLaunchKernelGGL((unit_kernel<K, COLD, false, false>), ugrid, ublock, 0, st, a, hd_ro);
   }
