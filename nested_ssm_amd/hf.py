@@ -5,9 +5,12 @@ A patched NemotronHMamba2Mixer runs prefill through the stock transformers
 forward, then captures the state into a V4Tier (join); every single-token
 decode call then runs
 
-    prologue  in_proj, causal conv1d update + SiLU      (stock torch ops)
-    state op  nssm_v4_step / nssm_fresh_step            (HIP, libnssm_hip.so)
-    epilogue  gated RMSNorm, out_proj                   (stock torch ops)
+    prologue  in_proj (torch GEMM); causal conv1d update + SiLU + x/B/C split
+              (nssm_conv_update; transformers' own functions under a padding mask)
+    state op  nssm_v4_step / _exact / _gated, or nssm_fresh_step (pb >= N)
+    epilogue  gated RMSNorm (nssm_gated_rmsnorm), out_proj (torch GEMM)
+
+all HIP launches in libnssm_hip.so.
 
 Rotation: the installed transformers (5.15) mixer never calls `self.act`, so a
 rotation wrapper on `act` (ActRotMask, scale/nemotron_retrofit.py:15-56) would
