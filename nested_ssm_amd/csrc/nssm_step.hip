@@ -1911,6 +1911,83 @@ int v4_step(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step
   return NSSM_E_DIMS;
 }
 
+
+// Width 4, four consecutive channels per thread (dims, strides and pointers 4-channel
+// aligned, as at the 9B shape): the 16 state values and 16 weights move as whole vectors,
+// the input as one 8 / 16-byte load and the output as one 8-byte store, so a wave
+// instruction carries 512 B of x / B / C instead of 128. Per channel the arithmetic is
+// conv_update_kernel's, in the same order.
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+template <int DT>
+__global__ void __launch_bounds__(256) conv_update4_kernel(ConvArgs a) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // 4-channel group
+  const int dq = a.dim >> 2;
+  if (i >= (int64_t)a.b * dq) return;
+  const int r = (int)(i / dq), ch0 = 4 * (int)(i - (int64_t)r * dq);
+  const size_t so = ((size_t)r * a.dim + ch0) * 4;  // first of the group's 16 state values
+  float s[16], w[16], xin[4];
+  uint32_t xraw[4];
+  if constexpr (DT == 0) {
+    const f4* sp = reinterpret_cast<const f4*>(static_cast<const float*>(a.state) + so);
+    const f4* wp = reinterpret_cast<const f4*>(static_cast<const float*>(a.w) + (size_t)ch0 * 4);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const f4 sv = sp[k], wv = wp[k];
+      s[4 * k] = sv.x; s[4 * k + 1] = sv.y; s[4 * k + 2] = sv.z; s[4 * k + 3] = sv.w;
+      w[4 * k] = wv.x; w[4 * k + 1] = wv.y; w[4 * k + 2] = wv.z; w[4 * k + 3] = wv.w;
+    }
+    const f4 xv = *reinterpret_cast<const f4*>(static_cast<const float*>(a.hbc) + (size_t)r * a.hbc_stride + ch0);
+    xin[0] = xv.x; xin[1] = xv.y; xin[2] = xv.z; xin[3] = xv.w;
+    f4* dp = reinterpret_cast<f4*>(static_cast<float*>(a.state) + so);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) dp[k] = f4{s[4 * k + 1], s[4 * k + 2], s[4 * k + 3], xin[k]};
+  } else {
+    // bf16: state and weights as 8 words of two values each (word j: elements 2j, 2j+1)
+    const u4v* sp = reinterpret_cast<const u4v*>(static_cast<const uint16_t*>(a.state) + so);
+    const u4v* wp = reinterpret_cast<const u4v*>(static_cast<const uint16_t*>(a.w) + (size_t)ch0 * 4);
+    const u4v s0 = sp[0], s1 = sp[1], w0 = wp[0], w1 = wp[1];
+    const uint32_t sw[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    const uint32_t ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      s[2 * j] = __uint_as_float(sw[j] << 16); s[2 * j + 1] = __uint_as_float(sw[j] & 0xffff0000u);
+      w[2 * j] = __uint_as_float(ww[j] << 16); w[2 * j + 1] = __uint_as_float(ww[j] & 0xffff0000u);
+    }
+    const u2v xv = *reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.hbc) + (size_t)r * a.hbc_stride + ch0);
+    xraw[0] = xv.x & 0xffffu; xraw[1] = xv.x >> 16; xraw[2] = xv.y & 0xffffu; xraw[3] = xv.y >> 16;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) xin[k] = __uint_as_float(xraw[k] << 16);
+    // channel k's new row: (s1, s2), (s3, x) of its two words
+    uint32_t nw[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      nw[2 * k] = (sw[2 * k] >> 16) | (sw[2 * k + 1] << 16);
+      nw[2 * k + 1] = (sw[2 * k + 1] >> 16) | (xraw[k] << 16);
+    }
+    u4v* dp = reinterpret_cast<u4v*>(static_cast<uint16_t*>(a.state) + so);
+    dp[0] = u4v{nw[0], nw[1], nw[2], nw[3]};
+    dp[1] = u4v{nw[4], nw[5], nw[6], nw[7]};
+  }
+  uint32_t o[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float acc = a.bias ? ld_dt<DT>(a.bias, ch0 + k) : 0.f;
+    acc = fmaf(s[4 * k + 1], w[4 * k], acc);
+    acc = fmaf(s[4 * k + 2], w[4 * k + 1], acc);
+    acc = fmaf(s[4 * k + 3], w[4 * k + 2], acc);
+    acc = fmaf(xin[k], w[4 * k + 3], acc);
+    float u = round_dt<DT>(acc);
+    u = round_dt<DT>(u / (1.f + expf(-u)));  // SiLU
+    if (a.mask) u = round_dt<DT>(u * a.mask[r]);
+    o[k] = nssm_f32_to_bf16(u);
+  }
+  const u2v ov{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+  uint16_t* dst = ch0 < a.I ? a.x + (size_t)r * a.I + ch0
+                  : ch0 < a.I + a.GN ? a.B + (size_t)r * a.GN + (ch0 - a.I)
+                                     : a.C + (size_t)r * a.GN + (ch0 - a.I - a.GN);
+  *reinterpret_cast<u2v*>(dst) = ov;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -2089,6 +2166,18 @@ int nssm_conv_update(int32_t b, int32_t dim, int32_t width, int32_t dtype, const
   if (dtype != NSSM_DT_F32 && dtype != NSSM_DT_BF16) return NSSM_E_KIND;
   if (b == 0 || dim == 0) return NSSM_OK;
   ConvArgs a{hbc, conv_state, weight, bias, mask, x_out, B_out, C_out, hbc_stride, b, dim, width, I, GN};
+  const bool f32 = dtype == NSSM_DT_F32;
+  const bool vec4 = width == 4 && I % 4 == 0 && GN % 4 == 0 && hbc_stride % 4 == 0 && aligned16(conv_state) &&
+                    aligned16(weight) && (f32 ? aligned16(hbc) : aligned8(hbc)) && aligned8(x_out) &&
+                    aligned8(B_out) && aligned8(C_out);
+  if (vec4) {
+    const unsigned grid4 = (unsigned)(((int64_t)b * (dim / 4) + 255) / 256);
+    if (f32)
+      hipLaunchKernelGGL(conv_update4_kernel<0>, dim3(grid4), dim3(256), 0, (hipStream_t)stream, a);
+    else
+      hipLaunchKernelGGL(conv_update4_kernel<1>, dim3(grid4), dim3(256), 0, (hipStream_t)stream, a);
+    return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
+  }
   const unsigned grid = (unsigned)(((int64_t)b * dim + 255) / 256);
   if (dtype == NSSM_DT_F32)
     hipLaunchKernelGGL(conv_update_kernel<0>, dim3(grid), dim3(256), 0, (hipStream_t)stream, a);
