@@ -269,7 +269,10 @@ def bench_prologue(args, dev):
     """The mixer's conv prologue at the 9B shape (conv_dim 12288 = x 10240 + B, C 2 x 1024,
     width 4, bf16): nssm_conv_update (one launch: state shift, conv, SiLU, x/B/C split)
     vs transformers' causal_conv1d_update + split + bf16 casts (the adapter's path when
-    a padding mask is given). Microseconds per layer-token and GB/s of algorithmic bytes."""
+    a padding mask is given); and the epilogue gated norm. Microseconds per layer-token and
+    GB/s of algorithmic bytes: for the HIP launches the device time (HIP graph replays of 27
+    launches, as one decode step issues them) and the eager time (one Python call per launch,
+    host-bound at this size); the torch paths eagerly, as the reference runs them."""
     from transformers.models.nemotron_h import modeling_nemotron_h as M
 
     from nested_ssm_amd import conv_update
@@ -298,17 +301,24 @@ def bench_prologue(args, dev):
     y = torch.randn(args.B, I, device=dev, generator=g)
     gate = proj[:, :I]
     norm = M.Zamba2RMSNormGated(I, group_size=I // G, eps=1e-5).to(dev, bf)
+    norm_out = torch.empty(args.B, I, device=dev, dtype=bf)
 
     def ours_norm(_):
-        gated_rmsnorm(y, gate, norm.weight, I // G, 1e-5)
+        gated_rmsnorm(y, gate, norm.weight, I // G, 1e-5, out=norm_out)
 
     def stock_norm(_):
         norm(y.to(bf)[:, None], gate[:, None])
 
     n = 200
     res = {}
-    for name, fn in (("nssm_conv_update", ours), ("torch_causal_conv1d_update", stock),
-                     ("nssm_gated_rmsnorm", ours_norm), ("torch_Zamba2RMSNormGated", stock_norm)):
+    for name, fn in (("nssm_conv_update", ours), ("nssm_gated_rmsnorm", ours_norm)):
+        reps = 27
+        replay = graphed(lambda _: [fn(i) for i in range(reps)], 1)
+        ms, _ = timed(replay, n // 4, 5, 1)
+        res[name + "_us"] = round(ms * 1e3 / reps, 2)
+        ms, _ = timed(fn, n, 20, 1)
+        res[name + "_eager_us"] = round(ms * 1e3, 2)
+    for name, fn in (("torch_causal_conv1d_update", stock), ("torch_Zamba2RMSNormGated", stock_norm)):
         ms, _ = timed(fn, n, 20, 1)
         res[name + "_us"] = round(ms * 1e3, 2)
     nbytes = args.B * (dim * 2 + 2 * dim * W * 2 + dim * 2) + dim * W * 2 + dim * 2
@@ -407,7 +417,8 @@ def main():
     ap.add_argument("--no-deploy", action="store_true",
                     help="skip the bf16 / e4m3 storage points measured beside the default headline")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of host work for the baseline")
-    ap.add_argument("--only", choices=["v4", "fresh"], default=None, help="profile one path only")
+    ap.add_argument("--only", choices=["v4", "fresh", "prologue"], default=None,
+                    help="profile one path only (prologue: the conv prologue and epilogue norm)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (5 times), for scaling HBM counters")
     args = ap.parse_args()
@@ -439,6 +450,9 @@ def main():
         log(f"steps rounded up to {args.steps} (a multiple of c, so flushes are counted evenly)")
 
     dev = "cuda"
+    if args.only == "prologue":
+        print(json.dumps({"prologue_epilogue": bench_prologue(args, dev)}), flush=True)
+        return
     log(f"device {torch.cuda.get_device_name(0)}; B={args.B} L={args.layers} k={args.k} c={args.c} cold={args.cold}")
     layers = make_layers(args.layers, dev, args.seed)
     inputs = make_inputs(args.layers, args.B, dev, args.seed + 7)

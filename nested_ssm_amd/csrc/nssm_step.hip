@@ -1676,6 +1676,72 @@ __global__ void __launch_bounds__(kNormThreads) gated_norm_kernel(NormArgs a) {
   }
 }
 
+// One wave per (request, group) when gs is a multiple of 256 channels and the rows are
+// 4-channel aligned: each lane takes 4 consecutive channels per 256 (y as 16 bytes, gate,
+// weight and out as 8 bytes in bf16), issues the weight loads with the others, and the sum
+// of squares is reduced inside the wave (no LDS, no barrier). Per channel the arithmetic
+// is gated_norm_kernel's; the sum runs in another order.
+constexpr int kNormWavePer = 8;  // 256-channel blocks per lane: gs <= 2048
+
+template <int DT>
+__device__ __forceinline__ void ld4_dt(const void* p, size_t i, float (&v)[4]) {
+  if constexpr (DT == 0) {
+    const f4 t = *reinterpret_cast<const f4*>(static_cast<const float*>(p) + i);
+    v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+  } else {
+    const u2v t = *reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(p) + i);
+    v[0] = __uint_as_float(t.x << 16); v[1] = __uint_as_float(t.x & 0xffff0000u);
+    v[2] = __uint_as_float(t.y << 16); v[3] = __uint_as_float(t.y & 0xffff0000u);
+  }
+}
+
+template <int DT>
+__global__ void __launch_bounds__(64) gated_norm_wave_kernel(NormArgs a) {
+  const int ng = a.I / a.gs, nb = a.gs >> 8;
+  const int r = blockIdx.x / ng, grp = blockIdx.x - r * ng;
+  const int lane = threadIdx.x;
+  const size_t c0 = (size_t)grp * a.gs + 4 * lane;
+  float v[kNormWavePer][4], w[kNormWavePer][4];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < kNormWavePer; ++k) {
+    if (k < nb) {
+      const size_t c = c0 + 256 * k;
+      float g[4];
+      const f4 yv = *reinterpret_cast<const f4*>(a.y + (size_t)r * a.I + c);
+      ld4_dt<DT>(a.gate, (size_t)r * a.gate_stride + c, g);
+      ld4_dt<DT>(a.w, c, w[k]);
+      const float ys[4] = {yv.x, yv.y, yv.z, yv.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[k][e] = round_dt<DT>(ys[e]) * (g[e] / (1.f + expf(-g[e])));  // y * silu(gate), fp32
+        ss = fmaf(v[k][e], v[k][e], ss);
+      }
+    }
+  }
+  ss += dpp<0xB1>(ss);
+  ss += dpp<0x4E>(ss);
+  ss += dpp<0x141>(ss);
+  ss += __shfl_xor(ss, 8);
+  ss += __shfl_xor(ss, 16);
+  ss += __shfl_xor(ss, 32);
+  const float rs = 1.f / sqrtf(ss / (float)a.gs + a.eps);
+#pragma unroll
+  for (int k = 0; k < kNormWavePer; ++k) {
+    if (k < nb) {
+      const size_t o = (size_t)r * a.I + c0 + 256 * k;
+      float t[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) t[e] = w[k][e] * round_dt<DT>(v[k][e] * rs);
+      if constexpr (DT == 0) *reinterpret_cast<f4*>(static_cast<float*>(a.out) + o) = f4{t[0], t[1], t[2], t[3]};
+      else
+        *reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.out) + o) =
+            u2v{nssm_f32_to_bf16(t[0]) | ((uint32_t)nssm_f32_to_bf16(t[1]) << 16),
+                nssm_f32_to_bf16(t[2]) | ((uint32_t)nssm_f32_to_bf16(t[3]) << 16)};
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // host side
 int g_units_override = 0;  // units (waves) per stream workgroup, 0 = automatic
@@ -2194,6 +2260,16 @@ int nssm_gated_rmsnorm(int32_t b, int32_t I, int32_t gs, int32_t dtype, const fl
   if (b == 0) return NSSM_OK;
   NormArgs a{y, gate, weight, out, gate_stride, I, gs, eps};
   const dim3 grid((unsigned)b * (unsigned)(I / gs));
+  // the wave kernel's 4-channel accesses: 16 bytes of y, 4 elements of the model dtype
+  const uintptr_t va = dtype == NSSM_DT_F32 ? 15u : 7u;
+  if (gs % 256 == 0 && gs / 256 <= kNormWavePer && gate_stride % 4 == 0 && aligned16(y) &&
+      !((uintptr_t)gate & va) && !((uintptr_t)weight & va) && !((uintptr_t)out & va)) {
+    if (dtype == NSSM_DT_F32)
+      hipLaunchKernelGGL(gated_norm_wave_kernel<0>, grid, dim3(64), 0, (hipStream_t)stream, a);
+    else
+      hipLaunchKernelGGL(gated_norm_wave_kernel<1>, grid, dim3(64), 0, (hipStream_t)stream, a);
+    return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
+  }
   if (dtype == NSSM_DT_F32)
     hipLaunchKernelGGL(gated_norm_kernel<0>, grid, dim3(kNormThreads), 0, (hipStream_t)stream, a);
   else

@@ -37,21 +37,26 @@ def test_conv_update_matches_oracle(dtype, b, I, gn, W, with_bias, with_mask):
     assert float((got != want).float().mean()) <= 0.01
 
 
-@pytest.mark.parametrize("dtype,b,I,gs", [(torch.float32, 4, 256, 64), (torch.bfloat16, 4, 256, 64),
-                                          (torch.bfloat16, 32, 10240, 1280), (torch.float32, 3, 2048, 2048)])
-def test_gated_rmsnorm_matches_oracle(dtype, b, I, gs):
+@pytest.mark.parametrize("dtype,b,I,gs,off", [
+    # one workgroup per group (gs not a multiple of 256, or the gate rows not 4-channel aligned)
+    (torch.float32, 4, 256, 64, 8), (torch.bfloat16, 4, 256, 64, 8),
+    (torch.bfloat16, 6, 2560, 1280, 1), (torch.float32, 2, 1024, 512, 2),
+    # one wave per group (the 9B shape: 8 groups of 1280; 1 and 3 blocks of 256 per lane)
+    (torch.bfloat16, 32, 10240, 1280, 8), (torch.float32, 3, 2048, 2048, 8),
+    (torch.float32, 2, 1024, 256, 4), (torch.bfloat16, 5, 1536, 768, 4)])
+def test_gated_rmsnorm_matches_oracle(dtype, b, I, gs, off):
     """The epilogue norm (nssm_gated_rmsnorm) against the oracle (itself equal to
     transformers' Zamba2RMSNormGated): fp32 rtol 1e-5; bf16 up to one-ulp flips in at
     most 1% of the outputs (the group's sum of squares runs in another order)."""
     from nested_ssm_amd import gated_rmsnorm
 
-    gen = torch.Generator().manual_seed(b + I)
+    gen = torch.Generator().manual_seed(b + I + off)
     y = torch.randn(b, I, generator=gen)
     proj = torch.randn(b, I + 40, generator=gen).to(dtype)  # gate is a slice of the in_proj output
-    gate = proj[:, 8:8 + I]
+    gate = proj[:, off:off + I]
     w = torch.randn(I, generator=gen).to(dtype)
     want = oracle.gated_rmsnorm(y, gate, w, gs, 1e-5).float()
-    got = gated_rmsnorm(y.cuda(), proj.cuda()[:, 8:8 + I], w.cuda(), gs, 1e-5).cpu().float()
+    got = gated_rmsnorm(y.cuda(), proj.cuda()[:, off:off + I], w.cuda(), gs, 1e-5).cpu().float()
     if dtype == torch.float32:
         assert torch.allclose(got, want, rtol=1e-5, atol=1e-6)
     else:
