@@ -128,6 +128,26 @@ __device__ __forceinline__ float max8(float v) {
 
 __device__ __forceinline__ float softplus_f(float v) { return v > 20.f ? v : log1pf(expf(v)); }
 
+// Workgroup order of the unit kernel, whose logical order is (request, group, the group's W
+// workgroups). The dispatcher deals workgroup i to XCD i % 8; in the paired order logical
+// (request, group) pair 8m + x goes to XCD x, its W workgroups in a row, so the arrays a
+// workgroup touches in less than whole cache lines (e4m3 row scales, y) and a pair's
+// coefficient rows stay in one XCD's L2, while the eight XCDs still work on one compact
+// window of the state (pairs 8m .. 8m + 7). Identity when the pair count is not a multiple
+// of 8. Bit mask of the cold kinds that use it (NSSM_COLD_FP8, _BF16_SINGLE, _FP8_BF16M),
+// measured on MI355X in ms per 27-layer step: e4m3 over a bf16 master B=448 c=4 10.82 ->
+// 10.59, ragged c=16 8.99 -> 8.82; e4m3 over an fp32 master 12.78 -> 12.68; single bf16 copy
+// B=256 c=32 6.13 -> 6.04, c=4 6.16 -> 6.14. fp32 cold (8.61 -> 8.69, the fused flush
+// slower) and fresh_kernel (11.44 -> 11.46) keep the plain order.
+#ifndef NSSM_XCD_KINDS
+#define NSSM_XCD_KINDS ((1 << NSSM_COLD_FP8) | (1 << NSSM_COLD_BF16_SINGLE) | (1 << NSSM_COLD_FP8_BF16M))
+#endif
+__device__ __forceinline__ int xcd_order(int i, int W, int npairs) {
+  if (npairs & 7) return i;
+  const int k = i >> 3;
+  return ((k / W) * 8 + (i & 7)) * W + k % W;
+}
+
 // Streaming access to the state: non-temporal (the state is touched once per
 // token and is far larger than L2 and the MALL) unless built otherwise.
 #ifndef NSSM_NT_LOAD
@@ -925,7 +945,9 @@ __device__ __forceinline__ void unit_body(const StepArgs& a, const float* __rest
   const int tid = threadIdx.x, lane = tid & 63, q = lane & 7, rr = lane >> 3;
   const int uw = blockDim.x >> 6, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int H = a.H, P = a.P, c = a.c, nub = (P >> 3) / uw;
-  const int ub = blockIdx.x % nub, hb = blockIdx.x / nub, h = hb % H, bi = hb / H, g = h / a.HG;
+  constexpr bool kXcd = (NSSM_XCD_KINDS >> COLD) & 1;
+  const int wg = kXcd ? xcd_order(blockIdx.x, a.HG * nub, a.b * a.G) : (int)blockIdx.x;
+  const int ub = wg % nub, hb = wg / nub, h = hb % H, bi = hb / H, g = h / a.HG;
   const int p0 = ub * uw * 8, p = p0 + wave * 8 + rr;
   const int slot = a.slot_ids ? a.slot_ids[bi] : bi;
   const size_t rh = (size_t)bi * H + h;
