@@ -12,8 +12,11 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("dtype,b,I,gn,W,with_bias,with_mask", [
+    # width 4: four channels per thread where I, gn and the strides are 4-channel aligned;
+    # width 2: one
     (torch.float32, 4, 128, 32, 4, True, False), (torch.bfloat16, 4, 128, 32, 4, True, True),
-    (torch.bfloat16, 64, 10240, 1024, 4, True, False), (torch.float32, 3, 64, 16, 2, False, True)])
+    (torch.bfloat16, 64, 10240, 1024, 4, True, False), (torch.bfloat16, 6, 256, 64, 4, False, True),
+    (torch.bfloat16, 5, 132, 12, 4, True, True), (torch.float32, 3, 64, 16, 2, False, True)])
 def test_conv_update_matches_oracle(dtype, b, I, gn, W, with_bias, with_mask):
     gen = torch.Generator().manual_seed(b + I + W)
     dim = I + 2 * gn
