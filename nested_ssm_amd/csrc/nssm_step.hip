@@ -134,13 +134,21 @@ __device__ __forceinline__ float softplus_f(float v) { return v > 20.f ? v : log
 // workgroup touches in less than whole cache lines (e4m3 row scales, y) and a pair's
 // coefficient rows stay in one XCD's L2, while the eight XCDs still work on one compact
 // window of the state (pairs 8m .. 8m + 7). Identity when the pair count is not a multiple
-// of 8. Bit mask of the cold kinds that use it (NSSM_COLD_FP8, _BF16_SINGLE, _FP8_BF16M),
-// measured on MI355X in ms per 27-layer step: e4m3 over a bf16 master B=448 c=4 10.82 ->
-// 10.59, ragged c=16 8.99 -> 8.82; e4m3 over an fp32 master 12.78 -> 12.68; single bf16 copy
-// B=256 c=32 6.13 -> 6.04, c=4 6.16 -> 6.14. fp32 cold (8.61 -> 8.69, the fused flush
-// slower) and fresh_kernel (11.44 -> 11.46) keep the plain order.
+// of 8. Bit masks of the cold kinds that use it always (NSSM_COLD_FP8, _BF16_SINGLE,
+// _FP8_BF16M) and of those that use it when the flush kernel does the flush (NSSM_COLD_FP32,
+// _BF16), measured on MI355X in ms per 27-layer step: e4m3 over a bf16 master B=448 c=4
+// 10.82 -> 10.59, ragged c=16 8.99 -> 8.82; e4m3 over an fp32 master 12.78 -> 12.68; single
+// bf16 copy B=256 c=32 6.13 -> 6.04, c=4 6.16 -> 6.14; fp32 c=64 7.91 -> 7.86, c=32 7.97 ->
+// 7.92, ragged B=384 c=64 12.18 -> 12.07, exact readout c=64 11.11 -> 10.58; bf16 read copy
+// over an fp32 master c=64 6.09 -> 5.99. Where the stream kernel replays the window itself,
+// fp32 cold (c=4 8.61 -> 8.69, its flush token slower; exact readout c=4 neutral, c=16 -1%)
+// and the bf16 read copy (c=4 8.44 -> 8.50) keep the plain order, as does fresh_kernel
+// (11.44 -> 11.46).
 #ifndef NSSM_XCD_KINDS
 #define NSSM_XCD_KINDS ((1 << NSSM_COLD_FP8) | (1 << NSSM_COLD_BF16_SINGLE) | (1 << NSSM_COLD_FP8_BF16M))
+#endif
+#ifndef NSSM_XCD_SPLIT_KINDS
+#define NSSM_XCD_SPLIT_KINDS ((1 << NSSM_COLD_FP32) | (1 << NSSM_COLD_BF16))
 #endif
 __device__ __forceinline__ int xcd_order(int i, int W, int npairs) {
   if (npairs & 7) return i;
@@ -945,7 +953,7 @@ __device__ __forceinline__ void unit_body(const StepArgs& a, const float* __rest
   const int tid = threadIdx.x, lane = tid & 63, q = lane & 7, rr = lane >> 3;
   const int uw = blockDim.x >> 6, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int H = a.H, P = a.P, c = a.c, nub = (P >> 3) / uw;
-  constexpr bool kXcd = (NSSM_XCD_KINDS >> COLD) & 1;
+  constexpr bool kXcd = ((NSSM_XCD_KINDS >> COLD) & 1) || (!FUSED && ((NSSM_XCD_SPLIT_KINDS >> COLD) & 1));
   const int wg = kXcd ? xcd_order(blockIdx.x, a.HG * nub, a.b * a.G) : (int)blockIdx.x;
   const int ub = wg % nub, hb = wg / nub, h = hb % H, bi = hb / H, g = h / a.HG;
   const int p0 = ub * uw * 8, p = p0 + wave * 8 + rr;
