@@ -8,7 +8,7 @@ The kernels live in libnssm_hip.so (C ABI: include/nssm.h), built in-tree by
 """
 from ._lib import COLD_KINDS, NssmError, lib  # noqa: F401
 from .ops import (  # noqa: F401
-    LayerParams, V4Tier, conv_update, fp8_cold_readout, fresh_step, gated_rmsnorm, rotate, set_launch,
+    LayerParams, V4Tier, conv_update, fp8_cold_readout, fresh_step, gated_rmsnorm, rotate, set_checks, set_launch,
 )
 
 __version__ = "0.1.0"

@@ -258,12 +258,14 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
     Ah = a.A[h];
     Dh = a.D[h];
     if constexpr (TIERED) {
-      // t >= 0 and 0 <= nv < c hold for every tier these kernels write; the
-      // clamps keep ring indexing inside the buffers even for a corrupted phase
+      // t >= 0 and 0 <= nv <= t % c hold for every tier these kernels write (a join
+      // sets nv = 0 at any phase, each token then advances both, a flush zeroes nv);
+      // the clamps keep every ring offset (t % c - nv + j, c - 1 - nv) in [0, c) even
+      // for a tier whose t or nv was written by hand
       if (slot >= 0 && slot < a.slots) {
         const size_t o = (size_t)slot * H + h;
         tt = max(a.t[o], 0);
-        nvv = min(max(a.nv[o], 0), c - 1);
+        nvv = min(max(a.nv[o], 0), tt % c);
         gl = a.glog[o];
       }
     }
@@ -1485,8 +1487,9 @@ __global__ void materialize_kernel(StepArgs a, float* __restrict__ S, int K, int
     return;
   }
   const size_t o = (size_t)slot * a.H + h;
-  const int nv = min(max(a.nv[o], 0), c - 1);
-  const int t0 = max(a.t[o] - nv, 0);  // step count at the snapshot; pending token i sits at ring (t0 + i) % c
+  const int tcur = max(a.t[o], 0);
+  const int nv = min(max(a.nv[o], 0), tcur % c);  // nv <= t % c, as prep clamps it
+  const int t0 = tcur - nv;  // step count at the snapshot; pending token i sits at ring (t0 + i) % c
   const size_t rh = o * c;
   if ((int)threadIdx.x < nv) lg[threadIdx.x] = a.ring_dt[rh + (t0 + threadIdx.x) % c] * a.A[h];
   __syncthreads();

@@ -105,10 +105,15 @@ class V4State(dict):
     """Per-mixer decode state (`m._v4state`). Keys: "tier" (V4Tier or None for
     the untiered path), "params" (LayerParams), "pb", "c". Item "t" reads and
     writes the decode phase kept on the device (callers reset it between
-    prompts, scale/probe_selfspec_policy.py:127-128). Items "qgate_n" and
-    "qgate_kept" (present once a query-gated token has run, as in
-    scale/v4_native_decode.py:153-154) read the gated and kept head counts kept
-    on the device (scale/run_recall_native.py:116-118 reads them with .get)."""
+    prompts, scale/probe_selfspec_policy.py:127-128). Writing it re-captures the
+    tier at the new phase: the exact current state is rebuilt (materialize) and
+    joined again with t = value, so the snapshot, the buffered window and glog
+    restart together (the reference keeps its older snapshot and lets the window
+    grow past c tokens, which a tier holding at most c buffered tokens cannot
+    represent). Items "qgate_n" and "qgate_kept" (present once a query-gated token
+    has run, as in scale/v4_native_decode.py:153-154) read the gated and kept head
+    counts kept on the device (scale/run_recall_native.py:116-118 reads them with
+    .get)."""
 
     def __getitem__(self, key):
         if key == "t":
@@ -134,11 +139,18 @@ class V4State(dict):
 
     def __setitem__(self, key, value):
         if key == "t":
+            t = int(value)
+            if t < 0:
+                raise ValueError(f"_v4state['t'] must be >= 0 (got {t})")
             tier = dict.get(self, "tier")
-            if tier is not None:
-                tier.t.fill_(int(value))
+            if tier is None:
+                dict.__setitem__(self, "t_fresh", t)
+            elif tier.cold == "off":  # no cold tier: the phase only counts tokens
+                tier.t.fill_(t)
             else:
-                dict.__setitem__(self, "t_fresh", int(value))
+                prm = dict.__getitem__(self, "params")
+                phase = torch.full((tier.slots,), t, dtype=torch.int32, device=tier.hot.device)
+                tier.join(prm, tier.materialize(prm), phase=phase)
             return
         dict.__setitem__(self, key, value)
 
@@ -206,8 +218,11 @@ def decode_step(m, hidden_states, cache_params, attention_mask):
         hot_only = not exact and bool(cfg.get("coldoff"))
         tau = 0.0 if exact or hot_only else float(cfg.get("qgate") or 0.0)
         if not hot_only and int(cfg["c"]) != tier.c:
-            raise NotImplementedError(f"window c={cfg['c']} exceeds the kernels' {ops.MAX_WINDOW}: it is "
-                                      "supported with the hot-only readout (coldoff=1) only")
+            if int(cfg["c"]) > ops.MAX_WINDOW:
+                raise NotImplementedError(f"window c={cfg['c']} exceeds the kernels' {ops.MAX_WINDOW}: it is "
+                                          "supported with the hot-only readout (coldoff=1) only")
+            raise NotImplementedError(f"v4cfg['c'] changed from {tier.c} to {cfg['c']} after capture; the "
+                                      "tier's flush window is fixed when the prefill state is captured")
         counts = None
         if tau > 0:
             counts = dict.get(st, "qcounts")

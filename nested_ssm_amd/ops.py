@@ -5,6 +5,7 @@ runs in libnssm_hip.so. Nothing in this module has a CPU path: inputs must be
 CUDA (HIP) tensors and the library must be built.
 """
 import ctypes
+import os
 from dataclasses import dataclass
 from typing import Optional
 
@@ -41,6 +42,29 @@ def step_workspace(b: int, H: int, G: int, c: int, device=None) -> torch.Tensor:
 
 def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
+
+
+# Duplicate slot ids in one call make the kernels' per-slot read-modify-writes race (the
+# tier rows, t / nv / glog and the ring of that slot), silently corrupting its state.
+# Checking needs a host sync (and so cannot run under graph capture): it is off unless
+# set_checks(slot_ids=True) or NSSM_CHECK_SLOTS=1 turns it on.
+_CHECK_SLOTS = os.environ.get("NSSM_CHECK_SLOTS", "0") not in ("", "0")
+
+
+def set_checks(slot_ids: bool = False) -> None:
+    """Turn the host-side check that a call's slot_ids are unique on or off (it
+    synchronises the host with the device on every step, join and materialize)."""
+    global _CHECK_SLOTS
+    _CHECK_SLOTS = bool(slot_ids)
+
+
+def _check_unique(slot_ids: Optional[torch.Tensor], what: str) -> None:
+    if not _CHECK_SLOTS or slot_ids is None:
+        return
+    if slot_ids.is_cuda and torch.cuda.is_current_stream_capturing():
+        return
+    if torch.unique(slot_ids).numel() != slot_ids.numel():
+        raise ValueError(f"{what}: slot_ids must be unique (duplicates race on the same tier rows)")
 
 
 def _need(t: torch.Tensor, name: str, dtype: torch.dtype, shape: tuple):
@@ -115,6 +139,7 @@ def fresh_step(prm: LayerParams, state: torch.Tensor, x, B, C, dt, y: Optional[t
         y = torch.empty(b, prm.H, prm.P, device=x.device, dtype=torch.float32)
     _need(y, "y", torch.float32, (b, prm.H, prm.P))
     pc, ic = prm.c_struct(), _inputs(prm, x, B, C, dt, slot_ids)
+    _check_unique(slot_ids, "fresh_step")
     ws = step_workspace(b, prm.H, prm.G, 0, x.device)
     check(lib().nssm_fresh_step(ctypes.byref(pc), state.data_ptr(), slots, ctypes.byref(ic), y.data_ptr(),
                                 ws.data_ptr(), ws.numel(), _stream()), "nssm_fresh_step")
@@ -203,6 +228,7 @@ class V4Tier:
             _need(slot_ids, "slot_ids", torch.int32, (b,))
         if phase is not None:
             _need(phase, "phase", torch.int32, (b,))
+        _check_unique(slot_ids, "V4Tier.join")
         pc, tc = prm.c_struct(), self.c_struct()
         check(lib().nssm_v4_join(ctypes.byref(pc), ctypes.byref(tc), state.data_ptr(), b, _ptr(slot_ids),
                                  _ptr(phase), _stream()), "nssm_v4_join")
@@ -228,6 +254,7 @@ class V4Tier:
         if counts is not None:
             _need(counts, "counts", torch.int64, (2,))
         pc, ic, tc = prm.c_struct(), _inputs(prm, x, B, C, dt, slot_ids), self.c_struct()
+        _check_unique(slot_ids, "V4Tier.step")
         ws = step_workspace(b, prm.H, prm.G, self.c, x.device)
         args = (ctypes.byref(pc), ctypes.byref(tc), ctypes.byref(ic), y.data_ptr(), ws.data_ptr(), ws.numel())
         if gated:
@@ -247,6 +274,7 @@ class V4Tier:
         _need(out, "out", torch.float32, (b, self.H, self.P, self.N))
         if slot_ids is not None:
             _need(slot_ids, "slot_ids", torch.int32, (b,))
+        _check_unique(slot_ids, "V4Tier.materialize")
         pc, tc = prm.c_struct(), self.c_struct()
         check(lib().nssm_v4_materialize(ctypes.byref(pc), ctypes.byref(tc), out.data_ptr(), b, _ptr(slot_ids),
                                         _stream()), "nssm_v4_materialize")

@@ -50,3 +50,43 @@ def assert_close_flips(got: torch.Tensor, ref: torch.Tensor, what: str, rel=1e-4
     frac = float(((got - ref).abs() > atol + rtol * ref.abs()).float().mean())
     assert frac <= frac_max, f"{what}: {frac:.3%} of elements beyond the fp32 bar"
     return r
+
+
+class Fresh64:
+    """The exact (fp64) fresh trajectory of a state on the GPU, in plain torch: the state the
+    tiers represent, for checks at full size. S <- exp(a) S + (dt x) (x) B', y = S C' + D x with
+    B' = R B, C' = R C per group, dt = softplus(dt_raw + dt_bias) (threshold 20, as torch and the
+    kernels), a = dt A; every operand is the kernels' input (bf16 or fp32) converted exactly to
+    fp64."""
+
+    def __init__(self, prm: LayerParams, S: torch.Tensor):
+        self.H, self.G = prm.H, prm.G
+        self.R = None if prm.R is None else prm.R.double()
+        self.dt_bias, self.A, self.D = prm.dt_bias.double(), prm.A.double(), prm.D.double()
+        self.S = S.double()
+
+    def _rot(self, v: torch.Tensor) -> torch.Tensor:
+        v = v.double()
+        if self.R is not None:
+            v = torch.einsum("bgn,gmn->bgm", v, self.R)
+        return v.repeat_interleave(self.H // self.G, dim=1)
+
+    def step(self, x, B, C, dt_raw, slots=None):
+        """Advance the rows `slots` (all when None); returns (a [b,H], C' [b,H,N], D x [b,H,P])."""
+        d = torch.nn.functional.softplus(dt_raw.double() + self.dt_bias[None, :])
+        a = d * self.A[None, :]
+        Bp, Cp = self._rot(B), self._rot(C)
+        u = (d[..., None] * x.double())[..., None]  # [b,H,P,1]
+        if slots is None:
+            self.S.mul_(torch.exp(a)[..., None, None]).addcmul_(u, Bp[:, :, None, :])
+        else:
+            sl = slots.long()
+            self.S[sl] = self.S[sl] * torch.exp(a)[..., None, None] + u * Bp[:, :, None, :]
+        return a, Cp, x.double() * self.D[None, :, None]
+
+    def readout(self, Cp, cols=None, rows=None):
+        """S[rows][..., cols] . C'[..., cols] (fp64)."""
+        S = self.S if rows is None else self.S[rows.long()]
+        if cols is not None:
+            S, Cp = S[..., cols], Cp[..., cols]
+        return torch.einsum("bhpn,bhn->bhp", S, Cp)

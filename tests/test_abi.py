@@ -230,3 +230,19 @@ def test_blocked_16bit_layout_unpacks_to_row_order(NC):
     assert torch.equal(got, want)
     if NC == 32:  # one segment: the blocked order is the row order
         assert torch.equal(flat.view(S, H, P, NC), want)
+
+
+def test_duplicate_slot_ids_are_refused_when_checked(monkeypatch):
+    """With the slot check on (the test suite turns it on), a call whose slot ids repeat
+    raises before any launch; unique ids and no ids pass; with the check off nothing is
+    checked (the product path does not sync the host for it)."""
+    from nested_ssm_amd import ops
+
+    monkeypatch.setattr(ops, "_CHECK_SLOTS", True)
+    with pytest.raises(ValueError, match="unique"):
+        ops._check_unique(torch.tensor([3, 1, 3], dtype=torch.int32), "V4Tier.step")
+    ops._check_unique(torch.tensor([3, 1, 2], dtype=torch.int32), "V4Tier.step")
+    ops._check_unique(None, "V4Tier.step")
+    ops.set_checks(slot_ids=False)
+    assert ops._CHECK_SLOTS is False
+    ops._check_unique(torch.tensor([3, 3], dtype=torch.int32), "V4Tier.step")

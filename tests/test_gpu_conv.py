@@ -11,16 +11,20 @@ from nested_ssm_amd import conv_update
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("dtype,b,I,gn,W,with_bias,with_mask", [
-    # width 4: four channels per thread where I, gn and the strides are 4-channel aligned;
-    # width 2: one
-    (torch.float32, 4, 128, 32, 4, True, False), (torch.bfloat16, 4, 128, 32, 4, True, True),
-    (torch.bfloat16, 64, 10240, 1024, 4, True, False), (torch.bfloat16, 6, 256, 64, 4, False, True),
-    (torch.bfloat16, 5, 132, 12, 4, True, True), (torch.float32, 3, 64, 16, 2, False, True)])
-def test_conv_update_matches_oracle(dtype, b, I, gn, W, with_bias, with_mask):
+@pytest.mark.parametrize("dtype,b,I,gn,W,with_bias,with_mask,extra", [
+    # width 4: four channels per thread where I, gn, the strides and the hbc slice are
+    # 4-channel aligned; width 2: one
+    (torch.float32, 4, 128, 32, 4, True, False, 24), (torch.bfloat16, 4, 128, 32, 4, True, True, 24),
+    (torch.bfloat16, 64, 10240, 1024, 4, True, False, 24), (torch.bfloat16, 6, 256, 64, 4, False, True, 24),
+    (torch.bfloat16, 5, 132, 12, 4, True, True, 24), (torch.float32, 3, 64, 16, 2, False, True, 24),
+    # width 4 on the one-channel-per-thread kernel: the hbc slice starts one element past a
+    # 4-channel boundary, or I and gn are not multiples of 4
+    (torch.bfloat16, 4, 128, 32, 4, True, True, 1), (torch.float32, 3, 64, 16, 4, True, False, 1),
+    (torch.bfloat16, 5, 130, 10, 4, True, False, 24), (torch.float32, 2, 130, 10, 4, False, True, 24)])
+def test_conv_update_matches_oracle(dtype, b, I, gn, W, with_bias, with_mask, extra):
     gen = torch.Generator().manual_seed(b + I + W)
     dim = I + 2 * gn
-    extra = 24  # hbc is a slice of a wider in_proj output (row stride dim + 2 extra)
+    # hbc is a slice of a wider in_proj output (row stride dim + 2 extra, first channel at extra)
     proj = torch.randn(b, dim + 2 * extra, generator=gen).to(dtype)
     hbc = proj[:, extra:extra + dim]
     st = torch.randn(b, dim, W, generator=gen).to(dtype)

@@ -350,3 +350,45 @@ def test_native_install_coldoff_with_an_unbounded_window(monkeypatch):
     tok = torch.zeros(2, 1, dtype=torch.long, device="cuda")
     with torch.no_grad(), pytest.raises(NotImplementedError, match="coldoff"):
         model(tok, past_key_values=pkv, use_cache=True)
+
+
+@pytest.mark.parametrize("corr,t_new", [(0, 1), (1, 3), (1, 0)])
+def test_phase_write_mid_window_recaptures_the_tier(monkeypatch, corr, t_new):
+    """Writing _v4state["t"] between decode tokens (scale/probe_selfspec_policy.py:127-128)
+    mid-window: the tier is re-captured from its exact current state at the new phase, so
+    the oracle replay re-joins there with its own current state; y at every token (stale or
+    exact readout) and the final state match, and the phase reads back as written."""
+    from nested_ssm_amd import hf
+    from nested_ssm_amd import v4_native_decode as V
+
+    pb, c = 32, 4
+    model = _tiny_model(seed=31)
+    assert V.install(model, pb=pb, c=c, cold_bf16=0, corr=corr) == 2
+    rec = Recorder(monkeypatch)
+    ids = torch.randint(0, 96, (3, 6), generator=torch.Generator().manual_seed(32)).cuda()
+    n_before, n_after = 2, 2 * c + 3
+    with torch.no_grad():
+        out = model(ids, use_cache=True)
+        pkv = out.past_key_values
+        tok = out.logits[:, -1:].argmax(-1)
+        for i in range(n_before + n_after):
+            if i == n_before:
+                for m in hf.mixers(model):
+                    assert m._v4state["t"] == n_before  # mid-window: nv = 2 buffered tokens
+                    m._v4state["t"] = t_new
+                    assert m._v4state["t"] == t_new
+            out = model(tok, past_key_values=pkv, use_cache=True)
+            tok = out.logits[:, -1:].argmax(-1)
+    for m in hf.mixers(model):
+        li = m.layer_idx
+        prm = _oracle_params(m, float(m.time_step_limit[0]))
+        ref = oracle.NativeV4(3, m.num_heads, m.head_dim, N, pb, c, exact=bool(corr))
+        ref.join(torch.arange(3), _rot(rec.states[li], prm.R, m.num_heads))
+        for step, ((x, B, C, dt), y) in enumerate(zip(rec.inputs[li], rec.ys[li])):
+            if step == n_before:
+                ref.join(torch.arange(3), ref.S.clone(), phase=torch.full((3,), t_new))
+            y_ref = ref.step(x, B, C, dt, prm)
+            assert_close32(y, y_ref, f"layer {li} step {step} (corr={corr}, t <- {t_new})")
+        tier = dict.get(m._v4state, "tier")
+        assert_close32(tier.materialize(m._v4state["params"]).cpu(), ref.S, f"layer {li} state")
+        assert m._v4state["t"] == t_new + n_after == int(ref.t[0])
