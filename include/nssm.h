@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define NSSM_ABI_VERSION 9
+#define NSSM_ABI_VERSION 10
 
 /* error codes */
 #define NSSM_OK 0
@@ -58,6 +58,10 @@ extern "C" {
 #define NSSM_E_LAUNCH (-5)      /* the HIP launch reported an error      */
 #define NSSM_E_TUNING (-6)      /* launch override does not fit the dims */
 #define NSSM_E_WORKSPACE (-7)   /* workspace NULL or too small           */
+#define NSSM_E_SCRATCH (-8)     /* the call needs more than NSSM_SCRATCH_BYTES of scratch */
+
+/* Size of the library's fixed per-device scratch array (nssm_v4_step_noalloc). */
+#define NSSM_SCRATCH_BYTES (32u << 20)
 
 /* model dtypes of the conv prologue's tensors */
 #define NSSM_DT_F32 0
@@ -168,6 +172,21 @@ int nssm_fresh_step(const nssm_layer_params* prm, float* state, int32_t slots,
 int nssm_v4_step(const nssm_layer_params* prm, const nssm_tier* tier,
                  const nssm_step_inputs* in, float* y, void* workspace,
                  int64_t workspace_bytes, void* stream);
+
+/* nssm_v4_step for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops and harnesses that forbid hipMalloc). No counterpart in the
+ * reference: the same kernels and results as nssm_v4_step, but the per-call workspace is
+ * the library's own file-scope device array of NSSM_SCRATCH_BYTES (32 MiB), one per GPU,
+ * held until the process ends (its address is looked up once per device, on the first
+ * call made with that device current). The call allocates nothing and returns
+ * NSSM_E_SCRATCH when nssm_step_workspace_bytes(b, H, G, 128, c) exceeds
+ * NSSM_SCRATCH_BYTES (at H = 128, G = 8: up to 1817 requests at c = 4, 711 at c = 32,
+ * 419 at c = 64). Nothing in the scratch needs to start at zero (every word a later
+ * kernel reads is written earlier in the same call). Every call on one GPU shares that
+ * GPU's array: calls that overlap in time on one GPU (different streams, or host threads
+ * enqueueing concurrently on one device) race on it; calls ordered on one stream do not. */
+int nssm_v4_step_noalloc(const nssm_layer_params* prm, const nssm_tier* tier,
+                         const nssm_step_inputs* in, float* y, void* stream);
 
 /* nssm_v4_step with the rank-c exact correction readout instead of the stale
  * one: replaces `_v4_decode` with v4cfg["corr"] = 1 (scale/v4_native_decode.py:81-117).

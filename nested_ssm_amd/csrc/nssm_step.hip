@@ -25,6 +25,9 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "../../include/nssm.h"
 #include "nssm_formats.h"
 
@@ -1805,6 +1808,33 @@ int check_ws(const nssm_layer_params* prm, int b, int c, const void* ws, int64_t
   return NSSM_OK;
 }
 
+// The no-allocation entry point's workspace: one fixed array per GPU (the code object's
+// device global, created with the module on each device and held until the process ends).
+// In host code `scratch` names a host-side stand-in: its device address on the current
+// device comes from hipGetSymbolAddress, looked up once per device and kept in
+// g_scratch_ptr; only that address is ever handed to a kernel.
+static __device__ __align__(256) unsigned char scratch[NSSM_SCRATCH_BYTES];
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the current device, or nullptr when it cannot be found.
+void* scratch_address() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p) return p;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+  if (!p) {
+    void* q = nullptr;
+    if (hipGetSymbolAddress(&q, HIP_SYMBOL(scratch)) != hipSuccess || !q) return nullptr;
+    g_scratch_ptr[dev].store(q, std::memory_order_release);
+    p = q;
+  }
+  return p;
+}
+
 // compute units of the current device (cached per device)
 int cu_count() {
   static int cache[64] = {};
@@ -2104,6 +2134,7 @@ const char* nssm_strerror(int code) {
     case NSSM_E_LAUNCH: return "HIP kernel launch failed";
     case NSSM_E_TUNING: return "launch override does not fit the dimensions";
     case NSSM_E_WORKSPACE: return "workspace missing or smaller than nssm_step_workspace_bytes()";
+    case NSSM_E_SCRATCH: return "the call needs more workspace than the library's fixed scratch array (NSSM_SCRATCH_BYTES) holds";
   }
   return "unknown nssm error";
 }
@@ -2173,6 +2204,20 @@ int nssm_fresh_step(const nssm_layer_params* prm, float* state, int32_t slots, c
 int nssm_v4_step(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step_inputs* in, float* y,
                  void* workspace, int64_t workspace_bytes, void* stream) {
   return v4_step(prm, tier, in, y, workspace, workspace_bytes, stream, 0);
+}
+
+int nssm_v4_step_noalloc(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step_inputs* in, float* y,
+                         void* stream) {
+  // the argument checks of nssm_v4_step first (they touch no device), then the size
+  int rc = check_params(prm);
+  if (rc) return rc;
+  if ((rc = check_inputs(in, y))) return rc;
+  if ((rc = check_tier(tier, true))) return rc;
+  const size_t need = ws_floats(in->b, prm->H, prm->G, tier->c) * sizeof(float);
+  if (need > (size_t)NSSM_SCRATCH_BYTES) return NSSM_E_SCRATCH;
+  void* ws = scratch_address();
+  if (!ws) return NSSM_E_LAUNCH;
+  return v4_step(prm, tier, in, y, ws, (int64_t)NSSM_SCRATCH_BYTES, stream, 0);
 }
 
 int nssm_v4_step_exact(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step_inputs* in, float* y,

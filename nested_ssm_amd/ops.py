@@ -235,7 +235,7 @@ class V4Tier:
 
     def step(self, prm: LayerParams, x, B, C, dt, y: Optional[torch.Tensor] = None,
              slot_ids: Optional[torch.Tensor] = None, exact: bool = False, hot_only: bool = False,
-             qgate: float = 0.0, counts: Optional[torch.Tensor] = None) -> torch.Tensor:
+             qgate: float = 0.0, counts: Optional[torch.Tensor] = None, noalloc: bool = False) -> torch.Tensor:
         """One decode token for b requests (slot_ids: their slots, default 0..b-1).
         exact=True reads the cold tier with the rank-c exact correction (corr=1,
         scale/v4_native_decode.py:81-117) instead of the stale readout. hot_only=True is
@@ -243,11 +243,15 @@ class V4Tier:
         qgate=tau > 0 drops the cold term of the heads whose query puts less than tau of
         its energy on the cold columns (scale/v4_native_decode.py:147-156), and adds the
         gated and kept head counts to counts (int64 [2] on the GPU) when given. The tier
-        evolves the same way in every case."""
+        evolves the same way in every case. noalloc=True runs the stale readout through
+        nssm_v4_step_noalloc, whose workspace is the library's fixed per-GPU scratch array
+        (with y given, the call allocates nothing; calls overlapping on one GPU race)."""
         b = x.shape[0]
         gated = hot_only or qgate > 0
         if exact and gated:
             raise ValueError("exact readout cannot be combined with hot_only or qgate")
+        if noalloc and (exact or gated):
+            raise ValueError("noalloc serves the stale readout only")
         if y is None:
             y = torch.empty(b, prm.H, prm.P, device=x.device, dtype=torch.float32)
         _need(y, "y", torch.float32, (b, prm.H, prm.P))
@@ -255,6 +259,10 @@ class V4Tier:
             _need(counts, "counts", torch.int64, (2,))
         pc, ic, tc = prm.c_struct(), _inputs(prm, x, B, C, dt, slot_ids), self.c_struct()
         _check_unique(slot_ids, "V4Tier.step")
+        if noalloc:
+            check(lib().nssm_v4_step_noalloc(ctypes.byref(pc), ctypes.byref(tc), ctypes.byref(ic), y.data_ptr(),
+                                             _stream()), "nssm_v4_step_noalloc")
+            return y
         ws = step_workspace(b, prm.H, prm.G, self.c, x.device)
         args = (ctypes.byref(pc), ctypes.byref(tc), ctypes.byref(ic), y.data_ptr(), ws.data_ptr(), ws.numel())
         if gated:

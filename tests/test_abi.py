@@ -47,7 +47,7 @@ def test_abi_version_and_codes_match_header():
     assert int(d["NSSM_COLD_FP8_BF16M"]) == _lib.COLD_FP8_BF16M
     assert (int(d["NSSM_DT_F32"]), int(d["NSSM_DT_BF16"])) == (_lib.DT_F32, _lib.DT_BF16)
     for code in ("NSSM_E_NULL", "NSSM_E_DIMS", "NSSM_E_ALIGN", "NSSM_E_KIND", "NSSM_E_LAUNCH", "NSSM_E_TUNING",
-                 "NSSM_E_WORKSPACE"):
+                 "NSSM_E_WORKSPACE", "NSSM_E_SCRATCH"):
         msg = L.nssm_strerror(int(d[code])).decode()
         assert msg and msg != "unknown nssm error"
     assert L.nssm_strerror(0).decode() == "ok"
@@ -246,3 +246,21 @@ def test_duplicate_slot_ids_are_refused_when_checked(monkeypatch):
     ops.set_checks(slot_ids=False)
     assert ops._CHECK_SLOTS is False
     ops._check_unique(torch.tensor([3, 3], dtype=torch.int32), "V4Tier.step")
+
+
+def test_noalloc_step_refuses_calls_beyond_its_scratch():
+    """nssm_v4_step_noalloc checks its arguments as nssm_v4_step does and refuses, before
+    any device call, a call whose workspace would exceed NSSM_SCRATCH_BYTES."""
+    L = _lib.lib()
+    fake = 4096
+    prm = _lib.LayerParams(128, 80, 128, 8, fake, fake, fake, None, 0.0)
+    tier = _lib.Tier(4096, 32, 4, _lib.COLD_FP32, *([fake] * 10))
+    need = lambda b: L.nssm_step_workspace_bytes(b, 128, 8, 128, 4)  # noqa: E731
+    limit = 32 << 20
+    assert need(1817) <= limit < need(1818)
+    big = _lib.StepInputs(1818, fake, fake, fake, fake, None)
+    assert L.nssm_v4_step_noalloc(ctypes.byref(prm), ctypes.byref(tier), ctypes.byref(big), fake, None) == -8
+    assert "scratch" in L.nssm_strerror(-8).decode()
+    assert L.nssm_v4_step_noalloc(None, ctypes.byref(tier), ctypes.byref(big), fake, None) == -1
+    bad = _lib.Tier(4096, 48, 4, _lib.COLD_FP32, *([fake] * 10))
+    assert L.nssm_v4_step_noalloc(ctypes.byref(prm), ctypes.byref(bad), ctypes.byref(big), fake, None) == -2
