@@ -8,8 +8,8 @@
  * or a negative NSSM_E* code (nssm_strerror() names it).
  *
  * Notation: b = requests in a call, H heads, P headdim, N d_state (128),
- * G groups (HG = H/G heads per group), K = k_hot (hot columns, a multiple of
- * 32 below N), NC = N-K cold columns, c = flush period in tokens.
+ * G groups (HG = H/G heads per group), K = k_hot (hot columns: 16, 32, 64 or
+ * 96), NC = N-K cold columns, c = flush period in tokens.
  *
  * Reference interfaces these entry points replace (files of the reference
  * repository omin-Kwon/nested_ssm):
@@ -124,9 +124,10 @@ typedef struct nssm_step_inputs {
  * All heads of a slot carry equal t and nv. hot, cold, master and ring_b are
  * 16-byte aligned, ring_x 8-byte aligned.
  * Unit-blocked (the bf16 read copies, the bf16 master): with row = (slot H + h) P + p,
- * element (row, col) sits at (row / 8) 8 NC + (col / 32) 256 + (row % 8) 32 + col % 32:
- * the 8 rows of a unit form one block, 32-column segment by segment, so a wave moves
- * whole cache lines of it (the sizes are those of [slots][H][P][NC]). */
+ * element (row, col) sits at (row / 8) 8 NC + (col / 32) 256 + (row % 8) w + col % 32,
+ * w = min(32, NC - 32 (col / 32)): the 8 rows of a unit form one block, 32-column segment
+ * by segment (a trailing 16-column segment when NC = 112), so a wave moves whole cache
+ * lines of it (the sizes are those of [slots][H][P][NC]). */
 typedef struct nssm_tier {
   int32_t slots, k_hot, c, cold_kind;
   float* hot;

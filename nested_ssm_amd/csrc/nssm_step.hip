@@ -179,12 +179,15 @@ __device__ __forceinline__ void st_stream(T v, T* p) {
 }
 // The 16-bit arrays (the bf16 read copies and the bf16 master) are kept unit-blocked: the
 // 8 rows of a unit (rows 8u .. 8u+7 of the [slots][H][P] row order) are one block of 8 NC
-// elements, segment-major ([NC / 32][8 rows][32 columns]), so one wave instruction over a
-// segment of a unit moves 512 contiguous bytes (whole cache lines) instead of 64 bytes of
-// each of 8 rows. Element (row, col) of such an array sits at blk16(row, col, NC); NC is a
-// multiple of 32.
+// elements, segment-major ([segment][8 rows][segment width]), so one wave instruction over
+// a segment of a unit moves 512 contiguous bytes (whole cache lines) instead of 64 bytes of
+// each of 8 rows. Segment s covers columns 32 s .. 32 s + w - 1 with w = min(32, NC - 32 s):
+// every segment is 32 columns wide except a trailing 16-column one when NC % 32 == 16
+// (k_hot = 16). Element (row, col) of such an array sits at blk16(row, col, NC); NC is a
+// multiple of 16.
 __host__ __device__ constexpr size_t blk16(size_t row, int col, int NC) {
-  return (row >> 3) * (size_t)(8 * NC) + (size_t)(col >> 5) * 256 + (row & 7) * 32 + (size_t)(col & 31);
+  return (row >> 3) * (size_t)(8 * NC) + (size_t)(col >> 5) * 256 +
+         (row & 7) * (size_t)(NC - (col & ~31) < 32 ? NC - (col & ~31) : 32) + (size_t)(col & 31);
 }
 constexpr int kBlkSeg = 64;  // u2v (4 bf16) between consecutive segments of a blocked row
 
@@ -352,15 +355,15 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
           const float* cq = &sRot[kPrepReq + r][a.K];
           f4 bv[kN / 32], cv[kN / 32];
 #pragma unroll
-          for (int i = 0; i < kN / 32; ++i) {
-            if (32 * i < NC) {
+          for (int i = 0; i < kN / 32; ++i) {  // NC is a multiple of 16: a float4 is inside or past it
+            if (32 * i + 4 * k8 < NC) {
               bv[i] = *reinterpret_cast<const f4*>(bj + 32 * i + 4 * k8);
               cv[i] = *reinterpret_cast<const f4*>(cq + 32 * i + 4 * k8);
             }
           }
 #pragma unroll
           for (int i = 0; i < kN / 32; ++i) {
-            if (32 * i < NC) {
+            if (32 * i + 4 * k8 < NC) {
               acc = fmaf(bv[i].x, cv[i].x, acc);
               acc = fmaf(bv[i].y, cv[i].y, acc);
               acc = fmaf(bv[i].z, cv[i].z, acc);
@@ -383,7 +386,7 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
       if (wave == 0) {
         const int r = lane >> 3, j = lane & 7;
         float ea = 0.f, ec = 0.f;
-        for (int n = 4 * j; n < kN; n += 32) {  // K is a multiple of 32: a float4 is hot or cold
+        for (int n = 4 * j; n < kN; n += 32) {  // K is a multiple of 16: a float4 is hot or cold
           const f4 v = *reinterpret_cast<const f4*>(&sRot[kPrepReq + r][n]);
           const float e = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
           ea += e;
@@ -501,9 +504,14 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
 //   segment     columns 32 s + 4 q + e of row p0 + rr (segment s, e = 0..3): hot columns, the
 //               fp32 cold copy, the fp32 master (one dwordx4 per segment moves 8 rows x 128 B,
 //               whole cache lines, per wave instruction), the bf16 read copies and the bf16
-//               master (unit-blocked, one dwordx2 per segment: 512 contiguous bytes).
+//               master (unit-blocked, one dwordx2 per segment: 512 contiguous bytes). A
+//               16-column half segment (the hot tier and the tail of the cold one at
+//               k_hot = 16) gives lane q columns 2 q, 2 q + 1 of it (one dwordx2 of fp32, one
+//               dword of bf16: 8 rows x 64 B).
 //   contiguous  columns CW q .. CW q + CW - 1 (CW = NC / 8) of row p0 + rr: the e4m3 read
-//               copies, so a lane's bytes are one contiguous dwordx3 (k = 32) load.
+//               copies, so a lane's bytes are one contiguous dwordx3 (k = 32) load. At
+//               k_hot = 16 (CW = 14, lane parts not word aligned) e4m3 is read in the segment
+//               mapping instead (a dword per segment, two bytes of the half segment).
 //   mfma        flush at c >= 16: lane (li = l & 15, lk = l >> 4) of a 16 x 16 tile holds row
 //               p0 + li, columns n0 + 4 lk .. +3: the accumulator layout of v_mfma_f32_16x16x4_f32.
 // Both unit mappings group a row's lanes as 8 consecutive lanes, so a row's dot product is
@@ -521,30 +529,35 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
 // copies are unit-blocked (blk16); the e4m3 copies row-major, read contiguously.
 template <int K, int COLD>
 struct Cfg {
-  static constexpr int HS = K / 32;
+  static constexpr int HS = K / 32;                              // full hot segments
+  static constexpr bool HH = (K % 32) != 0;                      // a hot half segment (K = 16)
+  static constexpr int HSR = HS > 0 ? HS : 1;
   static constexpr int NC = kN - K;
   static constexpr bool TIERED = COLD != NSSM_COLD_NONE && NC > 0;
-  static constexpr int CS = TIERED ? NC / 32 : 0;                // cold segments per row
+  static constexpr int CS = TIERED ? NC / 32 : 0;                // full cold segments per row
+  static constexpr bool CH = TIERED && (NC % 32) != 0;           // a cold half segment (K = 16)
   static constexpr int CSR = CS > 0 ? CS : 1;
   static constexpr bool E4M3 = COLD == NSSM_COLD_FP8 || COLD == NSSM_COLD_FP8_BF16M;  // e4m3 read copy
   static constexpr bool SEG = COLD == NSSM_COLD_FP32 || COLD == NSSM_COLD_BF16_SINGLE;  // single copy
   static constexpr bool B16 = COLD == NSSM_COLD_BF16 || COLD == NSSM_COLD_BF16_SINGLE;  // bf16 read copy
-  static constexpr bool SEGREAD = SEG || B16;                                           // segment read
-  static constexpr bool CONTIG = E4M3;                                                  // contiguous read
+  static constexpr bool CONTIG = E4M3 && !CH;                                           // contiguous e4m3 read
+  static constexpr bool SEG8 = E4M3 && CH;                                              // segment e4m3 read
+  static constexpr bool SEGREAD = SEG || B16 || SEG8;                                   // segment read
   static constexpr bool MASTER32 = COLD == NSSM_COLD_BF16 || COLD == NSSM_COLD_FP8;    // fp32 master
   static constexpr bool MASTER16 = COLD == NSSM_COLD_FP8_BF16M;                        // bf16 master
   static constexpr int CW = NC / 8;                              // contiguous columns per lane
-  static constexpr int WORDS = E4M3 ? CW / 4 : 0;
+  static constexpr int WORDS = CONTIG ? CW / 4 : 0;
   static constexpr int WR = WORDS > 0 ? WORDS : 1;
   static constexpr int CWR = CONTIG ? CW : 1;
   static constexpr int NT = NC / 16;                             // 16-column tiles of a row
 };
 
+typedef float f2 __attribute__((ext_vector_type(2)));
+
 // e4m3fn <-> fp32 on gfx950's conversion instructions (OCP e4m3fn, round to nearest even;
 // bit-identical to nssm_f32_to_e4m3fn / nssm_e4m3fn_to_f32 for the |v| <= 448 range the
 // kernels produce)
 __device__ __forceinline__ void fp8x4_to_f32(uint32_t w, float (&v)[4]) {
-  typedef float f2 __attribute__((ext_vector_type(2)));
   const f2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
   const f2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
   v[0] = lo.x; v[1] = lo.y; v[2] = hi.x; v[3] = hi.y;
@@ -580,14 +593,66 @@ __device__ __forceinline__ void ld_words(const uint32_t* p, uint32_t (&w)[N]) {
 template <int K, int COLD>
 struct UnitRaw {
   using C = Cfg<K, COLD>;
-  f4 hv[C::HS];
+  f4 hv[C::HSR];
+  f2 hh;                                                     // hot half segment
   f4 cf[COLD == NSSM_COLD_FP32 ? C::CSR : 1];               // fp32 cold copy, segment mapping
+  f2 cfh;                                                    // ... its half segment
   u2v cb[C::B16 ? C::CSR : 1];                              // bf16 read copy, segment mapping
+  uint32_t cbh;                                              // ... its half segment (2 x bf16)
   uint32_t cw[C::WR];                                        // e4m3 read copy, contiguous mapping
+  uint32_t c8[C::SEG8 ? C::CSR : 1];                        // e4m3 read copy, segment mapping
+  uint32_t c8h;                                              // ... its half segment (2 bytes)
   float sc;                                     // e4m3 row scale
   float xp;
   uint16_t xraw;
 };
+
+// The rotated coefficients a lane needs for its columns: B', C' of the hot columns and C' of
+// the cold ones, in the mappings the unit reads its state in.
+template <int K, int COLD>
+struct Coef {
+  using C = Cfg<K, COLD>;
+  float Bh[C::HSR][4], Ch[C::HSR][4];  // hot segments
+  float Bhh[2], Chh[2];                // hot half segment
+  float Cc[C::CSR][4], Cch[2];         // cold segments (segment reads) and the cold half segment
+  float Cq[C::CWR];                    // cold columns of the contiguous e4m3 mapping
+};
+
+template <int K, int COLD>
+__device__ __forceinline__ void coef_load(const float* wB, const float* wC, int q, Coef<K, COLD>& k) {
+  using C = Cfg<K, COLD>;
+#pragma unroll
+  for (int s = 0; s < C::HS; ++s) {
+    const f4 tb = *reinterpret_cast<const f4*>(wB + 32 * s + 4 * q);
+    const f4 tc = *reinterpret_cast<const f4*>(wC + 32 * s + 4 * q);
+    k.Bh[s][0] = tb.x; k.Bh[s][1] = tb.y; k.Bh[s][2] = tb.z; k.Bh[s][3] = tb.w;
+    k.Ch[s][0] = tc.x; k.Ch[s][1] = tc.y; k.Ch[s][2] = tc.z; k.Ch[s][3] = tc.w;
+  }
+  if constexpr (C::HH) {
+    const f2 tb = *reinterpret_cast<const f2*>(wB + 32 * C::HS + 2 * q);
+    const f2 tc = *reinterpret_cast<const f2*>(wC + 32 * C::HS + 2 * q);
+    k.Bhh[0] = tb.x; k.Bhh[1] = tb.y;
+    k.Chh[0] = tc.x; k.Chh[1] = tc.y;
+  }
+#pragma unroll
+  for (int s = 0; s < C::CSR; ++s) {
+    if constexpr (C::SEGREAD && C::CS > 0) {
+      const f4 tc = *reinterpret_cast<const f4*>(wC + K + 32 * s + 4 * q);
+      k.Cc[s][0] = tc.x; k.Cc[s][1] = tc.y; k.Cc[s][2] = tc.z; k.Cc[s][3] = tc.w;
+    } else {
+      k.Cc[s][0] = k.Cc[s][1] = k.Cc[s][2] = k.Cc[s][3] = 0.f;
+    }
+  }
+  if constexpr (C::CH) {
+    const f2 tc = *reinterpret_cast<const f2*>(wC + K + 32 * C::CS + 2 * q);
+    k.Cch[0] = tc.x; k.Cch[1] = tc.y;
+  }
+#pragma unroll
+  for (int i = 0; i < C::CWR; ++i) {
+    if constexpr (C::CONTIG) k.Cq[i] = wC[K + C::CW * q + i];
+    else k.Cq[i] = 0.f;
+  }
+}
 
 template <int K, int COLD>
 __device__ __forceinline__ void unit_load(const StepArgs& a, size_t row, size_t xrow, int q, UnitRaw<K, COLD>& d,
@@ -596,16 +661,29 @@ __device__ __forceinline__ void unit_load(const StepArgs& a, size_t row, size_t 
   const f4* hp = reinterpret_cast<const f4*>(a.hot + row * K) + q;
 #pragma unroll
   for (int s = 0; s < C::HS; ++s) d.hv[s] = ld_stream(hp + 8 * s);
+  if constexpr (C::HH) d.hh = ld_stream(reinterpret_cast<const f2*>(a.hot + row * K + 32 * C::HS) + q);
   if constexpr (C::TIERED) {
     if (!hot_only) {
       if constexpr (COLD == NSSM_COLD_FP32) {
-        const f4* p = reinterpret_cast<const f4*>(static_cast<const float*>(a.cold) + row * C::NC) + q;
+        const float* rp = static_cast<const float*>(a.cold) + row * C::NC;
+        const f4* p = reinterpret_cast<const f4*>(rp) + q;
 #pragma unroll
         for (int s = 0; s < C::CS; ++s) d.cf[s] = ld_stream(p + 8 * s);
+        if constexpr (C::CH) d.cfh = ld_stream(reinterpret_cast<const f2*>(rp + 32 * C::CS) + q);
       } else if constexpr (C::B16) {
-        const u2v* p = reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.cold) + blk16(row, 4 * q, C::NC));
+        const uint16_t* base = static_cast<const uint16_t*>(a.cold);
+        const u2v* p = reinterpret_cast<const u2v*>(base + blk16(row, 4 * q, C::NC));
 #pragma unroll
         for (int s = 0; s < C::CS; ++s) d.cb[s] = ld_stream(p + kBlkSeg * s);
+        if constexpr (C::CH)
+          d.cbh = ld_stream(reinterpret_cast<const uint32_t*>(base + blk16(row, 32 * C::CS + 2 * q, C::NC)));
+      } else if constexpr (C::SEG8) {
+        const uint8_t* rp = static_cast<const uint8_t*>(a.cold) + row * C::NC;
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(rp) + q;
+#pragma unroll
+        for (int s = 0; s < C::CS; ++s) d.c8[s] = ld_stream(p + 8 * s);
+        d.c8h = ld_stream(reinterpret_cast<const uint16_t*>(rp + 32 * C::CS) + q);
+        d.sc = a.scale[row];
       } else {
         ld_words<C::WORDS>(
             reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(a.cold) + row * C::NC + C::CW * q), d.cw);
@@ -623,16 +701,19 @@ __device__ __forceinline__ void bf16x4_to_f32(u2v w, float (&v)[4]) {
   v[2] = __uint_as_float(w.y << 16);
   v[3] = __uint_as_float(w.y & 0xffff0000u);
 }
+__device__ __forceinline__ void bf16x2_to_f32(uint32_t w, float (&v)[2]) {
+  v[0] = __uint_as_float(w << 16);
+  v[1] = __uint_as_float(w & 0xffff0000u);
+}
 // RNE to bf16 with gfx950's packed conversion (v_cvt_pk_bf16_f32), bit-identical to
 // nssm_f32_to_bf16 for non-NaN values, subnormals and ties included (checked against
 // torch's cast by the join test); 1-2% faster than the software rounding on the flush paths.
-__device__ __forceinline__ u2v f32x4_to_bf16(float a, float b, float c, float d) {
+__device__ __forceinline__ uint32_t f32x2_to_bf16(float a, float b) {
   typedef __bf16 b2 __attribute__((ext_vector_type(2)));
-  typedef float f2 __attribute__((ext_vector_type(2)));
-  u2v t;
-  t.x = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{a, b}), b2));
-  t.y = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{c, d}), b2));
-  return t;
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{a, b}), b2));
+}
+__device__ __forceinline__ u2v f32x4_to_bf16(float a, float b, float c, float d) {
+  return u2v{f32x2_to_bf16(a, b), f32x2_to_bf16(c, d)};
 }
 
 // w / sc rounded to nearest for sc > 0: one correctly rounded reciprocal per row, then
@@ -651,17 +732,20 @@ struct QDiv {
 
 // stale readout partial of one lane from its read-copy registers (times the row scale for e4m3)
 template <int K, int COLD>
-__device__ __forceinline__ float cold_partial(const UnitRaw<K, COLD>& d, const float (&Cc)[Cfg<K, COLD>::CSR][4],
-                                              const float (&Cq)[Cfg<K, COLD>::CWR]) {
+__device__ __forceinline__ float cold_partial(const UnitRaw<K, COLD>& d, const Coef<K, COLD>& k) {
   using C = Cfg<K, COLD>;
   float pc = 0.f;
   if constexpr (COLD == NSSM_COLD_FP32) {
 #pragma unroll
     for (int s = 0; s < C::CS; ++s) {
-      pc = fmaf(d.cf[s].x, Cc[s][0], pc);
-      pc = fmaf(d.cf[s].y, Cc[s][1], pc);
-      pc = fmaf(d.cf[s].z, Cc[s][2], pc);
-      pc = fmaf(d.cf[s].w, Cc[s][3], pc);
+      pc = fmaf(d.cf[s].x, k.Cc[s][0], pc);
+      pc = fmaf(d.cf[s].y, k.Cc[s][1], pc);
+      pc = fmaf(d.cf[s].z, k.Cc[s][2], pc);
+      pc = fmaf(d.cf[s].w, k.Cc[s][3], pc);
+    }
+    if constexpr (C::CH) {
+      pc = fmaf(d.cfh.x, k.Cch[0], pc);
+      pc = fmaf(d.cfh.y, k.Cch[1], pc);
     }
   } else if constexpr (C::B16) {
 #pragma unroll
@@ -669,15 +753,33 @@ __device__ __forceinline__ float cold_partial(const UnitRaw<K, COLD>& d, const f
       float v[4];
       bf16x4_to_f32(d.cb[s], v);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) pc = fmaf(v[e], Cc[s][e], pc);
+      for (int e = 0; e < 4; ++e) pc = fmaf(v[e], k.Cc[s][e], pc);
     }
+    if constexpr (C::CH) {
+      float v[2];
+      bf16x2_to_f32(d.cbh, v);
+      pc = fmaf(v[0], k.Cch[0], pc);
+      pc = fmaf(v[1], k.Cch[1], pc);
+    }
+  } else if constexpr (C::SEG8) {
+#pragma unroll
+    for (int s = 0; s < C::CS; ++s) {
+      float v[4];
+      fp8x4_to_f32(d.c8[s], v);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pc = fmaf(v[e], k.Cc[s][e], pc);
+    }
+    const f2 h = __builtin_amdgcn_cvt_pk_f32_fp8((int)d.c8h, false);
+    pc = fmaf(h.x, k.Cch[0], pc);
+    pc = fmaf(h.y, k.Cch[1], pc);
+    pc *= d.sc;
   } else if constexpr (C::E4M3) {
 #pragma unroll
     for (int i = 0; i < C::WORDS; ++i) {
       float v[4];
       fp8x4_to_f32(d.cw[i], v);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) pc = fmaf(v[e], Cq[4 * i + e], pc);
+      for (int e = 0; e < 4; ++e) pc = fmaf(v[e], k.Cq[4 * i + e], pc);
     }
     pc *= d.sc;
   }
@@ -688,24 +790,32 @@ __device__ __forceinline__ float cold_partial(const UnitRaw<K, COLD>& d, const f
 // readout partial.
 template <int K, int COLD>
 __device__ __forceinline__ float hot_update(const StepArgs& a, size_t row, int q, UnitRaw<K, COLD>& d,
-                                            const float* __restrict__ hd, const float (&Bh)[K / 32][4],
-                                            const float (&Ch)[K / 32][4]) {
+                                            const float* __restrict__ hd, const Coef<K, COLD>& k) {
+  using C = Cfg<K, COLD>;
   const float uu = hd[HD_DT] * d.xp;
   const float dec = hd[HD_DECAY];
   float ph = 0.f;
   f4* hp = reinterpret_cast<f4*>(a.hot + row * K) + q;
 #pragma unroll
-  for (int s = 0; s < K / 32; ++s) {
+  for (int s = 0; s < C::HS; ++s) {
     f4 v = d.hv[s];
-    v.x = fmaf(v.x, dec, uu * Bh[s][0]);
-    v.y = fmaf(v.y, dec, uu * Bh[s][1]);
-    v.z = fmaf(v.z, dec, uu * Bh[s][2]);
-    v.w = fmaf(v.w, dec, uu * Bh[s][3]);
-    ph = fmaf(v.x, Ch[s][0], ph);
-    ph = fmaf(v.y, Ch[s][1], ph);
-    ph = fmaf(v.z, Ch[s][2], ph);
-    ph = fmaf(v.w, Ch[s][3], ph);
+    v.x = fmaf(v.x, dec, uu * k.Bh[s][0]);
+    v.y = fmaf(v.y, dec, uu * k.Bh[s][1]);
+    v.z = fmaf(v.z, dec, uu * k.Bh[s][2]);
+    v.w = fmaf(v.w, dec, uu * k.Bh[s][3]);
+    ph = fmaf(v.x, k.Ch[s][0], ph);
+    ph = fmaf(v.y, k.Ch[s][1], ph);
+    ph = fmaf(v.z, k.Ch[s][2], ph);
+    ph = fmaf(v.w, k.Ch[s][3], ph);
     st_stream(v, hp + 8 * s);
+  }
+  if constexpr (C::HH) {
+    f2 v = d.hh;
+    v.x = fmaf(v.x, dec, uu * k.Bhh[0]);
+    v.y = fmaf(v.y, dec, uu * k.Bhh[1]);
+    ph = fmaf(v.x, k.Chh[0], ph);
+    ph = fmaf(v.y, k.Chh[1], ph);
+    st_stream(v, reinterpret_cast<f2*>(a.hot + row * K + 32 * C::HS) + q);
   }
   return ph;
 }
@@ -759,14 +869,11 @@ __device__ __forceinline__ float corr_partial(const StepArgs& a, const float* __
 template <int K, int COLD, bool EXACT, int KU = kMaxC / 8, bool PRE = false>
 __device__ __forceinline__ void unit_compute(const StepArgs& a, size_t sh, size_t rh, int p, int q,
                                              UnitRaw<K, COLD>& d, uint16_t* rx, bool cold, const float* __restrict__ hd,
-                                             const float (&Bh)[K / 32][4], const float (&Ch)[K / 32][4],
-                                             const float (&Cc)[Cfg<K, COLD>::CSR][4],
-                                             const float (&Cq)[Cfg<K, COLD>::CWR],
-                                             const CorrRaw<KU>* cr = nullptr) {
+                                             const Coef<K, COLD>& k, const CorrRaw<KU>* cr = nullptr) {
   const size_t row = sh * a.P + p, yrow = rh * a.P + p;
-  float part = hot_update<K, COLD>(a, row, q, d, hd, Bh, Ch);
+  float part = hot_update<K, COLD>(a, row, q, d, hd, k);
   if constexpr (Cfg<K, COLD>::TIERED) {
-    if (cold) part = fmaf(hd[HD_SNAPF], cold_partial<K, COLD>(d, Cc, Cq), part);
+    if (cold) part = fmaf(hd[HD_SNAPF], cold_partial<K, COLD>(d, k), part);
     if constexpr (EXACT) {
       if constexpr (PRE) part += corr_sum<KU>(hd, q, *cr, d.xp);
       else part += corr_partial<KU>(a, hd, sh, rh, p, q, d.xp);
@@ -779,56 +886,82 @@ __device__ __forceinline__ void unit_compute(const StepArgs& a, size_t sh, size_
   }
 }
 
-// Write the new cold values of one row in the segment mapping: the fp32 copy, the single
-// bf16 copy (RNE), or the master (fp32, or bf16 by RNE) and the bf16 / e4m3 read copy
-// quantized from the master's values.
-template <int COLD, int CS>
-__device__ __forceinline__ void cold_store(const StepArgs& a, size_t row, int q, const float (&v)[CS][4]) {
-  constexpr int NC = CS * 32;
+// Write the new cold values of one row in the segment mapping (v: full segments, vh: the
+// half segment of k_hot = 16): the fp32 copy, the single bf16 copy (RNE), or the master
+// (fp32, or bf16 by RNE) and the bf16 / e4m3 read copy quantized from the master's values.
+template <int COLD, int CS, bool CH>
+__device__ __forceinline__ void cold_store(const StepArgs& a, size_t row, int q, const float (&v)[CS > 0 ? CS : 1][4],
+                                           const float (&vh)[2]) {
+  constexpr int NC = CS * 32 + (CH ? 16 : 0);
   if constexpr (COLD == NSSM_COLD_FP32) {
-    f4* p = reinterpret_cast<f4*>(static_cast<float*>(a.cold) + row * NC) + q;
+    float* rp = static_cast<float*>(a.cold) + row * NC;
+    f4* p = reinterpret_cast<f4*>(rp) + q;
 #pragma unroll
     for (int s = 0; s < CS; ++s) st_stream(f4{v[s][0], v[s][1], v[s][2], v[s][3]}, p + 8 * s);
+    if constexpr (CH) st_stream(f2{vh[0], vh[1]}, reinterpret_cast<f2*>(rp + 32 * CS) + q);
   } else if constexpr (COLD == NSSM_COLD_BF16_SINGLE) {
-    u2v* p = reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.cold) + blk16(row, 4 * q, NC));
+    uint16_t* base = static_cast<uint16_t*>(a.cold);
+    u2v* p = reinterpret_cast<u2v*>(base + blk16(row, 4 * q, NC));
 #pragma unroll
     for (int s = 0; s < CS; ++s) st_stream(f32x4_to_bf16(v[s][0], v[s][1], v[s][2], v[s][3]), p + kBlkSeg * s);
+    if constexpr (CH)
+      st_stream(f32x2_to_bf16(vh[0], vh[1]), reinterpret_cast<uint32_t*>(base + blk16(row, 32 * CS + 2 * q, NC)));
   } else {
-    float w[CS][4];  // the master's values
+    float w[CS > 0 ? CS : 1][4], wh[2];  // the master's values
     if constexpr (COLD == NSSM_COLD_FP8_BF16M) {
-      u2v* pm = reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.master) + blk16(row, 4 * q, NC));
+      uint16_t* base = static_cast<uint16_t*>(a.master);
+      u2v* pm = reinterpret_cast<u2v*>(base + blk16(row, 4 * q, NC));
 #pragma unroll
       for (int s = 0; s < CS; ++s) {
         const u2v t = f32x4_to_bf16(v[s][0], v[s][1], v[s][2], v[s][3]);
         st_stream(t, pm + kBlkSeg * s);
         bf16x4_to_f32(t, w[s]);
       }
+      if constexpr (CH) {
+        const uint32_t t = f32x2_to_bf16(vh[0], vh[1]);
+        st_stream(t, reinterpret_cast<uint32_t*>(base + blk16(row, 32 * CS + 2 * q, NC)));
+        bf16x2_to_f32(t, wh);
+      }
     } else {
-      f4* pm = reinterpret_cast<f4*>(static_cast<float*>(a.master) + row * NC) + q;
+      float* rp = static_cast<float*>(a.master) + row * NC;
+      f4* pm = reinterpret_cast<f4*>(rp) + q;
 #pragma unroll
       for (int s = 0; s < CS; ++s) {
         st_stream(f4{v[s][0], v[s][1], v[s][2], v[s][3]}, pm + 8 * s);
 #pragma unroll
         for (int e = 0; e < 4; ++e) w[s][e] = v[s][e];
       }
+      if constexpr (CH) {
+        st_stream(f2{vh[0], vh[1]}, reinterpret_cast<f2*>(rp + 32 * CS) + q);
+        wh[0] = vh[0];
+        wh[1] = vh[1];
+      }
     }
     if constexpr (COLD == NSSM_COLD_BF16) {
-      u2v* p = reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.cold) + blk16(row, 4 * q, NC));
+      uint16_t* base = static_cast<uint16_t*>(a.cold);
+      u2v* p = reinterpret_cast<u2v*>(base + blk16(row, 4 * q, NC));
 #pragma unroll
       for (int s = 0; s < CS; ++s) st_stream(f32x4_to_bf16(w[s][0], w[s][1], w[s][2], w[s][3]), p + kBlkSeg * s);
+      if constexpr (CH)
+        st_stream(f32x2_to_bf16(wh[0], wh[1]), reinterpret_cast<uint32_t*>(base + blk16(row, 32 * CS + 2 * q, NC)));
     } else {  // e4m3 with the per-row amax scale of scale/vllm_v4_patch.py:106-111
       float am = 0.f;
 #pragma unroll
       for (int s = 0; s < CS; ++s)
 #pragma unroll
         for (int e = 0; e < 4; ++e) am = fmaxf(am, fabsf(w[s][e]));
+      if constexpr (CH) am = fmaxf(am, fmaxf(fabsf(wh[0]), fabsf(wh[1])));
       am = max8(am);
       const float sc = am / 448.0f + 1e-12f;
       const QDiv qd(sc);
-      uint32_t* p = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.cold) + row * NC) + q;
+      uint8_t* rp = static_cast<uint8_t*>(a.cold) + row * NC;
+      uint32_t* p = reinterpret_cast<uint32_t*>(rp) + q;
 #pragma unroll
       for (int s = 0; s < CS; ++s)
         st_stream(f32x4_to_fp8(qd(w[s][0]), qd(w[s][1]), qd(w[s][2]), qd(w[s][3])), p + 8 * s);
+      if constexpr (CH)
+        st_stream((uint16_t)__builtin_amdgcn_cvt_pk_fp8_f32(qd(wh[0]), qd(wh[1]), 0, false),
+                  reinterpret_cast<uint16_t*>(rp + 32 * CS) + q);
       if (q == 0) a.scale[row] = sc;
     }
   }
@@ -841,17 +974,15 @@ __device__ __forceinline__ void cold_store(const StepArgs& a, size_t row, int q,
 template <int K, int COLD, bool EXACT>
 __device__ __forceinline__ void unit_compute_flush(const StepArgs& a, size_t sh, size_t rh, int p, int q,
                                                    UnitRaw<K, COLD>& d, const float* __restrict__ hd,
-                                                   const float (&Bh)[K / 32][4], const float (&Ch)[K / 32][4],
-                                                   const float (&Cc)[Cfg<K, COLD>::CSR][4],
-                                                   const float (&Cq)[Cfg<K, COLD>::CWR], const float* sU,
-                                                   const float* sBc, int m, int ldu, int pofs) {
+                                                   const Coef<K, COLD>& k, const float* sU, const float* sBc, int m,
+                                                   int ldu, int pofs) {
   using C = Cfg<K, COLD>;
   constexpr int NC = C::NC, CS = C::CS;
   const size_t row = sh * a.P + p, yrow = rh * a.P + p;
-  float part = hot_update<K, COLD>(a, row, q, d, hd, Bh, Ch);
-  part = fmaf(hd[HD_SNAPF], cold_partial<K, COLD>(d, Cc, Cq), part);
+  float part = hot_update<K, COLD>(a, row, q, d, hd, k);
+  part = fmaf(hd[HD_SNAPF], cold_partial<K, COLD>(d, k), part);
   const float dtot = hd[HD_DTOT];
-  float nvv[CS][4];
+  float nvv[C::CSR][4], nvh[2] = {0.f, 0.f};
 #pragma unroll
   for (int s = 0; s < CS; ++s) {
     float t[4];
@@ -868,6 +999,22 @@ __device__ __forceinline__ void unit_compute_flush(const StepArgs& a, size_t sh,
 #pragma unroll
     for (int e = 0; e < 4; ++e) nvv[s][e] = t[e] * dtot;
   }
+  if constexpr (C::CH) {
+    float t[2];
+    if constexpr (COLD == NSSM_COLD_FP32) {
+      t[0] = d.cfh.x; t[1] = d.cfh.y;
+    } else if constexpr (COLD == NSSM_COLD_BF16_SINGLE) {
+      bf16x2_to_f32(d.cbh, t);
+    } else if constexpr (C::MASTER16) {
+      bf16x2_to_f32(ld_stream(reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(a.master) +
+                                                               blk16(row, 32 * CS + 2 * q, NC))), t);
+    } else {
+      const f2 m2 = ld_stream(reinterpret_cast<const f2*>(static_cast<const float*>(a.master) + row * NC + 32 * CS) + q);
+      t[0] = m2.x; t[1] = m2.y;
+    }
+    nvh[0] = t[0] * dtot;
+    nvh[1] = t[1] * dtot;
+  }
   for (int i = 0; i < m; ++i) {
     const float coef = sU[i * ldu + (p - pofs)];
     const float* bc = sBc + i * NC + 4 * q;
@@ -879,8 +1026,13 @@ __device__ __forceinline__ void unit_compute_flush(const StepArgs& a, size_t sh,
       nvv[s][2] = fmaf(coef, bb.z, nvv[s][2]);
       nvv[s][3] = fmaf(coef, bb.w, nvv[s][3]);
     }
+    if constexpr (C::CH) {
+      const f2 bb = *reinterpret_cast<const f2*>(sBc + i * NC + 32 * CS + 2 * q);
+      nvh[0] = fmaf(coef, bb.x, nvh[0]);
+      nvh[1] = fmaf(coef, bb.y, nvh[1]);
+    }
   }
-  cold_store<COLD, CS>(a, row, q, nvv);
+  cold_store<COLD, CS, C::CH>(a, row, q, nvv, nvh);
   // the exact readout's correction, once the replay's registers are free (nothing else
   // adds to part in between, so the sum is the same)
   if constexpr (EXACT) part += corr_partial<kFusedMaxWindow / 8>(a, hd, sh, rh, p, q, d.xp);
@@ -914,21 +1066,12 @@ __device__ __forceinline__ void stage_unit_window(float* sB, float* sU, int m, i
 template <int K, int COLD>
 __device__ __forceinline__ void unit_hot_only(const StepArgs& a, const float* __restrict__ hd, const Ws& ws, size_t sh,
                                            size_t rh, size_t pair, int p, int q) {
-  using C = Cfg<K, COLD>;
   UnitRaw<K, COLD> d;
   unit_load<K, COLD>(a, sh * a.P + p, rh * a.P + p, q, d, true);
-  const float* wB = ws.B + pair * kN;
-  const float* wC = ws.C + pair * kN;
-  float Bh[K / 32][4], Ch[K / 32][4], Cc[C::CSR][4] = {}, Cq[C::CWR] = {};
-#pragma unroll
-  for (int s = 0; s < K / 32; ++s) {
-    const f4 tb = *reinterpret_cast<const f4*>(wB + 32 * s + 4 * q);
-    const f4 tc = *reinterpret_cast<const f4*>(wC + 32 * s + 4 * q);
-    Bh[s][0] = tb.x; Bh[s][1] = tb.y; Bh[s][2] = tb.z; Bh[s][3] = tb.w;
-    Ch[s][0] = tc.x; Ch[s][1] = tc.y; Ch[s][2] = tc.z; Ch[s][3] = tc.w;
-  }
+  Coef<K, COLD> k;
+  coef_load<K, COLD>(ws.B + pair * kN, ws.C + pair * kN, q, k);
   uint16_t* rx = a.ring_x + (sh * a.c + (int)hd[HD_POS]) * a.P;
-  unit_compute<K, COLD, false>(a, sh, rh, p, q, d, rx, false, hd, Bh, Ch, Cc, Cq);
+  unit_compute<K, COLD, false>(a, sh, rh, p, q, d, rx, false, hd, k);
 }
 
 // Stream kernel: one unit (8 headdim rows of one head) per wave; a workgroup is UW waves
@@ -941,10 +1084,11 @@ __device__ __forceinline__ void unit_hot_only(const StepArgs& a, const float* __
 // the fused replay's registers leave 4 waves per SIMD for every launch; measured on MI355X
 // (B = 256, 27 layers, ms per step): fp32 cold c = 4 at 8 waves 8.57 (at 6: 8.59); e4m3
 // over a bf16 master (B = 448) spills at 8 (12.66) and runs 11.62 at 6; wider hot tiers
-// spill above 6 (k_hot = 64) and 5 (k_hot = 96).
+// spill above 6 (k_hot = 64) and 5 (k_hot = 96), and k_hot = 16 (14 cold columns per lane
+// and the half segments' coefficients) above 6.
 template <int K, int COLD>
 constexpr int unit_waves_per_eu() {
-  return K == 32 ? (Cfg<K, COLD>::E4M3 ? 6 : 8) : K == kN ? 8 : K == 64 ? 6 : 5;
+  return K == 32 ? (Cfg<K, COLD>::E4M3 ? 6 : 8) : K == kN ? 8 : K == 16 || K == 64 ? 6 : 5;
 }
 
 // GATED: the gated readout's variant, in which a head that prep marked HD_SKIP and that
@@ -953,7 +1097,7 @@ constexpr int unit_waves_per_eu() {
 template <int K, int COLD, bool FUSED, bool EXACT, bool GATED>
 __device__ __forceinline__ void unit_body(const StepArgs& a, const float* __restrict__ hd_ro) {
   using C = Cfg<K, COLD>;
-  constexpr int HS = C::HS, CS = C::CS, CSR = C::CSR, CWR = C::CWR, NC = C::NC;
+  constexpr int NC = C::NC;
   constexpr bool TIERED = C::TIERED;
   const int tid = threadIdx.x, lane = tid & 63, q = lane & 7, rr = lane >> 3;
   const int uw = blockDim.x >> 6, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -997,28 +1141,8 @@ __device__ __forceinline__ void unit_body(const StepArgs& a, const float* __rest
 
   const float* wB = ws.B + ((size_t)bi * a.G + g) * kN;
   const float* wC = ws.C + ((size_t)bi * a.G + g) * kN;
-  float Bh[HS][4], Ch[HS][4], Cc[CSR][4], Cq[CWR];
-#pragma unroll
-  for (int s = 0; s < HS; ++s) {
-    const f4 tb = *reinterpret_cast<const f4*>(wB + 32 * s + 4 * q);
-    const f4 tc = *reinterpret_cast<const f4*>(wC + 32 * s + 4 * q);
-    Bh[s][0] = tb.x; Bh[s][1] = tb.y; Bh[s][2] = tb.z; Bh[s][3] = tb.w;
-    Ch[s][0] = tc.x; Ch[s][1] = tc.y; Ch[s][2] = tc.z; Ch[s][3] = tc.w;
-  }
-#pragma unroll
-  for (int s = 0; s < CSR; ++s) {
-    if constexpr (C::SEGREAD && CS > 0) {
-      const f4 tc = *reinterpret_cast<const f4*>(wC + K + 32 * s + 4 * q);
-      Cc[s][0] = tc.x; Cc[s][1] = tc.y; Cc[s][2] = tc.z; Cc[s][3] = tc.w;
-    } else {
-      Cc[s][0] = Cc[s][1] = Cc[s][2] = Cc[s][3] = 0.f;
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < CWR; ++i) {
-    if constexpr (C::CONTIG) Cq[i] = wC[K + C::CW * q + i];
-    else Cq[i] = 0.f;
-  }
+  Coef<K, COLD> k;
+  coef_load<K, COLD>(wB, wC, q, k);
 
   if constexpr (FUSED && TIERED) {
     if (flushing) {
@@ -1030,7 +1154,7 @@ __device__ __forceinline__ void unit_body(const StepArgs& a, const float* __rest
       stage_unit_window<NC>(sBc, sU, m, P, p0, nr, a.ring_b + (((size_t)slot * a.G + g) * c + (c - m)) * NC, wB + K,
                             a.ring_x + (sh * c + (c - m)) * P, a.x + rh * P, ws.w + rh * c, tid, blockDim.x);
       __syncthreads();
-      unit_compute_flush<K, COLD, EXACT>(a, sh, rh, p, q, d, hd, Bh, Ch, Cc, Cq, sU, sBc, m, nr, p0);
+      unit_compute_flush<K, COLD, EXACT>(a, sh, rh, p, q, d, hd, k, sU, sBc, m, nr, p0);
       return;
     }
   }
@@ -1041,9 +1165,9 @@ __device__ __forceinline__ void unit_body(const StepArgs& a, const float* __rest
   // the stream kernel replays windows of at most kFusedMaxWindow tokens itself; the exact
   // readout's correction then covers at most that many
   if constexpr (kCorrPre)
-    unit_compute<K, COLD, EXACT, kCorrU, true>(a, sh, rh, p, q, d, rx, !flushing, hd, Bh, Ch, Cc, Cq, &cr);
+    unit_compute<K, COLD, EXACT, kCorrU, true>(a, sh, rh, p, q, d, rx, !flushing, hd, k, &cr);
   else
-    unit_compute<K, COLD, EXACT, kCorrU>(a, sh, rh, p, q, d, rx, !flushing, hd, Bh, Ch, Cc, Cq);
+    unit_compute<K, COLD, EXACT, kCorrU>(a, sh, rh, p, q, d, rx, !flushing, hd, k);
 }
 
 template <int K, int COLD, bool FUSED, bool EXACT>
@@ -1429,8 +1553,8 @@ __global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
 template <int K, int COLD>
 __global__ void __launch_bounds__(256) join_kernel(StepArgs a, const float* __restrict__ S,
                                                    const int32_t* __restrict__ phase) {
-  constexpr int HS = K / 32;
-  constexpr int CS = COLD == NSSM_COLD_NONE ? 0 : (kN - K) / 32;
+  using C = Cfg<K, COLD>;
+  constexpr int HS = C::HS, CS = C::CS;
   const int bi = blockIdx.x / a.H, h = blockIdx.x % a.H;
   const int slot = a.slot_ids ? a.slot_ids[bi] : bi;
   if (slot < 0 || slot >= a.slots) return;
@@ -1439,22 +1563,32 @@ __global__ void __launch_bounds__(256) join_kernel(StepArgs a, const float* __re
   for (int u = wave; u < (a.P >> 3); u += nw) {
     const int p = u * 8 + rr;
     const size_t row = ((size_t)slot * a.H + h) * a.P + p;
-    const f4* src = reinterpret_cast<const f4*>(S + (((size_t)bi * a.H + h) * a.P + p) * kN) + q;
-    f4 hv[HS];
+    const float* srow = S + (((size_t)bi * a.H + h) * a.P + p) * kN;
+    const f4* src = reinterpret_cast<const f4*>(srow) + q;
+    f4 hv[C::HSR];
+    f2 hh = f2{0.f, 0.f};
 #pragma unroll
     for (int s2 = 0; s2 < HS; ++s2) hv[s2] = ld_stream(src + 8 * s2);
-    if constexpr (CS > 0) {
-      float v[CS][4];
+    if constexpr (C::HH) hh = ld_stream(reinterpret_cast<const f2*>(srow + 32 * HS) + q);
+    if constexpr (C::TIERED) {
+      const float* crow = srow + K;  // the cold columns, in the segment mapping
+      float v[C::CSR][4], vh[2] = {0.f, 0.f};
 #pragma unroll
       for (int s2 = 0; s2 < CS; ++s2) {
-        const f4 t = ld_stream(src + 8 * (HS + s2));
+        const f4 t = ld_stream(reinterpret_cast<const f4*>(crow) + q + 8 * s2);
         v[s2][0] = t.x; v[s2][1] = t.y; v[s2][2] = t.z; v[s2][3] = t.w;
       }
-      cold_store<COLD, CS>(a, row, q, v);
+      if constexpr (C::CH) {
+        const f2 t = ld_stream(reinterpret_cast<const f2*>(crow + 32 * CS) + q);
+        vh[0] = t.x;
+        vh[1] = t.y;
+      }
+      cold_store<COLD, CS, C::CH>(a, row, q, v, vh);
     }
     f4* hp = reinterpret_cast<f4*>(a.hot + row * K) + q;
 #pragma unroll
     for (int s2 = 0; s2 < HS; ++s2) st_stream(hv[s2], hp + 8 * s2);
+    if constexpr (C::HH) st_stream(hh, reinterpret_cast<f2*>(a.hot + row * K + 32 * HS) + q);
   }
   if (tid == 0) {
     const size_t o = (size_t)slot * a.H + h;
@@ -1936,7 +2070,7 @@ int check_tier(const nssm_tier* tr, bool need_ring) {
   if ((tr->cold_kind == NSSM_COLD_BF16 || e4m3) && !tr->master) return NSSM_E_NULL;
   if (e4m3 && !tr->scale) return NSSM_E_NULL;
   if (tr->slots <= 0 || tr->c < 1 || tr->c > kMaxC) return NSSM_E_DIMS;
-  if (tr->k_hot != 32 && tr->k_hot != 64 && tr->k_hot != 96) return NSSM_E_DIMS;
+  if (tr->k_hot != 16 && tr->k_hot != 32 && tr->k_hot != 64 && tr->k_hot != 96) return NSSM_E_DIMS;
   if (!aligned16(tr->hot) || (cold && !aligned16(tr->cold)) || (tr->master && !aligned16(tr->master)))
     return NSSM_E_ALIGN;
   if (cold && need_ring && (!aligned8(tr->ring_x) || !aligned16(tr->ring_b))) return NSSM_E_ALIGN;
@@ -2033,6 +2167,7 @@ int v4_step(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step
   a.fch = a.split ? flush_chunk(prm->P, tier->k_hot, tier->cold_kind, tier->c) : 0;
   hipStream_t st = (hipStream_t)stream;
   switch (tier->k_hot) {
+    case 16: return dispatch_kind<16>(a, tier->cold_kind, L, st);
     case 32: return dispatch_kind<32>(a, tier->cold_kind, L, st);
     case 64: return dispatch_kind<64>(a, tier->cold_kind, L, st);
     case 96: return dispatch_kind<96>(a, tier->cold_kind, L, st);
@@ -2249,9 +2384,11 @@ int nssm_v4_join(const nssm_layer_params* prm, const nssm_tier* tier, const floa
   a.HG = prm->H / prm->G;
   const unsigned grid = (unsigned)b * prm->H;
   switch (tier->k_hot) {
+    case 16: launch_join<16>(a, tier->cold_kind, state, phase, grid, (hipStream_t)stream); break;
     case 32: launch_join<32>(a, tier->cold_kind, state, phase, grid, (hipStream_t)stream); break;
     case 64: launch_join<64>(a, tier->cold_kind, state, phase, grid, (hipStream_t)stream); break;
-    default: launch_join<96>(a, tier->cold_kind, state, phase, grid, (hipStream_t)stream); break;
+    case 96: launch_join<96>(a, tier->cold_kind, state, phase, grid, (hipStream_t)stream); break;
+    default: return NSSM_E_DIMS;
   }
   return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
 }

@@ -198,12 +198,18 @@ class V4Tier:
 
     def _rows(self, t: Optional[torch.Tensor], blocked: bool) -> Optional[torch.Tensor]:
         """[slots, H, P, NC] in row order. The bf16 read copies and the bf16 master are
-        stored unit-blocked (8 rows of a unit segment-major: [NC/32][8][32] per unit), which
-        this unpacks (a copy); other arrays are returned as they are."""
+        stored unit-blocked (8 rows of a unit segment-major: [NC // 32][8][32] per unit, then
+        [8][16] for a trailing 16-column segment when NC % 32 == 16), which this unpacks (a
+        copy); other arrays are returned as they are."""
         if t is None or not blocked:
             return t
         S, H, P, NC = t.shape
-        return t.reshape(S * H * P // 8, NC // 32, 8, 32).transpose(1, 2).reshape(S, H, P, NC)
+        n32 = NC // 32 * 32
+        blocks = t.reshape(S * H * P // 8, 8 * NC)
+        rows = blocks[:, :8 * n32].reshape(-1, NC // 32, 8, 32).transpose(1, 2).reshape(-1, 8, n32)
+        if n32 < NC:
+            rows = torch.cat([rows, blocks[:, 8 * n32:].reshape(-1, 8, NC - n32)], dim=-1)
+        return rows.reshape(S, H, P, NC)
 
     def cold_rows(self) -> Optional[torch.Tensor]:
         """The cold copy [slots, H, P, NC] in row order."""

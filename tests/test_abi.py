@@ -141,7 +141,7 @@ def test_entry_points_validate_before_launching():
     assert L.nssm_fresh_step(ctypes.byref(prm), fake, 2, ctypes.byref(inp), fake, fake, 1 << 30, None) == -2  # b > slots
     tier = _lib.Tier(4, 32, 4, 9, *([fake] * 10))
     assert L.nssm_v4_step(ctypes.byref(prm), ctypes.byref(tier), ctypes.byref(inp), fake, fake, 1 << 30, None) == -4
-    tier = _lib.Tier(4, 48, 4, 0, *([fake] * 10))  # k_hot not a multiple of 32
+    tier = _lib.Tier(4, 48, 4, 0, *([fake] * 10))  # k_hot not 16, 32, 64 or 96
     assert L.nssm_v4_step(ctypes.byref(prm), ctypes.byref(tier), ctypes.byref(inp), fake, fake, 1 << 30, None) == -2
     tier = _lib.Tier(4, 32, 0, 0, *([fake] * 10))  # c = 0
     assert L.nssm_v4_step(ctypes.byref(prm), ctypes.byref(tier), ctypes.byref(inp), fake, fake, 1 << 30, None) == -2
@@ -210,10 +210,11 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
         _lib.lib()
 
 
-@pytest.mark.parametrize("NC", [96, 64, 32])
+@pytest.mark.parametrize("NC", [96, 64, 32, 112])
 def test_blocked_16bit_layout_unpacks_to_row_order(NC):
     """The bf16 read copies and the bf16 master are stored unit-blocked: element (row, col)
-    at (row // 8) * 8 NC + (col // 32) * 256 + (row % 8) * 32 + col % 32 (include/nssm.h).
+    at (row // 8) * 8 NC + (col // 32) * 256 + (row % 8) * w + col % 32 with w = 32, or
+    16 in a trailing 16-column segment (NC = 112, k_hot = 16; include/nssm.h).
     V4Tier.cold_rows / master_rows unpack that order (checked here on the CPU against the
     formula; the GPU join test checks the kernels through them)."""
     from nested_ssm_amd.ops import V4Tier
@@ -223,7 +224,8 @@ def test_blocked_16bit_layout_unpacks_to_row_order(NC):
     flat = torch.empty(rows * NC, dtype=torch.int64)
     for r in range(rows):
         for cidx in range(NC):
-            off = (r // 8) * 8 * NC + (cidx // 32) * 256 + (r % 8) * 32 + cidx % 32
+            w = min(32, NC - cidx // 32 * 32)
+            off = (r // 8) * 8 * NC + (cidx // 32) * 256 + (r % 8) * w + cidx % 32
             flat[off] = r * 1000 + cidx
     got = V4Tier._rows(None, flat.view(S, H, P, NC), True)
     want = (torch.arange(rows)[:, None] * 1000 + torch.arange(NC)[None, :]).view(S, H, P, NC)

@@ -259,3 +259,10 @@ def test_full_size_ragged_config4(c, k):
         return sl, Snew, ph
 
     _run(b, k, c, "fp32", steps=256, seed=10 + c + k, slot_events=events, hot_every=32)
+
+
+@pytest.mark.parametrize("c", [16, 64])
+def test_full_size_k_hot_16(c):
+    """k_hot = 16 at the 9B head shape, B=256, fp32 cold, random phases, 2c + 8 steps, against
+    the fp64 closed form at 1e-5."""
+    _run(256, 16, c, "fp32", steps=2 * c + 8, seed=40 + c)

@@ -119,7 +119,7 @@ def _prefill_decode(model, ids, n_decode):
     return torch.stack(logits, 1), pkv
 
 
-@pytest.mark.parametrize("pb,c,cold_bf16", [(128, 16, 0), (32, 4, 0), (64, 3, 1)])
+@pytest.mark.parametrize("pb,c,cold_bf16", [(128, 16, 0), (32, 4, 0), (64, 3, 1), (16, 4, 0), (16, 16, 1)])
 def test_native_install_matches_oracle(monkeypatch, pb, c, cold_bf16):
     from nested_ssm_amd import v4_native_decode as V
 

@@ -513,3 +513,65 @@ def test_join_quantization_is_bit_exact(cold, master):
         q, sc = oracle.quant_fp8(mv)
         assert torch.equal(tier.scale.cpu().view(torch.int32), sc[..., 0].contiguous().view(torch.int32))
         assert torch.equal(tier.cold_t.cpu(), q.view(torch.uint8))
+
+
+# --------------------------------------------------------------------------- k_hot = 16
+@pytest.mark.parametrize("exact", [False, True])
+@pytest.mark.parametrize("c", [4, 16, 64])
+@pytest.mark.parametrize("cold", ["fp32", "bf16", "fp8"])
+def test_k_hot_16_matches_oracle(cold, c, exact):
+    """The narrowest trained hot width (scale/nemotron_retrofit.py:5,191): 16 hot columns
+    and 112 cold ones, a half segment on each side of the split, at the config-0 shape;
+    windows replayed in the stream kernel (c <= 16) and on the matrix cores (c = 64); the
+    stale and the exact readout, random phases."""
+    tier, ref, worst = _run_v4(4, 8, 1, 80, 16, c, cold, steps=2 * c + 5 if c > 4 else 64, seed=210 + c,
+                               phase=[0, 1, c - 1, c // 2], check_state_every=max(1, c // 2), exact=exact)
+    if cold == "fp8":
+        assert 0 < worst <= 2e-2
+
+
+@pytest.mark.parametrize("cold,c", [("bf16", 4), ("fp8", 4), ("bf16", 64), ("fp8", 40)])
+def test_k_hot_16_bf16_master_matches_oracle(cold, c):
+    """k_hot = 16 over the fused path's bf16 masters (one bf16 copy; e4m3 beside a bf16
+    master), both replay paths."""
+    _, _, worst = _run_v4(3, 8, 2, 80, 16, c, cold, steps=2 * c + 5, seed=230 + c, phase=[0, c - 1, c // 2],
+                          check_state_every=max(1, c // 2), master="bf16")
+    if cold == "fp8":
+        assert 0 < worst <= 2e-2
+
+
+def test_k_hot_16_gated_readouts_and_launch_shapes():
+    """coldoff / qgate readouts at k_hot = 16 with 1 and 4 units per stream workgroup."""
+    for units in (1, 4):
+        set_launch(units)
+        counts = torch.zeros(2, dtype=torch.int64, device="cuda")
+        tier, ref, _ = _run_v4(4, 8, 2, 64, 16, 4, "fp32", steps=15, seed=240 + units, phase=[0, 1, 3, 2],
+                               modes=_gate_modes(16), counts=counts)
+        assert tuple(counts.tolist()) == (ref.qgate_n, ref.qgate_kept)
+    set_launch(0)
+
+
+@pytest.mark.parametrize("cold,master", [("bf16", "bf16"), ("bf16", "fp32"), ("fp8", "fp32"), ("fp8", "bf16")])
+def test_join_quantization_is_bit_exact_k16(cold, master):
+    """The join's cold copies at k_hot = 16 (112 cold columns: the blocked 16-bit layout's
+    16-column tail segment, the e4m3 half-segment stores) against torch's casts, bit for bit."""
+    b, H, G, P, k = 3, 8, 2, 80, 16
+    gen = torch.Generator().manual_seed(250)
+    S = _rounding_state(b, H, P, gen)
+    prm = oracle.make_layer_params(H, P, 128, G, gen)
+    tier = V4Tier(b, H, P, G, k_hot=k, c=4, cold=cold, master=master)
+    tier.join(dev_params(prm), S.cuda())
+    torch.cuda.synchronize()
+    Sc = S[..., k:]
+    assert torch.equal(tier.hot.cpu().view(torch.int32), S[..., :k].contiguous().view(torch.int32))
+    ref_master = Sc.to(torch.bfloat16) if master == "bf16" else Sc
+    if tier.master is not None:
+        w = torch.int16 if master == "bf16" else torch.int32
+        assert torch.equal(tier.master_rows().cpu().view(w), ref_master.contiguous().view(w))
+    mv = ref_master.float()
+    if cold == "bf16":
+        assert torch.equal(tier.cold_rows().cpu().view(torch.int16), mv.to(torch.bfloat16).view(torch.int16))
+    else:
+        q, sc = oracle.quant_fp8(mv)
+        assert torch.equal(tier.scale.cpu().view(torch.int32), sc[..., 0].contiguous().view(torch.int32))
+        assert torch.equal(tier.cold_t.cpu(), q.view(torch.uint8))
