@@ -20,6 +20,8 @@
  *                        part), scale/vllm_v4_patch.py:140-179 (decode_readout)
  *   nssm_v4_step_gated   scale/v4_native_decode.py:118-127 (coldoff) and
  *                        :147-156 (qgate) of _v4_decode
+ *   nssm_v4_step_teacher scale/nemo9b_eval.py:41-85 (naive_mixer_forward, mode
+ *                        "v4": the teacher-forced evaluation readout)
  *   nssm_v4_join         scale/vllm_v4_patch.py:123-137 (prefill_snapshot),
  *                        scale/v4_native_decode.py:234-243,
  *                        scale/v4_fused_decode.py:121-159 (prefill capture)
@@ -201,6 +203,20 @@ int nssm_v4_step_noalloc(const nssm_layer_params* prm, const nssm_tier* tier,
 int nssm_v4_step_exact(const nssm_layer_params* prm, const nssm_tier* tier,
                        const nssm_step_inputs* in, float* y, void* workspace,
                        int64_t workspace_bytes, void* stream);
+
+/* nssm_v4_step with the teacher-forced v4 readout of scale/nemo9b_eval.py:41-85 (the
+ * per-token evaluation forward, mode "v4", lag 0): the snapshot is the cold state after
+ * the update of a flush token, read at that token without decay, and after it with the
+ * decay inclusive of the current token,
+ *   flush token:  y = hot C'[:K] + (new cold read copy) C'[K:] + D x
+ *   other tokens: y = hot C'[:K] + exp(glog + a) (cold_read C'[K:]) + D x.
+ * The reference snapshots at sequence positions t % c == 0 counted from 0: join a
+ * sequence's start (its state, zeros from scratch) with phase c - 1 so that its flush
+ * tokens are those. The tier bookkeeping is nssm_v4_step's, so the readouts may
+ * alternate on one tier. NSSM_E_KIND for NSSM_COLD_NONE. */
+int nssm_v4_step_teacher(const nssm_layer_params* prm, const nssm_tier* tier,
+                         const nssm_step_inputs* in, float* y, void* workspace,
+                         int64_t workspace_bytes, void* stream);
 
 /* nssm_v4_step with a gated stale readout: a skipped head's y is hot C'[:K] + D x
  * (no cold term) and, when it does not flush at this token, its cold columns are not

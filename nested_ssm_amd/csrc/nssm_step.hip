@@ -70,6 +70,7 @@ struct StepArgs {
   int32_t b, slots, H, P, G, HG, c, K;
   int32_t prb;    // requests per prep workgroup
   int32_t exact;  // rank-c exact correction readout instead of the stale one
+  int32_t tf;     // teacher-forced readout: inclusive decay; a flushing head reads its new state
   int32_t split;  // the flush kernel runs after the stream kernel (prep writes the pair flags)
   int32_t fch;    // window tokens the flush kernel stages in LDS at a time (multiple of 4)
   float dt_min;
@@ -86,8 +87,9 @@ struct StepArgs {
 // group) flush flags [b][G] (int32, padded to a multiple of 4), window weights
 // [b][H][c] (flush) and correction coefficients [b][H][c] (exact readout).
 // HD_SNAPF is the factor of the snapshot readout: exp(glog) (stale, the decay up
-// to the previous token), exp(glog + a) (exact, inclusive of this token) or 0 (a head
-// whose cold term the gated readout drops; HD_SKIP = 1 then).
+// to the previous token), exp(glog + a) (exact, and teacher-forced between flushes:
+// inclusive of this token), 1 (teacher-forced at a flush: the readout of the new state)
+// or 0 (a head whose cold term the gated readout drops; HD_SKIP = 1 then).
 enum { HD_DT = 0, HD_A, HD_DECAY, HD_SNAPF, HD_D, HD_FLUSH, HD_DTOT, HD_M, HD_POS, HD_SKIP, HD_STRIDE = 12 };
 __host__ __device__ constexpr size_t flag_words(int b, int G, int c) {
   return c > 0 ? (((size_t)b * G + 3) & ~(size_t)3) : 0;
@@ -429,7 +431,9 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
       }
       // stale: exp(glog), the decay up to the previous token (one-token lag);
       // exact: exp(glog + a), inclusive of this token (scale/v4_native_decode.py:89)
-      hd[HD_SNAPF] = skip ? 0.f : expf(exact ? gl + av : gl);
+      // teacher-forced (scale/nemo9b_eval.py:57-70): the snapshot is the state after the flush
+      // token's update, read undecayed at that token and with inclusive decay after it
+      hd[HD_SNAPF] = skip ? 0.f : a.tf ? (flush ? 1.f : expf(gl + av)) : expf(exact ? gl + av : gl);
       hd[HD_SKIP] = skip ? 1.f : 0.f;
       hd[HD_FLUSH] = flush ? 1.f : 0.f;
       hd[HD_POS] = (float)pos;
@@ -618,7 +622,9 @@ struct Coef {
   float Cq[C::CWR];                    // cold columns of the contiguous e4m3 mapping
 };
 
-template <int K, int COLD>
+// SEGC: also the cold columns' C' in the segment mapping (the segment reads, and the
+// teacher-forced flush readout of the values the lane stores)
+template <int K, int COLD, bool SEGC = Cfg<K, COLD>::SEGREAD>
 __device__ __forceinline__ void coef_load(const float* wB, const float* wC, int q, Coef<K, COLD>& k) {
   using C = Cfg<K, COLD>;
 #pragma unroll
@@ -636,7 +642,7 @@ __device__ __forceinline__ void coef_load(const float* wB, const float* wC, int 
   }
 #pragma unroll
   for (int s = 0; s < C::CSR; ++s) {
-    if constexpr (C::SEGREAD && C::CS > 0) {
+    if constexpr (SEGC && C::CS > 0) {
       const f4 tc = *reinterpret_cast<const f4*>(wC + K + 32 * s + 4 * q);
       k.Cc[s][0] = tc.x; k.Cc[s][1] = tc.y; k.Cc[s][2] = tc.z; k.Cc[s][3] = tc.w;
     } else {
@@ -886,26 +892,56 @@ __device__ __forceinline__ void unit_compute(const StepArgs& a, size_t sh, size_
   }
 }
 
+// Dot product of a lane's read-copy values with its C' (segment mapping).
+template <int CS, bool CH>
+__device__ __forceinline__ float seg_dot(const float (&r)[CS > 0 ? CS : 1][4], const float (&rh)[2],
+                                         const float (*cc)[4], const float* cch) {
+  float pc = 0.f;
+#pragma unroll
+  for (int s = 0; s < CS; ++s)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pc = fmaf(r[s][e], cc[s][e], pc);
+  if constexpr (CH) {
+    pc = fmaf(rh[0], cch[0], pc);
+    pc = fmaf(rh[1], cch[1], pc);
+  }
+  return pc;
+}
+
 // Write the new cold values of one row in the segment mapping (v: full segments, vh: the
 // half segment of k_hot = 16): the fp32 copy, the single bf16 copy (RNE), or the master
 // (fp32, or bf16 by RNE) and the bf16 / e4m3 read copy quantized from the master's values.
-template <int COLD, int CS, bool CH>
-__device__ __forceinline__ void cold_store(const StepArgs& a, size_t row, int q, const float (&v)[CS > 0 ? CS : 1][4],
-                                           const float (&vh)[2]) {
+// RD: returns the lane's readout partial of the read copy as stored (C' in the segment
+// mapping: cc [CS][4], cch [2]; e4m3 times the row scale), else 0.
+template <int COLD, int CS, bool CH, bool RD = false>
+__device__ __forceinline__ float cold_store(const StepArgs& a, size_t row, int q, const float (&v)[CS > 0 ? CS : 1][4],
+                                            const float (&vh)[2], const float (*cc)[4] = nullptr,
+                                            const float* cch = nullptr) {
   constexpr int NC = CS * 32 + (CH ? 16 : 0);
+  float pc = 0.f;
   if constexpr (COLD == NSSM_COLD_FP32) {
     float* rp = static_cast<float*>(a.cold) + row * NC;
     f4* p = reinterpret_cast<f4*>(rp) + q;
 #pragma unroll
     for (int s = 0; s < CS; ++s) st_stream(f4{v[s][0], v[s][1], v[s][2], v[s][3]}, p + 8 * s);
     if constexpr (CH) st_stream(f2{vh[0], vh[1]}, reinterpret_cast<f2*>(rp + 32 * CS) + q);
+    if constexpr (RD) pc = seg_dot<CS, CH>(v, vh, cc, cch);
   } else if constexpr (COLD == NSSM_COLD_BF16_SINGLE) {
     uint16_t* base = static_cast<uint16_t*>(a.cold);
     u2v* p = reinterpret_cast<u2v*>(base + blk16(row, 4 * q, NC));
+    float r[CS > 0 ? CS : 1][4], rh[2] = {0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < CS; ++s) st_stream(f32x4_to_bf16(v[s][0], v[s][1], v[s][2], v[s][3]), p + kBlkSeg * s);
-    if constexpr (CH)
-      st_stream(f32x2_to_bf16(vh[0], vh[1]), reinterpret_cast<uint32_t*>(base + blk16(row, 32 * CS + 2 * q, NC)));
+    for (int s = 0; s < CS; ++s) {
+      const u2v t = f32x4_to_bf16(v[s][0], v[s][1], v[s][2], v[s][3]);
+      st_stream(t, p + kBlkSeg * s);
+      bf16x4_to_f32(t, r[s]);
+    }
+    if constexpr (CH) {
+      const uint32_t t = f32x2_to_bf16(vh[0], vh[1]);
+      st_stream(t, reinterpret_cast<uint32_t*>(base + blk16(row, 32 * CS + 2 * q, NC)));
+      bf16x2_to_f32(t, rh);
+    }
+    if constexpr (RD) pc = seg_dot<CS, CH>(r, rh, cc, cch);
   } else {
     float w[CS > 0 ? CS : 1][4], wh[2];  // the master's values
     if constexpr (COLD == NSSM_COLD_FP8_BF16M) {
@@ -940,10 +976,19 @@ __device__ __forceinline__ void cold_store(const StepArgs& a, size_t row, int q,
     if constexpr (COLD == NSSM_COLD_BF16) {
       uint16_t* base = static_cast<uint16_t*>(a.cold);
       u2v* p = reinterpret_cast<u2v*>(base + blk16(row, 4 * q, NC));
+      float r[CS > 0 ? CS : 1][4], rh[2] = {0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < CS; ++s) st_stream(f32x4_to_bf16(w[s][0], w[s][1], w[s][2], w[s][3]), p + kBlkSeg * s);
-      if constexpr (CH)
-        st_stream(f32x2_to_bf16(wh[0], wh[1]), reinterpret_cast<uint32_t*>(base + blk16(row, 32 * CS + 2 * q, NC)));
+      for (int s = 0; s < CS; ++s) {
+        const u2v t = f32x4_to_bf16(w[s][0], w[s][1], w[s][2], w[s][3]);
+        st_stream(t, p + kBlkSeg * s);
+        bf16x4_to_f32(t, r[s]);
+      }
+      if constexpr (CH) {
+        const uint32_t t = f32x2_to_bf16(wh[0], wh[1]);
+        st_stream(t, reinterpret_cast<uint32_t*>(base + blk16(row, 32 * CS + 2 * q, NC)));
+        bf16x2_to_f32(t, rh);
+      }
+      if constexpr (RD) pc = seg_dot<CS, CH>(r, rh, cc, cch);
     } else {  // e4m3 with the per-row amax scale of scale/vllm_v4_patch.py:106-111
       float am = 0.f;
 #pragma unroll
@@ -956,22 +1001,36 @@ __device__ __forceinline__ void cold_store(const StepArgs& a, size_t row, int q,
       const QDiv qd(sc);
       uint8_t* rp = static_cast<uint8_t*>(a.cold) + row * NC;
       uint32_t* p = reinterpret_cast<uint32_t*>(rp) + q;
+      float r[CS > 0 ? CS : 1][4], rh[2] = {0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < CS; ++s)
-        st_stream(f32x4_to_fp8(qd(w[s][0]), qd(w[s][1]), qd(w[s][2]), qd(w[s][3])), p + 8 * s);
-      if constexpr (CH)
-        st_stream((uint16_t)__builtin_amdgcn_cvt_pk_fp8_f32(qd(wh[0]), qd(wh[1]), 0, false),
-                  reinterpret_cast<uint16_t*>(rp + 32 * CS) + q);
+      for (int s = 0; s < CS; ++s) {
+        const uint32_t t = f32x4_to_fp8(qd(w[s][0]), qd(w[s][1]), qd(w[s][2]), qd(w[s][3]));
+        st_stream(t, p + 8 * s);
+        if constexpr (RD) fp8x4_to_f32(t, r[s]);
+      }
+      if constexpr (CH) {
+        const int t = __builtin_amdgcn_cvt_pk_fp8_f32(qd(wh[0]), qd(wh[1]), 0, false);
+        st_stream((uint16_t)t, reinterpret_cast<uint16_t*>(rp + 32 * CS) + q);
+        if constexpr (RD) {
+          const f2 h = __builtin_amdgcn_cvt_pk_f32_fp8(t, false);
+          rh[0] = h.x;
+          rh[1] = h.y;
+        }
+      }
       if (q == 0) a.scale[row] = sc;
+      if constexpr (RD) pc = seg_dot<CS, CH>(r, rh, cc, cch) * sc;
     }
   }
+  return pc;
 }
 
 // One unit of a head that flushes at this token, in the stream kernel (short windows):
 // hot columns, the stale readout, and the exact cold state at this token, the decayed
 // snapshot plus the VALU replay of the staged window (sU [m][P] of this head,
 // sBc [m][NC]), scale/v4_fused_decode.py:76-85.
-template <int K, int COLD, bool EXACT>
+// TF (the teacher-forced readout): the cold term is the readout of the new state as stored
+// (the read copy), times HD_SNAPF = 1, instead of the stale snapshot's.
+template <int K, int COLD, bool EXACT, bool TF = false>
 __device__ __forceinline__ void unit_compute_flush(const StepArgs& a, size_t sh, size_t rh, int p, int q,
                                                    UnitRaw<K, COLD>& d, const float* __restrict__ hd,
                                                    const Coef<K, COLD>& k, const float* sU, const float* sBc, int m,
@@ -980,7 +1039,7 @@ __device__ __forceinline__ void unit_compute_flush(const StepArgs& a, size_t sh,
   constexpr int NC = C::NC, CS = C::CS;
   const size_t row = sh * a.P + p, yrow = rh * a.P + p;
   float part = hot_update<K, COLD>(a, row, q, d, hd, k);
-  part = fmaf(hd[HD_SNAPF], cold_partial<K, COLD>(d, k), part);
+  if constexpr (!TF) part = fmaf(hd[HD_SNAPF], cold_partial<K, COLD>(d, k), part);
   const float dtot = hd[HD_DTOT];
   float nvv[C::CSR][4], nvh[2] = {0.f, 0.f};
 #pragma unroll
@@ -1032,7 +1091,10 @@ __device__ __forceinline__ void unit_compute_flush(const StepArgs& a, size_t sh,
       nvh[1] = fmaf(coef, bb.y, nvh[1]);
     }
   }
-  cold_store<COLD, CS, C::CH>(a, row, q, nvv, nvh);
+  if constexpr (TF)
+    part = fmaf(hd[HD_SNAPF], cold_store<COLD, CS, C::CH, true>(a, row, q, nvv, nvh, k.Cc, k.Cch), part);
+  else
+    cold_store<COLD, CS, C::CH>(a, row, q, nvv, nvh);
   // the exact readout's correction, once the replay's registers are free (nothing else
   // adds to part in between, so the sum is the same)
   if constexpr (EXACT) part += corr_partial<kFusedMaxWindow / 8>(a, hd, sh, rh, p, q, d.xp);
@@ -1094,7 +1156,9 @@ constexpr int unit_waves_per_eu() {
 // GATED: the gated readout's variant, in which a head that prep marked HD_SKIP and that
 // does not flush takes the hot-only path (the other variants never wait for that flag
 // before their state loads).
-template <int K, int COLD, bool FUSED, bool EXACT, bool GATED>
+// TF: the teacher-forced readout's variant (a flushing head reads the state it replays;
+// the other heads read the snapshot as the stale variant does, with prep's factor).
+template <int K, int COLD, bool FUSED, bool EXACT, bool GATED, bool TF = false>
 __device__ __forceinline__ void unit_body(const StepArgs& a, const float* __restrict__ hd_ro) {
   using C = Cfg<K, COLD>;
   constexpr int NC = C::NC;
@@ -1142,7 +1206,7 @@ __device__ __forceinline__ void unit_body(const StepArgs& a, const float* __rest
   const float* wB = ws.B + ((size_t)bi * a.G + g) * kN;
   const float* wC = ws.C + ((size_t)bi * a.G + g) * kN;
   Coef<K, COLD> k;
-  coef_load<K, COLD>(wB, wC, q, k);
+  coef_load<K, COLD, C::SEGREAD || (TF && FUSED)>(wB, wC, q, k);
 
   if constexpr (FUSED && TIERED) {
     if (flushing) {
@@ -1154,7 +1218,7 @@ __device__ __forceinline__ void unit_body(const StepArgs& a, const float* __rest
       stage_unit_window<NC>(sBc, sU, m, P, p0, nr, a.ring_b + (((size_t)slot * a.G + g) * c + (c - m)) * NC, wB + K,
                             a.ring_x + (sh * c + (c - m)) * P, a.x + rh * P, ws.w + rh * c, tid, blockDim.x);
       __syncthreads();
-      unit_compute_flush<K, COLD, EXACT>(a, sh, rh, p, q, d, hd, k, sU, sBc, m, nr, p0);
+      unit_compute_flush<K, COLD, EXACT, TF>(a, sh, rh, p, q, d, hd, k, sU, sBc, m, nr, p0);
       return;
     }
   }
@@ -1177,6 +1241,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(unit_w
 template <int K, int COLD, bool FUSED>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(unit_waves_per_eu<K, COLD>()))) unit_kernel_gated(StepArgs a, const float* __restrict__ hd_ro) {
   unit_body<K, COLD, FUSED, false, true>(a, hd_ro);
+}
+// (the teacher-forced flush readout keeps a second coefficient set: k_hot = 16 over e4m3
+// spills above 5 waves)
+template <int K, int COLD>
+constexpr int unit_tf_waves_per_eu() {
+  return K == 16 && Cfg<K, COLD>::E4M3 ? 5 : unit_waves_per_eu<K, COLD>();
+}
+template <int K, int COLD, bool FUSED>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(unit_tf_waves_per_eu<K, COLD>()))) unit_kernel_tf(StepArgs a, const float* __restrict__ hd_ro) {
+  unit_body<K, COLD, FUSED, false, false, true>(a, hd_ro);
 }
 
 // Untiered step (the full fp32 state is the hot tier, K = N): one one-wave workgroup per 2
@@ -1286,7 +1360,9 @@ __device__ __forceinline__ void stage_window_dma(float* sB, uint16_t* sX, float*
     __builtin_amdgcn_global_load_lds(NSSM_GLOBAL(wgt + k0 + lane), NSSM_LOCAL(sW), 4, 0, 0);
 }
 
-template <int K, int COLD>
+// TF (the teacher-forced readout): y gets the readout of the new state as stored (the new
+// read copy; e4m3 partials formed after the row scale is known) instead of the old one's.
+template <int K, int COLD, bool TF = false>
 __global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
   using C = Cfg<K, COLD>;
   constexpr int NC = C::NC, NT = C::NT, nw = kFlushWaves, nthr = kFlushWaves * 64;
@@ -1479,8 +1555,6 @@ __global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
             pc = fmaf(rd[1], cq.y, pc);
             pc = fmaf(rd[2], cq.z, pc);
             pc = fmaf(rd[3], cq.w, pc);
-            pc += __shfl_xor(pc, 16);
-            pc += __shfl_xor(pc, 32);
             f4 nv = acc[i];
             nv.x = fmaf(dtot, old[i].x, nv.x);
             nv.y = fmaf(dtot, old[i].y, nv.y);
@@ -1499,10 +1573,24 @@ __global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
               st_stream(nv, reinterpret_cast<f4*>(static_cast<float*>(a.master) + row * NC + col));
             }
             acc[i] = nv;
-            if constexpr (COLD == NSSM_COLD_BF16)
-              st_stream(f32x4_to_bf16(nv.x, nv.y, nv.z, nv.w),
-                        reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.cold) + blk16(row, col, NC)));
-            if (lk == 0) sPart[p * NT + nt] = pc * rscale;
+            if constexpr (COLD == NSSM_COLD_BF16) {
+              const u2v t = f32x4_to_bf16(nv.x, nv.y, nv.z, nv.w);
+              st_stream(t, reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.cold) + blk16(row, col, NC)));
+              if constexpr (TF) bf16x4_to_f32(t, rd);  // the new read copy
+            } else if constexpr (TF) {
+              rd[0] = nv.x; rd[1] = nv.y; rd[2] = nv.z; rd[3] = nv.w;  // fp32 copy, or the rounded bf16 one
+            }
+            if constexpr (TF && !C::E4M3) {
+              pc = rd[0] * cq.x;
+              pc = fmaf(rd[1], cq.y, pc);
+              pc = fmaf(rd[2], cq.z, pc);
+              pc = fmaf(rd[3], cq.w, pc);
+            }
+            if constexpr (!(TF && C::E4M3)) {  // (teacher-forced e4m3: after the row scale below)
+              pc += __shfl_xor(pc, 16);
+              pc += __shfl_xor(pc, 32);
+              if (lk == 0) sPart[p * NT + nt] = pc * rscale;
+            }
             if constexpr (C::E4M3) {
               float am = fmaxf(fmaxf(fabsf(nv.x), fabsf(nv.y)), fmaxf(fabsf(nv.z), fabsf(nv.w)));
               am = fmaxf(am, __shfl_xor(am, 16));
@@ -1526,11 +1614,24 @@ __global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
               const float sc = am / 448.0f + 1e-12f;  // scale/vllm_v4_patch.py:106-111
               const QDiv qd(sc);
               const f4 nv = acc[i];
-              st_stream(f32x4_to_fp8(qd(nv.x), qd(nv.y), qd(nv.z), qd(nv.w)),
-                        reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.cold) + row * NC + nt * 16 + 4 * lk));
+              const uint32_t codes = f32x4_to_fp8(qd(nv.x), qd(nv.y), qd(nv.z), qd(nv.w));
+              st_stream(codes, reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.cold) + row * NC + nt * 16 + 4 * lk));
               if (nt == 0 && lk == 0) a.scale[row] = sc;
+              if constexpr (TF) {  // the readout of the new e4m3 copy
+                float rd[4];
+                fp8x4_to_f32(codes, rd);
+                const f4 cq = *reinterpret_cast<const f4*>(cq0 + nt * 16 + 4 * lk);
+                float pc = rd[0] * cq.x;
+                pc = fmaf(rd[1], cq.y, pc);
+                pc = fmaf(rd[2], cq.z, pc);
+                pc = fmaf(rd[3], cq.w, pc);
+                pc += __shfl_xor(pc, 16);
+                pc += __shfl_xor(pc, 32);
+                if (lk == 0) sPart[p * NT + nt] = pc * sc;
+              }
             }
           }
+          if constexpr (TF) __syncthreads();  // the partials of this pass's tiles
         }
       }
       // y += exp(glog) (stale cold readout); the next item's first barrier orders
@@ -2107,11 +2208,13 @@ int launch_pair(const StepArgs& a, const Launch& L, hipStream_t st) {
     const bool gated = a.hot_only || a.qgate_tau > 0.f;
     if (L.fused) {
       if (a.exact) hipLaunchKernelGGL((unit_kernel<K, COLD, true, true>), ugrid, ublock, L.lds, st, a, hd_ro);
+      else if (a.tf) hipLaunchKernelGGL((unit_kernel_tf<K, COLD, true>), ugrid, ublock, L.lds, st, a, hd_ro);
       else if (gated) hipLaunchKernelGGL((unit_kernel_gated<K, COLD, true>), ugrid, ublock, L.lds, st, a, hd_ro);
       else hipLaunchKernelGGL((unit_kernel<K, COLD, true, false>), ugrid, ublock, L.lds, st, a, hd_ro);
       return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
     }
     if (a.exact) hipLaunchKernelGGL((unit_kernel<K, COLD, false, true>), ugrid, ublock, 0, st, a, hd_ro);
+    else if (a.tf) hipLaunchKernelGGL((unit_kernel_tf<K, COLD, false>), ugrid, ublock, 0, st, a, hd_ro);
     else if (gated) hipLaunchKernelGGL((unit_kernel_gated<K, COLD, false>), ugrid, ublock, 0, st, a, hd_ro);
     else hipLaunchKernelGGL((unit_kernel<K, COLD, false, false>), ugrid, ublock, 0, st, a, hd_ro);
     // one resident round of workgroups: an empty launch dispatches no more than that,
@@ -2119,8 +2222,12 @@ int launch_pair(const StepArgs& a, const Launch& L, hipStream_t st) {
     const int items = a.b * a.H, cap = kFlushPerCU * cu_count();
     int grid = items < cap ? items : cap;
     if (grid < a.HG) grid = a.HG;  // the kernel's listing needs grid >= HG (items >= HG)
-    hipLaunchKernelGGL((flush_kernel<K, COLD>), dim3((unsigned)grid), dim3(kFlushWaves * 64),
-                       flush_lds_bytes(a.P, K, COLD, a.fch), st, a);
+    if (a.tf)
+      hipLaunchKernelGGL((flush_kernel<K, COLD, true>), dim3((unsigned)grid), dim3(kFlushWaves * 64),
+                         flush_lds_bytes(a.P, K, COLD, a.fch), st, a);
+    else
+      hipLaunchKernelGGL((flush_kernel<K, COLD>), dim3((unsigned)grid), dim3(kFlushWaves * 64),
+                         flush_lds_bytes(a.P, K, COLD, a.fch), st, a);
   } else if constexpr (K == kN) {  // untiered
     hipLaunchKernelGGL(fresh_kernel, dim3((unsigned)((size_t)a.b * a.H * (a.P / 2))), dim3(64), 0, st, a, hd_ro);
   } else {
@@ -2142,14 +2249,16 @@ int dispatch_kind(const StepArgs& a, int kind, const Launch& L, hipStream_t st) 
   return NSSM_E_KIND;
 }
 
+// readout: 0 stale, 1 exact (rank-c correction), 2 teacher-forced
 int v4_step(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step_inputs* in, float* y,
-            void* workspace, int64_t workspace_bytes, void* stream, int exact, int hot_only = 0,
+            void* workspace, int64_t workspace_bytes, void* stream, int readout, int hot_only = 0,
             float qgate_tau = 0.f, int64_t* qcounts = nullptr) {
+  const int exact = readout == 1;
   int rc = check_params(prm);
   if (rc) return rc;
   if ((rc = check_inputs(in, y))) return rc;
   if ((rc = check_tier(tier, true))) return rc;
-  if (exact && tier->cold_kind == NSSM_COLD_NONE) return NSSM_E_KIND;  // the correction needs the cold tier
+  if (readout && tier->cold_kind == NSSM_COLD_NONE) return NSSM_E_KIND;  // these readouts need the cold tier
   if (!(fabsf(qgate_tau) <= 3.0e38f)) return NSSM_E_DIMS;  // NaN or infinite threshold
   if (qcounts && (reinterpret_cast<uintptr_t>(qcounts) & 7)) return NSSM_E_ALIGN;
   if (!in->slot_ids && in->b > tier->slots) return NSSM_E_DIMS;
@@ -2158,6 +2267,7 @@ int v4_step(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step
   fill_common(a, prm, in, y, workspace);
   fill_tier(a, tier);
   a.exact = exact;
+  a.tf = readout == 2;
   a.hot_only = hot_only != 0;
   a.qgate_tau = qgate_tau;
   a.qcounts = reinterpret_cast<unsigned long long*>(qcounts);
@@ -2358,6 +2468,11 @@ int nssm_v4_step_noalloc(const nssm_layer_params* prm, const nssm_tier* tier, co
 int nssm_v4_step_exact(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step_inputs* in, float* y,
                        void* workspace, int64_t workspace_bytes, void* stream) {
   return v4_step(prm, tier, in, y, workspace, workspace_bytes, stream, 1);
+}
+
+int nssm_v4_step_teacher(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step_inputs* in, float* y,
+                         void* workspace, int64_t workspace_bytes, void* stream) {
+  return v4_step(prm, tier, in, y, workspace, workspace_bytes, stream, 2);
 }
 
 int nssm_v4_step_gated(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step_inputs* in, float* y,

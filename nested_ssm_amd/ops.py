@@ -241,7 +241,8 @@ class V4Tier:
 
     def step(self, prm: LayerParams, x, B, C, dt, y: Optional[torch.Tensor] = None,
              slot_ids: Optional[torch.Tensor] = None, exact: bool = False, hot_only: bool = False,
-             qgate: float = 0.0, counts: Optional[torch.Tensor] = None, noalloc: bool = False) -> torch.Tensor:
+             qgate: float = 0.0, counts: Optional[torch.Tensor] = None, noalloc: bool = False,
+             teacher: bool = False) -> torch.Tensor:
         """One decode token for b requests (slot_ids: their slots, default 0..b-1).
         exact=True reads the cold tier with the rank-c exact correction (corr=1,
         scale/v4_native_decode.py:81-117) instead of the stale readout. hot_only=True is
@@ -249,15 +250,21 @@ class V4Tier:
         qgate=tau > 0 drops the cold term of the heads whose query puts less than tau of
         its energy on the cold columns (scale/v4_native_decode.py:147-156), and adds the
         gated and kept head counts to counts (int64 [2] on the GPU) when given. The tier
-        evolves the same way in every case. noalloc=True runs the stale readout through
+        evolves the same way in every case. teacher=True is the teacher-forced readout of
+        scale/nemo9b_eval.py:41-85 (nssm_v4_step_teacher: a flush token reads the state it
+        flushes to, the others the snapshot with the decay inclusive of this token; join a
+        sequence's start at phase c - 1 to flush at positions t % c == 0 as that loop does).
+        noalloc=True runs the stale readout through
         nssm_v4_step_noalloc, whose workspace is the library's fixed per-GPU scratch array
         (with y given, the call allocates nothing; calls overlapping on one GPU race)."""
         b = x.shape[0]
         gated = hot_only or qgate > 0
         if exact and gated:
             raise ValueError("exact readout cannot be combined with hot_only or qgate")
-        if noalloc and (exact or gated):
+        if noalloc and (exact or gated or teacher):
             raise ValueError("noalloc serves the stale readout only")
+        if teacher and (exact or gated):
+            raise ValueError("the teacher-forced readout cannot be combined with exact, hot_only or qgate")
         if y is None:
             y = torch.empty(b, prm.H, prm.P, device=x.device, dtype=torch.float32)
         _need(y, "y", torch.float32, (b, prm.H, prm.P))
@@ -275,7 +282,9 @@ class V4Tier:
             check(lib().nssm_v4_step_gated(*args, int(hot_only), float(qgate), _ptr(counts), _stream()),
                   "nssm_v4_step_gated")
         else:
-            fn, name = (lib().nssm_v4_step_exact, "nssm_v4_step_exact") if exact else (lib().nssm_v4_step, "nssm_v4_step")
+            fn, name = ((lib().nssm_v4_step_exact, "nssm_v4_step_exact") if exact else
+                        (lib().nssm_v4_step_teacher, "nssm_v4_step_teacher") if teacher else
+                        (lib().nssm_v4_step, "nssm_v4_step"))
             check(fn(*args, _stream()), name)
         return y
 

@@ -38,6 +38,11 @@ Pinning status of each function (how it is checked, in tests/test_oracle.py):
                     qgate on constructed queries C = R^T e_n (all energy on one column):
                     a cold column is kept, a hot one dropped at any tau, and the counters
                     count heads; the state is the ungated one's in every mode
+  TeacherForcedV4   (scale/nemo9b_eval.py:41-85) the fp64 closed form from a fresh
+                    trajectory with the snapshot taken at the last t = c floor(t / c) after
+                    its update and the decay summed over (ts, t] (a snapshot before the
+                    update or an exclusive decay fails it; the decode readout of NativeV4
+                    is shown to differ); c = 1 and k = N give the fresh readout
   quant_fp8 / read  torch float8_e4m3fn cast; scale = amax/448 + 1e-12 per row
   fp8_readout       closed form of the reference docstring vs an fp64 loop
   hot_only_step     the hot columns of an fp64 fresh trajectory (they never read the cold ones)
@@ -47,7 +52,7 @@ Pinning status of each function (how it is checked, in tests/test_oracle.py):
                     fp64 per-group loop
 """
 from .v4_ref import (  # noqa: F401
-    LayerParams, NativeV4, TieredV4, conv_update, fp8_readout, fresh_step, gated_rmsnorm, hot_only_step,
+    LayerParams, NativeV4, TeacherForcedV4, TieredV4, conv_update, fp8_readout, fresh_step, gated_rmsnorm, hot_only_step,
     make_layer_params,
     make_rotation, make_state, make_step_inputs, quant_fp8, read_fp8, rotate, softplus_dt,
 )

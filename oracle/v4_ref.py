@@ -404,3 +404,77 @@ class TieredV4:
             cold = self._replay(self.cold[s], self.ring[s], prm.A)
             out.append(torch.cat([self.hot[s], cold], dim=-1))
         return torch.stack(out)
+
+
+# ---------------------------------------------------------------------------
+class TeacherForcedV4:
+    """The teacher-forced v4 readout of the reference's per-token evaluation forward,
+    scale/nemo9b_eval.py:41-85 (naive_mixer_forward, mode "v4", lag 0), per slot:
+
+      S_t = exp(a_t) S_{t-1} + (dt_t x_t) (x) B'_t                        (:53-54)
+      Gtot_t = Gtot_{t-1} + a_t                                           (:60)
+      if t % c == 0: Snap = q(S_t), gSnap = Gtot_t   (after the update)   (:61-71)
+      y_t = S_t[:k] C'_t[:k] + exp(Gtot_t - gSnap) (Snap[k:] C'_t[k:]) + D x_t   (:72-84)
+      (y_t = S_t C'_t + D x_t while t < warm, :75-78)
+
+    t counts the sequence's tokens from 0 (join sets it, with the state and its snapshot).
+    q: "fp32" the clone, "bf16" S.to(bf16).float() (:66-67), "fp8" e4m3 with either the
+    reference's per-column scale (fp8_scale="column": amax over P, clamp(1e-6) / 448,
+    :62-64) or the tier's per-row one (fp8_scale="row": amax over the cold columns / 448 +
+    1e-12, scale/vllm_v4_patch.py:106-111)."""
+
+    def __init__(self, slots: int, H: int, P: int, N: int, k: int, c: int, cold: str = "fp32",
+                 fp8_scale: str = "row", warm: int = 0, dtype=torch.float32):
+        assert 0 < k <= N and c >= 1 and cold in ("fp32", "bf16", "fp8") and fp8_scale in ("row", "column")
+        self.k, self.c, self.cold, self.fp8_scale, self.warm, self.dtype = k, c, cold, fp8_scale, warm, dtype
+        self.S = torch.zeros(slots, H, P, N, dtype=dtype)
+        self.snap = torch.zeros(slots, H, P, N - k, dtype=dtype)
+        self.gtot = torch.zeros(slots, H, dtype=dtype)
+        self.gsnap = torch.zeros(slots, H, dtype=dtype)
+        self.t = torch.zeros(slots, dtype=torch.int64)
+
+    def _q(self, S: torch.Tensor) -> torch.Tensor:
+        """The snapshot of full states S: its cold columns in the snapshot precision."""
+        k = self.k
+        if self.cold == "bf16":
+            return S[..., k:].to(torch.bfloat16).to(self.dtype)
+        if self.cold == "fp8":
+            if self.fp8_scale == "column":
+                sc = S.abs().amax(-2, keepdim=True).clamp(min=1e-6) / E4M3_MAX
+                return ((S / sc).to(torch.float8_e4m3fn).to(self.dtype) * sc)[..., k:]
+            q, sc = quant_fp8(S[..., k:].float())
+            return read_fp8(q, sc).to(self.dtype)
+        return S[..., k:].clone()
+
+    def join(self, slots, S_new: torch.Tensor, t0: Optional[torch.Tensor] = None):
+        """A sequence at position t0 (default 0) with state S_new: the snapshot is S_new."""
+        slots = torch.as_tensor(slots, dtype=torch.long)
+        self.S[slots] = S_new.to(self.dtype)
+        self.snap[slots] = self._q(self.S[slots])
+        self.gtot[slots] = 0
+        self.gsnap[slots] = 0
+        self.t[slots] = 0 if t0 is None else torch.as_tensor(t0, dtype=torch.int64)
+
+    def step(self, x, B, C, dt_raw, prm: LayerParams, slots: Optional[torch.Tensor] = None) -> torch.Tensor:
+        b = x.shape[0]
+        slots = torch.arange(b) if slots is None else torch.as_tensor(slots, dtype=torch.long)
+        k, c = self.k, self.c
+        prm = prm.to(self.dtype)
+        xf, Bp, Cp, dt, a = _prep(x, B, C, dt_raw, prm, self.dtype)
+        S = self.S[slots] * torch.exp(a)[..., None, None] + (dt[..., None, None] * Bp[:, :, None, :]) * xf[..., None]
+        self.S[slots] = S
+        gtot = self.gtot[slots] + a
+        self.gtot[slots] = gtot
+        t = self.t[slots]
+        snapt = t % c == 0
+        if bool(snapt.any()):
+            ss = slots[snapt]
+            self.snap[ss] = self._q(S[snapt])
+            self.gsnap[ss] = gtot[snapt]
+        glog = gtot - self.gsnap[slots]
+        y_v4 = torch.einsum("bhpn,bhn->bhp", S[..., :k], Cp[..., :k]) + \
+            torch.einsum("bhpn,bhn->bhp", self.snap[slots], Cp[..., k:]) * torch.exp(glog)[..., None]
+        y_fresh = torch.einsum("bhpn,bhn->bhp", S, Cp)
+        y = torch.where((t < self.warm)[:, None, None], y_fresh, y_v4)
+        self.t[slots] = t + 1
+        return y + xf * prm.D[None, :, None]

@@ -392,3 +392,69 @@ def test_phase_write_mid_window_recaptures_the_tier(monkeypatch, corr, t_new):
         tier = dict.get(m._v4state, "tier")
         assert_close32(tier.materialize(m._v4state["params"]).cpu(), ref.S, f"layer {li} state")
         assert m._v4state["t"] == t_new + n_after == int(ref.t[0])
+
+
+@pytest.mark.parametrize("cfg", [dict(mode="v4", c=4, pb=32), dict(mode="v4", c=4, pb=32, cold_bf16=1),
+                                 dict(mode="v4", c=16, pb=16), dict(mode="v4", c=3, pb=64, warm=5),
+                                 dict(mode="v4", c=4, pb=32, cold_fp8=1), dict(mode="fresh")])
+def test_teacher_forced_state_op_matches_oracle(cfg):
+    """The evaluation forward's state op (nemo9b_eval drop-in: one teacher-forced launch pair
+    per token, sequences from zero states) against the oracle's restatement of
+    scale/nemo9b_eval.py:41-85 on the same mixer inputs; fp32 1e-5, bf16 snapshot the bf16
+    bar, e4m3 (per-row scale) 2e-2."""
+    from helpers import assert_close_flips, max_rel
+    from nested_ssm_amd import hf, nemo9b_eval as NE
+
+    model = _tiny_model(seed=41)
+    m = hf.mixers(model)[0]
+    full = dict(NE.CFG, **cfg)
+    hidden = torch.randn(2, 13, 128, generator=torch.Generator().manual_seed(42)).cuda()
+    with torch.no_grad():
+        gate, x, B, C, dt = NE.teacher_forced_inputs(m, hidden)
+        ys = NE.state_op(m, x, B, C, dt, full).cpu()
+    prm = _oracle_params(m, float(m.time_step_limit[0]))
+    k = N if full["mode"] == "fresh" else full["pb"]
+    cold = "fp8" if full["cold_fp8"] else "bf16" if full["cold_bf16"] else "fp32"
+    ref = oracle.TeacherForcedV4(2, m.num_heads, m.head_dim, N, k, full["c"], cold=cold, warm=full["warm"])
+    ref.join(torch.arange(2), torch.zeros(2, m.num_heads, m.head_dim, N))
+    for t in range(13):
+        y_ref = ref.step(x[:, t].cpu(), B[:, t].cpu(), C[:, t].cpu(), dt[:, t].cpu(), prm)
+        if cold == "fp8":
+            assert max_rel(ys[:, t], y_ref) <= 2e-2
+        elif cold == "bf16":
+            assert_close_flips(ys[:, t], y_ref, f"token {t}")
+        else:
+            assert_close32(ys[:, t], y_ref, f"token {t} ({full})")
+
+
+def test_teacher_forced_forward_tracks_the_stock_forward():
+    """naive_mixer_forward bound to every mixer: mode "fresh" gives the stock forward's logits
+    within the bf16 cast of the kernel inputs, v4 with pb = N is the fresh forward, and v4 with
+    stale cold columns is not; unsupported CFG keys raise."""
+    from nested_ssm_amd import hf, nemo9b_eval as NE
+
+    ids = torch.randint(0, 96, (2, 12), generator=torch.Generator().manual_seed(43)).cuda()
+    model = _tiny_model(seed=44)
+    with torch.no_grad():
+        stock = model(ids, use_cache=False).logits.float()
+        for m in hf.mixers(model):
+            m.forward = NE.naive_mixer_forward.__get__(m)
+        saved = dict(NE.CFG)
+        try:
+            NE.CFG.update(mode="fresh")
+            fresh = model(ids, use_cache=False).logits.float()
+            NE.CFG.update(mode="v4", c=4, pb=N)
+            allhot = model(ids, use_cache=False).logits.float()
+            NE.CFG.update(mode="v4", c=8, pb=32)
+            v4 = model(ids, use_cache=False).logits.float()
+            NE.CFG.update(mode="v4", lag=1)
+            with pytest.raises(NotImplementedError, match="lag"):
+                model(ids, use_cache=False)
+        finally:
+            NE.CFG.clear()
+            NE.CFG.update(saved)
+    scale = stock.abs().max()
+    assert float((fresh - stock).abs().max() / scale) < 2e-2
+    assert torch.equal(allhot, fresh)
+    # stale cold columns move this small model's logits by ~1e-5 relative (fp32 rounding: ~1e-7)
+    assert float((v4 - fresh).abs().max() / scale) > 5e-6

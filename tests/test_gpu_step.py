@@ -575,3 +575,60 @@ def test_join_quantization_is_bit_exact_k16(cold, master):
         q, sc = oracle.quant_fp8(mv)
         assert torch.equal(tier.scale.cpu().view(torch.int32), sc[..., 0].contiguous().view(torch.int32))
         assert torch.equal(tier.cold_t.cpu(), q.view(torch.uint8))
+
+
+# --------------------------------------------------------------------------- teacher-forced readout
+@pytest.mark.parametrize("cold,k,c", [("fp32", 32, 4), ("fp32", 32, 16), ("fp32", 32, 64), ("fp32", 16, 4),
+                                      ("fp32", 16, 40), ("bf16", 32, 4), ("bf16", 32, 64), ("fp8", 32, 4),
+                                      ("fp8", 32, 64), ("fp8", 16, 16)])
+def test_teacher_forced_readout_matches_oracle(cold, k, c):
+    """nssm_v4_step_teacher against the oracle's restatement of the evaluation forward's v4
+    loop (scale/nemo9b_eval.py:41-85): a sequence joined at its start with phase c - 1 flushes
+    at positions t % c == 0, reads the new state there and the snapshot with inclusive decay
+    elsewhere; fp32 rtol = atol = 1e-5, a bf16 snapshot (RNE of the exact state) the bf16 bar,
+    e4m3 (the tier's per-row scale) 2e-2 relative. The state is checked too."""
+    b, H, G, P = 4, 8, 1, 80
+    gen, prm, S0 = _setup(b, H, P, G, seed=260 + k + c)
+    dprm = dev_params(prm)
+    ref = oracle.TeacherForcedV4(b, H, P, 128, k, c, cold=cold)
+    ref.join(torch.arange(b), S0)
+    tier = V4Tier(b, H, P, G, k_hot=k, c=c, cold=cold)
+    tier.join(dprm, *to_dev(S0), phase=torch.full((b,), c - 1, dtype=torch.int32, device="cuda"))
+    worst = 0.0
+    for step in range(2 * c + 5):
+        x, B, C, dt = oracle.make_step_inputs(b, H, P, 128, G, gen)
+        y_ref = ref.step(x, B, C, dt, prm)
+        y = tier.step(dprm, *to_dev(x, B, C, dt), teacher=True)
+        if cold == "fp8":
+            r = max_rel(y.cpu(), y_ref)
+            worst = max(worst, r)
+            assert r <= 2e-2, f"fp8 teacher-forced y step {step}: {r:.3g}"
+        elif cold == "bf16":
+            worst = max(worst, assert_close_flips(y, y_ref, f"bf16 teacher-forced y step {step}"))
+        else:
+            assert_close32(y, y_ref, f"teacher-forced y step {step}", **FP32_TOL)
+    assert_close32(tier.materialize(dprm), ref.S, "teacher-forced state", **FP32_TOL)
+
+
+def test_teacher_forced_readout_from_scratch_with_ragged_starts():
+    """Sequences that start from a zero state (the evaluation forward's start) in slots of
+    their own, at different times: each joins at phase c - 1; requests in a subset of slots."""
+    slots, H, G, P, k, c = 5, 8, 2, 48, 32, 4
+    gen, prm, _ = _setup(slots, H, P, G, seed=280)
+    dprm = dev_params(prm)
+    ref = oracle.TeacherForcedV4(slots, H, P, 128, k, c)
+    tier = V4Tier(slots, H, P, G, k_hot=k, c=c)
+    zeros = torch.zeros(slots, H, P, 128)
+    ref.join(torch.arange(slots), zeros)
+    tier.join(dprm, zeros.cuda(), phase=torch.full((slots,), c - 1, dtype=torch.int32, device="cuda"))
+    for step in range(20):
+        if step in (6, 13):  # a new sequence starts in slot 2 (from zeros)
+            ref.join(torch.tensor([2]), torch.zeros(1, H, P, 128))
+            tier.join(dprm, torch.zeros(1, H, P, 128, device="cuda"),
+                      slot_ids=torch.tensor([2], dtype=torch.int32, device="cuda"),
+                      phase=torch.tensor([c - 1], dtype=torch.int32, device="cuda"))
+        sl = torch.randperm(slots, generator=gen)[:4].to(torch.int32)
+        x, B, C, dt = oracle.make_step_inputs(4, H, P, 128, G, gen)
+        y_ref = ref.step(x, B, C, dt, prm, slots=sl.long())
+        y = tier.step(dprm, *to_dev(x, B, C, dt), slot_ids=sl.cuda(), teacher=True)
+        assert_close32(y, y_ref, f"teacher-forced ragged y step {step}", **FP32_TOL)

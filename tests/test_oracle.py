@@ -582,3 +582,87 @@ def test_gated_rmsnorm_matches_fp64_group_loop():
                 want[r, i] = float(w[i]) * v[j] * rs
     got = oracle.gated_rmsnorm(y, gate, w, gs, 1e-6)
     assert torch.allclose(got.double(), want, rtol=1e-6, atol=1e-7)
+
+
+# --------------------------------------------------------------------------- teacher-forced v4
+@pytest.mark.parametrize("k,c", [(32, 4), (16, 3), (96, 1), (32, 5)])
+def test_teacher_forced_v4_equals_closed_form(k, c):
+    """scale/nemo9b_eval.py:41-85 (mode "v4"): at sequence position tau,
+    y = S_tau[:k] C'[:k] + exp(sum_{i=ts+1}^{tau} a_i) S_ts[k:] C'[k:] + D x with
+    ts = c floor(tau / c) and S_ts the state AFTER token ts's update (fp64 fresh trajectory).
+    Negative controls: an exclusive decay (sum to tau - 1) and a snapshot taken before the
+    update (S_{ts-1}) both miss."""
+    b, H, P, G = 2, 4, 8, 2
+    gen, prm, S0 = _small(seed=300 + k + c, b=b, H=H, P=P, G=G)
+    steps = 3 * c + 2
+    ins = [oracle.make_step_inputs(b, H, P, N, G, gen) for _ in range(steps)]
+    traj, ays = _fresh_traj(S0, ins, prm)  # traj[i + 1]: after token i; ays[i]: token i's log decay
+    tf = oracle.TeacherForcedV4(b, H, P, N, k, c, dtype=torch.float64)
+    tf.join(torch.arange(b), S0.double())
+    prm64 = prm.to(torch.float64)
+    zero = torch.zeros(b, H, dtype=torch.float64)
+    for tau in range(steps):
+        x, B, C, dt = ins[tau]
+        y = tf.step(x, B, C, dt, prm)
+        ts = c * (tau // c)
+        Cp = _heads(oracle.rotate(C.double(), prm64.R), H)
+        dx = x.double() * prm64.D[None, :, None]
+        hot = torch.einsum("bhpn,bhn->bhp", traj[tau + 1][..., :k], Cp[..., :k])
+
+        def cold(state, lag):
+            return torch.exp(lag)[..., None] * torch.einsum("bhpn,bhn->bhp", state[..., k:], Cp[..., k:])
+
+        inc = sum((ays[i] for i in range(ts + 1, tau + 1)), zero)
+        want = hot + cold(traj[ts + 1], inc) + dx
+        assert torch.allclose(y, want, atol=1e-11), f"tau={tau}"
+        if tau > ts:
+            exc = sum((ays[i] for i in range(ts + 1, tau)), zero)
+            assert float((y - (hot + cold(traj[ts + 1], exc) + dx)).abs().max()) > 1e-6
+        assert float((y - (hot + cold(traj[ts], inc) + dx)).abs().max()) > 1e-6
+
+
+def test_teacher_forced_v4_reduces_to_fresh_and_differs_from_decode():
+    """c = 1 (a snapshot after every update) and k = N give the fresh readout; warm tokens
+    read fresh; the decode readout (NativeV4, one-token-lagged snapshot) is another one."""
+    b, H, P, G = 2, 8, 16, 2
+    gen, prm, S0 = _small(seed=320, b=b, H=H, P=P, G=G)
+    ins = [oracle.make_step_inputs(b, H, P, N, G, gen) for _ in range(9)]
+    fresh_S = S0.clone()
+    arms = {"c1": oracle.TeacherForcedV4(b, H, P, N, 32, 1), "kN": oracle.TeacherForcedV4(b, H, P, N, N, 4),
+            "warm": oracle.TeacherForcedV4(b, H, P, N, 32, 4, warm=3),
+            "tf": oracle.TeacherForcedV4(b, H, P, N, 32, 4)}
+    for a in arms.values():
+        a.join(torch.arange(b), S0)
+    dec = oracle.NativeV4(b, H, P, N, 32, 4)
+    dec.join(torch.arange(b), S0)
+    gap = 0.0
+    for tau, (x, B, C, dt) in enumerate(ins):
+        yf = oracle.fresh_step(fresh_S, x, B, C, dt, prm)
+        ys = {n: a.step(x, B, C, dt, prm) for n, a in arms.items()}
+        yd = dec.step(x, B, C, dt, prm)
+        assert torch.allclose(ys["c1"], yf, atol=1e-6)
+        assert torch.allclose(ys["kN"], yf, atol=1e-6)
+        if tau < 3 or tau % 4 == 0:  # warm tokens read the fresh state, and so do snapshot tokens
+            assert torch.allclose(ys["warm"], yf, atol=1e-6)
+        if tau % 4 == 0:
+            assert torch.allclose(ys["tf"], yf, atol=1e-6)
+        gap = max(gap, float((ys["tf"] - yd).abs().max()))
+    assert gap > 1e-3
+
+
+def test_teacher_forced_v4_fp8_row_scale_is_close_to_the_column_scale():
+    """The reference's evaluation scales its e4m3 snapshot per column (amax over P,
+    scale/nemo9b_eval.py:62-64); the tier's format scales per row (amax over the cold
+    columns). Both stay within the 2e-2 fp8 bar of the fp32 snapshot and of each other."""
+    b, H, P, G, k, c = 2, 8, 80, 2, 32, 4
+    gen, prm, S0 = _small(seed=330, b=b, H=H, P=P, G=G)
+    arms = {n: oracle.TeacherForcedV4(b, H, P, N, k, c, cold=cold, fp8_scale=sc)
+            for n, cold, sc in (("fp32", "fp32", "row"), ("row", "fp8", "row"), ("col", "fp8", "column"))}
+    for a in arms.values():
+        a.join(torch.arange(b), S0)
+    for _ in range(2 * c + 1):
+        x, B, C, dt = oracle.make_step_inputs(b, H, P, N, G, gen)
+        ys = {n: a.step(x, B, C, dt, prm) for n, a in arms.items()}
+        rel = lambda u, v: float((u - v).norm() / v.norm())  # noqa: E731
+        assert rel(ys["row"], ys["fp32"]) <= 2e-2 and rel(ys["col"], ys["fp32"]) <= 2e-2
+        assert rel(ys["row"], ys["col"]) <= 2e-2
