@@ -1310,17 +1310,50 @@ __global__ void __launch_bounds__(64) fresh_kernel(StepArgs a, const float* __re
 // over min(F, grid) workgroups whatever the requests' phases.
 //
 // Delta is contracted on the matrix cores as 16 x 16 tiles (p-tile pt, n-tile nt) of
-// v_mfma_f32_16x16x4_f32: A = B'^T (16 n x 4 tokens), B = w x (4 tokens x 16 p). The
-// window is staged in LDS by DMA fch tokens at a time (the whole window when it fits,
-// all its loads in flight together; zero past its end). Lane (li, lk) of a tile holds
-// Delta[pt*16 + li][nt*16 + 4 lk .. +3]; the state is read and written in that mapping,
-// its loads issued before the window's. Each wave holds kMfmaTiles tiles; a pass covers
-// as many tiles as the waves hold (e4m3: whole rows only, the row scale needs all of a
-// row's tiles). Per-tile readout partials and row maxima go through LDS and are summed
-// in a fixed order.
+// v_mfma_f32_16x16x32_bf16: A = (w B')^T (16 n x 32 tokens), B = x (32 tokens x 16 p). x
+// is bf16 already; v = w B' (fp32) is split into three bf16 parts with hi + mid + lo == v
+// exactly, so the three bf16 products per token are exact and accumulate in fp32: the
+// accuracy of an fp32 contraction at a fraction of fp32 MFMA's issue time (per 64 tokens
+// and tile, fp32 16x16x4: 16 steps of 32 cycles; bf16 16x16x32: 2 steps x 3 parts of 16).
+// The window is staged in LDS by DMA fch tokens at a time (the whole window when it fits,
+// all its loads in flight together), and each lane builds its operands from it: 8 tokens
+// of one cold column (or headdim row) per 16-byte operand, zero past the chunk. Lane
+// (li, lk) of a tile holds Delta[pt*16 + li][nt*16 + 4 lk .. +3]; the state is read and
+// written in that mapping, its loads issued before the window's. Each wave holds
+// kMfmaTiles tiles; a pass covers as many tiles as the waves hold (e4m3: whole rows only,
+// the row scale needs all of a row's tiles). Per-tile readout partials and row maxima go
+// through LDS and are summed in a fixed order.
+// Measured on MI355X (9B shape, B = 256, c = 64, fp32 cold), a full flush (32768 heads):
+// 965 us with the fp32 contraction, 810 us with this one. Tried and slower: one wave per
+// tile row (P / 16 waves per workgroup, 3 workgroups per CU, row scales and readouts
+// reduced in the wave) 1004 us; the window staged transposed and pre-split in LDS by the
+// workgroup (three bf16 copies of w B', token-contiguous rows) 1239 us.
 constexpr int kFlushWaves = 8;
 constexpr int kFlushPerCU = 2;  // flush workgroups per CU (the kernel's occupancy: 4 waves per SIMD)
 constexpr int kFlushList = 64;  // items a workgroup lists at a time
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+
+// The three bf16 parts of each of 8 fp32 values: hi = bf16(v), mid = bf16(v - hi),
+// lo = bf16(v - hi - mid), with hi + mid + lo == v exactly (each difference is exact in
+// fp32, and what is left after two 8-bit parts fits the third) for |v| above 2^-100.
+__device__ __forceinline__ void split3x8(const float (&v)[8], u4v& hi, u4v& mi, u4v& lo) {
+  uint32_t h[4], m[4], l[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float t[2];
+    h[j] = f32x2_to_bf16(v[2 * j], v[2 * j + 1]);
+    bf16x2_to_f32(h[j], t);
+    const float r0 = v[2 * j] - t[0], r1 = v[2 * j + 1] - t[1];
+    m[j] = f32x2_to_bf16(r0, r1);
+    bf16x2_to_f32(m[j], t);
+    l[j] = f32x2_to_bf16(r0 - t[0], r1 - t[1]);
+  }
+  hi = u4v{h[0], h[1], h[2], h[3]};
+  mi = u4v{m[0], m[1], m[2], m[3]};
+  lo = u4v{l[0], l[1], l[2], l[3]};
+}
 
 #define NSSM_GLOBAL(p) ((const __attribute__((address_space(1))) void*)(p))
 #define NSSM_LOCAL(p) ((__attribute__((address_space(3))) void*)(p))
@@ -1363,7 +1396,8 @@ __device__ __forceinline__ void stage_window_dma(float* sB, uint16_t* sX, float*
 // TF (the teacher-forced readout): y gets the readout of the new state as stored (the new
 // read copy; e4m3 partials formed after the row scale is known) instead of the old one's.
 template <int K, int COLD, bool TF = false>
-__global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
+__global__ void __launch_bounds__(kFlushWaves * 64) __attribute__((amdgpu_waves_per_eu(kFlushPerCU * kFlushWaves / 4)))
+flush_kernel(StepArgs a) {
   using C = Cfg<K, COLD>;
   constexpr int NC = C::NC, NT = C::NT, nw = kFlushWaves, nthr = kFlushWaves * 64;
   constexpr int TPP = C::E4M3 ? (nw * kMfmaTiles / NT) * NT : nw * kMfmaTiles;  // tiles per pass
@@ -1374,7 +1408,7 @@ __global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
   __shared__ int sItem[kFlushList], sSlot[kFlushList], sM[kFlushList];
   __shared__ float sDtot[kFlushList], sEg[kFlushList];
   __shared__ int sWave[kFlushWaves];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, lk = lane >> 4;
   const int H = a.H, P = a.P, c = a.c, G = a.G, HG = a.HG, fch = a.fch;
   const Ws ws(a.ws, a.b, H, G, c);
@@ -1504,26 +1538,47 @@ __global__ void __launch_bounds__(kFlushWaves * 64) flush_kernel(StepArgs a) {
             __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA has landed in LDS
             __syncthreads();
           }
-          // k-step s pairs token kk0 + lk of A = B'^T (16 n x 4 tokens) with the same token
-          // of B = w x (4 tokens x 16 p); the tiles' steps are independent
-          for (int kk0 = 0; kk0 < kn; kk0 += 4) {
-            const int kk = kk0 + lk;
-            const bool live = kk < kn;
-            const int kc = live ? kk : kn - 1;
-            const float wk = sW[kc];
-            float av[kMfmaTiles], bv[kMfmaTiles];
+          // 32-token k-steps of A = (w B')^T (16 n x 32 tokens) against B = x (32 tokens x 16 p):
+          // lane (li, lk) builds row / column li, tokens 8 lk .. 8 lk + 7 of each operand from
+          // the staged window (zero past the chunk), A as the three bf16 parts of v = w B'
+          // (hi + mid + lo == v), so the three bf16 products per token are exact and sum in
+          // fp32. The tiles' chains are independent.
+          for (int ks = 0; ks < kn; ks += 32) {
+            const int kb = ks + 8 * lk;
+            float wv[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) wv[j] = kb + j < kn ? sW[kb + j] : 0.f;
 #pragma unroll
             for (int i = 0; i < kMfmaTiles; ++i) {
               if (wave + i * nw < ntile) {  // wave-uniform
                 const int tt = t0 + wave + i * nw;
                 const int pt = tt / NT, nt = tt % NT;
-                av[i] = live ? sBc[kc * NC + nt * 16 + li] : 0.f;
-                bv[i] = live ? wk * bf2f(sX[kc * P + pt * 16 + li]) : 0.f;
-              }
-            }
+                // this lane's first window element of each operand; the empty asm keeps the
+                // compiler from turning the 8 per-token addresses of every tile into
+                // loop-carried registers (token j is then an immediate offset, j NC floats, or
+                // a scalar one, j P bf16)
+                int bo = kb * NC + nt * 16 + li, xo = kb * P + pt * 16 + li;
+                asm volatile("" : "+v"(bo), "+v"(xo));
+                float v[8];
+                uint32_t xw[4];
 #pragma unroll
-            for (int i = 0; i < kMfmaTiles; ++i)
-              if (wave + i * nw < ntile) acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], bv[i], acc[i], 0, 0, 0);
+                for (int j = 0; j < 8; ++j) {
+                  const bool live = kb + j < kn;
+                  v[j] = live ? wv[j] * sBc[bo + j * NC] : 0.f;
+                  const uint32_t xs = live ? sX[xo + j * P] : 0u;
+                  xw[j >> 1] = (j & 1) ? (xw[j >> 1] | (xs << 16)) : xs;
+                }
+                u4v hv, mv, lv;
+                split3x8(v, hv, mv, lv);
+                const bf16x8 xb = __builtin_bit_cast(bf16x8, (u4v{xw[0], xw[1], xw[2], xw[3]}));
+                acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, hv), xb, acc[i], 0, 0, 0);
+                acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, mv), xb, acc[i], 0, 0, 0);
+                acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, lv), xb, acc[i], 0, 0, 0);
+              }
+              // one tile's operands at a time: interleaving the tiles' builds costs more
+              // registers than the kernel's occupancy leaves
+              __builtin_amdgcn_sched_barrier(0);
+            }
           }
         }
         // new = total decay x old + Delta; readout partial of the old read copy
@@ -2291,7 +2346,6 @@ int v4_step(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step
 // the input as one 8 / 16-byte load and the output as one 8-byte store, so a wave
 // instruction carries 512 B of x / B / C instead of 128. Per channel the arithmetic is
 // conv_update_kernel's, in the same order.
-typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 template <int DT>
 __global__ void __launch_bounds__(256) conv_update4_kernel(ConvArgs a) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // 4-channel group
