@@ -230,36 +230,60 @@ def bench_v4(args, layers, inputs, dev):
     return ms_step, ms_launch, ms_ev, tier_gb
 
 
+DEPLOY_POINTS = [
+    # the v4-c4 storage points beyond the fp32 headline (scale/v4_fused_decode.py:149: the
+    # bf16 snapshot master; the reference bench's bf16 arm; the e4m3 deployment point)
+    ("v4 k32 c4 single bf16 copy, B=256", dict(B=256, cold="bf16", master="bf16")),
+    ("v4 k32 c4 e4m3 cold + bf16 master, B=256", dict(B=256, cold="fp8", master="bf16")),
+    ("v4 k32 c4 e4m3 cold + bf16 master, B=448", dict(B=448, cold="fp8", master="bf16")),
+    # the ragged continuous batch: 384 requests at random phases (each token flushes about
+    # B/c of them), fp32 cold
+    ("ragged B=384 k32 c16 fp32", dict(B=384, k=32, c=16, ragged=True)),
+    ("ragged B=384 k32 c64 fp32", dict(B=384, k=32, c=64, ragged=True)),
+    ("ragged B=384 k64 c16 fp32", dict(B=384, k=64, c=16, ragged=True)),
+    ("ragged B=384 k64 c64 fp32", dict(B=384, k=64, c=64, ragged=True)),
+]
+
+
 def bench_deploy(args, layers, inputs, dev, fresh_ms_256):
-    """The v4-c4 storage points beyond the fp32 headline, each against fresh at its own batch
-    size: one bf16 copy at B=256 (the bf16 snapshot master of scale/v4_fused_decode.py:149 and
-    the reference bench's bf16 arm) and e4m3 cold over a bf16 master at B=448 (the fp8
-    deployment point). Same layers, seeds and timing as the headline."""
+    """The deployment points of DEPLOY_POINTS, each against fresh at its own batch size.
+    Same layers, seeds and timing as the headline; fresh is measured once per batch size."""
     import copy
 
-    points = [("v4 k32 c4 single bf16 copy, B=256", dict(B=256, cold="bf16", master="bf16")),
-              ("v4 k32 c4 e4m3 cold + bf16 master, B=448", dict(B=448, cold="fp8", master="bf16"))]
     out = {}
-    for name, kw in points:
-        a = copy.copy(args)
-        a.__dict__.update(kw)
-        a.skip = 0.0
-        if a.B == 256:
-            inp, f_ms = inputs, fresh_ms_256
-        else:
-            inp = make_inputs(a.layers, a.B, dev, a.seed + 7)
-            log(f"deploy: fresh B={a.B} ...")
-            f_ms = bench_fresh(a, layers, inp, dev)[0]
-        log(f"deploy: {name} ...")
-        v_step, _, v_ev, _ = bench_v4(a, layers, inp, dev)
-        vb = a.B * bytes_v4_token(a.k, a.c, a.cold, a.master) + bytes_rotation()
-        out[name] = {"value": round(a.B / v_step * 1e3, 1), "unit": "state-op tokens/s",
-                     "ms_per_step": round(v_step, 4), "fresh_ms_per_step": round(f_ms, 4),
-                     "speedup_vs_fresh": round(f_ms / v_step, 3),
-                     "achieved_gbs": round(vb / (v_ev * 1e-3) / 1e9, 1),
-                     "frac": round(vb / (v_ev * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                     "algorithmic_bytes_per_launch": int(vb), "avg_launch_us_events": round(v_ev * 1e3, 2)}
-        log(f"deploy: {name}: {v_step:.3f} ms/step, {out[name]['speedup_vs_fresh']}x fresh")
+    fresh_ms = {256: fresh_ms_256}
+    by_b = {}
+    for name, kw in DEPLOY_POINTS:
+        by_b.setdefault(kw["B"], []).append((name, kw))
+    for B, pts in by_b.items():
+        inp = inputs if B == args.B else make_inputs(args.layers, B, dev, args.seed + 7)
+        if B not in fresh_ms:
+            a = copy.copy(args)
+            a.B = B
+            log(f"deploy: fresh B={B} ...")
+            fresh_ms[B] = bench_fresh(a, layers, inp, dev)[0]
+        for name, kw in pts:
+            a = copy.copy(args)
+            a.__dict__.update(kw)
+            if a.cold == "fp32":
+                a.master = "fp32"
+            a.skip = 0.0
+            if a.steps % a.c:
+                a.steps += a.c - a.steps % a.c
+            log(f"deploy: {name} ...")
+            v_step, _, v_ev, _ = bench_v4(a, layers, inp, dev)
+            vb = a.B * bytes_v4_token(a.k, a.c, a.cold, a.master) + bytes_rotation()
+            f_ms = fresh_ms[B]
+            out[name] = {"value": round(a.B / v_step * 1e3, 1), "unit": "state-op tokens/s",
+                         "ms_per_step": round(v_step, 4), "fresh_ms_per_step": round(f_ms, 4),
+                         "speedup_vs_fresh": round(f_ms / v_step, 3),
+                         "byte_bound_speedup": round(bytes_fresh_token() / bytes_v4_token(a.k, a.c, a.cold, a.master),
+                                                     3),
+                         "achieved_gbs": round(vb / (v_ev * 1e-3) / 1e9, 1),
+                         "frac": round(vb / (v_ev * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                         "algorithmic_bytes_per_launch": int(vb), "avg_launch_us_events": round(v_ev * 1e3, 2),
+                         "steps": a.steps}
+            log(f"deploy: {name}: {v_step:.3f} ms/step, {out[name]['speedup_vs_fresh']}x fresh")
         del inp
         torch.cuda.empty_cache()
     return out
@@ -332,6 +356,19 @@ def bench_prologue(args, dev):
     return res
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), as lscpu reports it."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
 def cpu_baseline(args, budget_s):
     """The oracle's reference step (full fp32 state updated every token, stale
     cold readout, scale/v4_native_decode.py semantics) on the host, one layer at
@@ -359,6 +396,7 @@ def cpu_baseline(args, budget_s):
         "value": round(B / (args.layers * t_layer), 2),
         "unit": "state-op tokens/s",
         "cores": threads,
+        "cpu": cpu_model(),
         "kind": "port",
         "sample": f"oracle NativeV4 step ({args.cold} cold, k={args.k}, c={args.c}"
                   f"{', exact readout' if args.exact else ''}{', hot-only readout' if args.coldoff else ''}"
@@ -369,16 +407,17 @@ def cpu_baseline(args, budget_s):
 
 def measured_traffic(key):
     """HBM bytes per layer-token measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
-    (calibrated against a plain copy) and recorded in profiles/*.md as
-    `traffic[<key>]: <bytes>`; None when no profile covers this workload."""
+    (calibrated against a plain copy) in an earlier profiled run of this workload and
+    recorded in profiles/*.md as `traffic[<key>]: <bytes>`: (bytes, that file), or
+    (None, None) when no profile covers it. Not measured in this run."""
     import glob
     import re
 
     for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*.md"))):
         for m in re.finditer(r"traffic\[(.*?)\]:\s*(\d+)", open(path).read()):
             if m.group(1) == key:
-                return int(m.group(2))
-    return None
+                return int(m.group(2)), os.path.relpath(path, ROOT)
+    return None, None
 
 
 def kernel_label(head, args):
@@ -498,7 +537,7 @@ def main():
                else f"query-gated tau={args.qgate:g}" if args.qgate > 0 else "stale")
     tkey = (f"v4 B={args.B} k={args.k} c={args.c} {args.cold}" + (" bf16-master" if args.master == "bf16" else "")
             + ("" if readout == "stale" else f" {readout}") if head == "v4" else f"fresh B={args.B}")
-    traffic = measured_traffic(tkey)
+    traffic, traffic_src = measured_traffic(tkey)
     out = {
         "metric": "state-op tokens/s at 9B shape B=256 (v4-c4 vs fresh); achieved HBM GB/s vs peak",
         "value": round(args.B / ms_step * 1e3, 1),
@@ -531,6 +570,8 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": traffic,
+            "traffic_source": (f"{traffic_src}: rocprofv3 FETCH_SIZE + WRITE_SIZE of an earlier profiled run of "
+                               f"this workload, scaled against a plain copy" if traffic_src else None),
             "kernel": kernel_label(head, args),
             "algorithmic_bytes_per_launch": int(per_launch_bytes),
             "avg_launch_us_events": round(ms_ev * 1e3, 2),
