@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define NSSM_ABI_VERSION 10
+#define NSSM_ABI_VERSION 11
 
 /* error codes */
 #define NSSM_OK 0
@@ -123,8 +123,8 @@ typedef struct nssm_step_inputs {
  *   t        int32 [slots][H]           decode steps (phase = t % c)
  *   nv       int32 [slots][H]           buffered tokens since the last snapshot
  *   glog     fp32 [slots][H]            log-decay since the snapshot, one token lagged
- * All heads of a slot carry equal t and nv. hot, cold, master and ring_b are
- * 16-byte aligned, ring_x 8-byte aligned.
+ * All heads of a slot carry equal t and nv. hot, cold, master, ring_x and ring_b
+ * are 16-byte aligned.
  * Unit-blocked (the bf16 read copies, the bf16 master): with row = (slot H + h) P + p,
  * element (row, col) sits at (row / 8) 8 NC + (col / 32) 256 + (row % 8) w + col % 32,
  * w = min(32, NC - 32 (col / 32)): the 8 rows of a unit form one block, 32-column segment

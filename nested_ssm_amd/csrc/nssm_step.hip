@@ -829,60 +829,70 @@ __device__ __forceinline__ float hot_update(const StepArgs& a, size_t row, int q
 // The exact readout's correction for row p of head (slot sh, request rh):
 // sum_j cw_j x_j[p] over the window j = 0 .. m-1, the buffered tokens at ring positions
 // pos - (m-1) + j and, last, this token (x = xcur); cw_j = w_j (C'_cold . B'_j) from the
-// prep kernel, scale/v4_native_decode.py:98-104. Lane q takes j = q, q + 8, ...; the
-// row's 8 lanes are summed with the rest of the readout. (Issuing these loads with the
-// unit's state loads costs more registers than the latency it hides.)
-// KU: window tokens per lane at most (the window is at most 8 KU long). The loads and the
-// sum are separate so a kernel with registers to spare issues the loads with its state loads.
-template <int KU>
+// prep kernel, scale/v4_native_decode.py:98-104. The window is at most 64 tokens, one per
+// lane: lane j loads the 16 bytes of buffered x token j holds for the wave's 8 rows
+// (p & ~7 ..) and its weight, and three exchange steps over lane bits 5, 4, 3 leave each
+// lane its own row's share of 8 of the 64 products (lane l's row is l >> 3); the row's 8
+// lanes are summed with the rest of the readout, lane q = 0 adding this token's term.
+// (Eight 2-byte loads per lane, token q + 8u for row p, ran the 9B-shape readout at c = 64
+// 10.6 ms against 7.9 for the stale one.) The loads and the sum are separate so a kernel
+// with registers to spare issues the loads with its state loads.
 struct CorrRaw {
-  float wv[KU], xv[KU];
+  uint4 xv;  // buffered x of window token `lane` for the wave's 8 rows (zero past m - 2)
+  float w;   // cw of window token `lane` (zero past m - 1)
 };
-template <int KU>
 __device__ __forceinline__ void corr_load(const StepArgs& a, const float* __restrict__ hd, size_t sh, size_t rh,
-                                          int p, int q, CorrRaw<KU>& cr) {
-  const int m = (int)hd[HD_M], P = a.P, c = a.c;
+                                          int p, int q, CorrRaw& cr) {
+  const int m = (int)hd[HD_M], P = a.P, c = a.c, lane = ((p & 7) << 3) | q;
   // window token j sits at ring position pos - (m - 1) + j
-  const uint16_t* rx0 = a.ring_x + (sh * c + ((int)hd[HD_POS] - (m - 1))) * P + p;
+  const uint16_t* rx = a.ring_x + (sh * c + ((int)hd[HD_POS] - (m - 1) + lane)) * P + (p & ~7);
   const float* cw = Ws(a.ws, a.b, a.H, a.G, c).cw + rh * c;
+  cr.w = lane < m ? cw[lane] : 0.f;
+  cr.xv = lane < m - 1 ? *reinterpret_cast<const uint4*>(rx) : make_uint4(0u, 0u, 0u, 0u);
+}
+__device__ __forceinline__ float corr_sum(const float* __restrict__ hd, int p, int q, const CorrRaw& cr, float xcur) {
+  const int m = (int)hd[HD_M], lane = ((p & 7) << 3) | q;
+  const uint32_t xw[4] = {cr.xv.x, cr.xv.y, cr.xv.z, cr.xv.w};
+  float v[8];  // w_j x_j[r] for the wave's rows r = 0 .. 7
 #pragma unroll
-  for (int u = 0; u < KU; ++u) {
-    const int j = q + 8 * u;
-    cr.wv[u] = j < m ? cw[j] : 0.f;
-    cr.xv[u] = j < m - 1 ? bf2f(rx0[(size_t)j * P]) : 0.f;
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = cr.w * __uint_as_float(xw[i] << 16);
+    v[2 * i + 1] = cr.w * __uint_as_float(xw[i] & 0xffff0000u);
   }
-}
-template <int KU>
-__device__ __forceinline__ float corr_sum(const float* __restrict__ hd, int q, const CorrRaw<KU>& cr, float xcur) {
-  const int m = (int)hd[HD_M];
-  float s = 0.f;
+  // keep the half of the rows whose bit matches the lane's, add the partner's share of it
+  const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
+  float s4[4], s2[2];
 #pragma unroll
-  for (int u = 0; u < KU; ++u) s = fmaf(cr.wv[u], q + 8 * u < m - 1 ? cr.xv[u] : xcur, s);
-  return s;
+  for (int i = 0; i < 4; ++i) s4[i] = (b5 ? v[4 + i] : v[i]) + __shfl_xor(b5 ? v[i] : v[4 + i], 32);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) s2[i] = (b4 ? s4[2 + i] : s4[i]) + __shfl_xor(b4 ? s4[i] : s4[2 + i], 16);
+  float s = (b3 ? s2[1] : s2[0]) + dpp<0x128>(b3 ? s2[0] : s2[1]);  // row_ror:8, lane ^ 8
+  // this token, window position m - 1 (cw from the lane that loaded it)
+  const float wl = m > 0 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cr.w), max(m, 1) - 1)) : 0.f;
+  return q == 0 ? fmaf(wl, xcur, s) : s;
 }
-template <int KU>
 __device__ __forceinline__ float corr_partial(const StepArgs& a, const float* __restrict__ hd, size_t sh, size_t rh,
                                               int p, int q, float xcur) {
-  CorrRaw<KU> cr;
-  corr_load<KU>(a, hd, sh, rh, p, q, cr);
-  return corr_sum<KU>(hd, q, cr, xcur);
+  CorrRaw cr;
+  corr_load(a, hd, sh, rh, p, q, cr);
+  return corr_sum(hd, p, q, cr, xcur);
 }
 
 // One unit of one token: hot columns, and (a head that does not flush at this token)
 // the stale readout of its cold read copy and the ring append of x. A flushing head's
 // cold columns are left to the flush kernel, which adds their readout to y.
 // PRE: the exact readout's correction loads were issued with the state (cr), else here.
-template <int K, int COLD, bool EXACT, int KU = kMaxC / 8, bool PRE = false>
+template <int K, int COLD, bool EXACT, bool PRE = false>
 __device__ __forceinline__ void unit_compute(const StepArgs& a, size_t sh, size_t rh, int p, int q,
                                              UnitRaw<K, COLD>& d, uint16_t* rx, bool cold, const float* __restrict__ hd,
-                                             const Coef<K, COLD>& k, const CorrRaw<KU>* cr = nullptr) {
+                                             const Coef<K, COLD>& k, const CorrRaw* cr = nullptr) {
   const size_t row = sh * a.P + p, yrow = rh * a.P + p;
   float part = hot_update<K, COLD>(a, row, q, d, hd, k);
   if constexpr (Cfg<K, COLD>::TIERED) {
     if (cold) part = fmaf(hd[HD_SNAPF], cold_partial<K, COLD>(d, k), part);
     if constexpr (EXACT) {
-      if constexpr (PRE) part += corr_sum<KU>(hd, q, *cr, d.xp);
-      else part += corr_partial<KU>(a, hd, sh, rh, p, q, d.xp);
+      if constexpr (PRE) part += corr_sum(hd, p, q, *cr, d.xp);
+      else part += corr_partial(a, hd, sh, rh, p, q, d.xp);
     }
   }
   part = sum8(part);
@@ -1097,7 +1107,7 @@ __device__ __forceinline__ void unit_compute_flush(const StepArgs& a, size_t sh,
     cold_store<COLD, CS, C::CH>(a, row, q, nvv, nvh);
   // the exact readout's correction, once the replay's registers are free (nothing else
   // adds to part in between, so the sum is the same)
-  if constexpr (EXACT) part += corr_partial<kFusedMaxWindow / 8>(a, hd, sh, rh, p, q, d.xp);
+  if constexpr (EXACT) part += corr_partial(a, hd, sh, rh, p, q, d.xp);
   part = sum8(part);
   if (q == 0) a.y[yrow] = fmaf(hd[HD_D], d.xp, part);
 }
@@ -1198,10 +1208,9 @@ __device__ __forceinline__ void unit_body(const StepArgs& a, const float* __rest
   unit_load<K, COLD>(a, row, rh * P + p, q, d, !FUSED && flushing);
   // the exact readout's correction: without the fused replay there are registers to issue
   // its loads now, beside the state's, instead of a second round trip after them
-  constexpr int kCorrU = (FUSED ? kFusedMaxWindow : kMaxC) / 8;
   constexpr bool kCorrPre = EXACT && !FUSED && TIERED;
-  CorrRaw<kCorrPre ? kCorrU : 1> cr;
-  if constexpr (kCorrPre) corr_load<kCorrU>(a, hd, sh, rh, p, q, cr);
+  CorrRaw cr;
+  if constexpr (kCorrPre) corr_load(a, hd, sh, rh, p, q, cr);
 
   const float* wB = ws.B + ((size_t)bi * a.G + g) * kN;
   const float* wC = ws.C + ((size_t)bi * a.G + g) * kN;
@@ -1226,12 +1235,10 @@ __device__ __forceinline__ void unit_body(const StepArgs& a, const float* __rest
   if constexpr (TIERED) {
     if (!flushing) rx = a.ring_x + (sh * c + (int)hd[HD_POS]) * P;
   }
-  // the stream kernel replays windows of at most kFusedMaxWindow tokens itself; the exact
-  // readout's correction then covers at most that many
   if constexpr (kCorrPre)
-    unit_compute<K, COLD, EXACT, kCorrU, true>(a, sh, rh, p, q, d, rx, !flushing, hd, k, &cr);
+    unit_compute<K, COLD, EXACT, true>(a, sh, rh, p, q, d, rx, !flushing, hd, k, &cr);
   else
-    unit_compute<K, COLD, EXACT, kCorrU>(a, sh, rh, p, q, d, rx, !flushing, hd, k);
+    unit_compute<K, COLD, EXACT>(a, sh, rh, p, q, d, rx, !flushing, hd, k);
 }
 
 template <int K, int COLD, bool FUSED, bool EXACT>
@@ -2229,7 +2236,7 @@ int check_tier(const nssm_tier* tr, bool need_ring) {
   if (tr->k_hot != 16 && tr->k_hot != 32 && tr->k_hot != 64 && tr->k_hot != 96) return NSSM_E_DIMS;
   if (!aligned16(tr->hot) || (cold && !aligned16(tr->cold)) || (tr->master && !aligned16(tr->master)))
     return NSSM_E_ALIGN;
-  if (cold && need_ring && (!aligned8(tr->ring_x) || !aligned16(tr->ring_b))) return NSSM_E_ALIGN;
+  if (cold && need_ring && (!aligned16(tr->ring_x) || !aligned16(tr->ring_b))) return NSSM_E_ALIGN;
   return NSSM_OK;
 }
 
