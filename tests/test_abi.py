@@ -183,6 +183,11 @@ def test_entry_points_validate_before_launching():
     assert L.nssm_v4_step_gated(*gargs, 0, float("inf"), None, None) == -2
     assert L.nssm_v4_step_gated(*gargs, 0, 0.5, fake + 4, None) == -3
     assert L.nssm_v4_step_gated(*gargs[:1], None, *gargs[2:], 1, 0.0, None, None) == -1
+    # the ring's x rows are read 16 bytes at a time: ring_x must be 16-byte aligned
+    ptrs = [fake] * 10
+    ptrs[4] = fake + 8
+    t8 = _lib.Tier(4, 32, 4, _lib.COLD_FP32, *ptrs)
+    assert L.nssm_v4_step(ctypes.byref(prm), ctypes.byref(t8), ctypes.byref(inp), fake, fake, 1 << 30, None) == -3
     assert L.nssm_set_launch(5) == -6
     assert L.nssm_set_launch(-1) == -6
     # 4 units per workgroup do not divide P / 8 = 10 rows blocks: refused before any launch
