@@ -10,6 +10,7 @@ JSON line (the driver contract); progress goes to stderr.
     python bench.py [--steps 64] [--warmup 8] [--B 256] [--c 4] [--k 32] [--cold fp32]
 """
 import argparse
+import dataclasses
 import json
 import os
 import sys
@@ -149,8 +150,11 @@ def per_launch_ms(launch_fn, n):
 
 
 def bench_fresh(args, layers, inputs, dev):
+    """The untiered update in the model's own basis, as the reference's fresh baselines run
+    (scale/bench_v4_decode.py:85-91, :236-254): no rotation of B and C (prep's identity path)."""
     from nested_ssm_amd import fresh_step
 
+    layers = [dataclasses.replace(lp, R=None) for lp in layers]
     g = torch.Generator(device=dev).manual_seed(args.seed + 1)
     states = [rand_state(args.B, dev, g) for _ in range(args.layers)]
     ys = [torch.empty(args.B, H, P, device=dev) for _ in range(args.layers)]
@@ -502,7 +506,7 @@ def main():
         log("fresh ...")
         f_step, f_launch, f_ev = bench_fresh(args, layers, inputs, dev)
         res["fresh"] = (f_step, f_launch, f_ev)
-        fb = args.B * bytes_fresh_token() + bytes_rotation()
+        fb = args.B * bytes_fresh_token()
         log(f"fresh: {f_step:.3f} ms/step, {args.B / f_step * 1e3:,.0f} tok/s, launch {f_ev * 1e3:.1f} us "
             f"-> {fb / (f_ev * 1e-3) / 1e9:,.0f} GB/s")
     if args.only != "fresh":
@@ -530,8 +534,8 @@ def main():
 
     head = "v4" if "v4" in res else "fresh"
     ms_step, ms_launch, ms_ev = res[head]
-    per_launch_bytes = args.B * (bytes_v4_token(args.k, args.c, args.cold, args.master, args.skip) if head == "v4"
-                                 else bytes_fresh_token()) + bytes_rotation()
+    per_launch_bytes = (args.B * bytes_v4_token(args.k, args.c, args.cold, args.master, args.skip) + bytes_rotation()
+                        if head == "v4" else args.B * bytes_fresh_token())
     achieved = per_launch_bytes / (ms_ev * 1e-3) / 1e9
     readout = ("exact" if args.exact else "hot-only" if args.coldoff
                else f"query-gated tau={args.qgate:g}" if args.qgate > 0 else "stale")
@@ -581,7 +585,7 @@ def main():
     if "fresh" in res and "v4" in res:
         out["fresh_tok_s"] = round(args.B / res["fresh"][0] * 1e3, 1)
         out["fresh_ms_per_step"] = round(res["fresh"][0], 4)
-        fb = args.B * bytes_fresh_token() + bytes_rotation()
+        fb = args.B * bytes_fresh_token()
         out["fresh_achieved_gbs"] = round(fb / (res["fresh"][2] * 1e-3) / 1e9, 1)
         out["speedup_v4_vs_fresh"] = round(res["fresh"][0] / res["v4"][0], 3)
     if deploy is not None:

@@ -1266,7 +1266,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(unit_t
 // within 8, a row mirror within 16, one swizzle across the two 16-lane halves). In-place RMW
 // at this shape ran 6.73 TB/s in a skeleton over a 1.34 GB buffer, against 6.40 with four
 // float4 per lane (the unit kernel's shape at K = N). Workgroups in request, head, row
-// order. The arithmetic per element is the hot update's.
+// order. The arithmetic per element is the hot update's. Measured at the 9B shape, B = 256
+// (414 us per launch): two row pairs per wave with the coefficients loaded once 444 us;
+// 4, 8, 16 or 40 consecutive workgroups on one XCD (whole y sectors per L2, so WRITE_SIZE
+// at the algorithmic bytes) 435-447 us; without prep (each wave computing its head's dt
+// and decay from the raw inputs, no rotation) 572 us.
 __global__ void __launch_bounds__(64) fresh_kernel(StepArgs a, const float* __restrict__ hd_ro) {
   const int lane = threadIdx.x, cl = lane & 31;
   const int H = a.H, P = a.P, np = P >> 1;

@@ -22,6 +22,8 @@ With a bf16 master the fp64 trajectory's cold columns are rounded to bf16 at the
 after every flush of a request, as the tier keeps them; the y and state bar is then the
 bf16 one (norm-wise 1e-4, at most 1% of the elements beyond the fp32 bar: the tier rounds
 its fp32 flush result, the reference the fp64 one, so isolated elements round apart)."""
+import dataclasses
+
 import pytest
 import torch
 
@@ -154,6 +156,27 @@ def test_config1_fresh_b256_64_steps():
         _, Cp, dx = ref.step(x, B, C, dt)
         assert_close32(y, ref.readout(Cp) + dx, f"fresh y step {step}")
     assert_close32(S, ref.S, "fresh final state")
+
+
+def test_config1_fresh_b256_without_rotation():
+    """Config 1 as the benchmark's fresh leg runs it: no rotation (prep's identity path),
+    B=256, 64 steps against the fp64 recurrence; on odd steps B and C sit 2 bytes off 8-byte
+    alignment."""
+    b = 256
+    prm = dataclasses.replace(_params(111), R=None)
+    g = torch.Generator(device=DEV).manual_seed(111)
+    S = torch.randn(b, H, P, N, device=DEV, generator=g).mul_(0.1)
+    ref = Fresh64(prm, S)
+    for step in range(64):
+        x, B, C, dt = _inputs(b, g)
+        if step % 2:
+            B = torch.cat([B.new_zeros(1), B.flatten()])[1:].view(b, G, N)
+            C = torch.cat([C.new_zeros(1), C.flatten()])[1:].view(b, G, N)
+            assert B.data_ptr() % 8 == 2 and C.data_ptr() % 8 == 2
+        y = fresh_step(prm, S, x, B, C, dt)
+        _, Cp, dx = ref.step(x, B, C, dt)
+        assert_close32(y, ref.readout(Cp) + dx, f"fresh (no rotation) y step {step}")
+    assert_close32(S, ref.S, "fresh (no rotation) final state")
 
 
 @pytest.mark.timeout(600)

@@ -173,9 +173,10 @@ def test_launch_shapes_agree(units, P):
         assert_close32(y, y_ref, f"fresh launch {units} units P={P} step {step}", **FP32_TOL)
 
 
-def test_out_of_range_slot_gives_nan_rows():
+@pytest.mark.parametrize("rotation", [True, False])
+def test_out_of_range_slot_gives_nan_rows(rotation):
     b, H, G, P = 2, 8, 1, 16
-    gen, prm, S0 = _setup(b, H, P, G, seed=1)
+    gen, prm, S0 = _setup(b, H, P, G, seed=1, rotation=rotation)
     dprm = dev_params(prm)
     (S_dev,) = to_dev(S0)
     x, B, C, dt = oracle.make_step_inputs(b, H, P, 128, G, gen)
@@ -183,6 +184,11 @@ def test_out_of_range_slot_gives_nan_rows():
     y = fresh_step(dprm, S_dev, *to_dev(x, B, C, dt), slot_ids=sl)
     assert torch.isnan(y[1]).all() and not torch.isnan(y[0]).any()
     assert torch.equal(S_dev[0].cpu(), S0[0])  # slot 0 untouched
+    # request 0 updated slot 1 as the oracle's step of that row does
+    S1 = S0[1:2].clone()
+    y_ref = oracle.fresh_step(S1, x[:1], B[:1], C[:1], dt[:1], prm)
+    assert_close32(y[:1], y_ref, "fresh slot-mapped y", **FP32_TOL)
+    assert_close32(S_dev[1:2], S1, "fresh slot-mapped state", **FP32_TOL)
 
 
 @pytest.mark.parametrize("k", [32, 64, 96])
