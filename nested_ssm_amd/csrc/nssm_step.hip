@@ -25,8 +25,11 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <atomic>
 #include <mutex>
+#include <set>
+#include <utility>
 
 #include "../../include/nssm.h"
 #include "nssm_formats.h"
@@ -38,7 +41,7 @@ constexpr int kMaxC = 64;
 constexpr int kFusedMaxWindow = 32;  // longest window the stream kernel replays itself
 constexpr int kMaxHG = 64;  // heads per group
 constexpr int kMaxUnitsPerWg = 4;  // waves (units) per stream workgroup
-constexpr int kMfmaTiles = 4;  // 16 x 16 flush-contraction tiles a wave keeps in registers
+constexpr int kMfmaTiles = 5;  // 16 x 16 flush-contraction tiles a wave keeps in registers
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2v __attribute__((ext_vector_type(2)));
@@ -73,6 +76,7 @@ struct StepArgs {
   int32_t tf;     // teacher-forced readout: inclusive decay; a flushing head reads its new state
   int32_t split;  // the flush kernel runs after the stream kernel (prep writes the pair flags)
   int32_t fch;    // window tokens the flush kernel stages in LDS at a time (multiple of 4)
+  int32_t fpipe;  // the flush kernel keeps two whole windows in LDS (stages the next item's early)
   float dt_min;
   // gated stale readout (no cold term for a skipped head): every head (hot_only), or the
   // heads whose query puts less than qgate_tau of its energy on the cold columns;
@@ -1369,39 +1373,57 @@ __device__ __forceinline__ void split3x8(const float (&v)[8], u4v& hi, u4v& mi, 
 #define NSSM_GLOBAL(p) ((const __attribute__((address_space(1))) void*)(p))
 #define NSSM_LOCAL(p) ((__attribute__((address_space(3))) void*)(p))
 
+// Bank swizzles of the staged window. The contraction's lane groups lk = 0 .. 3 (16 lanes
+// each; lanes 0-31 and 32-63 are served by the 32 LDS banks in separate cycles) read the
+// window tokens lk, lk + 4, ..., so lk = 0 and 1 read tokens of opposite parity. Within an
+// odd token the 16-byte granules of B' are XORed with 4 (16 floats: the other half of the
+// banks) when a token's B' spans whole 32-bank rows (NC % 32 == 0; NC % 32 == 16 offsets
+// odd tokens by itself), and the 4-byte granules of x with 8 (8 words) when P % 64 == 0.
+template <int NC>
+__host__ __device__ constexpr int flush_swz_b() { return NC % 32 == 0 ? 4 : 0; }
+__host__ __device__ constexpr int flush_swz_x(int P) { return P % 64 == 0 ? 8 : 0; }
+
 // Stage window tokens [k0, k0 + kn) of one head into LDS with gfx950's LDS DMA
 // (global_load_lds: lane L of a wave instruction writes its granule at base + L * size,
 // no registers in between): sB[e][n] = B'_tok[K + n] (16-byte granules), sX[e][p] =
-// x_tok[p] as bf16 (4-byte granules), sW[e] = w_tok. Window token m - 1 is this token
-// (B' from the workspace, x from the inputs); token tok < m - 1 sits at ring position
-// c - m + tok (rb0 and rx0 point at the ring rows of window token 0). Wave w issues the
-// instructions w, w + nw, ... of each block; the caller waits (vmcnt) and barriers.
+// x_tok[p] as bf16 (4-byte granules), both with the bank swizzles above (tok = k0 + e),
+// sW[e] = w_tok, and sC[n] = C'[K + n] of this token
+// (the readout's coefficients, read after the contraction). Window token m - 1 is this
+// token (B' from the workspace, x from the inputs); token tok < m - 1 sits at ring
+// position c - m + tok (rb0 and rx0 point at the ring rows of window token 0). Wave w
+// issues the instructions w, w + nw, ... of each block; the caller waits (vmcnt) and
+// barriers.
 template <int NC>
-__device__ __forceinline__ void stage_window_dma(float* sB, uint16_t* sX, float* sW, int k0, int kn, int m, int P,
-                                                 const float* rb0, const float* bcur, const uint16_t* rx0,
-                                                 const uint16_t* xcur, const float* wgt, int wave, int lane,
-                                                 int nw) {
+__device__ __forceinline__ void stage_window_dma(float* sB, uint16_t* sX, float* sW, float* sC, int k0, int kn,
+                                                 int m, int P, const float* rb0, const float* bcur,
+                                                 const uint16_t* rx0, const uint16_t* xcur, const float* wgt,
+                                                 const float* cq, int wave, int lane, int nw) {
   constexpr int NB4 = NC / 4;  // 16-byte granules per token of B'
   const int nb = kn * NB4;
   for (int q = wave; q * 64 < nb; q += nw) {
     const int gi = q * 64 + lane;
     if (gi < nb) {
       const int e = gi / NB4, tok = k0 + e;
-      const float* src = (tok < m - 1 ? rb0 + (size_t)tok * NC : bcur) + 4 * (gi - e * NB4);
+      const int gr = (gi - e * NB4) ^ (flush_swz_b<NC>() * (e & 1));  // the granule this slot holds
+      const float* src = (tok < m - 1 ? rb0 + (size_t)tok * NC : bcur) + 4 * gr;
       __builtin_amdgcn_global_load_lds(NSSM_GLOBAL(src), NSSM_LOCAL(sB + q * 256), 16, 0, 0);
     }
   }
   const int P2 = P >> 1, nx = kn * P2;  // 4-byte granules (2 x bf16) per token of x
+  const int swx = flush_swz_x(P);
   for (int q = wave; q * 64 < nx; q += nw) {
     const int gi = q * 64 + lane;
     if (gi < nx) {
       const int e = gi / P2, tok = k0 + e;
-      const uint16_t* src = (tok < m - 1 ? rx0 + (size_t)tok * P : xcur) + 2 * (gi - e * P2);
+      const int gr = (gi - e * P2) ^ (swx * (e & 1));
+      const uint16_t* src = (tok < m - 1 ? rx0 + (size_t)tok * P : xcur) + 2 * gr;
       __builtin_amdgcn_global_load_lds(NSSM_GLOBAL(src), NSSM_LOCAL(sX + q * 128), 4, 0, 0);
     }
   }
   if (wave == nw - 1 && lane < kn)
     __builtin_amdgcn_global_load_lds(NSSM_GLOBAL(wgt + k0 + lane), NSSM_LOCAL(sW), 4, 0, 0);
+  if (wave == nw - 2 && lane < NC / 4)
+    __builtin_amdgcn_global_load_lds(NSSM_GLOBAL(cq + 4 * lane), NSSM_LOCAL(sC), 16, 0, 0);
 }
 
 // TF (the teacher-forced readout): y gets the readout of the new state as stored (the new
@@ -1411,8 +1433,11 @@ __global__ void __launch_bounds__(kFlushWaves * 64) __attribute__((amdgpu_waves_
 flush_kernel(StepArgs a) {
   using C = Cfg<K, COLD>;
   constexpr int NC = C::NC, NT = C::NT, nw = kFlushWaves, nthr = kFlushWaves * 64;
-  constexpr int TPP = C::E4M3 ? (nw * kMfmaTiles / NT) * NT : nw * kMfmaTiles;  // tiles per pass
-  static_assert(TPP >= NT, "a pass must hold a whole row");
+  // work units: (n-tile, block of ptw consecutive p-tiles), one per wave and pass; the
+  // blocks are as many as fill the waves (at most kMfmaTiles p-tiles each), and an e4m3
+  // pass holds whole blocks (its row scales need every n-tile of a row)
+  constexpr int UPP = C::E4M3 ? (nw / NT) * NT : nw;  // units per pass
+  static_assert(UPP >= NT, "a pass must hold a whole row");
   extern __shared__ float lds[];
   // this workgroup's listed items and their scalars (loaded by the thread that lists
   // the item); sM = 0 marks an item with nothing to flush
@@ -1423,12 +1448,17 @@ flush_kernel(StepArgs a) {
   const int li = lane & 15, lk = lane >> 4;
   const int H = a.H, P = a.P, c = a.c, G = a.G, HG = a.HG, fch = a.fch;
   const Ws ws(a.ws, a.b, H, G, c);
-  float* sBc = lds;                                             // [fch][NC] B'
-  uint16_t* sX = reinterpret_cast<uint16_t*>(sBc + fch * NC);   // [fch][P] x (bf16)
-  float* sW = sBc + fch * NC + fch * P / 2;                     // [fch] window weights
-  float* sPart = sW + fch;       // [P][NT] readout partials of the old read copy
-  float* sAmx = sPart + P * NT;  // [P][NT] row maxima of the new values (e4m3 only)
-  const int ntot = (P / 16) * NT;
+  // window buffer: [fch][NC] B', [fch][P] x (bf16), [fch] weights; two of them when the
+  // next item's window is staged during this one's contraction (then every window is
+  // whole, m <= c <= fch)
+  const bool pipe = a.fpipe != 0;
+  const int wfl = fch * NC + fch * P / 2 + fch + NC;  // floats per window buffer (+ C'[K:])
+  const int nbuf = pipe ? 2 : 1;
+  float* sPart0 = lds + nbuf * wfl;        // [nbuf][P][NT] readout partials of the old read copy
+  float* sAmx = sPart0 + nbuf * P * NT;    // [P][NT] row maxima of the new values (e4m3 only)
+  const int PT = P / 16;
+  const int nblk0 = max((PT + kMfmaTiles - 1) / kMfmaTiles, min(PT, nw / NT));
+  const int ptw = (PT + nblk0 - 1) / nblk0, nunit = NT * ((PT + ptw - 1) / ptw);
 
   // 1. rank the flagged pairs: thread tid counts pairs [p0, p1) (whole int4 words of
   // the flag array, which is padded to a multiple of 4), then a block-wide exclusive
@@ -1491,10 +1521,35 @@ flush_kernel(StepArgs a) {
     }
     __syncthreads();
 
-    // 3. the listed items
-    for (int k = 0; k < jn; ++k) {
-      const int m = sM[k];
-      if (m == 0) continue;  // workgroup-uniform
+    // 3. the listed items. Staging of item kk's whole window (tokens 0 .. m-1) into buffer
+    // bf: window token m - 1 is this token (B' from the workspace, x from the inputs),
+    // token i < m - 1 sits at ring position c - m + i.
+    auto stage_item = [&](int kk, int bf) {
+      const int m2 = sM[kk], it2 = sItem[kk], sl2 = sSlot[kk];
+      const int b2 = it2 / H, h2 = it2 - b2 * H, g2 = h2 / HG;
+      float* wb = lds + bf * wfl;
+      stage_window_dma<NC>(wb, reinterpret_cast<uint16_t*>(wb + fch * NC), wb + fch * NC + fch * P / 2,
+                           wb + fch * NC + fch * P / 2 + fch, 0, m2, m2, P,
+                           a.ring_b + (((size_t)sl2 * G + g2) * c + (c - m2)) * NC,
+                           ws.B + ((size_t)b2 * G + g2) * kN + K,
+                           a.ring_x + (((size_t)sl2 * H + h2) * c + (c - m2)) * P, a.x + (size_t)it2 * P,
+                           ws.w + (size_t)it2 * c, ws.C + ((size_t)b2 * G + g2) * kN + K, wave, lane, nw);
+    };
+    auto next_item = [&](int kk) {  // the first listed item from kk on with a window
+      while (kk < jn && sM[kk] == 0) ++kk;
+      return kk;
+    };
+    int buf = 0;
+    if (pipe) {  // the first window, staged before the loop
+      const int k1 = next_item(0);
+      if (k1 < jn) {
+        stage_item(k1, 0);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+      }
+    }
+    for (int k = next_item(0); k < jn; k = next_item(k + 1)) {
+      const int m = sM[k];  // > 0: workgroup-uniform
       const int it = sItem[k], slot = sSlot[k];
       const float dtot = sDtot[k], eg = sEg[k];
       const int bi = it / H, h = it - bi * H, g = h / HG;
@@ -1507,13 +1562,27 @@ flush_kernel(StepArgs a) {
       const uint16_t* xcur = a.x + (size_t)it * P;
       const float* wgt = ws.w + (size_t)it * c;
       const size_t row0 = ((size_t)slot * H + h) * P;
+      float* sBc = lds + buf * wfl;
+      uint16_t* sX = reinterpret_cast<uint16_t*>(sBc + fch * NC);
+      float* sW = sBc + fch * NC + fch * P / 2;
+      const float* sCq = sW + fch;  // C'[K:]
+      float* sPart = sPart0 + buf * P * NT;
       // the values the flush starts from: the single copy, or the master (fp32 or bf16)
       const void* src = C::SEG ? static_cast<const void*>(a.cold) : static_cast<const void*>(a.master);
       constexpr bool SRC16 = COLD == NSSM_COLD_BF16_SINGLE || C::MASTER16;
       const bool whole = m <= fch;  // the window fits in LDS: staged once
 
-      for (int t0 = 0; t0 < ntot; t0 += TPP) {
-        const int ntile = min(TPP, ntot - t0);
+      // the next item's window goes to the other buffer during this item's contraction (the
+      // previous item's last barrier ordered every wave's reads of that buffer before it)
+      if (pipe) {
+        const int knext = next_item(k + 1);
+        if (knext < jn) stage_item(knext, buf ^ 1);
+      }
+      for (int u0 = 0; u0 < nunit; u0 += UPP) {
+        // this wave's work unit in the pass: n-tile nt, p-tiles pt0 .. pt0 + npt - 1
+        const int u = u0 + wave;
+        const bool act = wave < UPP && u < nunit;  // wave-uniform
+        const int nt = u % NT, pt0 = (u / NT) * ptw, npt = act ? min(ptw, PT - pt0) : 0;
         // the pass's state tiles are loaded before the window
         f4 old[kMfmaTiles];
         u2v old16[SRC16 ? kMfmaTiles : 1];
@@ -1522,10 +1591,9 @@ flush_kernel(StepArgs a) {
         float rsc[C::E4M3 ? kMfmaTiles : 1];
 #pragma unroll
         for (int i = 0; i < kMfmaTiles; ++i) {
-          const int tt = t0 + wave + i * nw;
-          if (wave + i * nw < ntile) {
-            const size_t row = row0 + (tt / NT) * 16 + li;
-            const int col = (tt % NT) * 16 + 4 * lk;
+          if (i < npt) {
+            const size_t row = row0 + (pt0 + i) * 16 + li;
+            const int col = nt * 16 + 4 * lk;
             if constexpr (SRC16)
               old16[i] = ld_stream(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(src) + blk16(row, col, NC)));
             else
@@ -1543,9 +1611,9 @@ flush_kernel(StepArgs a) {
         for (int i = 0; i < kMfmaTiles; ++i) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
         for (int k0 = 0; k0 < m; k0 += fch) {
           const int kn = min(fch, m - k0);
-          if (!whole || t0 == 0) {  // a whole window is staged once, in the first pass
+          if (!pipe && (!whole || u0 == 0)) {  // a whole window is staged once, in the first pass
             __syncthreads();  // the previous chunk (or item: window and partials) is consumed
-            stage_window_dma<NC>(sBc, sX, sW, k0, kn, m, P, rb0, bcur, rx0, xcur, wgt, wave, lane, nw);
+            stage_window_dma<NC>(sBc, sX, sW, sW + fch, k0, kn, m, P, rb0, bcur, rx0, xcur, wgt, cq0, wave, lane, nw);
             __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA has landed in LDS
             __syncthreads();
           }
@@ -1554,53 +1622,52 @@ flush_kernel(StepArgs a) {
           // the staged window (zero past the chunk), A as the three bf16 parts of v = w B'
           // (hi + mid + lo == v), so the three bf16 products per token are exact and sum in
           // fp32. The tiles' chains are independent.
-          for (int ks = 0; ks < kn; ks += 32) {
-            const int kb = ks + 8 * lk;
-            float wv[8];
+          for (int ks = 0; act && ks < kn; ks += 32) {
+            // lane group lk takes the chunk's tokens kb + 4 j, j = 0 .. 7, in both operands
+            // (any assignment of tokens to k that A and B share gives the same product)
+            const int kb = ks + lk, odd = lk & 1;
+            // A, once per step for all of the wave's tiles (they share the n-tile): this
+            // lane's row li of w B' over its 8 tokens, through the bank swizzle (token
+            // kb + 4 j has kb's parity); the empty asm keeps the compiler from turning the
+            // per-token addresses into loop-carried registers (token j is then an immediate
+            // offset, 4 j NC floats, or a scalar one, 4 j P bf16)
+            int bo = kb * NC + 4 * ((4 * nt + (li >> 2)) ^ (flush_swz_b<NC>() * odd)) + (li & 3);
+            asm volatile("" : "+v"(bo));
+            float v[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) wv[j] = kb + j < kn ? sW[kb + j] : 0.f;
+            for (int j = 0; j < 8; ++j) {
+              const bool live = kb + 4 * j < kn;
+              v[j] = live ? sW[kb + 4 * j] * sBc[bo + 4 * j * NC] : 0.f;
+            }
+            u4v hv, mv, lv;
+            split3x8(v, hv, mv, lv);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < kMfmaTiles; ++i) {
-              if (wave + i * nw < ntile) {  // wave-uniform
-                const int tt = t0 + wave + i * nw;
-                const int pt = tt / NT, nt = tt % NT;
-                // this lane's first window element of each operand; the empty asm keeps the
-                // compiler from turning the 8 per-token addresses of every tile into
-                // loop-carried registers (token j is then an immediate offset, j NC floats, or
-                // a scalar one, j P bf16)
-                int bo = kb * NC + nt * 16 + li, xo = kb * P + pt * 16 + li;
-                asm volatile("" : "+v"(bo), "+v"(xo));
-                float v[8];
+              if (i < npt) {  // wave-uniform
+                int xo = kb * P + 2 * ((8 * (pt0 + i) + (li >> 1)) ^ (flush_swz_x(P) * odd)) + (li & 1);
+                asm volatile("" : "+v"(xo));
                 uint32_t xw[4];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                  const bool live = kb + j < kn;
-                  v[j] = live ? wv[j] * sBc[bo + j * NC] : 0.f;
-                  const uint32_t xs = live ? sX[xo + j * P] : 0u;
+                  const uint32_t xs = kb + 4 * j < kn ? sX[xo + 4 * j * P] : 0u;
                   xw[j >> 1] = (j & 1) ? (xw[j >> 1] | (xs << 16)) : xs;
                 }
-                u4v hv, mv, lv;
-                split3x8(v, hv, mv, lv);
                 const bf16x8 xb = __builtin_bit_cast(bf16x8, (u4v{xw[0], xw[1], xw[2], xw[3]}));
                 acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, hv), xb, acc[i], 0, 0, 0);
                 acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, mv), xb, acc[i], 0, 0, 0);
                 acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, lv), xb, acc[i], 0, 0, 0);
               }
-              // one tile's operands at a time: interleaving the tiles' builds costs more
-              // registers than the kernel's occupancy leaves
-              __builtin_amdgcn_sched_barrier(0);
             }
           }
         }
         // new = total decay x old + Delta; readout partial of the old read copy
 #pragma unroll
         for (int i = 0; i < kMfmaTiles; ++i) {
-          if (wave + i * nw < ntile) {
-            const int tt = t0 + wave + i * nw;
-            const int pt = tt / NT, nt = tt % NT;
-            const int p = pt * 16 + li, col = nt * 16 + 4 * lk;
+          if (i < npt) {
+            const int p = (pt0 + i) * 16 + li, col = nt * 16 + 4 * lk;
             const size_t row = row0 + p;
-            const f4 cq = *reinterpret_cast<const f4*>(cq0 + col);
+            const f4 cq = *reinterpret_cast<const f4*>(sCq + col);
             if constexpr (SRC16) {
               float o4[4];
               bf16x4_to_f32(old16[i], o4);
@@ -1665,14 +1732,13 @@ flush_kernel(StepArgs a) {
             }
           }
         }
-        __syncthreads();  // partials and row maxima of this pass's tiles
+        if (pipe) __builtin_amdgcn_s_waitcnt(0);  // this wave's part of the next window has landed
+        __syncthreads();  // partials and row maxima of this pass's tiles (and the next window)
         if constexpr (C::E4M3) {
 #pragma unroll
           for (int i = 0; i < kMfmaTiles; ++i) {
-            if (wave + i * nw < ntile) {
-              const int tt = t0 + wave + i * nw;
-              const int pt = tt / NT, nt = tt % NT;
-              const int p = pt * 16 + li;
+            if (i < npt) {
+              const int p = (pt0 + i) * 16 + li;
               const size_t row = row0 + p;
               float am = 0.f;
 #pragma unroll
@@ -1686,7 +1752,7 @@ flush_kernel(StepArgs a) {
               if constexpr (TF) {  // the readout of the new e4m3 copy
                 float rd[4];
                 fp8x4_to_f32(codes, rd);
-                const f4 cq = *reinterpret_cast<const f4*>(cq0 + nt * 16 + 4 * lk);
+                const f4 cq = *reinterpret_cast<const f4*>(sCq + nt * 16 + 4 * lk);
                 float pc = rd[0] * cq.x;
                 pc = fmaf(rd[1], cq.y, pc);
                 pc = fmaf(rd[2], cq.z, pc);
@@ -1700,14 +1766,15 @@ flush_kernel(StepArgs a) {
           if constexpr (TF) __syncthreads();  // the partials of this pass's tiles
         }
       }
-      // y += exp(glog) (stale cold readout); the next item's first barrier orders
-      // these reads before sPart is written again
+      // y += exp(glog) (stale cold readout); the next item's first barrier (pipelined:
+      // its last, before this buffer of partials is written again) orders these reads
       if (tid < P) {
         float pc = 0.f;
 #pragma unroll
         for (int t2 = 0; t2 < NT; ++t2) pc += sPart[tid * NT + t2];
         a.y[(size_t)it * P + tid] = fmaf(eg, pc, yv);
       }
+      if (pipe) buf ^= 1;
     }
   }
 }
@@ -2082,6 +2149,10 @@ __global__ void __launch_bounds__(64) gated_norm_wave_kernel(NormArgs a) {
 // ---------------------------------------------------------------------------
 // host side
 int g_units_override = 0;  // units (waves) per stream workgroup, 0 = automatic
+#ifndef NSSM_FLUSH_PIPE
+#define NSSM_FLUSH_PIPE 1
+#endif
+constexpr bool g_flush_pipe = NSSM_FLUSH_PIPE;  // stage the next flush item's window early when two fit
 constexpr size_t kMaxLds = 64 * 1024;
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -2150,13 +2221,48 @@ int cu_count() {
 }
 
 
-// flush kernel LDS: a window chunk of fch tokens (B' fp32, x bf16, weights), per-tile
-// readout partials (+ e4m3 row maxima); the kernel's own lists take under 2 KB more
-size_t flush_lds_bytes(int P, int K, int kind, int fch) {
+// flush kernel LDS: a window buffer of fch tokens (B' fp32, x bf16, weights) and C'[K:]
+// with its per-tile readout partials, two of each when pipelined, (+ e4m3 row maxima);
+// the kernel's own lists take under 2 KB more
+size_t flush_lds_bytes(int P, int K, int kind, int fch, bool pipe = false) {
   const int NC = kN - K;
   const size_t tiles = (size_t)P * (NC / 16);
   const bool e4m3 = kind == NSSM_COLD_FP8 || kind == NSSM_COLD_FP8_BF16M;  // + row maxima
-  return ((size_t)fch * NC + (size_t)fch * P / 2 + fch + tiles * (e4m3 ? 2 : 1)) * sizeof(float);
+  const size_t buf = (size_t)fch * NC + (size_t)fch * P / 2 + fch + NC + tiles;
+  return ((pipe ? 2 : 1) * buf + (e4m3 ? tiles : 0)) * sizeof(float);
+}
+// LDS a flush workgroup may take: the device's per-workgroup limit, and a CU's LDS shared
+// by the kFlushPerCU resident workgroups
+size_t flush_lds_limit() {
+  static size_t cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return kMaxLds;
+  if (cache[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+      v = (int)kMaxLds;
+    cache[dev] = std::min((size_t)v, (size_t)160 * 1024 / kFlushPerCU);
+  }
+  return cache[dev];
+}
+// whether two whole windows of c tokens fit (the flush kernel then stages each item's
+// window during the previous item's contraction)
+bool flush_pipe(int P, int K, int kind, int c) {
+  return flush_lds_bytes(P, K, kind, (c + 3) & ~3, true) + 2048 <= flush_lds_limit();
+}
+// a kernel launched with more than 64 KB of dynamic LDS declares it first (once per
+// kernel and device)
+bool lds_opt_in(const void* fn) {
+  static std::mutex mu;
+  static std::set<std::pair<int, const void*>> done;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return false;
+  std::lock_guard<std::mutex> lk(mu);
+  if (done.count({dev, fn})) return true;
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)flush_lds_limit()) != hipSuccess)
+    return false;
+  done.insert({dev, fn});
+  return true;
 }
 // window tokens the flush kernel stages at a time: the whole window (c rounded up to the
 // matrix-core step of 4 tokens) when it fits, else the most that fit (0: none fit)
@@ -2288,12 +2394,16 @@ int launch_pair(const StepArgs& a, const Launch& L, hipStream_t st) {
     const int items = a.b * a.H, cap = kFlushPerCU * cu_count();
     int grid = items < cap ? items : cap;
     if (grid < a.HG) grid = a.HG;  // the kernel's listing needs grid >= HG (items >= HG)
-    if (a.tf)
-      hipLaunchKernelGGL((flush_kernel<K, COLD, true>), dim3((unsigned)grid), dim3(kFlushWaves * 64),
-                         flush_lds_bytes(a.P, K, COLD, a.fch), st, a);
-    else
-      hipLaunchKernelGGL((flush_kernel<K, COLD>), dim3((unsigned)grid), dim3(kFlushWaves * 64),
-                         flush_lds_bytes(a.P, K, COLD, a.fch), st, a);
+    const size_t flds = flush_lds_bytes(a.P, K, COLD, a.fch, a.fpipe != 0);
+    if (a.tf) {
+      if (flds > kMaxLds && !lds_opt_in(reinterpret_cast<const void*>(&flush_kernel<K, COLD, true>)))
+        return NSSM_E_LAUNCH;
+      hipLaunchKernelGGL((flush_kernel<K, COLD, true>), dim3((unsigned)grid), dim3(kFlushWaves * 64), flds, st, a);
+    } else {
+      if (flds > kMaxLds && !lds_opt_in(reinterpret_cast<const void*>(&flush_kernel<K, COLD>)))
+        return NSSM_E_LAUNCH;
+      hipLaunchKernelGGL((flush_kernel<K, COLD>), dim3((unsigned)grid), dim3(kFlushWaves * 64), flds, st, a);
+    }
   } else if constexpr (K == kN) {  // untiered
     hipLaunchKernelGGL(fresh_kernel, dim3((unsigned)((size_t)a.b * a.H * (a.P / 2))), dim3(64), 0, st, a, hd_ro);
   } else {
@@ -2341,6 +2451,8 @@ int v4_step(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step
   if ((rc = pick_launch(prm->P, tier->k_hot, tier->c, &L, tier->cold_kind))) return rc;
   a.split = !L.fused && tier->cold_kind != NSSM_COLD_NONE;
   a.fch = a.split ? flush_chunk(prm->P, tier->k_hot, tier->cold_kind, tier->c) : 0;
+  a.fpipe = a.split && g_flush_pipe && flush_pipe(prm->P, tier->k_hot, tier->cold_kind, tier->c);
+  if (a.fpipe) a.fch = (tier->c + 3) & ~3;
   hipStream_t st = (hipStream_t)stream;
   switch (tier->k_hot) {
     case 16: return dispatch_kind<16>(a, tier->cold_kind, L, st);
