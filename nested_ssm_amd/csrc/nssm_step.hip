@@ -1320,9 +1320,10 @@ __global__ void __launch_bounds__(64) fresh_kernel(StepArgs a, const float* __re
 //
 // Work split: prep flags each (request, group) pair with a flushing head. Every
 // workgroup ranks the flagged pairs (a block-wide prefix count over the flags) and
-// takes the flushing items j * gridDim.x + blockIdx.x of the ranked order (pair rank
-// r covers items r HG .. r HG + HG - 1, one per head), so F flushing heads spread
-// over min(F, grid) workgroups whatever the requests' phases.
+// takes a contiguous range of the ranked items (pair rank r covers items r HG .. r HG +
+// HG - 1, one per head), so F flushing heads spread over min(F, grid) workgroups whatever
+// the requests' phases, and a workgroup flushes the heads of a pair one after another
+// (their shared B' window and C' are staged once).
 //
 // Delta is contracted on the matrix cores as 16 x 16 tiles (p-tile pt, n-tile nt) of
 // v_mfma_f32_16x16x32_bf16: A = (w B')^T (16 n x 32 tokens), B = x (32 tokens x 16 p). x
@@ -1392,14 +1393,14 @@ __host__ __device__ constexpr int flush_swz_x(int P) { return P % 64 == 0 ? 8 : 
 // token (B' from the workspace, x from the inputs); token tok < m - 1 sits at ring
 // position c - m + tok (rb0 and rx0 point at the ring rows of window token 0). Wave w
 // issues the instructions w, w + nw, ... of each block; the caller waits (vmcnt) and
-// barriers.
+// barriers. withB = false leaves B' and C' as they are (the buffer holds this pair's).
 template <int NC>
 __device__ __forceinline__ void stage_window_dma(float* sB, uint16_t* sX, float* sW, float* sC, int k0, int kn,
                                                  int m, int P, const float* rb0, const float* bcur,
                                                  const uint16_t* rx0, const uint16_t* xcur, const float* wgt,
-                                                 const float* cq, int wave, int lane, int nw) {
+                                                 const float* cq, int wave, int lane, int nw, bool withB) {
   constexpr int NB4 = NC / 4;  // 16-byte granules per token of B'
-  const int nb = kn * NB4;
+  const int nb = withB ? kn * NB4 : 0;
   for (int q = wave; q * 64 < nb; q += nw) {
     const int gi = q * 64 + lane;
     if (gi < nb) {
@@ -1409,20 +1410,32 @@ __device__ __forceinline__ void stage_window_dma(float* sB, uint16_t* sX, float*
       __builtin_amdgcn_global_load_lds(NSSM_GLOBAL(src), NSSM_LOCAL(sB + q * 256), 16, 0, 0);
     }
   }
-  const int P2 = P >> 1, nx = kn * P2;  // 4-byte granules (2 x bf16) per token of x
-  const int swx = flush_swz_x(P);
-  for (int q = wave; q * 64 < nx; q += nw) {
+  // x: the buffered tokens of the chunk in 16-byte granules (8 bf16; ring rows are
+  // 16-byte aligned), this token (window token m - 1, from the inputs) in 4-byte ones; the
+  // bank swizzle is the same XOR in either unit (8 words)
+  const int P8 = P >> 3, swx = flush_swz_x(P);
+  const int nxr = max(0, min(kn, m - 1 - k0)) * P8;
+  for (int q = wave; q * 64 < nxr; q += nw) {
     const int gi = q * 64 + lane;
-    if (gi < nx) {
-      const int e = gi / P2, tok = k0 + e;
-      const int gr = (gi - e * P2) ^ (swx * (e & 1));
-      const uint16_t* src = (tok < m - 1 ? rx0 + (size_t)tok * P : xcur) + 2 * gr;
-      __builtin_amdgcn_global_load_lds(NSSM_GLOBAL(src), NSSM_LOCAL(sX + q * 128), 4, 0, 0);
+    if (gi < nxr) {
+      const int e = gi / P8;
+      const int gr = (gi - e * P8) ^ ((swx >> 2) * (e & 1));
+      __builtin_amdgcn_global_load_lds(NSSM_GLOBAL(rx0 + (size_t)(k0 + e) * P + 8 * gr), NSSM_LOCAL(sX + q * 512),
+                                       16, 0, 0);
+    }
+  }
+  if (wave == nw - 3 && m - 1 >= k0 && m - 1 < k0 + kn) {
+    const int e = m - 1 - k0, P2 = P >> 1;
+    for (int q = 0; q * 64 < P2; ++q) {
+      const int gi = q * 64 + lane;
+      if (gi < P2)
+        __builtin_amdgcn_global_load_lds(NSSM_GLOBAL(xcur + 2 * (gi ^ (swx * (e & 1)))),
+                                         NSSM_LOCAL(sX + e * P + q * 128), 4, 0, 0);
     }
   }
   if (wave == nw - 1 && lane < kn)
     __builtin_amdgcn_global_load_lds(NSSM_GLOBAL(wgt + k0 + lane), NSSM_LOCAL(sW), 4, 0, 0);
-  if (wave == nw - 2 && lane < NC / 4)
+  if (withB && wave == nw - 2 && lane < NC / 4)
     __builtin_amdgcn_global_load_lds(NSSM_GLOBAL(cq + 4 * lane), NSSM_LOCAL(sC), 16, 0, 0);
 }
 
@@ -1443,6 +1456,7 @@ flush_kernel(StepArgs a) {
   // the item); sM = 0 marks an item with nothing to flush
   __shared__ int sItem[kFlushList], sSlot[kFlushList], sM[kFlushList];
   __shared__ float sDtot[kFlushList], sEg[kFlushList];
+  __shared__ int sPairOf[kFlushList + 1];  // the pairs of a list's ranks
   __shared__ int sWave[kFlushWaves];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, lk = lane >> 4;
@@ -1487,37 +1501,44 @@ flush_kernel(StepArgs a) {
     total += s;
   }
   const int64_t fitems = (int64_t)total * HG;  // heads of flagged pairs
-  const int bx = blockIdx.x, grid = gridDim.x;  // grid >= HG (host)
-  const int nmine = fitems > bx ? (int)((fitems - bx + grid - 1) / grid) : 0;
+  // each workgroup takes a contiguous range of the ranked items (consecutive heads of a
+  // pair in a row: the pair's B' window is staged once for them)
+  const int bx = blockIdx.x, grid = gridDim.x;
+  const int64_t per_wg = (fitems + grid - 1) / grid;
+  const int64_t ilo = min((int64_t)bx * per_wg, fitems);
+  const int nmine = (int)(min(ilo + per_wg, fitems) - ilo);
+  int bkey0 = -1, bkey1 = -1;  // the pair whose B' and C' each window buffer holds (-1: none)
 
   for (int j0 = 0; j0 < nmine; j0 += kFlushList) {
     const int jn = min(kFlushList, nmine - j0);
     __syncthreads();  // the previous list is consumed
-    // 2. list items j0 .. j0 + jn - 1: pair rank r holds item j when
-    // r HG <= j grid + bx < (r + 1) HG (at most one j per rank, as grid >= HG)
+    // 2. list items ilo + j0 .. + jn - 1 (item ci: head ci % HG of the pair of rank
+    // ci / HG): the owners of ranks r_lo .. r_hi record their pairs, then one thread per item
+    const int64_t a0 = ilo + j0;
+    const int r_lo = (int)(a0 / HG), r_hi = (int)((a0 + jn - 1) / HG);
     if (cnt > 0) {
       int r = rank0;
-      for (int p = p0; p < p1; ++p) {
+      for (int p = p0; p < p1 && r <= r_hi; ++p) {
         if (ws.fg[p] == 0) continue;
-        const int64_t lo = (int64_t)r * HG - bx;
-        const int64_t j = lo <= 0 ? 0 : (lo + grid - 1) / grid;
-        const int64_t ci = j * grid + bx;
-        if (ci < (int64_t)(r + 1) * HG && j >= j0 && j < j0 + jn) {
-          const int hh = (int)(ci - (int64_t)r * HG);
-          const int bi = p / G, g = p - bi * G;
-          const int it = bi * H + g * HG + hh;
-          const int slot = a.slot_ids ? a.slot_ids[bi] : bi;
-          const float* hd = ws.hd + (size_t)it * HD_STRIDE;
-          const int k = (int)(j - j0);
-          const bool ok = slot >= 0 && slot < a.slots && hd[HD_FLUSH] != 0.f;
-          sItem[k] = it;
-          sSlot[k] = slot;
-          sM[k] = ok ? min(max((int)hd[HD_M], 1), c) : 0;
-          sDtot[k] = hd[HD_DTOT];
-          sEg[k] = hd[HD_SNAPF];
-        }
+        if (r >= r_lo) sPairOf[r - r_lo] = p;
         ++r;
       }
+    }
+    __syncthreads();
+    if (tid < jn) {
+      const int64_t ci = a0 + tid;
+      const int r = (int)(ci / HG), hh = (int)(ci - (int64_t)r * HG);
+      const int p = sPairOf[r - r_lo];
+      const int bi = p / G, g = p - bi * G;
+      const int it = bi * H + g * HG + hh;
+      const int slot = a.slot_ids ? a.slot_ids[bi] : bi;
+      const float* hd = ws.hd + (size_t)it * HD_STRIDE;
+      const bool ok = slot >= 0 && slot < a.slots && hd[HD_FLUSH] != 0.f;
+      sItem[tid] = it;
+      sSlot[tid] = slot;
+      sM[tid] = ok ? min(max((int)hd[HD_M], 1), c) : 0;
+      sDtot[tid] = hd[HD_DTOT];
+      sEg[tid] = hd[HD_SNAPF];
     }
     __syncthreads();
 
@@ -1527,13 +1548,17 @@ flush_kernel(StepArgs a) {
     auto stage_item = [&](int kk, int bf) {
       const int m2 = sM[kk], it2 = sItem[kk], sl2 = sSlot[kk];
       const int b2 = it2 / H, h2 = it2 - b2 * H, g2 = h2 / HG;
+      const int key = it2 / HG;
+      const bool withB = (bf ? bkey1 : bkey0) != key;  // a pair's heads share its B' window and C'
+      if (bf) bkey1 = key;
+      else bkey0 = key;
       float* wb = lds + bf * wfl;
       stage_window_dma<NC>(wb, reinterpret_cast<uint16_t*>(wb + fch * NC), wb + fch * NC + fch * P / 2,
                            wb + fch * NC + fch * P / 2 + fch, 0, m2, m2, P,
                            a.ring_b + (((size_t)sl2 * G + g2) * c + (c - m2)) * NC,
                            ws.B + ((size_t)b2 * G + g2) * kN + K,
                            a.ring_x + (((size_t)sl2 * H + h2) * c + (c - m2)) * P, a.x + (size_t)it2 * P,
-                           ws.w + (size_t)it2 * c, ws.C + ((size_t)b2 * G + g2) * kN + K, wave, lane, nw);
+                           ws.w + (size_t)it2 * c, ws.C + ((size_t)b2 * G + g2) * kN + K, wave, lane, nw, withB);
     };
     auto next_item = [&](int kk) {  // the first listed item from kk on with a window
       while (kk < jn && sM[kk] == 0) ++kk;
@@ -1613,7 +1638,11 @@ flush_kernel(StepArgs a) {
           const int kn = min(fch, m - k0);
           if (!pipe && (!whole || u0 == 0)) {  // a whole window is staged once, in the first pass
             __syncthreads();  // the previous chunk (or item: window and partials) is consumed
-            stage_window_dma<NC>(sBc, sX, sW, sW + fch, k0, kn, m, P, rb0, bcur, rx0, xcur, wgt, cq0, wave, lane, nw);
+            // whole windows keep the pair's B' and C' from its previous head
+            const bool withB = !whole || bkey0 != it / HG;
+            bkey0 = whole ? it / HG : -1;
+            stage_window_dma<NC>(sBc, sX, sW, sW + fch, k0, kn, m, P, rb0, bcur, rx0, xcur, wgt, cq0, wave, lane, nw,
+                                 withB);
             __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA has landed in LDS
             __syncthreads();
           }
@@ -2392,8 +2421,7 @@ int launch_pair(const StepArgs& a, const Launch& L, hipStream_t st) {
     // one resident round of workgroups: an empty launch dispatches no more than that,
     // and a full flush keeps every workgroup busy to the end
     const int items = a.b * a.H, cap = kFlushPerCU * cu_count();
-    int grid = items < cap ? items : cap;
-    if (grid < a.HG) grid = a.HG;  // the kernel's listing needs grid >= HG (items >= HG)
+    const int grid = items < cap ? items : cap;
     const size_t flds = flush_lds_bytes(a.P, K, COLD, a.fch, a.fpipe != 0);
     if (a.tf) {
       if (flds > kMaxLds && !lds_opt_in(reinterpret_cast<const void*>(&flush_kernel<K, COLD, true>)))
