@@ -40,9 +40,11 @@ def bytes_fresh_token():
     return 2 * H * P * N * 4 + bytes_io()
 
 
-def bytes_v4_token(k, c, cold, master="fp32", skip=0.0):
+def bytes_v4_token(k, c, cold, master="fp32", skip=0.0, exact=False):
     """skip: fraction of heads whose cold term a gated readout drops; such a head reads
-    no cold column on the c - 1 tokens of a window that do not flush."""
+    no cold column on the c - 1 tokens of a window that do not flush. exact: the rank-c
+    correction's reads of the buffered x (a token finds (c - 1) / 2 of them on average) and
+    its per-head weights (written by prep, read by the stream kernel, (c + 1) / 2 each)."""
     nc = N - k
     esz = {"fp32": 4, "bf16": 2, "fp8": 1}[cold]
     hot = 2 * H * P * k * 4
@@ -54,7 +56,8 @@ def bytes_v4_token(k, c, cold, master="fp32", skip=0.0):
         flush = H * P * nc * (2 * msz + esz) + (H * P * 4 if cold == "fp8" else 0)
     ring_entry = H * P * 2 + H * 4 + G * nc * 4  # x bf16, dt, B' cold
     ring = (c - 1) / c * 2 * ring_entry  # written by c-1 of c tokens, read once at the flush
-    return hot + read + flush / c + ring + bytes_io()
+    corr = (H * P * 2 * (c - 1) / 2 + 2 * H * 4 * (c + 1) / 2) if exact else 0.0
+    return hot + read + flush / c + ring + corr + bytes_io()
 
 
 def bytes_rotation():
@@ -278,6 +281,9 @@ def bench_deploy(args, layers, inputs, dev, fresh_ms_256):
             v_step, _, v_ev, _ = bench_v4(a, layers, inp, dev)
             vb = a.B * bytes_v4_token(a.k, a.c, a.cold, a.master) + bytes_rotation()
             f_ms = fresh_ms[B]
+            tr, tr_src = measured_traffic(f"v4 B={a.B} k={a.k} c={a.c} {a.cold}"
+                                          + (" bf16-master" if a.master == "bf16" else "")
+                                          + (" ragged" if a.ragged else ""))
             out[name] = {"value": round(a.B / v_step * 1e3, 1), "unit": "state-op tokens/s",
                          "ms_per_step": round(v_step, 4), "fresh_ms_per_step": round(f_ms, 4),
                          "speedup_vs_fresh": round(f_ms / v_step, 3),
@@ -286,7 +292,7 @@ def bench_deploy(args, layers, inputs, dev, fresh_ms_256):
                          "achieved_gbs": round(vb / (v_ev * 1e-3) / 1e9, 1),
                          "frac": round(vb / (v_ev * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                          "algorithmic_bytes_per_launch": int(vb), "avg_launch_us_events": round(v_ev * 1e3, 2),
-                         "steps": a.steps}
+                         "traffic": tr, "traffic_source": tr_src, "steps": a.steps}
             log(f"deploy: {name}: {v_step:.3f} ms/step, {out[name]['speedup_vs_fresh']}x fresh")
         del inp
         torch.cuda.empty_cache()
@@ -513,7 +519,7 @@ def main():
         log("v4 ...")
         v_step, v_launch, v_ev, tier_gb = bench_v4(args, layers, inputs, dev)
         res["v4"] = (v_step, v_launch, v_ev)
-        vb = args.B * bytes_v4_token(args.k, args.c, args.cold, args.master, args.skip) + bytes_rotation()
+        vb = args.B * bytes_v4_token(args.k, args.c, args.cold, args.master, args.skip, args.exact) + bytes_rotation()
         log(f"v4: {v_step:.3f} ms/step, {args.B / v_step * 1e3:,.0f} tok/s, launch {v_ev * 1e3:.1f} us "
             f"-> {vb / (v_ev * 1e-3) / 1e9:,.0f} GB/s (tiers {tier_gb:.1f} GB)")
 
@@ -534,13 +540,14 @@ def main():
 
     head = "v4" if "v4" in res else "fresh"
     ms_step, ms_launch, ms_ev = res[head]
-    per_launch_bytes = (args.B * bytes_v4_token(args.k, args.c, args.cold, args.master, args.skip) + bytes_rotation()
-                        if head == "v4" else args.B * bytes_fresh_token())
+    per_launch_bytes = (args.B * bytes_v4_token(args.k, args.c, args.cold, args.master, args.skip, args.exact)
+                        + bytes_rotation() if head == "v4" else args.B * bytes_fresh_token())
     achieved = per_launch_bytes / (ms_ev * 1e-3) / 1e9
     readout = ("exact" if args.exact else "hot-only" if args.coldoff
                else f"query-gated tau={args.qgate:g}" if args.qgate > 0 else "stale")
     tkey = (f"v4 B={args.B} k={args.k} c={args.c} {args.cold}" + (" bf16-master" if args.master == "bf16" else "")
-            + ("" if readout == "stale" else f" {readout}") if head == "v4" else f"fresh B={args.B}")
+            + ("" if readout == "stale" else f" {readout}") + (" ragged" if args.ragged else "")
+            if head == "v4" else f"fresh B={args.B}")
     traffic, traffic_src = measured_traffic(tkey)
     out = {
         "metric": "state-op tokens/s at 9B shape B=256 (v4-c4 vs fresh); achieved HBM GB/s vs peak",
