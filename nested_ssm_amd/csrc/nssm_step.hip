@@ -215,6 +215,20 @@ constexpr int kBlkSeg = 64;  // u2v (4 bf16) between consecutive segments of a b
 constexpr int kPrepThreads = 256;
 constexpr int kPrepReq = 8;  // requests per prep workgroup (at most)
 
+// A head's dt (softplus, with the dt_min floor of the native path) and the scalars every
+// stream kernel reads: dt, a = dt A, exp(a), D. Returns dt.
+__device__ __forceinline__ float head_scalars(float* __restrict__ hd, float draw, float dtb, float Ah, float Dh,
+                                              float dt_min) {
+  float dt = softplus_f(draw + dtb);
+  if (dt_min > 0.f) dt = fmaxf(dt, dt_min);
+  const float av = dt * Ah;
+  hd[HD_DT] = dt;
+  hd[HD_A] = av;
+  hd[HD_DECAY] = expf(av);
+  hd[HD_D] = Dh;
+  return dt;
+}
+
 template <bool TIERED>
 __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
   __shared__ float sX[2 * kPrepReq][kN];  // B (j < 8) and C (j >= 8) of the block's requests
@@ -233,6 +247,33 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
   const Ws ws(a.ws, a.b, H, G, c);
   const bool gate = TIERED && a.qgate_tau > 0.f && !a.hot_only;  // query gate (uniform)
   const bool rot_lds = TIERED && (a.exact || gate);              // B', C' kept in LDS
+
+  if constexpr (!TIERED) {
+    if (!a.R) {
+      // untiered without a rotation: B and C converted straight into the workspace and the
+      // head scalars written from registers, with no LDS and no barrier (at the 9B shape,
+      // B = 256: 6.2 us per launch through the staged path)
+      for (int i = tid; i < nreq * kN; i += kPrepThreads) {
+        const size_t o = ((size_t)r0 * G + g) * kN + (size_t)(i / kN) * G * kN + (i % kN);
+        ws.B[o] = bf2f(a.Bm[o]);
+        ws.C[o] = bf2f(a.Cm[o]);
+      }
+      if (tid < nreq * HG) {
+        const int hr = tid / HG, h = g * HG + (tid - hr * HG), bi = r0 + hr;
+        const int slot = a.slot_ids ? a.slot_ids[bi] : bi;
+        if (slot >= 0 && slot < a.slots) {
+          float* __restrict__ hd = ws.hd + ((size_t)bi * H + h) * HD_STRIDE;
+          head_scalars(hd, bf2f(a.dt_raw[(size_t)bi * H + h]), a.dt_bias[h], a.A[h], a.D[h], a.dt_min);
+          hd[HD_SNAPF] = 0.f;
+          hd[HD_FLUSH] = 0.f;
+          hd[HD_DTOT] = 1.f;
+          hd[HD_M] = 0.f;
+          hd[HD_POS] = 0.f;
+        }
+      }
+      return;
+    }
+  }
 
   // 1. independent loads: B and C of the block (zero past the last request), R, the
   // head inputs
@@ -409,14 +450,8 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
 
   // 3. per-head scalars and bookkeeping
   if (head_thread && slot >= 0 && slot < a.slots) {
-    float dt = softplus_f(draw + dtb);
-    if (a.dt_min > 0.f) dt = fmaxf(dt, a.dt_min);
-    const float av = dt * Ah;
     float* __restrict__ hd = ws.hd + ((size_t)bi * H + h) * HD_STRIDE;
-    hd[HD_DT] = dt;
-    hd[HD_A] = av;
-    hd[HD_DECAY] = expf(av);
-    hd[HD_D] = Dh;
+    const float dt = head_scalars(hd, draw, dtb, Ah, Dh, a.dt_min), av = dt * Ah;
     if constexpr (TIERED) {
       const size_t o = (size_t)slot * H + h;
       const int pos = tt % c;
