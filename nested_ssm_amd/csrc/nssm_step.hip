@@ -1367,18 +1367,22 @@ __global__ void __launch_bounds__(64) fresh_kernel(StepArgs a, const float* __re
 // accuracy of an fp32 contraction at a fraction of fp32 MFMA's issue time (per 64 tokens
 // and tile, fp32 16x16x4: 16 steps of 32 cycles; bf16 16x16x32: 2 steps x 3 parts of 16).
 // The window is staged in LDS by DMA fch tokens at a time (the whole window when it fits,
-// all its loads in flight together), and each lane builds its operands from it: 8 tokens
-// of one cold column (or headdim row) per 16-byte operand, zero past the chunk. Lane
-// (li, lk) of a tile holds Delta[pt*16 + li][nt*16 + 4 lk .. +3]; the state is read and
-// written in that mapping, its loads issued before the window's. Each wave holds
-// kMfmaTiles tiles; a pass covers as many tiles as the waves hold (e4m3: whole rows only,
-// the row scale needs all of a row's tiles). Per-tile readout partials and row maxima go
-// through LDS and are summed in a fixed order.
+// all its loads in flight together; with two whole windows in LDS, the next item's during
+// this item's contraction), and each lane builds its operands from it: 8 tokens of one
+// cold column (or headdim row) per 16-byte operand, zero past the chunk. A wave owns one
+// n-tile and up to kMfmaTiles consecutive p-tiles, so it builds the split A operand once
+// per 32-token step for all of them. Lane (li, lk) of a tile holds
+// Delta[pt*16 + li][nt*16 + 4 lk .. +3]; the state is read and written in that mapping, its
+// loads issued before the window's. An e4m3 pass holds whole rows (the row scale needs
+// all of a row's tiles). Per-tile readout partials and row maxima go through LDS and are
+// summed in a fixed order.
 // Measured on MI355X (9B shape, B = 256, c = 64, fp32 cold), a full flush (32768 heads):
-// 965 us with the fp32 contraction, 810 us with this one. Tried and slower: one wave per
-// tile row (P / 16 waves per workgroup, 3 workgroups per CU, row scales and readouts
-// reduced in the wave) 1004 us; the window staged transposed and pre-split in LDS by the
-// workgroup (three bf16 copies of w B', token-contiguous rows) 1239 us.
+// 965 us with the fp32 contraction, 810-850 with the three-part bf16 split, 714 with the
+// shared A operand and conflict-free window, 689-697 with a pair's B' staged once. Tried
+// and slower: one wave per tile row (P / 16 waves per workgroup, 3 workgroups per CU, row
+// scales and readouts reduced in the wave) 1004 us; the window staged transposed and
+// pre-split in LDS by the workgroup (three bf16 copies of w B', token-contiguous rows)
+// 1239 us.
 constexpr int kFlushWaves = 8;
 constexpr int kFlushPerCU = 2;  // flush workgroups per CU (the kernel's occupancy: 4 waves per SIMD)
 constexpr int kFlushList = 64;  // items a workgroup lists at a time
