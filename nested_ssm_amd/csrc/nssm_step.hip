@@ -29,6 +29,7 @@
 #include <atomic>
 #include <mutex>
 #include <set>
+#include <type_traits>
 #include <utility>
 
 #include "../../include/nssm.h"
@@ -77,6 +78,7 @@ struct StepArgs {
   int32_t split;  // the flush kernel runs after the stream kernel (prep writes the pair flags)
   int32_t fch;    // window tokens the flush kernel stages in LDS at a time (multiple of 4)
   int32_t fpipe;  // the flush kernel keeps two whole windows in LDS (stages the next item's early)
+  int32_t fw;     // the flush kernel forms the window weights and total decay itself (prep leaves them)
   float dt_min;
   // gated stale readout (no cold term for a skipped head): every head (hot_only), or the
   // heads whose query puts less than qgate_tau of its energy on the cold columns;
@@ -477,7 +479,11 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
       hd[HD_FLUSH] = flush ? 1.f : 0.f;
       hd[HD_POS] = (float)pos;
       if (flush) sFl[hr] = 1;
-      if (flush || exact) {
+      if (flush && !exact && a.fw) {
+        // the flush kernel forms the window weights from the ring's dt
+        hd[HD_DTOT] = 1.f;
+        hd[HD_M] = (float)(nvv + 1);
+      } else if (flush || exact) {
         // window = the nv buffered tokens at ring [pos-nv, pos) and this one (at a
         // flush pos = c-1): w_i = exp(sum_{l>i} a_l) dt_i, total decay exp(sum_l a_l);
         // the exact readout's coefficients are w_i s_i. The buffered dt are loaded
@@ -1368,32 +1374,49 @@ __global__ void __launch_bounds__(64) fresh_kernel(StepArgs a, const float* __re
 // and tile, fp32 16x16x4: 16 steps of 32 cycles; bf16 16x16x32: 2 steps x 3 parts of 16).
 // The window is staged in LDS by DMA fch tokens at a time (the whole window when it fits,
 // all its loads in flight together; with two whole windows in LDS, the next item's during
-// this item's contraction), and each lane builds its operands from it: 8 tokens of one
-// cold column (or headdim row) per 16-byte operand, zero past the chunk. A wave owns one
-// n-tile and up to kMfmaTiles consecutive p-tiles, so it builds the split A operand once
-// per 32-token step for all of them. Lane (li, lk) of a tile holds
-// Delta[pt*16 + li][nt*16 + 4 lk .. +3]; the state is read and written in that mapping, its
-// loads issued before the window's. An e4m3 pass holds whole rows (the row scale needs
-// all of a row's tiles). Per-tile readout partials and row maxima go through LDS and are
-// summed in a fixed order.
+// this item's contraction). A wave owns one n-tile and up to kMfmaTiles consecutive
+// p-tiles, so it builds the split A operand once per 32-token step for all of them (8
+// tokens of one cold column per lane, read from the staged B' and weights); the x operand
+// of each tile is two transposing LDS loads (ds_read_b64_tr_b16), and whole 32-token steps
+// read both operands without per-token predicates (a chunk's last partial step reads the
+// buffer's padding tokens and zeroes them). Lane (li, lk) of a tile holds
+// Delta[pt*16 + li][nt*16 + 4 lk .. +3]; the state is read and written in that mapping: the
+// pass's tiles are loaded before the contraction, every load is waited for once after it,
+// and the new values of all tiles are formed before the first store, so the stores go out
+// back to back and the pass's barrier publishes LDS only (the stores stay in flight). With
+// two whole windows in LDS the flush kernel also forms each window's weights w_i =
+// exp(sum_{l>i} a_l) dt_i and the total decay from the ring's dt (a 64-lane suffix scan,
+// off the prep kernel's critical path). An e4m3 pass holds whole rows (the row scale
+// needs all of a row's tiles). Per-tile readout partials and row maxima go through LDS and
+// are summed in a fixed order.
 // Measured on MI355X (9B shape, B = 256, c = 64, fp32 cold), a full flush (32768 heads):
 // 965 us with the fp32 contraction, 810-850 with the three-part bf16 split, 714 with the
-// shared A operand and conflict-free window, 689-697 with a pair's B' staged once. Tried
-// and slower: one wave per tile row (P / 16 waves per workgroup, 3 workgroups per CU, row
-// scales and readouts reduced in the wave) 1004 us; the window staged transposed and
-// pre-split in LDS by the workgroup (three bf16 copies of w B', token-contiguous rows)
-// 1239 us.
+// shared A operand and conflict-free window, 689-697 with a pair's B' staged once,
+// 661-681 with the transposing x loads, predicate-free steps and stores back to back; the
+// ragged batch's per-token launch (B = 384, ~768 heads) 28.9 -> 29.3 us while prep drops
+// 19.9 -> 13.5 us without the window weights. Per-item phase timestamps (s_memrealtime)
+// put the contraction at about 1.3 us of a CU per item and the rest in load, store and
+// DMA issue stalls behind the memory pipe. Tried and slower: one wave per tile row (P / 16
+// waves per workgroup, 3 workgroups per CU, row scales and readouts reduced in the wave)
+// 1004 us; the window staged transposed and pre-split in LDS by the workgroup (three bf16
+// copies of w B', token-contiguous rows) 1239 us; six-wave workgroups (one per work unit)
+// holding the next item's tiles in registers 809 us (only one such workgroup is resident per
+// CU); the next item's tiles in registers with eight waves (spills) 801 us; two helper
+// waves staging windows and writing y while six contract (ragged 33.8 us).
 constexpr int kFlushWaves = 8;
 constexpr int kFlushPerCU = 2;  // flush workgroups per CU (the kernel's occupancy: 4 waves per SIMD)
 constexpr int kFlushList = 64;  // items a workgroup lists at a time
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+typedef short short4v __attribute__((ext_vector_type(4)));
 
 // The three bf16 parts of each of 8 fp32 values: hi = bf16(v), mid = bf16(v - hi),
 // lo = bf16(v - hi - mid), with hi + mid + lo == v exactly (each difference is exact in
 // fp32, and what is left after two 8-bit parts fits the third) for |v| above 2^-100.
 __device__ __forceinline__ void split3x8(const float (&v)[8], u4v& hi, u4v& mi, u4v& lo) {
+  // the differences must round v itself, not be fused with the product that formed v
+#pragma clang fp contract(off)
   uint32_t h[4], m[4], l[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -1413,22 +1436,26 @@ __device__ __forceinline__ void split3x8(const float (&v)[8], u4v& hi, u4v& mi, 
 #define NSSM_GLOBAL(p) ((const __attribute__((address_space(1))) void*)(p))
 #define NSSM_LOCAL(p) ((__attribute__((address_space(3))) void*)(p))
 
-// Bank swizzles of the staged window. The contraction's lane groups lk = 0 .. 3 (16 lanes
-// each; lanes 0-31 and 32-63 are served by the 32 LDS banks in separate cycles) read the
-// window tokens lk, lk + 4, ..., so lk = 0 and 1 read tokens of opposite parity. Within an
-// odd token the 16-byte granules of B' are XORed with 4 (16 floats: the other half of the
-// banks) when a token's B' spans whole 32-bank rows (NC % 32 == 0; NC % 32 == 16 offsets
-// odd tokens by itself), and the 4-byte granules of x with 8 (8 words) when P % 64 == 0.
+// Window layout. The contraction's lane group lk (16 lanes; lanes 0-31 and 32-63 are served
+// by the 32 LDS banks in separate cycles) takes, in each 32-token step from ks, the tokens
+// ks + 16 q + 4 lk + r (q = 0, 1; r = 0 .. 3) as operand element 4 q + r. B' rows of tokens
+// 4 apart start on the same bank when a token's B' spans whole 32-bank rows (NC % 32 ==
+// 0), so within a token with bit 2 set its 16-byte granules are XORed with 4 (16 floats:
+// the other half of the banks; groups lk = 0 and 1 differ in that bit). x rows are read
+// with gfx950's transposing LDS load, 4 consecutive tokens per 16-lane group: a row is
+// flush_x_stride(P) bf16 long, P padded by 16 where P is a multiple of 32, so consecutive
+// rows start 32 bytes apart modulo the 128 bytes of the banks.
 template <int NC>
 __host__ __device__ constexpr int flush_swz_b() { return NC % 32 == 0 ? 4 : 0; }
-__host__ __device__ constexpr int flush_swz_x(int P) { return P % 64 == 0 ? 8 : 0; }
+__host__ __device__ constexpr int flush_x_stride(int P) { return P + (P % 32 == 0 ? 16 : 0); }
 
 // Stage window tokens [k0, k0 + kn) of one head into LDS with gfx950's LDS DMA
 // (global_load_lds: lane L of a wave instruction writes its granule at base + L * size,
 // no registers in between): sB[e][n] = B'_tok[K + n] (16-byte granules), sX[e][p] =
-// x_tok[p] as bf16 (4-byte granules), both with the bank swizzles above (tok = k0 + e),
+// x_tok[p] as bf16, both in the bank layout above (tok = k0 + e),
 // sW[e] = w_tok, and sC[n] = C'[K + n] of this token
-// (the readout's coefficients, read after the contraction). Window token m - 1 is this
+// (the readout's coefficients, read after the contraction); given dtcur, sW[e] = dt_tok instead
+// (the caller forms the weights). Window token m - 1 is this
 // token (B' from the workspace, x from the inputs); token tok < m - 1 sits at ring
 // position c - m + tok (rb0 and rx0 point at the ring rows of window token 0). Wave w
 // issues the instructions w, w + nw, ... of each block; the caller waits (vmcnt) and
@@ -1437,46 +1464,60 @@ template <int NC>
 __device__ __forceinline__ void stage_window_dma(float* sB, uint16_t* sX, float* sW, float* sC, int k0, int kn,
                                                  int m, int P, const float* rb0, const float* bcur,
                                                  const uint16_t* rx0, const uint16_t* xcur, const float* wgt,
-                                                 const float* cq, int wave, int lane, int nw, bool withB) {
+                                                 const float* cq, int wave, int lane, int nw, bool withB,
+                                                 const float* dtcur = nullptr) {
   constexpr int NB4 = NC / 4;  // 16-byte granules per token of B'
   const int nb = withB ? kn * NB4 : 0;
   for (int q = wave; q * 64 < nb; q += nw) {
     const int gi = q * 64 + lane;
     if (gi < nb) {
       const int e = gi / NB4, tok = k0 + e;
-      const int gr = (gi - e * NB4) ^ (flush_swz_b<NC>() * (e & 1));  // the granule this slot holds
+      const int gr = (gi - e * NB4) ^ (flush_swz_b<NC>() * ((e >> 2) & 1));  // the granule this slot holds
       const float* src = (tok < m - 1 ? rb0 + (size_t)tok * NC : bcur) + 4 * gr;
       __builtin_amdgcn_global_load_lds(NSSM_GLOBAL(src), NSSM_LOCAL(sB + q * 256), 16, 0, 0);
     }
   }
   // x: the buffered tokens of the chunk in 16-byte granules (8 bf16; ring rows are
-  // 16-byte aligned), this token (window token m - 1, from the inputs) in 4-byte ones; the
-  // bank swizzle is the same XOR in either unit (8 words)
-  const int P8 = P >> 3, swx = flush_swz_x(P);
-  const int nxr = max(0, min(kn, m - 1 - k0)) * P8;
+  // 16-byte aligned; a row's padding granules are filled from its first, and never read),
+  // this token (window token m - 1, from the inputs) in 4-byte ones
+  const int SX = flush_x_stride(P), P8 = P >> 3, S8 = SX >> 3;
+  const int nxr = max(0, min(kn, m - 1 - k0)) * S8;
   for (int q = wave; q * 64 < nxr; q += nw) {
     const int gi = q * 64 + lane;
     if (gi < nxr) {
-      const int e = gi / P8;
-      const int gr = (gi - e * P8) ^ ((swx >> 2) * (e & 1));
-      __builtin_amdgcn_global_load_lds(NSSM_GLOBAL(rx0 + (size_t)(k0 + e) * P + 8 * gr), NSSM_LOCAL(sX + q * 512),
-                                       16, 0, 0);
+      const int e = gi / S8, gr = gi - e * S8;
+      __builtin_amdgcn_global_load_lds(NSSM_GLOBAL(rx0 + (size_t)(k0 + e) * P + (gr < P8 ? 8 * gr : 0)),
+                                       NSSM_LOCAL(sX + q * 512), 16, 0, 0);
     }
   }
-  if (wave == nw - 3 && m - 1 >= k0 && m - 1 < k0 + kn) {
+  const int wx = nw >= 3 ? nw - 3 : 0, wc = nw >= 2 ? nw - 2 : 0;  // the waves of this token's x and of C'
+  if (wave == wx && m - 1 >= k0 && m - 1 < k0 + kn) {
     const int e = m - 1 - k0, P2 = P >> 1;
     for (int q = 0; q * 64 < P2; ++q) {
       const int gi = q * 64 + lane;
       if (gi < P2)
-        __builtin_amdgcn_global_load_lds(NSSM_GLOBAL(xcur + 2 * (gi ^ (swx * (e & 1)))),
-                                         NSSM_LOCAL(sX + e * P + q * 128), 4, 0, 0);
+        __builtin_amdgcn_global_load_lds(NSSM_GLOBAL(xcur + 2 * gi), NSSM_LOCAL(sX + e * SX + q * 128), 4, 0, 0);
     }
   }
-  if (wave == nw - 1 && lane < kn)
-    __builtin_amdgcn_global_load_lds(NSSM_GLOBAL(wgt + k0 + lane), NSSM_LOCAL(sW), 4, 0, 0);
-  if (withB && wave == nw - 2 && lane < NC / 4)
+  if (wave == nw - 1 && lane < kn)  // weights, or (dtcur given; whole windows) the buffered dt and this one
+    __builtin_amdgcn_global_load_lds(NSSM_GLOBAL(dtcur && lane == m - 1 ? dtcur : wgt + k0 + lane), NSSM_LOCAL(sW), 4,
+                                     0, 0);
+  if (withB && wave == wc && lane < NC / 4)
     __builtin_amdgcn_global_load_lds(NSSM_GLOBAL(cq + 4 * lane), NSSM_LOCAL(sC), 16, 0, 0);
 }
+
+// Workgroup barrier that publishes LDS only: the wave's global stores stay in flight
+// (HIP's __syncthreads also waits for them). A wave that staged LDS by DMA waits for its
+// own DMA (vmcnt) before it reaches this barrier.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Tokens a window buffer holds for a chunk of fch tokens: the contraction reads whole
+// 32-token steps (tokens past the chunk are read and dropped).
+__host__ __device__ constexpr int flush_alloc_tokens(int fch) { return (fch + 31) & ~31; }
 
 // TF (the teacher-forced readout): y gets the readout of the new state as stored (the new
 // read copy; e4m3 partials formed after the row scale is known) instead of the old one's.
@@ -1484,28 +1525,33 @@ template <int K, int COLD, bool TF = false>
 __global__ void __launch_bounds__(kFlushWaves * 64) __attribute__((amdgpu_waves_per_eu(kFlushPerCU * kFlushWaves / 4)))
 flush_kernel(StepArgs a) {
   using C = Cfg<K, COLD>;
-  constexpr int NC = C::NC, NT = C::NT, nw = kFlushWaves, nthr = kFlushWaves * 64;
+  constexpr int NC = C::NC, NT = C::NT, nw = kFlushWaves, nthr = nw * 64;
   // work units: (n-tile, block of ptw consecutive p-tiles), one per wave and pass; the
   // blocks are as many as fill the waves (at most kMfmaTiles p-tiles each), and an e4m3
   // pass holds whole blocks (its row scales need every n-tile of a row)
   constexpr int UPP = C::E4M3 ? (nw / NT) * NT : nw;  // units per pass
   static_assert(UPP >= NT, "a pass must hold a whole row");
+  // the values the flush starts from: the single copy, or the master (fp32 or bf16)
+  constexpr bool SRC16 = COLD == NSSM_COLD_BF16_SINGLE || C::MASTER16;
   extern __shared__ float lds[];
   // this workgroup's listed items and their scalars (loaded by the thread that lists
   // the item); sM = 0 marks an item with nothing to flush
   __shared__ int sItem[kFlushList], sSlot[kFlushList], sM[kFlushList];
-  __shared__ float sDtot[kFlushList], sEg[kFlushList];
+  __shared__ float sDtot[kFlushList], sEg[kFlushList], sAh[kFlushList];
   __shared__ int sPairOf[kFlushList + 1];  // the pairs of a list's ranks
+  __shared__ float sDT[2];                 // total decay of each window buffer's item (fw)
   __shared__ int sWave[kFlushWaves];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, lk = lane >> 4;
   const int H = a.H, P = a.P, c = a.c, G = a.G, HG = a.HG, fch = a.fch;
+  const int fa = flush_alloc_tokens(fch);
   const Ws ws(a.ws, a.b, H, G, c);
-  // window buffer: [fch][NC] B', [fch][P] x (bf16), [fch] weights; two of them when the
-  // next item's window is staged during this one's contraction (then every window is
+  // window buffer: [fa][NC] B', [fa][SX] x (bf16), [fa] weights, C'[K:]; two of them when
+  // the next item's window is staged during this one's contraction (then every window is
   // whole, m <= c <= fch)
-  const bool pipe = a.fpipe != 0;
-  const int wfl = fch * NC + fch * P / 2 + fch + NC;  // floats per window buffer (+ C'[K:])
+  const bool pipe = a.fpipe != 0, fw = pipe && a.fw != 0;
+  const int SX = flush_x_stride(P);
+  const int wfl = fa * NC + fa * SX / 2 + fa + NC;  // floats per window buffer
   const int nbuf = pipe ? 2 : 1;
   float* sPart0 = lds + nbuf * wfl;        // [nbuf][P][NT] readout partials of the old read copy
   float* sAmx = sPart0 + nbuf * P * NT;    // [P][NT] row maxima of the new values (e4m3 only)
@@ -1514,15 +1560,19 @@ flush_kernel(StepArgs a) {
   const int ptw = (PT + nblk0 - 1) / nblk0, nunit = NT * ((PT + ptw - 1) / ptw);
 
   // 1. rank the flagged pairs: thread tid counts pairs [p0, p1) (whole int4 words of
-  // the flag array, which is padded to a multiple of 4), then a block-wide exclusive
-  // prefix of the counts
+  // the flag array, which is padded to a multiple of 4), keeping the flags of its first 64
+  // pairs as a bit mask, then a block-wide exclusive prefix of the counts
   const int npair = a.b * G;
   const int per = (((npair + nthr - 1) / nthr) + 3) & ~3;
   const int p0 = min(tid * per, npair), p1 = min(p0 + per, npair);
   int cnt = 0;
+  uint64_t fmask = 0;
   for (int p = p0; p < p1; p += 4) {
     const int4 f = *reinterpret_cast<const int4*>(ws.fg + p);
-    cnt += (f.x != 0) + (p + 1 < p1 && f.y != 0) + (p + 2 < p1 && f.z != 0) + (p + 3 < p1 && f.w != 0);
+    const uint32_t bits = (uint32_t)(f.x != 0) | ((uint32_t)(p + 1 < p1 && f.y != 0) << 1) |
+                          ((uint32_t)(p + 2 < p1 && f.z != 0) << 2) | ((uint32_t)(p + 3 < p1 && f.w != 0) << 3);
+    if (p - p0 < 64) fmask |= (uint64_t)bits << (p - p0);
+    cnt += __builtin_popcount(bits);
   }
   int incl = cnt;
 #pragma unroll
@@ -1548,16 +1598,65 @@ flush_kernel(StepArgs a) {
   const int nmine = (int)(min(ilo + per_wg, fitems) - ilo);
   int bkey0 = -1, bkey1 = -1;  // the pair whose B' and C' each window buffer holds (-1: none)
 
+  // the state tiles of one pass of an item, in registers: issued early, used after the
+  // contraction
+  f4 old[kMfmaTiles];
+  u2v old16[SRC16 ? kMfmaTiles : 1];
+  u2v rb16[COLD == NSSM_COLD_BF16 ? kMfmaTiles : 1];
+  uint32_t r8[C::E4M3 ? kMfmaTiles : 1];
+  float rsc[C::E4M3 ? kMfmaTiles : 1];
+  // this wave's work unit in the pass from unit u0: n-tile nt, p-tiles pt0 .. pt0 + npt - 1
+  // (npt = 0: no unit in this pass)
+  auto unit_of = [&](int u0, int& nt, int& pt0) {
+    const int u = u0 + wave;
+    nt = u % NT;
+    pt0 = (u / NT) * ptw;
+    return wave < UPP && u < nunit ? min(ptw, PT - pt0) : 0;  // wave-uniform
+  };
+  auto load_tiles = [&](int kk, int u0) {
+    int nt, pt0;
+    const int npt = unit_of(u0, nt, pt0);
+    const int it2 = __builtin_amdgcn_readfirstlane(sItem[kk]);
+    const size_t row0 = ((size_t)__builtin_amdgcn_readfirstlane(sSlot[kk]) * H + it2 % H) * P;
+    const void* src = C::SEG ? static_cast<const void*>(a.cold) : static_cast<const void*>(a.master);
+#pragma unroll
+    for (int i = 0; i < kMfmaTiles; ++i) {
+      if (i < npt) {
+        const size_t row = row0 + (pt0 + i) * 16 + li;
+        const int col = nt * 16 + 4 * lk;
+        if constexpr (SRC16)
+          old16[i] = ld_stream(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(src) + blk16(row, col, NC)));
+        else
+          old[i] = ld_stream(reinterpret_cast<const f4*>(static_cast<const float*>(src) + row * NC + col));
+        if constexpr (COLD == NSSM_COLD_BF16)
+          rb16[i] = ld_stream(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.cold) + blk16(row, col, NC)));
+        if constexpr (C::E4M3) {
+          r8[i] = ld_stream(reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(a.cold) + row * NC + col));
+          rsc[i] = a.scale[row];
+        }
+      }
+    }
+  };
+
   for (int j0 = 0; j0 < nmine; j0 += kFlushList) {
     const int jn = min(kFlushList, nmine - j0);
     __syncthreads();  // the previous list is consumed
     // 2. list items ilo + j0 .. + jn - 1 (item ci: head ci % HG of the pair of rank
-    // ci / HG): the owners of ranks r_lo .. r_hi record their pairs, then one thread per item
+    // ci / HG): the owners of ranks r_lo .. r_hi record their pairs (from the mask; a
+    // thread with more than 64 pairs reads the flags past them again), then one thread
+    // per item
     const int64_t a0 = ilo + j0;
     const int r_lo = (int)(a0 / HG), r_hi = (int)((a0 + jn - 1) / HG);
-    if (cnt > 0) {
+    if (cnt > 0 && rank0 <= r_hi && rank0 + cnt > r_lo) {
       int r = rank0;
-      for (int p = p0; p < p1 && r <= r_hi; ++p) {
+      uint64_t mrem = fmask;
+      while (mrem != 0 && r <= r_hi) {
+        const int j = __builtin_ctzll(mrem);
+        mrem &= mrem - 1;
+        if (r >= r_lo) sPairOf[r - r_lo] = p0 + j;
+        ++r;
+      }
+      for (int p = p0 + 64; p < p1 && r <= r_hi; ++p) {
         if (ws.fg[p] == 0) continue;
         if (r >= r_lo) sPairOf[r - r_lo] = p;
         ++r;
@@ -1578,6 +1677,7 @@ flush_kernel(StepArgs a) {
       sM[tid] = ok ? min(max((int)hd[HD_M], 1), c) : 0;
       sDtot[tid] = hd[HD_DTOT];
       sEg[tid] = hd[HD_SNAPF];
+      sAh[tid] = a.A[it - bi * H];
     }
     __syncthreads();
 
@@ -1585,37 +1685,60 @@ flush_kernel(StepArgs a) {
     // bf: window token m - 1 is this token (B' from the workspace, x from the inputs),
     // token i < m - 1 sits at ring position c - m + i.
     auto stage_item = [&](int kk, int bf) {
-      const int m2 = sM[kk], it2 = sItem[kk], sl2 = sSlot[kk];
+      const int m2 = __builtin_amdgcn_readfirstlane(sM[kk]), it2 = __builtin_amdgcn_readfirstlane(sItem[kk]);
+      const int sl2 = __builtin_amdgcn_readfirstlane(sSlot[kk]);
       const int b2 = it2 / H, h2 = it2 - b2 * H, g2 = h2 / HG;
       const int key = it2 / HG;
       const bool withB = (bf ? bkey1 : bkey0) != key;  // a pair's heads share its B' window and C'
       if (bf) bkey1 = key;
       else bkey0 = key;
       float* wb = lds + bf * wfl;
-      stage_window_dma<NC>(wb, reinterpret_cast<uint16_t*>(wb + fch * NC), wb + fch * NC + fch * P / 2,
-                           wb + fch * NC + fch * P / 2 + fch, 0, m2, m2, P,
+      stage_window_dma<NC>(wb, reinterpret_cast<uint16_t*>(wb + fa * NC), wb + fa * NC + fa * SX / 2,
+                           wb + fa * NC + fa * SX / 2 + fa, 0, m2, m2, P,
                            a.ring_b + (((size_t)sl2 * G + g2) * c + (c - m2)) * NC,
                            ws.B + ((size_t)b2 * G + g2) * kN + K,
                            a.ring_x + (((size_t)sl2 * H + h2) * c + (c - m2)) * P, a.x + (size_t)it2 * P,
-                           ws.w + (size_t)it2 * c, ws.C + ((size_t)b2 * G + g2) * kN + K, wave, lane, nw, withB);
+                           fw ? a.ring_dt + ((size_t)sl2 * H + h2) * c + (c - m2) : ws.w + (size_t)it2 * c,
+                           ws.C + ((size_t)b2 * G + g2) * kN + K, wave, lane, nw, withB,
+                           fw ? ws.hd + (size_t)it2 * HD_STRIDE + HD_DT : nullptr);
+    };
+    // fw: the window weights of item kk in buffer bf from its staged dt (one wave, after
+    // its own DMA of them has landed): a_i = dt_i A_h, w_i = exp(sum_{l>i} a_l) dt_i (a
+    // suffix scan over the window's lanes, at most 64 tokens) and the total decay
+    // exp(sum_l a_l), as the reference's flush (scale/v4_fused_decode.py:76-79)
+    auto form_weights = [&](int kk, int bf) {
+      float* sWb = lds + bf * wfl + fa * NC + fa * SX / 2;
+      const int mm = sM[kk];
+      const float d = lane < mm ? sWb[lane] : 0.f;
+      float incl = d * sAh[kk];
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const float v = __shfl_down(incl, o);
+        if (lane + o < 64) incl += v;
+      }
+      const float after = __shfl_down(incl, 1);  // sum over l > lane
+      if (lane < mm) sWb[lane] = expf(lane + 1 < mm ? after : 0.f) * d;
+      if (lane == 0) sDT[bf] = expf(incl);
     };
     auto next_item = [&](int kk) {  // the first listed item from kk on with a window
       while (kk < jn && sM[kk] == 0) ++kk;
       return kk;
     };
     int buf = 0;
-    if (pipe) {  // the first window, staged before the loop
+    if (pipe) {  // the first window (and state tiles), staged before the loop
       const int k1 = next_item(0);
       if (k1 < jn) {
         stage_item(k1, 0);
         __builtin_amdgcn_s_waitcnt(0);
+        if (fw && wave == nw - 1) form_weights(k1, 0);
         __syncthreads();
       }
     }
     for (int k = next_item(0); k < jn; k = next_item(k + 1)) {
-      const int m = sM[k];  // > 0: workgroup-uniform
-      const int it = sItem[k], slot = sSlot[k];
-      const float dtot = sDtot[k], eg = sEg[k];
+      const int m = __builtin_amdgcn_readfirstlane(sM[k]);  // > 0; these are workgroup-uniform
+      const int it = __builtin_amdgcn_readfirstlane(sItem[k]), slot = __builtin_amdgcn_readfirstlane(sSlot[k]);
+      const float dtot = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(fw ? sDT[buf] : sDtot[k])));
+      const float eg = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sEg[k])));
       const int bi = it / H, h = it - bi * H, g = h / HG;
       float yv = 0.f;  // this head's y (hot part and D x, from the stream kernel)
       if (tid < P) yv = a.y[(size_t)it * P + tid];
@@ -1627,13 +1750,10 @@ flush_kernel(StepArgs a) {
       const float* wgt = ws.w + (size_t)it * c;
       const size_t row0 = ((size_t)slot * H + h) * P;
       float* sBc = lds + buf * wfl;
-      uint16_t* sX = reinterpret_cast<uint16_t*>(sBc + fch * NC);
-      float* sW = sBc + fch * NC + fch * P / 2;
-      const float* sCq = sW + fch;  // C'[K:]
+      uint16_t* sX = reinterpret_cast<uint16_t*>(sBc + fa * NC);
+      float* sW = sBc + fa * NC + fa * SX / 2;
+      const float* sCq = sW + fa;  // C'[K:]
       float* sPart = sPart0 + buf * P * NT;
-      // the values the flush starts from: the single copy, or the master (fp32 or bf16)
-      const void* src = C::SEG ? static_cast<const void*>(a.cold) : static_cast<const void*>(a.master);
-      constexpr bool SRC16 = COLD == NSSM_COLD_BF16_SINGLE || C::MASTER16;
       const bool whole = m <= fch;  // the window fits in LDS: staged once
 
       // the next item's window goes to the other buffer during this item's contraction (the
@@ -1642,37 +1762,76 @@ flush_kernel(StepArgs a) {
         const int knext = next_item(k + 1);
         if (knext < jn) stage_item(knext, buf ^ 1);
       }
+
       for (int u0 = 0; u0 < nunit; u0 += UPP) {
-        // this wave's work unit in the pass: n-tile nt, p-tiles pt0 .. pt0 + npt - 1
-        const int u = u0 + wave;
-        const bool act = wave < UPP && u < nunit;  // wave-uniform
-        const int nt = u % NT, pt0 = (u / NT) * ptw, npt = act ? min(ptw, PT - pt0) : 0;
-        // the pass's state tiles are loaded before the window
-        f4 old[kMfmaTiles];
-        u2v old16[SRC16 ? kMfmaTiles : 1];
-        u2v rb16[COLD == NSSM_COLD_BF16 ? kMfmaTiles : 1];
-        uint32_t r8[C::E4M3 ? kMfmaTiles : 1];
-        float rsc[C::E4M3 ? kMfmaTiles : 1];
-#pragma unroll
-        for (int i = 0; i < kMfmaTiles; ++i) {
-          if (i < npt) {
-            const size_t row = row0 + (pt0 + i) * 16 + li;
-            const int col = nt * 16 + 4 * lk;
-            if constexpr (SRC16)
-              old16[i] = ld_stream(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(src) + blk16(row, col, NC)));
-            else
-              old[i] = ld_stream(reinterpret_cast<const f4*>(static_cast<const float*>(src) + row * NC + col));
-            if constexpr (COLD == NSSM_COLD_BF16)
-              rb16[i] = ld_stream(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.cold) + blk16(row, col, NC)));
-            if constexpr (C::E4M3) {
-              r8[i] = ld_stream(reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(a.cold) + row * NC + col));
-              rsc[i] = a.scale[row];
-            }
-          }
-        }
+        int nt, pt0;
+        const int npt = unit_of(u0, nt, pt0);
+        load_tiles(k, u0);
         f4 acc[kMfmaTiles];
 #pragma unroll
         for (int i = 0; i < kMfmaTiles; ++i) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
+        // One 32-token k-step of A = (w B')^T (16 n x 32 tokens) against B = x (32 tokens x
+        // 16 p), tokens ks .. ks + 31 of the staged chunk of kn tokens: lane (li, lk) builds
+        // row / column li, tokens ks + lk + 4 j (j = 0 .. 7) of each operand (any assignment
+        // of tokens to k that A and B share gives the same product), A as the three bf16
+        // parts of v = w B' (hi + mid + lo == v), so the three bf16 products per token are
+        // exact and sum in fp32. A is built once per step for all of the wave's tiles (they
+        // share the n-tile). A step inside the chunk reads its operands unconditionally;
+        // the last step of a chunk that is not a whole number of steps (tail) reads the
+        // buffer's tokens past the chunk (held in the allocation, flush_alloc_tokens) and
+        // zeroes them in both operands.
+        auto kstep = [&](int ks, int kn, auto tail_tag, auto ntiles) {
+          constexpr bool TAIL = decltype(tail_tag)::value;
+          const int kg = ks + 4 * lk;  // this lane group's tokens: kg + 16 q + r
+          // A: this lane's row li of w B' over its 8 tokens, through the bank swizzle (bit 2
+          // of kg + 16 q + r is lk & 1); the empty asm keeps the compiler from turning the
+          // per-token addresses into loop-carried registers (token (q, r) is then an
+          // immediate offset, (16 q + r) NC floats)
+          int bo = kg * NC + 4 * ((4 * nt + (li >> 2)) ^ (flush_swz_b<NC>() * (lk & 1))) + (li & 3);
+          asm volatile("" : "+v"(bo));
+          const f4 w0 = *reinterpret_cast<const f4*>(sW + kg), w1 = *reinterpret_cast<const f4*>(sW + kg + 16);
+          float v[8];
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int e = 4 * q + r;
+              v[e] = (q ? w1[r] : w0[r]) * sBc[bo + (16 * q + r) * NC];
+              if constexpr (TAIL) v[e] = kg + 16 * q + r < kn ? v[e] : 0.f;
+            }
+          }
+          u4v hv, mv, lv;
+          split3x8(v, hv, mv, lv);
+          __builtin_amdgcn_sched_barrier(0);
+          // B = x of each tile by two transposing loads (ds_read_b64_tr_b16: within a 16-lane
+          // group, lane j's element r comes from lane (j >> 2) + 4 r, element j & 3): group
+          // lane li reads headdim rows 16 (pt0 + i) + 4 (li & 3) .. + 3 of token kg + 16 q +
+          // (li >> 2), so lane li gets row 16 (pt0 + i) + li of tokens kg + 16 q + r as
+          // elements 4 q + r, the tokens of A's elements. All loads first, then the products
+          // part by part across the tiles (independent accumulators back to back).
+          int xo = (kg + (li >> 2)) * SX + 16 * pt0 + 4 * (li & 3);
+          asm volatile("" : "+v"(xo));
+#pragma unroll
+          for (int i = 0; i < kMfmaTiles; ++i) {
+            if (i < ntiles) {  // wave-uniform
+              u2v h2[2];
+#pragma unroll
+              for (int q = 0; q < 2; ++q) {
+                short4v t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) short4v*)(sX + xo + 16 * q * SX + 16 * i));
+                if constexpr (TAIL) {
+#pragma unroll
+                  for (int r = 0; r < 4; ++r) t[r] = kg + 16 * q + r < kn ? t[r] : (short)0;
+                }
+                h2[q] = __builtin_bit_cast(u2v, t);
+              }
+              const bf16x8 xb = __builtin_bit_cast(bf16x8, (u4v{h2[0].x, h2[0].y, h2[1].x, h2[1].y}));
+              acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, hv), xb, acc[i], 0, 0, 0);
+              acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, mv), xb, acc[i], 0, 0, 0);
+              acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, lv), xb, acc[i], 0, 0, 0);
+            }
+          }
+        };
         for (int k0 = 0; k0 < m; k0 += fch) {
           const int kn = min(fch, m - k0);
           if (!pipe && (!whole || u0 == 0)) {  // a whole window is staged once, in the first pass
@@ -1680,61 +1839,32 @@ flush_kernel(StepArgs a) {
             // whole windows keep the pair's B' and C' from its previous head
             const bool withB = !whole || bkey0 != it / HG;
             bkey0 = whole ? it / HG : -1;
-            stage_window_dma<NC>(sBc, sX, sW, sW + fch, k0, kn, m, P, rb0, bcur, rx0, xcur, wgt, cq0, wave, lane, nw,
+            stage_window_dma<NC>(sBc, sX, sW, sW + fa, k0, kn, m, P, rb0, bcur, rx0, xcur, wgt, cq0, wave, lane, nw,
                                  withB);
             __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA has landed in LDS
             __syncthreads();
           }
-          // 32-token k-steps of A = (w B')^T (16 n x 32 tokens) against B = x (32 tokens x 16 p):
-          // lane (li, lk) builds row / column li, tokens 8 lk .. 8 lk + 7 of each operand from
-          // the staged window (zero past the chunk), A as the three bf16 parts of v = w B'
-          // (hi + mid + lo == v), so the three bf16 products per token are exact and sum in
-          // fp32. The tiles' chains are independent.
-          for (int ks = 0; act && ks < kn; ks += 32) {
-            // lane group lk takes the chunk's tokens kb + 4 j, j = 0 .. 7, in both operands
-            // (any assignment of tokens to k that A and B share gives the same product)
-            const int kb = ks + lk, odd = lk & 1;
-            // A, once per step for all of the wave's tiles (they share the n-tile): this
-            // lane's row li of w B' over its 8 tokens, through the bank swizzle (token
-            // kb + 4 j has kb's parity); the empty asm keeps the compiler from turning the
-            // per-token addresses into loop-carried registers (token j is then an immediate
-            // offset, 4 j NC floats, or a scalar one, 4 j P bf16)
-            int bo = kb * NC + 4 * ((4 * nt + (li >> 2)) ^ (flush_swz_b<NC>() * odd)) + (li & 3);
-            asm volatile("" : "+v"(bo));
-            float v[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              const bool live = kb + 4 * j < kn;
-              v[j] = live ? sW[kb + 4 * j] * sBc[bo + 4 * j * NC] : 0.f;
-            }
-            u4v hv, mv, lv;
-            split3x8(v, hv, mv, lv);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int i = 0; i < kMfmaTiles; ++i) {
-              if (i < npt) {  // wave-uniform
-                int xo = kb * P + 2 * ((8 * (pt0 + i) + (li >> 1)) ^ (flush_swz_x(P) * odd)) + (li & 1);
-                asm volatile("" : "+v"(xo));
-                uint32_t xw[4];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                  const uint32_t xs = kb + 4 * j < kn ? sX[xo + 4 * j * P] : 0u;
-                  xw[j >> 1] = (j & 1) ? (xw[j >> 1] | (xs << 16)) : xs;
-                }
-                const bf16x8 xb = __builtin_bit_cast(bf16x8, (u4v{xw[0], xw[1], xw[2], xw[3]}));
-                acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, hv), xb, acc[i], 0, 0, 0);
-                acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, mv), xb, acc[i], 0, 0, 0);
-                acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, lv), xb, acc[i], 0, 0, 0);
-              }
-            }
+          if (npt > 0) {
+            int ks = 0;
+            for (; ks + 32 <= kn; ks += 32) kstep(ks, kn, std::false_type{}, npt);
+            if (ks < kn) kstep(ks, kn, std::true_type{}, npt);
           }
         }
-        // new = total decay x old + Delta; readout partial of the old read copy
+        // Every load of this wave is waited for here, before its first store: the pass's
+        // state tiles, with pipe this wave's part of the next window, and the previous
+        // item's stores (loads and stores share one counter). The stores below then go out
+        // back to back, and the barrier after them waits for LDS only.
+        __builtin_amdgcn_s_waitcnt(0);
+        if (fw && u0 == 0 && wave == nw - 1) {  // the next item's weights (its dt staged above; published below)
+          const int knext = next_item(k + 1);
+          if (knext < jn) form_weights(knext, buf ^ 1);
+        }
+        // new = total decay x old + Delta (into acc; the bf16 copies rounded), and the
+        // readout partial of the old read copy
 #pragma unroll
         for (int i = 0; i < kMfmaTiles; ++i) {
           if (i < npt) {
             const int p = (pt0 + i) * 16 + li, col = nt * 16 + 4 * lk;
-            const size_t row = row0 + p;
             const f4 cq = *reinterpret_cast<const f4*>(sCq + col);
             if constexpr (SRC16) {
               float o4[4];
@@ -1761,23 +1891,15 @@ flush_kernel(StepArgs a) {
             nv.y = fmaf(dtot, old[i].y, nv.y);
             nv.z = fmaf(dtot, old[i].z, nv.z);
             nv.w = fmaf(dtot, old[i].w, nv.w);
-            if constexpr (COLD == NSSM_COLD_FP32) {
-              st_stream(nv, reinterpret_cast<f4*>(static_cast<float*>(a.cold) + row * NC + col));
-            } else if constexpr (SRC16) {  // bf16 single copy or bf16 master: RNE, and the
-              // e4m3 copy is quantized from the rounded values
-              const u2v t = f32x4_to_bf16(nv.x, nv.y, nv.z, nv.w);
-              st_stream(t, reinterpret_cast<u2v*>(static_cast<uint16_t*>(C::SEG ? a.cold : a.master) + blk16(row, col, NC)));
+            if constexpr (SRC16) {  // bf16 single copy or bf16 master: RNE (stored below as the
+              // bf16 of these exact values), and the e4m3 copy is quantized from the rounded values
               float r4[4];
-              bf16x4_to_f32(t, r4);
+              bf16x4_to_f32(f32x4_to_bf16(nv.x, nv.y, nv.z, nv.w), r4);
               nv = f4{r4[0], r4[1], r4[2], r4[3]};
-            } else {
-              st_stream(nv, reinterpret_cast<f4*>(static_cast<float*>(a.master) + row * NC + col));
             }
             acc[i] = nv;
             if constexpr (COLD == NSSM_COLD_BF16) {
-              const u2v t = f32x4_to_bf16(nv.x, nv.y, nv.z, nv.w);
-              st_stream(t, reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.cold) + blk16(row, col, NC)));
-              if constexpr (TF) bf16x4_to_f32(t, rd);  // the new read copy
+              if constexpr (TF) bf16x4_to_f32(f32x4_to_bf16(nv.x, nv.y, nv.z, nv.w), rd);  // the new read copy
             } else if constexpr (TF) {
               rd[0] = nv.x; rd[1] = nv.y; rd[2] = nv.z; rd[3] = nv.w;  // fp32 copy, or the rounded bf16 one
             }
@@ -1800,8 +1922,26 @@ flush_kernel(StepArgs a) {
             }
           }
         }
-        if (pipe) __builtin_amdgcn_s_waitcnt(0);  // this wave's part of the next window has landed
-        __syncthreads();  // partials and row maxima of this pass's tiles (and the next window)
+        // the stores: the fp32 copy, the single bf16 copy, or the master (fp32 or bf16) and
+        // the bf16 read copy (e4m3 codes after the row scale below)
+#pragma unroll
+        for (int i = 0; i < kMfmaTiles; ++i) {
+          if (i < npt) {
+            const size_t row = row0 + (pt0 + i) * 16 + li;
+            const int col = nt * 16 + 4 * lk;
+            if constexpr (COLD == NSSM_COLD_FP32)
+              st_stream(acc[i], reinterpret_cast<f4*>(static_cast<float*>(a.cold) + row * NC + col));
+            else if constexpr (SRC16)  // (acc holds bf16 values: this conversion is exact)
+              st_stream(f32x4_to_bf16(acc[i].x, acc[i].y, acc[i].z, acc[i].w),
+                        reinterpret_cast<u2v*>(static_cast<uint16_t*>(C::SEG ? a.cold : a.master) + blk16(row, col, NC)));
+            else
+              st_stream(acc[i], reinterpret_cast<f4*>(static_cast<float*>(a.master) + row * NC + col));
+            if constexpr (COLD == NSSM_COLD_BF16)  // the read copy: RNE of the fp32 master
+              st_stream(f32x4_to_bf16(acc[i].x, acc[i].y, acc[i].z, acc[i].w),
+                        reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.cold) + blk16(row, col, NC)));
+          }
+        }
+        lds_barrier();  // partials and row maxima of this pass's tiles (and the next window)
         if constexpr (C::E4M3) {
 #pragma unroll
           for (int i = 0; i < kMfmaTiles; ++i) {
@@ -1831,7 +1971,9 @@ flush_kernel(StepArgs a) {
               }
             }
           }
-          if constexpr (TF) __syncthreads();  // the partials of this pass's tiles
+          // every wave has read the row maxima (the next item rewrites them) and, teacher-
+          // forced, written its partials
+          lds_barrier();
         }
       }
       // y += exp(glog) (stale cold readout); the next item's first barrier (pipelined:
@@ -2293,10 +2435,10 @@ int cu_count() {
 // with its per-tile readout partials, two of each when pipelined, (+ e4m3 row maxima);
 // the kernel's own lists take under 2 KB more
 size_t flush_lds_bytes(int P, int K, int kind, int fch, bool pipe = false) {
-  const int NC = kN - K;
+  const int NC = kN - K, fa = flush_alloc_tokens(fch);
   const size_t tiles = (size_t)P * (NC / 16);
   const bool e4m3 = kind == NSSM_COLD_FP8 || kind == NSSM_COLD_FP8_BF16M;  // + row maxima
-  const size_t buf = (size_t)fch * NC + (size_t)fch * P / 2 + fch + NC + tiles;
+  const size_t buf = (size_t)fa * NC + (size_t)fa * flush_x_stride(P) / 2 + fa + NC + tiles;
   return ((pipe ? 2 : 1) * buf + (e4m3 ? tiles : 0)) * sizeof(float);
 }
 // LDS a flush workgroup may take: the device's per-workgroup limit, and a CU's LDS shared
@@ -2332,14 +2474,16 @@ bool lds_opt_in(const void* fn) {
   done.insert({dev, fn});
   return true;
 }
-// window tokens the flush kernel stages at a time: the whole window (c rounded up to the
-// matrix-core step of 4 tokens) when it fits, else the most that fit (0: none fit)
+// window tokens the flush kernel stages at a time: the whole window (c rounded up to a
+// multiple of 4) when its buffer (rounded up to 32 tokens, flush_alloc_tokens) fits, else
+// the most whole 32-token steps that fit (0: none fit)
 int flush_chunk(int P, int K, int kind, int c) {
   const size_t budget = kMaxLds - 2048;
-  const size_t fixed = flush_lds_bytes(P, K, kind, 0), per_tok = (size_t)(kN - K + P / 2 + 1) * sizeof(float);
-  const int fit = fixed >= budget ? 0 : (int)((budget - fixed) / per_tok) & ~3;
+  const size_t fixed = flush_lds_bytes(P, K, kind, 0);
+  const size_t per_tok = (size_t)(kN - K + flush_x_stride(P) / 2 + 1) * sizeof(float);
+  const int fit = fixed >= budget ? 0 : (int)((budget - fixed) / per_tok) & ~31;
   const int want = (c + 3) & ~3;
-  return want < fit ? want : fit;
+  return want <= fit ? want : fit;
 }
 
 // Longest window the stream kernel replays itself (VALU, window in LDS); longer ones go to
@@ -2462,15 +2606,13 @@ int launch_pair(const StepArgs& a, const Launch& L, hipStream_t st) {
     const int items = a.b * a.H, cap = kFlushPerCU * cu_count();
     const int grid = items < cap ? items : cap;
     const size_t flds = flush_lds_bytes(a.P, K, COLD, a.fch, a.fpipe != 0);
-    if (a.tf) {
-      if (flds > kMaxLds && !lds_opt_in(reinterpret_cast<const void*>(&flush_kernel<K, COLD, true>)))
-        return NSSM_E_LAUNCH;
-      hipLaunchKernelGGL((flush_kernel<K, COLD, true>), dim3((unsigned)grid), dim3(kFlushWaves * 64), flds, st, a);
-    } else {
-      if (flds > kMaxLds && !lds_opt_in(reinterpret_cast<const void*>(&flush_kernel<K, COLD>)))
-        return NSSM_E_LAUNCH;
-      hipLaunchKernelGGL((flush_kernel<K, COLD>), dim3((unsigned)grid), dim3(kFlushWaves * 64), flds, st, a);
-    }
+    auto go = [&](auto kern) {
+      if (flds > kMaxLds && !lds_opt_in(reinterpret_cast<const void*>(kern))) return NSSM_E_LAUNCH;
+      hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kFlushWaves * 64), flds, st, a);
+      return NSSM_OK;
+    };
+    const int frc = a.tf ? go(flush_kernel<K, COLD, true>) : go(flush_kernel<K, COLD, false>);
+    if (frc) return frc;
   } else if constexpr (K == kN) {  // untiered
     hipLaunchKernelGGL(fresh_kernel, dim3((unsigned)((size_t)a.b * a.H * (a.P / 2))), dim3(64), 0, st, a, hd_ro);
   } else {
@@ -2520,6 +2662,7 @@ int v4_step(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step
   a.fch = a.split ? flush_chunk(prm->P, tier->k_hot, tier->cold_kind, tier->c) : 0;
   a.fpipe = a.split && g_flush_pipe && flush_pipe(prm->P, tier->k_hot, tier->cold_kind, tier->c);
   if (a.fpipe) a.fch = (tier->c + 3) & ~3;
+  a.fw = a.fpipe && !exact;
   hipStream_t st = (hipStream_t)stream;
   switch (tier->k_hot) {
     case 16: return dispatch_kind<16>(a, tier->cold_kind, L, st);
