@@ -1589,13 +1589,14 @@ flush_kernel(StepArgs a) {
     rank0 += w2 < wave ? s : 0;
     total += s;
   }
-  const int64_t fitems = (int64_t)total * HG;  // heads of flagged pairs
+  const int fitems = total * HG;  // heads of flagged pairs (at most b H, far below 2^31: the workspace
+                                  // holds HD_STRIDE floats per head)
   // each workgroup takes a contiguous range of the ranked items (consecutive heads of a
   // pair in a row: the pair's B' window is staged once for them)
   const int bx = blockIdx.x, grid = gridDim.x;
-  const int64_t per_wg = (fitems + grid - 1) / grid;
-  const int64_t ilo = min((int64_t)bx * per_wg, fitems);
-  const int nmine = (int)(min(ilo + per_wg, fitems) - ilo);
+  const int per_wg = (fitems + grid - 1) / grid;
+  const int ilo = min(bx * per_wg, fitems);
+  const int nmine = min(ilo + per_wg, fitems) - ilo;
   int bkey0 = -1, bkey1 = -1;  // the pair whose B' and C' each window buffer holds (-1: none)
 
   // the state tiles of one pass of an item, in registers: issued early, used after the
@@ -1645,8 +1646,8 @@ flush_kernel(StepArgs a) {
     // ci / HG): the owners of ranks r_lo .. r_hi record their pairs (from the mask; a
     // thread with more than 64 pairs reads the flags past them again), then one thread
     // per item
-    const int64_t a0 = ilo + j0;
-    const int r_lo = (int)(a0 / HG), r_hi = (int)((a0 + jn - 1) / HG);
+    const int a0 = ilo + j0;
+    const int r_lo = a0 / HG, r_hi = (a0 + jn - 1) / HG;
     if (cnt > 0 && rank0 <= r_hi && rank0 + cnt > r_lo) {
       int r = rank0;
       uint64_t mrem = fmask;
@@ -1664,8 +1665,8 @@ flush_kernel(StepArgs a) {
     }
     __syncthreads();
     if (tid < jn) {
-      const int64_t ci = a0 + tid;
-      const int r = (int)(ci / HG), hh = (int)(ci - (int64_t)r * HG);
+      const int ci = a0 + tid;
+      const int r = ci / HG, hh = ci - r * HG;
       const int p = sPairOf[r - r_lo];
       const int bi = p / G, g = p - bi * G;
       const int it = bi * H + g * HG + hh;
