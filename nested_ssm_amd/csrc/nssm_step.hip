@@ -1639,30 +1639,42 @@ flush_kernel(StepArgs a) {
     }
   };
 
-  for (int j0 = 0; j0 < nmine; j0 += kFlushList) {
-    const int jn = min(kFlushList, nmine - j0);
-    __syncthreads();  // the previous list is consumed
-    // 2. list items ilo + j0 .. + jn - 1 (item ci: head ci % HG of the pair of rank
-    // ci / HG): the owners of ranks r_lo .. r_hi record their pairs (from the mask; a
-    // thread with more than 64 pairs reads the flags past them again), then one thread
-    // per item
-    const int a0 = ilo + j0;
-    const int r_lo = a0 / HG, r_hi = (a0 + jn - 1) / HG;
+  // 2. the pairs of this workgroup's ranks R0 .. R1 (items ilo .. ilo + nmine - 1; item ci is
+  // head ci % HG of the pair of rank ci / HG), recorded once in sPairOf by the threads that
+  // own them, from their masks (a thread with more than 64 pairs reads the flags past them
+  // again). When they are more than sPairOf holds (more than about kFlushList * HG items a
+  // workgroup), each list below records its own ranks, reading the flags again.
+  const int R0 = ilo / HG, R1 = nmine > 0 ? (ilo + nmine - 1) / HG : R0 - 1;
+  const bool once = R1 - R0 < kFlushList + 1;
+  auto record = [&](int r_lo, int r_hi, bool from_mask) {
     if (cnt > 0 && rank0 <= r_hi && rank0 + cnt > r_lo) {
-      int r = rank0;
-      uint64_t mrem = fmask;
-      while (mrem != 0 && r <= r_hi) {
-        const int j = __builtin_ctzll(mrem);
-        mrem &= mrem - 1;
-        if (r >= r_lo) sPairOf[r - r_lo] = p0 + j;
-        ++r;
+      int r = rank0, p = p0;
+      if (from_mask) {
+        uint64_t mrem = fmask;
+        while (mrem != 0 && r <= r_hi) {
+          const int j = __builtin_ctzll(mrem);
+          mrem &= mrem - 1;
+          if (r >= r_lo) sPairOf[r - r_lo] = p0 + j;
+          ++r;
+        }
+        p = p0 + 64;
       }
-      for (int p = p0 + 64; p < p1 && r <= r_hi; ++p) {
+      for (; p < p1 && r <= r_hi; ++p) {
         if (ws.fg[p] == 0) continue;
         if (r >= r_lo) sPairOf[r - r_lo] = p;
         ++r;
       }
     }
+  };
+  if (once) record(R0, R1, true);
+
+  for (int j0 = 0; j0 < nmine; j0 += kFlushList) {
+    const int jn = min(kFlushList, nmine - j0);
+    __syncthreads();  // the pairs are recorded; the previous list is consumed
+    // list items ilo + j0 .. + jn - 1, one thread per item
+    const int a0 = ilo + j0;
+    const int r_lo = once ? R0 : a0 / HG;  // the rank sPairOf[0] holds
+    if (!once) record(r_lo, (a0 + jn - 1) / HG, false);
     __syncthreads();
     if (tid < jn) {
       const int ci = a0 + tid;

@@ -255,6 +255,25 @@ def test_flush_windows_and_head_blocks(c, units):
     _run_v4(b, H, G, P, k, c, "fp32", steps=2 * c + 3, seed=40 + c + units, check_state_every=c)
 
 
+def test_flush_kernel_many_pairs_per_workgroup():
+    """A flush over more (request, group) pairs than the flush kernel records at once per
+    workgroup (one head per group, 4352 requests x 8 groups flushing together: about 68
+    pairs per workgroup, and 68 flags per ranking thread, past its 64-flag mask), so its
+    lists read the flags again. After the window every head's state equals the untiered
+    recurrence run on the GPU from the same state and inputs (fp32, rtol = atol = 1e-5)."""
+    b, H, G, P, k, c = 4352, 8, 8, 16, 32, 33
+    gen, prm, S0 = _setup(b, H, P, G, seed=303)
+    dprm = dev_params(prm)
+    (S_dev,) = to_dev(S0)
+    tier = V4Tier(b, H, P, G, k_hot=k, c=c, cold="fp32")
+    tier.join(dprm, S_dev)
+    for _ in range(c):
+        x, B, C, dt = to_dev(*oracle.make_step_inputs(b, H, P, 128, G, gen))
+        tier.step(dprm, x, B, C, dt)
+        fresh_step(dprm, S_dev, x, B, C, dt)
+    assert_close32(tier.materialize(dprm), S_dev, "state after a flush of 34816 heads", **FP32_TOL)
+
+
 @pytest.mark.parametrize("cold,k,c,P,units", [
     ("bf16", 32, 16, 80, 2), ("fp8", 32, 16, 80, 2), ("fp8", 64, 33, 48, 2), ("fp32", 96, 20, 80, 2),
     ("fp32", 32, 17, 256, 4), ("fp8", 32, 40, 256, 4), ("bf16", 64, 64, 256, 4), ("fp8", 32, 16, 80, 1),
