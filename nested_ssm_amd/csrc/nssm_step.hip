@@ -200,14 +200,14 @@ __host__ __device__ constexpr size_t blk16(size_t row, int col, int NC) {
 constexpr int kBlkSeg = 64;  // u2v (4 bf16) between consecutive segments of a blocked row
 
 // ---------------------------------------------------------------------------
-// prep: one workgroup (256 threads) per (group g, block of prb <= 8 requests).
-//  * rotation: [B' C'] = R_g [B C] for the block, a 128 x 128 by 128 x 16 product on
-//    the matrix cores (v_mfma_f32_16x16x4_f32, fp32 products and sums): columns
-//    j < 8 are B of request j, j >= 8 C of request j - 8 (staged in LDS); wave w owns
-//    the output row tiles w and w + 4. A lane loads R as float4 (R[m][k..k+3]); the
-//    four MFMA steps of a 16-wide k block take the float4's elements in turn, and the
-//    B operand takes the same k order, so each step pairs equal k. The group's R is
-//    read once per block;
+// prep: one workgroup (256 threads) per (group g, block of prb <= kPrepReq requests).
+//  * rotation: [B' C'] = R_g [B C] for the block, a 128 x 128 by 128 x 2 kPrepReq product
+//    on the matrix cores (v_mfma_f32_16x16x4_f32, fp32 products and sums) in 16-column
+//    tiles: columns j < kPrepReq are B of request j, the others C of request j - kPrepReq
+//    (staged in LDS); wave w owns the output row tiles w and w + 4. A lane loads R as
+//    float4 (R[m][k..k+3]); the four MFMA steps of a 16-wide k block take the float4's
+//    elements in turn, and the B operand takes the same k order, so each step pairs equal
+//    k. The group's R is read once per block;
 //  * one thread per (request, head) of the block computes the head's dt, decay,
 //    stale-read factor, flush flag and, at a flush, the window weights; updates t,
 //    nv, glog; appends dt and (rotation lanes) the B' cold columns to the ring at
@@ -215,7 +215,10 @@ constexpr int kBlkSeg = 64;  // u2v (4 bf16) between consecutive segments of a b
 //    positions [c-m, c).
 // Latency bound: every independent global load is issued before the first barrier.
 constexpr int kPrepThreads = 256;
-constexpr int kPrepReq = 8;  // requests per prep workgroup (at most)
+// Requests per prep workgroup (at most; a multiple of 8). Measured with 16 (a 128 x 32 product,
+// half the workgroups): prep at the 9B shape 9.6 -> 12.9 us per launch at B = 256 and 13.5 ->
+// 14.6 us at B = 384 (each workgroup's chain grows more than the launch shrinks).
+constexpr int kPrepReq = 8;
 
 // A head's dt (softplus, with the dt_min floor of the native path) and the scalars every
 // stream kernel reads: dt, a = dt A, exp(a), D. Returns dt.
@@ -233,7 +236,7 @@ __device__ __forceinline__ float head_scalars(float* __restrict__ hd, float draw
 
 template <bool TIERED>
 __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
-  __shared__ float sX[2 * kPrepReq][kN];  // B (j < 8) and C (j >= 8) of the block's requests
+  __shared__ float sX[2 * kPrepReq][kN];  // B (j < kPrepReq) and C (j >= kPrepReq) of the block's requests
   __shared__ int sSlot[kPrepReq], sTr[kPrepReq], sNvr[kPrepReq], sFl[kPrepReq];
   // exact readout and query gate: B', C' of the block; s_j = C'_cold . B'_j over each
   // window; each request's cold energy fraction; gated / kept head counts
@@ -332,35 +335,39 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
   }
   __syncthreads();
 
-  // 2. rotation and its stores
+  // 2. rotation and its stores: column tile ct of the product holds columns j = 16 ct + li
+  // (B of request j for j < kPrepReq, C of request j - kPrepReq after)
   if (Rg) {
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2) {
-      f4 acc = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kb = 0; kb < kN / 16; ++kb) {
-        const f4 xb = *reinterpret_cast<const f4*>(&sX[li][kb * 16 + 4 * lk]);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ra[t2][kb].x, xb.x, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ra[t2][kb].y, xb.y, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ra[t2][kb].z, xb.z, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ra[t2][kb].w, xb.w, acc, 0, 0, 0);
-      }
-      // lane (li, lk) holds rows m0 + 4 lk .. +3 of column li
-      const int m0 = (wave + 4 * t2) * 16 + 4 * lk;
-      const int r = li & (kPrepReq - 1), which = li >> 3;
-      if constexpr (TIERED) {
-        if (rot_lds) *reinterpret_cast<f4*>(&sRot[li][m0]) = acc;
-      }
-      const int sl = r < nreq ? sSlot[r] : -1;
-      if (sl >= 0 && sl < a.slots) {
-        *reinterpret_cast<f4*>((which ? ws.C : ws.B) + ((size_t)(r0 + r) * G + g) * kN + m0) = acc;
+      for (int ct = 0; ct < 2 * kPrepReq / 16; ++ct) {
+        f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < kN / 16; ++kb) {
+          const f4 xb = *reinterpret_cast<const f4*>(&sX[16 * ct + li][kb * 16 + 4 * lk]);
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ra[t2][kb].x, xb.x, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ra[t2][kb].y, xb.y, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ra[t2][kb].z, xb.z, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ra[t2][kb].w, xb.w, acc, 0, 0, 0);
+        }
+        // lane (li, lk) holds rows m0 + 4 lk .. +3 of column 16 ct + li
+        const int m0 = (wave + 4 * t2) * 16 + 4 * lk;
+        const int j = 16 * ct + li, r = j % kPrepReq, which = j / kPrepReq;
         if constexpr (TIERED) {
-          // ring append of the B' cold columns (tokens that do not flush; a flush
-          // token's columns are read from the workspace). x goes to the ring from
-          // the stream kernel.
-          const int tr = sTr[r];
-          if (which == 0 && m0 >= a.K && (tr + 1) % c != 0)
-            *reinterpret_cast<f4*>(a.ring_b + (((size_t)sl * G + g) * c + tr % c) * (kN - a.K) + (m0 - a.K)) = acc;
+          if (rot_lds) *reinterpret_cast<f4*>(&sRot[j][m0]) = acc;
+        }
+        const int sl = r < nreq ? sSlot[r] : -1;
+        if (sl >= 0 && sl < a.slots) {
+          *reinterpret_cast<f4*>((which ? ws.C : ws.B) + ((size_t)(r0 + r) * G + g) * kN + m0) = acc;
+          if constexpr (TIERED) {
+            // ring append of the B' cold columns (tokens that do not flush; a flush
+            // token's columns are read from the workspace). x goes to the ring from
+            // the stream kernel.
+            const int tr = sTr[r];
+            if (which == 0 && m0 >= a.K && (tr + 1) % c != 0)
+              *reinterpret_cast<f4*>(a.ring_b + (((size_t)sl * G + g) * c + tr % c) * (kN - a.K) + (m0 - a.K)) = acc;
+          }
         }
       }
     }
@@ -428,12 +435,12 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
   }
 
   // 2c. query gate: rho_r = sum_{n>=K} C'_n^2 / max(sum_n C'_n^2, 1e-9) of each request
-  // (scale/v4_native_decode.py:147-156); wave 0, 8 lanes per request
+  // (scale/v4_native_decode.py:147-156); 8 lanes per request
   if constexpr (TIERED) {
     if (gate) {
       __syncthreads();  // sRot
-      if (wave == 0) {
-        const int r = lane >> 3, j = lane & 7;
+      if (tid < 8 * kPrepReq) {
+        const int r = tid >> 3, j = tid & 7;
         float ea = 0.f, ec = 0.f;
         for (int n = 4 * j; n < kN; n += 32) {  // K is a multiple of 16: a float4 is hot or cold
           const f4 v = *reinterpret_cast<const f4*>(&sRot[kPrepReq + r][n]);
