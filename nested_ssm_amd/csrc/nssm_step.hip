@@ -1399,7 +1399,10 @@ __global__ void __launch_bounds__(64) fresh_kernel(StepArgs a, const float* __re
 // Measured on MI355X (9B shape, B = 256, c = 64, fp32 cold), a full flush (32768 heads):
 // 965 us with the fp32 contraction, 810-850 with the three-part bf16 split, 714 with the
 // shared A operand and conflict-free window, 689-697 with a pair's B' staged once,
-// 661-681 with the transposing x loads, predicate-free steps and stores back to back; the
+// 661-681 with the transposing x loads, predicate-free steps and stores back to back,
+// 576-592 with plain state accesses (ld_flush / st_flush: WRITE_SIZE per full flush 1.25 ->
+// 1.00 GB; e4m3 over a bf16 master 931 -> 690 us, the bf16 read copy over an fp32 master
+// 1046 -> 819); the
 // ragged batch's per-token launch (B = 384, ~768 heads) 28.9 -> 29.3 us while prep drops
 // 19.9 -> 13.5 us without the window weights. Per-item phase timestamps (s_memrealtime)
 // put the contraction at about 1.3 us of a CU per item and the rest in load, store and
@@ -1438,6 +1441,23 @@ __device__ __forceinline__ void split3x8(const float (&v)[8], u4v& hi, u4v& mi, 
   hi = u4v{h[0], h[1], h[2], h[3]};
   mi = u4v{m[0], m[1], m[2], m[3]};
   lo = u4v{l[0], l[1], l[2], l[3]};
+}
+
+// The flush kernel's state accesses: a 16 x 16 tile row is 64 bytes of fp32, half of a
+// 128-byte line whose other half another wave of the workgroup reads and writes at about the
+// same time; plain accesses let L2 merge the halves (non-temporal ones went to HBM apart).
+#ifndef NSSM_FLUSH_NT
+#define NSSM_FLUSH_NT 0
+#endif
+template <class T>
+__device__ __forceinline__ T ld_flush(const T* p) {
+  if constexpr (NSSM_FLUSH_NT) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+template <class T>
+__device__ __forceinline__ void st_flush(T v, T* p) {
+  if constexpr (NSSM_FLUSH_NT) __builtin_nontemporal_store(v, p);
+  else *p = v;
 }
 
 #define NSSM_GLOBAL(p) ((const __attribute__((address_space(1))) void*)(p))
@@ -1633,13 +1653,13 @@ flush_kernel(StepArgs a) {
         const size_t row = row0 + (pt0 + i) * 16 + li;
         const int col = nt * 16 + 4 * lk;
         if constexpr (SRC16)
-          old16[i] = ld_stream(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(src) + blk16(row, col, NC)));
+          old16[i] = ld_flush(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(src) + blk16(row, col, NC)));
         else
-          old[i] = ld_stream(reinterpret_cast<const f4*>(static_cast<const float*>(src) + row * NC + col));
+          old[i] = ld_flush(reinterpret_cast<const f4*>(static_cast<const float*>(src) + row * NC + col));
         if constexpr (COLD == NSSM_COLD_BF16)
-          rb16[i] = ld_stream(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.cold) + blk16(row, col, NC)));
+          rb16[i] = ld_flush(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.cold) + blk16(row, col, NC)));
         if constexpr (C::E4M3) {
-          r8[i] = ld_stream(reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(a.cold) + row * NC + col));
+          r8[i] = ld_flush(reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(a.cold) + row * NC + col));
           rsc[i] = a.scale[row];
         }
       }
@@ -1950,14 +1970,14 @@ flush_kernel(StepArgs a) {
             const size_t row = row0 + (pt0 + i) * 16 + li;
             const int col = nt * 16 + 4 * lk;
             if constexpr (COLD == NSSM_COLD_FP32)
-              st_stream(acc[i], reinterpret_cast<f4*>(static_cast<float*>(a.cold) + row * NC + col));
+              st_flush(acc[i], reinterpret_cast<f4*>(static_cast<float*>(a.cold) + row * NC + col));
             else if constexpr (SRC16)  // (acc holds bf16 values: this conversion is exact)
-              st_stream(f32x4_to_bf16(acc[i].x, acc[i].y, acc[i].z, acc[i].w),
+              st_flush(f32x4_to_bf16(acc[i].x, acc[i].y, acc[i].z, acc[i].w),
                         reinterpret_cast<u2v*>(static_cast<uint16_t*>(C::SEG ? a.cold : a.master) + blk16(row, col, NC)));
             else
-              st_stream(acc[i], reinterpret_cast<f4*>(static_cast<float*>(a.master) + row * NC + col));
+              st_flush(acc[i], reinterpret_cast<f4*>(static_cast<float*>(a.master) + row * NC + col));
             if constexpr (COLD == NSSM_COLD_BF16)  // the read copy: RNE of the fp32 master
-              st_stream(f32x4_to_bf16(acc[i].x, acc[i].y, acc[i].z, acc[i].w),
+              st_flush(f32x4_to_bf16(acc[i].x, acc[i].y, acc[i].z, acc[i].w),
                         reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.cold) + blk16(row, col, NC)));
           }
         }
@@ -1975,7 +1995,7 @@ flush_kernel(StepArgs a) {
               const QDiv qd(sc);
               const f4 nv = acc[i];
               const uint32_t codes = f32x4_to_fp8(qd(nv.x), qd(nv.y), qd(nv.z), qd(nv.w));
-              st_stream(codes, reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.cold) + row * NC + nt * 16 + 4 * lk));
+              st_flush(codes, reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.cold) + row * NC + nt * 16 + 4 * lk));
               if (nt == 0 && lk == 0) a.scale[row] = sc;
               if constexpr (TF) {  // the readout of the new e4m3 copy
                 float rd[4];
