@@ -1319,8 +1319,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(unit_t
 // at this shape ran 6.73 TB/s in a skeleton over a 1.34 GB buffer, against 6.40 with four
 // float4 per lane (the unit kernel's shape at K = N). Workgroups in request, head, row
 // order. The arithmetic per element is the hot update's. Measured at the 9B shape, B = 256
-// (414 us per launch): two row pairs per wave with the coefficients loaded once 444 us;
-// 4, 8, 16 or 40 consecutive workgroups on one XCD (whole y sectors per L2, so WRITE_SIZE
+// (414 us per launch): two or four row pairs per wave with the coefficients loaded once and
+// the rows' y written by one store (WRITE_SIZE falls from 1.031 to 1.000 of the state and y
+// bytes) 425 us; 4, 8, 16 or 40 consecutive workgroups on one XCD (whole y sectors per L2, so WRITE_SIZE
 // at the algorithmic bytes) 435-447 us; without prep (each wave computing its head's dt
 // and decay from the raw inputs, no rotation) 572 us.
 __global__ void __launch_bounds__(64) fresh_kernel(StepArgs a, const float* __restrict__ hd_ro) {
