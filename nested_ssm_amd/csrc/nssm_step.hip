@@ -219,6 +219,7 @@ constexpr int kPrepThreads = 256;
 // half the workgroups): prep at the 9B shape 9.6 -> 12.9 us per launch at B = 256 and 13.5 ->
 // 14.6 us at B = 384 (each workgroup's chain grows more than the launch shrinks).
 constexpr int kPrepReq = 8;
+constexpr int kPrepStage = kPrepReq * kN / kPrepThreads;  // B (and C) elements a prep thread stages
 
 // A head's dt (softplus, with the dt_min floor of the native path) and the scalars every
 // stream kernel reads: dt, a = dt A, exp(a), D. Returns dt.
@@ -257,11 +258,25 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
     if (!a.R) {
       // untiered without a rotation: B and C converted straight into the workspace and the
       // head scalars written from registers, with no LDS and no barrier (at the 9B shape,
-      // B = 256: 6.2 us per launch through the staged path)
-      for (int i = tid; i < nreq * kN; i += kPrepThreads) {
+      // B = 256: 6.2 us per launch through the staged path). Every load is issued before
+      // the first store (one memory round trip, not one per element a thread converts).
+      // (a thread's elements past the block load its last element, so no load is predicated)
+      float bv[kPrepStage], cv[kPrepStage];
+#pragma unroll
+      for (int u = 0; u < kPrepStage; ++u) {
+        const int i = min(tid + u * kPrepThreads, nreq * kN - 1);
         const size_t o = ((size_t)r0 * G + g) * kN + (size_t)(i / kN) * G * kN + (i % kN);
-        ws.B[o] = bf2f(a.Bm[o]);
-        ws.C[o] = bf2f(a.Cm[o]);
+        bv[u] = bf2f(a.Bm[o]);
+        cv[u] = bf2f(a.Cm[o]);
+      }
+#pragma unroll
+      for (int u = 0; u < kPrepStage; ++u) {
+        const int i = tid + u * kPrepThreads;
+        const size_t o = ((size_t)r0 * G + g) * kN + (size_t)(i / kN) * G * kN + (i % kN);
+        if (i < nreq * kN) {
+          ws.B[o] = bv[u];
+          ws.C[o] = cv[u];
+        }
       }
       if (tid < nreq * HG) {
         const int hr = tid / HG, h = g * HG + (tid - hr * HG), bi = r0 + hr;
@@ -281,17 +296,17 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
   }
 
   // 1. independent loads: B and C of the block (zero past the last request), R, the
-  // head inputs
-  for (int i = tid; i < kPrepReq * kN; i += kPrepThreads) {
-    const int r = i / kN, n = i - r * kN;
-    float bv = 0.f, cv = 0.f;
-    if (r < nreq) {
-      const size_t o = ((size_t)(r0 + r) * G + g) * kN + n;
-      bv = bf2f(a.Bm[o]);
-      cv = bf2f(a.Cm[o]);
-    }
-    sX[r][n] = bv;
-    sX[kPrepReq + r][n] = cv;
+  // head inputs, all issued before the first LDS store
+  // (rows past the block load the block's last request and are zeroed after, so no load is
+  // predicated)
+  float bst[kPrepStage], cst[kPrepStage];
+#pragma unroll
+  for (int u = 0; u < kPrepStage; ++u) {
+    const int i = tid + u * kPrepThreads, r = i / kN, n = i - r * kN;
+    const size_t o = ((size_t)(r0 + min(r, nreq - 1)) * G + g) * kN + n;
+    bst[u] = bf2f(a.Bm[o]);
+    cst[u] = bf2f(a.Cm[o]);
+    if (r >= nreq) bst[u] = cst[u] = 0.f;
   }
   const float* __restrict__ Rg = a.R ? a.R + (size_t)g * kN * kN : nullptr;
   f4 ra[2][kN / 16];  // this lane's R operands of its two row tiles
@@ -332,6 +347,12 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
       sTr[hr] = tt;
       sNvr[hr] = nvv;
     }
+  }
+#pragma unroll
+  for (int u = 0; u < kPrepStage; ++u) {
+    const int i = tid + u * kPrepThreads, r = i / kN, n = i - r * kN;
+    sX[r][n] = bst[u];
+    sX[kPrepReq + r][n] = cst[u];
   }
   __syncthreads();
 
