@@ -220,6 +220,7 @@ constexpr int kPrepThreads = 256;
 // 14.6 us at B = 384 (each workgroup's chain grows more than the launch shrinks).
 constexpr int kPrepReq = 8;
 constexpr int kPrepStage = kPrepReq * kN / kPrepThreads;  // B (and C) elements a prep thread stages
+constexpr int kPrepDotBatch = 4;  // exact readout: window dots a prep lane group loads at once
 
 // A head's dt (softplus, with the dt_min floor of the native path) and the scalars every
 // stream kernel reads: dt, a = dt A, exp(a), D. Returns dt.
@@ -418,38 +419,103 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
     if (a.exact) {
       __syncthreads();  // sRot
       // 8 lanes per (request, window token): lane k of the group takes columns K + 32 i + 4 k
-      // (float4 each, all loads at once), then a DPP sum over the group's 8 lanes. The loop
-      // bound is uniform over each aligned 8-lane group, so every group's lanes sum together.
+      // (float4 each), then a DPP sum over the group's 8 lanes. The loop bounds are uniform
+      // over each aligned 8-lane group, so every group's lanes sum together.
       const int NC = kN - a.K, k8 = tid & 7;
-      for (int it = tid >> 3; it < nreq * c; it += kPrepThreads / 8) {
-        const int r = it / c, j = it - r * c;
-        const int sl = sSlot[r], nv = sNvr[r];
-        const bool live = sl >= 0 && sl < a.slots && j <= nv;
-        float acc = 0.f;
-        if (live) {
-          const float* bj = j < nv ? a.ring_b + (((size_t)sl * G + g) * c + (sTr[r] % c - nv + j)) * NC
-                                   : &sRot[r][a.K];
-          const float* cq = &sRot[kPrepReq + r][a.K];
-          f4 bv[kN / 32], cv[kN / 32];
+      constexpr int NG = kPrepThreads / 8;  // 8-lane groups
+      if (nreq * c <= NG) {
+        // one (request, window token) item per group: buffered tokens from the ring, this
+        // token (j = nv) from LDS
+        const int it = tid >> 3;
+        if (it < nreq * c) {
+          const int r = it / c, j = it - r * c;
+          const int sl = sSlot[r], nv = sNvr[r];
+          const bool live = sl >= 0 && sl < a.slots && j <= nv;
+          float acc = 0.f;
+          if (live) {
+            const float* bj = j < nv ? a.ring_b + (((size_t)sl * G + g) * c + (sTr[r] % c - nv + j)) * NC
+                                     : &sRot[r][a.K];
+            const float* cq = &sRot[kPrepReq + r][a.K];
+            f4 bv[kN / 32], cv[kN / 32];
 #pragma unroll
-          for (int i = 0; i < kN / 32; ++i) {  // NC is a multiple of 16: a float4 is inside or past it
-            if (32 * i + 4 * k8 < NC) {
-              bv[i] = *reinterpret_cast<const f4*>(bj + 32 * i + 4 * k8);
-              cv[i] = *reinterpret_cast<const f4*>(cq + 32 * i + 4 * k8);
+            for (int i = 0; i < kN / 32; ++i) {  // NC is a multiple of 16: a float4 is inside or past it
+              if (32 * i + 4 * k8 < NC) {
+                bv[i] = *reinterpret_cast<const f4*>(bj + 32 * i + 4 * k8);
+                cv[i] = *reinterpret_cast<const f4*>(cq + 32 * i + 4 * k8);
+              }
+            }
+#pragma unroll
+            for (int i = 0; i < kN / 32; ++i) {
+              if (32 * i + 4 * k8 < NC) {
+                acc = fmaf(bv[i].x, cv[i].x, acc);
+                acc = fmaf(bv[i].y, cv[i].y, acc);
+                acc = fmaf(bv[i].z, cv[i].z, acc);
+                acc = fmaf(bv[i].w, cv[i].w, acc);
+              }
             }
           }
+          acc = sum8(acc);
+          if (live && k8 == 0) sS[r][j] = acc;
+        }
+      } else {
+        // more items than groups: buffered tokens (j < nv) from the ring, kPrepDotBatch items
+        // per group and round with every load unpredicated (an item that is not buffered, or
+        // of a slot out of range, reads its request's first buffered row, which live items
+        // read too; a column past the cold tier reads the tier's last float4; both dropped),
+        // so each round is one memory round trip; then this token (j = nv) from LDS
+        for (int it0 = tid >> 3; it0 < nreq * c; it0 += kPrepDotBatch * NG) {
+          f4 bv[kPrepDotBatch][kN / 32];
+#pragma unroll
+          for (int u = 0; u < kPrepDotBatch; ++u) {
+            const int it = min(it0 + u * NG, nreq * c - 1), r = it / c, j = it - r * c;
+            const int sl = sSlot[r], nv = sNvr[r];
+            const int slc = sl >= 0 && sl < a.slots ? sl : 0;
+            const int pos = sTr[r] % c - nv + (j < nv ? j : 0);  // in [0, c): nv <= t % c
+            const float* bj = a.ring_b + (((size_t)slc * G + g) * c + pos) * NC;
+#pragma unroll
+            for (int i = 0; i < kN / 32; ++i)
+              bv[u][i] = *reinterpret_cast<const f4*>(bj + min(32 * i + 4 * k8, NC - 4));
+          }
+#pragma unroll
+          for (int u = 0; u < kPrepDotBatch; ++u) {
+            const int itr = it0 + u * NG, it = min(itr, nreq * c - 1), r = it / c, j = it - r * c;
+            const int sl = sSlot[r];
+            const bool live = itr < nreq * c && sl >= 0 && sl < a.slots && j < sNvr[r];
+            const float* cq = &sRot[kPrepReq + r][a.K];
+            float acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < kN / 32; ++i) {
+              if (32 * i + 4 * k8 < NC) {
+                const f4 cv = *reinterpret_cast<const f4*>(cq + 32 * i + 4 * k8);
+                acc = fmaf(bv[u][i].x, cv.x, acc);
+                acc = fmaf(bv[u][i].y, cv.y, acc);
+                acc = fmaf(bv[u][i].z, cv.z, acc);
+                acc = fmaf(bv[u][i].w, cv.w, acc);
+              }
+            }
+            acc = sum8(acc);
+            if (live && k8 == 0) sS[r][j] = acc;
+          }
+        }
+        for (int r = tid >> 3; r < nreq; r += NG) {
+          const int sl = sSlot[r];
+          const float* bq = &sRot[r][a.K];
+          const float* cq = &sRot[kPrepReq + r][a.K];
+          float acc = 0.f;
 #pragma unroll
           for (int i = 0; i < kN / 32; ++i) {
             if (32 * i + 4 * k8 < NC) {
-              acc = fmaf(bv[i].x, cv[i].x, acc);
-              acc = fmaf(bv[i].y, cv[i].y, acc);
-              acc = fmaf(bv[i].z, cv[i].z, acc);
-              acc = fmaf(bv[i].w, cv[i].w, acc);
+              const f4 b4 = *reinterpret_cast<const f4*>(bq + 32 * i + 4 * k8);
+              const f4 c4 = *reinterpret_cast<const f4*>(cq + 32 * i + 4 * k8);
+              acc = fmaf(b4.x, c4.x, acc);
+              acc = fmaf(b4.y, c4.y, acc);
+              acc = fmaf(b4.z, c4.z, acc);
+              acc = fmaf(b4.w, c4.w, acc);
             }
           }
+          acc = sum8(acc);
+          if (sl >= 0 && sl < a.slots && k8 == 0) sS[r][sNvr[r]] = acc;
         }
-        acc = sum8(acc);
-        if (live && k8 == 0) sS[r][j] = acc;
       }
       __syncthreads();  // sS
     }
