@@ -2814,6 +2814,16 @@ __global__ void __launch_bounds__(256) conv_update4_kernel(ConvArgs a) {
   if (i >= (int64_t)a.b * dq) return;
   const int r = (int)(i / dq), ch0 = 4 * (int)(i - (int64_t)r * dq);
   const size_t so = ((size_t)r * a.dim + ch0) * 4;  // first of the group's 16 state values
+  // the bias and mask loads go out first, beside the state loads (one round trip in all)
+  // (raw bits inside the branch, converted after it, so nothing waits for them there)
+  f4 bf = f4{0.f, 0.f, 0.f, 0.f};  // fp32 bias
+  u2v bh = u2v{0u, 0u};            // bf16 bias, channels 2 j, 2 j + 1 in word j
+  float mk = 1.f;
+  if (a.bias) {
+    if constexpr (DT == 0) bf = *reinterpret_cast<const f4*>(static_cast<const float*>(a.bias) + ch0);
+    else bh = *reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.bias) + ch0);
+  }
+  if (a.mask) mk = a.mask[r];
   float s[16], w[16], xin[4];
   uint32_t xraw[4];
   if constexpr (DT == 0) {
@@ -2860,14 +2870,15 @@ __global__ void __launch_bounds__(256) conv_update4_kernel(ConvArgs a) {
   uint32_t o[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    float acc = a.bias ? ld_dt<DT>(a.bias, ch0 + k) : 0.f;
+    const uint32_t bw = k < 2 ? bh.x : bh.y;
+    float acc = DT == 0 ? bf[k] : __uint_as_float(k & 1 ? bw & 0xffff0000u : bw << 16);  // the bias (0 without one)
     acc = fmaf(s[4 * k + 1], w[4 * k], acc);
     acc = fmaf(s[4 * k + 2], w[4 * k + 1], acc);
     acc = fmaf(s[4 * k + 3], w[4 * k + 2], acc);
     acc = fmaf(xin[k], w[4 * k + 3], acc);
     float u = round_dt<DT>(acc);
     u = round_dt<DT>(u / (1.f + expf(-u)));  // SiLU
-    if (a.mask) u = round_dt<DT>(u * a.mask[r]);
+    if (a.mask) u = round_dt<DT>(u * mk);
     o[k] = nssm_f32_to_bf16(u);
   }
   const u2v ov{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
@@ -3080,7 +3091,7 @@ int nssm_conv_update(int32_t b, int32_t dim, int32_t width, int32_t dtype, const
   const bool f32 = dtype == NSSM_DT_F32;
   const bool vec4 = width == 4 && I % 4 == 0 && GN % 4 == 0 && hbc_stride % 4 == 0 && aligned16(conv_state) &&
                     aligned16(weight) && (f32 ? aligned16(hbc) : aligned8(hbc)) && aligned8(x_out) &&
-                    aligned8(B_out) && aligned8(C_out);
+                    aligned8(B_out) && aligned8(C_out) && (!bias || (f32 ? aligned16(bias) : aligned8(bias)));
   if (vec4) {
     const unsigned grid4 = (unsigned)(((int64_t)b * (dim / 4) + 255) / 256);
     if (f32)
