@@ -48,12 +48,20 @@ def bytes_v4_token(k, c, cold, master="fp32", skip=0.0, exact=False):
     nc = N - k
     esz = {"fp32": 4, "bf16": 2, "fp8": 1}[cold]
     hot = 2 * H * P * k * 4
-    read = (H * P * nc * esz + (H * P * 4 if cold == "fp8" else 0)) * (1.0 - skip * (c - 1) / c)
+    scale = H * P * 4 if cold == "fp8" else 0  # e4m3 row scales
+    keep = (c - 1) / c * (1.0 - skip)  # tokens that read the read copy (no flush, cold term kept)
     if cold == "fp32" or (cold == "bf16" and master == "bf16"):
-        flush = H * P * nc * esz  # rewrite of the single copy (its read is the stale read)
-    else:  # master read + master write + read-copy write (+ scale)
+        # a single copy: read by every token (at the flush, the stale readout and the replay's
+        # start in one), rewritten at the flush
+        read = H * P * nc * esz * (keep + 1 / c)
+        flush = H * P * nc * esz
+    else:
+        # beside a master: the read copy (+ row scale) is read by the tokens that do not flush;
+        # the flush token reads the master and the row scale (its stale readout requantizes the
+        # master's values) and writes master, read copy and scale
         msz = 4 if master == "fp32" else 2
-        flush = H * P * nc * (2 * msz + esz) + (H * P * 4 if cold == "fp8" else 0)
+        read = (H * P * nc * esz + scale) * keep + scale / c
+        flush = H * P * nc * (2 * msz + esz) + scale
     ring_entry = H * P * 2 + H * 4 + G * nc * 4  # x bf16, dt, B' cold
     ring = (c - 1) / c * 2 * ring_entry  # written by c-1 of c tokens, read once at the flush
     corr = (H * P * 2 * (c - 1) / 2 + 2 * H * 4 * (c + 1) / 2) if exact else 0.0

@@ -9,7 +9,8 @@
  *
  * Notation: b = requests in a call, H heads, P headdim, N d_state (128),
  * G groups (HG = H/G heads per group), K = k_hot (hot columns: 16, 32, 64 or
- * 96), NC = N-K cold columns, c = flush period in tokens.
+ * 96; 0 for the teacher-forced readout only), NC = N-K cold columns, c = flush
+ * period in tokens.
  *
  * Reference interfaces these entry points replace (files of the reference
  * repository omin-Kwon/nested_ssm):
@@ -20,8 +21,9 @@
  *                        part), scale/vllm_v4_patch.py:140-179 (decode_readout)
  *   nssm_v4_step_gated   scale/v4_native_decode.py:118-127 (coldoff) and
  *                        :147-156 (qgate) of _v4_decode
- *   nssm_v4_step_teacher scale/nemo9b_eval.py:41-85 (naive_mixer_forward, mode
- *                        "v4": the teacher-forced evaluation readout)
+ *   nssm_v4_step_teacher scale/nemo9b_eval.py:41-85 (naive_mixer_forward, modes
+ *                        "v4" and, with k_hot = 0, "c1": the teacher-forced
+ *                        evaluation readout)
  *   nssm_v4_join         scale/vllm_v4_patch.py:123-137 (prefill_snapshot),
  *                        scale/v4_native_decode.py:234-243,
  *                        scale/v4_fused_decode.py:121-159 (prefill capture)
@@ -49,7 +51,7 @@
 extern "C" {
 #endif
 
-#define NSSM_ABI_VERSION 11
+#define NSSM_ABI_VERSION 12
 
 /* error codes */
 #define NSSM_OK 0
@@ -124,7 +126,9 @@ typedef struct nssm_step_inputs {
  *   nv       int32 [slots][H]           buffered tokens since the last snapshot
  *   glog     fp32 [slots][H]            log-decay since the snapshot, one token lagged
  * All heads of a slot carry equal t and nv. hot, cold, master, ring_x and ring_b
- * are 16-byte aligned.
+ * are 16-byte aligned. k_hot = 0 (every column cold; hot may be NULL, it is never
+ * read) needs a cold tier and serves nssm_v4_step_teacher, join and materialize; the
+ * other step entry points return NSSM_E_DIMS for it.
  * Unit-blocked (the bf16 read copies, the bf16 master): with row = (slot H + h) P + p,
  * element (row, col) sits at (row / 8) 8 NC + (col / 32) 256 + (row % 8) w + col % 32,
  * w = min(32, NC - 32 (col / 32)): the 8 rows of a unit form one block, 32-column segment
@@ -213,7 +217,10 @@ int nssm_v4_step_exact(const nssm_layer_params* prm, const nssm_tier* tier,
  * The reference snapshots at sequence positions t % c == 0 counted from 0: join a
  * sequence's start (its state, zeros from scratch) with phase c - 1 so that its flush
  * tokens are those. The tier bookkeeping is nssm_v4_step's, so the readouts may
- * alternate on one tier. NSSM_E_KIND for NSSM_COLD_NONE. */
+ * alternate on one tier. With k_hot = 0 every column is read from the snapshot: the
+ * loop's mode "c1" (scale/nemo9b_eval.py:79-80),
+ *   y = exp(glog + a) (cold_read C') + D x   (the new read copy at a flush token).
+ * NSSM_E_KIND for NSSM_COLD_NONE. */
 int nssm_v4_step_teacher(const nssm_layer_params* prm, const nssm_tier* tier,
                          const nssm_step_inputs* in, float* y, void* workspace,
                          int64_t workspace_bytes, void* stream);

@@ -1173,22 +1173,109 @@ __device__ __forceinline__ float cold_store(const StepArgs& a, size_t row, int q
   return pc;
 }
 
+// The read-copy values of master values v: bf16 RNE, or the e4m3 codes of v / sc decoded (qd
+// divides by the row's stored scale sc; the caller multiplies the readout by sc). Between
+// flushes the stored read copy is exactly this quantization of the unchanged master: the join
+// and every flush write both from the same values, with the same conversions.
+template <int COLD>
+__device__ __forceinline__ void requant4(const float (&v)[4], const QDiv& qd, float (&r)[4]) {
+  if constexpr (COLD == NSSM_COLD_BF16) bf16x4_to_f32(f32x4_to_bf16(v[0], v[1], v[2], v[3]), r);
+  else fp8x4_to_f32(f32x4_to_fp8(qd(v[0]), qd(v[1]), qd(v[2]), qd(v[3])), r);
+}
+template <int COLD>
+__device__ __forceinline__ void requant2(const float (&v)[2], const QDiv& qd, float (&r)[2]) {
+  if constexpr (COLD == NSSM_COLD_BF16) {
+    bf16x2_to_f32(f32x2_to_bf16(v[0], v[1]), r);
+  } else {
+    const f2 h = __builtin_amdgcn_cvt_pk_f32_fp8(__builtin_amdgcn_cvt_pk_fp8_f32(qd(v[0]), qd(v[1]), 0, false), false);
+    r[0] = h.x;
+    r[1] = h.y;
+  }
+}
+
+// C' of the cold columns in the segment mapping (k.Cc, k.Cch), for a kernel whose unit reads
+// its e4m3 copy in the contiguous mapping and needs the segment one only on a flush.
+template <int K, int COLD>
+__device__ __forceinline__ void coef_cold_seg(const float* wC, int q, Coef<K, COLD>& k) {
+  using C = Cfg<K, COLD>;
+#pragma unroll
+  for (int s = 0; s < C::CS; ++s) {
+    const f4 tc = *reinterpret_cast<const f4*>(wC + K + 32 * s + 4 * q);
+    k.Cc[s][0] = tc.x; k.Cc[s][1] = tc.y; k.Cc[s][2] = tc.z; k.Cc[s][3] = tc.w;
+  }
+  if constexpr (C::CH) {
+    const f2 tc = *reinterpret_cast<const f2*>(wC + K + 32 * C::CS + 2 * q);
+    k.Cch[0] = tc.x; k.Cch[1] = tc.y;
+  }
+}
+
 // One unit of a head that flushes at this token, in the stream kernel (short windows):
 // hot columns, the stale readout, and the exact cold state at this token, the decayed
 // snapshot plus the VALU replay of the staged window (sU [m][P] of this head,
-// sBc [m][NC]), scale/v4_fused_decode.py:76-85.
+// sBc [m][NC]), scale/v4_fused_decode.py:76-85. A single copy is read once (it is both the
+// stale snapshot and the replay's start); beside a master (fused_requant) only the master is
+// read, and the stale readout is formed from its values quantized again (requant4: the stored
+// read copy, bit for bit), so the flush token moves no read-copy bytes in.
 // TF (the teacher-forced readout): the cold term is the readout of the new state as stored
 // (the read copy), times HD_SNAPF = 1, instead of the stale snapshot's.
+// The master values of one unit row in the segment mapping (and, e4m3, the row scale), for
+// a flushing head of a kind with a master: loaded with the hot columns, ahead of the window
+// staging and its barrier.
+template <int K, int COLD>
+struct MasterRaw {
+  using C = Cfg<K, COLD>;
+  u2v m16[C::MASTER16 ? C::CSR : 1];
+  uint32_t m16h;
+  f4 m32[C::MASTER32 ? C::CSR : 1];
+  f2 m32h;
+  float sc;
+};
+template <int K, int COLD>
+__device__ __forceinline__ void master_load(const StepArgs& a, size_t row, int q, MasterRaw<K, COLD>& mr) {
+  using C = Cfg<K, COLD>;
+  constexpr int NC = C::NC, CS = C::CS;
+  if constexpr (C::MASTER16) {
+    const u2v* pm = reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.master) + blk16(row, 4 * q, NC));
+#pragma unroll
+    for (int s = 0; s < CS; ++s) mr.m16[s] = ld_stream(pm + kBlkSeg * s);
+    if constexpr (C::CH)
+      mr.m16h = ld_stream(reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(a.master) +
+                                                            blk16(row, 32 * CS + 2 * q, NC)));
+  } else if constexpr (C::MASTER32) {
+    const f4* pm = reinterpret_cast<const f4*>(static_cast<const float*>(a.master) + row * NC) + q;
+#pragma unroll
+    for (int s = 0; s < CS; ++s) mr.m32[s] = ld_stream(pm + 8 * s);
+    if constexpr (C::CH)
+      mr.m32h = ld_stream(reinterpret_cast<const f2*>(static_cast<const float*>(a.master) + row * NC + 32 * CS) + q);
+  }
+  if constexpr (C::E4M3) mr.sc = a.scale[row];
+}
+
+// Whether the fused replay of a kind with a master forms the stale readout from the master
+// (requant4) instead of loading the read copy: where the stream kernel compiles without
+// spills at its occupancy bound. The bf16 read copy at k_hot = 32 (64 registers) and the
+// k_hot = 16 kinds (80) spill three registers around the replay loop that way, and keep
+// the load.
+template <int K, int COLD>
+constexpr bool fused_requant() {
+  return (Cfg<K, COLD>::MASTER32 || Cfg<K, COLD>::MASTER16) && K != 16 && !(K == 32 && COLD == NSSM_COLD_BF16);
+}
+
 template <int K, int COLD, bool EXACT, bool TF = false>
 __device__ __forceinline__ void unit_compute_flush(const StepArgs& a, size_t sh, size_t rh, int p, int q,
                                                    UnitRaw<K, COLD>& d, const float* __restrict__ hd,
                                                    const Coef<K, COLD>& k, const float* sU, const float* sBc, int m,
-                                                   int ldu, int pofs) {
+                                                   int ldu, int pofs, const MasterRaw<K, COLD>* mr = nullptr) {
   using C = Cfg<K, COLD>;
   constexpr int NC = C::NC, CS = C::CS;
+  constexpr bool kMaster = fused_requant<K, COLD>();  // the read copy was not loaded
+  constexpr bool kRequant = kMaster && !TF;  // the stale readout from the master's values
   const size_t row = sh * a.P + p, yrow = rh * a.P + p;
   float part = hot_update<K, COLD>(a, row, q, d, hd, k);
-  if constexpr (!TF) part = fmaf(hd[HD_SNAPF], cold_partial<K, COLD>(d, k), part);
+  if constexpr (!TF && !kMaster) part = fmaf(hd[HD_SNAPF], cold_partial<K, COLD>(d, k), part);
+  const float osc = kRequant && C::E4M3 ? (mr ? mr->sc : a.scale[row]) : 1.f;  // the stored row scale
+  const QDiv oq(osc);
+  float pc = 0.f;  // kRequant: the stale readout partial of the requantized master
   const float dtot = hd[HD_DTOT];
   float nvv[C::CSR][4], nvh[2] = {0.f, 0.f};
 #pragma unroll
@@ -1199,10 +1286,16 @@ __device__ __forceinline__ void unit_compute_flush(const StepArgs& a, size_t sh,
     } else if constexpr (COLD == NSSM_COLD_BF16_SINGLE) {
       bf16x4_to_f32(d.cb[s], t);
     } else if constexpr (C::MASTER16) {
-      bf16x4_to_f32(ld_stream(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.master) + blk16(row, 4 * q, NC)) + kBlkSeg * s), t);
+      bf16x4_to_f32(mr ? mr->m16[s] : ld_stream(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.master) + blk16(row, 4 * q, NC)) + kBlkSeg * s), t);
     } else {  // fp32 master
-      const f4 m4 = ld_stream(reinterpret_cast<const f4*>(static_cast<const float*>(a.master) + row * NC) + q + 8 * s);
+      const f4 m4 = mr ? mr->m32[s] : ld_stream(reinterpret_cast<const f4*>(static_cast<const float*>(a.master) + row * NC) + q + 8 * s);
       t[0] = m4.x; t[1] = m4.y; t[2] = m4.z; t[3] = m4.w;
+    }
+    if constexpr (kRequant) {
+      float r[4];
+      requant4<COLD>(t, oq, r);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pc = fmaf(r[e], k.Cc[s][e], pc);
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) nvv[s][e] = t[e] * dtot;
@@ -1214,15 +1307,22 @@ __device__ __forceinline__ void unit_compute_flush(const StepArgs& a, size_t sh,
     } else if constexpr (COLD == NSSM_COLD_BF16_SINGLE) {
       bf16x2_to_f32(d.cbh, t);
     } else if constexpr (C::MASTER16) {
-      bf16x2_to_f32(ld_stream(reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(a.master) +
+      bf16x2_to_f32(mr ? mr->m16h : ld_stream(reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(a.master) +
                                                                blk16(row, 32 * CS + 2 * q, NC))), t);
     } else {
-      const f2 m2 = ld_stream(reinterpret_cast<const f2*>(static_cast<const float*>(a.master) + row * NC + 32 * CS) + q);
+      const f2 m2 = mr ? mr->m32h : ld_stream(reinterpret_cast<const f2*>(static_cast<const float*>(a.master) + row * NC + 32 * CS) + q);
       t[0] = m2.x; t[1] = m2.y;
+    }
+    if constexpr (kRequant) {
+      float r[2];
+      requant2<COLD>(t, oq, r);
+      pc = fmaf(r[0], k.Cch[0], pc);
+      pc = fmaf(r[1], k.Cch[1], pc);
     }
     nvh[0] = t[0] * dtot;
     nvh[1] = t[1] * dtot;
   }
+  if constexpr (kRequant) part = fmaf(hd[HD_SNAPF], C::E4M3 ? pc * osc : pc, part);
   for (int i = 0; i < m; ++i) {
     const float coef = sU[i * ldu + (p - pofs)];
     const float* bc = sBc + i * NC + 4 * q;
@@ -1299,7 +1399,7 @@ __device__ __forceinline__ void unit_hot_only(const StepArgs& a, const float* __
 // and the half segments' coefficients) above 6.
 template <int K, int COLD>
 constexpr int unit_waves_per_eu() {
-  return K == 32 ? (Cfg<K, COLD>::E4M3 ? 6 : 8) : K == kN ? 8 : K == 16 || K == 64 ? 6 : 5;
+  return K == 32 ? (Cfg<K, COLD>::E4M3 ? 6 : 8) : K == kN ? 8 : K == 16 || K == 64 ? 6 : K == 0 ? 6 : 5;
 }
 
 // GATED: the gated readout's variant, in which a head that prep marked HD_SKIP and that
@@ -1343,8 +1443,10 @@ __device__ __forceinline__ void unit_body(const StepArgs& a, const float* __rest
     }
   }
   UnitRaw<K, COLD> d;
-  // a flushing head's cold columns are needed here only when the replay is fused
-  unit_load<K, COLD>(a, row, rh * P + p, q, d, !FUSED && flushing);
+  // a flushing head's read copy is needed here only when the replay is fused and the copy is
+  // the replay's start (a single copy); beside a master the fused replay reads the master alone
+  constexpr bool kMaster = fused_requant<K, COLD>();
+  unit_load<K, COLD>(a, row, rh * P + p, q, d, flushing && (!FUSED || kMaster));
   // the exact readout's correction: without the fused replay there are registers to issue
   // its loads now, beside the state's, instead of a second round trip after them
   constexpr bool kCorrPre = EXACT && !FUSED && TIERED;
@@ -1363,10 +1465,18 @@ __device__ __forceinline__ void unit_body(const StepArgs& a, const float* __rest
       const int nr = uw * 8;
       float* sBc = lds;           // [m][NC]
       float* sU = lds + c * NC;   // [m][nr]
+      // beside a master, the master (and e4m3 row scale) loads go out with the hot columns'
+      // ahead of the staging, so the window's and the state's latencies overlap (the e4m3
+      // flush token over a bf16 master: 380 -> 365 us at B = 256, 662 -> 635 at B = 448)
+      MasterRaw<K, COLD> mr;
+      constexpr bool kEarly = kMaster;
+      if constexpr (kEarly) master_load<K, COLD>(a, row, q, mr);
       stage_unit_window<NC>(sBc, sU, m, P, p0, nr, a.ring_b + (((size_t)slot * a.G + g) * c + (c - m)) * NC, wB + K,
                             a.ring_x + (sh * c + (c - m)) * P, a.x + rh * P, ws.w + rh * c, tid, blockDim.x);
+      // the stale readout of the requantized master takes C' in the segment mapping
+      if constexpr (kMaster && !TF && C::CONTIG) coef_cold_seg<K, COLD>(wC, q, k);
       __syncthreads();
-      unit_compute_flush<K, COLD, EXACT, TF>(a, sh, rh, p, q, d, hd, k, sU, sBc, m, nr, p0);
+      unit_compute_flush<K, COLD, EXACT, TF>(a, sh, rh, p, q, d, hd, k, sU, sBc, m, nr, p0, kEarly ? &mr : nullptr);
       return;
     }
   }
@@ -1716,10 +1826,10 @@ flush_kernel(StepArgs a) {
 
   // the state tiles of one pass of an item, in registers: issued early, used after the
   // contraction
+  // (beside a master the old read copy is not loaded: it is the master's quantization, formed
+  // again from the master tiles, requant4)
   f4 old[kMfmaTiles];
   u2v old16[SRC16 ? kMfmaTiles : 1];
-  u2v rb16[COLD == NSSM_COLD_BF16 ? kMfmaTiles : 1];
-  uint32_t r8[C::E4M3 ? kMfmaTiles : 1];
   float rsc[C::E4M3 ? kMfmaTiles : 1];
   // this wave's work unit in the pass from unit u0: n-tile nt, p-tiles pt0 .. pt0 + npt - 1
   // (npt = 0: no unit in this pass)
@@ -1744,12 +1854,7 @@ flush_kernel(StepArgs a) {
           old16[i] = ld_flush(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(src) + blk16(row, col, NC)));
         else
           old[i] = ld_flush(reinterpret_cast<const f4*>(static_cast<const float*>(src) + row * NC + col));
-        if constexpr (COLD == NSSM_COLD_BF16)
-          rb16[i] = ld_flush(reinterpret_cast<const u2v*>(static_cast<const uint16_t*>(a.cold) + blk16(row, col, NC)));
-        if constexpr (C::E4M3) {
-          r8[i] = ld_flush(reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(a.cold) + row * NC + col));
-          rsc[i] = a.scale[row];
-        }
+        if constexpr (C::E4M3) rsc[i] = a.scale[row];
       }
     }
   };
@@ -2003,12 +2108,10 @@ flush_kernel(StepArgs a) {
             float rscale = 1.f;
             if constexpr (C::SEG) {  // the single copy is the read copy
               rd[0] = old[i].x; rd[1] = old[i].y; rd[2] = old[i].z; rd[3] = old[i].w;
-            } else if constexpr (COLD == NSSM_COLD_BF16) {
-              rd[0] = __uint_as_float(rb16[i].x << 16); rd[1] = __uint_as_float(rb16[i].x & 0xffff0000u);
-              rd[2] = __uint_as_float(rb16[i].y << 16); rd[3] = __uint_as_float(rb16[i].y & 0xffff0000u);
-            } else {
-              fp8x4_to_f32(r8[i], rd);
-              rscale = rsc[i];
+            } else {  // the master's read copy: bf16 RNE, or e4m3 at the stored row scale
+              const float ov[4] = {old[i].x, old[i].y, old[i].z, old[i].w};
+              if constexpr (C::E4M3) rscale = rsc[i];
+              requant4<COLD>(ov, QDiv(rscale), rd);
             }
             float pc = rd[0] * cq.x;
             pc = fmaf(rd[1], cq.y, pc);
@@ -2677,13 +2780,15 @@ int check_tier(const nssm_tier* tr, bool need_ring) {
   if (!tr) return NSSM_E_NULL;
   if (tr->cold_kind < NSSM_COLD_FP32 || tr->cold_kind > NSSM_COLD_FP8_BF16M) return NSSM_E_KIND;
   const bool cold = tr->cold_kind != NSSM_COLD_NONE;
-  if (!tr->hot || !tr->t || !tr->nv || !tr->glog || (cold && !tr->cold)) return NSSM_E_NULL;
+  // (k_hot = 0: no hot tier, every column cold; its hot pointer is never read)
+  if ((!tr->hot && tr->k_hot > 0) || !tr->t || !tr->nv || !tr->glog || (cold && !tr->cold)) return NSSM_E_NULL;
   if (cold && need_ring && (!tr->ring_x || !tr->ring_dt || !tr->ring_b)) return NSSM_E_NULL;
   const bool e4m3 = tr->cold_kind == NSSM_COLD_FP8 || tr->cold_kind == NSSM_COLD_FP8_BF16M;
   if ((tr->cold_kind == NSSM_COLD_BF16 || e4m3) && !tr->master) return NSSM_E_NULL;
   if (e4m3 && !tr->scale) return NSSM_E_NULL;
   if (tr->slots <= 0 || tr->c < 1 || tr->c > kMaxC) return NSSM_E_DIMS;
-  if (tr->k_hot != 16 && tr->k_hot != 32 && tr->k_hot != 64 && tr->k_hot != 96) return NSSM_E_DIMS;
+  if (tr->k_hot != 0 && tr->k_hot != 16 && tr->k_hot != 32 && tr->k_hot != 64 && tr->k_hot != 96) return NSSM_E_DIMS;
+  if (tr->k_hot == 0 && !cold) return NSSM_E_DIMS;
   if (!aligned16(tr->hot) || (cold && !aligned16(tr->cold)) || (tr->master && !aligned16(tr->master)))
     return NSSM_E_ALIGN;
   if (cold && need_ring && (!aligned16(tr->ring_x) || !aligned16(tr->ring_b))) return NSSM_E_ALIGN;
@@ -2709,6 +2814,11 @@ void fill_tier(StepArgs& a, const nssm_tier* tr) {
 template <int K, int COLD>
 int launch_pair(const StepArgs& a, const Launch& L, hipStream_t st) {
   constexpr bool TIERED = K < kN && COLD != NSSM_COLD_NONE;
+  // k_hot = 0 (every column cold, the evaluation forward's mode "c1") serves the
+  // teacher-forced readout only: the other stream and flush variants are not instantiated
+  constexpr bool kTfOnly = K == 0;
+  if constexpr (kTfOnly && !TIERED) return NSSM_E_KIND;
+  if (kTfOnly && !a.tf) return NSSM_E_DIMS;
   if (a.b == 0) return NSSM_OK;
   StepArgs ap = a;
   ap.prb = prep_requests(a.HG);
@@ -2719,16 +2829,24 @@ int launch_pair(const StepArgs& a, const Launch& L, hipStream_t st) {
   if constexpr (TIERED) {
     const bool gated = a.hot_only || a.qgate_tau > 0.f;
     if (L.fused) {
-      if (a.exact) hipLaunchKernelGGL((unit_kernel<K, COLD, true, true>), ugrid, ublock, L.lds, st, a, hd_ro);
-      else if (a.tf) hipLaunchKernelGGL((unit_kernel_tf<K, COLD, true>), ugrid, ublock, L.lds, st, a, hd_ro);
-      else if (gated) hipLaunchKernelGGL((unit_kernel_gated<K, COLD, true>), ugrid, ublock, L.lds, st, a, hd_ro);
-      else hipLaunchKernelGGL((unit_kernel<K, COLD, true, false>), ugrid, ublock, L.lds, st, a, hd_ro);
+      if constexpr (kTfOnly) {
+        hipLaunchKernelGGL((unit_kernel_tf<K, COLD, true>), ugrid, ublock, L.lds, st, a, hd_ro);
+      } else {
+        if (a.exact) hipLaunchKernelGGL((unit_kernel<K, COLD, true, true>), ugrid, ublock, L.lds, st, a, hd_ro);
+        else if (a.tf) hipLaunchKernelGGL((unit_kernel_tf<K, COLD, true>), ugrid, ublock, L.lds, st, a, hd_ro);
+        else if (gated) hipLaunchKernelGGL((unit_kernel_gated<K, COLD, true>), ugrid, ublock, L.lds, st, a, hd_ro);
+        else hipLaunchKernelGGL((unit_kernel<K, COLD, true, false>), ugrid, ublock, L.lds, st, a, hd_ro);
+      }
       return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
     }
-    if (a.exact) hipLaunchKernelGGL((unit_kernel<K, COLD, false, true>), ugrid, ublock, 0, st, a, hd_ro);
-    else if (a.tf) hipLaunchKernelGGL((unit_kernel_tf<K, COLD, false>), ugrid, ublock, 0, st, a, hd_ro);
-    else if (gated) hipLaunchKernelGGL((unit_kernel_gated<K, COLD, false>), ugrid, ublock, 0, st, a, hd_ro);
-    else hipLaunchKernelGGL((unit_kernel<K, COLD, false, false>), ugrid, ublock, 0, st, a, hd_ro);
+    if constexpr (kTfOnly) {
+      hipLaunchKernelGGL((unit_kernel_tf<K, COLD, false>), ugrid, ublock, 0, st, a, hd_ro);
+    } else {
+      if (a.exact) hipLaunchKernelGGL((unit_kernel<K, COLD, false, true>), ugrid, ublock, 0, st, a, hd_ro);
+      else if (a.tf) hipLaunchKernelGGL((unit_kernel_tf<K, COLD, false>), ugrid, ublock, 0, st, a, hd_ro);
+      else if (gated) hipLaunchKernelGGL((unit_kernel_gated<K, COLD, false>), ugrid, ublock, 0, st, a, hd_ro);
+      else hipLaunchKernelGGL((unit_kernel<K, COLD, false, false>), ugrid, ublock, 0, st, a, hd_ro);
+    }
     // one resident round of workgroups: an empty launch dispatches no more than that,
     // and a full flush keeps every workgroup busy to the end
     const int items = a.b * a.H, cap = kFlushPerCU * cu_count();
@@ -2739,11 +2857,13 @@ int launch_pair(const StepArgs& a, const Launch& L, hipStream_t st) {
       hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kFlushWaves * 64), flds, st, a);
       return NSSM_OK;
     };
-    const int frc = a.tf ? go(flush_kernel<K, COLD, true>) : go(flush_kernel<K, COLD, false>);
+    int frc;
+    if constexpr (kTfOnly) frc = go(flush_kernel<K, COLD, true>);
+    else frc = a.tf ? go(flush_kernel<K, COLD, true>) : go(flush_kernel<K, COLD, false>);
     if (frc) return frc;
   } else if constexpr (K == kN) {  // untiered
     hipLaunchKernelGGL(fresh_kernel, dim3((unsigned)((size_t)a.b * a.H * (a.P / 2))), dim3(64), 0, st, a, hd_ro);
-  } else {
+  } else if constexpr (!kTfOnly) {  // hot tier only
     hipLaunchKernelGGL((unit_kernel<K, COLD, false, false>), ugrid, ublock, 0, st, a, hd_ro);
   }
   return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
@@ -2772,6 +2892,7 @@ int v4_step(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step
   if ((rc = check_inputs(in, y))) return rc;
   if ((rc = check_tier(tier, true))) return rc;
   if (readout && tier->cold_kind == NSSM_COLD_NONE) return NSSM_E_KIND;  // these readouts need the cold tier
+  if (tier->k_hot == 0 && readout != 2) return NSSM_E_DIMS;  // every column cold: teacher-forced only
   if (!(fabsf(qgate_tau) <= 3.0e38f)) return NSSM_E_DIMS;  // NaN or infinite threshold
   if (qcounts && (reinterpret_cast<uintptr_t>(qcounts) & 7)) return NSSM_E_ALIGN;
   if (!in->slot_ids && in->b > tier->slots) return NSSM_E_DIMS;
@@ -2793,6 +2914,7 @@ int v4_step(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step
   a.fw = a.fpipe && !exact;
   hipStream_t st = (hipStream_t)stream;
   switch (tier->k_hot) {
+    case 0: return dispatch_kind<0>(a, tier->cold_kind, L, st);
     case 16: return dispatch_kind<16>(a, tier->cold_kind, L, st);
     case 32: return dispatch_kind<32>(a, tier->cold_kind, L, st);
     case 64: return dispatch_kind<64>(a, tier->cold_kind, L, st);
@@ -2918,9 +3040,10 @@ int64_t nssm_step_workspace_bytes(int32_t b, int32_t H, int32_t G, int32_t N, in
 int nssm_tier_sizes(int32_t slots, int32_t H, int32_t P, int32_t N, int32_t G, int32_t k_hot, int32_t c,
                     int32_t cold_kind, int64_t* sz) {
   if (!sz) return NSSM_E_NULL;
-  if (slots <= 0 || H <= 0 || P <= 0 || N != kN || G <= 0 || k_hot <= 0 || k_hot >= N || c < 1 || c > kMaxC)
+  if (slots <= 0 || H <= 0 || P <= 0 || N != kN || G <= 0 || k_hot < 0 || k_hot >= N || c < 1 || c > kMaxC)
     return NSSM_E_DIMS;
   if (cold_kind < NSSM_COLD_FP32 || cold_kind > NSSM_COLD_FP8_BF16M) return NSSM_E_KIND;
+  if (k_hot == 0 && cold_kind == NSSM_COLD_NONE) return NSSM_E_DIMS;  // no column kept at all
   const int64_t rows = (int64_t)slots * H * P;
   const int64_t NC = N - k_hot;
   int64_t esz = 0, msz = 0;  // bytes per element of the cold copy and of the master
@@ -3025,6 +3148,7 @@ int nssm_v4_join(const nssm_layer_params* prm, const nssm_tier* tier, const floa
   a.HG = prm->H / prm->G;
   const unsigned grid = (unsigned)b * prm->H;
   switch (tier->k_hot) {
+    case 0: launch_join<0>(a, tier->cold_kind, state, phase, grid, (hipStream_t)stream); break;
     case 16: launch_join<16>(a, tier->cold_kind, state, phase, grid, (hipStream_t)stream); break;
     case 32: launch_join<32>(a, tier->cold_kind, state, phase, grid, (hipStream_t)stream); break;
     case 64: launch_join<64>(a, tier->cold_kind, state, phase, grid, (hipStream_t)stream); break;

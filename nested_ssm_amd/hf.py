@@ -57,10 +57,14 @@ class ActRotMask(nn.Module):
         b, t, _ = x.shape
         return torch.einsum("btgn,gmn->btgm", x.view(b, t, self.ng, self.ds), self.R.to(x.dtype))
 
-    def _mask(self, x):
+    def _mask(self, x):  # (B, T, G, N): the coordinates at and above width zeroed (per request for a tensor)
         b, t = x.shape[:2]
-        if self.width < self.ds:
-            x = torch.cat([x[..., :self.width], torch.zeros_like(x[..., self.width:])], -1)
+        w = self.width
+        if torch.is_tensor(w):
+            keep = torch.arange(self.ds, device=x.device)[None, :] < w.to(x.device)[:, None]  # [B, N]
+            x = x * keep.to(x.dtype)[:, None, None, :]
+        elif w < self.ds:
+            x = torch.cat([x[..., :w], torch.zeros_like(x[..., w:])], -1)
         return x.reshape(b, t, self.ng * self.ds)
 
     def rotmask(self, x):
@@ -72,6 +76,18 @@ class ActRotMask(nn.Module):
             h, B, C = torch.split(x, [self.inter, self.ng * self.ds, self.ng * self.ds], dim=-1)
             x = torch.cat([h, self._mask(self._rot(B)), self._mask(self._rot(C))], dim=-1)
         return x
+
+
+def get_wrappers(model):
+    """Every ActRotMask of a model (scale/nemotron_retrofit.py:111-112)."""
+    return [m for m in model.modules() if isinstance(m, ActRotMask)]
+
+
+def set_width(model, w):
+    """Set the width mask of every wrapper (scale/nemotron_retrofit.py:114-116): rotated B and C
+    coordinates at and above w are zeroed (the evaluation forward folds a scalar w into R)."""
+    for m in get_wrappers(model):
+        m.width = w
 
 
 def mixer_rotation(m):

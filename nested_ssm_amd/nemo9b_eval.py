@@ -6,19 +6,27 @@ state_fp8, cold_fp8; scale/nemo9b_eval.py:12-17) and `naive_mixer_forward(self,
 input_states, cache_params=None, cache_position=None, attention_mask=None, **kw)`, bound to
 a NemotronHMamba2Mixer as the reference's driver does (`m.forward =
 naive_mixer_forward.__get__(m)`, scale/nemo9b_eval.py:185-186) to score whole sequences with
-the per-token v4 loop of scale/nemo9b_eval.py:41-85. A forward runs in_proj, the causal
-conv1d and the activation in torch (as the reference), then one state-op launch pair per
-token: mode "fresh" (or pb >= d_state) the untiered step, mode "v4" the teacher-forced
-readout of a tier that starts each sequence from a zero state (nssm_v4_step_teacher; the
-exact readout for the first `warm` tokens), then the gated norm and out_proj.
+the per-token loop of scale/nemo9b_eval.py:41-85. A forward runs in_proj, the causal conv1d
+and the activation in torch (as the reference), then one state-op launch pair per token:
+mode "fresh" (or "v4" with pb >= d_state) the untiered step; mode "v4" the teacher-forced
+readout of a tier with pb hot columns that starts each sequence from a zero state
+(nssm_v4_step_teacher; the exact readout for the first `warm` tokens); mode "c1" (every
+column stale, :79-80) the same readout of a tier with no hot column (k_hot = 0); then the
+gated norm and out_proj.
 
 The rotation R is read from the mixer (an ActRotMask-wrapped act, `_v4R` or `v4R`) and
 applied in fp32 inside the kernels; the wrapper's own activation is used, not its rotation.
-Deviations, each raising NotImplementedError: lag != 0, state_bf16, state_fp8, mode "c1"
-(every column stale: k_hot = 0 is not a tier), a width mask below d_state (set_width), and
-warm > 0 over a bf16 or e4m3 snapshot. cold_fp8 uses the tier's e4m3 format, the per-row
-scale amax / 448 + 1e-12 of scale/vllm_v4_patch.py:106-111, where the reference scales per
-column (amax over the head dimension, :62-64).
+A width below d_state (set_width, scale/nemotron_retrofit.py:114-116, as the driver's
+"hot-alone" needle arm sets it, scale/nemo9b_eval.py:198) zeroes the rotated B and C at and
+above `width` (ActRotMask._mask): the kernels get the rotation with those rows zeroed,
+diag(mask) R (the identity's when there is no R), which is the same product.
+
+cold_fp8 stores the tier's e4m3 format, the per-row scale amax / 448 + 1e-12 of
+scale/vllm_v4_patch.py:106-111, where this loop scales per column (amax over the head
+dimension, :62-64); the readout stays within the 2e-2 fp8 bar of that column emulation.
+Deviations, each raising NotImplementedError: lag != 0, state_bf16, state_fp8, a width
+given per request (a tensor), warm > 0 over a bf16 or e4m3 snapshot, and warm > 0 in mode
+"c1".
 """
 import torch
 
@@ -34,22 +42,44 @@ def _dt_min(m) -> float:
     return float(lim[0]) if lim is not None else float(getattr(m, "time_step_min", 0.0))
 
 
+def _wrapped(m) -> bool:
+    act = m.act
+    return hasattr(act, "R") and hasattr(act, "act")
+
+
 def _activation(m):
     """The mixer's activation without a rotation wrapper's rotation (the kernels rotate)."""
-    act = m.act
-    if hasattr(act, "R") and hasattr(act, "act"):
-        if getattr(act, "width", m.ssm_state_size) < m.ssm_state_size:
-            raise NotImplementedError("a width mask below d_state (set_width) is not served by the kernels")
-        return act.act
-    return act
+    return m.act.act if _wrapped(m) else m.act
+
+
+def _width(m) -> int:
+    """The rotation wrapper's width (set_width), d_state without a wrapper."""
+    N = m.ssm_state_size
+    w = getattr(m.act, "width", N) if _wrapped(m) else N
+    if torch.is_tensor(w):
+        raise NotImplementedError("a width per request (a tensor, ActRotMask._mask) is not served by the kernels")
+    return min(int(w), N)
+
+
+def _params(m):
+    """The kernels' layer parameters: the mixer's, with the width mask folded into R."""
+    prm = hf.layer_params(m, _dt_min(m))
+    w = _width(m)
+    if w < m.ssm_state_size:
+        G, N = m.n_groups, m.ssm_state_size
+        R = prm.R if prm.R is not None else torch.eye(N, device=prm.A.device).repeat(G, 1, 1)
+        R = R.clone()
+        R[:, w:, :] = 0.0  # rows m >= width: B'_m = C'_m = 0 (ActRotMask._mask)
+        prm.R = R.contiguous()
+    return prm
 
 
 def _check_cfg(cfg):
     for key in ("lag", "state_bf16", "state_fp8"):
         if cfg.get(key, 0):
             raise NotImplementedError(f"CFG[{key!r}] = {cfg[key]} is not served by the MI355X kernels")
-    if cfg["mode"] not in ("fresh", "v4"):
-        raise NotImplementedError(f"mode {cfg['mode']!r}: only 'fresh' and 'v4' are served by the kernels")
+    if cfg["mode"] not in ("fresh", "v4", "c1"):
+        raise NotImplementedError(f"mode {cfg['mode']!r}: 'fresh', 'v4' and 'c1' are served by the kernels")
 
 
 def teacher_forced_inputs(m, input_states):
@@ -87,13 +117,13 @@ def state_op(m, x, B, C, dt, cfg=None):
     N = m.ssm_state_size
     if N != N_STATE:
         raise ValueError(f"the MI355X kernels need d_state = {N_STATE} (mixer has {N})")
-    prm = hf.layer_params(m, _dt_min(m))
+    prm = _params(m)
     dev = x.device
     ys = torch.empty(B_, T, m.num_heads, m.head_dim, device=dev, dtype=torch.float32)
-    pb, c, warm = int(cfg["pb"]), int(cfg["c"]), int(cfg.get("warm", 0))
+    mode, pb, c, warm = cfg["mode"], int(cfg["pb"]), int(cfg["c"]), int(cfg.get("warm", 0))
     zeros = torch.zeros(B_, m.num_heads, m.head_dim, N, device=dev, dtype=torch.float32)
     y_t = torch.empty(B_, m.num_heads, m.head_dim, device=dev, dtype=torch.float32)
-    if cfg["mode"] == "fresh" or pb >= N:
+    if mode == "fresh" or (mode == "v4" and pb >= N):
         for t in range(T):  # the state starts from zeros and evolves in place
             fresh_step(prm, zeros, x[:, t].contiguous(), B[:, t].contiguous(), C[:, t].contiguous(),
                        dt[:, t].contiguous(), y=y_t)
@@ -103,7 +133,10 @@ def state_op(m, x, B, C, dt, cfg=None):
     if warm > 0 and cold != "fp32":
         raise NotImplementedError("warm tokens read the exact state; over a bf16 / e4m3 snapshot the kernels' "
                                   "exact readout reads the rounded snapshot instead")
-    tier = _tier(m, B_, pb, c, cold, dev)
+    k = 0 if mode == "c1" else pb  # c1: every column read from the snapshot
+    if warm > 0 and k == 0:
+        raise NotImplementedError("warm tokens in mode 'c1': a tier without hot columns has no exact readout")
+    tier = _tier(m, B_, k, c, cold, dev)
     # the sequence starts from zeros at position 0, a flush position: phase c - 1
     tier.join(prm, zeros, phase=torch.full((B_,), c - 1, dtype=torch.int32, device=dev))
     for t in range(T):

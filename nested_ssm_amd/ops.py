@@ -156,7 +156,10 @@ class V4Tier:
     vLLM paths keep the full fp32 state, scale/v4_native_decode.py:65-67). "bf16":
     the fused path's bf16 master (scale/v4_fused_decode.py:149,156-158): bf16 cold
     is then one bf16 copy, rewritten with the RNE of each flush; fp8 cold keeps a
-    bf16 master beside the e4m3 copy. fp32 cold is its own fp32 master."""
+    bf16 master beside the e4m3 copy. fp32 cold is its own fp32 master.
+
+    k_hot = 0 (every column cold, the evaluation forward's mode "c1") serves the
+    teacher-forced readout only (step(..., teacher=True))."""
 
     def __init__(self, slots: int, H: int, P: int, G: int, k_hot: int = 32, c: int = 4, cold: str = "fp32",
                  device="cuda", N: int = N_STATE, master: str = "fp32"):
@@ -265,6 +268,8 @@ class V4Tier:
             raise ValueError("noalloc serves the stale readout only")
         if teacher and (exact or gated):
             raise ValueError("the teacher-forced readout cannot be combined with exact, hot_only or qgate")
+        if self.k == 0 and not teacher:
+            raise ValueError("a tier with k_hot = 0 (every column cold) serves the teacher-forced readout only")
         if y is None:
             y = torch.empty(b, prm.H, prm.P, device=x.device, dtype=torch.float32)
         _need(y, "y", torch.float32, (b, prm.H, prm.P))

@@ -42,7 +42,14 @@ Pinning status of each function (how it is checked, in tests/test_oracle.py):
                     trajectory with the snapshot taken at the last t = c floor(t / c) after
                     its update and the decay summed over (ts, t] (a snapshot before the
                     update or an exclusive decay fails it; the decode readout of NativeV4
-                    is shown to differ); c = 1 and k = N give the fresh readout
+                    is shown to differ); c = 1 and k = N give the fresh readout; k = 0
+                    (mode "c1") the same closed form with no hot term; master="bf16" the
+                    fp64 trajectory with the cold columns rounded to bf16 at the join and
+                    at every snapshot (no rounding, or rounding every token, fails it)
+  mask_width        (set_width) the first `width` rotated coordinates of an explicit fp64
+                    rotation kept, the rest zero; a fresh trajectory under it keeps the
+                    masked state columns at zero and equals the trajectory of the
+                    width-dimensional rotated model
   quant_fp8 / read  torch float8_e4m3fn cast; scale = amax/448 + 1e-12 per row
   fp8_readout       closed form of the reference docstring vs an fp64 loop
   hot_only_step     the hot columns of an fp64 fresh trajectory (they never read the cold ones)
@@ -54,5 +61,5 @@ Pinning status of each function (how it is checked, in tests/test_oracle.py):
 from .v4_ref import (  # noqa: F401
     LayerParams, NativeV4, TeacherForcedV4, TieredV4, conv_update, fp8_readout, fresh_step, gated_rmsnorm, hot_only_step,
     make_layer_params,
-    make_rotation, make_state, make_step_inputs, quant_fp8, read_fp8, rotate, softplus_dt,
+    make_rotation, make_state, make_step_inputs, mask_width, quant_fp8, read_fp8, rotate, softplus_dt,
 )

@@ -93,10 +93,18 @@ def _heads(v: torch.Tensor, H: int) -> torch.Tensor:
     return v.repeat_interleave(H // G, dim=1)
 
 
-def _prep(x, B, C, dt_raw, prm: LayerParams, dtype):
+def mask_width(X: torch.Tensor, width: Optional[int]) -> torch.Tensor:
+    """ActRotMask._mask with a scalar width (set_width): the rotated coordinates at and
+    above `width` zeroed, the others kept (scale/nemotron_retrofit.py:29-37, :114-116)."""
+    if width is None or width >= X.shape[-1]:
+        return X
+    return torch.cat([X[..., :width], torch.zeros_like(X[..., width:])], -1)
+
+
+def _prep(x, B, C, dt_raw, prm: LayerParams, dtype, width: Optional[int] = None):
     xf = x.to(dtype)
-    Bp = _heads(rotate(B.to(dtype), prm.R), prm.H)
-    Cp = _heads(rotate(C.to(dtype), prm.R), prm.H)
+    Bp = _heads(mask_width(rotate(B.to(dtype), prm.R), width), prm.H)
+    Cp = _heads(mask_width(rotate(C.to(dtype), prm.R), width), prm.H)
     dt = softplus_dt(dt_raw.to(dtype), prm.dt_bias, prm.dt_min)
     a = dt * prm.A[None, :]
     return xf, Bp, Cp, dt, a
@@ -159,11 +167,13 @@ def gated_rmsnorm(y: torch.Tensor, gate: torch.Tensor, weight: torch.Tensor, gro
 
 # ---------------------------------------------------------------------------
 # fresh (untiered) step
-def fresh_step(S: torch.Tensor, x, B, C, dt_raw, prm: LayerParams, dtype=torch.float32) -> torch.Tensor:
+def fresh_step(S: torch.Tensor, x, B, C, dt_raw, prm: LayerParams, dtype=torch.float32,
+               width: Optional[int] = None) -> torch.Tensor:
     """S <- exp(dt A) S + (dt B') x;  y = S C' + D x  (S updated in place, y returned).
     scale/v4_native_decode.py:49-78 with pb >= N (the R applied by ActRotMask),
-    the same recurrence as transformers' mamba2_selective_state_update."""
-    xf, Bp, Cp, dt, a = _prep(x, B, C, dt_raw, prm, dtype)
+    the same recurrence as transformers' mamba2_selective_state_update. width: B' and C'
+    masked to their first `width` coordinates (mask_width)."""
+    xf, Bp, Cp, dt, a = _prep(x, B, C, dt_raw, prm, dtype, width)
     dA = torch.exp(a)[..., None, None]
     dB = dt[..., None, None] * Bp[:, :, None, :]
     S.copy_(S * dA + dB * xf[..., None])
@@ -421,12 +431,20 @@ class TeacherForcedV4:
     q: "fp32" the clone, "bf16" S.to(bf16).float() (:66-67), "fp8" e4m3 with either the
     reference's per-column scale (fp8_scale="column": amax over P, clamp(1e-6) / 448,
     :62-64) or the tier's per-row one (fp8_scale="row": amax over the cold columns / 448 +
-    1e-12, scale/vllm_v4_patch.py:106-111)."""
+    1e-12, scale/vllm_v4_patch.py:106-111).
+
+    k = 0 is the loop's mode "c1" (:79-80): every column read from the snapshot,
+    y_t = exp(Gtot_t - gSnap) (Snap C'_t) + D x_t. master="bf16" keeps the cold columns as
+    a bf16 master (the fused path's, scale/v4_fused_decode.py:149,156-158), as NativeV4
+    does: they are rounded to bf16 (RNE) at the join and at every snapshot, evolve in fp32
+    in between, and the snapshot is taken from the rounded values."""
 
     def __init__(self, slots: int, H: int, P: int, N: int, k: int, c: int, cold: str = "fp32",
-                 fp8_scale: str = "row", warm: int = 0, dtype=torch.float32):
-        assert 0 < k <= N and c >= 1 and cold in ("fp32", "bf16", "fp8") and fp8_scale in ("row", "column")
+                 fp8_scale: str = "row", warm: int = 0, dtype=torch.float32, master: str = "fp32"):
+        assert 0 <= k <= N and c >= 1 and cold in ("fp32", "bf16", "fp8") and fp8_scale in ("row", "column")
+        assert master in ("fp32", "bf16") and not (cold == "fp32" and master == "bf16")
         self.k, self.c, self.cold, self.fp8_scale, self.warm, self.dtype = k, c, cold, fp8_scale, warm, dtype
+        self.master = master
         self.S = torch.zeros(slots, H, P, N, dtype=dtype)
         self.snap = torch.zeros(slots, H, P, N - k, dtype=dtype)
         self.gtot = torch.zeros(slots, H, dtype=dtype)
@@ -446,21 +464,31 @@ class TeacherForcedV4:
             return read_fp8(q, sc).to(self.dtype)
         return S[..., k:].clone()
 
+    def _round_master(self, S: torch.Tensor) -> torch.Tensor:
+        """S with its cold columns rounded to the master precision."""
+        if self.master == "fp32":
+            return S
+        k = self.k
+        return torch.cat([S[..., :k], S[..., k:].to(torch.bfloat16).to(S.dtype)], dim=-1)
+
     def join(self, slots, S_new: torch.Tensor, t0: Optional[torch.Tensor] = None):
         """A sequence at position t0 (default 0) with state S_new: the snapshot is S_new."""
         slots = torch.as_tensor(slots, dtype=torch.long)
-        self.S[slots] = S_new.to(self.dtype)
+        self.S[slots] = self._round_master(S_new.to(self.dtype))
         self.snap[slots] = self._q(self.S[slots])
         self.gtot[slots] = 0
         self.gsnap[slots] = 0
         self.t[slots] = 0 if t0 is None else torch.as_tensor(t0, dtype=torch.int64)
 
-    def step(self, x, B, C, dt_raw, prm: LayerParams, slots: Optional[torch.Tensor] = None) -> torch.Tensor:
+    def step(self, x, B, C, dt_raw, prm: LayerParams, slots: Optional[torch.Tensor] = None,
+             width: Optional[int] = None) -> torch.Tensor:
+        """One token; width: B' and C' masked to their first `width` coordinates (the
+        rotation wrapper's set_width, mask_width)."""
         b = x.shape[0]
         slots = torch.arange(b) if slots is None else torch.as_tensor(slots, dtype=torch.long)
         k, c = self.k, self.c
         prm = prm.to(self.dtype)
-        xf, Bp, Cp, dt, a = _prep(x, B, C, dt_raw, prm, self.dtype)
+        xf, Bp, Cp, dt, a = _prep(x, B, C, dt_raw, prm, self.dtype, width)
         S = self.S[slots] * torch.exp(a)[..., None, None] + (dt[..., None, None] * Bp[:, :, None, :]) * xf[..., None]
         self.S[slots] = S
         gtot = self.gtot[slots] + a
@@ -469,6 +497,9 @@ class TeacherForcedV4:
         snapt = t % c == 0
         if bool(snapt.any()):
             ss = slots[snapt]
+            if self.master != "fp32":
+                S = torch.where(snapt[:, None, None, None], self._round_master(S), S)
+                self.S[slots] = S
             self.snap[ss] = self._q(S[snapt])
             self.gsnap[ss] = gtot[snapt]
         glog = gtot - self.gsnap[slots]

@@ -394,18 +394,26 @@ def test_phase_write_mid_window_recaptures_the_tier(monkeypatch, corr, t_new):
         assert m._v4state["t"] == t_new + n_after == int(ref.t[0])
 
 
-@pytest.mark.parametrize("cfg", [dict(mode="v4", c=4, pb=32), dict(mode="v4", c=4, pb=32, cold_bf16=1),
-                                 dict(mode="v4", c=16, pb=16), dict(mode="v4", c=3, pb=64, warm=5),
-                                 dict(mode="v4", c=4, pb=32, cold_fp8=1), dict(mode="fresh")])
-def test_teacher_forced_state_op_matches_oracle(cfg):
+@pytest.mark.parametrize("cfg,width", [(dict(mode="v4", c=4, pb=32), None), (dict(mode="v4", c=4, pb=32, cold_bf16=1), None),
+                                       (dict(mode="v4", c=16, pb=16), None), (dict(mode="v4", c=3, pb=64, warm=5), None),
+                                       (dict(mode="v4", c=4, pb=32, cold_fp8=1), None), (dict(mode="fresh"), None),
+                                       (dict(mode="c1", c=4), None), (dict(mode="c1", c=16, cold_fp8=1), None),
+                                       (dict(mode="c1", c=3, cold_bf16=1), None),
+                                       (dict(mode="fresh"), 32), (dict(mode="v4", c=4, pb=32), 48),
+                                       (dict(mode="c1", c=4), 64)])
+def test_teacher_forced_state_op_matches_oracle(cfg, width):
     """The evaluation forward's state op (nemo9b_eval drop-in: one teacher-forced launch pair
     per token, sequences from zero states) against the oracle's restatement of
-    scale/nemo9b_eval.py:41-85 on the same mixer inputs; fp32 1e-5, bf16 snapshot the bf16
-    bar, e4m3 (per-row scale) 2e-2."""
+    scale/nemo9b_eval.py:41-85 on the same mixer inputs, modes "fresh", "v4" and "c1" (every
+    column stale), with and without a width mask (set_width: the oracle masks the rotated
+    B and C, the drop-in folds the mask into R); fp32 1e-5, bf16 snapshot the bf16 bar, e4m3
+    (per-row scale) 2e-2."""
     from helpers import assert_close_flips, max_rel
     from nested_ssm_amd import hf, nemo9b_eval as NE
 
     model = _tiny_model(seed=41)
+    if width is not None:
+        hf.set_width(model, width)
     m = hf.mixers(model)[0]
     full = dict(NE.CFG, **cfg)
     hidden = torch.randn(2, 13, 128, generator=torch.Generator().manual_seed(42)).cuda()
@@ -413,12 +421,12 @@ def test_teacher_forced_state_op_matches_oracle(cfg):
         gate, x, B, C, dt = NE.teacher_forced_inputs(m, hidden)
         ys = NE.state_op(m, x, B, C, dt, full).cpu()
     prm = _oracle_params(m, float(m.time_step_limit[0]))
-    k = N if full["mode"] == "fresh" else full["pb"]
+    k = N if full["mode"] == "fresh" else 0 if full["mode"] == "c1" else full["pb"]
     cold = "fp8" if full["cold_fp8"] else "bf16" if full["cold_bf16"] else "fp32"
     ref = oracle.TeacherForcedV4(2, m.num_heads, m.head_dim, N, k, full["c"], cold=cold, warm=full["warm"])
     ref.join(torch.arange(2), torch.zeros(2, m.num_heads, m.head_dim, N))
     for t in range(13):
-        y_ref = ref.step(x[:, t].cpu(), B[:, t].cpu(), C[:, t].cpu(), dt[:, t].cpu(), prm)
+        y_ref = ref.step(x[:, t].cpu(), B[:, t].cpu(), C[:, t].cpu(), dt[:, t].cpu(), prm, width=width)
         if cold == "fp8":
             assert max_rel(ys[:, t], y_ref) <= 2e-2
         elif cold == "bf16":
@@ -458,3 +466,54 @@ def test_teacher_forced_forward_tracks_the_stock_forward():
     assert torch.equal(allhot, fresh)
     # stale cold columns move this small model's logits by ~1e-5 relative (fp32 rounding: ~1e-7)
     assert float((v4 - fresh).abs().max() / scale) > 5e-6
+
+
+def test_reference_eval_driver_loop_runs_on_the_drop_in():
+    """The evaluation driver of scale/nemo9b_eval.py:175-208 on the tiny model with
+    naive_mixer_forward bound to every mixer: the validation forward, the ppl loop over modes
+    ["c1", "v4"] and c, the needle arms fresh, hot-alone (set_width(model, pb)) and the mode
+    loop again at full width. Every forward runs; c1 and v4 differ from fresh and from each
+    other, hot-alone differs from fresh, and the full width restores the fresh logits (the
+    numerics of each arm are checked against the oracle at the state op)."""
+    from nested_ssm_amd import hf, nemo9b_eval as NE
+
+    ids = torch.randint(0, 96, (2, 36), generator=torch.Generator().manual_seed(45)).cuda()  # c = 16 flushes twice
+    model = _tiny_model(seed=46)
+    pb, cs = 32, [4, 16]
+    out = {}
+    saved = dict(NE.CFG)
+    try:
+        with torch.no_grad():
+            hf.set_width(model, 128)
+            for m in hf.mixers(model):
+                m.forward = NE.naive_mixer_forward.__get__(m)
+            NE.CFG["mode"] = "fresh"
+            out["fresh"] = model(ids, use_cache=False).logits.float()
+            for mode in ["c1", "v4"]:
+                for c in cs:
+                    NE.CFG.update(mode=mode, c=c, pb=pb)
+                    out[f"{mode}_c{c}"] = model(ids, use_cache=False).logits.float()
+            NE.CFG.update(mode="fresh")
+            out["needle_fresh"] = model(ids, use_cache=False).logits.float()
+            hf.set_width(model, pb)  # hot-alone: the cold columns discarded
+            out["needle_hotalone"] = model(ids, use_cache=False).logits.float()
+            hf.set_width(model, 128)
+            for mode in ["c1", "v4"]:
+                for c in cs:
+                    NE.CFG.update(mode=mode, c=c, pb=pb)
+                    out[f"needle_{mode}_c{c}"] = model(ids, use_cache=False).logits.float()
+    finally:
+        NE.CFG.clear()
+        NE.CFG.update(saved)
+    for name, v in out.items():
+        assert bool(torch.isfinite(v).all()), name
+    scale = out["fresh"].abs().max()
+    gap = lambda a, b: float((out[a] - out[b]).abs().max() / scale)  # noqa: E731
+    assert torch.equal(out["needle_fresh"], out["fresh"])
+    assert gap("needle_hotalone", "fresh") > 5e-6
+    for c in cs:
+        for arm in (f"c1_c{c}", f"v4_c{c}"):
+            assert gap(arm, "fresh") > 5e-6 and gap(arm, "needle_hotalone") > 5e-6, arm
+        assert gap(f"c1_c{c}", f"v4_c{c}") > 5e-6
+        assert torch.equal(out[f"needle_c1_c{c}"], out[f"c1_c{c}"])
+        assert torch.equal(out[f"needle_v4_c{c}"], out[f"v4_c{c}"])

@@ -57,7 +57,7 @@ def test_fresh_dt_min_and_identity_rotation():
 
 
 def _run_v4(b, H, G, P, k, c, cold, steps, seed, slots=None, phase=None, check_state_every=1, exact=False,
-            master="fp32", modes=None, counts=None):
+            master="fp32", modes=None, counts=None, each=None):
     gen, prm, S0 = _setup(b, H, P, G, seed)
     dprm = dev_params(prm)
     ref = oracle.NativeV4(b, H, P, 128, k, c, cold=cold, exact=exact, master=master)
@@ -95,6 +95,8 @@ def _run_v4(b, H, G, P, k, c, cold, steps, seed, slots=None, phase=None, check_s
                 assert_close32(tier.materialize(dprm), ref.S, f"materialized state step {step}", **FP32_TOL)
             else:  # a bf16 master: isolated one-ulp rounding flips (see assert_close_flips)
                 assert_close_flips(tier.materialize(dprm), ref.S, f"materialized state step {step}")
+        if each is not None:
+            each(step, tier, ref)
     return tier, ref, worst
 
 
@@ -540,6 +542,35 @@ def test_join_quantization_is_bit_exact(cold, master):
         assert torch.equal(tier.cold_t.cpu(), q.view(torch.uint8))
 
 
+def _assert_read_copy_is_master_quantization(tier, what):
+    """The stored read copy equals the quantization of the stored master, bit for bit: bf16
+    RNE, or the e4m3 codes of master / scale with the row scale amax / 448 + 1e-12."""
+    torch.cuda.synchronize()
+    mv = tier.master_rows().cpu().float()
+    if tier.cold == "bf16":
+        assert torch.equal(tier.cold_rows().cpu().view(torch.int16), mv.to(torch.bfloat16).view(torch.int16)), what
+    else:
+        q, sc = oracle.quant_fp8(mv)
+        assert torch.equal(tier.scale.cpu().view(torch.int32), sc[..., 0].contiguous().view(torch.int32)), what
+        assert torch.equal(tier.cold_t.cpu(), q.view(torch.uint8)), what
+
+
+@pytest.mark.parametrize("cold,master,k,c", [("fp8", "bf16", 32, 4), ("fp8", "fp32", 32, 4), ("bf16", "fp32", 64, 4),
+                                             ("fp8", "bf16", 96, 8), ("bf16", "fp32", 32, 4), ("fp8", "bf16", 32, 64),
+                                             ("fp8", "fp32", 32, 40), ("bf16", "fp32", 32, 64),
+                                             ("fp8", "bf16", 16, 64)])
+def test_read_copy_is_the_masters_quantization_after_flushes(cold, master, k, c):
+    """A flushing head beside a master forms its stale readout from the master's values
+    quantized again instead of loading the read copy (the fused replay, and the flush kernel
+    on the matrix cores). That is exact because the stored read copy is, after the join and
+    after every flush, the quantization of the stored master: checked bit for bit after every
+    step at random phases, both replay paths, with y against the oracle (fp8 2e-2, bf16 bar)."""
+    b, H, G, P = 4, 8, 2, 80
+    _run_v4(b, H, G, P, k, c, cold, steps=2 * c + 3, seed=300 + k + c, phase=[0, 1, c - 1, c // 2],
+            check_state_every=0, master=master,
+            each=lambda step, tier, ref: _assert_read_copy_is_master_quantization(tier, f"step {step}"))
+
+
 # --------------------------------------------------------------------------- k_hot = 16
 @pytest.mark.parametrize("exact", [False, True])
 @pytest.mark.parametrize("c", [4, 16, 64])
@@ -603,21 +634,29 @@ def test_join_quantization_is_bit_exact_k16(cold, master):
 
 
 # --------------------------------------------------------------------------- teacher-forced readout
-@pytest.mark.parametrize("cold,k,c", [("fp32", 32, 4), ("fp32", 32, 16), ("fp32", 32, 64), ("fp32", 16, 4),
-                                      ("fp32", 16, 40), ("bf16", 32, 4), ("bf16", 32, 64), ("fp8", 32, 4),
-                                      ("fp8", 32, 64), ("fp8", 16, 16)])
-def test_teacher_forced_readout_matches_oracle(cold, k, c):
-    """nssm_v4_step_teacher against the oracle's restatement of the evaluation forward's v4
-    loop (scale/nemo9b_eval.py:41-85): a sequence joined at its start with phase c - 1 flushes
-    at positions t % c == 0, reads the new state there and the snapshot with inclusive decay
-    elsewhere; fp32 rtol = atol = 1e-5, a bf16 snapshot (RNE of the exact state) the bf16 bar,
-    e4m3 (the tier's per-row scale) 2e-2 relative. The state is checked too."""
+@pytest.mark.parametrize("cold,k,c,master", [
+    ("fp32", 32, 4, "fp32"), ("fp32", 32, 16, "fp32"), ("fp32", 32, 64, "fp32"), ("fp32", 16, 4, "fp32"),
+    ("fp32", 16, 40, "fp32"), ("bf16", 32, 4, "fp32"), ("bf16", 32, 64, "fp32"), ("fp8", 32, 4, "fp32"),
+    ("fp8", 32, 64, "fp32"), ("fp8", 16, 16, "fp32"),
+    # the fused path's bf16 masters: one bf16 copy, e4m3 beside a bf16 master; both replay paths
+    ("bf16", 32, 4, "bf16"), ("bf16", 32, 64, "bf16"), ("fp8", 32, 4, "bf16"), ("fp8", 32, 64, "bf16"),
+    ("fp8", 16, 16, "bf16"), ("bf16", 16, 40, "bf16"),
+    # mode "c1": every column read from the snapshot (k_hot = 0)
+    ("fp32", 0, 4, "fp32"), ("fp32", 0, 16, "fp32"), ("fp32", 0, 64, "fp32"), ("bf16", 0, 4, "fp32"),
+    ("fp8", 0, 16, "fp32"), ("fp8", 0, 64, "bf16")])
+def test_teacher_forced_readout_matches_oracle(cold, k, c, master):
+    """nssm_v4_step_teacher against the oracle's restatement of the evaluation forward's loop
+    (scale/nemo9b_eval.py:41-85; mode "v4", and "c1" at k_hot = 0): a sequence joined at its
+    start with phase c - 1 flushes at positions t % c == 0, reads the new state there and the
+    snapshot with inclusive decay elsewhere; fp32 rtol = atol = 1e-5, a bf16 snapshot (RNE of
+    the exact state) and a bf16 master the bf16 bar, e4m3 (the tier's per-row scale) 2e-2
+    relative. The state is checked too (a bf16 master by the bf16 bar)."""
     b, H, G, P = 4, 8, 1, 80
     gen, prm, S0 = _setup(b, H, P, G, seed=260 + k + c)
     dprm = dev_params(prm)
-    ref = oracle.TeacherForcedV4(b, H, P, 128, k, c, cold=cold)
+    ref = oracle.TeacherForcedV4(b, H, P, 128, k, c, cold=cold, master=master)
     ref.join(torch.arange(b), S0)
-    tier = V4Tier(b, H, P, G, k_hot=k, c=c, cold=cold)
+    tier = V4Tier(b, H, P, G, k_hot=k, c=c, cold=cold, master=master)
     tier.join(dprm, *to_dev(S0), phase=torch.full((b,), c - 1, dtype=torch.int32, device="cuda"))
     worst = 0.0
     for step in range(2 * c + 5):
@@ -628,11 +667,42 @@ def test_teacher_forced_readout_matches_oracle(cold, k, c):
             r = max_rel(y.cpu(), y_ref)
             worst = max(worst, r)
             assert r <= 2e-2, f"fp8 teacher-forced y step {step}: {r:.3g}"
-        elif cold == "bf16":
+        elif cold == "bf16" or master == "bf16":
             worst = max(worst, assert_close_flips(y, y_ref, f"bf16 teacher-forced y step {step}"))
         else:
             assert_close32(y, y_ref, f"teacher-forced y step {step}", **FP32_TOL)
-    assert_close32(tier.materialize(dprm), ref.S, "teacher-forced state", **FP32_TOL)
+    if master == "bf16":
+        assert_close_flips(tier.materialize(dprm), ref.S, "teacher-forced state (bf16 master)")
+    else:
+        assert_close32(tier.materialize(dprm), ref.S, "teacher-forced state", **FP32_TOL)
+
+
+@pytest.mark.parametrize("b,H,G,k,c", [(4, 8, 1, 32, 4), (4, 8, 1, 32, 16), (2, 128, 8, 32, 4), (2, 128, 8, 32, 16),
+                                       (2, 128, 8, 0, 16), (4, 8, 1, 16, 64)])
+def test_teacher_forced_e4m3_within_the_reference_column_emulation(b, H, G, k, c):
+    """The evaluation forward's own e4m3 snapshot is scaled per column (amax over the head
+    dimension, clamp(1e-6) / 448, scale/nemo9b_eval.py:62-68); the tier stores the per-row
+    scale of scale/vllm_v4_patch.py:106-111. nssm_v4_step_teacher over an e4m3 tier (fp32 and
+    bf16 masters) stays within the fp8 bar, 2e-2 norm-wise relative on y, of the reference's
+    column emulation (oracle TeacherForcedV4(cold="fp8", fp8_scale="column")) on every one of
+    2c + 5 tokens, at the config-0 shape and at the 9B head shape (H = 128, G = 8)."""
+    P = 80
+    gen, prm, S0 = _setup(b, H, P, G, seed=400 + H + k + c)
+    dprm = dev_params(prm)
+    ref = oracle.TeacherForcedV4(b, H, P, 128, k, c, cold="fp8", fp8_scale="column")
+    ref.join(torch.arange(b), S0)
+    tiers = {m: V4Tier(b, H, P, G, k_hot=k, c=c, cold="fp8", master=m) for m in ("fp32", "bf16")}
+    for t in tiers.values():
+        t.join(dprm, *to_dev(S0), phase=torch.full((b,), c - 1, dtype=torch.int32, device="cuda"))
+    worst = 0.0
+    for step in range(2 * c + 5):
+        x, B, C, dt = oracle.make_step_inputs(b, H, P, 128, G, gen)
+        y_ref = ref.step(x, B, C, dt, prm)
+        for m, t in tiers.items():
+            r = max_rel(t.step(dprm, *to_dev(x, B, C, dt), teacher=True).cpu(), y_ref)
+            worst = max(worst, r)
+            assert r <= 2e-2, f"{m} master step {step}: {r:.3g} against the column-scale emulation"
+    assert worst > 0
 
 
 def test_teacher_forced_readout_from_scratch_with_ragged_starts():
@@ -657,3 +727,17 @@ def test_teacher_forced_readout_from_scratch_with_ragged_starts():
         y_ref = ref.step(x, B, C, dt, prm, slots=sl.long())
         y = tier.step(dprm, *to_dev(x, B, C, dt), slot_ids=sl.cuda(), teacher=True)
         assert_close32(y, y_ref, f"teacher-forced ragged y step {step}", **FP32_TOL)
+
+
+def test_c1_tier_refuses_the_other_readouts():
+    """A tier with k_hot = 0 (mode "c1") serves the teacher-forced readout only: the stale,
+    exact, gated and no-allocation steps raise before launching."""
+    b, H, G, P = 2, 8, 1, 80
+    gen, prm, S0 = _setup(b, H, P, G, seed=420)
+    dprm = dev_params(prm)
+    tier = V4Tier(b, H, P, G, k_hot=0, c=4)
+    tier.join(dprm, *to_dev(S0))
+    x, B, C, dt = to_dev(*oracle.make_step_inputs(b, H, P, 128, G, gen))
+    for kw in (dict(), dict(exact=True), dict(hot_only=True), dict(qgate=0.5), dict(noalloc=True)):
+        with pytest.raises(ValueError, match="k_hot = 0"):
+            tier.step(dprm, x, B, C, dt, **kw)

@@ -585,9 +585,9 @@ def test_gated_rmsnorm_matches_fp64_group_loop():
 
 
 # --------------------------------------------------------------------------- teacher-forced v4
-@pytest.mark.parametrize("k,c", [(32, 4), (16, 3), (96, 1), (32, 5)])
+@pytest.mark.parametrize("k,c", [(32, 4), (16, 3), (96, 1), (32, 5), (0, 4), (0, 1)])
 def test_teacher_forced_v4_equals_closed_form(k, c):
-    """scale/nemo9b_eval.py:41-85 (mode "v4"): at sequence position tau,
+    """scale/nemo9b_eval.py:41-85 (mode "v4"; k = 0 is mode "c1", :79-80): at sequence position tau,
     y = S_tau[:k] C'[:k] + exp(sum_{i=ts+1}^{tau} a_i) S_ts[k:] C'[k:] + D x with
     ts = c floor(tau / c) and S_ts the state AFTER token ts's update (fp64 fresh trajectory).
     Negative controls: an exclusive decay (sum to tau - 1) and a snapshot taken before the
@@ -666,3 +666,81 @@ def test_teacher_forced_v4_fp8_row_scale_is_close_to_the_column_scale():
         rel = lambda u, v: float((u - v).norm() / v.norm())  # noqa: E731
         assert rel(ys["row"], ys["fp32"]) <= 2e-2 and rel(ys["col"], ys["fp32"]) <= 2e-2
         assert rel(ys["row"], ys["col"]) <= 2e-2
+
+
+@pytest.mark.parametrize("cold,k,c", [("bf16", 32, 4), ("fp8", 32, 3), ("fp8", 0, 4), ("bf16", 16, 1)])
+def test_teacher_forced_v4_bf16_master_state_is_the_rounded_recurrence(cold, k, c):
+    """master="bf16": the state is the fp64 fresh recurrence with the cold columns rounded to
+    bf16 at the join and at every snapshot position (t % c == 0) - the state NativeV4's pinned
+    bf16 master holds when its flushes fall on the same tokens (joined at phase c - 1) - and
+    the snapshot is the quantization of the rounded values. Negative controls: without the
+    rounding, and with a rounding at every token, the state differs."""
+    b, H, P, G = 2, 4, 16, 2
+    gen, prm, S0 = _small(seed=340 + k + c, b=b, H=H, P=P, G=G)
+    S0 = S0 * 7.0  # magnitudes whose bf16 rounding is far above fp64 noise
+    tf = oracle.TeacherForcedV4(b, H, P, N, k, c, cold=cold, master="bf16", dtype=torch.float64)
+    tf.join(torch.arange(b), S0.double())
+    nat = oracle.NativeV4(b, H, P, N, k, c, cold=cold, master="bf16", dtype=torch.float64) if k else None
+    if nat is not None:
+        nat.join(torch.arange(b), S0.double(), phase=torch.full((b,), c - 1))
+    rnd = lambda S: torch.cat([S[..., :k], S[..., k:].to(torch.bfloat16).double()], -1)  # noqa: E731
+    S = rnd(S0.double())
+    S_none, S_every = S0.double().clone(), rnd(S0.double())
+    prm64 = prm.to(torch.float64)
+    for tau in range(3 * c + 2):
+        x, B, C, dt = oracle.make_step_inputs(b, H, P, N, G, gen)
+        tf.step(x, B, C, dt, prm)
+        for T in (S, S_none, S_every):
+            oracle.fresh_step(T, x, B, C, dt, prm64, dtype=torch.float64)
+        if tau % c == 0:
+            S.copy_(rnd(S))
+            snap = S[..., k:].clone()
+        S_every.copy_(rnd(S_every))
+        assert torch.allclose(tf.S, S, rtol=0, atol=1e-12), f"tau={tau}"
+        if nat is not None:
+            nat.step(x, B, C, dt, prm)
+            assert torch.allclose(nat.S, S, rtol=0, atol=1e-12), f"NativeV4 tau={tau}"
+        if tau > 0:
+            assert float((tf.S - S_none).abs().max()) > 1e-7
+        if tau % c != 0:
+            assert float((tf.S - S_every).abs().max()) > 1e-7
+    # the snapshot is the quantization of the rounded cold columns at the last snapshot token
+    if cold == "bf16":
+        assert torch.equal(tf.snap, snap.to(torch.bfloat16).double())
+    else:
+        assert torch.equal(tf.snap, oracle.read_fp8(*oracle.quant_fp8(snap.float())).double())
+
+
+def test_mask_width_is_the_width_dimensional_model():
+    """set_width (scale/nemotron_retrofit.py:29-37, :114-116): mask_width keeps the first w
+    coordinates of an explicit fp64 rotation R B; a fresh trajectory under it keeps state
+    columns >= w at exactly zero and equals the w-dimensional model built from the first w
+    rows of R (S_w <- exp(a) S_w + dt x (R_w B), y = S_w (R_w C) + D x) - not the full
+    model, and not the identity rotation masked."""
+    b, H, P, G, w = 2, 4, 8, 2, 48
+    gen, prm, _ = _small(seed=350, b=b, H=H, P=P, G=G)
+    R = prm.R.double()
+    X = torch.randn(5, G, N, generator=gen, dtype=torch.float64)
+    want = torch.zeros(5, G, N, dtype=torch.float64)
+    for t in range(5):
+        for g in range(G):
+            want[t, g, :w] = R[g, :w] @ X[t, g]
+    assert torch.allclose(oracle.mask_width(oracle.rotate(X, R), w), want, atol=1e-12)
+    S = torch.zeros(b, H, P, N, dtype=torch.float64)
+    S_full = S.clone()
+    Sw = torch.zeros(b, H, P, w, dtype=torch.float64)
+    prm64 = prm.to(torch.float64)
+    Rh = R[:, :w].repeat_interleave(H // G, dim=0)  # [H, w, N]
+    for tau in range(6):
+        x, B, C, dt = oracle.make_step_inputs(b, H, P, N, G, gen)
+        y = oracle.fresh_step(S, x, B, C, dt, prm64, dtype=torch.float64, width=w)
+        y_full = oracle.fresh_step(S_full, x, B, C, dt, prm64, dtype=torch.float64)
+        d = oracle.softplus_dt(dt.double(), prm64.dt_bias)
+        a = d * prm64.A[None, :]
+        Bw = torch.einsum("hmn,bhn->bhm", Rh, B.double().repeat_interleave(H // G, dim=1))
+        Cw = torch.einsum("hmn,bhn->bhm", Rh, C.double().repeat_interleave(H // G, dim=1))
+        Sw = Sw * torch.exp(a)[..., None, None] + (d[..., None] * x.double())[..., None] * Bw[:, :, None, :]
+        y_w = torch.einsum("bhpm,bhm->bhp", Sw, Cw) + x.double() * prm64.D[None, :, None]
+        assert torch.equal(S[..., w:], torch.zeros_like(S[..., w:]))
+        assert torch.allclose(S[..., :w], Sw, atol=1e-12) and torch.allclose(y, y_w, atol=1e-12)
+        assert float((y - y_full).abs().max()) > 1e-4
