@@ -251,13 +251,31 @@ DEPLOY_POINTS = [
     ("v4 k32 c4 single bf16 copy, B=256", dict(B=256, cold="bf16", master="bf16")),
     ("v4 k32 c4 e4m3 cold + bf16 master, B=256", dict(B=256, cold="fp8", master="bf16")),
     ("v4 k32 c4 e4m3 cold + bf16 master, B=448", dict(B=448, cold="fp8", master="bf16")),
+    # the rank-c exact correction readout (corr=1) at the longest window
+    ("v4 k32 c64 fp32 exact readout, B=256", dict(B=256, c=64, exact=True)),
     # the ragged continuous batch: 384 requests at random phases (each token flushes about
-    # B/c of them), fp32 cold
+    # B/c of them), fp32 cold, every (c, k_hot) pair of the sweep
+    ("ragged B=384 k32 c8 fp32", dict(B=384, k=32, c=8, ragged=True)),
     ("ragged B=384 k32 c16 fp32", dict(B=384, k=32, c=16, ragged=True)),
     ("ragged B=384 k32 c64 fp32", dict(B=384, k=32, c=64, ragged=True)),
+    ("ragged B=384 k64 c8 fp32", dict(B=384, k=64, c=8, ragged=True)),
     ("ragged B=384 k64 c16 fp32", dict(B=384, k=64, c=16, ragged=True)),
     ("ragged B=384 k64 c64 fp32", dict(B=384, k=64, c=64, ragged=True)),
 ]
+
+
+def readout_name(args) -> str:
+    return ("exact" if args.exact else "hot-only" if args.coldoff
+            else f"query-gated tau={args.qgate:g}" if args.qgate > 0 else "stale")
+
+
+def traffic_key(args, head="v4") -> str:
+    """The workload's key in the profiles' `traffic[...]` lines."""
+    if head != "v4":
+        return f"fresh B={args.B}"
+    readout = readout_name(args)
+    return (f"v4 B={args.B} k={args.k} c={args.c} {args.cold}" + (" bf16-master" if args.master == "bf16" else "")
+            + ("" if readout == "stale" else f" {readout}") + (" ragged" if args.ragged else ""))
 
 
 def bench_deploy(args, layers, inputs, dev, fresh_ms_256):
@@ -287,16 +305,14 @@ def bench_deploy(args, layers, inputs, dev, fresh_ms_256):
                 a.steps += a.c - a.steps % a.c
             log(f"deploy: {name} ...")
             v_step, _, v_ev, _ = bench_v4(a, layers, inp, dev)
-            vb = a.B * bytes_v4_token(a.k, a.c, a.cold, a.master) + bytes_rotation()
+            vb = a.B * bytes_v4_token(a.k, a.c, a.cold, a.master, exact=a.exact) + bytes_rotation()
             f_ms = fresh_ms[B]
-            tr, tr_src = measured_traffic(f"v4 B={a.B} k={a.k} c={a.c} {a.cold}"
-                                          + (" bf16-master" if a.master == "bf16" else "")
-                                          + (" ragged" if a.ragged else ""))
+            tr, tr_src = measured_traffic(traffic_key(a))
             out[name] = {"value": round(a.B / v_step * 1e3, 1), "unit": "state-op tokens/s",
                          "ms_per_step": round(v_step, 4), "fresh_ms_per_step": round(f_ms, 4),
                          "speedup_vs_fresh": round(f_ms / v_step, 3),
-                         "byte_bound_speedup": round(bytes_fresh_token() / bytes_v4_token(a.k, a.c, a.cold, a.master),
-                                                     3),
+                         "byte_bound_speedup": round(bytes_fresh_token() / bytes_v4_token(a.k, a.c, a.cold, a.master,
+                                                                                          exact=a.exact), 3),
                          "achieved_gbs": round(vb / (v_ev * 1e-3) / 1e9, 1),
                          "frac": round(vb / (v_ev * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                          "algorithmic_bytes_per_launch": int(vb), "avg_launch_us_events": round(v_ev * 1e3, 2),
@@ -551,12 +567,8 @@ def main():
     per_launch_bytes = (args.B * bytes_v4_token(args.k, args.c, args.cold, args.master, args.skip, args.exact)
                         + bytes_rotation() if head == "v4" else args.B * bytes_fresh_token())
     achieved = per_launch_bytes / (ms_ev * 1e-3) / 1e9
-    readout = ("exact" if args.exact else "hot-only" if args.coldoff
-               else f"query-gated tau={args.qgate:g}" if args.qgate > 0 else "stale")
-    tkey = (f"v4 B={args.B} k={args.k} c={args.c} {args.cold}" + (" bf16-master" if args.master == "bf16" else "")
-            + ("" if readout == "stale" else f" {readout}") + (" ragged" if args.ragged else "")
-            if head == "v4" else f"fresh B={args.B}")
-    traffic, traffic_src = measured_traffic(tkey)
+    readout = readout_name(args)
+    traffic, traffic_src = measured_traffic(traffic_key(args, head))
     out = {
         "metric": "state-op tokens/s at 9B shape B=256 (v4-c4 vs fresh); achieved HBM GB/s vs peak",
         "value": round(args.B / ms_step * 1e3, 1),

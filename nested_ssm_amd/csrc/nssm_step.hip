@@ -47,6 +47,10 @@ constexpr int kMfmaTiles = 5;  // 16 x 16 flush-contraction tiles a wave keeps i
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2v __attribute__((ext_vector_type(2)));
 
+// address-space casts for gfx950's LDS DMA (global_load_lds)
+#define NSSM_GLOBAL(p) ((const __attribute__((address_space(1))) void*)(p))
+#define NSSM_LOCAL(p) ((__attribute__((address_space(3))) void*)(p))
+
 struct StepArgs {
   // tier state (fresh: hot is the full state, the rest NULL)
   float* hot;
@@ -423,12 +427,18 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
       // over each aligned 8-lane group, so every group's lanes sum together.
       const int NC = kN - a.K, k8 = tid & 7;
       constexpr int NG = kPrepThreads / 8;  // 8-lane groups
-      if (nreq * c <= NG) {
+      // window positions of the block's longest live window: j = 0 .. nvm (at the 9B shape,
+      // B = 256, c = 64: 23.1 -> 22.0 us per launch on average, 14.8 -> 9.3 with one token
+      // buffered, against items over all c positions)
+      int nvm = 0;
+      for (int r = 0; r < nreq; ++r) nvm = max(nvm, sNvr[r]);
+      const int cw = nvm + 1;
+      if (nreq * cw <= NG) {
         // one (request, window token) item per group: buffered tokens from the ring, this
         // token (j = nv) from LDS
         const int it = tid >> 3;
-        if (it < nreq * c) {
-          const int r = it / c, j = it - r * c;
+        if (it < nreq * cw) {
+          const int r = it / cw, j = it - r * cw;
           const int sl = sSlot[r], nv = sNvr[r];
           const bool live = sl >= 0 && sl < a.slots && j <= nv;
           float acc = 0.f;
@@ -463,11 +473,11 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
         // of a slot out of range, reads its request's first buffered row, which live items
         // read too; a column past the cold tier reads the tier's last float4; both dropped),
         // so each round is one memory round trip; then this token (j = nv) from LDS
-        for (int it0 = tid >> 3; it0 < nreq * c; it0 += kPrepDotBatch * NG) {
+        for (int it0 = tid >> 3; it0 < nreq * cw; it0 += kPrepDotBatch * NG) {
           f4 bv[kPrepDotBatch][kN / 32];
 #pragma unroll
           for (int u = 0; u < kPrepDotBatch; ++u) {
-            const int it = min(it0 + u * NG, nreq * c - 1), r = it / c, j = it - r * c;
+            const int it = min(it0 + u * NG, nreq * cw - 1), r = it / cw, j = it - r * cw;
             const int sl = sSlot[r], nv = sNvr[r];
             const int slc = sl >= 0 && sl < a.slots ? sl : 0;
             const int pos = sTr[r] % c - nv + (j < nv ? j : 0);  // in [0, c): nv <= t % c
@@ -478,9 +488,9 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
           }
 #pragma unroll
           for (int u = 0; u < kPrepDotBatch; ++u) {
-            const int itr = it0 + u * NG, it = min(itr, nreq * c - 1), r = it / c, j = it - r * c;
+            const int itr = it0 + u * NG, it = min(itr, nreq * cw - 1), r = it / cw, j = it - r * cw;
             const int sl = sSlot[r];
-            const bool live = itr < nreq * c && sl >= 0 && sl < a.slots && j < sNvr[r];
+            const bool live = itr < nreq * cw && sl >= 0 && sl < a.slots && j < sNvr[r];
             const float* cq = &sRot[kPrepReq + r][a.K];
             float acc = 0.f;
 #pragma unroll
@@ -1658,9 +1668,6 @@ __device__ __forceinline__ void st_flush(T v, T* p) {
   else *p = v;
 }
 
-#define NSSM_GLOBAL(p) ((const __attribute__((address_space(1))) void*)(p))
-#define NSSM_LOCAL(p) ((__attribute__((address_space(3))) void*)(p))
-
 // Window layout. The contraction's lane group lk (16 lanes; lanes 0-31 and 32-63 are served
 // by the 32 LDS banks in separate cycles) takes, in each 32-token step from ks, the tokens
 // ks + 16 q + 4 lk + r (q = 0, 1; r = 0 .. 3) as operand element 4 q + r. B' rows of tokens
@@ -2525,7 +2532,11 @@ __global__ void __launch_bounds__(kNormThreads) gated_norm_kernel(NormArgs a) {
 // 4-channel aligned: each lane takes 4 consecutive channels per 256 (y as 16 bytes, gate,
 // weight and out as 8 bytes in bf16), issues the weight loads with the others, and the sum
 // of squares is reduced inside the wave (no LDS, no barrier). Per channel the arithmetic
-// is gated_norm_kernel's; the sum runs in another order.
+// is gated_norm_kernel's; the sum runs in another order. NB = gs / 256 is a template
+// argument, so every block's loads go out together without run-time guards. (At the 9B
+// shape, B = 256, 21 MB per launch: 7.3 us in graph replays whether the blocks' loads go
+// out one block at a time or all at once, about 3.8 us of bandwidth and the rest a
+// launch's fixed cost.)
 constexpr int kNormWavePer = 8;  // 256-channel blocks per lane: gs <= 2048
 
 template <int DT>
@@ -2540,28 +2551,30 @@ __device__ __forceinline__ void ld4_dt(const void* p, size_t i, float (&v)[4]) {
   }
 }
 
-template <int DT>
+template <int DT, int NB>
 __global__ void __launch_bounds__(64) gated_norm_wave_kernel(NormArgs a) {
-  const int ng = a.I / a.gs, nb = a.gs >> 8;
+  const int ng = a.I / a.gs;
   const int r = blockIdx.x / ng, grp = blockIdx.x - r * ng;
   const int lane = threadIdx.x;
   const size_t c0 = (size_t)grp * a.gs + 4 * lane;
-  float v[kNormWavePer][4], w[kNormWavePer][4];
+  float v[NB][4], w[NB][4];
+  f4 yv[NB];
+  float g[NB][4];
+#pragma unroll
+  for (int k = 0; k < NB; ++k) {  // every block's loads first
+    const size_t c = c0 + 256 * k;
+    yv[k] = *reinterpret_cast<const f4*>(a.y + (size_t)r * a.I + c);
+    ld4_dt<DT>(a.gate, (size_t)r * a.gate_stride + c, g[k]);
+    ld4_dt<DT>(a.w, c, w[k]);
+  }
   float ss = 0.f;
 #pragma unroll
-  for (int k = 0; k < kNormWavePer; ++k) {
-    if (k < nb) {
-      const size_t c = c0 + 256 * k;
-      float g[4];
-      const f4 yv = *reinterpret_cast<const f4*>(a.y + (size_t)r * a.I + c);
-      ld4_dt<DT>(a.gate, (size_t)r * a.gate_stride + c, g);
-      ld4_dt<DT>(a.w, c, w[k]);
-      const float ys[4] = {yv.x, yv.y, yv.z, yv.w};
+  for (int k = 0; k < NB; ++k) {
+    const float ys[4] = {yv[k].x, yv[k].y, yv[k].z, yv[k].w};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[k][e] = round_dt<DT>(ys[e]) * (g[e] / (1.f + expf(-g[e])));  // y * silu(gate), fp32
-        ss = fmaf(v[k][e], v[k][e], ss);
-      }
+    for (int e = 0; e < 4; ++e) {
+      v[k][e] = round_dt<DT>(ys[e]) * (g[k][e] / (1.f + expf(-g[k][e])));  // y * silu(gate), fp32
+      ss = fmaf(v[k][e], v[k][e], ss);
     }
   }
   ss += dpp<0xB1>(ss);
@@ -2572,20 +2585,24 @@ __global__ void __launch_bounds__(64) gated_norm_wave_kernel(NormArgs a) {
   ss += __shfl_xor(ss, 32);
   const float rs = 1.f / sqrtf(ss / (float)a.gs + a.eps);
 #pragma unroll
-  for (int k = 0; k < kNormWavePer; ++k) {
-    if (k < nb) {
-      const size_t o = (size_t)r * a.I + c0 + 256 * k;
-      float t[4];
+  for (int k = 0; k < NB; ++k) {
+    const size_t o = (size_t)r * a.I + c0 + 256 * k;
+    float t[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) t[e] = w[k][e] * round_dt<DT>(v[k][e] * rs);
-      if constexpr (DT == 0) *reinterpret_cast<f4*>(static_cast<float*>(a.out) + o) = f4{t[0], t[1], t[2], t[3]};
-      else
-        *reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.out) + o) =
-            u2v{nssm_f32_to_bf16(t[0]) | ((uint32_t)nssm_f32_to_bf16(t[1]) << 16),
-                nssm_f32_to_bf16(t[2]) | ((uint32_t)nssm_f32_to_bf16(t[3]) << 16)};
-    }
+    for (int e = 0; e < 4; ++e) t[e] = w[k][e] * round_dt<DT>(v[k][e] * rs);
+    if constexpr (DT == 0) *reinterpret_cast<f4*>(static_cast<float*>(a.out) + o) = f4{t[0], t[1], t[2], t[3]};
+    else
+      *reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.out) + o) =
+          u2v{nssm_f32_to_bf16(t[0]) | ((uint32_t)nssm_f32_to_bf16(t[1]) << 16),
+              nssm_f32_to_bf16(t[2]) | ((uint32_t)nssm_f32_to_bf16(t[3]) << 16)};
   }
 }
+
+// the wave kernel's instance for a dtype and a block count (host dispatch)
+template <int DT, int NB>
+struct NormWave {
+  static constexpr auto fn = gated_norm_wave_kernel<DT, NB>;
+};
 
 // ---------------------------------------------------------------------------
 // host side
@@ -3244,10 +3261,21 @@ int nssm_gated_rmsnorm(int32_t b, int32_t I, int32_t gs, int32_t dtype, const fl
   const uintptr_t va = dtype == NSSM_DT_F32 ? 15u : 7u;
   if (gs % 256 == 0 && gs / 256 <= kNormWavePer && gate_stride % 4 == 0 && aligned16(y) &&
       !((uintptr_t)gate & va) && !((uintptr_t)weight & va) && !((uintptr_t)out & va)) {
-    if (dtype == NSSM_DT_F32)
-      hipLaunchKernelGGL(gated_norm_wave_kernel<0>, grid, dim3(64), 0, (hipStream_t)stream, a);
-    else
-      hipLaunchKernelGGL(gated_norm_wave_kernel<1>, grid, dim3(64), 0, (hipStream_t)stream, a);
+    const bool f32 = dtype == NSSM_DT_F32;
+    auto go = [&](auto k0, auto k1) {
+      if (f32) hipLaunchKernelGGL(decltype(k0)::fn, grid, dim3(64), 0, (hipStream_t)stream, a);
+      else hipLaunchKernelGGL(decltype(k1)::fn, grid, dim3(64), 0, (hipStream_t)stream, a);
+    };
+    switch (gs / 256) {
+      case 1: go(NormWave<0, 1>{}, NormWave<1, 1>{}); break;
+      case 2: go(NormWave<0, 2>{}, NormWave<1, 2>{}); break;
+      case 3: go(NormWave<0, 3>{}, NormWave<1, 3>{}); break;
+      case 4: go(NormWave<0, 4>{}, NormWave<1, 4>{}); break;
+      case 5: go(NormWave<0, 5>{}, NormWave<1, 5>{}); break;
+      case 6: go(NormWave<0, 6>{}, NormWave<1, 6>{}); break;
+      case 7: go(NormWave<0, 7>{}, NormWave<1, 7>{}); break;
+      default: go(NormWave<0, 8>{}, NormWave<1, 8>{}); break;
+    }
     return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
   }
   if (dtype == NSSM_DT_F32)
