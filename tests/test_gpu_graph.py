@@ -111,3 +111,47 @@ def test_fresh_step_graph_replays_match_eager():
             torch.cuda.synchronize()
             assert torch.equal(ys[l], ye), f"y layer {l} replay {step}"
             assert torch.equal(Sg[l], Se[l])
+
+
+@pytest.mark.parametrize("c,cold,master", [(4, "fp32", "fp32"), (64, "fp32", "fp32"), (64, "fp8", "bf16")])
+def test_noalloc_step_first_called_inside_a_capture(c, cold, master):
+    """nssm_v4_step_noalloc serves code under graph capture: its per-device set-up (the
+    scratch array's device address, looked up with hipGetSymbolAddress, and at c = 64 the
+    flush kernel's LDS limit) runs on its first call, which here happens inside the capture
+    (no earlier no-allocation call in this process: this file is collected before the
+    no-allocation tests). The replays, with eager work and host synchronisations between
+    them, give y and tiers bit-identical to eager nssm_v4_step twins; a window the stream
+    kernel replays (c = 4) and one the flush kernel replays (c = 64)."""
+    b, nl, k = 6, 2, 32
+    layers = _layers(nl, seed=30 + c)
+    g = torch.Generator(device="cuda").manual_seed(3)
+    S0 = [torch.randn(b, H, P, N, device="cuda", generator=g).mul_(0.1) for _ in range(nl)]
+    phase = torch.randint(0, c, (b,), device="cuda", generator=g, dtype=torch.int32)
+    tg = [V4Tier(b, H, P, G, k_hot=k, c=c, cold=cold, master=master) for _ in range(nl)]
+    te = [V4Tier(b, H, P, G, k_hot=k, c=c, cold=cold, master=master) for _ in range(nl)]
+    for l in range(nl):
+        tg[l].join(layers[l], S0[l], phase=phase)
+        te[l].join(layers[l], S0[l], phase=phase)
+    static = _inputs(b, nl, g)
+    ys = [torch.empty(b, H, P, device="cuda") for _ in range(nl)]
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        for l in range(nl):
+            tg[l].step(layers[l], *static[l], y=ys[l], noalloc=True)
+    torch.cuda.synchronize()
+    for step in range(c + 3 if c <= 16 else 5):
+        fresh = _inputs(b, nl, g)
+        for dst, src in zip(static, fresh):
+            for d, s_ in zip(dst, src):
+                d.copy_(s_)
+        graph.replay()
+        ye = [te[l].step(layers[l], *fresh[l]) for l in range(nl)]  # eager work between the replays
+        torch.cuda.synchronize()
+        for l in range(nl):
+            assert torch.equal(ys[l], ye[l]), f"y layer {l} replay {step}"
+            for f in ("hot", "cold_t", "master", "scale", "t", "nv", "glog"):
+                a_, e_ = getattr(tg[l], f), getattr(te[l], f)
+                if a_ is not None:
+                    assert torch.equal(a_.view(torch.uint8), e_.view(torch.uint8)), f"{f} layer {l} replay {step}"
