@@ -155,7 +155,8 @@ int nssm_tier_sizes(int32_t slots, int32_t H, int32_t P, int32_t N, int32_t G,
 
 /* Bytes of device workspace a step needs for b requests (c = 0 for the
  * untiered step), or a negative NSSM_E* code. The workspace holds the rotated
- * B and C, per-head decay scalars and flush weights of one call; it is
+ * B and C, per-head decay scalars, flush weights and the exact readout's window
+ * dots of one call; it is
  * caller-owned, 16-byte aligned, and must not be shared by steps that run
  * concurrently on different streams. */
 int64_t nssm_step_workspace_bytes(int32_t b, int32_t H, int32_t G, int32_t N, int32_t c);
@@ -187,8 +188,8 @@ int nssm_v4_step(const nssm_layer_params* prm, const nssm_tier* tier,
  * held until the process ends (its address is looked up once per device, on the first
  * call made with that device current). The call allocates nothing and returns
  * NSSM_E_SCRATCH when nssm_step_workspace_bytes(b, H, G, 128, c) exceeds
- * NSSM_SCRATCH_BYTES (at H = 128, G = 8: up to 1817 requests at c = 4, 711 at c = 32,
- * 419 at c = 64). Nothing in the scratch needs to start at zero (every word a later
+ * NSSM_SCRATCH_BYTES (at H = 128, G = 8: up to 2028 requests at c = 4, 1055 at c = 32,
+ * 682 at c = 64). Nothing in the scratch needs to start at zero (every word a later
  * kernel reads is written earlier in the same call). Every call on one GPU shares that
  * GPU's array: calls that overlap in time on one GPU (different streams, or host threads
  * enqueueing concurrently on one device) race on it; calls ordered on one stream do not. */

@@ -95,17 +95,18 @@ struct StepArgs {
 // Workspace carve-up for b requests (floats): rotated B and C [b][G][N] each,
 // per-head scalars [b][H][HD_STRIDE]; tiered steps (c > 0) add the per-(request,
 // group) flush flags [b][G] (int32, padded to a multiple of 4), window weights
-// [b][H][c] (flush) and correction coefficients [b][H][c] (exact readout).
+// [b][H][c] (a flush whose weights prep forms) and the exact readout's window dots
+// s_j = C'_cold . B'_j [b][G][c].
 // HD_SNAPF is the factor of the snapshot readout: exp(glog) (stale, the decay up
 // to the previous token), exp(glog + a) (exact, and teacher-forced between flushes:
 // inclusive of this token), 1 (teacher-forced at a flush: the readout of the new state)
 // or 0 (a head whose cold term the gated readout drops; HD_SKIP = 1 then).
-enum { HD_DT = 0, HD_A, HD_DECAY, HD_SNAPF, HD_D, HD_FLUSH, HD_DTOT, HD_M, HD_POS, HD_SKIP, HD_STRIDE = 12 };
+enum { HD_DT = 0, HD_A, HD_DECAY, HD_SNAPF, HD_D, HD_FLUSH, HD_DTOT, HD_M, HD_POS, HD_SKIP, HD_AH, HD_STRIDE = 12 };
 __host__ __device__ constexpr size_t flag_words(int b, int G, int c) {
   return c > 0 ? (((size_t)b * G + 3) & ~(size_t)3) : 0;
 }
 struct Ws {
-  float *B, *C, *hd, *w, *cw;
+  float *B, *C, *hd, *w, *s;
   int* fg;
   __host__ __device__ Ws(float* base, int b, int H, int G, int c) {
     B = base;
@@ -113,11 +114,11 @@ struct Ws {
     hd = C + (size_t)b * G * kN;
     fg = reinterpret_cast<int*>(hd + (size_t)b * H * HD_STRIDE);
     w = hd + (size_t)b * H * HD_STRIDE + flag_words(b, G, c);
-    cw = w + (size_t)b * H * c;
+    s = w + (size_t)b * H * c;
   }
 };
 size_t ws_floats(int b, int H, int G, int c) {
-  return (size_t)b * (2 * G * kN + H * HD_STRIDE + 2 * H * c) + flag_words(b, G, c);
+  return (size_t)b * (2 * G * kN + H * HD_STRIDE + H * c + G * c) + flag_words(b, G, c);
 }
 
 __device__ __forceinline__ float bf2f(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
@@ -227,7 +228,7 @@ constexpr int kPrepStage = kPrepReq * kN / kPrepThreads;  // B (and C) elements 
 constexpr int kPrepDotBatch = 4;  // exact readout: window dots a prep lane group loads at once
 
 // A head's dt (softplus, with the dt_min floor of the native path) and the scalars every
-// stream kernel reads: dt, a = dt A, exp(a), D. Returns dt.
+// stream kernel reads: dt, a = dt A, exp(a), D, A. Returns dt.
 __device__ __forceinline__ float head_scalars(float* __restrict__ hd, float draw, float dtb, float Ah, float Dh,
                                               float dt_min) {
   float dt = softplus_f(draw + dtb);
@@ -237,6 +238,7 @@ __device__ __forceinline__ float head_scalars(float* __restrict__ hd, float draw
   hd[HD_A] = av;
   hd[HD_DECAY] = expf(av);
   hd[HD_D] = Dh;
+  hd[HD_AH] = Ah;
   return dt;
 }
 
@@ -244,10 +246,9 @@ template <bool TIERED>
 __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
   __shared__ float sX[2 * kPrepReq][kN];  // B (j < kPrepReq) and C (j >= kPrepReq) of the block's requests
   __shared__ int sSlot[kPrepReq], sTr[kPrepReq], sNvr[kPrepReq], sFl[kPrepReq];
-  // exact readout and query gate: B', C' of the block; s_j = C'_cold . B'_j over each
-  // window; each request's cold energy fraction; gated / kept head counts
+  // exact readout and query gate: B', C' of the block; each request's cold energy
+  // fraction; gated / kept head counts
   __shared__ float sRot[TIERED ? 2 * kPrepReq : 1][TIERED ? kN : 1];
-  __shared__ float sS[TIERED ? kPrepReq : 1][TIERED ? kMaxC : 1];
   __shared__ float sRho[kPrepReq];
   __shared__ int sQc[2];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -418,7 +419,11 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
   }
 
   // 2b. exact readout: s_j = C'_cold . B'_j for each request's window, j = 0 .. nv
-  // (buffered tokens at ring positions t % c - nv + j, then this token)
+  // (buffered tokens at ring positions t % c - nv + j, then this token), written to the
+  // workspace per (request, group); the stream kernel forms the weights w_j and sums
+  // w_j s_j x_j itself. (Splitting the buffered positions over four workgroups per (group,
+  // request block), each repeating the rotation, measured slower: 15.0 -> 18.7 us per
+  // launch at the 9B shape, B = 256, c = 64.)
   if constexpr (TIERED) {
     if (a.exact) {
       __syncthreads();  // sRot
@@ -426,25 +431,25 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
       // (float4 each), then a DPP sum over the group's 8 lanes. The loop bounds are uniform
       // over each aligned 8-lane group, so every group's lanes sum together.
       const int NC = kN - a.K, k8 = tid & 7;
+      float* __restrict__ sw = ws.s + ((size_t)r0 * G + g) * c;  // request r: sw + r G c
       constexpr int NG = kPrepThreads / 8;  // 8-lane groups
-      // window positions of the block's longest live window: j = 0 .. nvm (at the 9B shape,
-      // B = 256, c = 64: 23.1 -> 22.0 us per launch on average, 14.8 -> 9.3 with one token
-      // buffered, against items over all c positions)
-      int nvm = 0;
-      for (int r = 0; r < nreq; ++r) nvm = max(nvm, sNvr[r]);
-      const int cw = nvm + 1;
-      if (nreq * cw <= NG) {
-        // one (request, window token) item per group: buffered tokens from the ring, this
-        // token (j = nv) from LDS
+      // buffered positions of the block's longest live window, j = 0 .. nb - 1 (at the 9B
+      // shape, B = 256, c = 64: 23.1 -> 22.0 us per launch on average, 14.8 -> 9.3 with one
+      // token buffered, against items over all c positions)
+      int nb = 0;
+      for (int r = 0; r < nreq; ++r) nb = max(nb, sNvr[r]);
+      const int ni = nreq * nb, nc = nreq;  // buffered items, this token's items
+      if (ni + nc <= NG) {
+        // one item per group: buffered tokens from the ring, then this token from LDS
         const int it = tid >> 3;
-        if (it < nreq * cw) {
-          const int r = it / cw, j = it - r * cw;
-          const int sl = sSlot[r], nv = sNvr[r];
-          const bool live = sl >= 0 && sl < a.slots && j <= nv;
+        if (it < ni + nc) {
+          const bool cur = it >= ni;
+          const int r = cur ? it - ni : it / nb, j = cur ? sNvr[r] : it - r * nb;
+          const int sl2 = sSlot[r], nv = sNvr[r];
+          const bool live = sl2 >= 0 && sl2 < a.slots && (cur || j < nv);
           float acc = 0.f;
           if (live) {
-            const float* bj = j < nv ? a.ring_b + (((size_t)sl * G + g) * c + (sTr[r] % c - nv + j)) * NC
-                                     : &sRot[r][a.K];
+            const float* bj = cur ? &sRot[r][a.K] : a.ring_b + (((size_t)sl2 * G + g) * c + (sTr[r] % c - nv + j)) * NC;
             const float* cq = &sRot[kPrepReq + r][a.K];
             f4 bv[kN / 32], cv[kN / 32];
 #pragma unroll
@@ -465,21 +470,21 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
             }
           }
           acc = sum8(acc);
-          if (live && k8 == 0) sS[r][j] = acc;
+          if (live && k8 == 0) sw[(size_t)r * G * c + j] = acc;
         }
       } else {
-        // more items than groups: buffered tokens (j < nv) from the ring, kPrepDotBatch items
-        // per group and round with every load unpredicated (an item that is not buffered, or
-        // of a slot out of range, reads its request's first buffered row, which live items
-        // read too; a column past the cold tier reads the tier's last float4; both dropped),
-        // so each round is one memory round trip; then this token (j = nv) from LDS
-        for (int it0 = tid >> 3; it0 < nreq * cw; it0 += kPrepDotBatch * NG) {
+        // more items than groups: buffered tokens from the ring, kPrepDotBatch items per
+        // group and round with every load unpredicated (an item that is not buffered, or of
+        // a slot out of range, reads its request's first buffered row, which live items read
+        // too; a column past the cold tier reads the tier's last float4; both dropped), so
+        // each round is one memory round trip; then this token from LDS
+        for (int it0 = tid >> 3; it0 < ni; it0 += kPrepDotBatch * NG) {
           f4 bv[kPrepDotBatch][kN / 32];
 #pragma unroll
           for (int u = 0; u < kPrepDotBatch; ++u) {
-            const int it = min(it0 + u * NG, nreq * cw - 1), r = it / cw, j = it - r * cw;
-            const int sl = sSlot[r], nv = sNvr[r];
-            const int slc = sl >= 0 && sl < a.slots ? sl : 0;
+            const int it = min(it0 + u * NG, ni - 1), r = it / nb, j = it - r * nb;
+            const int sl2 = sSlot[r], nv = sNvr[r];
+            const int slc = sl2 >= 0 && sl2 < a.slots ? sl2 : 0;
             const int pos = sTr[r] % c - nv + (j < nv ? j : 0);  // in [0, c): nv <= t % c
             const float* bj = a.ring_b + (((size_t)slc * G + g) * c + pos) * NC;
 #pragma unroll
@@ -488,9 +493,9 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
           }
 #pragma unroll
           for (int u = 0; u < kPrepDotBatch; ++u) {
-            const int itr = it0 + u * NG, it = min(itr, nreq * cw - 1), r = it / cw, j = it - r * cw;
-            const int sl = sSlot[r];
-            const bool live = itr < nreq * cw && sl >= 0 && sl < a.slots && j < sNvr[r];
+            const int itr = it0 + u * NG, it = min(itr, ni - 1), r = it / nb, j = it - r * nb;
+            const int sl2 = sSlot[r];
+            const bool live = itr < ni && sl2 >= 0 && sl2 < a.slots && j < sNvr[r];
             const float* cq = &sRot[kPrepReq + r][a.K];
             float acc = 0.f;
 #pragma unroll
@@ -504,11 +509,11 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
               }
             }
             acc = sum8(acc);
-            if (live && k8 == 0) sS[r][j] = acc;
+            if (live && k8 == 0) sw[(size_t)r * G * c + j] = acc;
           }
         }
-        for (int r = tid >> 3; r < nreq; r += NG) {
-          const int sl = sSlot[r];
+        for (int r = tid >> 3; r < nc; r += NG) {
+          const int sl2 = sSlot[r];
           const float* bq = &sRot[r][a.K];
           const float* cq = &sRot[kPrepReq + r][a.K];
           float acc = 0.f;
@@ -524,10 +529,9 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
             }
           }
           acc = sum8(acc);
-          if (sl >= 0 && sl < a.slots && k8 == 0) sS[r][sNvr[r]] = acc;
+          if (sl2 >= 0 && sl2 < a.slots && k8 == 0) sw[(size_t)r * G * c + sNvr[r]] = acc;
         }
       }
-      __syncthreads();  // sS
     }
   }
 
@@ -583,21 +587,14 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
       hd[HD_FLUSH] = flush ? 1.f : 0.f;
       hd[HD_POS] = (float)pos;
       if (flush) sFl[hr] = 1;
-      if (flush && !exact && a.fw) {
-        // the flush kernel forms the window weights from the ring's dt
-        hd[HD_DTOT] = 1.f;
-        hd[HD_M] = (float)(nvv + 1);
-      } else if (flush || exact) {
+      if (flush && !a.fw) {
         // window = the nv buffered tokens at ring [pos-nv, pos) and this one (at a
-        // flush pos = c-1): w_i = exp(sum_{l>i} a_l) dt_i, total decay exp(sum_l a_l);
-        // the exact readout's coefficients are w_i s_i. The buffered dt are loaded
-        // 16 at a time.
+        // flush pos = c-1): w_i = exp(sum_{l>i} a_l) dt_i, total decay exp(sum_l a_l).
+        // The buffered dt are loaded 16 at a time.
         const int mw = nvv + 1;
         const float* __restrict__ rdt = a.ring_dt + o * c + (pos - nvv);
         float* __restrict__ w = ws.w + ((size_t)bi * H + h) * c;
-        float* __restrict__ cw = ws.cw + ((size_t)bi * H + h) * c;
-        if (flush) w[mw - 1] = dt;
-        if (exact) cw[mw - 1] = dt * sS[hr][mw - 1];
+        w[mw - 1] = dt;
         float suf = dt * Ah;
         for (int i0 = mw - 2; i0 >= 0; i0 -= 16) {
           float v[16];
@@ -606,9 +603,7 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
 #pragma unroll
           for (int u = 0; u < 16; ++u) {
             if (i0 - u >= 0) {
-              const float wi = expf(suf) * v[u];
-              if (flush) w[i0 - u] = wi;
-              if (exact) cw[i0 - u] = wi * sS[hr][i0 - u];
+              w[i0 - u] = expf(suf) * v[u];
               suf += v[u] * Ah;
             }
           }
@@ -616,8 +611,10 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
         hd[HD_DTOT] = expf(suf);
         hd[HD_M] = (float)mw;
       } else {
+        // the flush kernel forms a flushing window's weights from the ring's dt, the exact
+        // readout's stream kernel its correction weights; both read the window length
         hd[HD_DTOT] = 1.f;
-        hd[HD_M] = 0.f;
+        hd[HD_M] = flush || exact ? (float)(nvv + 1) : 0.f;
       }
       if (flush) {
         a.nv[o] = 0;
@@ -977,36 +974,52 @@ __device__ __forceinline__ float hot_update(const StepArgs& a, size_t row, int q
 
 // The exact readout's correction for row p of head (slot sh, request rh):
 // sum_j cw_j x_j[p] over the window j = 0 .. m-1, the buffered tokens at ring positions
-// pos - (m-1) + j and, last, this token (x = xcur); cw_j = w_j (C'_cold . B'_j) from the
-// prep kernel, scale/v4_native_decode.py:98-104. The window is at most 64 tokens, one per
-// lane: lane j loads the 16 bytes of buffered x token j holds for the wave's 8 rows
-// (p & ~7 ..) and its weight, and three exchange steps over lane bits 5, 4, 3 leave each
-// lane its own row's share of 8 of the 64 products (lane l's row is l >> 3); the row's 8
-// lanes are summed with the rest of the readout, lane q = 0 adding this token's term.
-// (Eight 2-byte loads per lane, token q + 8u for row p, ran the 9B-shape readout at c = 64
-// 10.6 ms against 7.9 for the stale one.) The loads and the sum are separate so a kernel
-// with registers to spare issues the loads with its state loads.
+// pos - (m-1) + j and, last, this token (x = xcur); cw_j = w_j s_j with the window weight
+// w_j = exp(sum_{l>j} a_l) dt_j (a_l = dt_l A) and s_j = C'_cold . B'_j from the prep kernel,
+// scale/v4_native_decode.py:89-104. The window is at most 64 tokens, one per lane: lane j
+// loads the 16 bytes of buffered x token j holds for the wave's 8 rows (p & ~7 ..), its dt
+// (the ring's, this token's from the head scalars) and s_j; a suffix sum over the lanes
+// gives the weights, and three exchange steps over lane bits 5, 4, 3 leave each lane its
+// own row's share of 8 of the 64 products (lane l's row is l >> 3); the row's 8 lanes are
+// summed with the rest of the readout, lane q = 0 adding this token's term. (Eight 2-byte
+// loads per lane, token q + 8u for row p, ran the 9B-shape readout at c = 64 10.6 ms
+// against 7.9 for the stale one.) The loads and the sum are separate so a kernel with
+// registers to spare issues the loads with its state loads.
 struct CorrRaw {
   uint4 xv;  // buffered x of window token `lane` for the wave's 8 rows (zero past m - 2)
-  float w;   // cw of window token `lane` (zero past m - 1)
+  float dt;  // dt of window token `lane` (zero past m - 1)
+  float s;   // s of window token `lane` (zero past m - 1)
 };
 __device__ __forceinline__ void corr_load(const StepArgs& a, const float* __restrict__ hd, size_t sh, size_t rh,
                                           int p, int q, CorrRaw& cr) {
   const int m = (int)hd[HD_M], P = a.P, c = a.c, lane = ((p & 7) << 3) | q;
+  const int H = a.H, h = (int)(rh % H);
   // window token j sits at ring position pos - (m - 1) + j
-  const uint16_t* rx = a.ring_x + (sh * c + ((int)hd[HD_POS] - (m - 1) + lane)) * P + (p & ~7);
-  const float* cw = Ws(a.ws, a.b, a.H, a.G, c).cw + rh * c;
-  cr.w = lane < m ? cw[lane] : 0.f;
+  const int j0 = (int)hd[HD_POS] - (m - 1);
+  const uint16_t* rx = a.ring_x + (sh * c + (j0 + lane)) * P + (p & ~7);
+  const float* sw = Ws(a.ws, a.b, H, a.G, c).s + ((rh / H) * a.G + h / a.HG) * c;
+  cr.s = lane < m ? sw[lane] : 0.f;
+  cr.dt = lane < m - 1 ? a.ring_dt[sh * c + (j0 + lane)] : lane == m - 1 ? hd[HD_DT] : 0.f;
   cr.xv = lane < m - 1 ? *reinterpret_cast<const uint4*>(rx) : make_uint4(0u, 0u, 0u, 0u);
 }
 __device__ __forceinline__ float corr_sum(const float* __restrict__ hd, int p, int q, const CorrRaw& cr, float xcur) {
   const int m = (int)hd[HD_M], lane = ((p & 7) << 3) | q;
+  // w_j = exp(sum_{l>j} a_l) dt_j: an inclusive suffix sum of a_l over the lanes (zero past
+  // m - 1), shifted down by one lane
+  float su = cr.dt * hd[HD_AH];
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const float t = __shfl_down(su, d);
+    if (lane + d < 64) su += t;
+  }
+  su = __shfl_down(su, 1);
+  const float cw = expf(lane < 63 ? su : 0.f) * cr.dt * cr.s;
   const uint32_t xw[4] = {cr.xv.x, cr.xv.y, cr.xv.z, cr.xv.w};
   float v[8];  // w_j x_j[r] for the wave's rows r = 0 .. 7
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    v[2 * i] = cr.w * __uint_as_float(xw[i] << 16);
-    v[2 * i + 1] = cr.w * __uint_as_float(xw[i] & 0xffff0000u);
+    v[2 * i] = cw * __uint_as_float(xw[i] << 16);
+    v[2 * i + 1] = cw * __uint_as_float(xw[i] & 0xffff0000u);
   }
   // keep the half of the rows whose bit matches the lane's, add the partner's share of it
   const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
@@ -1016,8 +1029,8 @@ __device__ __forceinline__ float corr_sum(const float* __restrict__ hd, int p, i
 #pragma unroll
   for (int i = 0; i < 2; ++i) s2[i] = (b4 ? s4[2 + i] : s4[i]) + __shfl_xor(b4 ? s4[i] : s4[2 + i], 16);
   float s = (b3 ? s2[1] : s2[0]) + dpp<0x128>(b3 ? s2[0] : s2[1]);  // row_ror:8, lane ^ 8
-  // this token, window position m - 1 (cw from the lane that loaded it)
-  const float wl = m > 0 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cr.w), max(m, 1) - 1)) : 0.f;
+  // this token, window position m - 1 (cw of the lane that formed it)
+  const float wl = m > 0 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cw), max(m, 1) - 1)) : 0.f;
   return q == 0 ? fmaf(wl, xcur, s) : s;
 }
 __device__ __forceinline__ float corr_partial(const StepArgs& a, const float* __restrict__ hd, size_t sh, size_t rh,
@@ -1500,8 +1513,14 @@ __device__ __forceinline__ void unit_body(const StepArgs& a, const float* __rest
     unit_compute<K, COLD, EXACT>(a, sh, rh, p, q, d, rx, !flushing, hd, k);
 }
 
+// (the exact readout's fused replay over a 32-column fp32 or bf16 hot tier keeps the
+// correction's window weights beside the replay's registers: 8 waves spill there)
 template <int K, int COLD, bool FUSED, bool EXACT>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(unit_waves_per_eu<K, COLD>()))) unit_kernel(StepArgs a, const float* __restrict__ hd_ro) {
+constexpr int unit_any_waves_per_eu() {
+  return EXACT && FUSED && K == 32 && unit_waves_per_eu<K, COLD>() == 8 ? 7 : unit_waves_per_eu<K, COLD>();
+}
+template <int K, int COLD, bool FUSED, bool EXACT>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(unit_any_waves_per_eu<K, COLD, FUSED, EXACT>()))) unit_kernel(StepArgs a, const float* __restrict__ hd_ro) {
   unit_body<K, COLD, FUSED, EXACT, false>(a, hd_ro);
 }
 template <int K, int COLD, bool FUSED>
@@ -2928,7 +2947,7 @@ int v4_step(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step
   a.fch = a.split ? flush_chunk(prm->P, tier->k_hot, tier->cold_kind, tier->c) : 0;
   a.fpipe = a.split && g_flush_pipe && flush_pipe(prm->P, tier->k_hot, tier->cold_kind, tier->c);
   if (a.fpipe) a.fch = (tier->c + 3) & ~3;
-  a.fw = a.fpipe && !exact;
+  a.fw = a.fpipe;
   hipStream_t st = (hipStream_t)stream;
   switch (tier->k_hot) {
     case 0: return dispatch_kind<0>(a, tier->cold_kind, L, st);

@@ -151,9 +151,9 @@ def test_entry_points_validate_before_launching():
     need = L.nssm_step_workspace_bytes(4, 8, 1, 128, 0)
     assert need == 4 * (2 * 128 + 12 * 8) * 4
     # tiered: plus per-(request, group) flush flags [b][G] (padded to a multiple of 4),
-    # window weights and exact-readout coefficients [b][H][c] each
-    assert L.nssm_step_workspace_bytes(4, 8, 1, 128, 4) == need + 4 * 4 + 2 * 4 * 8 * 4 * 4
-    assert L.nssm_step_workspace_bytes(3, 8, 2, 128, 4) == 4 * (3 * (2 * 2 * 128 + 12 * 8 + 2 * 8 * 4) + 8)
+    # window weights [b][H][c] and the exact readout's window dots [b][G][c]
+    assert L.nssm_step_workspace_bytes(4, 8, 1, 128, 4) == need + 4 * 4 + (4 * 8 * 4 + 4 * 1 * 4) * 4
+    assert L.nssm_step_workspace_bytes(3, 8, 2, 128, 4) == 4 * (3 * (2 * 2 * 128 + 12 * 8 + 8 * 4 + 2 * 4) + 8)
     assert L.nssm_step_workspace_bytes(4, 8, 3, 128, 4) == -2
     assert L.nssm_fresh_step(ctypes.byref(prm), fake, 4, ctypes.byref(inp), fake, None, need, None) == -7
     assert L.nssm_fresh_step(ctypes.byref(prm), fake, 4, ctypes.byref(inp), fake, fake, need - 4, None) == -7
@@ -264,8 +264,8 @@ def test_noalloc_step_refuses_calls_beyond_its_scratch():
     tier = _lib.Tier(4096, 32, 4, _lib.COLD_FP32, *([fake] * 10))
     need = lambda b: L.nssm_step_workspace_bytes(b, 128, 8, 128, 4)  # noqa: E731
     limit = 32 << 20
-    assert need(1817) <= limit < need(1818)
-    big = _lib.StepInputs(1818, fake, fake, fake, fake, None)
+    assert need(2028) <= limit < need(2029)
+    big = _lib.StepInputs(2029, fake, fake, fake, fake, None)
     assert L.nssm_v4_step_noalloc(ctypes.byref(prm), ctypes.byref(tier), ctypes.byref(big), fake, None) == -8
     assert "scratch" in L.nssm_strerror(-8).decode()
     assert L.nssm_v4_step_noalloc(None, ctypes.byref(tier), ctypes.byref(big), fake, None) == -1
