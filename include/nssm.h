@@ -24,6 +24,9 @@
  *   nssm_v4_step_teacher scale/nemo9b_eval.py:41-85 (naive_mixer_forward, modes
  *                        "v4" and, with k_hot = 0, "c1": the teacher-forced
  *                        evaluation readout)
+ *   nssm_v4_step_teacher_lagged  the same loop with CFG["lag"] = 1
+ *                        (scale/nemo9b_eval.py:44,59,70: readers one snapshot
+ *                        behind, the asynchronous-flush model)
  *   nssm_v4_join         scale/vllm_v4_patch.py:123-137 (prefill_snapshot),
  *                        scale/v4_native_decode.py:234-243,
  *                        scale/v4_fused_decode.py:121-159 (prefill capture)
@@ -51,7 +54,7 @@
 extern "C" {
 #endif
 
-#define NSSM_ABI_VERSION 12
+#define NSSM_ABI_VERSION 13
 
 /* error codes */
 #define NSSM_OK 0
@@ -127,8 +130,8 @@ typedef struct nssm_step_inputs {
  *   glog     fp32 [slots][H]            log-decay since the snapshot, one token lagged
  * All heads of a slot carry equal t and nv. hot, cold, master, ring_x and ring_b
  * are 16-byte aligned. k_hot = 0 (every column cold; hot may be NULL, it is never
- * read) needs a cold tier and serves nssm_v4_step_teacher, join and materialize; the
- * other step entry points return NSSM_E_DIMS for it.
+ * read) needs a cold tier and serves nssm_v4_step_teacher(_lagged), join and
+ * materialize; the other step entry points return NSSM_E_DIMS for it.
  * Unit-blocked (the bf16 read copies, the bf16 master): with row = (slot H + h) P + p,
  * element (row, col) sits at (row / 8) 8 NC + (col / 32) 256 + (row % 8) w + col % 32,
  * w = min(32, NC - 32 (col / 32)): the 8 rows of a unit form one block, 32-column segment
@@ -225,6 +228,32 @@ int nssm_v4_step_exact(const nssm_layer_params* prm, const nssm_tier* tier,
 int nssm_v4_step_teacher(const nssm_layer_params* prm, const nssm_tier* tier,
                          const nssm_step_inputs* in, float* y, void* workspace,
                          int64_t workspace_bytes, void* stream);
+
+/* The lagged snapshot of a tier (caller-owned):
+ *   cold   the read copy of the snapshot before the tier's last one: cold's dtype and
+ *          layout and size, 16-byte aligned
+ *   scale  its fp32 row scales [slots][H][P] (FP8 and FP8_BF16M, else NULL)
+ *   wlog   fp32 [slots][H]: the log-decay between that snapshot and the tier's last
+ * At a join both snapshots are the joined state: a caller copies the tier's cold (and
+ * scale) rows of the joined slots into these and zeroes their wlog. */
+typedef struct nssm_lag {
+  void* cold;
+  float* scale;
+  float* wlog;
+} nssm_lag;
+
+/* nssm_v4_step_teacher with the evaluation loop's lag = 1 (scale/nemo9b_eval.py:44,59,70):
+ * the readout is of the snapshot before the last one, decayed from it,
+ *   flush token:  y = hot C'[:K] + exp(w) (old read copy C'[K:]) + D x, w = the
+ *                 log-decay of the window this token closes; the old read copy then
+ *                 becomes the lagged one (lag->cold, lag->scale) and lag->wlog = w
+ *   other tokens: y = hot C'[:K] + exp(glog + a + wlog) (lag->cold C'[K:]) + D x.
+ * The tier evolves as with nssm_v4_step; only these steps keep `lag` current, so a tier
+ * read this way takes this readout on every step. k_hot = 0 is mode "c1" with lag = 1.
+ * NSSM_E_KIND for NSSM_COLD_NONE. */
+int nssm_v4_step_teacher_lagged(const nssm_layer_params* prm, const nssm_tier* tier,
+                                const nssm_lag* lag, const nssm_step_inputs* in, float* y,
+                                void* workspace, int64_t workspace_bytes, void* stream);
 
 /* nssm_v4_step with a gated stale readout: a skipped head's y is hot C'[:K] + D x
  * (no cold term) and, when it does not flush at this token, its cold columns are not

@@ -38,6 +38,10 @@ class Tier(ctypes.Structure):
                [(f, c_vp) for f in TIER_FIELDS]
 
 
+class Lag(ctypes.Structure):
+    _fields_ = [("cold", c_vp), ("scale", c_vp), ("wlog", c_vp)]
+
+
 _lib = None
 
 
@@ -67,6 +71,8 @@ def lib():
     L.nssm_v4_step_exact.argtypes = [P_(LayerParams), P_(Tier), P_(StepInputs), c_vp, c_vp, c_i64, c_vp]
     L.nssm_v4_step_noalloc.argtypes = [P_(LayerParams), P_(Tier), P_(StepInputs), c_vp, c_vp]
     L.nssm_v4_step_teacher.argtypes = [P_(LayerParams), P_(Tier), P_(StepInputs), c_vp, c_vp, c_i64, c_vp]
+    L.nssm_v4_step_teacher_lagged.argtypes = [P_(LayerParams), P_(Tier), P_(Lag), P_(StepInputs), c_vp, c_vp, c_i64,
+                                              c_vp]
     L.nssm_v4_step_gated.argtypes = [P_(LayerParams), P_(Tier), P_(StepInputs), c_vp, c_vp, c_i64, c_i32,
                                      ctypes.c_float, c_vp, c_vp]
     L.nssm_v4_join.argtypes = [P_(LayerParams), P_(Tier), c_vp, c_i32, c_vp, c_vp, c_vp]
@@ -81,7 +87,7 @@ def lib():
     L.nssm_host_e4m3fn_to_f32.argtypes = [c_vp, c_vp, ctypes.c_int64]
     L.nssm_host_f32_to_bf16.argtypes = [c_vp, c_vp, ctypes.c_int64]
     for fn in ("nssm_fresh_step", "nssm_v4_step", "nssm_v4_step_noalloc", "nssm_v4_step_exact", "nssm_v4_step_gated",
-               "nssm_v4_step_teacher",
+               "nssm_v4_step_teacher", "nssm_v4_step_teacher_lagged",
                "nssm_v4_join",
                "nssm_v4_materialize",
                "nssm_fp8_readout", "nssm_rotate", "nssm_conv_update", "nssm_gated_rmsnorm", "nssm_set_launch",
@@ -101,7 +107,7 @@ def check(rc: int, what: str) -> None:
 
 # symbols include/nssm.h declares (checked by the CPU test-suite)
 EXPORTED = ("nssm_tier_sizes", "nssm_step_workspace_bytes", "nssm_fresh_step", "nssm_v4_step", "nssm_v4_step_noalloc",
-            "nssm_v4_step_exact", "nssm_v4_step_teacher",
+            "nssm_v4_step_exact", "nssm_v4_step_teacher", "nssm_v4_step_teacher_lagged",
             "nssm_v4_step_gated", "nssm_v4_join",
             "nssm_v4_materialize", "nssm_fp8_readout", "nssm_rotate", "nssm_conv_update", "nssm_gated_rmsnorm",
             "nssm_set_launch",

@@ -90,6 +90,13 @@ struct StepArgs {
   int32_t hot_only;
   float qgate_tau;
   unsigned long long* qcounts;
+  // lagged teacher-forced readout (scale/nemo9b_eval.py:44,59,70, lag = 1): the read copy of
+  // the snapshot before the last (cold2, scale2: cold's and scale's dtype and layout) and,
+  // per (slot, head), the log-decay between those two snapshots (wlag)
+  int32_t lag;
+  void* cold2;
+  float* scale2;
+  float* wlag;
 };
 
 // Workspace carve-up for b requests (floats): rotated B and C [b][G][N] each,
@@ -581,8 +588,16 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
       // stale: exp(glog), the decay up to the previous token (one-token lag);
       // exact: exp(glog + a), inclusive of this token (scale/v4_native_decode.py:89)
       // teacher-forced (scale/nemo9b_eval.py:57-70): the snapshot is the state after the flush
-      // token's update, read undecayed at that token and with inclusive decay after it
-      hd[HD_SNAPF] = skip ? 0.f : a.tf ? (flush ? 1.f : expf(gl + av)) : expf(exact ? gl + av : gl);
+      // token's update, read undecayed at that token and with inclusive decay after it;
+      // lagged (:59,70): the snapshot before it, decayed by the window between the two (wlag)
+      // as well; at a flush the old snapshot becomes the lagged one, wlag this window's decay
+      if (a.lag) {
+        const float wl = a.wlag[o];
+        hd[HD_SNAPF] = expf(flush ? gl + av : gl + av + wl);
+        if (flush) a.wlag[o] = gl + av;
+      } else {
+        hd[HD_SNAPF] = skip ? 0.f : a.tf ? (flush ? 1.f : expf(gl + av)) : expf(exact ? gl + av : gl);
+      }
       hd[HD_SKIP] = skip ? 1.f : 0.f;
       hd[HD_FLUSH] = flush ? 1.f : 0.f;
       hd[HD_POS] = (float)pos;
@@ -806,10 +821,15 @@ __device__ __forceinline__ void coef_load(const float* wB, const float* wC, int 
   }
 }
 
+// cold_src / scale_src: the read copy to read (default the tier's; the lagged readout reads
+// its second one)
 template <int K, int COLD>
 __device__ __forceinline__ void unit_load(const StepArgs& a, size_t row, size_t xrow, int q, UnitRaw<K, COLD>& d,
-                                          bool hot_only = false) {
+                                          bool hot_only = false, const void* cold_src = nullptr,
+                                          const float* scale_src = nullptr) {
   using C = Cfg<K, COLD>;
+  const void* const cold = cold_src ? cold_src : a.cold;
+  const float* const scale = scale_src ? scale_src : a.scale;
   const f4* hp = reinterpret_cast<const f4*>(a.hot + row * K) + q;
 #pragma unroll
   for (int s = 0; s < C::HS; ++s) d.hv[s] = ld_stream(hp + 8 * s);
@@ -817,34 +837,68 @@ __device__ __forceinline__ void unit_load(const StepArgs& a, size_t row, size_t 
   if constexpr (C::TIERED) {
     if (!hot_only) {
       if constexpr (COLD == NSSM_COLD_FP32) {
-        const float* rp = static_cast<const float*>(a.cold) + row * C::NC;
+        const float* rp = static_cast<const float*>(cold) + row * C::NC;
         const f4* p = reinterpret_cast<const f4*>(rp) + q;
 #pragma unroll
         for (int s = 0; s < C::CS; ++s) d.cf[s] = ld_stream(p + 8 * s);
         if constexpr (C::CH) d.cfh = ld_stream(reinterpret_cast<const f2*>(rp + 32 * C::CS) + q);
       } else if constexpr (C::B16) {
-        const uint16_t* base = static_cast<const uint16_t*>(a.cold);
+        const uint16_t* base = static_cast<const uint16_t*>(cold);
         const u2v* p = reinterpret_cast<const u2v*>(base + blk16(row, 4 * q, C::NC));
 #pragma unroll
         for (int s = 0; s < C::CS; ++s) d.cb[s] = ld_stream(p + kBlkSeg * s);
         if constexpr (C::CH)
           d.cbh = ld_stream(reinterpret_cast<const uint32_t*>(base + blk16(row, 32 * C::CS + 2 * q, C::NC)));
       } else if constexpr (C::SEG8) {
-        const uint8_t* rp = static_cast<const uint8_t*>(a.cold) + row * C::NC;
+        const uint8_t* rp = static_cast<const uint8_t*>(cold) + row * C::NC;
         const uint32_t* p = reinterpret_cast<const uint32_t*>(rp) + q;
 #pragma unroll
         for (int s = 0; s < C::CS; ++s) d.c8[s] = ld_stream(p + 8 * s);
         d.c8h = ld_stream(reinterpret_cast<const uint16_t*>(rp + 32 * C::CS) + q);
-        d.sc = a.scale[row];
+        d.sc = scale[row];
       } else {
         ld_words<C::WORDS>(
-            reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(a.cold) + row * C::NC + C::CW * q), d.cw);
-        d.sc = a.scale[row];
+            reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(cold) + row * C::NC + C::CW * q), d.cw);
+        d.sc = scale[row];
       }
     }
   }
   d.xraw = a.x[xrow];
   d.xp = bf2f(d.xraw);
+}
+
+// The lagged readout's flush: the old read copy as unit_load read it (d), written to the
+// tier's second read copy in the same mapping, before the flush replaces the first.
+template <int K, int COLD>
+__device__ __forceinline__ void lag_store(const StepArgs& a, size_t row, int q, const UnitRaw<K, COLD>& d) {
+  using C = Cfg<K, COLD>;
+  if constexpr (C::TIERED) {
+    if constexpr (COLD == NSSM_COLD_FP32) {
+      float* rp = static_cast<float*>(a.cold2) + row * C::NC;
+      f4* p = reinterpret_cast<f4*>(rp) + q;
+#pragma unroll
+      for (int s = 0; s < C::CS; ++s) st_stream(d.cf[s], p + 8 * s);
+      if constexpr (C::CH) st_stream(d.cfh, reinterpret_cast<f2*>(rp + 32 * C::CS) + q);
+    } else if constexpr (C::B16) {
+      uint16_t* base = static_cast<uint16_t*>(a.cold2);
+      u2v* p = reinterpret_cast<u2v*>(base + blk16(row, 4 * q, C::NC));
+#pragma unroll
+      for (int s = 0; s < C::CS; ++s) st_stream(d.cb[s], p + kBlkSeg * s);
+      if constexpr (C::CH) st_stream(d.cbh, reinterpret_cast<uint32_t*>(base + blk16(row, 32 * C::CS + 2 * q, C::NC)));
+    } else if constexpr (C::SEG8) {
+      uint8_t* rp = static_cast<uint8_t*>(a.cold2) + row * C::NC;
+      uint32_t* p = reinterpret_cast<uint32_t*>(rp) + q;
+#pragma unroll
+      for (int s = 0; s < C::CS; ++s) st_stream(d.c8[s], p + 8 * s);
+      st_stream((uint16_t)d.c8h, reinterpret_cast<uint16_t*>(rp + 32 * C::CS) + q);
+      if (q == 0) a.scale2[row] = d.sc;
+    } else {
+      uint32_t* p = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.cold2) + row * C::NC + C::CW * q);
+#pragma unroll
+      for (int i = 0; i < C::WORDS; ++i) st_stream(d.cw[i], p + i);
+      if (q == 0) a.scale2[row] = d.sc;
+    }
+  }
 }
 
 __device__ __forceinline__ void bf16x4_to_f32(u2v w, float (&v)[4]) {
@@ -1284,14 +1338,14 @@ constexpr bool fused_requant() {
   return (Cfg<K, COLD>::MASTER32 || Cfg<K, COLD>::MASTER16) && K != 16 && !(K == 32 && COLD == NSSM_COLD_BF16);
 }
 
-template <int K, int COLD, bool EXACT, bool TF = false>
+template <int K, int COLD, bool EXACT, bool TF = false, bool LAG = false>
 __device__ __forceinline__ void unit_compute_flush(const StepArgs& a, size_t sh, size_t rh, int p, int q,
                                                    UnitRaw<K, COLD>& d, const float* __restrict__ hd,
                                                    const Coef<K, COLD>& k, const float* sU, const float* sBc, int m,
                                                    int ldu, int pofs, const MasterRaw<K, COLD>* mr = nullptr) {
   using C = Cfg<K, COLD>;
   constexpr int NC = C::NC, CS = C::CS;
-  constexpr bool kMaster = fused_requant<K, COLD>();  // the read copy was not loaded
+  constexpr bool kMaster = fused_requant<K, COLD>() && !LAG;  // the read copy was not loaded
   constexpr bool kRequant = kMaster && !TF;  // the stale readout from the master's values
   const size_t row = sh * a.P + p, yrow = rh * a.P + p;
   float part = hot_update<K, COLD>(a, row, q, d, hd, k);
@@ -1430,7 +1484,10 @@ constexpr int unit_waves_per_eu() {
 // before their state loads).
 // TF: the teacher-forced readout's variant (a flushing head reads the state it replays;
 // the other heads read the snapshot as the stale variant does, with prep's factor).
-template <int K, int COLD, bool FUSED, bool EXACT, bool GATED, bool TF = false>
+// LAG: the lagged teacher-forced readout's (a stale readout with prep's factor): a head
+// that does not flush reads the second read copy (the snapshot before the last); a flushing
+// head reads the old read copy, stores it there and replaces the first.
+template <int K, int COLD, bool FUSED, bool EXACT, bool GATED, bool TF = false, bool LAG = false>
 __device__ __forceinline__ void unit_body(const StepArgs& a, const float* __restrict__ hd_ro) {
   using C = Cfg<K, COLD>;
   constexpr int NC = C::NC;
@@ -1468,8 +1525,13 @@ __device__ __forceinline__ void unit_body(const StepArgs& a, const float* __rest
   UnitRaw<K, COLD> d;
   // a flushing head's read copy is needed here only when the replay is fused and the copy is
   // the replay's start (a single copy); beside a master the fused replay reads the master alone
-  constexpr bool kMaster = fused_requant<K, COLD>();
-  unit_load<K, COLD>(a, row, rh * P + p, q, d, flushing && (!FUSED || kMaster));
+  constexpr bool kMaster = fused_requant<K, COLD>() && !LAG;
+  if constexpr (LAG) {
+    unit_load<K, COLD>(a, row, rh * P + p, q, d, flushing && !FUSED, flushing ? a.cold : a.cold2,
+                       flushing ? a.scale : a.scale2);
+  } else {
+    unit_load<K, COLD>(a, row, rh * P + p, q, d, flushing && (!FUSED || kMaster));
+  }
   // the exact readout's correction: without the fused replay there are registers to issue
   // its loads now, beside the state's, instead of a second round trip after them
   constexpr bool kCorrPre = EXACT && !FUSED && TIERED;
@@ -1499,7 +1561,9 @@ __device__ __forceinline__ void unit_body(const StepArgs& a, const float* __rest
       // the stale readout of the requantized master takes C' in the segment mapping
       if constexpr (kMaster && !TF && C::CONTIG) coef_cold_seg<K, COLD>(wC, q, k);
       __syncthreads();
-      unit_compute_flush<K, COLD, EXACT, TF>(a, sh, rh, p, q, d, hd, k, sU, sBc, m, nr, p0, kEarly ? &mr : nullptr);
+      if constexpr (LAG) lag_store<K, COLD>(a, row, q, d);
+      unit_compute_flush<K, COLD, EXACT, TF, LAG>(a, sh, rh, p, q, d, hd, k, sU, sBc, m, nr, p0,
+                                                  kEarly ? &mr : nullptr);
       return;
     }
   }
@@ -1536,6 +1600,12 @@ constexpr int unit_tf_waves_per_eu() {
 template <int K, int COLD, bool FUSED>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(unit_tf_waves_per_eu<K, COLD>()))) unit_kernel_tf(StepArgs a, const float* __restrict__ hd_ro) {
   unit_body<K, COLD, FUSED, false, false, true>(a, hd_ro);
+}
+// (the lagged readout's fused replay also stores the old read copy: at k_hot = 32 over an
+// fp32 hot tier, 8 waves spill)
+template <int K, int COLD, bool FUSED>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(unit_any_waves_per_eu<K, COLD, FUSED, true>()))) unit_kernel_lag(StepArgs a, const float* __restrict__ hd_ro) {
+  unit_body<K, COLD, FUSED, false, false, false, true>(a, hd_ro);
 }
 
 // Untiered step (the full fp32 state is the hot tier, K = N): one one-wave workgroup per 2
@@ -1772,9 +1842,12 @@ __host__ __device__ constexpr int flush_alloc_tokens(int fch) { return (fch + 31
 
 // TF (the teacher-forced readout): y gets the readout of the new state as stored (the new
 // read copy; e4m3 partials formed after the row scale is known) instead of the old one's.
-template <int K, int COLD, bool TF = false>
+// LAG (the lagged teacher-forced readout): the stale readout of the old read copy, which is
+// also stored to the tier's second read copy (cold2, scale2) before the first is replaced.
+template <int K, int COLD, bool TF = false, bool LAG = false>
 __global__ void __launch_bounds__(kFlushWaves * 64) __attribute__((amdgpu_waves_per_eu(kFlushPerCU * kFlushWaves / 4)))
 flush_kernel(StepArgs a) {
+  static_assert(!(TF && LAG), "the lagged readout reads the old snapshot");
   using C = Cfg<K, COLD>;
   constexpr int NC = C::NC, NT = C::NT, nw = kFlushWaves, nthr = nw * 64;
   // work units: (n-tile, block of ptw consecutive p-tiles), one per wave and pass; the
@@ -2138,6 +2211,20 @@ flush_kernel(StepArgs a) {
               const float ov[4] = {old[i].x, old[i].y, old[i].z, old[i].w};
               if constexpr (C::E4M3) rscale = rsc[i];
               requant4<COLD>(ov, QDiv(rscale), rd);
+            }
+            if constexpr (LAG) {  // the old read copy becomes the lagged one
+              const size_t row = row0 + p;
+              if constexpr (COLD == NSSM_COLD_FP32) {
+                st_flush(old[i], reinterpret_cast<f4*>(static_cast<float*>(a.cold2) + row * NC + col));
+              } else if constexpr (C::B16) {  // (rd holds bf16 values: this conversion is exact)
+                st_flush(f32x4_to_bf16(rd[0], rd[1], rd[2], rd[3]),
+                         reinterpret_cast<u2v*>(static_cast<uint16_t*>(a.cold2) + blk16(row, col, NC)));
+              } else {  // e4m3: the codes of the old values at the stored scale
+                const QDiv qd(rscale);
+                st_flush(f32x4_to_fp8(qd(old[i].x), qd(old[i].y), qd(old[i].z), qd(old[i].w)),
+                         reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.cold2) + row * NC + col));
+                if (nt == 0 && lk == 0) a.scale2[row] = rscale;
+              }
             }
             float pc = rd[0] * cq.x;
             pc = fmaf(rd[1], cq.y, pc);
@@ -2854,7 +2941,7 @@ int launch_pair(const StepArgs& a, const Launch& L, hipStream_t st) {
   // teacher-forced readout only: the other stream and flush variants are not instantiated
   constexpr bool kTfOnly = K == 0;
   if constexpr (kTfOnly && !TIERED) return NSSM_E_KIND;
-  if (kTfOnly && !a.tf) return NSSM_E_DIMS;
+  if (kTfOnly && !a.tf && !a.lag) return NSSM_E_DIMS;
   if (a.b == 0) return NSSM_OK;
   StepArgs ap = a;
   ap.prb = prep_requests(a.HG);
@@ -2865,7 +2952,9 @@ int launch_pair(const StepArgs& a, const Launch& L, hipStream_t st) {
   if constexpr (TIERED) {
     const bool gated = a.hot_only || a.qgate_tau > 0.f;
     if (L.fused) {
-      if constexpr (kTfOnly) {
+      if (a.lag) {
+        hipLaunchKernelGGL((unit_kernel_lag<K, COLD, true>), ugrid, ublock, L.lds, st, a, hd_ro);
+      } else if constexpr (kTfOnly) {
         hipLaunchKernelGGL((unit_kernel_tf<K, COLD, true>), ugrid, ublock, L.lds, st, a, hd_ro);
       } else {
         if (a.exact) hipLaunchKernelGGL((unit_kernel<K, COLD, true, true>), ugrid, ublock, L.lds, st, a, hd_ro);
@@ -2875,7 +2964,9 @@ int launch_pair(const StepArgs& a, const Launch& L, hipStream_t st) {
       }
       return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
     }
-    if constexpr (kTfOnly) {
+    if (a.lag) {
+      hipLaunchKernelGGL((unit_kernel_lag<K, COLD, false>), ugrid, ublock, 0, st, a, hd_ro);
+    } else if constexpr (kTfOnly) {
       hipLaunchKernelGGL((unit_kernel_tf<K, COLD, false>), ugrid, ublock, 0, st, a, hd_ro);
     } else {
       if (a.exact) hipLaunchKernelGGL((unit_kernel<K, COLD, false, true>), ugrid, ublock, 0, st, a, hd_ro);
@@ -2894,7 +2985,8 @@ int launch_pair(const StepArgs& a, const Launch& L, hipStream_t st) {
       return NSSM_OK;
     };
     int frc;
-    if constexpr (kTfOnly) frc = go(flush_kernel<K, COLD, true>);
+    if (a.lag) frc = go(flush_kernel<K, COLD, false, true>);
+    else if constexpr (kTfOnly) frc = go(flush_kernel<K, COLD, true>);
     else frc = a.tf ? go(flush_kernel<K, COLD, true>) : go(flush_kernel<K, COLD, false>);
     if (frc) return frc;
   } else if constexpr (K == kN) {  // untiered
@@ -2918,17 +3010,28 @@ int dispatch_kind(const StepArgs& a, int kind, const Launch& L, hipStream_t st) 
   return NSSM_E_KIND;
 }
 
-// readout: 0 stale, 1 exact (rank-c correction), 2 teacher-forced
+// The second read copy of a lagged readout: cold's dtype and layout (scale with the e4m3
+// kinds), and the per-(slot, head) decay of the window between the two snapshots.
+int check_lag(const nssm_tier* tr, const nssm_lag* lg) {
+  if (!lg) return NSSM_E_NULL;
+  const bool e4m3 = tr->cold_kind == NSSM_COLD_FP8 || tr->cold_kind == NSSM_COLD_FP8_BF16M;
+  if (!lg->cold || !lg->wlog || (e4m3 && !lg->scale)) return NSSM_E_NULL;
+  if (!aligned16(lg->cold)) return NSSM_E_ALIGN;
+  return NSSM_OK;
+}
+
+// readout: 0 stale, 1 exact (rank-c correction), 2 teacher-forced, 3 lagged teacher-forced
 int v4_step(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step_inputs* in, float* y,
             void* workspace, int64_t workspace_bytes, void* stream, int readout, int hot_only = 0,
-            float qgate_tau = 0.f, int64_t* qcounts = nullptr) {
+            float qgate_tau = 0.f, int64_t* qcounts = nullptr, const nssm_lag* lag = nullptr) {
   const int exact = readout == 1;
   int rc = check_params(prm);
   if (rc) return rc;
   if ((rc = check_inputs(in, y))) return rc;
   if ((rc = check_tier(tier, true))) return rc;
   if (readout && tier->cold_kind == NSSM_COLD_NONE) return NSSM_E_KIND;  // these readouts need the cold tier
-  if (tier->k_hot == 0 && readout != 2) return NSSM_E_DIMS;  // every column cold: teacher-forced only
+  if (readout == 3 && (rc = check_lag(tier, lag))) return rc;
+  if (tier->k_hot == 0 && readout < 2) return NSSM_E_DIMS;  // every column cold: teacher-forced only
   if (!(fabsf(qgate_tau) <= 3.0e38f)) return NSSM_E_DIMS;  // NaN or infinite threshold
   if (qcounts && (reinterpret_cast<uintptr_t>(qcounts) & 7)) return NSSM_E_ALIGN;
   if (!in->slot_ids && in->b > tier->slots) return NSSM_E_DIMS;
@@ -2938,6 +3041,12 @@ int v4_step(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step
   fill_tier(a, tier);
   a.exact = exact;
   a.tf = readout == 2;
+  if (readout == 3) {
+    a.lag = 1;
+    a.cold2 = lag->cold;
+    a.scale2 = lag->scale;
+    a.wlag = lag->wlog;
+  }
   a.hot_only = hot_only != 0;
   a.qgate_tau = qgate_tau;
   a.qcounts = reinterpret_cast<unsigned long long*>(qcounts);
@@ -3158,6 +3267,12 @@ int nssm_v4_step_exact(const nssm_layer_params* prm, const nssm_tier* tier, cons
 int nssm_v4_step_teacher(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step_inputs* in, float* y,
                          void* workspace, int64_t workspace_bytes, void* stream) {
   return v4_step(prm, tier, in, y, workspace, workspace_bytes, stream, 2);
+}
+
+int nssm_v4_step_teacher_lagged(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_lag* lag,
+                                const nssm_step_inputs* in, float* y, void* workspace, int64_t workspace_bytes,
+                                void* stream) {
+  return v4_step(prm, tier, in, y, workspace, workspace_bytes, stream, 3, 0, 0.f, nullptr, lag);
 }
 
 int nssm_v4_step_gated(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step_inputs* in, float* y,

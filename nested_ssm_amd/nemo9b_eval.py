@@ -11,8 +11,9 @@ and the activation in torch (as the reference), then one state-op launch pair pe
 mode "fresh" (or "v4" with pb >= d_state) the untiered step; mode "v4" the teacher-forced
 readout of a tier with pb hot columns that starts each sequence from a zero state
 (nssm_v4_step_teacher; the exact readout for the first `warm` tokens); mode "c1" (every
-column stale, :79-80) the same readout of a tier with no hot column (k_hot = 0); then the
-gated norm and out_proj.
+column stale, :79-80) the same readout of a tier with no hot column (k_hot = 0); with
+lag = 1 (:44,59,70, readers one snapshot behind) either mode's lagged form
+(nssm_v4_step_teacher_lagged); then the gated norm and out_proj.
 
 The rotation R is read from the mixer (an ActRotMask-wrapped act, `_v4R` or `v4R`) and
 applied in fp32 inside the kernels; the wrapper's own activation is used, not its rotation.
@@ -24,9 +25,9 @@ diag(mask) R (the identity's when there is no R), which is the same product.
 cold_fp8 stores the tier's e4m3 format, the per-row scale amax / 448 + 1e-12 of
 scale/vllm_v4_patch.py:106-111, where this loop scales per column (amax over the head
 dimension, :62-64); the readout stays within the 2e-2 fp8 bar of that column emulation.
-Deviations, each raising NotImplementedError: lag != 0, state_bf16, state_fp8, a width
-given per request (a tensor), warm > 0 over a bf16 or e4m3 snapshot, and warm > 0 in mode
-"c1".
+Deviations, each raising NotImplementedError: state_bf16, state_fp8, a width given per
+request (a tensor), lag other than 0 or 1, and warm > 0 over a bf16 or e4m3 snapshot, in
+mode "c1" or with lag = 1.
 """
 import torch
 
@@ -75,9 +76,11 @@ def _params(m):
 
 
 def _check_cfg(cfg):
-    for key in ("lag", "state_bf16", "state_fp8"):
+    for key in ("state_bf16", "state_fp8"):
         if cfg.get(key, 0):
             raise NotImplementedError(f"CFG[{key!r}] = {cfg[key]} is not served by the MI355X kernels")
+    if int(cfg.get("lag", 0)) not in (0, 1):
+        raise NotImplementedError(f"CFG['lag'] = {cfg['lag']}: lags 0 and 1 are served by the kernels")
     if cfg["mode"] not in ("fresh", "v4", "c1"):
         raise NotImplementedError(f"mode {cfg['mode']!r}: 'fresh', 'v4' and 'c1' are served by the kernels")
 
@@ -98,12 +101,13 @@ def teacher_forced_inputs(m, input_states):
             dt.to(bf))
 
 
-def _tier(m, b, pb, c, cold, device):
+def _tier(m, b, pb, c, cold, device, lag=False):
     """The mixer's evaluation tier, kept between forwards of the same batch and split."""
-    key = (b, pb, c, cold)
+    key = (b, pb, c, cold, lag)
     t = getattr(m, "_tf_tier", None)
     if t is None or t[0] != key:
-        t = (key, V4Tier(b, m.num_heads, m.head_dim, m.n_groups, k_hot=pb, c=c, cold=cold, device=device))
+        t = (key, V4Tier(b, m.num_heads, m.head_dim, m.n_groups, k_hot=pb, c=c, cold=cold, device=device,
+                         lag=lag))
         m._tf_tier = t
     return t[1]
 
@@ -134,9 +138,12 @@ def state_op(m, x, B, C, dt, cfg=None):
         raise NotImplementedError("warm tokens read the exact state; over a bf16 / e4m3 snapshot the kernels' "
                                   "exact readout reads the rounded snapshot instead")
     k = 0 if mode == "c1" else pb  # c1: every column read from the snapshot
+    lag = bool(int(cfg.get("lag", 0)))
     if warm > 0 and k == 0:
         raise NotImplementedError("warm tokens in mode 'c1': a tier without hot columns has no exact readout")
-    tier = _tier(m, B_, k, c, cold, dev)
+    if warm > 0 and lag:
+        raise NotImplementedError("warm tokens with lag = 1: the exact readout does not keep the lagged snapshot")
+    tier = _tier(m, B_, k, c, cold, dev, lag)
     # the sequence starts from zeros at position 0, a flush position: phase c - 1
     tier.join(prm, zeros, phase=torch.full((B_,), c - 1, dtype=torch.int32, device=dev))
     for t in range(T):

@@ -159,10 +159,15 @@ class V4Tier:
     bf16 master beside the e4m3 copy. fp32 cold is its own fp32 master.
 
     k_hot = 0 (every column cold, the evaluation forward's mode "c1") serves the
-    teacher-forced readout only (step(..., teacher=True))."""
+    teacher-forced readout only (step(..., teacher=True)).
+
+    lag=True keeps the lagged snapshot of the evaluation forward's lag = 1
+    (scale/nemo9b_eval.py:44,59,70): a second read copy (cold2, scale2) and the log-decay
+    between the two snapshots per (slot, head) (wlag); such a tier is read with the lagged
+    teacher-forced readout (step(..., teacher=True)) only."""
 
     def __init__(self, slots: int, H: int, P: int, G: int, k_hot: int = 32, c: int = 4, cold: str = "fp32",
-                 device="cuda", N: int = N_STATE, master: str = "fp32"):
+                 device="cuda", N: int = N_STATE, master: str = "fp32", lag: bool = False):
         if cold not in COLD_KINDS:
             raise ValueError(f"cold must be one of {sorted(COLD_KINDS)} (got {cold!r})")
         if cold != "off" and (cold, master) not in _lib.STORAGE_KINDS:
@@ -190,6 +195,12 @@ class V4Tier:
         self.t = torch.zeros((slots, H), device=dev, dtype=torch.int32)
         self.nv = torch.zeros((slots, H), device=dev, dtype=torch.int32)
         self.glog = torch.zeros((slots, H), device=dev, dtype=torch.float32)
+        if lag and not tiered:
+            raise ValueError("the lagged readout needs a cold tier")
+        self.lag = lag
+        self.cold2 = torch.empty_like(self.cold_t) if lag else None
+        self.scale2 = torch.empty_like(self.scale) if lag and self.scale is not None else None
+        self.wlag = torch.zeros((slots, H), device=dev, dtype=torch.float32) if lag else None
         got = [self._field(f) for f in TIER_FIELDS]
         for f, tns, want in zip(TIER_FIELDS, got, sizes):
             have = 0 if tns is None else tns.numel() * tns.element_size()
@@ -228,6 +239,9 @@ class V4Tier:
     def c_struct(self) -> _lib.Tier:
         return _lib.Tier(self.slots, self.k, self.c, self.kind, *[_ptr(self._field(f)) for f in TIER_FIELDS])
 
+    def lag_struct(self) -> _lib.Lag:
+        return _lib.Lag(_ptr(self.cold2), _ptr(self.scale2), _ptr(self.wlag))
+
     def join(self, prm: LayerParams, state: torch.Tensor, slot_ids: Optional[torch.Tensor] = None,
              phase: Optional[torch.Tensor] = None):
         """Capture full states [b,H,P,N] fp32 into slots (end of prefill)."""
@@ -241,6 +255,12 @@ class V4Tier:
         pc, tc = prm.c_struct(), self.c_struct()
         check(lib().nssm_v4_join(ctypes.byref(pc), ctypes.byref(tc), state.data_ptr(), b, _ptr(slot_ids),
                                  _ptr(phase), _stream()), "nssm_v4_join")
+        if self.lag:  # both snapshots are the joined state (a slot's rows are contiguous in every layout)
+            sl = (torch.arange(b, device=state.device) if slot_ids is None else slot_ids).long()
+            self.cold2.index_copy_(0, sl, self.cold_t.index_select(0, sl))
+            if self.scale2 is not None:
+                self.scale2.index_copy_(0, sl, self.scale.index_select(0, sl))
+            self.wlag.index_fill_(0, sl, 0.0)
 
     def step(self, prm: LayerParams, x, B, C, dt, y: Optional[torch.Tensor] = None,
              slot_ids: Optional[torch.Tensor] = None, exact: bool = False, hot_only: bool = False,
@@ -256,7 +276,9 @@ class V4Tier:
         evolves the same way in every case. teacher=True is the teacher-forced readout of
         scale/nemo9b_eval.py:41-85 (nssm_v4_step_teacher: a flush token reads the state it
         flushes to, the others the snapshot with the decay inclusive of this token; join a
-        sequence's start at phase c - 1 to flush at positions t % c == 0 as that loop does).
+        sequence's start at phase c - 1 to flush at positions t % c == 0 as that loop does);
+        on a lagged tier its lag = 1 form (nssm_v4_step_teacher_lagged: the snapshot before
+        the last).
         noalloc=True runs the stale readout through
         nssm_v4_step_noalloc, whose workspace is the library's fixed per-GPU scratch array
         (with y given, the call allocates nothing; calls overlapping on one GPU race)."""
@@ -270,6 +292,8 @@ class V4Tier:
             raise ValueError("the teacher-forced readout cannot be combined with exact, hot_only or qgate")
         if self.k == 0 and not teacher:
             raise ValueError("a tier with k_hot = 0 (every column cold) serves the teacher-forced readout only")
+        if self.lag and not teacher:
+            raise ValueError("a lagged tier serves the (lagged) teacher-forced readout only")
         if y is None:
             y = torch.empty(b, prm.H, prm.P, device=x.device, dtype=torch.float32)
         _need(y, "y", torch.float32, (b, prm.H, prm.P))
@@ -286,6 +310,10 @@ class V4Tier:
         if gated:
             check(lib().nssm_v4_step_gated(*args, int(hot_only), float(qgate), _ptr(counts), _stream()),
                   "nssm_v4_step_gated")
+        elif self.lag:
+            lc = self.lag_struct()
+            check(lib().nssm_v4_step_teacher_lagged(args[0], args[1], ctypes.byref(lc), *args[2:], _stream()),
+                  "nssm_v4_step_teacher_lagged")
         else:
             fn, name = ((lib().nssm_v4_step_exact, "nssm_v4_step_exact") if exact else
                         (lib().nssm_v4_step_teacher, "nssm_v4_step_teacher") if teacher else

@@ -45,7 +45,10 @@ Pinning status of each function (how it is checked, in tests/test_oracle.py):
                     is shown to differ); c = 1 and k = N give the fresh readout; k = 0
                     (mode "c1") the same closed form with no hot term; master="bf16" the
                     fp64 trajectory with the cold columns rounded to bf16 at the join and
-                    at every snapshot (no rounding, or rounding every token, fails it)
+                    at every snapshot (no rounding, or rounding every token, fails it);
+                    lag=1 the same closed form one snapshot behind (the state after
+                    token c (floor(t / c) - 1), the joined state before the first two
+                    snapshots, decay from it to t; the unlagged snapshot fails it)
   mask_width        (set_width) the first `width` rotated coordinates of an explicit fp64
                     rotation kept, the rest zero; a fresh trajectory under it keeps the
                     masked state columns at zero and equals the trajectory of the

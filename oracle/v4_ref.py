@@ -419,13 +419,18 @@ class TieredV4:
 # ---------------------------------------------------------------------------
 class TeacherForcedV4:
     """The teacher-forced v4 readout of the reference's per-token evaluation forward,
-    scale/nemo9b_eval.py:41-85 (naive_mixer_forward, mode "v4", lag 0), per slot:
+    scale/nemo9b_eval.py:41-85 (naive_mixer_forward, mode "v4"), per slot:
 
       S_t = exp(a_t) S_{t-1} + (dt_t x_t) (x) B'_t                        (:53-54)
       Gtot_t = Gtot_{t-1} + a_t                                           (:60)
-      if t % c == 0: Snap = q(S_t), gSnap = Gtot_t   (after the update)   (:61-71)
-      y_t = S_t[:k] C'_t[:k] + exp(Gtot_t - gSnap) (Snap[k:] C'_t[k:]) + D x_t   (:72-84)
+      if t % c == 0: SnapL, gSnapL = Snap, gSnap                          (:59)
+                     Snap = q(S_t), gSnap = Gtot_t   (after the update)   (:61-71)
+      (Rd, gRd) = (SnapL, gSnapL) if lag else (Snap, gSnap)               (:70)
+      y_t = S_t[:k] C'_t[:k] + exp(Gtot_t - gRd) (Rd[k:] C'_t[k:]) + D x_t   (:72-84)
       (y_t = S_t C'_t + D x_t while t < warm, :75-78)
+
+    lag = 1 is the loop's asynchronous-flush model: readers see the snapshot one flush
+    behind (the one before the last).
 
     t counts the sequence's tokens from 0 (join sets it, with the state and its snapshot).
     q: "fp32" the clone, "bf16" S.to(bf16).float() (:66-67), "fp8" e4m3 with either the
@@ -440,15 +445,17 @@ class TeacherForcedV4:
     in between, and the snapshot is taken from the rounded values."""
 
     def __init__(self, slots: int, H: int, P: int, N: int, k: int, c: int, cold: str = "fp32",
-                 fp8_scale: str = "row", warm: int = 0, dtype=torch.float32, master: str = "fp32"):
+                 fp8_scale: str = "row", warm: int = 0, dtype=torch.float32, master: str = "fp32", lag: int = 0):
         assert 0 <= k <= N and c >= 1 and cold in ("fp32", "bf16", "fp8") and fp8_scale in ("row", "column")
-        assert master in ("fp32", "bf16") and not (cold == "fp32" and master == "bf16")
+        assert master in ("fp32", "bf16") and not (cold == "fp32" and master == "bf16") and lag in (0, 1)
         self.k, self.c, self.cold, self.fp8_scale, self.warm, self.dtype = k, c, cold, fp8_scale, warm, dtype
-        self.master = master
+        self.master, self.lag = master, lag
         self.S = torch.zeros(slots, H, P, N, dtype=dtype)
         self.snap = torch.zeros(slots, H, P, N - k, dtype=dtype)
+        self.snapl = torch.zeros(slots, H, P, N - k, dtype=dtype)
         self.gtot = torch.zeros(slots, H, dtype=dtype)
         self.gsnap = torch.zeros(slots, H, dtype=dtype)
+        self.gsnapl = torch.zeros(slots, H, dtype=dtype)
         self.t = torch.zeros(slots, dtype=torch.int64)
 
     def _q(self, S: torch.Tensor) -> torch.Tensor:
@@ -472,12 +479,15 @@ class TeacherForcedV4:
         return torch.cat([S[..., :k], S[..., k:].to(torch.bfloat16).to(S.dtype)], dim=-1)
 
     def join(self, slots, S_new: torch.Tensor, t0: Optional[torch.Tensor] = None):
-        """A sequence at position t0 (default 0) with state S_new: the snapshot is S_new."""
+        """A sequence at position t0 (default 0) with state S_new: the snapshot, and the lagged
+        one, is S_new."""
         slots = torch.as_tensor(slots, dtype=torch.long)
         self.S[slots] = self._round_master(S_new.to(self.dtype))
         self.snap[slots] = self._q(self.S[slots])
+        self.snapl[slots] = self.snap[slots]
         self.gtot[slots] = 0
         self.gsnap[slots] = 0
+        self.gsnapl[slots] = 0
         self.t[slots] = 0 if t0 is None else torch.as_tensor(t0, dtype=torch.int64)
 
     def step(self, x, B, C, dt_raw, prm: LayerParams, slots: Optional[torch.Tensor] = None,
@@ -500,11 +510,14 @@ class TeacherForcedV4:
             if self.master != "fp32":
                 S = torch.where(snapt[:, None, None, None], self._round_master(S), S)
                 self.S[slots] = S
+            self.snapl[ss] = self.snap[ss]
+            self.gsnapl[ss] = self.gsnap[ss]
             self.snap[ss] = self._q(S[snapt])
             self.gsnap[ss] = gtot[snapt]
-        glog = gtot - self.gsnap[slots]
+        rd, grd = (self.snapl, self.gsnapl) if self.lag else (self.snap, self.gsnap)
+        glog = gtot - grd[slots]
         y_v4 = torch.einsum("bhpn,bhn->bhp", S[..., :k], Cp[..., :k]) + \
-            torch.einsum("bhpn,bhn->bhp", self.snap[slots], Cp[..., k:]) * torch.exp(glog)[..., None]
+            torch.einsum("bhpn,bhn->bhp", rd[slots], Cp[..., k:]) * torch.exp(glog)[..., None]
         y_fresh = torch.einsum("bhpn,bhn->bhp", S, Cp)
         y = torch.where((t < self.warm)[:, None, None], y_fresh, y_v4)
         self.t[slots] = t + 1

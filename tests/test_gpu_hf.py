@@ -400,14 +400,17 @@ def test_phase_write_mid_window_recaptures_the_tier(monkeypatch, corr, t_new):
                                        (dict(mode="c1", c=4), None), (dict(mode="c1", c=16, cold_fp8=1), None),
                                        (dict(mode="c1", c=3, cold_bf16=1), None),
                                        (dict(mode="fresh"), 32), (dict(mode="v4", c=4, pb=32), 48),
-                                       (dict(mode="c1", c=4), 64)])
+                                       (dict(mode="c1", c=4), 64),
+                                       (dict(mode="v4", c=4, pb=32, lag=1), None), (dict(mode="c1", c=3, lag=1), None),
+                                       (dict(mode="v4", c=4, pb=32, cold_fp8=1, lag=1), None),
+                                       (dict(mode="v4", c=16, pb=32, cold_bf16=1, lag=1), 48)])
 def test_teacher_forced_state_op_matches_oracle(cfg, width):
     """The evaluation forward's state op (nemo9b_eval drop-in: one teacher-forced launch pair
     per token, sequences from zero states) against the oracle's restatement of
     scale/nemo9b_eval.py:41-85 on the same mixer inputs, modes "fresh", "v4" and "c1" (every
     column stale), with and without a width mask (set_width: the oracle masks the rotated
-    B and C, the drop-in folds the mask into R); fp32 1e-5, bf16 snapshot the bf16 bar, e4m3
-    (per-row scale) 2e-2."""
+    B and C, the drop-in folds the mask into R), lag 0 and 1 (:44,59,70); fp32 1e-5, bf16
+    snapshot the bf16 bar, e4m3 (per-row scale) 2e-2."""
     from helpers import assert_close_flips, max_rel
     from nested_ssm_amd import hf, nemo9b_eval as NE
 
@@ -423,7 +426,8 @@ def test_teacher_forced_state_op_matches_oracle(cfg, width):
     prm = _oracle_params(m, float(m.time_step_limit[0]))
     k = N if full["mode"] == "fresh" else 0 if full["mode"] == "c1" else full["pb"]
     cold = "fp8" if full["cold_fp8"] else "bf16" if full["cold_bf16"] else "fp32"
-    ref = oracle.TeacherForcedV4(2, m.num_heads, m.head_dim, N, k, full["c"], cold=cold, warm=full["warm"])
+    ref = oracle.TeacherForcedV4(2, m.num_heads, m.head_dim, N, k, full["c"], cold=cold, warm=full["warm"],
+                                 lag=int(full["lag"]))
     ref.join(torch.arange(2), torch.zeros(2, m.num_heads, m.head_dim, N))
     for t in range(13):
         y_ref = ref.step(x[:, t].cpu(), B[:, t].cpu(), C[:, t].cpu(), dt[:, t].cpu(), prm, width=width)
@@ -438,7 +442,8 @@ def test_teacher_forced_state_op_matches_oracle(cfg, width):
 def test_teacher_forced_forward_tracks_the_stock_forward():
     """naive_mixer_forward bound to every mixer: mode "fresh" gives the stock forward's logits
     within the bf16 cast of the kernel inputs, v4 with pb = N is the fresh forward, and v4 with
-    stale cold columns is not; unsupported CFG keys raise."""
+    stale cold columns is not, nor its lagged form (lag = 1) the same; unsupported CFG keys
+    raise."""
     from nested_ssm_amd import hf, nemo9b_eval as NE
 
     ids = torch.randint(0, 96, (2, 12), generator=torch.Generator().manual_seed(43)).cuda()
@@ -456,7 +461,9 @@ def test_teacher_forced_forward_tracks_the_stock_forward():
             NE.CFG.update(mode="v4", c=8, pb=32)
             v4 = model(ids, use_cache=False).logits.float()
             NE.CFG.update(mode="v4", lag=1)
-            with pytest.raises(NotImplementedError, match="lag"):
+            lagged = model(ids, use_cache=False).logits.float()
+            NE.CFG.update(lag=0, state_bf16=1)
+            with pytest.raises(NotImplementedError, match="state_bf16"):
                 model(ids, use_cache=False)
         finally:
             NE.CFG.clear()
@@ -466,6 +473,7 @@ def test_teacher_forced_forward_tracks_the_stock_forward():
     assert torch.equal(allhot, fresh)
     # stale cold columns move this small model's logits by ~1e-5 relative (fp32 rounding: ~1e-7)
     assert float((v4 - fresh).abs().max() / scale) > 5e-6
+    assert not torch.equal(lagged, v4) and bool(torch.isfinite(lagged).all())
 
 
 def test_reference_eval_driver_loop_runs_on_the_drop_in():

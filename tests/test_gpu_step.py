@@ -729,6 +729,80 @@ def test_teacher_forced_readout_from_scratch_with_ragged_starts():
         assert_close32(y, y_ref, f"teacher-forced ragged y step {step}", **FP32_TOL)
 
 
+@pytest.mark.parametrize("cold,k,c,master", [
+    ("fp32", 32, 4, "fp32"), ("fp32", 32, 16, "fp32"), ("fp32", 32, 64, "fp32"), ("fp32", 16, 40, "fp32"),
+    ("bf16", 32, 4, "fp32"), ("bf16", 32, 64, "fp32"), ("fp8", 32, 4, "fp32"), ("fp8", 16, 64, "fp32"),
+    ("bf16", 32, 4, "bf16"), ("bf16", 16, 40, "bf16"), ("fp8", 32, 16, "bf16"), ("fp8", 32, 64, "bf16"),
+    ("fp32", 0, 4, "fp32"), ("fp32", 0, 64, "fp32"), ("fp8", 0, 16, "bf16"), ("bf16", 0, 64, "fp32")])
+def test_teacher_forced_lagged_readout_matches_oracle(cold, k, c, master):
+    """nssm_v4_step_teacher_lagged against the oracle's restatement of the evaluation loop with
+    lag = 1 (scale/nemo9b_eval.py:44,59,70): the readout is of the snapshot before the last one,
+    decayed from it (the joined state until the second flush); both replay paths (the stream
+    kernel's up to 16 tokens, 32 for one bf16 copy, and the flush kernel's), every storage kind,
+    k_hot 0 (mode "c1"), 16 and 32. fp32 rtol = atol = 1e-5, bf16 the bf16 bar, e4m3 2e-2
+    relative; over 3c + 5 tokens (three flushes), and the state."""
+    b, H, G, P = 4, 8, 1, 80
+    gen, prm, S0 = _setup(b, H, P, G, seed=460 + k + c)
+    dprm = dev_params(prm)
+    ref = oracle.TeacherForcedV4(b, H, P, 128, k, c, cold=cold, master=master, lag=1)
+    ref.join(torch.arange(b), S0)
+    tier = V4Tier(b, H, P, G, k_hot=k, c=c, cold=cold, master=master, lag=True)
+    tier.join(dprm, *to_dev(S0), phase=torch.full((b,), c - 1, dtype=torch.int32, device="cuda"))
+    for step in range(3 * c + 5):
+        x, B, C, dt = oracle.make_step_inputs(b, H, P, 128, G, gen)
+        y_ref = ref.step(x, B, C, dt, prm)
+        y = tier.step(dprm, *to_dev(x, B, C, dt), teacher=True)
+        if cold == "fp8":
+            r = max_rel(y.cpu(), y_ref)
+            assert r <= 2e-2, f"fp8 lagged y step {step}: {r:.3g}"
+        elif cold == "bf16" or master == "bf16":
+            assert_close_flips(y, y_ref, f"bf16 lagged y step {step}")
+        else:
+            assert_close32(y, y_ref, f"lagged y step {step}", **FP32_TOL)
+    if master == "bf16":
+        assert_close_flips(tier.materialize(dprm), ref.S, "lagged state (bf16 master)")
+    else:
+        assert_close32(tier.materialize(dprm), ref.S, "lagged state", **FP32_TOL)
+
+
+def test_teacher_forced_lagged_readout_with_ragged_starts():
+    """Sequences from zero states in slots of their own, joined at different times with
+    phase c - 1, in a subset of slots per token: the lagged readout against the oracle."""
+    slots, H, G, P, k, c = 5, 8, 2, 48, 32, 4
+    gen, prm, _ = _setup(slots, H, P, G, seed=290)
+    dprm = dev_params(prm)
+    ref = oracle.TeacherForcedV4(slots, H, P, 128, k, c, lag=1)
+    tier = V4Tier(slots, H, P, G, k_hot=k, c=c, lag=True)
+    zeros = torch.zeros(slots, H, P, 128)
+    ref.join(torch.arange(slots), zeros)
+    tier.join(dprm, zeros.cuda(), phase=torch.full((slots,), c - 1, dtype=torch.int32, device="cuda"))
+    for step in range(24):
+        if step in (7, 15):  # a new sequence starts in slot 3
+            ref.join(torch.tensor([3]), torch.zeros(1, H, P, 128))
+            tier.join(dprm, torch.zeros(1, H, P, 128, device="cuda"),
+                      slot_ids=torch.tensor([3], dtype=torch.int32, device="cuda"),
+                      phase=torch.tensor([c - 1], dtype=torch.int32, device="cuda"))
+        sl = torch.randperm(slots, generator=gen)[:4].to(torch.int32)
+        x, B, C, dt = oracle.make_step_inputs(4, H, P, 128, G, gen)
+        y_ref = ref.step(x, B, C, dt, prm, slots=sl.long())
+        y = tier.step(dprm, *to_dev(x, B, C, dt), slot_ids=sl.cuda(), teacher=True)
+        assert_close32(y, y_ref, f"lagged ragged y step {step}", **FP32_TOL)
+
+
+def test_lagged_tier_refuses_the_other_readouts():
+    """A lagged tier keeps its second snapshot through the lagged teacher-forced readout only:
+    the stale, exact, gated and no-allocation steps raise before launching."""
+    b, H, G, P = 2, 8, 1, 80
+    gen, prm, S0 = _setup(b, H, P, G, seed=430)
+    dprm = dev_params(prm)
+    tier = V4Tier(b, H, P, G, k_hot=32, c=4, lag=True)
+    tier.join(dprm, *to_dev(S0))
+    x, B, C, dt = to_dev(*oracle.make_step_inputs(b, H, P, 128, G, gen))
+    for kw in (dict(), dict(exact=True), dict(hot_only=True), dict(qgate=0.5), dict(noalloc=True)):
+        with pytest.raises(ValueError):
+            tier.step(dprm, x, B, C, dt, **kw)
+
+
 def test_c1_tier_refuses_the_other_readouts():
     """A tier with k_hot = 0 (mode "c1") serves the teacher-forced readout only: the stale,
     exact, gated and no-allocation steps raise before launching."""

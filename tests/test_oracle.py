@@ -621,6 +621,39 @@ def test_teacher_forced_v4_equals_closed_form(k, c):
         assert float((y - (hot + cold(traj[ts], inc) + dx)).abs().max()) > 1e-6
 
 
+@pytest.mark.parametrize("k,c", [(32, 4), (16, 3), (0, 4), (32, 1)])
+def test_teacher_forced_v4_lagged_equals_closed_form(k, c):
+    """scale/nemo9b_eval.py:44,59,70 (lag = 1, the asynchronous-flush model): readers see the
+    snapshot before the last one. At position tau the cold term is
+    exp(sum_{i=lo}^{tau} a_i) S_lo[k:] C'[k:] with lo = c (floor(tau / c) - 1) + 1 (the state
+    after token c (floor(tau / c) - 1)), or lo = 0 (the joined state) for tau < c. Negative
+    control: the unlagged snapshot (lo = c floor(tau / c) + 1) misses from the second window on."""
+    b, H, P, G = 2, 4, 8, 2
+    gen, prm, S0 = _small(seed=330 + k + c, b=b, H=H, P=P, G=G)
+    steps = 3 * c + 2
+    ins = [oracle.make_step_inputs(b, H, P, N, G, gen) for _ in range(steps)]
+    traj, ays = _fresh_traj(S0, ins, prm)
+    tf = oracle.TeacherForcedV4(b, H, P, N, k, c, dtype=torch.float64, lag=1)
+    tf.join(torch.arange(b), S0.double())
+    prm64 = prm.to(torch.float64)
+    zero = torch.zeros(b, H, dtype=torch.float64)
+    for tau in range(steps):
+        x, B, C, dt = ins[tau]
+        y = tf.step(x, B, C, dt, prm)
+        Cp = _heads(oracle.rotate(C.double(), prm64.R), H)
+        dx = x.double() * prm64.D[None, :, None]
+        hot = torch.einsum("bhpn,bhn->bhp", traj[tau + 1][..., :k], Cp[..., :k])
+
+        def term(lo):
+            dec = sum((ays[i] for i in range(lo, tau + 1)), zero)
+            return torch.exp(dec)[..., None] * torch.einsum("bhpn,bhn->bhp", traj[lo][..., k:], Cp[..., k:])
+
+        lo = c * (tau // c - 1) + 1 if tau >= c else 0
+        assert torch.allclose(y, hot + term(lo) + dx, atol=1e-11), f"tau={tau}"
+        if tau >= c:
+            assert float((y - (hot + term(c * (tau // c) + 1) + dx)).abs().max()) > 1e-6
+
+
 def test_teacher_forced_v4_reduces_to_fresh_and_differs_from_decode():
     """c = 1 (a snapshot after every update) and k = N give the fresh readout; warm tokens
     read fresh; the decode readout (NativeV4, one-token-lagged snapshot) is another one."""
