@@ -1522,59 +1522,111 @@ __device__ __forceinline__ void unit_body(const StepArgs& a, const float* __rest
       return;
     }
   }
-  UnitRaw<K, COLD> d;
   // a flushing head's read copy is needed here only when the replay is fused and the copy is
   // the replay's start (a single copy); beside a master the fused replay reads the master alone
   constexpr bool kMaster = fused_requant<K, COLD>() && !LAG;
-  if constexpr (LAG) {
-    unit_load<K, COLD>(a, row, rh * P + p, q, d, flushing && !FUSED, flushing ? a.cold : a.cold2,
-                       flushing ? a.scale : a.scale2);
-  } else {
-    unit_load<K, COLD>(a, row, rh * P + p, q, d, flushing && (!FUSED || kMaster));
-  }
-  // the exact readout's correction: without the fused replay there are registers to issue
-  // its loads now, beside the state's, instead of a second round trip after them
   constexpr bool kCorrPre = EXACT && !FUSED && TIERED;
-  CorrRaw cr;
-  if constexpr (kCorrPre) corr_load(a, hd, sh, rh, p, q, cr);
-
-  const float* wB = ws.B + ((size_t)bi * a.G + g) * kN;
-  const float* wC = ws.C + ((size_t)bi * a.G + g) * kN;
-  Coef<K, COLD> k;
-  coef_load<K, COLD, C::SEGREAD || (TF && FUSED)>(wB, wC, q, k);
-
-  if constexpr (FUSED && TIERED) {
-    if (flushing) {
-      extern __shared__ float lds[];
-      const int m = min(max((int)hd[HD_M], 1), c);
-      const int nr = uw * 8;
-      float* sBc = lds;           // [m][NC]
-      float* sU = lds + c * NC;   // [m][nr]
-      // beside a master, the master (and e4m3 row scale) loads go out with the hot columns'
-      // ahead of the staging, so the window's and the state's latencies overlap (the e4m3
-      // flush token over a bf16 master: 380 -> 365 us at B = 256, 662 -> 635 at B = 448)
-      MasterRaw<K, COLD> mr;
-      constexpr bool kEarly = kMaster;
-      if constexpr (kEarly) master_load<K, COLD>(a, row, q, mr);
-      stage_unit_window<NC>(sBc, sU, m, P, p0, nr, a.ring_b + (((size_t)slot * a.G + g) * c + (c - m)) * NC, wB + K,
-                            a.ring_x + (sh * c + (c - m)) * P, a.x + rh * P, ws.w + rh * c, tid, blockDim.x);
-      // the stale readout of the requantized master takes C' in the segment mapping
-      if constexpr (kMaster && !TF && C::CONTIG) coef_cold_seg<K, COLD>(wC, q, k);
-      __syncthreads();
-      if constexpr (LAG) lag_store<K, COLD>(a, row, q, d);
-      unit_compute_flush<K, COLD, EXACT, TF, LAG>(a, sh, rh, p, q, d, hd, k, sU, sBc, m, nr, p0,
-                                                  kEarly ? &mr : nullptr);
-      return;
+  // Where the head scalars are scalar loads, each path issues its own loads after the flag,
+  // so the common path's go out together (e4m3 over a bf16 master, B = 256: non-flush tokens
+  // 162 -> 157 us, 5.87 -> 5.76 ms per 27-layer step; B = 448 10.17 -> 10.02). Over fp32
+  // cold (a vector load of the flag) the hot columns' loads are issued ahead of the flag's
+  // wait, shared by both paths (the split order: 8.45 -> 8.59 ms at the headline); so are
+  // the gated and teacher-forced variants' (their replay spills in the split order).
+  if constexpr (!kVecHd && !GATED && !TF) {
+    if constexpr (FUSED && TIERED) {
+      if (flushing) {
+        UnitRaw<K, COLD> d;
+        unit_load<K, COLD>(a, row, rh * P + p, q, d, kMaster);
+        const float* wB = ws.B + ((size_t)bi * a.G + g) * kN;
+        const float* wC = ws.C + ((size_t)bi * a.G + g) * kN;
+        Coef<K, COLD> k;
+        coef_load<K, COLD, C::SEGREAD || TF>(wB, wC, q, k);
+        extern __shared__ float lds[];
+        const int m = min(max((int)hd[HD_M], 1), c);
+        const int nr = uw * 8;
+        float* sBc = lds;           // [m][NC]
+        float* sU = lds + c * NC;   // [m][nr]
+        // beside a master, the master (and e4m3 row scale) loads go out with the hot columns'
+        // ahead of the staging, so the window's and the state's latencies overlap (the e4m3
+        // flush token over a bf16 master: 380 -> 365 us at B = 256, 662 -> 635 at B = 448)
+        MasterRaw<K, COLD> mr;
+        constexpr bool kEarly = kMaster;
+        if constexpr (kEarly) master_load<K, COLD>(a, row, q, mr);
+        stage_unit_window<NC>(sBc, sU, m, P, p0, nr, a.ring_b + (((size_t)slot * a.G + g) * c + (c - m)) * NC,
+                              wB + K, a.ring_x + (sh * c + (c - m)) * P, a.x + rh * P, ws.w + rh * c, tid,
+                              blockDim.x);
+        // the stale readout of the requantized master takes C' in the segment mapping
+        if constexpr (kMaster && !TF && C::CONTIG) coef_cold_seg<K, COLD>(wC, q, k);
+        __syncthreads();
+        if constexpr (LAG) lag_store<K, COLD>(a, row, q, d);
+        unit_compute_flush<K, COLD, EXACT, TF, LAG>(a, sh, rh, p, q, d, hd, k, sU, sBc, m, nr, p0,
+                                                    kEarly ? &mr : nullptr);
+        return;
+      }
     }
+    UnitRaw<K, COLD> d;
+    if constexpr (LAG) unit_load<K, COLD>(a, row, rh * P + p, q, d, flushing, a.cold2, a.scale2);
+    else unit_load<K, COLD>(a, row, rh * P + p, q, d, flushing);
+    CorrRaw cr;
+    if constexpr (kCorrPre) corr_load(a, hd, sh, rh, p, q, cr);
+    const float* wB = ws.B + ((size_t)bi * a.G + g) * kN;
+    const float* wC = ws.C + ((size_t)bi * a.G + g) * kN;
+    Coef<K, COLD> k;
+    coef_load<K, COLD, C::SEGREAD>(wB, wC, q, k);
+    uint16_t* rx = nullptr;
+    if constexpr (TIERED) {
+      if (!flushing) rx = a.ring_x + (sh * c + (int)hd[HD_POS]) * P;
+    }
+    if constexpr (kCorrPre)
+      unit_compute<K, COLD, EXACT, true>(a, sh, rh, p, q, d, rx, !flushing, hd, k, &cr);
+    else
+      unit_compute<K, COLD, EXACT>(a, sh, rh, p, q, d, rx, !flushing, hd, k);
+  } else {
+    UnitRaw<K, COLD> d;
+    if constexpr (LAG) {
+      unit_load<K, COLD>(a, row, rh * P + p, q, d, flushing && !FUSED, flushing ? a.cold : a.cold2,
+                         flushing ? a.scale : a.scale2);
+    } else {
+      unit_load<K, COLD>(a, row, rh * P + p, q, d, flushing && (!FUSED || kMaster));
+    }
+    // the exact readout's correction: without the fused replay there are registers to issue
+    // its loads now, beside the state's, instead of a second round trip after them
+    CorrRaw cr;
+    if constexpr (kCorrPre) corr_load(a, hd, sh, rh, p, q, cr);
+    const float* wB = ws.B + ((size_t)bi * a.G + g) * kN;
+    const float* wC = ws.C + ((size_t)bi * a.G + g) * kN;
+    Coef<K, COLD> k;
+    coef_load<K, COLD, C::SEGREAD || (TF && FUSED)>(wB, wC, q, k);
+    if constexpr (FUSED && TIERED) {
+      if (flushing) {
+        extern __shared__ float lds[];
+        const int m = min(max((int)hd[HD_M], 1), c);
+        const int nr = uw * 8;
+        float* sBc = lds;           // [m][NC]
+        float* sU = lds + c * NC;   // [m][nr]
+        MasterRaw<K, COLD> mr;
+        constexpr bool kEarly = kMaster;
+        if constexpr (kEarly) master_load<K, COLD>(a, row, q, mr);
+        stage_unit_window<NC>(sBc, sU, m, P, p0, nr, a.ring_b + (((size_t)slot * a.G + g) * c + (c - m)) * NC,
+                              wB + K, a.ring_x + (sh * c + (c - m)) * P, a.x + rh * P, ws.w + rh * c, tid,
+                              blockDim.x);
+        if constexpr (kMaster && !TF && C::CONTIG) coef_cold_seg<K, COLD>(wC, q, k);
+        __syncthreads();
+        if constexpr (LAG) lag_store<K, COLD>(a, row, q, d);
+        unit_compute_flush<K, COLD, EXACT, TF, LAG>(a, sh, rh, p, q, d, hd, k, sU, sBc, m, nr, p0,
+                                                    kEarly ? &mr : nullptr);
+        return;
+      }
+    }
+    uint16_t* rx = nullptr;
+    if constexpr (TIERED) {
+      if (!flushing) rx = a.ring_x + (sh * c + (int)hd[HD_POS]) * P;
+    }
+    if constexpr (kCorrPre)
+      unit_compute<K, COLD, EXACT, true>(a, sh, rh, p, q, d, rx, !flushing, hd, k, &cr);
+    else
+      unit_compute<K, COLD, EXACT>(a, sh, rh, p, q, d, rx, !flushing, hd, k);
   }
-  uint16_t* rx = nullptr;
-  if constexpr (TIERED) {
-    if (!flushing) rx = a.ring_x + (sh * c + (int)hd[HD_POS]) * P;
-  }
-  if constexpr (kCorrPre)
-    unit_compute<K, COLD, EXACT, true>(a, sh, rh, p, q, d, rx, !flushing, hd, k, &cr);
-  else
-    unit_compute<K, COLD, EXACT>(a, sh, rh, p, q, d, rx, !flushing, hd, k);
 }
 
 // (the exact readout's fused replay over a 32-column fp32 or bf16 hot tier keeps the
