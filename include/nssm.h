@@ -35,6 +35,7 @@
  *                        the cache, rebuilt from the tiers
  *   nssm_fp8_readout     scale/bench_v4_decode.py:33-60 (_fp8_matvec /
  *                        fp8_cold_readout)
+ *   nssm_check_slots     none (device-side slot id check for callers that cannot sync)
  *   nssm_rotate          scale/nemotron_retrofit.py:24-27 (ActRotMask._rot),
  *                        scale/vllm_v4_patch.py:41-45 (rot_flat)
  *   nssm_gated_rmsnorm   scale/v4_native_decode.py:170-171 (self.norm(y, gate):
@@ -54,7 +55,7 @@
 extern "C" {
 #endif
 
-#define NSSM_ABI_VERSION 13
+#define NSSM_ABI_VERSION 14
 
 /* error codes */
 #define NSSM_OK 0
@@ -289,6 +290,19 @@ int nssm_fp8_readout(const float* q, const uint8_t* s8, const float* scale, floa
                      int32_t rows, int32_t nc, int32_t pd, void* stream);
 
 /* out[t][g][m] = sum_n R[g][m][n] * in[t][g][n]; in bf16, out fp32. */
+/* Duplicate and out-of-range slot ids of one call, found on the device with no host sync
+ * (no counterpart in the reference, whose callers own one slot per sequence: it is for
+ * callers that cannot synchronise to check slot_ids on the host before a step, join or
+ * materialize; the kernels themselves do not check uniqueness). Enqueue it on the call's
+ * stream with the call's slot_ids [b]; owner: int64 [slots], 8-byte aligned; state: int32
+ * [2]; both zero before the first check and then left to this function. state[1] gets bit
+ * 0 when two requests of one call name the same slot and bit 1 when an id is outside
+ * [0, slots); the bits stay set until the caller clears them (read state[1] after a sync,
+ * outside graph capture). Each check (a graph replay too) uses a tag of its own, kept in
+ * state[0]. One workgroup; b up to 2^31 - 1. */
+int nssm_check_slots(const int32_t* slot_ids, int32_t b, int32_t slots, int64_t* owner, int32_t* state,
+                     void* stream);
+
 int nssm_rotate(const uint16_t* in, const float* R, float* out, int32_t T, int32_t G, int32_t N,
                 void* stream);
 

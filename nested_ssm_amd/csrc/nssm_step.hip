@@ -2518,6 +2518,30 @@ __global__ void fp8_readout_kernel(const float* __restrict__ q, const uint8_t* _
 }
 
 // rotation of flat [T][G][N] bf16 vectors; one workgroup per (t, g), one thread per output m
+// Duplicate and out-of-range slot ids of one call, on the device (one workgroup, so every
+// thread uses the same tag): tag = state[0] + 1, never 0 (the owner words start at 0); request i
+// exchanges (tag << 32 | i) into owner[slot] (64-bit vector atomics), and an old value with
+// this call's tag (another request of the call holds the slot) sets bit 0 of state[1], an id
+// outside [0, slots) bit 1; after every request, state[0] advances, so each call, graph
+// replays included, has a tag of its own.
+__global__ void __launch_bounds__(1024) check_slots_kernel(const int32_t* __restrict__ slot_ids, int b, int slots,
+                                                           unsigned long long* owner, int32_t* state) {
+  const uint32_t tag = (uint32_t)state[0] + 1u == 0u ? 1u : (uint32_t)state[0] + 1u;
+  int bad = 0;
+  for (int i = threadIdx.x; i < b; i += blockDim.x) {
+    const int s = slot_ids[i];
+    if (s < 0 || s >= slots) {
+      bad |= 2;
+      continue;
+    }
+    const unsigned long long old = atomicExch(owner + s, ((unsigned long long)tag << 32) | (uint32_t)i);
+    if ((uint32_t)(old >> 32) == tag) bad |= 1;
+  }
+  if (bad) atomicOr(state + 1, bad);
+  __syncthreads();  // every exchange of this call is done
+  if (threadIdx.x == 0) state[0] = (int32_t)tag;
+}
+
 __global__ void rotate_kernel(const uint16_t* __restrict__ in, const float* __restrict__ R, float* __restrict__ out,
                               int G, int N) {
   extern __shared__ float sv[];
@@ -3390,6 +3414,17 @@ int nssm_fp8_readout(const float* q, const uint8_t* s8, const float* scale, floa
   if (rows == 0) return NSSM_OK;
   dim3 grid((unsigned)((pd + 127) / 128), (unsigned)rows);
   hipLaunchKernelGGL(fp8_readout_kernel, grid, dim3(128), 0, (hipStream_t)stream, q, s8, scale, y, rows, nc, pd);
+  return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
+}
+
+int nssm_check_slots(const int32_t* slot_ids, int32_t b, int32_t slots, int64_t* owner, int32_t* state,
+                     void* stream) {
+  if (!slot_ids || !owner || !state) return NSSM_E_NULL;
+  if (b < 0 || slots <= 0) return NSSM_E_DIMS;
+  if (reinterpret_cast<uintptr_t>(owner) & 7) return NSSM_E_ALIGN;
+  if (b == 0) return NSSM_OK;
+  hipLaunchKernelGGL(check_slots_kernel, dim3(1), dim3(b < 1024 ? ((b + 63) & ~63) : 1024), 0, (hipStream_t)stream,
+                     slot_ids, b, slots, reinterpret_cast<unsigned long long*>(owner), state);
   return hipGetLastError() == hipSuccess ? NSSM_OK : NSSM_E_LAUNCH;
 }
 

@@ -46,16 +46,22 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
 
 # Duplicate slot ids in one call make the kernels' per-slot read-modify-writes race (the
 # tier rows, t / nv / glog and the ring of that slot), silently corrupting its state.
-# Checking needs a host sync (and so cannot run under graph capture): it is off unless
-# set_checks(slot_ids=True) or NSSM_CHECK_SLOTS=1 turns it on.
+# Two checks: on the device (nssm_check_slots, one small launch before each call with
+# slot_ids; no sync, graph-safe; V4Tier.slot_errors() reads what it found), on unless
+# set_checks(device_slots=False) or NSSM_DEVICE_SLOT_CHECK=0; and on the host (raises at
+# once, but needs a host sync and so skips graph capture), off unless
+# set_checks(slot_ids=True) or NSSM_CHECK_SLOTS=1.
 _CHECK_SLOTS = os.environ.get("NSSM_CHECK_SLOTS", "0") not in ("", "0")
+_DEVICE_SLOT_CHECK = os.environ.get("NSSM_DEVICE_SLOT_CHECK", "1") not in ("", "0")
 
 
-def set_checks(slot_ids: bool = False) -> None:
+def set_checks(slot_ids: bool = False, device_slots: bool = True) -> None:
     """Turn the host-side check that a call's slot_ids are unique on or off (it
-    synchronises the host with the device on every step, join and materialize)."""
-    global _CHECK_SLOTS
+    synchronises the host with the device on every step, join and materialize), and the
+    device-side one (nssm_check_slots before each call with slot_ids)."""
+    global _CHECK_SLOTS, _DEVICE_SLOT_CHECK
     _CHECK_SLOTS = bool(slot_ids)
+    _DEVICE_SLOT_CHECK = bool(device_slots)
 
 
 def _check_unique(slot_ids: Optional[torch.Tensor], what: str) -> None:
@@ -201,6 +207,9 @@ class V4Tier:
         self.cold2 = torch.empty_like(self.cold_t) if lag else None
         self.scale2 = torch.empty_like(self.scale) if lag and self.scale is not None else None
         self.wlag = torch.zeros((slots, H), device=dev, dtype=torch.float32) if lag else None
+        # the device-side slot id check's owner words and (call counter, error bits)
+        self.slot_owner = torch.zeros(slots, device=dev, dtype=torch.int64)
+        self.slot_state = torch.zeros(2, device=dev, dtype=torch.int32)
         got = [self._field(f) for f in TIER_FIELDS]
         for f, tns, want in zip(TIER_FIELDS, got, sizes):
             have = 0 if tns is None else tns.numel() * tns.element_size()
@@ -242,6 +251,24 @@ class V4Tier:
     def lag_struct(self) -> _lib.Lag:
         return _lib.Lag(_ptr(self.cold2), _ptr(self.scale2), _ptr(self.wlag))
 
+    def check_slots(self, slot_ids: torch.Tensor) -> None:
+        """Enqueue nssm_check_slots for one call's slot_ids (int32 [b] on the GPU): no sync;
+        what it finds accumulates until slot_errors()."""
+        _need(slot_ids, "slot_ids", torch.int32, (slot_ids.shape[0],))
+        check(lib().nssm_check_slots(slot_ids.data_ptr(), slot_ids.shape[0], self.slots, self.slot_owner.data_ptr(),
+                                     self.slot_state.data_ptr(), _stream()), "nssm_check_slots")
+
+    def _device_check(self, slot_ids: Optional[torch.Tensor]) -> None:
+        if _DEVICE_SLOT_CHECK and slot_ids is not None:
+            self.check_slots(slot_ids)
+
+    def slot_errors(self) -> int:
+        """The device-side slot check's findings since the last call (synchronises): bit 0,
+        two requests of one call named the same slot; bit 1, an id outside [0, slots). Clears them."""
+        bits = int(self.slot_state[1].item())
+        self.slot_state[1:].zero_()
+        return bits
+
     def join(self, prm: LayerParams, state: torch.Tensor, slot_ids: Optional[torch.Tensor] = None,
              phase: Optional[torch.Tensor] = None):
         """Capture full states [b,H,P,N] fp32 into slots (end of prefill)."""
@@ -252,6 +279,7 @@ class V4Tier:
         if phase is not None:
             _need(phase, "phase", torch.int32, (b,))
         _check_unique(slot_ids, "V4Tier.join")
+        self._device_check(slot_ids)
         pc, tc = prm.c_struct(), self.c_struct()
         check(lib().nssm_v4_join(ctypes.byref(pc), ctypes.byref(tc), state.data_ptr(), b, _ptr(slot_ids),
                                  _ptr(phase), _stream()), "nssm_v4_join")
@@ -301,6 +329,7 @@ class V4Tier:
             _need(counts, "counts", torch.int64, (2,))
         pc, ic, tc = prm.c_struct(), _inputs(prm, x, B, C, dt, slot_ids), self.c_struct()
         _check_unique(slot_ids, "V4Tier.step")
+        self._device_check(slot_ids)
         if noalloc:
             check(lib().nssm_v4_step_noalloc(ctypes.byref(pc), ctypes.byref(tc), ctypes.byref(ic), y.data_ptr(),
                                              _stream()), "nssm_v4_step_noalloc")
@@ -331,6 +360,7 @@ class V4Tier:
         if slot_ids is not None:
             _need(slot_ids, "slot_ids", torch.int32, (b,))
         _check_unique(slot_ids, "V4Tier.materialize")
+        self._device_check(slot_ids)
         pc, tc = prm.c_struct(), self.c_struct()
         check(lib().nssm_v4_materialize(ctypes.byref(pc), ctypes.byref(tc), out.data_ptr(), b, _ptr(slot_ids),
                                         _stream()), "nssm_v4_materialize")

@@ -255,6 +255,20 @@ def test_duplicate_slot_ids_are_refused_when_checked(monkeypatch):
     ops._check_unique(torch.tensor([3, 3], dtype=torch.int32), "V4Tier.step")
 
 
+def test_check_slots_argument_errors():
+    """nssm_check_slots refuses NULL buffers, sizes out of range and a misaligned owner array
+    before any device call."""
+    L = _lib.lib()
+    fake = 4096
+    assert L.nssm_check_slots(None, 4, 8, fake, fake, None) == -1
+    assert L.nssm_check_slots(fake, 4, 8, None, fake, None) == -1
+    assert L.nssm_check_slots(fake, 4, 8, fake, None, None) == -1
+    assert L.nssm_check_slots(fake, -1, 8, fake, fake, None) == -2
+    assert L.nssm_check_slots(fake, 4, 0, fake, fake, None) == -2
+    assert L.nssm_check_slots(fake, 4, 8, fake + 4, fake, None) == -3
+    assert L.nssm_check_slots(fake, 0, 8, fake, fake, None) == 0  # nothing to check
+
+
 def test_noalloc_step_refuses_calls_beyond_its_scratch():
     """nssm_v4_step_noalloc checks its arguments as nssm_v4_step does and refuses, before
     any device call, a call whose workspace would exceed NSSM_SCRATCH_BYTES."""

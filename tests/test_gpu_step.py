@@ -193,6 +193,54 @@ def test_out_of_range_slot_gives_nan_rows(rotation):
     assert_close32(S_dev[1:2], S1, "fresh slot-mapped state", **FP32_TOL)
 
 
+def test_device_slot_check_finds_duplicates_and_out_of_range_ids():
+    """nssm_check_slots (V4Tier.check_slots, enqueued before every call with slot_ids): unique
+    ids over many calls, each a different permutation and subset, find nothing; two requests
+    naming one slot set bit 0, an id outside [0, slots) bit 1; the bits stay until
+    slot_errors() clears them. Under graph capture each replay uses a tag of its own: replays
+    over changing unique ids find nothing, and one with a duplicate is found."""
+    tier = V4Tier(64, 8, 16, 1, k_hot=32, c=4)
+    gen = torch.Generator().manual_seed(500)
+    for _ in range(20):
+        ids = torch.randperm(64, generator=gen)[:int(torch.randint(1, 65, (1,), generator=gen))]
+        tier.check_slots(ids.to(torch.int32).cuda())
+    assert tier.slot_errors() == 0
+    tier.check_slots(torch.tensor([3, 9, 3], dtype=torch.int32, device="cuda"))
+    tier.check_slots(torch.tensor([0, 1, 2], dtype=torch.int32, device="cuda"))
+    assert tier.slot_errors() == 1
+    assert tier.slot_errors() == 0
+    tier.check_slots(torch.tensor([5, 64, -1], dtype=torch.int32, device="cuda"))
+    assert tier.slot_errors() == 2
+    big = V4Tier(3000, 8, 16, 1, k_hot=32, c=4)  # more requests than one workgroup's threads
+    ids = torch.randperm(3000, generator=gen).to(torch.int32).cuda()
+    big.check_slots(ids)
+    assert big.slot_errors() == 0
+    ids[2500] = ids[7]
+    big.check_slots(ids)
+    assert big.slot_errors() == 1
+    # graph replays: the same captured check over new contents of its id buffer
+    buf = torch.arange(16, dtype=torch.int32, device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        tier.check_slots(buf)  # warm-up outside the capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    assert tier.slot_errors() == 0
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        tier.check_slots(buf)
+    for r in range(6):
+        buf.copy_(torch.randperm(64, generator=gen)[:16].to(torch.int32))
+        g.replay()
+        torch.cuda.synchronize()
+        assert tier.slot_errors() == 0, f"replay {r}"
+    buf[5] = buf[11]
+    g.replay()
+    torch.cuda.synchronize()
+    assert tier.slot_errors() == 1
+
+
 @pytest.mark.parametrize("k", [32, 64, 96])
 def test_hot_only_tier(k):
     b, H, G, P = 3, 8, 2, 80
