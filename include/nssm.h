@@ -109,10 +109,11 @@ typedef struct nssm_step_inputs {
   const uint16_t* C;        /* [b][G][N] bf16, before rotation */
   const uint16_t* dt;       /* [b][H] bf16, before dt_bias and softplus */
   const int32_t* slot_ids;  /* [b] state slot of each request, unique; NULL = 0..b-1.
-                               The kernels do not check uniqueness: duplicates race on
-                               that slot's tier rows, phase and ring (undefined state).
-                               An id outside [0, slots) gives NaN rows of y and leaves
-                               every slot untouched. */
+                               The step kernels do not check uniqueness: duplicates race
+                               on that slot's tier rows, phase and ring (undefined
+                               state); nssm_check_slots flags them on the device. An id
+                               outside [0, slots) gives NaN rows of y and leaves every
+                               slot untouched. */
 } nssm_step_inputs;
 
 /* Tiered state of one layer for `slots` sequence slots (all buffers are
