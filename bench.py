@@ -43,8 +43,9 @@ def bytes_fresh_token():
 def bytes_v4_token(k, c, cold, master="fp32", skip=0.0, exact=False):
     """skip: fraction of heads whose cold term a gated readout drops; such a head reads
     no cold column on the c - 1 tokens of a window that do not flush. exact: the rank-c
-    correction's reads of the buffered x (a token finds (c - 1) / 2 of them on average) and
-    its per-head weights (written by prep, read by the stream kernel, (c + 1) / 2 each)."""
+    correction's reads of the buffered x and dt (a token finds (c - 1) / 2 of them on
+    average) and its window dots per group (written by prep, read by the stream kernel,
+    (c + 1) / 2 each)."""
     nc = N - k
     esz = {"fp32": 4, "bf16": 2, "fp8": 1}[cold]
     hot = 2 * H * P * k * 4
@@ -64,7 +65,7 @@ def bytes_v4_token(k, c, cold, master="fp32", skip=0.0, exact=False):
         flush = H * P * nc * (2 * msz + esz) + scale
     ring_entry = H * P * 2 + H * 4 + G * nc * 4  # x bf16, dt, B' cold
     ring = (c - 1) / c * 2 * ring_entry  # written by c-1 of c tokens, read once at the flush
-    corr = (H * P * 2 * (c - 1) / 2 + 2 * H * 4 * (c + 1) / 2) if exact else 0.0
+    corr = (H * P * 2 * (c - 1) / 2 + H * 4 * (c - 1) / 2 + 2 * G * 4 * (c + 1) / 2) if exact else 0.0
     return hot + read + flush / c + ring + corr + bytes_io()
 
 
