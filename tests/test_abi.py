@@ -255,6 +255,28 @@ def test_duplicate_slot_ids_are_refused_when_checked(monkeypatch):
     ops._check_unique(torch.tensor([3, 3], dtype=torch.int32), "V4Tier.step")
 
 
+def test_lagged_readout_argument_errors():
+    """nssm_v4_step_teacher_lagged checks its second snapshot before any device call: NULL
+    struct or buffers, the e4m3 kinds' scale, alignment; the tier's own checks come first."""
+    L = _lib.lib()
+    fake = 4096
+    prm = _lib.LayerParams(8, 80, 128, 1, fake, fake, fake, None, 0.0)
+    inp = _lib.StepInputs(4, fake, fake, fake, fake, None)
+    tier = _lib.Tier(4, 32, 4, _lib.COLD_FP32, *([fake] * 10))
+    e8 = _lib.Tier(4, 32, 4, _lib.COLD_FP8_BF16M, *([fake] * 10))
+    call = lambda t, lag: L.nssm_v4_step_teacher_lagged(  # noqa: E731
+        ctypes.byref(prm), ctypes.byref(t), lag, ctypes.byref(inp), fake, fake, 1 << 30, None)
+    assert call(tier, None) == -1
+    assert call(tier, ctypes.byref(_lib.Lag(None, None, fake))) == -1
+    assert call(tier, ctypes.byref(_lib.Lag(fake, None, None))) == -1
+    assert call(e8, ctypes.byref(_lib.Lag(fake, None, fake))) == -1  # e4m3 without row scales
+    assert call(tier, ctypes.byref(_lib.Lag(fake + 4, None, fake))) == -3
+    off = _lib.Tier(4, 32, 4, _lib.COLD_NONE, *([fake] * 10))
+    assert call(off, ctypes.byref(_lib.Lag(fake, None, fake))) == -4  # no cold tier to lag
+    bad = _lib.Tier(4, 48, 4, _lib.COLD_FP32, *([fake] * 10))
+    assert call(bad, ctypes.byref(_lib.Lag(fake, None, fake))) == -2
+
+
 def test_check_slots_argument_errors():
     """nssm_check_slots refuses NULL buffers, sizes out of range and a misaligned owner array
     before any device call."""
