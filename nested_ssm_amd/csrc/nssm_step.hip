@@ -42,7 +42,7 @@ constexpr int kMaxC = 64;
 constexpr int kFusedMaxWindow = 32;  // longest window the stream kernel replays itself
 constexpr int kMaxHG = 64;  // heads per group
 constexpr int kMaxUnitsPerWg = 4;  // waves (units) per stream workgroup
-constexpr int kMfmaTiles = 5;  // 16 x 16 flush-contraction tiles a wave keeps in registers
+constexpr int kMfmaTiles = 4;  // 16 x 16 flush-contraction tiles a wave keeps in registers
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2v __attribute__((ext_vector_type(2)));
@@ -249,10 +249,17 @@ __device__ __forceinline__ float head_scalars(float* __restrict__ hd, float draw
   return dt;
 }
 
+// A pair flag naming the request's slot and its heads' window length m (1 <= m <= kMaxC < 128):
+// positive, or -1 (the heads' scalars are read instead) for a slot past 2^24.
+__device__ __forceinline__ int flush_flag(int slot, int m) { return slot < (1 << 24) ? (slot << 7) | m : -1; }
+
 template <bool TIERED>
 __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
   __shared__ float sX[2 * kPrepReq][kN];  // B (j < kPrepReq) and C (j >= kPrepReq) of the block's requests
-  __shared__ int sSlot[kPrepReq], sTr[kPrepReq], sNvr[kPrepReq], sFl[kPrepReq];
+  __shared__ int sSlot[kPrepReq], sTr[kPrepReq], sNvr[kPrepReq];
+  // per request of the block: its flushing heads in group g, and the least and greatest
+  // window length among them (the pair flag, step 4)
+  __shared__ int sFl[kPrepReq], sFmx[kPrepReq], sFmn[kPrepReq];
   // exact readout and query gate: B', C' of the block; each request's cold energy
   // fraction; gated / kept head counts
   __shared__ float sRot[TIERED ? 2 * kPrepReq : 1][TIERED ? kN : 1];
@@ -330,7 +337,11 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
       for (int kb = 0; kb < kN / 16; ++kb)
         ra[t2][kb] = *reinterpret_cast<const f4*>(Rg + (size_t)((wave + 4 * t2) * 16 + li) * kN + kb * 16 + 4 * lk);
   }
-  if (tid < kPrepReq) sFl[tid] = 0;
+  if (tid < kPrepReq) {
+    sFl[tid] = 0;
+    sFmx[tid] = 0;
+    sFmn[tid] = kMaxC + 1;
+  }
   if (tid < 2) sQc[tid] = 0;
   const int hr = tid / HG, hh = tid - hr * HG;  // the head thread's request and head
   const bool head_thread = tid < nreq * HG;
@@ -601,7 +612,11 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
       hd[HD_SKIP] = skip ? 1.f : 0.f;
       hd[HD_FLUSH] = flush ? 1.f : 0.f;
       hd[HD_POS] = (float)pos;
-      if (flush) sFl[hr] = 1;
+      if (flush) {
+        atomicAdd(&sFl[hr], 1);
+        atomicMax(&sFmx[hr], nvv + 1);
+        atomicMin(&sFmn[hr], nvv + 1);
+      }
       if (flush && !a.fw) {
         // window = the nv buffered tokens at ring [pos-nv, pos) and this one (at a
         // flush pos = c-1): w_i = exp(sum_{l>i} a_l) dt_i, total decay exp(sum_l a_l).
@@ -648,12 +663,18 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
       hd[HD_POS] = 0.f;
     }
   }
-  // 4. the flush kernel's per-(request, group) flags: some head of the pair flushes
-  // (every pair of the block is written, so no flag survives from an earlier token)
+  // 4. the flush kernel's per-(request, group) flags (every pair of the block is written, so
+  // no flag survives from an earlier token): 0, no head of the pair flushes; otherwise
+  // flush_flag of the request's slot and window length when every head of the pair flushes
+  // a window of the same length (the flush kernel then lists the pair's heads without
+  // reading their scalars), else -1
   if constexpr (TIERED) {
     if (a.split || (gate && a.qcounts)) {
       __syncthreads();
-      if (a.split && tid < nreq) ws.fg[(size_t)(r0 + tid) * G + g] = sFl[tid];
+      if (a.split && tid < nreq) {
+        const int n = sFl[tid];
+        ws.fg[(size_t)(r0 + tid) * G + g] = n == 0 ? 0 : n == HG && sFmx[tid] == sFmn[tid] ? flush_flag(sSlot[tid], sFmx[tid]) : -1;
+      }
       if (gate && a.qcounts && tid == 0) {
         atomicAdd(a.qcounts, (unsigned long long)sQc[0]);
         atomicAdd(a.qcounts + 1, (unsigned long long)sQc[1]);
@@ -1821,6 +1842,12 @@ __device__ __forceinline__ void st_flush(T v, T* p) {
 template <int NC>
 __host__ __device__ constexpr int flush_swz_b() { return NC % 32 == 0 ? 4 : 0; }
 __host__ __device__ constexpr int flush_x_stride(int P) { return P + (P % 32 == 0 ? 16 : 0); }
+// Floats of one window buffer of fa tokens: [fa][NC] B', [fa][SX] x (bf16), [fa] weights,
+// C'[K:] of the readout, and two scalars of its item (A_h and the readout factor HD_SNAPF)
+// padded to 4.
+__host__ __device__ constexpr int flush_win_floats(int fa, int NC, int P) {
+  return fa * NC + fa * flush_x_stride(P) / 2 + fa + NC + 4;
+}
 
 // Stage window tokens [k0, k0 + kn) of one head into LDS with gfx950's LDS DMA
 // (global_load_lds: lane L of a wave instruction writes its granule at base + L * size,
@@ -1828,7 +1855,8 @@ __host__ __device__ constexpr int flush_x_stride(int P) { return P + (P % 32 == 
 // x_tok[p] as bf16, both in the bank layout above (tok = k0 + e),
 // sW[e] = w_tok, and sC[n] = C'[K + n] of this token
 // (the readout's coefficients, read after the contraction); given dtcur, sW[e] = dt_tok instead
-// (the caller forms the weights). Window token m - 1 is this
+// (the caller forms the weights); given sScal, sScal[0] = *scA, sScal[1] = *scE (the item's
+// scalars). Window token m - 1 is this
 // token (B' from the workspace, x from the inputs); token tok < m - 1 sits at ring
 // position c - m + tok (rb0 and rx0 point at the ring rows of window token 0). Wave w
 // issues the instructions w, w + nw, ... of each block; the caller waits (vmcnt) and
@@ -1838,7 +1866,11 @@ __device__ __forceinline__ void stage_window_dma(float* sB, uint16_t* sX, float*
                                                  int m, int P, const float* rb0, const float* bcur,
                                                  const uint16_t* rx0, const uint16_t* xcur, const float* wgt,
                                                  const float* cq, int wave, int lane, int nw, bool withB,
-                                                 const float* dtcur = nullptr) {
+                                                 const float* dtcur = nullptr, float* sScal = nullptr,
+                                                 const float* scA = nullptr, const float* scE = nullptr) {
+  // (the lane index opaque: each lane condition below is formed here, not hoisted by the
+  // caller's loops into a scalar lane mask held across them)
+  asm volatile("" : "+v"(lane));
   constexpr int NB4 = NC / 4;  // 16-byte granules per token of B'
   const int nb = withB ? kn * NB4 : 0;
   for (int q = wave; q * 64 < nb; q += nw) {
@@ -1877,6 +1909,8 @@ __device__ __forceinline__ void stage_window_dma(float* sB, uint16_t* sX, float*
                                      0, 0);
   if (withB && wave == wc && lane < NC / 4)
     __builtin_amdgcn_global_load_lds(NSSM_GLOBAL(cq + 4 * lane), NSSM_LOCAL(sC), 16, 0, 0);
+  if (sScal && wave == nw - 1 && lane < 2)
+    __builtin_amdgcn_global_load_lds(NSSM_GLOBAL(lane ? scE : scA), NSSM_LOCAL(sScal), 4, 0, 0);
 }
 
 // Workgroup barrier that publishes LDS only: the wave's global stores stay in flight
@@ -1886,6 +1920,59 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// The LDS byte address of a pointer into LDS.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// Two transposing LDS loads (ds_read_b64_tr_b16, 16-bit elements) at byte offset OFF from a0
+// and a1, and the wait for them, in one asm statement. Through the builtin the compiler waits
+// for every outstanding global load before the first such load (it does not tell them from
+// the LDS DMA of the other window buffer), so the state tiles and the next window could not
+// be in flight during the contraction. The window read here was published by a barrier
+// after its DMA had landed; the asm has side effects, so it stays after that barrier.
+template <int OFF>
+__device__ __forceinline__ void ds_read_tr16_pair_at(uint32_t a0, uint32_t a1, short4v& t0, short4v& t1) {
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %2 offset:%4\n\t"
+      "ds_read_b64_tr_b16 %1, %3 offset:%4\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(t0), "=&v"(t1)
+      : "v"(a0), "v"(a1), "i"(OFF));
+}
+// tile i of a row of 16-column tiles (32 bytes apart); i is a constant where it is unrolled
+__device__ __forceinline__ void ds_read_tr16_pair(uint32_t a0, uint32_t a1, int i, short4v& t0, short4v& t1) {
+  static_assert(kMfmaTiles <= 5, "one case per tile");
+  switch (i) {
+    case 0: ds_read_tr16_pair_at<0>(a0, a1, t0, t1); break;
+    case 1: ds_read_tr16_pair_at<32>(a0, a1, t0, t1); break;
+    case 2: ds_read_tr16_pair_at<64>(a0, a1, t0, t1); break;
+    case 3: ds_read_tr16_pair_at<96>(a0, a1, t0, t1); break;
+    default: ds_read_tr16_pair_at<128>(a0, a1, t0, t1); break;
+  }
+}
+
+// The flush kernel's static LDS: a list's items, their scalars and element offsets (formed
+// once per item by the thread that lists it, so the waves read them instead of each forming
+// them with scalar divisions and 64-bit products), and the ranking's scratch.
+struct FlushList {
+  int item[kFlushList], slot[kFlushList], m[kFlushList];  // m = 0: nothing to flush
+  int pair[kFlushList], head[kFlushList];                   // request * G + group, head
+  float dtot[kFlushList], eg[kFlushList];                   // (chunked windows) total decay, readout factor
+  long long orow[kFlushList];  // first state row: (slot H + head) P
+  long long ord[kFlushList];   // ring dt of window token 0: (slot H + head) c + c - m
+  long long orb[kFlushList];   // ring B' of window token 0: ((slot G + group) c + c - m) NC
+  int pairOf[kFlushList + 1];  // the pairs of a list's ranks
+  float dT[2];                 // total decay of each window buffer's item (fw)
+  int wave[kFlushWaves];
+};
+
+__device__ __forceinline__ long long rfl64(long long v) {
+  const int lo = __builtin_amdgcn_readfirstlane((int)(v & 0xffffffff));
+  const int hi = __builtin_amdgcn_readfirstlane((int)(v >> 32));
+  return (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
 }
 
 // Tokens a window buffer holds for a chunk of fch tokens: the contraction reads whole
@@ -1912,22 +1999,27 @@ flush_kernel(StepArgs a) {
   extern __shared__ float lds[];
   // this workgroup's listed items and their scalars (loaded by the thread that lists
   // the item); sM = 0 marks an item with nothing to flush
-  __shared__ int sItem[kFlushList], sSlot[kFlushList], sM[kFlushList];
-  __shared__ float sDtot[kFlushList], sEg[kFlushList], sAh[kFlushList];
-  __shared__ int sPairOf[kFlushList + 1];  // the pairs of a list's ranks
-  __shared__ float sDT[2];                 // total decay of each window buffer's item (fw)
-  __shared__ int sWave[kFlushWaves];
-  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int li = lane & 15, lk = lane >> 4;
+  __shared__ FlushList sL;
+  int(&sItem)[kFlushList] = sL.item;
+  int(&sSlot)[kFlushList] = sL.slot;
+  int(&sM)[kFlushList] = sL.m;
+  float(&sDtot)[kFlushList] = sL.dtot;
+  float(&sEg)[kFlushList] = sL.eg;
+  int(&sPairOf)[kFlushList + 1] = sL.pairOf;
+  float(&sDT)[2] = sL.dT;
+  int(&sWave)[kFlushWaves] = sL.wave;
+  int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  int li = lane & 15, lk = lane >> 4;
   const int H = a.H, P = a.P, c = a.c, G = a.G, HG = a.HG, fch = a.fch;
   const int fa = flush_alloc_tokens(fch);
   const Ws ws(a.ws, a.b, H, G, c);
-  // window buffer: [fa][NC] B', [fa][SX] x (bf16), [fa] weights, C'[K:]; two of them when
-  // the next item's window is staged during this one's contraction (then every window is
-  // whole, m <= c <= fch)
+  // window buffer (flush_win_floats): two of them when the next item's window is staged during
+  // this one's contraction (then every window is whole, m <= c <= fch)
   const bool pipe = a.fpipe != 0, fw = pipe && a.fw != 0;
   const int SX = flush_x_stride(P);
-  const int wfl = fa * NC + fa * SX / 2 + fa + NC;  // floats per window buffer
+  const int wfl = flush_win_floats(fa, NC, P);
+  auto scal = [&](int bf) { return lds + bf * wfl + fa * NC + fa * SX / 2 + fa + NC; };  // A_h, HD_SNAPF
   const int nbuf = pipe ? 2 : 1;
   float* sPart0 = lds + nbuf * wfl;        // [nbuf][P][NT] readout partials of the old read copy
   float* sAmx = sPart0 + nbuf * P * NT;    // [P][NT] row maxima of the new values (e4m3 only)
@@ -1993,8 +2085,7 @@ flush_kernel(StepArgs a) {
   auto load_tiles = [&](int kk, int u0) {
     int nt, pt0;
     const int npt = unit_of(u0, nt, pt0);
-    const int it2 = __builtin_amdgcn_readfirstlane(sItem[kk]);
-    const size_t row0 = ((size_t)__builtin_amdgcn_readfirstlane(sSlot[kk]) * H + it2 % H) * P;
+    const size_t row0 = (size_t)rfl64(sL.orow[kk]);
     const void* src = C::SEG ? static_cast<const void*>(a.cold) : static_cast<const void*>(a.master);
 #pragma unroll
     for (int i = 0; i < kMfmaTiles; ++i) {
@@ -2053,15 +2144,33 @@ flush_kernel(StepArgs a) {
       const int p = sPairOf[r - r_lo];
       const int bi = p / G, g = p - bi * G;
       const int it = bi * H + g * HG + hh;
-      const int slot = a.slot_ids ? a.slot_ids[bi] : bi;
+      // a positive flag carries the slot and the window length of every head of the pair
+      // (prep's flush_flag): no head scalar is read here
+      const int fl = ws.fg[p];
       const float* hd = ws.hd + (size_t)it * HD_STRIDE;
-      const bool ok = slot >= 0 && slot < a.slots && hd[HD_FLUSH] != 0.f;
+      int slot = fl >> 7, m = fl & 127;
+      bool ok = slot < a.slots;
+      if (fl <= 0) {
+        slot = a.slot_ids ? a.slot_ids[bi] : bi;
+        ok = slot >= 0 && slot < a.slots && hd[HD_FLUSH] != 0.f;
+        m = (int)hd[HD_M];
+      }
+      const int mc = ok ? min(max(m, 1), c) : 0, h = g * HG + hh;
       sItem[tid] = it;
       sSlot[tid] = slot;
-      sM[tid] = ok ? min(max((int)hd[HD_M], 1), c) : 0;
-      sDtot[tid] = hd[HD_DTOT];
-      sEg[tid] = hd[HD_SNAPF];
-      sAh[tid] = a.A[it - bi * H];
+      sM[tid] = mc;
+      sL.pair[tid] = p;
+      sL.head[tid] = h;
+      if (ok) {
+        const long long sh = (long long)slot * H + h;
+        sL.orow[tid] = sh * P;
+        sL.ord[tid] = sh * c + (c - mc);
+        sL.orb[tid] = (((long long)slot * G + g) * c + (c - mc)) * NC;
+      }
+      if (!pipe) {  // (whole windows stage these scalars with the window)
+        sDtot[tid] = hd[HD_DTOT];
+        sEg[tid] = hd[HD_SNAPF];
+      }
     }
     __syncthreads();
 
@@ -2070,21 +2179,19 @@ flush_kernel(StepArgs a) {
     // token i < m - 1 sits at ring position c - m + i.
     auto stage_item = [&](int kk, int bf) {
       const int m2 = __builtin_amdgcn_readfirstlane(sM[kk]), it2 = __builtin_amdgcn_readfirstlane(sItem[kk]);
-      const int sl2 = __builtin_amdgcn_readfirstlane(sSlot[kk]);
-      const int b2 = it2 / H, h2 = it2 - b2 * H, g2 = h2 / HG;
-      const int key = it2 / HG;
+      const int key = __builtin_amdgcn_readfirstlane(sL.pair[kk]), h2 = __builtin_amdgcn_readfirstlane(sL.head[kk]);
+      const size_t od = (size_t)rfl64(sL.ord[kk]);
       const bool withB = (bf ? bkey1 : bkey0) != key;  // a pair's heads share its B' window and C'
       if (bf) bkey1 = key;
       else bkey0 = key;
       float* wb = lds + bf * wfl;
       stage_window_dma<NC>(wb, reinterpret_cast<uint16_t*>(wb + fa * NC), wb + fa * NC + fa * SX / 2,
-                           wb + fa * NC + fa * SX / 2 + fa, 0, m2, m2, P,
-                           a.ring_b + (((size_t)sl2 * G + g2) * c + (c - m2)) * NC,
-                           ws.B + ((size_t)b2 * G + g2) * kN + K,
-                           a.ring_x + (((size_t)sl2 * H + h2) * c + (c - m2)) * P, a.x + (size_t)it2 * P,
-                           fw ? a.ring_dt + ((size_t)sl2 * H + h2) * c + (c - m2) : ws.w + (size_t)it2 * c,
-                           ws.C + ((size_t)b2 * G + g2) * kN + K, wave, lane, nw, withB,
-                           fw ? ws.hd + (size_t)it2 * HD_STRIDE + HD_DT : nullptr);
+                           wb + fa * NC + fa * SX / 2 + fa, 0, m2, m2, P, a.ring_b + (size_t)rfl64(sL.orb[kk]),
+                           ws.B + (size_t)key * kN + K, a.ring_x + od * P, a.x + (size_t)it2 * P,
+                           fw ? a.ring_dt + od : ws.w + (size_t)it2 * c, ws.C + (size_t)key * kN + K, wave, lane,
+                           nw, withB,
+                           fw ? ws.hd + (size_t)it2 * HD_STRIDE + HD_DT : nullptr, scal(bf), a.A + h2,
+                           ws.hd + (size_t)it2 * HD_STRIDE + HD_SNAPF);
     };
     // fw: the window weights of item kk in buffer bf from its staged dt (one wave, after
     // its own DMA of them has landed): a_i = dt_i A_h, w_i = exp(sum_{l>i} a_l) dt_i (a
@@ -2093,46 +2200,51 @@ flush_kernel(StepArgs a) {
     auto form_weights = [&](int kk, int bf) {
       float* sWb = lds + bf * wfl + fa * NC + fa * SX / 2;
       const int mm = sM[kk];
-      const float d = lane < mm ? sWb[lane] : 0.f;
-      float incl = d * sAh[kk];
+      int ln = lane;
+      asm volatile("" : "+v"(ln));  // (lane conditions formed here, not hoisted as lane masks)
+      const float d = ln < mm ? sWb[ln] : 0.f;
+      float incl = d * scal(bf)[0];
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
         const float v = __shfl_down(incl, o);
-        if (lane + o < 64) incl += v;
+        if (ln + o < 64) incl += v;
       }
       const float after = __shfl_down(incl, 1);  // sum over l > lane
-      if (lane < mm) sWb[lane] = expf(lane + 1 < mm ? after : 0.f) * d;
-      if (lane == 0) sDT[bf] = expf(incl);
+      if (ln < mm) sWb[ln] = expf(ln + 1 < mm ? after : 0.f) * d;
+      if (ln == 0) sDT[bf] = expf(incl);
     };
     auto next_item = [&](int kk) {  // the first listed item from kk on with a window
       while (kk < jn && sM[kk] == 0) ++kk;
       return kk;
     };
     int buf = 0;
-    if (pipe) {  // the first window (and state tiles), staged before the loop
+    float yv = 0.f;  // the item's y (hot part and D x, from the stream kernel)
+    if (pipe) {
+      // the first item's window, state tiles (its first pass) and y, in one round trip;
+      // then the second item's window, in flight during the first item's contraction
       const int k1 = next_item(0);
       if (k1 < jn) {
         stage_item(k1, 0);
+        load_tiles(k1, 0);
+        if (tid < P) yv = a.y[(size_t)sItem[k1] * P + tid];
         __builtin_amdgcn_s_waitcnt(0);
         if (fw && wave == nw - 1) form_weights(k1, 0);
         __syncthreads();
+        const int k2 = next_item(k1 + 1);
+        if (k2 < jn) stage_item(k2, 1);
       }
     }
     for (int k = next_item(0); k < jn; k = next_item(k + 1)) {
+      // the lane indices, opaque to the compiler from here on: per-lane conditions are formed
+      // where they are used instead of hoisted out of the item loop as 64-bit lane masks held
+      // in scalar registers for the whole loop (which spilled them)
+      asm volatile("" : "+v"(tid), "+v"(lane), "+v"(li), "+v"(lk));
       const int m = __builtin_amdgcn_readfirstlane(sM[k]);  // > 0; these are workgroup-uniform
-      const int it = __builtin_amdgcn_readfirstlane(sItem[k]), slot = __builtin_amdgcn_readfirstlane(sSlot[k]);
+      const int it = __builtin_amdgcn_readfirstlane(sItem[k]), pr = __builtin_amdgcn_readfirstlane(sL.pair[k]);
       const float dtot = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(fw ? sDT[buf] : sDtot[k])));
-      const float eg = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sEg[k])));
-      const int bi = it / H, h = it - bi * H, g = h / HG;
-      float yv = 0.f;  // this head's y (hot part and D x, from the stream kernel)
-      if (tid < P) yv = a.y[(size_t)it * P + tid];
-      const float* bcur = ws.B + ((size_t)bi * G + g) * kN + K;  // this token's B'[K:]
-      const float* cq0 = ws.C + ((size_t)bi * G + g) * kN + K;   // C'[K:]
-      const float* rb0 = a.ring_b + (((size_t)slot * G + g) * c + (c - m)) * NC;
-      const uint16_t* rx0 = a.ring_x + (((size_t)slot * H + h) * c + (c - m)) * P;
-      const uint16_t* xcur = a.x + (size_t)it * P;
-      const float* wgt = ws.w + (size_t)it * c;
-      const size_t row0 = ((size_t)slot * H + h) * P;
+      const float eg = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(pipe ? scal(buf)[1] : sEg[k])));
+      const size_t row0 = (size_t)rfl64(sL.orow[k]);
+      if (!pipe && tid < P) yv = a.y[(size_t)it * P + tid];
       float* sBc = lds + buf * wfl;
       uint16_t* sX = reinterpret_cast<uint16_t*>(sBc + fa * NC);
       float* sW = sBc + fa * NC + fa * SX / 2;
@@ -2140,17 +2252,14 @@ flush_kernel(StepArgs a) {
       float* sPart = sPart0 + buf * P * NT;
       const bool whole = m <= fch;  // the window fits in LDS: staged once
 
-      // the next item's window goes to the other buffer during this item's contraction (the
-      // previous item's last barrier ordered every wave's reads of that buffer before it)
-      if (pipe) {
-        const int knext = next_item(k + 1);
-        if (knext < jn) stage_item(knext, buf ^ 1);
-      }
-
-      for (int u0 = 0; u0 < nunit; u0 += UPP) {
+      // the passes (at least one: P >= 16), as a do-while so the compiler sees that the
+      // pass's wait below separates every prefetch of the state tiles from the next
+      int u0 = 0;
+      do {
         int nt, pt0;
         const int npt = unit_of(u0, nt, pt0);
-        load_tiles(k, u0);
+        asm volatile("" : "+v"(tid), "+v"(lane), "+v"(li), "+v"(lk));  // (as at the item's top)
+        if (!pipe || u0 > 0) load_tiles(k, u0);  // (whole windows: the first pass's were loaded before)
         f4 acc[kMfmaTiles];
 #pragma unroll
         for (int i = 0; i < kMfmaTiles; ++i) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
@@ -2195,14 +2304,16 @@ flush_kernel(StepArgs a) {
           // part by part across the tiles (independent accumulators back to back).
           int xo = (kg + (li >> 2)) * SX + 16 * pt0 + 4 * (li & 3);
           asm volatile("" : "+v"(xo));
+          const uint32_t xa0 = lds_addr(sX + xo), xa1 = lds_addr(sX + xo + 16 * SX);
 #pragma unroll
           for (int i = 0; i < kMfmaTiles; ++i) {
             if (i < ntiles) {  // wave-uniform
               u2v h2[2];
+              short4v tq[2];
+              ds_read_tr16_pair(xa0, xa1, i, tq[0], tq[1]);
 #pragma unroll
               for (int q = 0; q < 2; ++q) {
-                short4v t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (__attribute__((address_space(3))) short4v*)(sX + xo + 16 * q * SX + 16 * i));
+                short4v t = tq[q];
                 if constexpr (TAIL) {
 #pragma unroll
                   for (int r = 0; r < 4; ++r) t[r] = kg + 16 * q + r < kn ? t[r] : (short)0;
@@ -2221,9 +2332,12 @@ flush_kernel(StepArgs a) {
           if (!pipe && (!whole || u0 == 0)) {  // a whole window is staged once, in the first pass
             __syncthreads();  // the previous chunk (or item: window and partials) is consumed
             // whole windows keep the pair's B' and C' from its previous head
-            const bool withB = !whole || bkey0 != it / HG;
-            bkey0 = whole ? it / HG : -1;
-            stage_window_dma<NC>(sBc, sX, sW, sW + fa, k0, kn, m, P, rb0, bcur, rx0, xcur, wgt, cq0, wave, lane, nw,
+            const bool withB = !whole || bkey0 != pr;
+            bkey0 = whole ? pr : -1;
+            const size_t od = (size_t)rfl64(sL.ord[k]);
+            stage_window_dma<NC>(sBc, sX, sW, sW + fa, k0, kn, m, P, a.ring_b + (size_t)rfl64(sL.orb[k]),
+                                 ws.B + (size_t)pr * kN + K, a.ring_x + od * P, a.x + (size_t)it * P,
+                                 ws.w + (size_t)it * c, ws.C + (size_t)pr * kN + K, wave, lane, nw,
                                  withB);
             __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA has landed in LDS
             __syncthreads();
@@ -2371,7 +2485,8 @@ flush_kernel(StepArgs a) {
           // forced, written its partials
           lds_barrier();
         }
-      }
+        u0 += UPP;
+      } while (u0 < nunit);
       // y += exp(glog) (stale cold readout); the next item's first barrier (pipelined:
       // its last, before this buffer of partials is written again) orders these reads
       if (tid < P) {
@@ -2380,7 +2495,19 @@ flush_kernel(StepArgs a) {
         for (int t2 = 0; t2 < NT; ++t2) pc += sPart[tid * NT + t2];
         a.y[(size_t)it * P + tid] = fmaf(eg, pc, yv);
       }
-      if (pipe) buf ^= 1;
+      if (pipe) {
+        // every wave has passed this item's last barrier, so its reads of window buffer buf
+        // are done: the item after next is staged into it, and the next item's state tiles
+        // (first pass) and y are loaded, all in flight during the next item's contraction
+        const int kn1 = next_item(k + 1);
+        if (kn1 < jn) {
+          const int kn2 = next_item(kn1 + 1);
+          if (kn2 < jn) stage_item(kn2, buf);
+          load_tiles(kn1, 0);
+          if (tid < P) yv = a.y[(size_t)sItem[kn1] * P + tid];
+        }
+        buf ^= 1;
+      }
     }
   }
 }
@@ -2868,7 +2995,7 @@ size_t flush_lds_bytes(int P, int K, int kind, int fch, bool pipe = false) {
   const int NC = kN - K, fa = flush_alloc_tokens(fch);
   const size_t tiles = (size_t)P * (NC / 16);
   const bool e4m3 = kind == NSSM_COLD_FP8 || kind == NSSM_COLD_FP8_BF16M;  // + row maxima
-  const size_t buf = (size_t)fa * NC + (size_t)fa * flush_x_stride(P) / 2 + fa + NC + tiles;
+  const size_t buf = (size_t)flush_win_floats(fa, NC, P) + tiles;
   return ((pipe ? 2 : 1) * buf + (e4m3 ? tiles : 0)) * sizeof(float);
 }
 // LDS a flush workgroup may take: the device's per-workgroup limit, and a CU's LDS shared
@@ -2888,7 +3015,7 @@ size_t flush_lds_limit() {
 // whether two whole windows of c tokens fit (the flush kernel then stages each item's
 // window during the previous item's contraction)
 bool flush_pipe(int P, int K, int kind, int c) {
-  return flush_lds_bytes(P, K, kind, (c + 3) & ~3, true) + 2048 <= flush_lds_limit();
+  return flush_lds_bytes(P, K, kind, (c + 3) & ~3, true) + sizeof(FlushList) + 256 <= flush_lds_limit();
 }
 // a kernel launched with more than 64 KB of dynamic LDS declares it first (once per
 // kernel and device)
