@@ -42,7 +42,7 @@ constexpr int kMaxC = 64;
 constexpr int kFusedMaxWindow = 32;  // longest window the stream kernel replays itself
 constexpr int kMaxHG = 64;  // heads per group
 constexpr int kMaxUnitsPerWg = 4;  // waves (units) per stream workgroup
-constexpr int kMfmaTiles = 4;  // 16 x 16 flush-contraction tiles a wave keeps in registers
+constexpr int kMfmaTiles = 5;  // 16 x 16 flush-contraction tiles a wave keeps in registers
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2v __attribute__((ext_vector_type(2)));
@@ -1975,6 +1975,15 @@ __device__ __forceinline__ long long rfl64(long long v) {
   return (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
 }
 
+// The flush kernel's work units of an item: (n-tile, block of ptw consecutive p-tiles), the
+// blocks as many as fill the nw waves (at most kMfmaTiles p-tiles each); NT n-tiles, P / 16
+// p-tiles.
+__device__ __forceinline__ int flush_ptw(int P, int NT, int nw) {
+  const int PT = P / 16;
+  const int nblk0 = max((PT + kMfmaTiles - 1) / kMfmaTiles, min(PT, nw / NT));
+  return (PT + nblk0 - 1) / nblk0;
+}
+
 // Tokens a window buffer holds for a chunk of fch tokens: the contraction reads whole
 // 32-token steps (tokens past the chunk are read and dropped).
 __host__ __device__ constexpr int flush_alloc_tokens(int fch) { return (fch + 31) & ~31; }
@@ -2023,9 +2032,7 @@ flush_kernel(StepArgs a) {
   const int nbuf = pipe ? 2 : 1;
   float* sPart0 = lds + nbuf * wfl;        // [nbuf][P][NT] readout partials of the old read copy
   float* sAmx = sPart0 + nbuf * P * NT;    // [P][NT] row maxima of the new values (e4m3 only)
-  const int PT = P / 16;
-  const int nblk0 = max((PT + kMfmaTiles - 1) / kMfmaTiles, min(PT, nw / NT));
-  const int ptw = (PT + nblk0 - 1) / nblk0, nunit = NT * ((PT + ptw - 1) / ptw);
+  const int PT = P / 16, ptw = flush_ptw(P, NT, nw), nunit = NT * ((PT + ptw - 1) / ptw);
 
   // 1. rank the flagged pairs: thread tid counts pairs [p0, p1) (whole int4 words of
   // the flag array, which is padded to a multiple of 4), keeping the flags of its first 64
@@ -2252,8 +2259,8 @@ flush_kernel(StepArgs a) {
       float* sPart = sPart0 + buf * P * NT;
       const bool whole = m <= fch;  // the window fits in LDS: staged once
 
-      // the passes (at least one: P >= 16), as a do-while so the compiler sees that the
-      // pass's wait below separates every prefetch of the state tiles from the next
+      // the passes (at least one: P >= 16; one at the 9B shape), as a do-while so the compiler
+      // sees that the pass's wait below separates every prefetch of the state tiles from the next
       int u0 = 0;
       do {
         int nt, pt0;
