@@ -1750,8 +1750,10 @@ __global__ void __launch_bounds__(64) fresh_kernel(StepArgs a, const float* __re
 // accuracy of an fp32 contraction at a fraction of fp32 MFMA's issue time (per 64 tokens
 // and tile, fp32 16x16x4: 16 steps of 32 cycles; bf16 16x16x32: 2 steps x 3 parts of 16).
 // The window is staged in LDS by DMA fch tokens at a time (the whole window when it fits,
-// all its loads in flight together; with two whole windows in LDS, the next item's during
-// this item's contraction). A wave owns one n-tile and up to kMfmaTiles consecutive
+// all its loads in flight together; with two whole windows in LDS, the first item's window,
+// state tiles and y in one round trip, and after each item's last barrier the window of the
+// item after next and the next item's tiles and y, in flight during the next contraction).
+// A wave owns one n-tile and up to kMfmaTiles consecutive
 // p-tiles, so it builds the split A operand once per 32-token step for all of them (8
 // tokens of one cold column per lane, read from the staged B' and weights); the x operand
 // of each tile is two transposing LDS loads (ds_read_b64_tr_b16), and whole 32-token steps
@@ -1772,11 +1774,12 @@ __global__ void __launch_bounds__(64) fresh_kernel(StepArgs a, const float* __re
 // 661-681 with the transposing x loads, predicate-free steps and stores back to back,
 // 576-592 with plain state accesses (ld_flush / st_flush: WRITE_SIZE per full flush 1.25 ->
 // 1.00 GB; e4m3 over a bf16 master 931 -> 690 us, the bf16 read copy over an fp32 master
-// 1046 -> 819); the
-// ragged batch's per-token launch (B = 384, ~768 heads) 28.9 -> 29.3 us while prep drops
-// 19.9 -> 13.5 us without the window weights. Per-item phase timestamps (s_memrealtime)
-// put the contraction at about 1.3 us of a CU per item and the rest in load, store and
-// DMA issue stalls behind the memory pipe. Tried and slower: one wave per tile row (P / 16
+// 1046 -> 819); 555-590 with the pair flags carrying slot and window length, per-item
+// offsets listed once, the next item's tiles loaded early and no scratch (the ragged
+// batch's per-token launch, B = 384, ~768 heads: 27.5 -> 25.6 us). Shader-clock timestamps
+// in an instrumented copy put the contraction at about 2,000 cycles of an item and most of
+// the rest in the item's own instructions between its loads and the contraction, not in
+// waits on memory. Tried and slower: one wave per tile row (P / 16
 // waves per workgroup, 3 workgroups per CU, row scales and readouts reduced in the wave)
 // 1004 us; the window staged transposed and pre-split in LDS by the workgroup (three bf16
 // copies of w B', token-contiguous rows) 1239 us; six-wave workgroups (one per work unit)
