@@ -391,6 +391,37 @@ def bench_prologue(args, dev):
     return res
 
 
+def stream_probe(dev, achieved_gbs, gib=2, reps=10):
+    """The device's practical HBM rate in this run, beside the state op's: nssm_stream_probe's
+    plain streaming read of `gib` GiB and copy of `gib` / 2 GiB (read + write counted), each the
+    mean of `reps` launches timed with HIP events on the stream they run on. The 8 TB/s peak
+    stays the roofline's denominator; this says how much of the gap any streaming kernel keeps."""
+    from nested_ssm_amd._lib import check, lib
+
+    L = lib()
+    n = gib << 30
+    src = torch.zeros(n // 4, device=dev)
+    dst = torch.empty_like(src)
+    s = torch.cuda.current_stream()
+    out = {"kernel": "nssm_stream_probe (non-temporal 16-byte loads, 4096 workgroups)", "read_bytes": n}
+    for mode, key, nb in ((0, "read_gbs", n), (1, "copy_gbs", n // 2)):
+        for _ in range(3):
+            check(L.nssm_stream_probe(src.data_ptr(), dst.data_ptr(), nb, mode, s.cuda_stream), "nssm_stream_probe")
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(reps):
+            L.nssm_stream_probe(src.data_ptr(), dst.data_ptr(), nb, mode, s.cuda_stream)
+        e1.record(s)
+        e1.synchronize()
+        sec = e0.elapsed_time(e1) / reps * 1e-3
+        out[key] = round(nb * (2 if mode else 1) / sec / 1e9, 1)
+    out["copy_bytes_each_way"] = n // 2
+    out["state_op_achieved_over_read"] = round(achieved_gbs / out["read_gbs"], 4)
+    del src, dst
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_model() -> str:
     """The host CPU's model name (/proc/cpuinfo), as lscpu reports it."""
     try:
@@ -620,6 +651,11 @@ def main():
         out["deployment_points"] = deploy
     if prologue is not None:
         out["prologue_epilogue"] = prologue
+    if args.only is None:
+        log("stream probe ...")
+        out["stream_probe"] = stream_probe(dev, achieved)
+        log(f"stream probe: read {out['stream_probe']['read_gbs']:,.0f} GB/s, copy "
+            f"{out['stream_probe']['copy_gbs']:,.0f} GB/s (read + write)")
     if not args.no_cpu:
         log("cpu baseline ...")
         out["cpu_baseline"] = cpu_baseline(args, args.cpu_budget)

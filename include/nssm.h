@@ -36,6 +36,7 @@
  *   nssm_fp8_readout     scale/bench_v4_decode.py:33-60 (_fp8_matvec /
  *                        fp8_cold_readout)
  *   nssm_check_slots     none (device-side slot id check for callers that cannot sync)
+ *   nssm_stream_probe    none (a plain streaming read / copy, for HBM rate comparisons)
  *   nssm_rotate          scale/nemotron_retrofit.py:24-27 (ActRotMask._rot),
  *                        scale/vllm_v4_patch.py:41-45 (rot_flat)
  *   nssm_gated_rmsnorm   scale/v4_native_decode.py:170-171 (self.norm(y, gate):
@@ -55,7 +56,7 @@
 extern "C" {
 #endif
 
-#define NSSM_ABI_VERSION 14
+#define NSSM_ABI_VERSION 15
 
 /* error codes */
 #define NSSM_OK 0
@@ -331,6 +332,13 @@ int nssm_conv_update(int32_t b, int32_t dim, int32_t width, int32_t dtype, const
 int nssm_gated_rmsnorm(int32_t b, int32_t I, int32_t gs, int32_t dtype, const float* y,
                        const void* gate, int64_t gate_stride, const void* weight, float eps,
                        void* out, void* stream);
+
+/* Measurement aid, no counterpart in the reference: one launch of a plain streaming
+ * kernel over `bytes` of device memory on `stream`, the HBM rate the state op is
+ * compared with on the same device. mode 0 reads src (dst: 16 writable bytes, written
+ * only when the sum of what was read is +inf); mode 1 copies src to dst. src and dst 16-byte
+ * aligned (NSSM_E_ALIGN); bytes a positive multiple of 16384 (NSSM_E_DIMS). */
+int nssm_stream_probe(const void* src, void* dst, int64_t bytes, int32_t mode, void* stream);
 
 /* Launch-shape override for the stream kernel (0 = automatic): units (waves, each
  * streaming 8 headdim rows of one head) per workgroup, at most 4; a step returns

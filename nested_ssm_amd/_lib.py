@@ -84,6 +84,7 @@ def lib():
     L.nssm_conv_update.argtypes = [c_i32, c_i32, c_i32, c_i32, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32,
                                    c_vp, c_vp, c_vp, c_vp]
     L.nssm_set_launch.argtypes = [c_i32]
+    L.nssm_stream_probe.argtypes = [c_vp, c_vp, c_i64, c_i32, c_vp]
     L.nssm_host_f32_to_e4m3fn.argtypes = [c_vp, c_vp, ctypes.c_int64]
     L.nssm_host_e4m3fn_to_f32.argtypes = [c_vp, c_vp, ctypes.c_int64]
     L.nssm_host_f32_to_bf16.argtypes = [c_vp, c_vp, ctypes.c_int64]
@@ -92,7 +93,7 @@ def lib():
                "nssm_v4_join",
                "nssm_v4_materialize",
                "nssm_fp8_readout", "nssm_rotate", "nssm_conv_update", "nssm_gated_rmsnorm", "nssm_set_launch",
-               "nssm_tier_sizes", "nssm_check_slots"):
+               "nssm_stream_probe", "nssm_tier_sizes", "nssm_check_slots"):
         getattr(L, fn).restype = ctypes.c_int
     for fn in ("nssm_host_f32_to_e4m3fn", "nssm_host_e4m3fn_to_f32", "nssm_host_f32_to_bf16"):
         getattr(L, fn).restype = None
@@ -112,6 +113,6 @@ EXPORTED = ("nssm_tier_sizes", "nssm_step_workspace_bytes", "nssm_fresh_step", "
             "nssm_v4_step_gated", "nssm_v4_join",
             "nssm_v4_materialize", "nssm_fp8_readout", "nssm_rotate", "nssm_conv_update", "nssm_gated_rmsnorm",
             "nssm_check_slots",
-            "nssm_set_launch",
+            "nssm_set_launch", "nssm_stream_probe",
             "nssm_host_f32_to_e4m3fn", "nssm_host_e4m3fn_to_f32", "nssm_host_f32_to_bf16",
             "nssm_strerror", "nssm_abi_version")

@@ -307,3 +307,17 @@ def test_noalloc_step_refuses_calls_beyond_its_scratch():
     assert L.nssm_v4_step_noalloc(None, ctypes.byref(tier), ctypes.byref(big), fake, None) == -1
     bad = _lib.Tier(4096, 48, 4, _lib.COLD_FP32, *([fake] * 10))
     assert L.nssm_v4_step_noalloc(ctypes.byref(prm), ctypes.byref(bad), ctypes.byref(big), fake, None) == -2
+
+
+def test_stream_probe_argument_errors():
+    """nssm_stream_probe refuses NULL buffers, sizes that are not whole 16 KiB chunks, an
+    unknown mode and misaligned buffers before any device call."""
+    L = _lib.lib()
+    fake, chunk = 4096, 16384
+    assert L.nssm_stream_probe(None, fake, chunk, 0, None) == -1
+    assert L.nssm_stream_probe(fake, None, chunk, 1, None) == -1
+    assert L.nssm_stream_probe(fake, fake, 0, 0, None) == -2
+    assert L.nssm_stream_probe(fake, fake, chunk + 16, 0, None) == -2
+    assert L.nssm_stream_probe(fake, fake, chunk, 2, None) == -2
+    assert L.nssm_stream_probe(fake + 4, fake, chunk, 0, None) == -3
+    assert L.nssm_stream_probe(fake, fake + 8, chunk, 1, None) == -3
