@@ -471,6 +471,85 @@ def cpu_baseline(args, budget_s):
     }
 
 
+TRAFFIC_COPY_BYTES = 256 << 20  # the calibration copy of a traffic pass
+# per-dispatch counter rows of the launches of one layer-token (join and materialize are
+# outside the timed steps and left out)
+TRAFFIC_KERNELS = {"v4": ("prep_kernel<", "unit_kernel", "flush_kernel<"), "fresh": ("prep_kernel<", "fresh_kernel(")}
+
+
+def workload_argv(args):
+    """bench.py flags that rebuild this workload (for a child pass)."""
+    av = ["--B", str(args.B), "--k", str(args.k), "--c", str(args.c), "--cold", args.cold, "--master", args.master,
+          "--seed", str(args.seed), "--qgate", repr(args.qgate)]
+    return av + [f for f, on in (("--exact", args.exact), ("--coldoff", args.coldoff), ("--ragged", args.ragged))
+                 if on]
+
+
+def traffic_pass(args, head, dev):
+    """The child side of live_traffic: 2 layers of the workload over whole flush windows
+    (at least 8 tokens, then bench_v4's per-launch pass of one more window), then one
+    nssm_stream_probe copy of TRAFFIC_COPY_BYTES for the counters' scale."""
+    from nested_ssm_amd._lib import check, lib
+
+    args.layers, args.warmup, args.graph = 2, 0, False
+    args.steps = ((8 + args.c - 1) // args.c) * args.c
+    layers = make_layers(args.layers, dev, args.seed)
+    inputs = make_inputs(args.layers, args.B, dev, args.seed + 7)
+    (bench_v4 if head == "v4" else bench_fresh)(args, layers, inputs, dev)
+    src = torch.zeros(TRAFFIC_COPY_BYTES // 4, device=dev)
+    dst = torch.empty_like(src)
+    check(lib().nssm_stream_probe(src.data_ptr(), dst.data_ptr(), TRAFFIC_COPY_BYTES, 1,
+                                  torch.cuda.current_stream().cuda_stream), "nssm_stream_probe")
+    torch.cuda.synchronize()
+
+
+def live_traffic(args, head):
+    """HBM bytes per layer-token of this workload, measured in this run: two child passes of
+    `bench.py --traffic-pass` under `rocprofv3 --pmc FETCH_SIZE`, then `--pmc WRITE_SIZE`
+    (one counter block per pass), each counter scaled by what it reads for the pass's copy
+    of known size. Returns (bytes, None) or (None, the reason it could not be measured)."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+
+    prof = shutil.which("rocprofv3") or ("/opt/rocm/bin/rocprofv3" if os.path.exists("/opt/rocm/bin/rocprofv3")
+                                         else None)
+    if prof is None:
+        return None, "rocprofv3 not found"
+    env = dict(os.environ, TMPDIR=os.environ.get("TMPDIR", "/tmp"))
+    total = 0.0
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = tempfile.mkdtemp(prefix="nssm_pmc_")
+        cmd = ["timeout", "-s", "KILL", "150", prof, "--pmc", ctr, "-f", "csv", "-d", d, "-o", "pmc", "--",
+               sys.executable, os.path.join(ROOT, "bench.py"), "--traffic-pass", "--only", head] + workload_argv(args)
+        try:
+            r = subprocess.run(cmd, capture_output=True, text=True, timeout=180, env=env)
+            rows = []
+            for root, _, files in os.walk(d):
+                for f in files:
+                    if f.endswith("counter_collection.csv"):
+                        rows += [x for x in csv.DictReader(open(os.path.join(root, f))) if x["Counter_Name"] == ctr]
+        except (OSError, subprocess.SubprocessError) as e:
+            return None, f"{ctr} pass: {e}"
+        finally:
+            shutil.rmtree(d, ignore_errors=True)
+        if r.returncode != 0 or not rows:
+            return None, f"{ctr} pass exited {r.returncode} with {len(rows)} counter rows"
+        per = {}
+        for x in rows:
+            per.setdefault(x["Kernel_Name"], []).append(float(x["Counter_Value"]))
+        copy = [v for k, vs in per.items() if "stream_probe_kernel<true>" in k for v in vs]
+        if not copy or copy[0] <= 0:
+            return None, f"{ctr} pass: no calibration copy"
+        scale = TRAFFIC_COPY_BYTES / copy[0]  # bytes per counter unit
+        found = [k for k in per if any(s in k for s in TRAFFIC_KERNELS[head])]
+        if not any("prep_kernel<" in k for k in found) or len(found) < 2:
+            return None, f"{ctr} pass: kernels of the workload missing"
+        total += sum(sum(per[k]) / len(per[k]) * scale for k in found)
+    return int(round(total)), None
+
+
 def measured_traffic(key):
     """HBM bytes per layer-token measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
     (calibrated against a plain copy) in an earlier profiled run of this workload and
@@ -526,6 +605,10 @@ def main():
                     help="profile one path only (prologue: the conv prologue and epilogue norm)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (5 times), for scaling HBM counters")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the rocprofv3 counter passes that measure the headline's HBM traffic")
+    ap.add_argument("--traffic-pass", action="store_true",
+                    help="(internal) the workload of one counter pass: 2 layers, whole windows, and a copy")
     args = ap.parse_args()
     if args.cold == "fp32":
         args.master = "fp32"  # fp32 cold is its own master
@@ -541,6 +624,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_per_dispatch_each_way": n * 4, "dispatches": 5}), flush=True)
+        return
+
+    if args.traffic_pass:
+        traffic_pass(args, args.only or "v4", "cuda")
         return
 
     if args.gpus != 1:
@@ -601,6 +688,20 @@ def main():
     achieved = per_launch_bytes / (ms_ev * 1e-3) / 1e9
     readout = readout_name(args)
     traffic, traffic_src = measured_traffic(traffic_key(args, head))
+    traffic_src = (f"{traffic_src}: rocprofv3 FETCH_SIZE + WRITE_SIZE of an earlier profiled run of this workload, "
+                   f"scaled against a plain copy" if traffic_src else None)
+    live_err = None
+    under_profiler = any(k.startswith("ROCPROFILER") for k in os.environ)
+    if args.only is None and not args.no_traffic and not under_profiler:
+        log("traffic passes (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE) ...")
+        live, live_err = live_traffic(args, head)
+        if live is not None:
+            traffic, traffic_src = live, (
+                "measured in this run: rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, over 2 layers of this "
+                "workload (whole windows), each scaled by its reading for a copy of 256 MiB in the same pass")
+            log(f"traffic: {traffic:,} B per layer-token ({traffic / per_launch_bytes:.3f} of the algorithmic)")
+        else:
+            log(f"traffic passes failed ({live_err}); the profiled figure is reported")
     out = {
         "metric": "state-op tokens/s at 9B shape B=256 (v4-c4 vs fresh); achieved HBM GB/s vs peak",
         "value": round(args.B / ms_step * 1e3, 1),
@@ -633,8 +734,9 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": traffic,
-            "traffic_source": (f"{traffic_src}: rocprofv3 FETCH_SIZE + WRITE_SIZE of an earlier profiled run of "
-                               f"this workload, scaled against a plain copy" if traffic_src else None),
+            "traffic_source": traffic_src,
+            **({"traffic_over_algorithmic": round(traffic / per_launch_bytes, 4)} if traffic else {}),
+            **({"traffic_live_error": live_err} if live_err else {}),
             "kernel": kernel_label(head, args),
             "algorithmic_bytes_per_launch": int(per_launch_bytes),
             "avg_launch_us_events": round(ms_ev * 1e3, 2),
