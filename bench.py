@@ -191,11 +191,13 @@ def bench_fresh(args, layers, inputs, dev):
 
 def bench_v4(args, layers, inputs, dev):
     from nested_ssm_amd import V4Tier
+    from nested_ssm_amd.ops import x_ring_for
 
     g = torch.Generator(device=dev).manual_seed(args.seed + 1)
     tiers, ys = [], []
     for l in range(args.layers):
-        t = V4Tier(args.B, H, P, G, k_hot=args.k, c=args.c, cold=args.cold, device=dev, master=args.master)
+        t = V4Tier(args.B, H, P, G, k_hot=args.k, c=args.c, cold=args.cold, device=dev, master=args.master,
+                   x_ring=x_ring_for(args.c, args.exact))
         S0 = rand_state(args.B, dev, g)
         phase = (torch.randint(0, args.c, (args.B,), device=dev, generator=g, dtype=torch.int32)
                  if args.ragged else None)

@@ -56,7 +56,7 @@
 extern "C" {
 #endif
 
-#define NSSM_ABI_VERSION 15
+#define NSSM_ABI_VERSION 16
 
 /* error codes */
 #define NSSM_OK 0
@@ -71,6 +71,14 @@ extern "C" {
 
 /* Size of the library's fixed per-device scratch array (nssm_v4_step_noalloc). */
 #define NSSM_SCRATCH_BYTES (32u << 20)
+
+/* x ring layouts (nssm_tier.x_layout). Row-major: a token's append is one run per head,
+ * the layout of the stale readouts. Unit-blocked: the exact readout's per-token window reads
+ * are one run per unit, at the cost of appends that write 16 bytes into each unit's line
+ * (9B shape, c = 64: exact readout 9.06 -> 8.90 ms per step; stale c = 4 8.48 -> 8.69). Every
+ * entry point serves both. */
+#define NSSM_XRING_ROW 0
+#define NSSM_XRING_UNIT 1
 
 /* model dtypes of the conv prologue's tensors */
 #define NSSM_DT_F32 0
@@ -125,7 +133,9 @@ typedef struct nssm_step_inputs {
  *   scale    fp32 [slots][H][P]         (FP8 and FP8_BF16M, else NULL)
  *   master   [slots][H][P][NC]          fp32 for BF16 / FP8, bf16 for FP8_BF16M
  *                                       (unit-blocked, below), else NULL
- *   ring_x   bf16 [slots][H][c][P]      x of buffered tokens
+ *   ring_x   bf16 [slots][H][c][P]      x of buffered tokens (x_layout NSSM_XRING_ROW), or
+ *            [slots][H][P/8][c][8]      unit-blocked (NSSM_XRING_UNIT: a unit's 8 rows at
+ *                                       its c ring positions are one contiguous run)
  *   ring_dt  fp32 [slots][H][c]         softplus'd dt of buffered tokens
  *   ring_b   fp32 [slots][G][c][NC]     rotated B cold columns of buffered tokens
  *   t        int32 [slots][H]           decode steps (phase = t % c)
@@ -152,6 +162,7 @@ typedef struct nssm_tier {
   int32_t* t;
   int32_t* nv;
   float* glog;
+  int32_t x_layout; /* NSSM_XRING_ROW or NSSM_XRING_UNIT (NSSM_E_KIND otherwise) */
 } nssm_tier;
 
 /* Byte size of each tier buffer, in the struct's order (hot, cold, scale,

@@ -15,6 +15,8 @@ COLD_KINDS = {"fp32": COLD_FP32, "bf16": COLD_BF16, "fp8": COLD_FP8, "off": COLD
 STORAGE_KINDS = {("fp32", "fp32"): COLD_FP32, ("bf16", "fp32"): COLD_BF16, ("fp8", "fp32"): COLD_FP8,
                  ("bf16", "bf16"): COLD_BF16_SINGLE, ("fp8", "bf16"): COLD_FP8_BF16M}
 DT_F32, DT_BF16 = 0, 1  # model dtypes of nssm_conv_update (NSSM_DT_*)
+XRING_ROW, XRING_UNIT = 0, 1  # x ring layouts (NSSM_XRING_*)
+XRING_LAYOUTS = {"row": XRING_ROW, "unit": XRING_UNIT}
 
 TIER_FIELDS = ("hot", "cold", "scale", "master", "ring_x", "ring_dt", "ring_b", "t", "nv", "glog")
 
@@ -35,7 +37,7 @@ class StepInputs(ctypes.Structure):
 
 class Tier(ctypes.Structure):
     _fields_ = [("slots", c_i32), ("k_hot", c_i32), ("c", c_i32), ("cold_kind", c_i32)] + \
-               [(f, c_vp) for f in TIER_FIELDS]
+               [(f, c_vp) for f in TIER_FIELDS] + [("x_layout", c_i32)]
 
 
 class Lag(ctypes.Structure):

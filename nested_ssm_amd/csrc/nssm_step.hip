@@ -76,6 +76,10 @@ struct StepArgs {
   float* y;
   float* ws;  // workspace (see Ws below)
   int32_t b, slots, H, P, G, HG, c, K;
+  // x ring layout (NSSM_XRING_*): element (slot H + head, position pos, headdim row p) sits at
+  // (slot H + head) c P + pos xs_tok + (p / 8) xs_unit + p % 8, so the 8 rows of a unit at
+  // one position are one 16-byte granule in either layout
+  int32_t xs_tok, xs_unit;
   int32_t prb;    // requests per prep workgroup
   int32_t exact;  // rank-c exact correction readout instead of the stale one
   int32_t tf;     // teacher-forced readout: inclusive decay; a flushing head reads its new state
@@ -210,6 +214,12 @@ __host__ __device__ constexpr size_t blk16(size_t row, int col, int NC) {
          (row & 7) * (size_t)(NC - (col & ~31) < 32 ? NC - (col & ~31) : 32) + (size_t)(col & 31);
 }
 constexpr int kBlkSeg = 64;  // u2v (4 bf16) between consecutive segments of a blocked row
+// Offset of x ring element (sh = slot H + head, ring position pos, headdim row p), in the
+// call's layout (StepArgs::xs_tok, xs_unit); rows p & ~7 .. p | 7 are contiguous.
+__device__ __forceinline__ size_t xring(const StepArgs& a, size_t sh, int pos, int p) {
+  return sh * (size_t)a.c * (size_t)a.P + (size_t)pos * (size_t)a.xs_tok + (size_t)(p >> 3) * (size_t)a.xs_unit +
+         (size_t)(p & 7);
+}
 
 // ---------------------------------------------------------------------------
 // prep: one workgroup (256 threads) per (group g, block of prb <= kPrepReq requests).
@@ -1067,11 +1077,11 @@ struct CorrRaw {
 };
 __device__ __forceinline__ void corr_load(const StepArgs& a, const float* __restrict__ hd, size_t sh, size_t rh,
                                           int p, int q, CorrRaw& cr) {
-  const int m = (int)hd[HD_M], P = a.P, c = a.c, lane = ((p & 7) << 3) | q;
+  const int m = (int)hd[HD_M], c = a.c, lane = ((p & 7) << 3) | q;
   const int H = a.H, h = (int)(rh % H);
   // window token j sits at ring position pos - (m - 1) + j
   const int j0 = (int)hd[HD_POS] - (m - 1);
-  const uint16_t* rx = a.ring_x + (sh * c + (j0 + lane)) * P + (p & ~7);
+  const uint16_t* rx = a.ring_x + xring(a, sh, j0 + lane, p & ~7);
   const float* sw = Ws(a.ws, a.b, H, a.G, c).s + ((rh / H) * a.G + h / a.HG) * c;
   cr.s = lane < m ? sw[lane] : 0.f;
   cr.dt = lane < m - 1 ? a.ring_dt[sh * c + (j0 + lane)] : lane == m - 1 ? hd[HD_DT] : 0.f;
@@ -1135,7 +1145,7 @@ __device__ __forceinline__ void unit_compute(const StepArgs& a, size_t sh, size_
   part = sum8(part);
   if (q == 0) {
     a.y[yrow] = fmaf(hd[HD_D], d.xp, part);
-    if (rx) rx[p] = d.xraw;  // ring append of x (tokens that do not flush)
+    if (rx) rx[p & 7] = d.xraw;  // ring append of x (tokens that do not flush; rx: the unit's granule)
   }
 }
 
@@ -1452,9 +1462,10 @@ __device__ __forceinline__ void unit_compute_flush(const StepArgs& a, size_t sh,
 // Window of one head for the rows [p0, p0 + nr) of a unit workgroup, in LDS:
 // sB[i][n] = B'_i[K + n] (the group's cold columns) and sU[i][r] = w_i x_i[p0 + r]; window
 // token m - 1 is this token (B' from the workspace, x from the inputs), token i < m - 1 sits
-// at ring position c - m + i (rb0 and rx0 point at the ring rows of window token 0).
+// at ring position c - m + i (rb0 points at the B' ring row of window token 0, rx0 at the x
+// ring element of window token 0, row 0; xs_tok, xs_unit: the x ring's strides).
 template <int NC>
-__device__ __forceinline__ void stage_unit_window(float* sB, float* sU, int m, int P, int p0, int nr,
+__device__ __forceinline__ void stage_unit_window(float* sB, float* sU, int m, int xs_tok, int xs_unit, int p0, int nr,
                                                   const float* rb0, const float* bcur, const uint16_t* rx0,
                                                   const uint16_t* xcur, const float* wgt, int tid, int nthr) {
   constexpr int NB4 = NC / 4;
@@ -1465,7 +1476,7 @@ __device__ __forceinline__ void stage_unit_window(float* sB, float* sU, int m, i
   }
   for (int i = tid; i < m * nr; i += nthr) {
     const int e = i / nr, r = i - e * nr;
-    const uint16_t xs = e < m - 1 ? rx0[(size_t)e * P + p0 + r] : xcur[p0 + r];
+    const uint16_t xs = e < m - 1 ? rx0[(size_t)e * xs_tok + ((p0 + r) >> 3) * xs_unit + ((p0 + r) & 7)] : xcur[p0 + r];
     sU[i] = wgt[e] * bf2f(xs);
   }
 }
@@ -1479,7 +1490,7 @@ __device__ __forceinline__ void unit_hot_only(const StepArgs& a, const float* __
   unit_load<K, COLD>(a, sh * a.P + p, rh * a.P + p, q, d, true);
   Coef<K, COLD> k;
   coef_load<K, COLD>(ws.B + pair * kN, ws.C + pair * kN, q, k);
-  uint16_t* rx = a.ring_x + (sh * a.c + (int)hd[HD_POS]) * a.P;
+  uint16_t* rx = a.ring_x + xring(a, sh, (int)hd[HD_POS], p & ~7);
   unit_compute<K, COLD, false>(a, sh, rh, p, q, d, rx, false, hd, k);
 }
 
@@ -1573,9 +1584,9 @@ __device__ __forceinline__ void unit_body(const StepArgs& a, const float* __rest
         MasterRaw<K, COLD> mr;
         constexpr bool kEarly = kMaster;
         if constexpr (kEarly) master_load<K, COLD>(a, row, q, mr);
-        stage_unit_window<NC>(sBc, sU, m, P, p0, nr, a.ring_b + (((size_t)slot * a.G + g) * c + (c - m)) * NC,
-                              wB + K, a.ring_x + (sh * c + (c - m)) * P, a.x + rh * P, ws.w + rh * c, tid,
-                              blockDim.x);
+        stage_unit_window<NC>(sBc, sU, m, a.xs_tok, a.xs_unit, p0, nr,
+                              a.ring_b + (((size_t)slot * a.G + g) * c + (c - m)) * NC, wB + K,
+                              a.ring_x + xring(a, sh, c - m, 0), a.x + rh * P, ws.w + rh * c, tid, blockDim.x);
         // the stale readout of the requantized master takes C' in the segment mapping
         if constexpr (kMaster && !TF && C::CONTIG) coef_cold_seg<K, COLD>(wC, q, k);
         __syncthreads();
@@ -1596,7 +1607,7 @@ __device__ __forceinline__ void unit_body(const StepArgs& a, const float* __rest
     coef_load<K, COLD, C::SEGREAD>(wB, wC, q, k);
     uint16_t* rx = nullptr;
     if constexpr (TIERED) {
-      if (!flushing) rx = a.ring_x + (sh * c + (int)hd[HD_POS]) * P;
+      if (!flushing) rx = a.ring_x + xring(a, sh, (int)hd[HD_POS], p & ~7);
     }
     if constexpr (kCorrPre)
       unit_compute<K, COLD, EXACT, true>(a, sh, rh, p, q, d, rx, !flushing, hd, k, &cr);
@@ -1628,9 +1639,9 @@ __device__ __forceinline__ void unit_body(const StepArgs& a, const float* __rest
         MasterRaw<K, COLD> mr;
         constexpr bool kEarly = kMaster;
         if constexpr (kEarly) master_load<K, COLD>(a, row, q, mr);
-        stage_unit_window<NC>(sBc, sU, m, P, p0, nr, a.ring_b + (((size_t)slot * a.G + g) * c + (c - m)) * NC,
-                              wB + K, a.ring_x + (sh * c + (c - m)) * P, a.x + rh * P, ws.w + rh * c, tid,
-                              blockDim.x);
+        stage_unit_window<NC>(sBc, sU, m, a.xs_tok, a.xs_unit, p0, nr,
+                              a.ring_b + (((size_t)slot * a.G + g) * c + (c - m)) * NC, wB + K,
+                              a.ring_x + xring(a, sh, c - m, 0), a.x + rh * P, ws.w + rh * c, tid, blockDim.x);
         if constexpr (kMaster && !TF && C::CONTIG) coef_cold_seg<K, COLD>(wC, q, k);
         __syncthreads();
         if constexpr (LAG) lag_store<K, COLD>(a, row, q, d);
@@ -1641,7 +1652,7 @@ __device__ __forceinline__ void unit_body(const StepArgs& a, const float* __rest
     }
     uint16_t* rx = nullptr;
     if constexpr (TIERED) {
-      if (!flushing) rx = a.ring_x + (sh * c + (int)hd[HD_POS]) * P;
+      if (!flushing) rx = a.ring_x + xring(a, sh, (int)hd[HD_POS], p & ~7);
     }
     if constexpr (kCorrPre)
       unit_compute<K, COLD, EXACT, true>(a, sh, rh, p, q, d, rx, !flushing, hd, k, &cr);
@@ -1861,13 +1872,15 @@ __host__ __device__ constexpr int flush_win_floats(int fa, int NC, int P) {
 // (the caller forms the weights); given sScal, sScal[0] = *scA, sScal[1] = *scE (the item's
 // scalars). Window token m - 1 is this
 // token (B' from the workspace, x from the inputs); token tok < m - 1 sits at ring
-// position c - m + tok (rb0 and rx0 point at the ring rows of window token 0). Wave w
+// position c - m + tok (rb0 points at the B' ring row of window token 0, rx0 at the x ring
+// granule of window token 0, rows 0 .. 7; xs_tok, xs_unit: the x ring's strides). Wave w
 // issues the instructions w, w + nw, ... of each block; the caller waits (vmcnt) and
 // barriers. withB = false leaves B' and C' as they are (the buffer holds this pair's).
 template <int NC>
 __device__ __forceinline__ void stage_window_dma(float* sB, uint16_t* sX, float* sW, float* sC, int k0, int kn,
                                                  int m, int P, const float* rb0, const float* bcur,
-                                                 const uint16_t* rx0, const uint16_t* xcur, const float* wgt,
+                                                 const uint16_t* rx0, int xs_tok, int xs_unit,
+                                                 const uint16_t* xcur, const float* wgt,
                                                  const float* cq, int wave, int lane, int nw, bool withB,
                                                  const float* dtcur = nullptr, float* sScal = nullptr,
                                                  const float* scA = nullptr, const float* scE = nullptr) {
@@ -1894,8 +1907,9 @@ __device__ __forceinline__ void stage_window_dma(float* sB, uint16_t* sX, float*
     const int gi = q * 64 + lane;
     if (gi < nxr) {
       const int e = gi / S8, gr = gi - e * S8;
-      __builtin_amdgcn_global_load_lds(NSSM_GLOBAL(rx0 + (size_t)(k0 + e) * P + (gr < P8 ? 8 * gr : 0)),
-                                       NSSM_LOCAL(sX + q * 512), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(
+          NSSM_GLOBAL(rx0 + (size_t)(k0 + e) * xs_tok + (size_t)(gr < P8 ? gr : 0) * xs_unit), NSSM_LOCAL(sX + q * 512),
+          16, 0, 0);
     }
   }
   const int wx = nw >= 3 ? nw - 3 : 0, wc = nw >= 2 ? nw - 2 : 0;  // the waves of this token's x and of C'
@@ -2197,7 +2211,9 @@ flush_kernel(StepArgs a) {
       float* wb = lds + bf * wfl;
       stage_window_dma<NC>(wb, reinterpret_cast<uint16_t*>(wb + fa * NC), wb + fa * NC + fa * SX / 2,
                            wb + fa * NC + fa * SX / 2 + fa, 0, m2, m2, P, a.ring_b + (size_t)rfl64(sL.orb[kk]),
-                           ws.B + (size_t)key * kN + K, a.ring_x + od * P, a.x + (size_t)it2 * P,
+                           ws.B + (size_t)key * kN + K,
+                           a.ring_x + (size_t)rfl64(sL.orow[kk]) * c + (size_t)(c - m2) * a.xs_tok, a.xs_tok, a.xs_unit,
+                           a.x + (size_t)it2 * P,
                            fw ? a.ring_dt + od : ws.w + (size_t)it2 * c, ws.C + (size_t)key * kN + K, wave, lane,
                            nw, withB,
                            fw ? ws.hd + (size_t)it2 * HD_STRIDE + HD_DT : nullptr, scal(bf), a.A + h2,
@@ -2344,9 +2360,10 @@ flush_kernel(StepArgs a) {
             // whole windows keep the pair's B' and C' from its previous head
             const bool withB = !whole || bkey0 != pr;
             bkey0 = whole ? pr : -1;
-            const size_t od = (size_t)rfl64(sL.ord[k]);
             stage_window_dma<NC>(sBc, sX, sW, sW + fa, k0, kn, m, P, a.ring_b + (size_t)rfl64(sL.orb[k]),
-                                 ws.B + (size_t)pr * kN + K, a.ring_x + od * P, a.x + (size_t)it * P,
+                                 ws.B + (size_t)pr * kN + K,
+                                 a.ring_x + (size_t)rfl64(sL.orow[k]) * c + (size_t)(c - m) * a.xs_tok, a.xs_tok,
+                                 a.xs_unit, a.x + (size_t)it * P,
                                  ws.w + (size_t)it * c, ws.C + (size_t)pr * kN + K, wave, lane, nw,
                                  withB);
             __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA has landed in LDS
@@ -2630,7 +2647,7 @@ __global__ void materialize_kernel(StepArgs a, float* __restrict__ S, int K, int
       float v = dtot * snap;
       for (int i = 0; i < nv; ++i) {
         const int pos = (t0 + i) % c;
-        const float u = w[i] * bf2f(a.ring_x[(rh + pos) * a.P + p]);
+        const float u = w[i] * bf2f(a.ring_x[xring(a, o, pos, p)]);
         v = fmaf(u, a.ring_b[(rbg + pos) * NC + n], v);
       }
       dst[K + n] = v;
@@ -3155,6 +3172,7 @@ int check_tier(const nssm_tier* tr, bool need_ring) {
   if ((tr->cold_kind == NSSM_COLD_BF16 || e4m3) && !tr->master) return NSSM_E_NULL;
   if (e4m3 && !tr->scale) return NSSM_E_NULL;
   if (tr->slots <= 0 || tr->c < 1 || tr->c > kMaxC) return NSSM_E_DIMS;
+  if (tr->x_layout != NSSM_XRING_ROW && tr->x_layout != NSSM_XRING_UNIT) return NSSM_E_KIND;
   if (tr->k_hot != 0 && tr->k_hot != 16 && tr->k_hot != 32 && tr->k_hot != 64 && tr->k_hot != 96) return NSSM_E_DIMS;
   if (tr->k_hot == 0 && !cold) return NSSM_E_DIMS;
   if (!aligned16(tr->hot) || (cold && !aligned16(tr->cold)) || (tr->master && !aligned16(tr->master)))
@@ -3163,7 +3181,7 @@ int check_tier(const nssm_tier* tr, bool need_ring) {
   return NSSM_OK;
 }
 
-void fill_tier(StepArgs& a, const nssm_tier* tr) {
+void fill_tier(StepArgs& a, const nssm_tier* tr, int P) {
   a.hot = tr->hot;
   a.cold = tr->cold;
   a.scale = tr->scale;
@@ -3177,6 +3195,9 @@ void fill_tier(StepArgs& a, const nssm_tier* tr) {
   a.slots = tr->slots;
   a.c = tr->c;
   a.K = tr->k_hot;
+  const bool unit = tr->x_layout == NSSM_XRING_UNIT;
+  a.xs_tok = unit ? 8 : P;
+  a.xs_unit = unit ? 8 * tr->c : 8;
 }
 
 template <int K, int COLD>
@@ -3283,7 +3304,7 @@ int v4_step(const nssm_layer_params* prm, const nssm_tier* tier, const nssm_step
   if ((rc = check_ws(prm, in->b, tier->c, workspace, workspace_bytes))) return rc;
   StepArgs a = {};
   fill_common(a, prm, in, y, workspace);
-  fill_tier(a, tier);
+  fill_tier(a, tier, prm->P);
   a.exact = exact;
   a.tf = readout == 2;
   if (readout == 3) {
@@ -3536,7 +3557,7 @@ int nssm_v4_join(const nssm_layer_params* prm, const nssm_tier* tier, const floa
   if (b < 0 || (!slot_ids && b > tier->slots)) return NSSM_E_DIMS;
   if (b == 0) return NSSM_OK;
   StepArgs a = {};
-  fill_tier(a, tier);
+  fill_tier(a, tier, prm->P);
   a.slot_ids = slot_ids;
   a.H = prm->H;
   a.P = prm->P;
@@ -3564,7 +3585,7 @@ int nssm_v4_materialize(const nssm_layer_params* prm, const nssm_tier* tier, flo
   if (b < 0 || (!slot_ids && b > tier->slots)) return NSSM_E_DIMS;
   if (b == 0) return NSSM_OK;
   StepArgs a = {};
-  fill_tier(a, tier);
+  fill_tier(a, tier, prm->P);
   a.slot_ids = slot_ids;
   a.A = prm->A;
   a.H = prm->H;

@@ -293,8 +293,10 @@ def capture(m, cache_params, dt_min: float):
         return
     kind = _cold_kind(cfg)
     master = cfg.get("master", "fp32") if kind in ("bf16", "fp8") else "fp32"
+    # the x ring's layout follows the readout configured at capture (either layout serves
+    # every readout if corr changes later)
     tier = V4Tier(b, m.num_heads, m.head_dim, m.n_groups, k_hot=pb, c=c, cold=kind, device=S.device,
-                  master=master)
+                  master=master, x_ring=ops.x_ring_for(c, bool(cfg.get("corr"))))
     tier.join(prm, Srot.contiguous())
     m._v4state = V4State(tier=tier, params=prm, pb=pb, c=c, rotated=prm.R is not None)
 

@@ -152,6 +152,15 @@ def fresh_step(prm: LayerParams, state: torch.Tensor, x, B, C, dt, y: Optional[t
     return y
 
 
+def x_ring_for(c: int, exact: bool) -> str:
+    """The x ring layout for a tier read mostly with the given readout: "unit" for the exact
+    readout over windows longer than 16 tokens (its per-token window reads, c - 1 tokens per
+    head, then outweigh the appends: 9B shape, c = 64, 9.02 -> 8.84 ms per step), "row"
+    otherwise (exact c = 16: 8.03-8.07 -> 8.14-8.16 ms with "unit"; the stale readouts read the
+    ring only at a flush)."""
+    return "unit" if exact and c > 16 else "row"
+
+
 class V4Tier:
     """Tiered state of one layer for `slots` sequence slots (hot fp32 [slots,H,P,K],
     cold fp32/bf16/fp8 [slots,H,P,NC] (+ master and per-row scale), ring of the last
@@ -170,10 +179,19 @@ class V4Tier:
     lag=True keeps the lagged snapshot of the evaluation forward's lag = 1
     (scale/nemo9b_eval.py:44,59,70): a second read copy (cold2, scale2) and the log-decay
     between the two snapshots per (slot, head) (wlag); such a tier is read with the lagged
-    teacher-forced readout (step(..., teacher=True)) only."""
+    teacher-forced readout (step(..., teacher=True)) only.
+
+    x_ring: the layout of the ring's x (NSSM_XRING_*): "row" ([slots, H, c, P], the default:
+    the cheapest per-token append) or "unit" ([slots, H, P / 8, c, 8]: the exact readout's
+    window reads are one run per unit). Both serve every readout; only their speed differs."""
 
     def __init__(self, slots: int, H: int, P: int, G: int, k_hot: int = 32, c: int = 4, cold: str = "fp32",
-                 device="cuda", N: int = N_STATE, master: str = "fp32", lag: bool = False):
+                 device="cuda", N: int = N_STATE, master: str = "fp32", lag: bool = False, x_ring: str = "row"):
+        if x_ring not in _lib.XRING_LAYOUTS:
+            raise ValueError(f"x_ring must be one of {sorted(_lib.XRING_LAYOUTS)} (got {x_ring!r})")
+        if x_ring == "unit" and P % 8:
+            raise ValueError(f"x_ring='unit' needs P a multiple of 8 (got {P})")
+        self.x_layout = _lib.XRING_LAYOUTS[x_ring]
         if cold not in COLD_KINDS:
             raise ValueError(f"cold must be one of {sorted(COLD_KINDS)} (got {cold!r})")
         if cold != "off" and (cold, master) not in _lib.STORAGE_KINDS:
@@ -195,7 +213,8 @@ class V4Tier:
         master_dt = {_lib.COLD_BF16: torch.float32, _lib.COLD_FP8: torch.float32,
                      _lib.COLD_FP8_BF16M: torch.bfloat16}.get(self.kind)
         self.master = e((slots, H, P, NC), master_dt) if master_dt is not None else None
-        self.ring_x = e((slots, H, c, P), torch.bfloat16) if tiered else None
+        xshape = (slots, H, c, P) if self.x_layout == _lib.XRING_ROW else (slots, H, P // 8, c, 8)
+        self.ring_x = e(xshape, torch.bfloat16) if tiered else None
         self.ring_dt = e((slots, H, c), torch.float32) if tiered else None
         self.ring_b = e((slots, G, c, NC), torch.float32) if tiered else None
         self.t = torch.zeros((slots, H), device=dev, dtype=torch.int32)
@@ -246,7 +265,8 @@ class V4Tier:
         return sum(t.numel() * t.element_size() for t in (self._field(f) for f in TIER_FIELDS) if t is not None)
 
     def c_struct(self) -> _lib.Tier:
-        return _lib.Tier(self.slots, self.k, self.c, self.kind, *[_ptr(self._field(f)) for f in TIER_FIELDS])
+        return _lib.Tier(self.slots, self.k, self.c, self.kind, *[_ptr(self._field(f)) for f in TIER_FIELDS],
+                         self.x_layout)
 
     def lag_struct(self) -> _lib.Lag:
         return _lib.Lag(_ptr(self.cold2), _ptr(self.scale2), _ptr(self.wlag))

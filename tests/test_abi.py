@@ -45,6 +45,7 @@ def test_abi_version_and_codes_match_header():
     assert int(d["NSSM_COLD_NONE"]) == _lib.COLD_NONE
     assert int(d["NSSM_COLD_BF16_SINGLE"]) == _lib.COLD_BF16_SINGLE
     assert int(d["NSSM_COLD_FP8_BF16M"]) == _lib.COLD_FP8_BF16M
+    assert (int(d["NSSM_XRING_ROW"]), int(d["NSSM_XRING_UNIT"])) == (_lib.XRING_ROW, _lib.XRING_UNIT)
     assert (int(d["NSSM_DT_F32"]), int(d["NSSM_DT_BF16"])) == (_lib.DT_F32, _lib.DT_BF16)
     for code in ("NSSM_E_NULL", "NSSM_E_DIMS", "NSSM_E_ALIGN", "NSSM_E_KIND", "NSSM_E_LAUNCH", "NSSM_E_TUNING",
                  "NSSM_E_WORKSPACE", "NSSM_E_SCRATCH"):
@@ -147,6 +148,8 @@ def test_entry_points_validate_before_launching():
     assert L.nssm_v4_step(ctypes.byref(prm), ctypes.byref(tier), ctypes.byref(inp), fake, fake, 1 << 30, None) == -2
     tier = _lib.Tier(4, 32, 4, 2, *([fake] * 2 + [None] + [fake] * 7))  # fp8 without a scale buffer
     assert L.nssm_v4_step(ctypes.byref(prm), ctypes.byref(tier), ctypes.byref(inp), fake, fake, 1 << 30, None) == -1
+    tier = _lib.Tier(4, 32, 4, 0, *([fake] * 10), 2)  # x ring layout neither row nor unit
+    assert L.nssm_v4_step(ctypes.byref(prm), ctypes.byref(tier), ctypes.byref(inp), fake, fake, 1 << 30, None) == -4
     # workspace: NULL, too small, misaligned
     need = L.nssm_step_workspace_bytes(4, 8, 1, 128, 0)
     assert need == 4 * (2 * 128 + 12 * 8) * 4
@@ -206,6 +209,8 @@ def test_python_layer_rejects_cpu_tensors_and_wrong_dtypes():
         nested_ssm_amd.fresh_step(prm, torch.zeros(2, 8, 80, 128), x, x, x, x)
     with pytest.raises(ValueError):
         V4Tier(2, 8, 80, 1, cold="int4")
+    with pytest.raises(ValueError, match="x_ring"):
+        V4Tier(2, 8, 80, 1, x_ring="tiled")
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

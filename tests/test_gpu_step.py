@@ -57,13 +57,13 @@ def test_fresh_dt_min_and_identity_rotation():
 
 
 def _run_v4(b, H, G, P, k, c, cold, steps, seed, slots=None, phase=None, check_state_every=1, exact=False,
-            master="fp32", modes=None, counts=None, each=None):
+            master="fp32", modes=None, counts=None, each=None, x_ring="row"):
     gen, prm, S0 = _setup(b, H, P, G, seed)
     dprm = dev_params(prm)
     ref = oracle.NativeV4(b, H, P, 128, k, c, cold=cold, exact=exact, master=master)
     ph = None if phase is None else torch.as_tensor(phase, dtype=torch.int32)
     ref.join(torch.arange(b), S0, phase=None if ph is None else ph.long())
-    tier = V4Tier(b, H, P, G, k_hot=k, c=c, cold=cold, master=master)
+    tier = V4Tier(b, H, P, G, k_hot=k, c=c, cold=cold, master=master, x_ring=x_ring)
     tier.join(dprm, *to_dev(S0), phase=None if ph is None else ph.cuda())
     worst = 0.0
     for step in range(steps):
@@ -359,19 +359,31 @@ def test_v4_exact_readout_matches_oracle(cold, k, c, phase):
             exact=True)
 
 
-def test_v4_exact_readout_equals_fresh_at_9b_shape_alternating_modes():
+@pytest.mark.parametrize("cold,k,c,phase,exact", [
+    ("fp32", 32, 4, [0, 1, 2, 3], True), ("fp32", 32, 40, [0, 7, 39, 20], True), ("fp8", 96, 33, [5, 0, 32, 17], True),
+    ("fp32", 64, 64, [3, 60, 63, 0], False), ("bf16", 32, 16, [1, 15, 8, 0], False)])
+def test_unit_blocked_x_ring_matches_oracle(cold, k, c, phase, exact):
+    """Tiers whose x ring is unit-blocked (NSSM_XRING_UNIT): the exact and stale readouts,
+    the fused (c <= 16) and flush-kernel replays, the ring appends and the materialized
+    state match the oracle as with the row-major ring."""
+    _run_v4(4, 8, 2, 80, k, c, cold, steps=2 * c + 5, seed=120 + k + c, phase=phase,
+            check_state_every=max(1, c // 2), exact=exact, x_ring="unit")
+
+
+@pytest.mark.parametrize("x_ring", ["row", "unit"])
+def test_v4_exact_readout_equals_fresh_at_9b_shape_alternating_modes(x_ring):
     """fp32 cold at the 9B head shape (H=128, G=8, B=64): steps alternate between the
     stale and the exact readout on one tier (the tier evolves the same way). Every
     exact y equals the fresh y of the fp64 trajectory from the same start (the exact
     readout is the current cold state's); hot columns and the materialized state track
-    it; random phases. rtol = atol = 1e-5."""
+    it; random phases; both x ring layouts. rtol = atol = 1e-5."""
     b, H, P, G, k, c = 64, 128, 80, 8, 32, 4
     gen, prm, _ = _setup(1, H, P, G, seed=91)
     dprm = dev_params(prm)
     g = torch.Generator(device="cuda").manual_seed(5)
     S = torch.randn(b, H, P, 128, device="cuda", generator=g).mul_(0.1)
     phase = torch.randint(0, c, (b,), device="cuda", generator=g, dtype=torch.int32)
-    tier = V4Tier(b, H, P, G, k_hot=k, c=c, cold="fp32")
+    tier = V4Tier(b, H, P, G, k_hot=k, c=c, cold="fp32", x_ring=x_ring)
     tier.join(dprm, S, phase=phase)
     ref = Fresh64(dprm, S)
     for step in range(4 * c + 1):
