@@ -222,11 +222,11 @@ __device__ __forceinline__ size_t xring(const StepArgs& a, size_t sh, int pos, i
 }
 
 // ---------------------------------------------------------------------------
-// prep: one workgroup (256 threads) per (group g, block of prb <= kPrepReq requests).
+// prep: one workgroup (kPrepThreads threads) per (group g, block of prb <= kPrepReq requests).
 //  * rotation: [B' C'] = R_g [B C] for the block, a 128 x 128 by 128 x 2 kPrepReq product
 //    on the matrix cores (v_mfma_f32_16x16x4_f32, fp32 products and sums) in 16-column
 //    tiles: columns j < kPrepReq are B of request j, the others C of request j - kPrepReq
-//    (staged in LDS); wave w owns the output row tiles w and w + 4. A lane loads R as
+//    (staged in LDS); wave w of W owns the output row tiles w, w + W, ... A lane loads R as
 //    float4 (R[m][k..k+3]); the four MFMA steps of a 16-wide k block take the float4's
 //    elements in turn, and the B operand takes the same k order, so each step pairs equal
 //    k. The group's R is read once per block;
@@ -236,7 +236,15 @@ __device__ __forceinline__ size_t xring(const StepArgs& a, size_t sh, int pos, i
 //    position t % c. A flush token sits at c-1, so a flush window is always ring
 //    positions [c-m, c).
 // Latency bound: every independent global load is issued before the first barrier.
-constexpr int kPrepThreads = 256;
+// Threads per prep workgroup: 8 waves, one rotation row tile each (at the 9B shape, 256
+// threads (two row tiles per wave) measured 8.57 -> 8.14 us per launch at B = 256, c = 4,
+// 11.65 -> 10.79 for the ragged B = 384, c = 64 batch and 15.5 -> 15.05 with the exact
+// readout's window dots at c = 64: twice the loads in flight per CU).
+#ifndef NSSM_PREP_THREADS
+#define NSSM_PREP_THREADS 512
+#endif
+constexpr int kPrepThreads = NSSM_PREP_THREADS;
+constexpr int kPrepRowTiles = (kN / 16) / (kPrepThreads / 64);  // rotation row tiles per wave
 // Requests per prep workgroup (at most; a multiple of 8). Measured with 16 (a 128 x 32 product,
 // half the workgroups): prep at the 9B shape 9.6 -> 12.9 us per launch at B = 256 and 13.5 ->
 // 14.6 us at B = 384 (each workgroup's chain grows more than the launch shrinks).
@@ -339,13 +347,14 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
     if (r >= nreq) bst[u] = cst[u] = 0.f;
   }
   const float* __restrict__ Rg = a.R ? a.R + (size_t)g * kN * kN : nullptr;
-  f4 ra[2][kN / 16];  // this lane's R operands of its two row tiles
+  f4 ra[kPrepRowTiles][kN / 16];  // this lane's R operands of its row tiles
   if (Rg) {
 #pragma unroll
-    for (int t2 = 0; t2 < 2; ++t2)
+    for (int t2 = 0; t2 < kPrepRowTiles; ++t2)
 #pragma unroll
       for (int kb = 0; kb < kN / 16; ++kb)
-        ra[t2][kb] = *reinterpret_cast<const f4*>(Rg + (size_t)((wave + 4 * t2) * 16 + li) * kN + kb * 16 + 4 * lk);
+        ra[t2][kb] = *reinterpret_cast<const f4*>(
+            Rg + (size_t)((wave + (kPrepThreads / 64) * t2) * 16 + li) * kN + kb * 16 + 4 * lk);
   }
   if (tid < kPrepReq) {
     sFl[tid] = 0;
@@ -394,7 +403,7 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
   // (B of request j for j < kPrepReq, C of request j - kPrepReq after)
   if (Rg) {
 #pragma unroll
-    for (int t2 = 0; t2 < 2; ++t2) {
+    for (int t2 = 0; t2 < kPrepRowTiles; ++t2) {
 #pragma unroll
       for (int ct = 0; ct < 2 * kPrepReq / 16; ++ct) {
         f4 acc = f4{0.f, 0.f, 0.f, 0.f};
@@ -407,7 +416,7 @@ __global__ void __launch_bounds__(kPrepThreads) prep_kernel(StepArgs a) {
           acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ra[t2][kb].w, xb.w, acc, 0, 0, 0);
         }
         // lane (li, lk) holds rows m0 + 4 lk .. +3 of column 16 ct + li
-        const int m0 = (wave + 4 * t2) * 16 + 4 * lk;
+        const int m0 = (wave + (kPrepThreads / 64) * t2) * 16 + 4 * lk;
         const int j = 16 * ct + li, r = j % kPrepReq, which = j / kPrepReq;
         if constexpr (TIERED) {
           if (rot_lds) *reinterpret_cast<f4*>(&sRot[j][m0]) = acc;
