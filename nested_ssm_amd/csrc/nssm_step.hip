@@ -250,7 +250,10 @@ constexpr int kPrepRowTiles = (kN / 16) / (kPrepThreads / 64);  // rotation row 
 // 14.6 us at B = 384 (each workgroup's chain grows more than the launch shrinks).
 constexpr int kPrepReq = 8;
 constexpr int kPrepStage = kPrepReq * kN / kPrepThreads;  // B (and C) elements a prep thread stages
-constexpr int kPrepDotBatch = 4;  // exact readout: window dots a prep lane group loads at once
+#ifndef NSSM_PREP_DOT_BATCH
+#define NSSM_PREP_DOT_BATCH 4
+#endif
+constexpr int kPrepDotBatch = NSSM_PREP_DOT_BATCH;  // exact readout: window dots a prep lane group loads at once
 
 // A head's dt (softplus, with the dt_min floor of the native path) and the scalars every
 // stream kernel reads: dt, a = dt A, exp(a), D, A. Returns dt.
