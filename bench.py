@@ -578,7 +578,7 @@ def kernel_label(head, args):
             f"(one layer-token, three launches)")
 
 
-def main():
+def parse_args(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=64)
@@ -611,12 +611,17 @@ def main():
                     help="skip the rocprofv3 counter passes that measure the headline's HBM traffic")
     ap.add_argument("--traffic-pass", action="store_true",
                     help="(internal) the workload of one counter pass: 2 layers, whole windows, and a copy")
-    args = ap.parse_args()
+    args = ap.parse_args(argv)
     if args.cold == "fp32":
         args.master = "fp32"  # fp32 cold is its own master
     if args.exact and (args.coldoff or args.qgate > 0):
         ap.error("--exact cannot be combined with --coldoff or --qgate")
     args.skip = 0.0
+    return args
+
+
+def main():
+    args = parse_args()
 
     if args.copy_calibration_mib:
         n = args.copy_calibration_mib * (1 << 20) // 4

@@ -326,3 +326,22 @@ def test_stream_probe_argument_errors():
     assert L.nssm_stream_probe(fake, fake, chunk, 2, None) == -2
     assert L.nssm_stream_probe(fake + 4, fake, chunk, 0, None) == -3
     assert L.nssm_stream_probe(fake, fake + 8, chunk, 1, None) == -3
+
+
+@pytest.mark.parametrize("argv", [
+    [], ["--c", "64", "--exact"], ["--B", "384", "--k", "64", "--c", "16", "--ragged"],
+    ["--cold", "fp8", "--master", "bf16", "--B", "448"], ["--qgate", "0.25", "--seed", "3"], ["--coldoff"]])
+def test_bench_traffic_pass_rebuilds_the_workload(argv):
+    """bench.py's counter passes run the workload again in a child process from the flags
+    workload_argv forms: parsed back, they name the same workload (batch, tier shape,
+    storage, readout, phases, seed)."""
+    import sys
+
+    sys.path.insert(0, ROOT)
+    import bench
+
+    a = bench.parse_args(argv)
+    b = bench.parse_args(bench.workload_argv(a) + ["--traffic-pass", "--only", "v4"])
+    keys = ("B", "k", "c", "cold", "master", "exact", "coldoff", "qgate", "ragged", "seed")
+    assert {k: getattr(a, k) for k in keys} == {k: getattr(b, k) for k in keys}
+    assert b.traffic_pass and bench.traffic_key(a) == bench.traffic_key(b)
