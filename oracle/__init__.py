@@ -1,9 +1,10 @@
 """CPU oracle for the Mamba2 v4 tiered decode step — TEST INFRASTRUCTURE ONLY.
 
 This package restates, in plain PyTorch on the CPU, the arithmetic of the
-reference repository's decode step (omin-Kwon/nested_ssm, scale/*.py). It is
-the checker: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
-leg may import it, and never as the thing that is measured or shipped. The
+reference repository's decode step (omin-Kwon/nested_ssm, scale/*.py). It
+serves only to check the product: only tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg may import it, and never as the thing that is
+measured or shipped. The
 product path (nested_ssm_amd) never imports it and has no CPU fallback.
 
 Precision convention (one fp32 convention for the whole path, as the
