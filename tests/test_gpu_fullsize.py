@@ -1,17 +1,17 @@
-"""GPU: the benchmark configurations at their full per-layer sizes (9B head shape
+"""GPU: the benchmark workloads at their full per-layer sizes (9B head shape
 H=128, P=80, N=128, G=8) and full step counts.
 
 Two references:
-  * the CPU oracle itself (oracle.NativeV4, fp32) on identical seeded inputs: config 2
-    (B=256, k=32, c=4, fp32 cold, phase-aligned, 64 steps: y at every step and the final
-    state at rtol = atol = 1e-5) and config 3 (B=448, e4m3 cold with the per-row scale,
-    c=4, 128 steps: y within 2e-2 relative of the oracle's fp8-cold emulation at every
-    step). Config 3's emulation re-quantizes every slot's snapshot on every token, which
+  * the CPU oracle itself (oracle.NativeV4, fp32) on identical seeded inputs: v4 at
+    B=256, k=32, c=4, fp32 cold, phase-aligned, 64 steps (y at every step and the final
+    state at rtol = atol = 1e-5) and v4 at B=448, e4m3 cold with the per-row scale, c=4,
+    128 steps (y within 2e-2 relative of the oracle's fp8-cold emulation at every step).
+    The e4m3 emulation re-quantizes every slot's snapshot on every token, which
     costs the host about 1.5 s per token at B=448, so the oracle follows a strided subset
     of 64 of the 448 requests (the requests are independent; the GPU runs all 448 in every
     launch and the full batch is checked below);
   * an fp64 trajectory on the GPU (helpers.Fresh64: the exact state the tiers represent)
-    for configs 1 and 4 and the other storage kinds at full batch: y is the stale-readout
+    for fresh at B=256, the ragged B=384 batch and the other storage kinds at full batch: y is the stale-readout
     closed form hot C' + exp(glog) (read(snapshot) C') + D x built in fp64 from the fresh
     trajectory, where the snapshot is the fresh state at the request's last flush and
     read() is the read copy's precision (e4m3: torch's e4m3fn cast with the per-row
@@ -142,8 +142,8 @@ def _run(b, k, c, cold, steps, seed, slot_events=None, master="fp32", aligned=Fa
     return worst
 
 
-def test_config1_fresh_b256_64_steps():
-    """Config 1: the untiered step at B=256, 64 steps, against the fp64 recurrence (y at
+def test_fresh_b256_27_layers_64_steps_against_fp64():
+    """The untiered step at B=256, 64 steps, against the fp64 recurrence (y at
     every step and the final state at rtol = atol = 1e-5)."""
     b = 256
     prm = _params(101)
@@ -158,8 +158,8 @@ def test_config1_fresh_b256_64_steps():
     assert_close32(S, ref.S, "fresh final state")
 
 
-def test_config1_fresh_b256_without_rotation():
-    """Config 1 as the benchmark's fresh leg runs it: no rotation (prep's identity path),
+def test_fresh_b256_without_rotation_against_fp64():
+    """The untiered step at B=256 as the benchmark's fresh leg runs it: no rotation (prep's identity path),
     B=256, 64 steps against the fp64 recurrence; on odd steps B and C sit 2 bytes off 8-byte
     alignment."""
     b = 256
@@ -180,8 +180,8 @@ def test_config1_fresh_b256_without_rotation():
 
 
 @pytest.mark.timeout(600)
-def test_config2_b256_phase_aligned_against_the_oracle():
-    """Config 2 as specified: B=256, k=32, c=4, fp32 cold, phase-aligned, 64 steps; y at
+def test_v4_fp32_b256_k32_c4_phase_aligned_against_the_oracle():
+    """v4 at B=256, k=32, c=4, fp32 cold, phase-aligned, 64 steps; y at
     every step, the final state (materialized), the hot columns and the cold copy (t = 64
     is a flush boundary) against the CPU oracle's NativeV4 on identical seeded inputs."""
     b, k, c = 256, 32, 4
@@ -198,17 +198,17 @@ def test_config2_b256_phase_aligned_against_the_oracle():
         x, B, C, dt = oracle.make_step_inputs(b, H, P, N, G, gen)
         y = tier.step(dprm, *to_dev(x, B, C, dt))
         y_ref = ref.step(x, B, C, dt, prm)
-        assert_close32(y, y_ref, f"config 2 y step {step}")
+        assert_close32(y, y_ref, f"B=256 y step {step}")
     assert int(ref.t[0]) % c == 0
-    assert_close32(tier.materialize(dprm), ref.S, "config 2 final state")
-    assert_close32(tier.hot, ref.S[..., :k], "config 2 hot columns")
-    assert_close32(tier.cold_t, ref.S[..., k:], "config 2 cold copy")
+    assert_close32(tier.materialize(dprm), ref.S, "B=256 final state")
+    assert_close32(tier.hot, ref.S[..., :k], "B=256 hot columns")
+    assert_close32(tier.cold_t, ref.S[..., k:], "B=256 cold copy")
 
 
 @pytest.mark.timeout(600)
 @pytest.mark.parametrize("master", ["fp32", "bf16"])
-def test_config3_b448_fp8_against_the_oracle_emulation(master):
-    """Config 3: B=448, e4m3 cold with the per-(seq, head, row) scale, c=4, k=32, 128 steps,
+def test_v4_e4m3_b448_c4_against_the_oracle_emulation(master):
+    """v4 at B=448, e4m3 cold with the per-(seq, head, row) scale, c=4, k=32, 128 steps,
     over an exact fp32 master or the fused path's bf16 master; y of 64 of the 448 requests
     (every 7th) within 2e-2 relative of the oracle's fp8-cold emulation over the exact fp32
     state (scale/vllm_v4_patch.py:106-120, 164-179) at every step."""
@@ -231,24 +231,24 @@ def test_config3_b448_fp8_against_the_oracle_emulation(master):
         r = max_rel(y, y_ref)
         worst = max(worst, r)
         worst_abs = max(worst_abs, float((y - y_ref).abs().max()))
-        assert r <= 2e-2, f"config 3 ({master} master) y step {step}: norm-wise rel err {r:.3g}"
+        assert r <= 2e-2, f"B=448 e4m3 ({master} master) y step {step}: norm-wise rel err {r:.3g}"
     assert 0 < worst <= 2e-2, (worst, worst_abs)
 
 
 def test_full_size_fp8_b448_random_phases():
-    """Config-3 storage for all 448 requests, random phases, 128 steps, against the fp64
+    """e4m3 cold with the per-row scale for all 448 requests, random phases, 128 steps, against the fp64
     closed form (the snapshot quantized by torch's e4m3fn cast)."""
     assert _run(448, 32, 4, "fp8", steps=128, seed=2) > 0
 
 
 def test_full_size_fp8_bf16_master_b448():
-    """Config-3 storage over the fused reference's bf16 shadow master: B=448, e4m3 read
+    """e4m3 cold with the per-row scale over the fused reference's bf16 shadow master: B=448, e4m3 read
     copy with per-row scale, bf16 master, c=4, 128 steps, random phases."""
     assert _run(448, 32, 4, "fp8", steps=128, seed=3, master="bf16") > 0
 
 
 def test_full_size_v4_b256_random_phases():
-    """Config-2 storage with random phases (every token flushes a quarter of the requests),
+    """fp32 cold (k=32, c=4) with random phases (every token flushes a quarter of the requests),
     64 steps, against the fp64 closed form at 1e-5."""
     _run(256, 32, 4, "fp32", steps=64, seed=1)
 
@@ -268,8 +268,8 @@ def test_full_size_bf16_read_copy_fp32_master_b256(c):
 
 
 @pytest.mark.parametrize("c,k", [(8, 32), (16, 32), (64, 32), (8, 64), (16, 64), (64, 64)])
-def test_full_size_ragged_config4(c, k):
-    """Config 4: 384 slots, random phases, 48 requests leave and new ones join every 8 steps,
+def test_full_size_ragged_b384_every_window(c, k):
+    """The ragged batch: 384 slots, random phases, 48 requests leave and new ones join every 8 steps,
     256 steps, fp32 cold; y at every step and the final state at 1e-5."""
     b = 384
 

@@ -101,7 +101,7 @@ def _run_v4(b, H, G, P, k, c, cold, steps, seed, slots=None, phase=None, check_s
 
 
 @pytest.mark.parametrize("k,c", [(32, 4), (64, 16), (96, 3), (32, 1), (32, 64)])
-def test_v4_fp32_config0(k, c):
+def test_v4_fp32_b4_h8_g1(k, c):
     tier, ref, _ = _run_v4(4, 8, 1, 80, k, c, "fp32", steps=64 if c != 64 else 130, seed=21 + k + c)
     # the fp32 cold copy equals the fresh cold columns right after a flush
     if int(ref.t[0]) % c == 0:
@@ -427,7 +427,7 @@ def test_v4_bf16_master_matches_oracle(cold, k, c, P):
 
 
 def test_fp8_bf16_master_within_the_reference_fp8_emulation():
-    """Config-3 storage (e4m3 read copy, per-row scale) kept over a bf16 master, against
+    """e4m3 read copy with the per-row scale kept over a bf16 master, against
     the reference's fp8-cold emulation with the exact fp32 state
     (scale/vllm_v4_patch.py:106-120, 164-179): y within 2e-2 relative at every one of
     128 steps, random phases."""
@@ -637,7 +637,7 @@ def test_read_copy_is_the_masters_quantization_after_flushes(cold, master, k, c)
 @pytest.mark.parametrize("cold", ["fp32", "bf16", "fp8"])
 def test_k_hot_16_matches_oracle(cold, c, exact):
     """The narrowest trained hot width (scale/nemotron_retrofit.py:5,191): 16 hot columns
-    and 112 cold ones, a half segment on each side of the split, at the config-0 shape;
+    and 112 cold ones, a half segment on each side of the split, at the B=4, H=8, G=1 shape;
     windows replayed in the stream kernel (c <= 16) and on the matrix cores (c = 64); the
     stale and the exact readout, random phases."""
     tier, ref, worst = _run_v4(4, 8, 1, 80, 16, c, cold, steps=2 * c + 5 if c > 4 else 64, seed=210 + c,
@@ -745,7 +745,7 @@ def test_teacher_forced_e4m3_within_the_reference_column_emulation(b, H, G, k, c
     scale of scale/vllm_v4_patch.py:106-111. nssm_v4_step_teacher over an e4m3 tier (fp32 and
     bf16 masters) stays within the fp8 bar, 2e-2 norm-wise relative on y, of the reference's
     column emulation (oracle TeacherForcedV4(cold="fp8", fp8_scale="column")) on every one of
-    2c + 5 tokens, at the config-0 shape and at the 9B head shape (H = 128, G = 8)."""
+    2c + 5 tokens, at the B = 4, H = 8, G = 1 shape and at the 9B head shape (H = 128, G = 8)."""
     P = 80
     gen, prm, S0 = _setup(b, H, P, G, seed=400 + H + k + c)
     dprm = dev_params(prm)
