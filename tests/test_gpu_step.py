@@ -705,6 +705,10 @@ def test_join_quantization_is_bit_exact_k16(cold, master):
     ("fp32", 0, 4, "fp32"), ("fp32", 0, 16, "fp32"), ("fp32", 0, 64, "fp32"), ("bf16", 0, 4, "fp32"),
     ("fp8", 0, 16, "fp32"), ("fp8", 0, 64, "bf16")])
 def test_teacher_forced_readout_matches_oracle(cold, k, c, master):
+    _teacher_forced_case(cold, k, c, master)
+
+
+def _teacher_forced_case(cold, k, c, master, x_ring="row"):
     """nssm_v4_step_teacher against the oracle's restatement of the evaluation forward's loop
     (scale/nemo9b_eval.py:41-85; mode "v4", and "c1" at k_hot = 0): a sequence joined at its
     start with phase c - 1 flushes at positions t % c == 0, reads the new state there and the
@@ -716,7 +720,7 @@ def test_teacher_forced_readout_matches_oracle(cold, k, c, master):
     dprm = dev_params(prm)
     ref = oracle.TeacherForcedV4(b, H, P, 128, k, c, cold=cold, master=master)
     ref.join(torch.arange(b), S0)
-    tier = V4Tier(b, H, P, G, k_hot=k, c=c, cold=cold, master=master)
+    tier = V4Tier(b, H, P, G, k_hot=k, c=c, cold=cold, master=master, x_ring=x_ring)
     tier.join(dprm, *to_dev(S0), phase=torch.full((b,), c - 1, dtype=torch.int32, device="cuda"))
     worst = 0.0
     for step in range(2 * c + 5):
@@ -795,6 +799,10 @@ def test_teacher_forced_readout_from_scratch_with_ragged_starts():
     ("bf16", 32, 4, "bf16"), ("bf16", 16, 40, "bf16"), ("fp8", 32, 16, "bf16"), ("fp8", 32, 64, "bf16"),
     ("fp32", 0, 4, "fp32"), ("fp32", 0, 64, "fp32"), ("fp8", 0, 16, "bf16"), ("bf16", 0, 64, "fp32")])
 def test_teacher_forced_lagged_readout_matches_oracle(cold, k, c, master):
+    _teacher_forced_lagged_case(cold, k, c, master)
+
+
+def _teacher_forced_lagged_case(cold, k, c, master, x_ring="row"):
     """nssm_v4_step_teacher_lagged against the oracle's restatement of the evaluation loop with
     lag = 1 (scale/nemo9b_eval.py:44,59,70): the readout is of the snapshot before the last one,
     decayed from it (the joined state until the second flush); both replay paths (the stream
@@ -806,7 +814,7 @@ def test_teacher_forced_lagged_readout_matches_oracle(cold, k, c, master):
     dprm = dev_params(prm)
     ref = oracle.TeacherForcedV4(b, H, P, 128, k, c, cold=cold, master=master, lag=1)
     ref.join(torch.arange(b), S0)
-    tier = V4Tier(b, H, P, G, k_hot=k, c=c, cold=cold, master=master, lag=True)
+    tier = V4Tier(b, H, P, G, k_hot=k, c=c, cold=cold, master=master, lag=True, x_ring=x_ring)
     tier.join(dprm, *to_dev(S0), phase=torch.full((b,), c - 1, dtype=torch.int32, device="cuda"))
     for step in range(3 * c + 5):
         x, B, C, dt = oracle.make_step_inputs(b, H, P, 128, G, gen)
@@ -875,3 +883,13 @@ def test_c1_tier_refuses_the_other_readouts():
     for kw in (dict(), dict(exact=True), dict(hot_only=True), dict(qgate=0.5), dict(noalloc=True)):
         with pytest.raises(ValueError, match="k_hot = 0"):
             tier.step(dprm, x, B, C, dt, **kw)
+
+
+@pytest.mark.parametrize("lag,cold,k,c,master", [
+    (False, "fp32", 32, 4, "fp32"), (False, "fp8", 32, 64, "bf16"), (False, "fp32", 0, 64, "fp32"),
+    (True, "fp32", 32, 16, "fp32"), (True, "bf16", 16, 40, "bf16"), (True, "fp8", 32, 64, "bf16")])
+def test_teacher_forced_readouts_on_a_unit_blocked_x_ring(lag, cold, k, c, master):
+    """The teacher-forced and lagged readouts over a unit-blocked x ring (NSSM_XRING_UNIT):
+    both replay paths read the ring through its strides and match the oracle as with the
+    row-major ring, by the same bars."""
+    (_teacher_forced_lagged_case if lag else _teacher_forced_case)(cold, k, c, master, x_ring="unit")
