@@ -139,10 +139,11 @@ def test_native_install_matches_oracle(monkeypatch, pb, c, cold_bf16):
             assert st["t"] == int(ref.t[0])
 
 
-@pytest.mark.parametrize("pb,c,cold_bf16", [(32, 4, 0), (64, 16, 1)])
+@pytest.mark.parametrize("pb,c,cold_bf16", [(32, 4, 0), (64, 16, 1), (32, 32, 0)])
 def test_native_install_corr_matches_oracle(monkeypatch, pb, c, cold_bf16):
     """install(..., corr=1): the rank-c exact correction readout
-    (scale/v4_native_decode.py:81-117) against the oracle's exact mode."""
+    (scale/v4_native_decode.py:81-117) against the oracle's exact mode (at c = 32 over the
+    unit-blocked x ring the capture picks for it)."""
     from nested_ssm_amd import v4_native_decode as V
 
     model = _tiny_model(seed=11)
@@ -154,6 +155,7 @@ def test_native_install_corr_matches_oracle(monkeypatch, pb, c, cold_bf16):
     cold = "bf16" if cold_bf16 else "fp32"
     for m, ref in _replay_and_check(model, rec, pb, c, cold, lambda m: float(m.time_step_limit[0]), exact=True):
         assert m._v4state["t"] == int(ref.t[0])
+        assert m._v4state["tier"].x_layout == (1 if c > 16 else 0)
 
 
 def test_native_install_corr_gives_the_untiered_model():
